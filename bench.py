@@ -1,0 +1,175 @@
+#!/usr/bin/env python3
+"""Headline benchmark: aggregate decode tokens/s of the batched decode step (sn_step) on one MI355X.
+
+Workload: a Qwen3-4B-architecture dense model, random init (seeded N(0, 0.02) weights
+quantized to Q4_0 with ggml's reference quantizer; fp32 embedding and norms; untied Q4_0 LM head), 32 sequences whose
+2048-cell contexts are already in the paged fp16 KV cache (seeded N(0, 1) cells: a step costs the same whatever they
+hold), one new token per sequence per step, greedy argmax fed back as the next token. A step is one sn_step call of 32
+rows: inputs resident on the GPU, one host round trip (the 32 tokens back).
+
+Output: one JSON line. `value` = 32 * steps / wall time of the timed steps. `roofline` is the kernel class that takes
+the most GPU time in a separate profiled pass of the same steps (HIP events around every launch on the engine's
+stream), its algorithmic bytes / time against 8 TB/s; `roofline_gemm` is the Q4_0 matmul's (the metric's "Q4_0 GEMV %
+HBM peak"). `cpu_baseline` times the oracle (oracle/, a C restatement of ggml's CPU semantics) on the host cores for
+one step of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "sonic-llm_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def model_file(cfg_kw, seed, path=None):
+    import sllm_next as S
+    d = os.environ.get("SN_BENCH_DIR") or "/tmp"
+    path = path or os.path.join(d, f"sonic_qwen3_{cfg_kw['n_layer']}L_{cfg_kw['n_embd']}_{seed}.gguf")
+    done = path + ".done"
+    if not (os.path.exists(path) and os.path.exists(done)):
+        t = time.time()
+        S.write_model(path, S.model_cfg(**cfg_kw), seed, nthreads=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
+        open(done, "w").write("ok")
+        log(f"[bench] wrote {path} ({os.path.getsize(path) / 1e9:.2f} GB) in {time.time() - t:.1f}s")
+    return path
+
+
+def cpu_baseline(path, seqs, ctx, seed):
+    """The oracle's step for the same rows on the host cores: one step of `seqs` rows at position ctx (its KV cells are
+    zeros: the cost of a step does not depend on what they hold)."""
+    import numpy as np
+
+    from oracle import oracle as O
+    from oracle.gguf import GGUF
+
+    O.build() if not os.path.exists(O.LIB_PATH) else None
+    ref = O.Qwen3(GGUF(path), n_seq=seqs, ctx=ctx + 1)
+    r = np.random.default_rng(seed)
+    tok = r.integers(0, ref.V, seqs).astype(np.int32)
+    seq = np.arange(seqs, dtype=np.int32)
+    pos = np.full(seqs, ctx, np.int32)
+    ref.k[:, :, :ctx] = 0  # touch the cells the step reads before timing
+    ref.v[:, :, :ctx] = 0
+    t = time.perf_counter()
+    ref.step(tok, seq, pos, seq)
+    dt = time.perf_counter() - t
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count())
+    return {"value": seqs / dt, "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"one decode step of the full workload ({seqs} rows at position {ctx}, all layers and the LM "
+                      f"head) through oracle/oracle.c (ggml-semantics CPU restatement: Q8_0 activations, integer block "
+                      f"dots, fp32 attention over fp16 cells; ggml b11669 itself is not available offline), "
+                      f"{dt:.1f} s on {cores} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--seqs", type=int, default=32)
+    ap.add_argument("--ctx", type=int, default=2048)
+    ap.add_argument("--prof-steps", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--model", default=None, help="GGUF path (generated when missing)")
+    ap.add_argument("--seed", type=int, default=42)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (sequences would shard "
+              f"across GPUs with no per-step exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import sllm_next as S
+
+    cfg = dict(S.QWEN3_4B)
+    path = model_file(cfg, args.seed, args.model)
+    B, ctx = args.seqs, args.ctx
+    total = ctx + args.warmup + args.steps + args.prof_steps + 1
+    t = time.time()
+    eng = S.Engine(path, slots=B, ctx=total, max_rows=B)
+    for s in range(B):
+        eng.fill_kv(s, ctx, args.seed)
+    log(f"[bench] engine open + {B} x {ctx} cells in {time.time() - t:.1f}s")
+    seq = np.arange(B, dtype=np.int32)
+    rows = np.arange(B, dtype=np.int32)
+    tok = np.random.default_rng(args.seed).integers(0, eng.V, B).astype(np.int32)
+    pos = np.full(B, ctx, np.int32)
+
+    def step():
+        nonlocal tok
+        tok = eng.step(tok, seq, pos, rows)
+        pos[:] += 1
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    gpu_ms = 0.0
+    for _ in range(args.steps):
+        step()
+        gpu_ms += eng.last_gpu_ms()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    value = B * args.steps / dt
+    log(f"[bench] {args.steps} steps: {dt * 1e3 / args.steps:.3f} ms/step wall, {gpu_ms / args.steps:.3f} ms/step GPU")
+
+    # profiled pass: per-kernel-class time and algorithmic bytes
+    eng.prof(True)
+    for _ in range(args.prof_steps):
+        step()
+    prof = eng.prof_read()
+    eng.prof(False)
+    kernels = {}
+    for name, p in prof.items():
+        if p["launches"]:
+            gbs = p["bytes"] / (p["ms"] * 1e-3) / 1e9
+            kernels[name] = {"ms_per_step": p["ms"] / args.prof_steps, "launches_per_step": p["launches"] / args.prof_steps,
+                             "bytes_per_launch": p["bytes"] / p["launches"], "us_per_launch": 1e3 * p["ms"] / p["launches"],
+                             "GBps": gbs, "frac": gbs * 1e9 / HBM_PEAK}
+    log("[bench] kernels " + json.dumps(kernels))
+    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
+
+    def roof(k):
+        c = kernels[k]
+        return {"kernel": k, "bound": "hbm", "achieved": round(c["GBps"], 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": round(c["frac"], 4), "traffic": None, "bytes_per_launch": round(c["bytes_per_launch"]),
+                "us_per_launch": round(c["us_per_launch"], 2)}
+
+    eng.close()
+    cpu = None
+    if not args.no_cpu:
+        t = time.time()
+        cpu = cpu_baseline(path, B, ctx, args.seed)
+        log(f"[bench] cpu baseline in {time.time() - t:.1f}s: {cpu['value']:.2f} tok/s")
+    line = {
+        "metric": "agg decode tok/s, Qwen3-4B-arch Q4_0 x32 seqs; Q4_0 GEMV % HBM peak",
+        "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "q4_0 x q8_0 -> f32 (fp16 MFMA); f16 KV, f32 softmax",
+        "data": "synthetic: random-init weights (seeded), random token ids, seeded N(0,1) fp16 context cells",
+        "config": {"workload": "Qwen3-4B-arch Q4_0 batched decode step (BASELINE.json configs[2])", "seqs": B,
+                   "ctx": ctx, "layers": cfg["n_layer"], "hidden": cfg["n_embd"], "heads": cfg["n_head"],
+                   "kv_heads": cfg["n_head_kv"], "ffn": cfg["n_ff"], "vocab": cfg["n_vocab"], "page_cells": 64,
+                   "gpu_ms_per_step": round(gpu_ms / args.steps, 4)},
+        "roofline": roof(dom),
+        "roofline_gemm": roof("gemm") if "gemm" in kernels else None,
+        "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,44 @@
+// sn_ext.h — engine calls beyond sn.h: per-kernel GPU timing of steps (the role of the reference's SN_PROF switch,
+// core.h:232-302 / sn_load.inc.h:49-61, which gives every kernel of a step its own timestamps summed by name) and a
+// readback of a step's row buffers for stage-by-stage checks. None of these changes what a step computes.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#include "sn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// kernel classes of a step
+enum {
+    SNX_K_GEMM = 0,   // Q4_0 x Q8_0 matmuls (q/k/v, o, gate/up, down, LM head) incl. their k-slice reductions
+    SNX_K_ATTN = 1,   // paged attention: partials and merge
+    SNX_K_QUANT = 2,  // Q8_0 activation quantizers (with the RMSNorm fused in front)
+    SNX_K_ROPE = 3,   // QK-norm + RoPE + K/V cache write
+    SNX_K_OTHER = 4,  // embedding, argmax, copies
+    SNX_K_COUNT = 5
+};
+
+// Profiling on (resets the counters) or off. While on, every launch of a step is bracketed by HIP events on the
+// engine's stream, so steps take slightly longer; the tokens are the same.
+void snx_prof(sn_engine* e, int on);
+// The totals since profiling was turned on for one class: GPU milliseconds, launches, and the algorithmic bytes those
+// launches move (matmul: Q4_0 weights + fp32 input rows + fp32 output rows; attention: the fp16 K/V cells each
+// (sequence, KV head) reads once + q + output + page-table entries). 0, or -1 for an unknown class.
+int snx_prof_read(const sn_engine* e, int kind, double* ms, int* launches, double* bytes);
+
+// Give slot `slot` the cells [0, n) (pages as a step would take them) holding seeded N(0, 1) fp16 K and V in every
+// layer: a context "already in the cache" for throughput runs (what the cells hold does not change what a step
+// costs). The values depend only on (seed, slot, layer, cell). 0, -2 out of pages, or -1 (err).
+int snx_fill_kv(sn_engine* e, int slot, int n, uint64_t seed, char* err, int err_len);
+
+// The last step's row buffers: 0 the residual rows x [R][E], 1 the last layer's q|k|v rows (q after QK-norm and RoPE;
+// k, v as the matmul wrote them) [R][H*128 + 2*KVH*128], 2 its attention output [R][H*128], 3 its SwiGLU output
+// [R][F]. n floats into dst. 0, or -1.
+int snx_debug_read(sn_engine* e, int which, float* dst, size_t n);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,68 @@
+// sn_kernels.h — kernel-level C ABI of libsn_hip.so: the hot kernels of sn_step on caller-owned device memory, for
+// the single-matmul and single-attention configurations, parity tests and roofline timing. Pointers prefixed d_ are
+// device pointers; `stream` is a hipStream_t (NULL: the default stream). All calls are asynchronous on `stream`
+// unless stated. Each entry names the reference kernel it stands for.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// ---- Q4_0 x Q8_0 matmul: Y[m][n] (+)= sum_k X[m][k] W[n][k] ----------------------------------------------------------
+// Replaces the Q4_0 mat-vec / few-row / block matmuls dispatched by mm() (core_mm.inc.h:307-325; kernels.metal:1324-1411,
+// :1413-1490, :746-1007) with ggml CPU numerics (Q8_0 activations, integer block sums).
+enum { SNK_EPI_STORE = 0, SNK_EPI_ADD = 1, SNK_EPI_SWIGLU = 2 };
+
+// bytes of a matrix of N rows x K (K % 32 == 0) in the stripe layout; GGUF Q4_0 rows -> stripes
+size_t snk_q4_stripes_bytes(int N, int K);
+int snk_q4_repack(const void* d_q4, int N, int K, void* d_stripes, void* stream);
+// the stripes dequantized back to fp32 [N][K] with the matmul's own unpack (d * (q - 8)): for the bit-exactness check
+// against ggml's dequantize_row_q4_0
+int snk_q4_dequant(const void* d_stripes, int N, int K, float* d_w, void* stream);
+// activation operand: M fp32 rows (ldx apart) quantized to Q8_0 (ggml x86 quantize_row_q8_0), RMS-normed by d_norm_w
+// first when it is not NULL (the rmsnorm of kernels.metal:121-140 fused in front)
+size_t snk_xa_bytes(int M, int K);
+int snk_quant_act(const float* d_x, int M, int K, int ldx, const float* d_norm_w, float eps, void* d_xa, void* stream);
+// the matmul; epi: store, add into d_y, or SwiGLU over interleaved gate/up stripe pairs (N = 2F, output F columns).
+// d_ws: k-slice partials of snk_q4_workspace_bytes(M, N, K) bytes (may be 0). 0, or -1 (workspace too small).
+size_t snk_q4_workspace_bytes(int M, int N, int K);
+int snk_q4_gemm(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi, void* d_ws,
+                size_t ws_bytes, void* stream);
+// average device time (microseconds) of one matmul launch over `iters` launches timed with HIP events on `stream`,
+// the weights taken from n_copies stripe copies in turn (copies beyond the 256 MB Infinity Cache keep the reads in HBM).
+// Synchronous.
+double snk_q4_gemm_time(const void* const* d_stripes, int n_copies, const void* d_xa, int M, int N, int K, float* d_y,
+                        int ldy, void* d_ws, size_t ws_bytes, int iters, void* stream);
+
+// ---- paged GQA attention (decode and verify rows) -------------------------------------------------------------------
+// Replaces attn_part + attn_merge (kernels.metal:1122-1192) and fa2 (kernels.metal:2674-2770). q: [rows][H][128] fp32
+// (ldq floats apart); K/V pool fp16, page p of KV head h at pool + ((p * KVH + h) * page_cells) * 128; d_pt:
+// [sequences][max_pages] int32; out: [rows][ldo] fp32. Row r of sequence seq[r] attends cells 0 .. pos[r].
+typedef struct snk_attn snk_attn;
+// the work list of a set of rows (host arrays), built once and reused by snk_attn_run; NULL on failure (err)
+snk_attn* snk_attn_new(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH, int max_pages,
+                       int page_cells, char* err, int err_len);
+int snk_attn_run(snk_attn* p, const float* d_q, int ldq, const void* d_kpool, const void* d_vpool, const int32_t* d_pt,
+                 float scale, float* d_out, int ldo, void* stream);
+// average device time (microseconds) of one run (partials + merge) over `iters` runs (HIP events); synchronous
+double snk_attn_time(snk_attn* p, const float* d_q, int ldq, const void* d_kpool, const void* d_vpool,
+                     const int32_t* d_pt, float scale, float* d_out, int ldo, int iters, void* stream);
+void snk_attn_free(snk_attn* p);
+
+// ---- per-head QK-norm + NEOX RoPE + K/V cache write (qk_rope, kernels.metal:149-197) -------------------------------
+// d_qkv: R rows of [q: H*128 | k: KVH*128 | v: KVH*128] fp32, ldqkv floats apart; q is normed and rotated in place, k
+// (normed, rotated) and v go to cell pos[r] of sequence seq[r] as fp16. theta_scale = base^(-2/128) (computed by the
+// caller in fp32, as ggml does); theta_i = pos * theta_scale^i by i successive fp32 multiplies.
+int snk_qk_rope(float* d_qkv, int ldqkv, int R, int H, int KVH, const float* d_qw, const float* d_kw, float eps,
+                float theta_scale, const int32_t* d_seq, const int32_t* d_pos, const int32_t* d_pt, int max_pages,
+                int page_cells, void* d_kpool, void* d_vpool, void* stream);
+
+// ---- MFMA operand layout check: D = A . B for one v_mfma_f32_16x16x32_f16 (A, B as 64 lanes x 8 fp16 each, D as 64
+// lanes x 4 fp32), the raw lane contents in and out
+int snk_mfma_probe(const void* d_a, const void* d_b, float* d_d, void* stream);
+
+#ifdef __cplusplus
+}
+#endif

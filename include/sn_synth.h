@@ -1,0 +1,29 @@
+// sn_synth.h — synthetic random-init models for the benchmarks and tests (a tool beside the engine, not a hot-path
+// entry point). It stands where the reference's tests build a model file with sllm-core's testutil.rs tiny_model
+// (engine/sllm-core/src/testutil.rs:22-162); the configs' models are random-init, so the file is generated.
+#pragma once
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+    int n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab;
+    int n_expert, n_expert_used, n_ff_exp;  // > 0: a qwen3moe model (experts in every layer)
+    int nextn;                              // 1: one multi-token-prediction layer after the model's own (blk.<n_layer>)
+    float rope_base, eps;
+    float w_std;    // std of the Q4_0 matrices before quantization (configs: 0.02)
+    float emb_std;  // std of the fp32 embedding table
+} snx_model_cfg;
+
+// Write the model to `path` (GGUF v3; Q4_0 matrices quantized with ggml's quantize_row_q4_0_ref; norms 1 + N(0, 0.1)).
+// nthreads <= 0: all cores. The bytes depend only on (cfg, seed). 0, or -1 with the reason in err.
+int snx_write_model(const char* path, const snx_model_cfg* cfg, uint64_t seed, int nthreads, char* err, int err_len);
+
+// ggml quantize_row_q4_0_ref of k values (k % 32 == 0): 18-byte blocks into y.
+void snx_quantize_q4_0(const float* x, uint8_t* y, int64_t k);
+
+#ifdef __cplusplus
+}
+#endif

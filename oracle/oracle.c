@@ -1,0 +1,482 @@
+// CPU oracle (test infrastructure only; see oracle.h for what each function restates and where it is cited).
+// Built with -ffp-contract=off so every float expression rounds exactly as written.
+#include "oracle.h"
+
+#include <immintrin.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define QK 32
+
+static int nthr(int n) {
+#ifdef _OPENMP
+    return n > 0 ? n : omp_get_max_threads();
+#else
+    (void) n;
+    return 1;
+#endif
+}
+
+// ---- fp16: F16C round-to-nearest-even conversion (ggml's GGML_FP32_TO_FP16 on x86) ----
+uint16_t or_f32_to_f16(float f) { return (uint16_t) _cvtss_sh(f, _MM_FROUND_TO_NEAREST_INT); }
+float or_f16_to_f32(uint16_t h) { return _cvtsh_ss(h); }
+
+static float h2f(const uint8_t* p) {
+    uint16_t h;
+    memcpy(&h, p, 2);
+    return or_f16_to_f32(h);
+}
+static void f2h_store(uint8_t* p, float f) {
+    const uint16_t h = or_f32_to_f16(f);
+    memcpy(p, &h, 2);
+}
+
+// ---- Q4_0: ggml quantize_row_q4_0_ref. The element of largest |x| (the first on ties) maps to q = 0:
+// d = max / -8, id = 1/d, q = min(15, (int8)(x*id + 8.5)) (truncation toward zero), d stored fp16.
+void or_quantize_row_q4_0(const float* x, uint8_t* y, int64_t k) {
+    const int64_t nb = k / QK;
+    for (int64_t i = 0; i < nb; i++) {
+        const float* xb = x + i * QK;
+        uint8_t* yb = y + i * 18;
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < QK; j++) {
+            const float v = xb[j];
+            if (amax < fabsf(v)) {
+                amax = fabsf(v);
+                max = v;
+            }
+        }
+        const float d = max / -8;
+        const float id = d ? 1.0f / d : 0.0f;
+        f2h_store(yb, d);
+        for (int j = 0; j < QK / 2; ++j) {
+            const float x0 = xb[j] * id;
+            const float x1 = xb[QK / 2 + j] * id;
+            int8_t t0 = (int8_t) (x0 + 8.5f), t1 = (int8_t) (x1 + 8.5f);
+            const uint8_t xi0 = (uint8_t) (t0 < 15 ? t0 : 15);
+            const uint8_t xi1 = (uint8_t) (t1 < 15 ? t1 : 15);
+            yb[2 + j] = (uint8_t) (xi0 | (xi1 << 4));
+        }
+    }
+}
+
+// ggml dequantize_row_q4_0: y[j] = (qs[j] & 15 - 8) * d, y[j + 16] = (qs[j] >> 4 - 8) * d
+// (patch 0001:543-565 restates the same loop; kernels.metal:21-28 is the GPU form)
+void or_dequantize_row_q4_0(const uint8_t* x, float* y, int64_t k) {
+    const int64_t nb = k / QK;
+    for (int64_t i = 0; i < nb; i++) {
+        const uint8_t* b = x + i * 18;
+        const float d = h2f(b);
+        for (int j = 0; j < QK / 2; ++j) {
+            const int x0 = (b[2 + j] & 0x0F) - 8;
+            const int x1 = (b[2 + j] >> 4) - 8;
+            y[i * QK + j] = x0 * d;
+            y[i * QK + j + QK / 2] = x1 * d;
+        }
+    }
+}
+
+// ggml x86 quantize_row_q8_0 (the activations of every Q4_0 mul_mat on the CPU backend): per 32-block,
+// amax = max |x|, d = amax / 127 (stored fp16), id = 127 / amax (0 when amax is 0), q = round-half-even(x * id).
+void or_quantize_row_q8_0(const float* x, uint8_t* y, int64_t k) {
+    const int64_t nb = k / QK;
+    for (int64_t i = 0; i < nb; i++) {
+        const float* xb = x + i * QK;
+        uint8_t* yb = y + i * 34;
+        float amax = 0.0f;
+        for (int j = 0; j < QK; j++) amax = fmaxf(amax, fabsf(xb[j]));
+        const float d = amax / 127.f;
+        const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+        f2h_store(yb, d);
+        for (int j = 0; j < QK; ++j) {
+            const float v = xb[j] * id;
+            yb[2 + j] = (uint8_t) (int8_t) (int) nearbyintf(v);
+        }
+    }
+}
+
+void or_dequantize_row_q8_0(const uint8_t* x, float* y, int64_t k) {
+    const int64_t nb = k / QK;
+    for (int64_t i = 0; i < nb; i++) {
+        const uint8_t* b = x + i * 34;
+        const float d = h2f(b);
+        for (int j = 0; j < QK; ++j) y[i * QK + j] = (int8_t) b[2 + j] * d;
+    }
+}
+
+// ggml_vec_dot_q4_0_q8_0 (generic form): per block the integer sum of (q4 - 8) * q8, then sumf += sumi * dw * dx
+float or_vec_dot_q4_0_q8_0(int64_t k, const uint8_t* w, const uint8_t* xq) {
+    const int64_t nb = k / QK;
+    float sumf = 0.0f;
+    for (int64_t ib = 0; ib < nb; ++ib) {
+        const uint8_t* bw = w + ib * 18;
+        const uint8_t* bx = xq + ib * 34;
+        int sumi0 = 0, sumi1 = 0;
+        for (int j = 0; j < QK / 2; ++j) {
+            const int v0 = (bw[2 + j] & 0x0F) - 8;
+            const int v1 = (bw[2 + j] >> 4) - 8;
+            sumi0 += v0 * (int8_t) bx[2 + j];
+            sumi1 += v1 * (int8_t) bx[2 + j + QK / 2];
+        }
+        const int sumi = sumi0 + sumi1;
+        sumf += sumi * h2f(bw) * h2f(bx);
+    }
+    return sumf;
+}
+
+void or_mul_mat_q4_0(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nthreads) {
+    const int64_t nb = K / QK;
+    uint8_t* xq = (uint8_t*) malloc((size_t) (M * nb * 34));
+    for (int64_t m = 0; m < M; ++m) or_quantize_row_q8_0(X + m * K, xq + m * nb * 34, K);
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t m = 0; m < M; ++m) Y[m * N + n] = or_vec_dot_q4_0_q8_0(K, W + n * nb * 18, xq + m * nb * 34);
+    free(xq);
+}
+
+void or_mul_mat_q4_0_f64(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, double* Y, int nthreads) {
+    const int64_t nb = K / QK;
+#pragma omp parallel num_threads(nthr(nthreads))
+    {
+        float* row = (float*) malloc((size_t) K * sizeof(float));
+#pragma omp for schedule(static)
+        for (int64_t n = 0; n < N; ++n) {
+            or_dequantize_row_q4_0(W + n * nb * 18, row, K);
+            for (int64_t m = 0; m < M; ++m) {
+                double s = 0.0;
+                for (int64_t k = 0; k < K; ++k) s += (double) row[k] * (double) X[m * K + k];
+                Y[m * N + n] = s;
+            }
+        }
+        free(row);
+    }
+}
+
+// ---- elementwise ----
+// ggml rms_norm (squares summed in double) followed by the weight multiply: y = (x * scale) * w
+void or_rmsnorm(const float* x, const float* w, int64_t n, float eps, float* y) {
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; i++) sum += (double) (x[i] * x[i]);
+    const float mean = (float) (sum / n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t i = 0; i < n; i++) y[i] = (x[i] * scale) * (w ? w[i] : 1.0f);
+}
+
+float or_silu(float x) { return x / (1.0f + expf(-x)); }
+
+int32_t or_argmax(const float* x, int64_t n, const int32_t* ban, int nban) {
+    float best = -INFINITY;
+    int32_t idx = -1;
+    for (int64_t i = 0; i < n; i++) {
+        int banned = 0;
+        for (int b = 0; b < nban; ++b) banned |= ban[b] == i;
+        if (!banned && (idx < 0 || x[i] > best)) {  // strictly greater: an equal score keeps the lower id
+            best = x[i];
+            idx = (int32_t) i;
+        }
+    }
+    return idx;
+}
+
+void or_top2(const float* x, int64_t n, int32_t* i1, float* v1, int32_t* i2, float* v2, float* lse) {
+    float m1 = -INFINITY, m2 = -INFINITY;
+    int32_t a = 0x7fffffff, b = 0x7fffffff;
+    for (int64_t i = 0; i < n; i++) {
+        if (x[i] > m1) {
+            m2 = m1;
+            b = a;
+            m1 = x[i];
+            a = (int32_t) i;
+        } else if (x[i] > m2) {
+            m2 = x[i];
+            b = (int32_t) i;
+        }
+    }
+    double s = 0.0;
+    for (int64_t i = 0; i < n; i++) s += exp((double) x[i] - (double) m1);
+    *i1 = a;
+    *v1 = m1;
+    *i2 = b;
+    *v2 = m2;
+    *lse = (float) ((double) m1 + log(s));
+}
+
+// ggml_rope_cache_init with ext_factor 0, freq_scale 1, mscale 1: theta starts at p and is multiplied by theta_scale
+// after each pair, in fp32
+void or_rope_cache(int32_t pos, float theta_scale, int D, float* cs) {
+    float theta = (float) pos;
+    for (int i = 0; i < D / 2; ++i) {
+        cs[2 * i] = cosf(theta);
+        cs[2 * i + 1] = sinf(theta);
+        theta *= theta_scale;
+    }
+}
+
+void or_qk_norm_rope(float* x, const float* w, int D, float eps, const float* cs, int do_norm) {
+    if (do_norm) or_rmsnorm(x, w, D, eps, x);
+    for (int i = 0; i < D / 2; ++i) {
+        const float c = cs[2 * i], s = cs[2 * i + 1];
+        const float x0 = x[i], x1 = x[i + D / 2];
+        x[i] = x0 * c - x1 * s;
+        x[i + D / 2] = x0 * s + x1 * c;
+    }
+}
+
+// ---- attention over a list of cells (cell c's K head vector at kp[c], V at vp[c]) ----
+static void attn_cells(const float* q, int D, int n, const uint16_t* const* kp, const uint16_t* const* vp, float scale,
+                       float* out, int f64) {
+    if (n <= 0) {
+        for (int d = 0; d < D; ++d) out[d] = 0.0f;
+        return;
+    }
+    if (f64) {
+        double* s = (double*) malloc((size_t) n * sizeof(double));
+        double m = -INFINITY;
+        for (int c = 0; c < n; ++c) {
+            double t = 0.0;
+            for (int d = 0; d < D; ++d) t += (double) q[d] * (double) or_f16_to_f32(kp[c][d]);
+            s[c] = t * (double) scale;
+            if (s[c] > m) m = s[c];
+        }
+        double l = 0.0;
+        for (int c = 0; c < n; ++c) {
+            s[c] = exp(s[c] - m);
+            l += s[c];
+        }
+        for (int d = 0; d < D; ++d) {
+            double o = 0.0;
+            for (int c = 0; c < n; ++c) o += s[c] * (double) or_f16_to_f32(vp[c][d]);
+            out[d] = (float) (o / l);
+        }
+        free(s);
+        return;
+    }
+    float* s = (float*) malloc((size_t) n * sizeof(float));
+    float m = -INFINITY;
+    for (int c = 0; c < n; ++c) {
+        float t = 0.0f;
+        for (int d = 0; d < D; ++d) t += q[d] * or_f16_to_f32(kp[c][d]);
+        s[c] = t * scale;
+        if (s[c] > m) m = s[c];
+    }
+    double l = 0.0;
+    for (int c = 0; c < n; ++c) {
+        s[c] = expf(s[c] - m);
+        l += (double) s[c];
+    }
+    const float il = (float) (1.0 / l);
+    for (int c = 0; c < n; ++c) s[c] *= il;
+    for (int d = 0; d < D; ++d) {
+        float o = 0.0f;
+        for (int c = 0; c < n; ++c) o += s[c] * or_f16_to_f32(vp[c][d]);
+        out[d] = o;
+    }
+    free(s);
+}
+
+static const uint16_t* pool_cell(const uint16_t* pool, const int32_t* pt, int max_pages, int page_cells, int KVH, int D,
+                                 int s, int h, int c) {
+    const int p = pt[(size_t) s * max_pages + c / page_cells];
+    return pool + (((size_t) p * KVH + h) * page_cells + c % page_cells) * D;
+}
+
+void or_paged_attn(const float* q, int nq, const int32_t* qseq, const int32_t* qpos, int H, int KVH, int D,
+                   const uint16_t* kpool, const uint16_t* vpool, int page_cells, const int32_t* pt, int max_pages,
+                   float scale, float* out, int f64, int nthreads) {
+    const int G = H / KVH;
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(dynamic, 1)
+    for (int rh = 0; rh < nq * H; ++rh) {
+        const int r = rh / H, h = rh % H, kh = h / G, n = qpos[r] + 1;
+        const uint16_t** kp = (const uint16_t**) malloc((size_t) n * sizeof(void*));
+        const uint16_t** vp = (const uint16_t**) malloc((size_t) n * sizeof(void*));
+        for (int c = 0; c < n; ++c) {
+            kp[c] = pool_cell(kpool, pt, max_pages, page_cells, KVH, D, qseq[r], kh, c);
+            vp[c] = pool_cell(vpool, pt, max_pages, page_cells, KVH, D, qseq[r], kh, c);
+        }
+        attn_cells(q + ((size_t) r * H + h) * D, D, n, kp, vp, scale, out + ((size_t) r * H + h) * D, f64);
+        free(kp);
+        free(vp);
+    }
+}
+
+void or_paged_attn_chunked(const float* q, int nq, const int32_t* qseq, const int32_t* qpos, int H, int KVH, int D,
+                           const uint16_t* kpool, const uint16_t* vpool, int page_cells, const int32_t* pt,
+                           int max_pages, float scale, int chunk, float* out) {
+    const int G = H / KVH;
+    float* acc = (float*) malloc((size_t) D * sizeof(float));
+    float* pa = (float*) malloc((size_t) D * sizeof(float));
+    for (int r = 0; r < nq; ++r)
+        for (int h = 0; h < H; ++h) {
+            const int kh = h / G, n = qpos[r] + 1;
+            const float* qh = q + ((size_t) r * H + h) * D;
+            float M = -INFINITY, L = 0.0f;
+            for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+            for (int c0 = 0; c0 < n; c0 += chunk) {
+                const int c1 = c0 + chunk < n ? c0 + chunk : n;
+                // the chunk's partial: its own max, sum and unnormalised accumulator
+                float m = -INFINITY, l = 0.0f;
+                for (int d = 0; d < D; ++d) pa[d] = 0.0f;
+                float* s = (float*) malloc((size_t) (c1 - c0) * sizeof(float));
+                for (int c = c0; c < c1; ++c) {
+                    const uint16_t* kc = pool_cell(kpool, pt, max_pages, page_cells, KVH, D, qseq[r], kh, c);
+                    float t = 0.0f;
+                    for (int d = 0; d < D; ++d) t += qh[d] * or_f16_to_f32(kc[d]);
+                    s[c - c0] = t * scale;
+                    if (s[c - c0] > m) m = s[c - c0];
+                }
+                for (int c = c0; c < c1; ++c) {
+                    const uint16_t* vc = pool_cell(vpool, pt, max_pages, page_cells, KVH, D, qseq[r], kh, c);
+                    const float p = expf(s[c - c0] - m);
+                    l += p;
+                    for (int d = 0; d < D; ++d) pa[d] += p * or_f16_to_f32(vc[d]);
+                }
+                free(s);
+                // merged in chunk order (attn_merge)
+                const float mn = M > m ? M : m;
+                const float e0 = expf(M - mn), e1 = expf(m - mn);
+                for (int d = 0; d < D; ++d) acc[d] = acc[d] * e0 + pa[d] * e1;
+                L = L * e0 + l * e1;
+                M = mn;
+            }
+            for (int d = 0; d < D; ++d) out[((size_t) r * H + h) * D + d] = n > 0 ? acc[d] / L : 0.0f;
+        }
+    free(acc);
+    free(pa);
+}
+
+// ---- MoE routing (moe_topk, mode 0) ----
+void or_moe_route(const float* logits, int n_expert, int k, int32_t* ids, float* w) {
+    float m = -INFINITY;
+    for (int i = 0; i < n_expert; ++i) m = fmaxf(m, logits[i]);
+    float* p = (float*) malloc((size_t) n_expert * sizeof(float));
+    float tot = 0.0f;
+    for (int i = 0; i < n_expert; ++i) {
+        p[i] = expf(logits[i] - m);
+        tot += p[i];
+    }
+    float sel = 0.0f;
+    for (int j = 0; j < k; ++j) {
+        int bi = -1;
+        for (int i = 0; i < n_expert; ++i)
+            if (bi < 0 || p[i] > p[bi]) bi = i;
+        ids[j] = bi;
+        w[j] = p[bi] / tot;
+        sel += w[j];
+        p[bi] = -INFINITY;
+    }
+    sel = fmaxf(sel, 6.103515625e-5f);
+    for (int j = 0; j < k; ++j) w[j] = w[j] / sel;
+    free(p);
+}
+
+int or_accept(const int32_t* draft, const int32_t* target, int k) {
+    int a = 0;
+    while (a < k && draft[a] == target[a]) ++a;
+    return a;
+}
+
+// ---- the Qwen3 step ----
+static void mm(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nt) {
+    or_mul_mat_q4_0(W, N, K, X, M, Y, nt);
+}
+
+void or_qwen3_step(const or_qwen3* m, or_kv* kv, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos,
+                   int n_out, const int32_t* out_rows, float* logits, float* hidden, int32_t* out_tok, int nthreads) {
+    const int E = m->n_embd, H = m->n_head, KVH = m->n_head_kv, D = m->head_dim, F = m->n_ff, V = m->n_vocab;
+    const int QD = H * D, KD = KVH * D, G = H / KVH;
+    const float theta_scale = powf(m->rope_base, -2.0f / D);
+    const float scale = 1.0f / sqrtf((float) D);
+    float* x = (float*) malloc((size_t) R * E * 4);
+    float* h = (float*) malloc((size_t) R * E * 4);
+    float* q = (float*) malloc((size_t) R * QD * 4);
+    float* k = (float*) malloc((size_t) R * KD * 4);
+    float* v = (float*) malloc((size_t) R * KD * 4);
+    float* ao = (float*) malloc((size_t) R * QD * 4);
+    float* y = (float*) malloc((size_t) R * (E > QD ? E : QD) * 4);
+    const int FF = F > m->n_ff_exp ? F : m->n_ff_exp;
+    float* g = (float*) malloc((size_t) R * FF * 4);
+    float* u = (float*) malloc((size_t) R * FF * 4);
+    float* cs = (float*) malloc((size_t) R * D * 4);
+    for (int r = 0; r < R; ++r) {
+        memcpy(x + (size_t) r * E, m->tok_embd + (size_t) tok[r] * E, (size_t) E * 4);
+        or_rope_cache(pos[r], theta_scale, D, cs + (size_t) r * D);
+    }
+    const size_t lstride = (size_t) kv->ctx * KD;  // one layer of one sequence
+    for (int il = 0; il < m->n_layer; ++il) {
+        const or_layer* L = &m->layers[il];
+        for (int r = 0; r < R; ++r) or_rmsnorm(x + (size_t) r * E, L->attn_norm, E, m->eps, h + (size_t) r * E);
+        mm(L->wq, QD, E, h, R, q, nthreads);
+        mm(L->wk, KD, E, h, R, k, nthreads);
+        mm(L->wv, KD, E, h, R, v, nthreads);
+        for (int r = 0; r < R; ++r) {
+            for (int hh = 0; hh < H; ++hh) or_qk_norm_rope(q + (size_t) r * QD + hh * D, L->q_norm, D, m->eps, cs + (size_t) r * D, 1);
+            for (int hh = 0; hh < KVH; ++hh) or_qk_norm_rope(k + (size_t) r * KD + hh * D, L->k_norm, D, m->eps, cs + (size_t) r * D, 1);
+            // the row's cell: K and V in fp16
+            const size_t base = ((size_t) seq[r] * m->n_layer + il) * lstride + (size_t) pos[r] * KD;
+            for (int i = 0; i < KD; ++i) {
+                kv->k[base + i] = or_f32_to_f16(k[(size_t) r * KD + i]);
+                kv->v[base + i] = or_f32_to_f16(v[(size_t) r * KD + i]);
+            }
+        }
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(dynamic, 1)
+        for (int rh = 0; rh < R * H; ++rh) {
+            const int r = rh / H, hh = rh % H, kh = hh / G, n = pos[r] + 1;
+            const size_t base = ((size_t) seq[r] * m->n_layer + il) * lstride;
+            const uint16_t** kp = (const uint16_t**) malloc((size_t) n * sizeof(void*));
+            const uint16_t** vp = (const uint16_t**) malloc((size_t) n * sizeof(void*));
+            for (int c = 0; c < n; ++c) {
+                kp[c] = kv->k + base + (size_t) c * KD + (size_t) kh * D;
+                vp[c] = kv->v + base + (size_t) c * KD + (size_t) kh * D;
+            }
+            attn_cells(q + (size_t) r * QD + hh * D, D, n, kp, vp, scale, ao + (size_t) r * QD + hh * D, 0);
+            free(kp);
+            free(vp);
+        }
+        mm(L->wo, E, QD, ao, R, y, nthreads);
+        for (size_t i = 0; i < (size_t) R * E; ++i) x[i] += y[i];
+        for (int r = 0; r < R; ++r) or_rmsnorm(x + (size_t) r * E, L->ffn_norm, E, m->eps, h + (size_t) r * E);
+        if (m->n_expert > 0) {
+            const int NE = m->n_expert, K = m->n_expert_used, FE = m->n_ff_exp;
+            const size_t gsz = (size_t) FE * (E / QK) * 18, dsz = (size_t) E * (FE / QK) * 18;
+            for (int r = 0; r < R; ++r) {
+                float* lg = (float*) malloc((size_t) NE * 4);
+                int32_t ids[64];
+                float w[64];
+                for (int e = 0; e < NE; ++e) {
+                    float s = 0.0f;
+                    for (int i = 0; i < E; ++i) s += m->layers[il].router[(size_t) e * E + i] * h[(size_t) r * E + i];
+                    lg[e] = s;
+                }
+                or_moe_route(lg, NE, K, ids, w);
+                float* acc = (float*) calloc((size_t) E, 4);
+                for (int j = 0; j < K; ++j) {
+                    mm(L->eg + ids[j] * gsz, FE, E, h + (size_t) r * E, 1, g, nthreads);
+                    mm(L->eu + ids[j] * gsz, FE, E, h + (size_t) r * E, 1, u, nthreads);
+                    for (int i = 0; i < FE; ++i) g[i] = or_silu(g[i]) * u[i];
+                    mm(L->ed + ids[j] * dsz, E, FE, g, 1, y, nthreads);
+                    for (int i = 0; i < E; ++i) acc[i] += w[j] * y[i];
+                }
+                for (int i = 0; i < E; ++i) x[(size_t) r * E + i] += acc[i];
+                free(acc);
+                free(lg);
+            }
+        } else {
+            mm(L->wg, F, E, h, R, g, nthreads);
+            mm(L->wu, F, E, h, R, u, nthreads);
+            for (size_t i = 0; i < (size_t) R * F; ++i) g[i] = or_silu(g[i]) * u[i];
+            mm(L->wd, E, F, g, R, y, nthreads);
+            for (size_t i = 0; i < (size_t) R * E; ++i) x[i] += y[i];
+        }
+    }
+    float* ho = (float*) malloc((size_t) (n_out > 0 ? n_out : 1) * E * 4);
+    for (int j = 0; j < n_out; ++j) or_rmsnorm(x + (size_t) out_rows[j] * E, m->output_norm, E, m->eps, ho + (size_t) j * E);
+    if (hidden) memcpy(hidden, ho, (size_t) n_out * E * 4);
+    if (n_out > 0) mm(m->output, V, E, ho, n_out, logits, nthreads);
+    for (int j = 0; j < n_out; ++j) out_tok[j] = or_argmax(logits + (size_t) j * V, V, NULL, 0);
+    free(ho);
+    free(x); free(h); free(q); free(k); free(v); free(ao); free(y); free(g); free(u); free(cs);
+}

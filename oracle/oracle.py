@@ -1,0 +1,298 @@
+"""ctypes face of the CPU oracle (oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, never by the
+product package. Every function restates the reference's (or ggml's) arithmetic; oracle.h names the file:line each
+follows.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+P = C.c_void_p
+I64 = C.c_int64
+
+
+def _declare(L):
+    L.or_f32_to_f16.argtypes = [C.c_float]
+    L.or_f32_to_f16.restype = C.c_uint16
+    L.or_f16_to_f32.argtypes = [C.c_uint16]
+    L.or_f16_to_f32.restype = C.c_float
+    for f in ("or_quantize_row_q4_0", "or_dequantize_row_q4_0", "or_quantize_row_q8_0", "or_dequantize_row_q8_0"):
+        getattr(L, f).argtypes = [P, P, I64]
+        getattr(L, f).restype = None
+    L.or_vec_dot_q4_0_q8_0.argtypes = [I64, P, P]
+    L.or_vec_dot_q4_0_q8_0.restype = C.c_float
+    L.or_mul_mat_q4_0.argtypes = [P, I64, I64, P, I64, P, C.c_int]
+    L.or_mul_mat_q4_0_f64.argtypes = [P, I64, I64, P, I64, P, C.c_int]
+    L.or_rmsnorm.argtypes = [P, P, I64, C.c_float, P]
+    L.or_silu.argtypes = [C.c_float]
+    L.or_silu.restype = C.c_float
+    L.or_argmax.argtypes = [P, I64, P, C.c_int]
+    L.or_argmax.restype = C.c_int32
+    L.or_top2.argtypes = [P, I64, P, P, P, P, P]
+    L.or_rope_cache.argtypes = [C.c_int32, C.c_float, C.c_int, P]
+    L.or_qk_norm_rope.argtypes = [P, P, C.c_int, C.c_float, P, C.c_int]
+    L.or_paged_attn.argtypes = [P, C.c_int, P, P, C.c_int, C.c_int, C.c_int, P, P, C.c_int, P, C.c_int, C.c_float,
+                                P, C.c_int, C.c_int]
+    L.or_paged_attn_chunked.argtypes = [P, C.c_int, P, P, C.c_int, C.c_int, C.c_int, P, P, C.c_int, P, C.c_int,
+                                        C.c_float, C.c_int, P]
+    L.or_moe_route.argtypes = [P, C.c_int, C.c_int, P, P]
+    L.or_accept.argtypes = [P, P, C.c_int]
+    L.or_accept.restype = C.c_int
+    L.or_qwen3_step.argtypes = [P, P, C.c_int, P, P, P, C.c_int, P, P, P, P, C.c_int]
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ---- fp16 ----
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    """RNE fp16 bits (uint16) of fp32 values, via the oracle's F16C conversion."""
+    x = np.ascontiguousarray(x, np.float32)
+    return np.array([lib().or_f32_to_f16(float(v)) for v in x.ravel()], np.uint16).reshape(x.shape)
+
+
+# ---- Q4_0 / Q8_0 ----
+def quantize_q4_0(w: np.ndarray) -> np.ndarray:
+    """[N][K] fp32 -> [N][K/32*18] uint8 (ggml quantize_row_q4_0_ref per row)."""
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    out = np.empty((N, K // 32 * 18), np.uint8)
+    lib().or_quantize_row_q4_0(_p(w), _p(out), N * K)
+    return out
+
+
+def dequantize_q4_0(q: np.ndarray, K: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.uint8)
+    N = q.size // (K // 32 * 18)
+    out = np.empty((N, K), np.float32)
+    lib().or_dequantize_row_q4_0(_p(q), _p(out), N * K)
+    return out
+
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    M, K = x.shape
+    out = np.empty((M, K // 32 * 34), np.uint8)
+    lib().or_quantize_row_q8_0(_p(x), _p(out), M * K)
+    return out
+
+
+def dequantize_q8_0(q: np.ndarray, K: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.uint8)
+    M = q.size // (K // 32 * 34)
+    out = np.empty((M, K), np.float32)
+    lib().or_dequantize_row_q8_0(_p(q), _p(out), M * K)
+    return out
+
+
+def mul_mat_q4_0(Wq: np.ndarray, K: int, X: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    """Y[M][N] = X[M][K] . W[N][K]^T, ggml CPU semantics (Q8_0 activations, integer block dots)."""
+    Wq = np.ascontiguousarray(Wq, np.uint8)
+    X = np.ascontiguousarray(X, np.float32)
+    N = Wq.size // (K // 32 * 18)
+    M = X.shape[0]
+    Y = np.empty((M, N), np.float32)
+    lib().or_mul_mat_q4_0(_p(Wq), N, K, _p(X), M, _p(Y), nthreads)
+    return Y
+
+
+def mul_mat_q4_0_f64(Wq: np.ndarray, K: int, X: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    Wq = np.ascontiguousarray(Wq, np.uint8)
+    X = np.ascontiguousarray(X, np.float32)
+    N = Wq.size // (K // 32 * 18)
+    M = X.shape[0]
+    Y = np.empty((M, N), np.float64)
+    lib().or_mul_mat_q4_0_f64(_p(Wq), N, K, _p(X), M, _p(Y), nthreads)
+    return Y
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray | None, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    wp = None if w is None else _p(np.ascontiguousarray(w, np.float32))
+    n = x.shape[-1]
+    for i in range(x.size // n):
+        lib().or_rmsnorm(C.c_void_p(x.ctypes.data + 4 * n * i), wp, n, eps, C.c_void_p(y.ctypes.data + 4 * n * i))
+    return y
+
+
+def argmax(x: np.ndarray, ban=()) -> int:
+    x = np.ascontiguousarray(x, np.float32)
+    b = np.ascontiguousarray(np.array(ban, np.int32))
+    return int(lib().or_argmax(_p(x), x.size, _p(b) if len(ban) else None, len(ban)))
+
+
+def top2(x: np.ndarray):
+    x = np.ascontiguousarray(x, np.float32)
+    i1, i2 = C.c_int32(), C.c_int32()
+    v1, v2, lse = C.c_float(), C.c_float(), C.c_float()
+    lib().or_top2(_p(x), x.size, C.byref(i1), C.byref(v1), C.byref(i2), C.byref(v2), C.byref(lse))
+    return i1.value, v1.value, i2.value, v2.value, lse.value
+
+
+def rope_cache(pos: int, theta_scale: float, D: int) -> np.ndarray:
+    cs = np.empty(D, np.float32)
+    lib().or_rope_cache(pos, theta_scale, D, _p(cs))
+    return cs
+
+
+def qk_norm_rope(x: np.ndarray, w: np.ndarray, eps: float, cs: np.ndarray, do_norm: bool = True) -> np.ndarray:
+    y = np.array(x, np.float32, copy=True)
+    lib().or_qk_norm_rope(_p(y), _p(np.ascontiguousarray(w, np.float32)), y.size, eps, _p(cs), int(do_norm))
+    return y
+
+
+def paged_attn(q, qseq, qpos, KVH, kpool, vpool, page_cells, pt, scale, f64=False, nthreads=0):
+    """q: [nq][H][D] fp32; kpool/vpool: uint16 fp16 bits [pages][KVH][page_cells][D]; pt: [S][max_pages] int32."""
+    q = np.ascontiguousarray(q, np.float32)
+    nq, H, D = q.shape
+    out = np.empty_like(q)
+    qs = np.ascontiguousarray(qseq, np.int32)
+    qp = np.ascontiguousarray(qpos, np.int32)
+    pt = np.ascontiguousarray(pt, np.int32)
+    lib().or_paged_attn(_p(q), nq, _p(qs), _p(qp), H, KVH, D, _p(np.ascontiguousarray(kpool)),
+                        _p(np.ascontiguousarray(vpool)), page_cells, _p(pt), pt.shape[1], scale, _p(out), int(f64),
+                        nthreads)
+    return out
+
+
+def paged_attn_chunked(q, qseq, qpos, KVH, kpool, vpool, page_cells, pt, scale, chunk):
+    q = np.ascontiguousarray(q, np.float32)
+    nq, H, D = q.shape
+    out = np.empty_like(q)
+    qs = np.ascontiguousarray(qseq, np.int32)
+    qp = np.ascontiguousarray(qpos, np.int32)
+    pt = np.ascontiguousarray(pt, np.int32)
+    lib().or_paged_attn_chunked(_p(q), nq, _p(qs), _p(qp), H, KVH, D, _p(np.ascontiguousarray(kpool)),
+                                _p(np.ascontiguousarray(vpool)), page_cells, _p(pt), pt.shape[1], scale, chunk,
+                                _p(out))
+    return out
+
+
+def moe_route(logits: np.ndarray, k: int):
+    lg = np.ascontiguousarray(logits, np.float32)
+    ids = np.empty(k, np.int32)
+    w = np.empty(k, np.float32)
+    lib().or_moe_route(_p(lg), lg.size, k, _p(ids), _p(w))
+    return ids, w
+
+
+def accept(draft, target) -> int:
+    d = np.ascontiguousarray(draft, np.int32)
+    t = np.ascontiguousarray(target, np.int32)
+    return int(lib().or_accept(_p(d), _p(t), d.size))
+
+
+# ---- the Qwen3 model step ----
+class _Layer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("attn_norm", "q_norm", "k_norm", "ffn_norm", "wq", "wk", "wv", "wo", "wg",
+                                          "wu", "wd", "router", "eg", "eu", "ed")]
+
+
+class _Model(C.Structure):
+    _fields_ = [("n_layer", C.c_int), ("n_embd", C.c_int), ("n_head", C.c_int), ("n_head_kv", C.c_int),
+                ("head_dim", C.c_int), ("n_ff", C.c_int), ("n_vocab", C.c_int), ("n_expert", C.c_int),
+                ("n_expert_used", C.c_int), ("n_ff_exp", C.c_int), ("eps", C.c_float), ("rope_base", C.c_float),
+                ("tok_embd", C.c_void_p), ("output_norm", C.c_void_p), ("output", C.c_void_p),
+                ("layers", C.POINTER(_Layer))]
+
+
+class _KV(C.Structure):
+    _fields_ = [("n_seq", C.c_int), ("ctx", C.c_int), ("n_layer", C.c_int), ("n_kv", C.c_int),
+                ("head_dim", C.c_int), ("k", C.c_void_p), ("v", C.c_void_p)]
+
+
+class Qwen3:
+    """The oracle's Qwen3 model over a parsed GGUF (oracle.gguf.GGUF) and its own contiguous fp16 KV cache."""
+
+    def __init__(self, gguf, n_seq: int, ctx: int):
+        g = gguf
+        a = g.kv["general.architecture"]
+        self.arch = a
+        self.E = int(g.kv[f"{a}.embedding_length"])
+        self.L = int(g.kv[f"{a}.block_count"])
+        self.H = int(g.kv[f"{a}.attention.head_count"])
+        self.KVH = int(g.kv[f"{a}.attention.head_count_kv"])
+        self.D = int(g.kv.get(f"{a}.attention.key_length", self.E // self.H))
+        self.F = int(g.kv.get(f"{a}.feed_forward_length", 0))
+        self.NE = int(g.kv.get(f"{a}.expert_count", 0))
+        self.NEU = int(g.kv.get(f"{a}.expert_used_count", 0))
+        self.FE = int(g.kv.get(f"{a}.expert_feed_forward_length", 0))
+        self.eps = float(g.kv[f"{a}.attention.layer_norm_rms_epsilon"])
+        self.base = float(g.kv[f"{a}.rope.freq_base"])
+        emb = g.tensor("token_embd.weight")
+        self.V = emb.shape[0]
+        self._keep = []
+
+        def ptr(name):
+            t = g.tensor(name)
+            t = np.ascontiguousarray(t)
+            self._keep.append(t)
+            return t.ctypes.data
+
+        layers = (_Layer * self.L)()
+        for i in range(self.L):
+            p = f"blk.{i}."
+            ly = layers[i]
+            for f, n in (("attn_norm", "attn_norm"), ("q_norm", "attn_q_norm"), ("k_norm", "attn_k_norm"),
+                         ("ffn_norm", "ffn_norm"), ("wq", "attn_q"), ("wk", "attn_k"), ("wv", "attn_v"),
+                         ("wo", "attn_output")):
+                setattr(ly, f, ptr(p + n + ".weight"))
+            if self.NE:
+                ly.router = ptr(p + "ffn_gate_inp.weight")
+                ly.eg = ptr(p + "ffn_gate_exps.weight")
+                ly.eu = ptr(p + "ffn_up_exps.weight")
+                ly.ed = ptr(p + "ffn_down_exps.weight")
+            else:
+                ly.wg = ptr(p + "ffn_gate.weight")
+                ly.wu = ptr(p + "ffn_up.weight")
+                ly.wd = ptr(p + "ffn_down.weight")
+        self._layers = layers
+        self.m = _Model(self.L, self.E, self.H, self.KVH, self.D, self.F, self.V, self.NE, self.NEU, self.FE,
+                        self.eps, self.base, ptr("token_embd.weight"), ptr("output_norm.weight"),
+                        ptr("output.weight"), layers)
+        self.n_seq, self.ctx = n_seq, ctx
+        shape = (n_seq, self.L, ctx, self.KVH, self.D)
+        self.k = np.zeros(shape, np.uint16)
+        self.v = np.zeros(shape, np.uint16)
+        self.kv = _KV(n_seq, ctx, self.L, self.KVH, self.D, self.k.ctypes.data, self.v.ctypes.data)
+
+    def step(self, tok, seq, pos, out_rows, want_hidden=False, nthreads=0):
+        tok = np.ascontiguousarray(tok, np.int32)
+        seq = np.ascontiguousarray(seq, np.int32)
+        pos = np.ascontiguousarray(pos, np.int32)
+        out_rows = np.ascontiguousarray(out_rows, np.int32)
+        n_out = out_rows.size
+        logits = np.empty((max(n_out, 1), self.V), np.float32)
+        hidden = np.empty((max(n_out, 1), self.E), np.float32) if want_hidden else None
+        out_tok = np.empty(max(n_out, 1), np.int32)
+        lib().or_qwen3_step(C.byref(self.m), C.byref(self.kv), tok.size, _p(tok), _p(seq), _p(pos), n_out,
+                            _p(out_rows), _p(logits), _p(hidden) if want_hidden else None, _p(out_tok), nthreads)
+        return out_tok[:n_out], logits[:n_out], (hidden[:n_out] if want_hidden else None)

@@ -1,0 +1,192 @@
+// Paged-KV GQA decode/verify attention for gfx950 (head_dim 128).
+//
+// Replaces the reference's attn_part + attn_merge (kernels.metal:1122-1192, dispatched by qwen_attn_write,
+// sn_attn.inc.h:176-192) and the verify rows' fa2/fa2r (kernels.metal:2674-2770): softmax(q.K^T * scale).V over each
+// row's cells 0..pos, in fixed chunks of cells whose (acc, m, l) partials are merged in chunk order.
+//
+// A workgroup (4 wavefronts) takes one (query group, KV head, 256-cell chunk); wavefront w takes 64 of the cells.
+// The G query heads of the KV head for each of the group's rows make up to 16 MFMA columns, so the K and V of a cell
+// are read once for all of them:
+//   S^T = K . Q^T : v_mfma_f32_16x16x32_f16, A = 16 cells x 32 dims of fp16 K, B = the queries in fp16 hi + lo
+//                   (q*scale = hi + lo to 2^-22), so the scores are fp32-accurate;
+//   O   = P . V   : A = 16 queries x 32 cells of p in fp16 hi + lo, B = 32 cells x 16 dims of fp16 V.
+// Scores of cells past a row's position are -inf and their p exactly 0, so a row's result does not depend on the
+// other rows of its group, and a verify row equals the same row run alone.
+#include "sn_kernels_internal.h"
+
+#define ATT_D 128
+
+// x = hi + lo in fp16 (to 2^-22 relative): slot j of the two fragments
+__device__ __forceinline__ void split_hl(float x, half8& hi, half8& lo, int j) {
+    const _Float16 h = (_Float16) x;
+    hi[j] = h;
+    lo[j] = (_Float16) (x - (float) h);
+}
+
+__device__ __forceinline__ uint32_t pick_half(uint32_t w_lo_cell, uint32_t w_hi_cell, int odd) {
+    // the fp16 at half `odd` of two words (cells j, j+1) packed as (cell j, cell j+1)
+    return __builtin_amdgcn_perm(w_hi_cell, w_lo_cell, odd ? 0x07060302u : 0x05040100u);
+}
+
+__global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
+    __shared__ float s_o[4][16][ATT_D + 4];
+    __shared__ float s_m[4][16], s_l[4][16];
+
+    const AttnItem it = a.items[blockIdx.x];
+    const AttnGroup gr = a.groups[it.group];
+    const int kvh = blockIdx.y;
+    const int G = a.H / a.KVH;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int pos_last = gr.pos0 + gr.nrows - 1;
+    const int cbase = it.chunk * ATT_CHUNK + 64 * wave;  // this wavefront's first cell
+    const size_t head_stride = (size_t) a.page_cells * ATT_D;
+
+    // this lane's query (as a B column of S^T and the A row of O): n = row * G + head-in-group
+    const int qrow = n / G, qhead = kvh * G + n % G;
+    const bool qvalid = qrow < gr.nrows;
+    const int qpos = gr.pos0 + qrow;
+
+    // Q^T fragments: MFMA t covers dims 32t .. 32t+31; lane (n, g) holds dims 32t + 8g .. +7 of query n
+    half8 qh[4], ql[4];
+    {
+        const float* qp = a.q + (size_t) (gr.row0 + (qvalid ? qrow : 0)) * a.ldq + (size_t) qhead * ATT_D;
+        for (int t = 0; t < 4; ++t)
+            for (int j = 0; j < 8; ++j) {
+                const float v = qvalid ? qp[32 * t + 8 * g + j] * a.scale : 0.0f;
+                split_hl(v, qh[t], ql[t], j);
+            }
+    }
+
+    // cell addresses: K rows for S (cell = cbase + 16 jg + n), V rows for O (cells cbase + 32 st + 16 jg + 4 g + v)
+    const int32_t* ptrow = a.pt + (size_t) gr.seq * a.max_pages;
+    auto cell_ptr = [&](const uint16_t* pool, int c) -> const uint16_t* {
+        const int p = ptrow[c / a.page_cells];
+        return pool + ((size_t) p * a.KVH + kvh) * head_stride + (size_t) (c % a.page_cells) * ATT_D;
+    };
+
+    // ---- scores for the wavefront's 64 cells: 4 groups of 16 cells
+    floatx4 s[4];
+    for (int jg = 0; jg < 4; ++jg) {
+        const int c = cbase + 16 * jg + n;
+        u32x4 kf[4];
+        if (c <= pos_last) {
+            const uint16_t* kp = cell_ptr(a.kpool, c);
+            for (int t = 0; t < 4; ++t) kf[t] = *(const u32x4*) (kp + 32 * t + 8 * g);
+        } else {
+            for (int t = 0; t < 4; ++t) kf[t] = (u32x4){0u, 0u, 0u, 0u};
+        }
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 4; ++t) {
+            const half8 kh = __builtin_bit_cast(half8, kf[t]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[t], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[t], acc, 0, 0, 0);
+        }
+        s[jg] = acc;  // lane (n, g): cells cbase + 16 jg + 4 g + v, query n
+    }
+
+    // ---- the wavefront's softmax statistics per query (lanes n, n+16, n+32, n+48 share query n)
+    float m = -INFINITY;
+    for (int jg = 0; jg < 4; ++jg)
+        for (int v = 0; v < 4; ++v) {
+            const int c = cbase + 16 * jg + 4 * g + v;
+            const bool ok = qvalid && c <= qpos;
+            s[jg][v] = ok ? s[jg][v] : -INFINITY;
+            m = fmaxf(m, s[jg][v]);
+        }
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    float l = 0.0f;
+    for (int jg = 0; jg < 4; ++jg)
+        for (int v = 0; v < 4; ++v) {
+            const float p = m == -INFINITY ? 0.0f : __expf(s[jg][v] - m);
+            s[jg][v] = p;
+            l += p;
+        }
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+
+    // ---- O = P . V over two steps of 32 cells; MFMA t covers output dims {8 c + t : c = 0..15}
+    floatx4 o[8];
+    for (int t = 0; t < 8; ++t) o[t] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    for (int st = 0; st < 2; ++st) {
+        // P fragment: k slot 4 jj + v <-> cell cbase + 32 st + 16 jj + 4 g + v
+        half8 ph, pl;
+        for (int jj = 0; jj < 2; ++jj)
+            for (int v = 0; v < 4; ++v) split_hl(s[2 * st + jj][v], ph, pl, 4 * jj + v);
+        u32x4 vf[8];
+        for (int jj = 0; jj < 2; ++jj)
+            for (int v = 0; v < 4; ++v) {
+                const int c = cbase + 32 * st + 16 * jj + 4 * g + v;
+                vf[4 * jj + v] = c <= pos_last ? *(const u32x4*) (cell_ptr(a.vpool, c) + 8 * n) : (u32x4){0u, 0u, 0u, 0u};
+            }
+        for (int t = 0; t < 8; ++t) {
+            u32x4 bw;
+            for (int i = 0; i < 4; ++i) bw[i] = pick_half(vf[2 * i][t >> 1], vf[2 * i + 1][t >> 1], t & 1);
+            const half8 vb = __builtin_bit_cast(half8, bw);
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vb, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, o[t], 0, 0, 0);
+        }
+    }
+
+    // ---- the 4 wavefronts combined in wavefront order
+    if (g == 0) {
+        s_m[wave][n] = m;
+        s_l[wave][n] = l;
+    }
+    for (int t = 0; t < 8; ++t)
+        for (int v = 0; v < 4; ++v) s_o[wave][4 * g + v][8 * n + t] = o[t][v];
+    __syncthreads();
+    // thread -> (query qq, 8 dims)
+    const int qq = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
+    const int row = qq / G, head = kvh * G + qq % G;
+    if (row >= gr.nrows) return;
+    float M = -INFINITY;
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w][qq]);
+    float e[4], L = 0.0f;
+    for (int w = 0; w < 4; ++w) {
+        e[w] = s_m[w][qq] == -INFINITY ? 0.0f : __expf(s_m[w][qq] - M);
+        L += s_l[w][qq] * e[w];
+    }
+    float* dst = a.part + (((size_t) (gr.row0 + row) * a.H + head) * a.max_chunks + it.chunk) * (ATT_D + 2);
+    for (int d = 0; d < 8; ++d) {
+        float acc = 0.0f;
+        for (int w = 0; w < 4; ++w) acc += s_o[w][qq][d0 + d] * e[w];
+        dst[d0 + d] = acc;
+    }
+    if ((threadIdx.x & 15) == 0) {
+        dst[ATT_D] = M;
+        dst[ATT_D + 1] = L;
+    }
+}
+
+// per (row, head): the chunks' partials in chunk order; out = acc / l. One wavefront, 2 dims a lane.
+__global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
+    const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int nc = a.row_pos[r] / ATT_CHUNK + 1;
+    const float* p0 = a.part + ((size_t) r * a.H + h) * a.max_chunks * (ATT_D + 2);
+    float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    for (int c = 0; c < nc; ++c) {
+        const float* pc = p0 + (size_t) c * (ATT_D + 2);
+        const float mc = pc[ATT_D], lc = pc[ATT_D + 1];
+        if (mc == -INFINITY) continue;  // a chunk with no cell for this row
+        const float mn = fmaxf(M, mc);
+        const float e0 = M == -INFINITY ? 0.0f : __expf(M - mn), e1 = __expf(mc - mn);
+        o0 = o0 * e0 + pc[2 * lane] * e1;
+        o1 = o1 * e0 + pc[2 * lane + 1] * e1;
+        L = L * e0 + lc * e1;
+        M = mn;
+    }
+    const float il = L > 0.0f ? 1.0f / L : 0.0f;
+    float* out = a.out + (size_t) r * a.ldo + (size_t) h * ATT_D;
+    out[2 * lane] = o0 * il;
+    out[2 * lane + 1] = o1 * il;
+}
+
+int paged_attention(const AttnArgs& a, hipStream_t st) {
+    if (a.n_items <= 0) return 0;
+    if (a.H % a.KVH != 0 || 16 % (a.H / a.KVH) != 0) return -1;
+    hipLaunchKernelGGL(k_attn_part, dim3(a.n_items, a.KVH), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_attn_merge, dim3(a.n_rows, a.H), dim3(64), 0, st, a);
+    return 0;
+}

@@ -1,0 +1,253 @@
+// Row kernels of the step: token embedding, per-head QK-norm + NEOX RoPE + the fp16 K/V cache write, and greedy
+// argmax (with the top-2 / log-sum-exp record of sn_want_probs).
+#include "sn_kernels_internal.h"
+
+// ---- embedding: the token's fp32 table row (embed_rows / embed_into, sn_state.inc.h:250-272; the table is fp32 here)
+__global__ void k_embed(const float* __restrict__ table, int E, const int32_t* __restrict__ tok, float* __restrict__ x) {
+    const int r = blockIdx.x;
+    const float* src = table + (size_t) tok[r] * E;
+    for (int i = threadIdx.x; i < E; i += blockDim.x) x[(size_t) r * E + i] = src[i];
+}
+
+void embed_rows(const float* table, int E, const int32_t* tok, int R, float* x, hipStream_t st) {
+    if (R > 0) hipLaunchKernelGGL(k_embed, dim3(R), dim3(256), 0, st, table, E, tok, x);
+}
+
+// ---- QK-norm + RoPE + K/V into the cache (qk_rope, kernels.metal:149-197) -------------------------------------------
+// One workgroup (4 wavefronts) per row; a wavefront takes one head at a time, lane i the rotation pair (i, i + 64).
+// Per head: RMSNorm over 128 dims with weight w, then y_i = x_i cos - x_{i+64} sin, y_{i+64} = x_i sin + x_{i+64} cos
+// with theta_i = p * s^i formed by i successive fp32 multiplies from p (ggml_rope_cache_init's loop), s = base^(-2/128)
+// computed on the host. q stays in place (fp32); k and v go to the row's cell in fp16.
+__global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ldqkv, int H, int KVH,
+                                                 const float* __restrict__ qw, const float* __restrict__ kw, float eps,
+                                                 float theta_scale, const int32_t* __restrict__ seq,
+                                                 const int32_t* __restrict__ pos, const int32_t* __restrict__ pt,
+                                                 int max_pages, int page_cells, uint16_t* __restrict__ kpool,
+                                                 uint16_t* __restrict__ vpool) {
+    const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int p = pos[r];
+    float theta = (float) p;
+    for (int i = 0; i < lane; ++i) theta *= theta_scale;
+    const float c = cosf(theta), s = sinf(theta);
+    float* row = qkv + (size_t) r * ldqkv;
+    const int page = pt[(size_t) seq[r] * max_pages + p / page_cells];
+    const int off = p % page_cells;
+    for (int h = wave; h < H + KVH; h += 4) {
+        const bool isq = h < H;
+        float* x = row + (size_t) h * 128;  // q heads then k heads, contiguous
+        const float* w = isq ? qw : kw;
+        float x0 = x[lane], x1 = x[lane + 64];
+        float ss = x0 * x0 + x1 * x1;
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        const float sc = 1.0f / sqrtf(ss / 128.f + eps);
+        x0 = (x0 * sc) * w[lane];
+        x1 = (x1 * sc) * w[lane + 64];
+        const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
+        if (isq) {
+            x[lane] = y0;
+            x[lane + 64] = y1;
+        } else {
+            uint16_t* kc = kpool + (((size_t) page * KVH + (h - H)) * page_cells + off) * 128;
+            kc[lane] = __builtin_bit_cast(uint16_t, (_Float16) y0);
+            kc[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16) y1);
+        }
+    }
+    const float* v = row + (size_t) (H + KVH) * 128;
+    for (int i = threadIdx.x; i < KVH * 128; i += 256) {
+        const int hh = i / 128, d = i % 128;
+        vpool[(((size_t) page * KVH + hh) * page_cells + off) * 128 + d] = __builtin_bit_cast(uint16_t, (_Float16) v[i]);
+    }
+}
+
+void qk_norm_rope_kv(float* qkv, int ldqkv, int R, int H, int KVH, const float* qw, const float* kw, float eps,
+                     float theta_scale, const int32_t* seq, const int32_t* pos, const int32_t* pt, int max_pages,
+                     int page_cells, uint16_t* kpool, uint16_t* vpool, hipStream_t st) {
+    if (R > 0)
+        hipLaunchKernelGGL(k_qk_rope, dim3(R), dim3(256), 0, st, qkv, ldqkv, H, KVH, qw, kw, eps, theta_scale, seq, pos,
+                           pt, max_pages, page_cells, kpool, vpool);
+}
+
+// ---- greedy argmax (argmax / argmax_p, kernels.metal:327-442) -------------------------------------------------------
+// The first index of the largest score; rows with skip[r] never take the ids in ban. rec (optional): per row 8 words:
+// chosen id, chosen score, best id, best score, second id, second score, log-sum-exp, 0 (ids ascending among ties).
+struct Top2 {
+    float m1;
+    int i1;
+    float m2;
+    int i2;
+};
+__device__ __forceinline__ bool better(float v, int i, float w, int j) { return v > w || (v == w && i < j); }
+__device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
+    Top2 w = a, l = b;
+    if (better(b.m1, b.i1, a.m1, a.i1)) {
+        w = b;
+        l = a;
+    }
+    Top2 o = w;
+    if (better(l.m1, l.i1, w.m2, w.i2)) {
+        o.m2 = l.m1;
+        o.i2 = l.i1;
+    }
+    return o;
+}
+
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ logits, int V, const int32_t* __restrict__ ban,
+                                                 int nban, const uint8_t* __restrict__ skip, int32_t* __restrict__ out,
+                                                 float* __restrict__ rec) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    __shared__ Top2 st2[16];
+    __shared__ float ssum[16];
+    __shared__ float s_max;
+    const int r = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const float* x = logits + (size_t) r * V;
+    const int nb = (skip && skip[r]) ? nban : 0;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    Top2 tp = {-INFINITY, 0x7fffffff, -INFINITY, 0x7fffffff};
+    for (int i = t; i < V; i += 1024) {
+        const float v = x[i];
+        bool b = false;
+        for (int k = 0; k < nb; ++k) b = b || i == ban[k];
+        if (v > best && !b) {
+            best = v;
+            idx = i;
+        }
+        if (rec) {
+            if (v > tp.m1) {
+                tp.m2 = tp.m1; tp.i2 = tp.i1; tp.m1 = v; tp.i1 = i;
+            } else if (v > tp.m2) {
+                tp.m2 = v; tp.i2 = i;
+            }
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int oi = __shfl_xor(idx, o);
+        if (better(ov, oi, best, idx)) {
+            best = ov;
+            idx = oi;
+        }
+        if (rec) {
+            Top2 q;
+            q.m1 = __shfl_xor(tp.m1, o); q.i1 = __shfl_xor(tp.i1, o);
+            q.m2 = __shfl_xor(tp.m2, o); q.i2 = __shfl_xor(tp.i2, o);
+            tp = top2_merge(tp, q);
+        }
+    }
+    if (lane == 0) {
+        sv[w] = best;
+        si[w] = idx;
+        st2[w] = tp;
+    }
+    __syncthreads();
+    if (t == 0) {
+        for (int k = 1; k < 16; ++k) {
+            if (better(sv[k], si[k], best, idx)) {
+                best = sv[k];
+                idx = si[k];
+            }
+            if (rec) tp = top2_merge(tp, st2[k]);
+        }
+        out[r] = idx;
+        s_max = tp.m1;
+    }
+    if (!rec) return;
+    __syncthreads();
+    const float mx = s_max;
+    float s = 0.0f;
+    if (mx > -INFINITY)
+        for (int i = t; i < V; i += 1024) s += expf(x[i] - mx);
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) ssum[w] = s;
+    __syncthreads();
+    if (t == 0) {
+        float z = 0.0f;
+        for (int k = 0; k < 16; ++k) z += ssum[k];
+        float* p = rec + (size_t) r * 8;
+        p[0] = __builtin_bit_cast(float, idx);
+        p[1] = best;
+        p[2] = __builtin_bit_cast(float, tp.i1);
+        p[3] = tp.m1;
+        p[4] = __builtin_bit_cast(float, tp.i2);
+        p[5] = tp.m2;
+        p[6] = mx > -INFINITY ? mx + logf(z) : -INFINITY;
+        p[7] = 0.0f;
+    }
+}
+
+void argmax_rows(const float* logits, int V, int n, const int32_t* ban, int nban, const uint8_t* skip, int32_t* out,
+                 float* rec, hipStream_t st) {
+    if (n > 0) hipLaunchKernelGGL(k_argmax, dim3(n), dim3(1024), 0, st, logits, V, ban, nban, skip, out, rec);
+}
+
+// ---- page operations of the cache (sn_copy / sn_clear / freed pages; sn_seq.inc.h:5-145) ----------------------------
+__global__ void k_kv_page_op(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int KVH, int page_cells, int src,
+                             int dst, int a, int b) {
+    const int l = blockIdx.x, t = blockIdx.y, h = blockIdx.z;
+    uint16_t* pool = (t == 0 ? kbase : vbase) + (size_t) l * layer_halves;
+    uint16_t* d = pool + (((size_t) dst * KVH + h) * page_cells + a) * 128;
+    const uint16_t* s = src >= 0 ? pool + (((size_t) src * KVH + h) * page_cells + a) * 128 : nullptr;
+    const int n = (b - a) * 128;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) d[i] = s ? s[i] : (uint16_t) 0;
+}
+
+void kv_page_op(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L, int KVH, int page_cells, int src, int dst,
+                int a, int b, hipStream_t st) {
+    if (b > a)
+        hipLaunchKernelGGL(k_kv_page_op, dim3(L, 2, KVH), dim3(256), 0, st, kbase, vbase, layer_halves, KVH, page_cells,
+                           src, dst, a, b);
+}
+
+__global__ void k_kv_stage(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int KVH, int page_cells,
+                           const int32_t* pages, int n, uint16_t* staging, int save) {
+    const int l = blockIdx.y, t = blockIdx.z;
+    const int c = blockIdx.x;  // cell
+    if (c >= n) return;
+    uint16_t* pool = (t == 0 ? kbase : vbase) + (size_t) l * layer_halves;
+    const int p = pages[c / page_cells];
+    uint16_t* stg = staging + (((size_t) l * 2 + t) * n + c) * (size_t) KVH * 128;
+    for (int i = threadIdx.x; i < KVH * 128; i += blockDim.x) {
+        const int h = i / 128, d = i % 128;
+        uint16_t* cell = pool + (((size_t) p * KVH + h) * page_cells + c % page_cells) * 128 + d;
+        if (save) stg[i] = *cell;
+        else *cell = stg[i];
+    }
+}
+
+void kv_stage(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L, int KVH, int page_cells,
+              const int32_t* pages, int n, uint16_t* staging, int save, hipStream_t st) {
+    if (n > 0)
+        hipLaunchKernelGGL(k_kv_stage, dim3(n, L, 2), dim3(256), 0, st, kbase, vbase, layer_halves, KVH, page_cells,
+                           pages, n, staging, save);
+}
+
+// ---- synthetic context: seeded N(0, 1) fp16 cells (snx_fill_kv) ------------------------------------------------------
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ void k_kv_fill(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int KVH, int page_cells,
+                          const int32_t* pages, int n, uint64_t seed) {
+    const int c = blockIdx.x, l = blockIdx.y, t = blockIdx.z;  // cell, layer, K or V
+    if (c >= n) return;
+    uint16_t* pool = (t == 0 ? kbase : vbase) + (size_t) l * layer_halves;
+    const int p = pages[c / page_cells];
+    for (int i = threadIdx.x; i < KVH * 128; i += blockDim.x) {
+        const int h = i / 128, d = i % 128;
+        const uint64_t key = seed ^ mix64(((uint64_t) l * 2 + t) * 0x100000000ull + (uint64_t) c * 4096 + i);
+        const uint64_t a = mix64(key), b = mix64(key ^ 0x9E3779B97F4A7C15ull);
+        const float u1 = ((a >> 40) + 1) * 0x1.0p-24f, u2 = (b >> 40) * 0x1.0p-24f;
+        const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.2831853f * u2);
+        pool[(((size_t) p * KVH + h) * page_cells + c % page_cells) * 128 + d] = __builtin_bit_cast(uint16_t, (_Float16) z);
+    }
+}
+
+void kv_fill_normal(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L, int KVH, int page_cells,
+                    const int32_t* pages, int n, uint64_t seed, hipStream_t st) {
+    if (n > 0)
+        hipLaunchKernelGGL(k_kv_fill, dim3(n, L, 2), dim3(256), 0, st, kbase, vbase, layer_halves, KVH, page_cells, pages,
+                           n, seed);
+}

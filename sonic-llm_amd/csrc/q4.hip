@@ -1,0 +1,342 @@
+// Q4_0 x Q8_0 matmul for gfx950: Y[m][n] (+)= sum_k X[m][k] W[n][k].
+//
+// Replaces the reference's Q4_0 mat-vec / few-row / block matmuls (kernels.metal:1324-1411 mv_q4_0_*, :1413-1490
+// mvm_q4_0_*, :746-1007 qmm_ks/qmmh_ks_q4_0_*, dispatched by mm() in core_mm.inc.h:307-325), with ggml's CPU numerics
+// (Q8_0-quantized activations, integer block sums scaled by dw*dx) instead of the reference's fp16 weights.
+//
+// How a block's sum is formed: the weights' (q-8) are exact in fp16, the activation's dx*q8 is exact as an fp16
+// hi + lo pair, and v_mfma_f32_16x16x32_f16 multiplies exactly and accumulates in fp32, so the two MFMAs of a block
+// give dx*isum (to fp32 rounding); one fma per output then adds dw * that to the fp32 accumulator. Each output's sum
+// runs over blocks in K order within a k-slice, and k-slices are added in slice order; neither depends on the number
+// of rows, so a row's result is the same in any step (sn.h:1-3).
+#include "sn_kernels_internal.h"
+
+// ---------------------------------------------------------------------------------------------------------------------
+// weight upload: GGUF rows -> stripes (sn_common.h)
+// Source stripe s goes to destination stripe s * sstride + soff (sstride 2 interleaves a gate and an up matrix).
+__global__ void k_q4_repack(const uint8_t* __restrict__ src, int N, int K, uint8_t* __restrict__ dst, int sstride,
+                            int soff) {
+    const int nb = K / 32, ngroups = (nb + 3) / 4;
+    const int tile = blockIdx.x;  // (stripe, group)
+    const int stripe = tile / ngroups, grp = tile % ngroups;
+    const int l = threadIdx.x, n = l & 15, g = l >> 4;
+    const int row = stripe * 16 + n;
+    uint8_t* t = dst + ((size_t) (stripe * sstride + soff) * ngroups + grp) * Q4T_BYTES;
+    uint8_t q[16];
+    uint16_t d[4];
+    for (int b = 0; b < 4; ++b) {
+        const int blk = grp * 4 + b;
+        const bool ok = row < N && blk < nb;
+        const uint8_t* s = src + ((size_t) row * nb + blk) * 18;
+        for (int j = 0; j < 4; ++j) q[4 * b + j] = ok ? s[2 + 4 * g + j] : 0;
+        d[b] = ok ? (uint16_t) (s[0] | (s[1] << 8)) : 0;
+    }
+    for (int j = 0; j < 16; ++j) t[16 * l + j] = q[j];
+    if (g == 0)
+        for (int b = 0; b < 4; ++b) {
+            t[Q4T_SCALE_OFF + 8 * n + 2 * b] = (uint8_t) d[b];
+            t[Q4T_SCALE_OFF + 8 * n + 2 * b + 1] = (uint8_t) (d[b] >> 8);
+        }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// activation quantizer: fp32 rows (optionally RMS-normed by weight nw first) -> xa operand (sn_common.h).
+// One workgroup of 256 threads per row. The norm is ggml's: y = (x * scale) * w, scale = 1/sqrt(mean(x^2) + eps).
+__device__ __forceinline__ float block_reduce_sum256(float v, float* red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ __forceinline__ void quant_block_store(const float* v, int m, int b, int nb, uint8_t* __restrict__ xa) {
+    // v: the block's 32 values (already normed). ggml x86 quantize_row_q8_0.
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    const float d = amax / 127.f;
+    const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+    const float dh = (float) (_Float16) d;
+    uint8_t* base = xa + ((size_t) ((m >> 4) * nb + b)) * XA_BLOCK_BYTES;
+    for (int g = 0; g < 4; ++g) {
+        half8 hi, lo;
+        for (int j = 0; j < 8; ++j) {
+            const int e = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
+            const float q = __builtin_rintf(v[e] * id);
+            const float x = dh * q;  // exact
+            const _Float16 h = (_Float16) x;
+            hi[j] = h;
+            lo[j] = (_Float16) (x - (float) h);
+        }
+        const int lane = (m & 15) + 16 * g;
+        *(half8*) (base + 16 * lane) = hi;
+        *(half8*) (base + 1024 + 16 * lane) = lo;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, const int32_t* __restrict__ rows,
+                                                   int K, int ldx, const float* __restrict__ nw, float eps,
+                                                   uint8_t* __restrict__ xa, float* __restrict__ xn, int ldn) {
+    __shared__ float red[4];
+    const int m = blockIdx.x, nb = K / 32;
+    const float* x = X + (size_t) (rows ? rows[m] : m) * ldx;
+    float scale = 1.0f;
+    if (nw) {
+        float s = 0.0f;
+        for (int i = threadIdx.x; i < K; i += 256) s += x[i] * x[i];
+        s = block_reduce_sum256(s, red);
+        scale = 1.0f / sqrtf(s / (float) K + eps);
+    }
+    for (int b = threadIdx.x; b < nb; b += 256) {
+        float v[32];
+        for (int j = 0; j < 32; ++j) {
+            const float t = x[32 * b + j];
+            v[j] = nw ? (t * scale) * nw[32 * b + j] : t;
+        }
+        if (xn)
+            for (int j = 0; j < 32; ++j) xn[(size_t) m * ldn + 32 * b + j] = v[j];
+        quant_block_store(v, m, b, nb, xa);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// the matmul
+__device__ __forceinline__ half8 q4_unpack(uint32_t w) {
+    // (q - 8) of the 8 nibbles of w as fp16: low nibbles are elements 4g..4g+3, high nibbles 16+4g..16+4g+3.
+    // 0x6400 | q is fp16(1024 + q); subtracting 1032 is exact.
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u);
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u);
+    const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u);
+    const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u);
+    const half2v off = {(_Float16) 1032.0f, (_Float16) 1032.0f};
+    const half2v h0 = __builtin_bit_cast(half2v, p0) - off;
+    const half2v h1 = __builtin_bit_cast(half2v, p1) - off;
+    const half2v h2 = __builtin_bit_cast(half2v, p2) - off;
+    const half2v h3 = __builtin_bit_cast(half2v, p3) - off;
+    half8 r;
+    r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
+    r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
+    return r;
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// One workgroup = 4 wavefronts; wavefront w owns NT 16-row stripes (consecutive) and sweeps the groups of its k-slice.
+// MT 16-row tiles of activation rows (M <= 16 MT; grid.z walks further row tiles for bigger M).
+template <int MT, int NT>
+__global__ __launch_bounds__(256) void k_q4_gemm(GemmArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int stripe0 = (blockIdx.x * 4 + wave) * NT;
+    if (stripe0 >= a.nstripes) return;
+    const int slice = blockIdx.y, mt0 = blockIdx.z * MT;
+    const int c0 = slice * a.gps, c1 = min(c0 + a.gps, a.ngroups);
+    const int nb = a.K / 32;
+    const int n_in = lane & 15;
+
+    floatx4 acc[NT][MT];
+    for (int t = 0; t < NT; ++t)
+        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+
+    for (int c = c0; c < c1; ++c) {
+        half8 ahi[4][MT], alo[4][MT];
+        for (int b = 0; b < 4; ++b) {
+            const int blk = 4 * c + b;
+            for (int mt = 0; mt < MT; ++mt) {
+                if (blk < nb && mt0 + mt < a.mtiles) {
+                    const uint8_t* p = a.xa + ((size_t) (mt0 + mt) * nb + blk) * XA_BLOCK_BYTES + 16 * lane;
+                    ahi[b][mt] = *(const half8*) p;
+                    alo[b][mt] = *(const half8*) (p + 1024);
+                } else {
+                    ahi[b][mt] = (half8){};
+                    alo[b][mt] = (half8){};
+                }
+            }
+        }
+        for (int t = 0; t < NT; ++t) {
+            const int s = stripe0 + t;
+            if (s >= a.nstripes) break;
+            const uint8_t* tp = a.w + ((size_t) s * a.ngroups + c) * Q4T_BYTES;
+            const u32x4 wq = *(const u32x4*) (tp + 16 * lane);
+            // the 4 scales as one 8-byte load of fp16 (a bit_cast of a u32x2 element here lost the second word)
+            const half4v sc = *(const half4v*) (tp + Q4T_SCALE_OFF + 8 * n_in);
+            const float dw[4] = {(float) sc[0], (float) sc[1], (float) sc[2], (float) sc[3]};
+            for (int b = 0; b < 4; ++b) {
+                const half8 bw = q4_unpack(wq[b]);
+                for (int mt = 0; mt < MT; ++mt) {
+                    floatx4 r = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[b][mt], bw, zero, 0, 0, 0);
+                    r = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[b][mt], bw, r, 0, 0, 0);
+                    for (int v = 0; v < 4; ++v) acc[t][mt][v] = __builtin_fmaf(r[v], dw[b], acc[t][mt][v]);
+                }
+            }
+        }
+    }
+
+    // lane (n, g) holds rows 4g+v of each row tile, column n of each stripe
+    const int g = lane >> 4;
+    for (int t = 0; t < NT; ++t) {
+        const int s = stripe0 + t;
+        if (s >= a.nstripes) break;
+        const int col = s * 16 + n_in;
+        for (int mt = 0; mt < MT; ++mt)
+            for (int v = 0; v < 4; ++v) {
+                const int row = (mt0 + mt) * 16 + 4 * g + v;
+                if (row >= a.M || col >= a.N) continue;
+                const float val = acc[t][mt][v];
+                if (a.ks > 1) {
+                    a.part[((size_t) slice * a.M + row) * a.N + col] = val;
+                } else if (a.epi == EPI_STORE) {
+                    a.y[(size_t) row * a.ldy + col] = val;
+                } else if (a.epi == EPI_ADD) {
+                    a.y[(size_t) row * a.ldy + col] += val;
+                }
+            }
+    }
+    if (a.ks == 1 && a.epi == EPI_SWIGLU) {
+        // stripes 2p (gate) and 2p+1 (up) of a pair are in the same wavefront (NT even, stripe0 even)
+        for (int t = 0; t + 1 < NT; t += 2) {
+            const int s = stripe0 + t;
+            if (s + 1 >= a.nstripes) break;
+            const int col = (s / 2) * 16 + n_in;
+            for (int mt = 0; mt < MT; ++mt)
+                for (int v = 0; v < 4; ++v) {
+                    const int row = (mt0 + mt) * 16 + 4 * g + v;
+                    if (row >= a.M || col >= a.N / 2) continue;
+                    a.y[(size_t) row * a.ldy + col] = silu(acc[t][mt][v]) * acc[t + 1][mt][v];
+                }
+        }
+    }
+}
+
+// k-slice partials added in slice order, then the epilogue
+__global__ void k_q4_reduce(GemmArgs a) {
+    const int outN = a.epi == EPI_SWIGLU ? a.N / 2 : a.N;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.M * outN) return;
+    const int row = i / outN, col = i % outN;
+    auto sum = [&](int c) {
+        float s = 0.0f;
+        for (int k = 0; k < a.ks; ++k) s += a.part[((size_t) k * a.M + row) * a.N + c];
+        return s;
+    };
+    if (a.epi == EPI_SWIGLU) {
+        // output column col = 16 p + n is gate column 32 p + n and up column 32 p + 16 + n
+        const int p = col / 16, n = col % 16;
+        a.y[(size_t) row * a.ldy + col] = silu(sum(32 * p + n)) * sum(32 * p + 16 + n);
+    } else if (a.epi == EPI_ADD) {
+        a.y[(size_t) row * a.ldy + col] += sum(col);
+    } else {
+        a.y[(size_t) row * a.ldy + col] = sum(col);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// host side
+
+// The launch shape of a matrix depends on (N, K) only, never on the rows (row invariance).
+GemmPlan q4_plan(int N, int K) {
+    GemmPlan p;
+    p.nstripes = (N + 15) / 16;
+    p.ngroups = (K / 32 + 3) / 4;
+    p.nt = p.nstripes >= 4096 ? 2 : 1;
+    const int waves = (p.nstripes + p.nt - 1) / p.nt;
+    // k-slices of at least 4 groups (512 values) until there are about 2048 wavefronts
+    int ks = 1;
+    while (waves * ks < 2048 && (p.ngroups + ks) / (ks + 1) >= 4) ++ks;
+    p.ks = ks;
+    p.gps = (p.ngroups + ks - 1) / ks;
+    p.ks = (p.ngroups + p.gps - 1) / p.gps;
+    return p;
+}
+
+size_t q4_workspace_bytes(int M, int N, int K) {
+    const GemmPlan p = q4_plan(N, K);
+    return p.ks > 1 ? (size_t) p.ks * M * N * sizeof(float) : 0;
+}
+
+template <int MT, int NT>
+static void launch_mt(const GemmArgs& a, int mblocks, hipStream_t st) {
+    dim3 grid((a.nstripes + 4 * NT - 1) / (4 * NT), a.ks, mblocks);
+    hipLaunchKernelGGL((k_q4_gemm<MT, NT>), grid, dim3(256), 0, st, a);
+}
+
+int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* part,
+            size_t part_bytes, hipStream_t st) {
+    if (M <= 0) return 0;
+    const GemmPlan p = q4_plan(N, K);
+    GemmArgs a;
+    a.w = w; a.xa = xa; a.y = y; a.part = part;
+    a.M = M; a.N = N; a.K = K; a.ldy = ldy; a.epi = epi;
+    a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
+    a.mtiles = (M + 15) / 16;
+    int nt = p.nt;
+    if (epi == EPI_SWIGLU && nt < 2) nt = 2;  // a gate/up stripe pair in one wavefront
+    if (p.ks > 1 && (part == nullptr || part_bytes < (size_t) p.ks * M * N * sizeof(float))) return -1;
+    const int MT = a.mtiles == 1 ? 1 : 2;
+    const int mblocks = (a.mtiles + MT - 1) / MT;
+    if (MT == 1) {
+        if (nt == 1) launch_mt<1, 1>(a, mblocks, st); else launch_mt<1, 2>(a, mblocks, st);
+    } else {
+        if (nt == 1) launch_mt<2, 1>(a, mblocks, st); else launch_mt<2, 2>(a, mblocks, st);
+    }
+    if (p.ks > 1) {
+        const int outN = epi == EPI_SWIGLU ? N / 2 : N;
+        const int tot = M * outN;
+        hipLaunchKernelGGL(k_q4_reduce, dim3((tot + 255) / 256), dim3(256), 0, st, a);
+    }
+    return 0;
+}
+
+void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int soff, hipStream_t st) {
+    const int tiles = ((N + 15) / 16) * ((K / 32 + 3) / 4);
+    hipLaunchKernelGGL(k_q4_repack, dim3(tiles), dim3(64), 0, st, src, N, K, dst, sstride, soff);
+}
+
+void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const float* nw, float eps, uint8_t* xa,
+               float* xn, int ldn, hipStream_t st) {
+    if (M <= 0) return;
+    hipLaunchKernelGGL(k_quant_act, dim3(M), dim3(256), 0, st, x, rows, K, ldx, nw, eps, xa, xn, ldn);
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// checks: the matmul's own dequantization written out, and one MFMA's lane contents
+__global__ void k_q4_dequant(const uint8_t* __restrict__ w, int N, int K, float* __restrict__ out) {
+    const int nb = K / 32, ngroups = (nb + 3) / 4;
+    const int tile = blockIdx.x, stripe = tile / ngroups, grp = tile % ngroups;
+    const int lane = threadIdx.x, n = lane & 15, g = lane >> 4, row = stripe * 16 + n;
+    const uint8_t* tp = w + (size_t) tile * Q4T_BYTES;
+    const u32x4 wq = *(const u32x4*) (tp + 16 * lane);
+    const half4v sc = *(const half4v*) (tp + Q4T_SCALE_OFF + 8 * n);
+    const float dw[4] = {(float) sc[0], (float) sc[1], (float) sc[2], (float) sc[3]};
+    for (int b = 0; b < 4; ++b) {
+        const int blk = 4 * grp + b;
+        if (row >= N || blk >= nb) continue;
+        const half8 q = q4_unpack(wq[b]);
+        for (int j = 0; j < 8; ++j) {
+            const int e = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
+            out[(size_t) row * K + 32 * blk + e] = (float) q[j] * dw[b];
+        }
+    }
+}
+
+extern "C" int snk_q4_dequant(const void* d_stripes, int N, int K, float* d_w, void* stream) {
+    if (N <= 0 || K <= 0 || K % 32) return -1;
+    const int tiles = ((N + 15) / 16) * ((K / 32 + 3) / 4);
+    hipLaunchKernelGGL(k_q4_dequant, dim3(tiles), dim3(64), 0, (hipStream_t) stream, (const uint8_t*) d_stripes, N, K,
+                       d_w);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+__global__ void k_mfma_probe(const half8* a, const half8* b, floatx4* d) {
+    const int l = threadIdx.x;
+    const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+    d[l] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[l], b[l], z, 0, 0, 0);
+}
+
+extern "C" int snk_mfma_probe(const void* d_a, const void* d_b, float* d_d, void* stream) {
+    hipLaunchKernelGGL(k_mfma_probe, dim3(1), dim3(64), 0, (hipStream_t) stream, (const half8*) d_a, (const half8*) d_b,
+                       (floatx4*) d_d);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}

@@ -1,0 +1,52 @@
+// Shared definitions of the MI355X (gfx950) decode/verify step: vector types, MFMA fragment types, error macro, and the
+// device-side layouts every kernel agrees on.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define SN_WAVE 64
+
+// HIP call check for host code: on failure, format the reason into (err, err_len) and return `ret`.
+#define SN_HIP_TRY(call, ret)                                                                              \
+    do {                                                                                                   \
+        hipError_t e_ = (call);                                                                            \
+        if (e_ != hipSuccess) {                                                                            \
+            sn_set_err(err, err_len, "%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, __LINE__); \
+            return ret;                                                                                    \
+        }                                                                                                  \
+    } while (0)
+
+void sn_set_err(char* err, int err_len, const char* fmt, ...);
+
+// ---- Q4_0 weights in HBM ("stripes") -------------------------------------------------------------------------------
+// A GGUF Q4_0 matrix (N rows of K/32 18-byte blocks: fp16 d, 16 nibble bytes) is re-laid at upload into tiles of 16
+// rows x 4 blocks, 1152 bytes each, so that one wavefront reads a tile with one 16-byte load per lane:
+//   bytes [0, 1024): lane l = n + 16 g (n = row in tile, g = 0..3) holds, for blocks b = 0..3 of the tile, the 4 bytes
+//                    qs[4g .. 4g+3] of row n (offset 16 l + 4 b). Byte j's low nibble is element j, its high nibble
+//                    element j + 16, so lane (n, g) holds elements {4g..4g+3} and {16+4g..16+4g+3} of each block.
+//   bytes [1024, 1152): the 16 rows' fp16 scales d, 4 per row (offset 1024 + 8 n + 2 b).
+// Tiles of one 16-row stripe follow each other along K, so a stripe is one contiguous stream of K/128 tiles.
+// Bytes per weight are those of GGUF (18 per 32); only their order changes. Rows are padded to 16 and blocks to 4
+// with zero tiles.
+#define Q4T_BYTES 1152
+#define Q4T_SCALE_OFF 1024
+
+// ---- activation operand ("xa"): Q8_0-quantized rows as fp16 MFMA fragments -----------------------------------------
+// Rows are quantized to Q8_0 exactly as ggml's x86 CPU backend does (per 32-block: d = amax/127 stored fp16,
+// q = round-half-even(x * 127/amax)). The dequantized value v = fp16(d) * q is exact in fp32 (11 x 7 bits) and is
+// stored as two fp16 values hi = fp16(v), lo = fp16(v - hi), which together hold v to within 2^-25 absolute.
+// Layout for row tile mt (16 rows) and block b: 2048 bytes = [hi: 64 lanes x 8 halves][lo: 64 lanes x 8 halves];
+// lane l = m + 16 g holds elements {4g..4g+3, 16+4g..16+4g+3} of row m (the same order as the weight tile lanes),
+// so one 16-byte load per lane gives the A operand of v_mfma_f32_16x16x32_f16.
+#define XA_BLOCK_BYTES 2048
+
+static inline size_t xa_bytes(int M, int K) { return (size_t) ((M + 15) / 16) * (K / 32) * XA_BLOCK_BYTES; }
+static inline size_t q4t_bytes(int N, int K) { return (size_t) ((N + 15) / 16) * ((K / 32 + 3) / 4) * Q4T_BYTES; }

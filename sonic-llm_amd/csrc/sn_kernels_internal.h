@@ -1,0 +1,84 @@
+// Kernel launchers shared by the engine (engine.cpp) and the kernel-level C ABI (snk.cpp). Host-side only.
+#pragma once
+#include "sn_common.h"
+
+enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
+
+struct GemmArgs {
+    const uint8_t* w;
+    const uint8_t* xa;
+    float* y;
+    float* part;
+    int M, N, K, ldy, epi;
+    int nstripes, ngroups, ks, gps, mtiles;
+};
+
+struct GemmPlan {
+    int nstripes, ngroups, nt, ks, gps;
+};
+
+GemmPlan q4_plan(int N, int K);
+size_t q4_workspace_bytes(int M, int N, int K);
+// GGUF Q4_0 rows -> stripes; source stripe s lands at destination stripe s * sstride + soff.
+void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int soff, hipStream_t st);
+// rows (optional): row m of the operand is row rows[m] of x. nw (optional): RMSNorm weight applied first.
+// xn (optional): the normed fp32 rows, ldn apart.
+void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const float* nw, float eps, uint8_t* xa,
+               float* xn, int ldn, hipStream_t st);
+int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* part,
+            size_t part_bytes, hipStream_t st);
+
+// ---- paged attention ----
+// One work item = (query group, KV head, chunk of ATT_CHUNK cells). A query group is up to 16/G rows of one
+// sequence (G = H/KVH query heads per KV head); its rows' positions rise by one (draft rows, prompt rows).
+#define ATT_CHUNK 256
+struct AttnGroup {
+    int32_t row0;   // first row of the group (rows row0 .. row0 + nrows - 1)
+    int32_t nrows;  // 1 .. 16/G
+    int32_t seq;    // the sequence (page-table row)
+    int32_t pos0;   // position of the first row; row i is at pos0 + i and attends cells 0 .. pos0 + i
+};
+struct AttnItem {
+    int32_t group;  // index into the group list
+    int32_t chunk;  // cells chunk*ATT_CHUNK ..
+};
+struct AttnArgs {
+    const float* q;          // [rows][H][D] fp32 (normed, roped; the softmax scale is applied inside)
+    int ldq;                 // floats between rows of q
+    const uint16_t* kpool;   // fp16 cells: page p, kv head h: kpool + ((p * KVH + h) * page_cells) * D
+    const uint16_t* vpool;
+    const int32_t* pt;       // [n_seq][max_pages] page table
+    int max_pages;
+    int page_cells;          // 32 or 64
+    const AttnGroup* groups;
+    const AttnItem* items;
+    int n_items;
+    float* part;             // partials [rows][H][max_chunks][130]: acc[128], m, l
+    int max_chunks;
+    float* out;              // [rows][ldo] fp32 (merge output), or NULL
+    int ldo;
+    uint8_t* xa;             // merge output as an xa operand (K = H*D), or NULL
+    int H, KVH;
+    float scale;
+    int n_rows;
+    const int32_t* row_pos;  // [rows] position of each row (merge: its chunk count)
+};
+int paged_attention(const AttnArgs& a, hipStream_t st);
+
+// ---- elementwise / row kernels ----
+void embed_rows(const float* table, int E, const int32_t* tok, int R, float* x, hipStream_t st);
+void qk_norm_rope_kv(float* qkv, int ldqkv, int R, int H, int KVH, const float* qw, const float* kw, float eps,
+                     float theta_scale, const int32_t* seq, const int32_t* pos, const int32_t* pt, int max_pages,
+                     int page_cells, uint16_t* kpool, uint16_t* vpool, hipStream_t st);
+// cells [a, b) of page `dst` in every layer: copied from page `src` (src >= 0) or zeroed (src < 0)
+void kv_page_op(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L, int KVH, int page_cells, int src, int dst,
+                int a, int b, hipStream_t st);
+// cells [0, n) of a slot (page list on the device) between the pool and a cell-major staging buffer
+// [L][K, V][n][KVH][128] (save: pool -> staging; load: staging -> pool)
+void kv_stage(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L, int KVH, int page_cells,
+              const int32_t* pages, int n, uint16_t* staging, int save, hipStream_t st);
+// seeded N(0, 1) fp16 into cells [0, n) of a slot (page list on the device), every layer, K and V
+void kv_fill_normal(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L, int KVH, int page_cells,
+                    const int32_t* pages, int n, uint64_t seed, hipStream_t st);
+void argmax_rows(const float* logits, int V, int n, const int32_t* ban, int nban, const uint8_t* skip, int32_t* out,
+                 float* rec, hipStream_t st);

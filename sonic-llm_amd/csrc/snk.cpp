@@ -1,0 +1,183 @@
+// The kernel-level C ABI (include/sn_kernels.h) over the launchers the engine uses.
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "../../include/sn_kernels.h"
+#include "sn_kernels_internal.h"
+
+extern "C" size_t snk_q4_stripes_bytes(int N, int K) { return q4t_bytes(N, K); }
+
+extern "C" int snk_q4_repack(const void* d_q4, int N, int K, void* d_stripes, void* stream) {
+    if (N <= 0 || K <= 0 || K % 32) return -1;
+    q4_repack((const uint8_t*) d_q4, N, K, (uint8_t*) d_stripes, 1, 0, (hipStream_t) stream);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" size_t snk_xa_bytes(int M, int K) { return xa_bytes(M, K); }
+
+extern "C" int snk_quant_act(const float* d_x, int M, int K, int ldx, const float* d_norm_w, float eps, void* d_xa,
+                             void* stream) {
+    if (M <= 0 || K <= 0 || K % 32 || ldx < K) return -1;
+    quant_act(d_x, nullptr, M, K, ldx, d_norm_w, eps, (uint8_t*) d_xa, nullptr, 0, (hipStream_t) stream);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" size_t snk_q4_workspace_bytes(int M, int N, int K) { return q4_workspace_bytes(M, N, K); }
+
+extern "C" int snk_q4_gemm(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi,
+                           void* d_ws, size_t ws_bytes, void* stream) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 32 || epi < 0 || epi > 2) return -1;
+    if (epi == SNK_EPI_SWIGLU ? (N % 32 != 0 || ldy < N / 2) : ldy < N) return -1;
+    const int rc = q4_gemm((const uint8_t*) d_stripes, (const uint8_t*) d_xa, M, N, K, d_y, ldy, epi, (float*) d_ws,
+                           ws_bytes, (hipStream_t) stream);
+    return rc == 0 && hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" double snk_q4_gemm_time(const void* const* d_stripes, int n_copies, const void* d_xa, int M, int N, int K,
+                                   float* d_y, int ldy, void* d_ws, size_t ws_bytes, int iters, void* stream) {
+    hipStream_t st = (hipStream_t) stream;
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return -1.0;
+    // one untimed launch per copy
+    for (int c = 0; c < n_copies; ++c)
+        q4_gemm((const uint8_t*) d_stripes[c], (const uint8_t*) d_xa, M, N, K, d_y, ldy, EPI_STORE, (float*) d_ws,
+                ws_bytes, st);
+    hipEventRecord(a, st);
+    for (int i = 0; i < iters; ++i)
+        q4_gemm((const uint8_t*) d_stripes[i % n_copies], (const uint8_t*) d_xa, M, N, K, d_y, ldy, EPI_STORE,
+                (float*) d_ws, ws_bytes, st);
+    hipEventRecord(b, st);
+    hipEventSynchronize(b);
+    float ms = 0.0f;
+    hipEventElapsedTime(&ms, a, b);
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    return hipGetLastError() == hipSuccess ? 1000.0 * ms / iters : -1.0;
+}
+
+// ---- attention work lists
+struct snk_attn {
+    int n_rows, H, KVH, max_pages, page_cells, max_chunks, n_items;
+    AttnGroup* d_groups = nullptr;
+    AttnItem* d_items = nullptr;
+    int32_t* d_pos = nullptr;
+    float* d_part = nullptr;
+};
+
+extern "C" snk_attn* snk_attn_new(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH, int max_pages,
+                                  int page_cells, char* err, int err_len) {
+    if (n_rows <= 0 || H <= 0 || KVH <= 0 || H % KVH || 16 % (H / KVH) || (page_cells != 32 && page_cells != 64)) {
+        sn_set_err(err, err_len, "snk_attn_new: bad shape");
+        return nullptr;
+    }
+    const int gmax = 16 / (H / KVH);
+    std::vector<AttnGroup> groups;
+    std::vector<AttnItem> items;
+    int maxpos = 0;
+    for (int r = 0; r < n_rows;) {
+        if (pos[r] < 0 || pos[r] >= max_pages * page_cells) {
+            sn_set_err(err, err_len, "snk_attn_new: a position is outside the page table");
+            return nullptr;
+        }
+        int n = 1;
+        while (r + n < n_rows && n < gmax && seq[r + n] == seq[r] && pos[r + n] == pos[r] + n) ++n;
+        groups.push_back({r, n, seq[r], pos[r]});
+        const int last = pos[r] + n - 1;
+        maxpos = std::max(maxpos, last);
+        for (int c = 0; c <= last / ATT_CHUNK; ++c) items.push_back({(int) groups.size() - 1, c});
+        r += n;
+    }
+    snk_attn* p = new snk_attn();
+    p->n_rows = n_rows;
+    p->H = H;
+    p->KVH = KVH;
+    p->max_pages = max_pages;
+    p->page_cells = page_cells;
+    p->max_chunks = maxpos / ATT_CHUNK + 1;
+    p->n_items = (int) items.size();
+    bool ok = hipMalloc(&p->d_groups, groups.size() * sizeof(AttnGroup)) == hipSuccess &&
+              hipMalloc(&p->d_items, items.size() * sizeof(AttnItem)) == hipSuccess &&
+              hipMalloc(&p->d_pos, (size_t) n_rows * 4) == hipSuccess &&
+              hipMalloc(&p->d_part, (size_t) n_rows * H * p->max_chunks * 130 * 4) == hipSuccess;
+    ok = ok && hipMemcpy(p->d_groups, groups.data(), groups.size() * sizeof(AttnGroup), hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(p->d_items, items.data(), items.size() * sizeof(AttnItem), hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(p->d_pos, pos, (size_t) n_rows * 4, hipMemcpyHostToDevice) == hipSuccess;
+    if (!ok) {
+        sn_set_err(err, err_len, "snk_attn_new: device allocation failed");
+        snk_attn_free(p);
+        return nullptr;
+    }
+    return p;
+}
+
+static AttnArgs attn_args(snk_attn* p, const float* d_q, int ldq, const void* d_kpool, const void* d_vpool,
+                          const int32_t* d_pt, float scale, float* d_out, int ldo) {
+    AttnArgs a{};
+    a.q = d_q;
+    a.ldq = ldq;
+    a.kpool = (const uint16_t*) d_kpool;
+    a.vpool = (const uint16_t*) d_vpool;
+    a.pt = d_pt;
+    a.max_pages = p->max_pages;
+    a.page_cells = p->page_cells;
+    a.groups = p->d_groups;
+    a.items = p->d_items;
+    a.n_items = p->n_items;
+    a.part = p->d_part;
+    a.max_chunks = p->max_chunks;
+    a.out = d_out;
+    a.ldo = ldo;
+    a.H = p->H;
+    a.KVH = p->KVH;
+    a.scale = scale;
+    a.n_rows = p->n_rows;
+    a.row_pos = p->d_pos;
+    return a;
+}
+
+extern "C" int snk_attn_run(snk_attn* p, const float* d_q, int ldq, const void* d_kpool, const void* d_vpool,
+                            const int32_t* d_pt, float scale, float* d_out, int ldo, void* stream) {
+    if (!p || ldq < p->H * 128 || ldo < p->H * 128) return -1;
+    const AttnArgs a = attn_args(p, d_q, ldq, d_kpool, d_vpool, d_pt, scale, d_out, ldo);
+    if (paged_attention(a, (hipStream_t) stream) != 0) return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" double snk_attn_time(snk_attn* p, const float* d_q, int ldq, const void* d_kpool, const void* d_vpool,
+                                const int32_t* d_pt, float scale, float* d_out, int ldo, int iters, void* stream) {
+    hipStream_t st = (hipStream_t) stream;
+    const AttnArgs a = attn_args(p, d_q, ldq, d_kpool, d_vpool, d_pt, scale, d_out, ldo);
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.0;
+    paged_attention(a, st);
+    hipEventRecord(e0, st);
+    for (int i = 0; i < iters; ++i) paged_attention(a, st);
+    hipEventRecord(e1, st);
+    hipEventSynchronize(e1);
+    float ms = 0.0f;
+    hipEventElapsedTime(&ms, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    return hipGetLastError() == hipSuccess ? 1000.0 * ms / iters : -1.0;
+}
+
+extern "C" void snk_attn_free(snk_attn* p) {
+    if (!p) return;
+    hipFree(p->d_groups);
+    hipFree(p->d_items);
+    hipFree(p->d_pos);
+    hipFree(p->d_part);
+    delete p;
+}
+
+extern "C" int snk_qk_rope(float* d_qkv, int ldqkv, int R, int H, int KVH, const float* d_qw, const float* d_kw,
+                           float eps, float theta_scale, const int32_t* d_seq, const int32_t* d_pos, const int32_t* d_pt,
+                           int max_pages, int page_cells, void* d_kpool, void* d_vpool, void* stream) {
+    if (R <= 0 || H <= 0 || KVH <= 0 || ldqkv < (H + 2 * KVH) * 128 || (page_cells != 32 && page_cells != 64)) return -1;
+    qk_norm_rope_kv(d_qkv, ldqkv, R, H, KVH, d_qw, d_kw, eps, theta_scale, d_seq, d_pos, d_pt, max_pages, page_cells,
+                    (uint16_t*) d_kpool, (uint16_t*) d_vpool, (hipStream_t) stream);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}

@@ -1,0 +1,141 @@
+"""Paged GQA attention on the GPU against the oracle, through the C ABI (include/sn_kernels.h).
+
+Tolerance: within 1e-3 relative / 2e-3 absolute of the fp32 oracle (different reduction
+order); also checked against the fp64 closed form. Invariants: a verify row (grouped with its sequence's other draft
+rows) gives bitwise the output of the same row run alone (draft_test.m:45-67), and the result does not depend on where
+the pages sit in the pool.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import sllm_next as S
+from oracle import oracle as O
+from tests import gpu_util as U
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 2e-3
+H, KVH, D = 32, 8, 128
+
+
+def setup_module(module):
+    U.torch().cuda.init()
+
+
+def config2_case(seed=2, S_=32, page=32, lo=256, hi=4096, n_share=8, share_cells=1024):
+    """32 sequences, ctx ~ U[256, 4096], 32-token pages from a seeded permutation of one pool;
+    sequences 0..7 share their first 1024 cells (their own ctx drawn from [1024, 4096] so each holds the prefix)."""
+    r = np.random.default_rng(seed)
+    ctx = r.integers(lo, hi + 1, S_)
+    ctx[:n_share] = r.integers(share_cells, hi + 1, n_share)
+    maxp = (hi + page - 1) // page
+    sp = share_cells // page
+    need = sum((c + page - 1) // page for c in ctx) - (n_share - 1) * sp
+    perm = r.permutation(need).astype(np.int32)
+    pt = np.full((S_, maxp), -1, np.int32)
+    k = 0
+    for s in range(S_):
+        for c in range((ctx[s] + page - 1) // page):
+            if 0 < s < n_share and c < sp:
+                pt[s, c] = pt[0, c]
+            else:
+                pt[s, c] = perm[k]
+                k += 1
+    kpool = r.standard_normal((need, KVH, page, D), dtype=np.float32).astype(np.float16).view(np.uint16)
+    vpool = r.standard_normal((need, KVH, page, D), dtype=np.float32).astype(np.float16).view(np.uint16)
+    q = r.standard_normal((S_, H, D), dtype=np.float32)
+    return q, np.arange(S_, dtype=np.int32), (ctx - 1).astype(np.int32), kpool, vpool, pt, page
+
+
+def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None):
+    L = S.lib()
+    err = __import__("ctypes").create_string_buffer(256)
+    seq = np.ascontiguousarray(seq, np.int32)
+    pos = np.ascontiguousarray(pos, np.int32)
+    for s_, p_ in zip(seq, pos):  # every cell a row reads has a page (host-side check before the launch)
+        assert np.all(pt[s_, :p_ // page + 1] >= 0)
+    plan = L.snk_attn_new(len(seq), seq.ctypes.data, pos.ctypes.data, H, KVH, pt.shape[1], page, err, 256)
+    assert plan, err.value
+    if bufs is None:
+        bufs = (U.dev(kpool), U.dev(vpool), U.dev(pt))
+    dq = U.dev(q)
+    out = U.empty(q.size * 4)
+    rc = L.snk_attn_run(plan, U.ptr(dq), H * D, U.ptr(bufs[0]), U.ptr(bufs[1]), U.ptr(bufs[2]), scale, U.ptr(out),
+                        H * D, U.stream())
+    L.snk_attn_free(plan)
+    assert rc == 0
+    return U.host(out, np.float32)[:q.size].reshape(q.shape)
+
+
+def test_config2_paged_attention():
+    q, seq, pos, kp, vp, pt, page = config2_case()
+    scale = 1 / math.sqrt(D)
+    got = attn_gpu(q, seq, pos, kp, vp, pt, page, scale)
+    ref = O.paged_attn(q, seq, pos, KVH, kp, vp, page, pt, scale)
+    err = np.abs(got - ref)
+    print(f"config 2: max abs err {err.max():.3g}")
+    assert np.all(err <= ATOL + RTOL * np.abs(ref))
+    ref64 = O.paged_attn(q, seq, pos, KVH, kp, vp, page, pt, scale, f64=True)
+    assert np.max(np.abs(got - ref64)) < 1e-4
+
+
+@pytest.mark.parametrize("page", [32, 64])
+def test_short_and_ragged_contexts(page):
+    # contexts of 1 cell, chunk and page edges
+    ctxs = np.array([1, 2, 31, 32, 33, 63, 64, 65, 255, 256, 257, 511, 512, 513, 1000], np.int32)
+    r = np.random.default_rng(5)
+    S_ = len(ctxs)
+    maxp = (ctxs.max() + page - 1) // page
+    npg = int(sum((c + page - 1) // page for c in ctxs))
+    perm = r.permutation(npg).astype(np.int32)
+    pt = np.full((S_, maxp), -1, np.int32)
+    k = 0
+    for s in range(S_):
+        for c in range((ctxs[s] + page - 1) // page):
+            pt[s, c] = perm[k]
+            k += 1
+    kp = r.standard_normal((npg, KVH, page, D), dtype=np.float32).astype(np.float16).view(np.uint16)
+    vp = r.standard_normal((npg, KVH, page, D), dtype=np.float32).astype(np.float16).view(np.uint16)
+    q = r.standard_normal((S_, H, D), dtype=np.float32) * 3
+    seq = np.arange(S_, dtype=np.int32)
+    pos = ctxs - 1
+    scale = 1 / math.sqrt(D)
+    got = attn_gpu(q, seq, pos, kp, vp, pt, page, scale)
+    ref = O.paged_attn(q, seq, pos, KVH, kp, vp, page, pt, scale)
+    assert np.all(np.abs(got - ref) <= ATOL + RTOL * np.abs(ref))
+
+
+def test_verify_rows_equal_single_rows_bitwise():
+    q, seq, pos, kp, vp, pt, page = config2_case(seed=7, S_=4, lo=300, hi=800, n_share=0)
+    scale = 1 / math.sqrt(D)
+    # 4 draft rows of each sequence at positions p0 .. p0 + 3 (causal within the draft)
+    rows_seq = np.repeat(seq, 4).astype(np.int32)
+    p0 = pos - 3
+    rows_pos = (np.repeat(p0, 4) + np.tile(np.arange(4), len(seq))).astype(np.int32)
+    r = np.random.default_rng(8)
+    qv = r.standard_normal((len(rows_seq), H, D), dtype=np.float32)
+    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    grouped = attn_gpu(qv, rows_seq, rows_pos, kp, vp, pt, page, scale, bufs)
+    for i in range(len(rows_seq)):
+        one = attn_gpu(qv[i:i + 1].copy(), rows_seq[i:i + 1].copy(), rows_pos[i:i + 1].copy(), kp, vp, pt, page,
+                       scale, bufs)
+        assert np.array_equal(one[0].view(np.uint32), grouped[i].view(np.uint32)), i
+    ref = O.paged_attn(qv, rows_seq, rows_pos, KVH, kp, vp, page, pt, scale)
+    assert np.all(np.abs(grouped - ref) <= ATOL + RTOL * np.abs(ref))
+
+
+def test_page_placement_does_not_matter():
+    q, seq, pos, kp, vp, pt, page = config2_case(seed=9, S_=6, lo=200, hi=1500, n_share=0)
+    scale = 1 / math.sqrt(D)
+    a = attn_gpu(q, seq, pos, kp, vp, pt, page, scale)
+    r = np.random.default_rng(10)
+    perm = r.permutation(kp.shape[0]).astype(np.int32)  # move page p to perm[p]
+    kp2 = np.empty_like(kp)
+    vp2 = np.empty_like(vp)
+    kp2[perm] = kp
+    vp2[perm] = vp
+    pt2 = np.where(pt >= 0, perm[np.maximum(pt, 0)], -1).astype(np.int32)
+    b = attn_gpu(q, seq, pos, kp2, vp2, pt2, page, scale)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

@@ -1,0 +1,168 @@
+"""Q4_0 x Q8_0 matmul on the GPU against the oracle (ggml CPU semantics), through the C ABI (include/sn_kernels.h).
+
+Tolerances: dequantized weights bit-exact with dequantize_row_q4_0; Q8_0 activations
+bit-exact with the oracle's quantizer on identical inputs; outputs within 1e-3 relative / 2e-3 absolute of the oracle
+(the only difference is the fp32 summation order).
+"""
+import numpy as np
+import pytest
+
+import sllm_next as S
+from oracle import oracle as O
+from tests import gpu_util as U
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 2e-3
+
+
+def setup_module(module):
+    U.torch().cuda.init()
+
+
+def gemm_gpu(Wq, N, K, X, epi=0, y0=None, wbuf=None):
+    L = S.lib()
+    st = U.stream()
+    M = X.shape[0]
+    if wbuf is None:
+        wraw = U.dev(Wq)
+        wbuf = U.empty(L.snk_q4_stripes_bytes(N, K))
+        assert L.snk_q4_repack(U.ptr(wraw), N, K, U.ptr(wbuf), st) == 0
+    x = U.dev(X.astype(np.float32))
+    xa = U.empty(L.snk_xa_bytes(M, K))
+    assert L.snk_quant_act(U.ptr(x), M, K, K, None, 0.0, U.ptr(xa), st) == 0
+    outN = N // 2 if epi == 2 else N
+    y = U.dev(y0.astype(np.float32)) if y0 is not None else U.empty(M * outN * 4)
+    wsb = L.snk_q4_workspace_bytes(M, N, K)
+    ws = U.empty(wsb)
+    assert L.snk_q4_gemm(U.ptr(wbuf), U.ptr(xa), M, N, K, U.ptr(y), outN, epi, U.ptr(ws), wsb, st) == 0
+    return U.host(y, np.float32)[:M * outN].reshape(M, outN), U.host(xa, np.uint8)
+
+
+def test_mfma_layout_probe():
+    # A[i][k] at lane i + 16 (k // 8), slot k % 8; B[k][j] at lane j + 16 (k // 8), slot k % 8;
+    # D[i][j] at lane j + 16 (i // 4), slot i % 4 -- the layout every kernel here assumes.
+    r = np.random.default_rng(0)
+    A = r.integers(-4, 5, (16, 32)).astype(np.float16)
+    B = r.integers(-4, 5, (32, 16)).astype(np.float16)
+    a = np.zeros((64, 8), np.float16)
+    b = np.zeros((64, 8), np.float16)
+    for lane in range(64):
+        for s in range(8):
+            a[lane, s] = A[lane % 16, 8 * (lane // 16) + s]
+            b[lane, s] = B[8 * (lane // 16) + s, lane % 16]
+    da, db = U.dev(a), U.dev(b)
+    dd = U.empty(64 * 4 * 4)
+    assert S.lib().snk_mfma_probe(U.ptr(da), U.ptr(db), U.ptr(dd), U.stream()) == 0
+    d = U.host(dd, np.float32)[:256].reshape(64, 4)
+    D = A.astype(np.float32) @ B.astype(np.float32)
+    want = np.zeros((64, 4), np.float32)
+    for lane in range(64):
+        for v in range(4):
+            want[lane, v] = D[4 * (lane // 16) + v, lane % 16]
+    assert np.array_equal(d, want)
+
+
+def test_dequant_bit_exact():
+    r = np.random.default_rng(1)
+    N, K = 200, 352  # rows not a multiple of 16, blocks not a multiple of 4
+    w = r.normal(0, 0.02, (N, K)).astype(np.float32)
+    w[0, :32] = 0
+    Wq = O.quantize_q4_0(w)
+    L = S.lib()
+    wraw = U.dev(Wq)
+    wbuf = U.empty(L.snk_q4_stripes_bytes(N, K))
+    st = U.stream()
+    assert L.snk_q4_repack(U.ptr(wraw), N, K, U.ptr(wbuf), st) == 0
+    out = U.empty(N * K * 4)
+    assert L.snk_q4_dequant(U.ptr(wbuf), N, K, U.ptr(out), st) == 0
+    got = U.host(out, np.float32)[:N * K].reshape(N, K)
+    want = O.dequantize_q4_0(Wq, K)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_activation_quantization_bit_exact():
+    r = np.random.default_rng(2)
+    M, K = 37, 2560
+    X = r.normal(0, 1, (M, K)).astype(np.float32)
+    X[3, :64] = 0.0
+    X[5] *= 1e-3
+    Wq = O.quantize_q4_0(r.normal(0, 0.02, (16, K)).astype(np.float32))
+    _, xa = gemm_gpu(Wq, 16, K, X)
+    got = U.xa_decode(xa, M, K)
+    want = O.dequantize_q8_0(O.quantize_q8_0(X), K)
+    # the same Q8_0 blocks; each value held as fp16 hi + lo, exact except below fp16's normal range (2^-25 absolute)
+    normal = [m for m in range(M) if m != 5]
+    assert np.array_equal(got[normal], want[normal])
+    assert np.all(np.abs(got - want) <= 2.0 ** -25)
+
+
+def test_config1_q4_matmul_4096x4096_b8():
+    # W 4096x4096 ~ N(0, 0.02) quantized with ggml's reference quantizer, X [8, 4096] ~ N(0, 1)
+    r = np.random.default_rng(1)
+    N = K = 4096
+    Wq = O.quantize_q4_0(r.normal(0, 0.02, (N, K)).astype(np.float32))
+    X = r.normal(0, 1, (8, K)).astype(np.float32)
+    Y, _ = gemm_gpu(Wq, N, K, X)
+    ref = O.mul_mat_q4_0(Wq, K, X)
+    err = np.abs(Y - ref)
+    print(f"config 1: max abs err {err.max():.3g}, max rel {np.max(err / (np.abs(ref) + 1e-30)):.3g}")
+    assert np.all(err <= ATOL + RTOL * np.abs(ref))
+    # the exact value: fp64 over the Q8_0 activations
+    ex = O.mul_mat_q4_0_f64(Wq, K, O.dequantize_q8_0(O.quantize_q8_0(X), K))
+    assert np.max(np.abs(Y - ex)) <= 1e-5 * np.max(np.abs(ex))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (3, 160, 96), (16, 512, 512), (17, 6144, 2560), (32, 2560, 9728),
+                                   (33, 1024, 4096), (64, 304, 1024)])
+def test_matmul_shapes(M, N, K):
+    r = np.random.default_rng(M * 7 + N)
+    Wq = O.quantize_q4_0(r.normal(0, 0.02, (N, K)).astype(np.float32))
+    X = r.normal(0, 1, (M, K)).astype(np.float32)
+    Y, _ = gemm_gpu(Wq, N, K, X)
+    ref = O.mul_mat_q4_0(Wq, K, X)
+    assert np.all(np.abs(Y - ref) <= ATOL + RTOL * np.abs(ref))
+
+
+def test_epilogue_add_and_swiglu():
+    r = np.random.default_rng(3)
+    M, F, K = 20, 256, 512
+    Wg = O.quantize_q4_0(r.normal(0, 0.02, (F, K)).astype(np.float32))
+    Wu = O.quantize_q4_0(r.normal(0, 0.02, (F, K)).astype(np.float32))
+    X = r.normal(0, 1, (M, K)).astype(np.float32)
+    # add into an existing output
+    y0 = r.normal(0, 1, (M, F)).astype(np.float32)
+    Y, _ = gemm_gpu(Wg, F, K, X, epi=1, y0=y0)
+    ref = y0 + O.mul_mat_q4_0(Wg, K, X)
+    assert np.all(np.abs(Y - ref) <= ATOL + RTOL * np.abs(ref))
+    # SwiGLU over gate / up stripes interleaved in pairs
+    L = S.lib()
+    st = U.stream()
+    sb = L.snk_q4_stripes_bytes(F, K)
+    gb, ub = U.empty(sb), U.empty(sb)
+    assert L.snk_q4_repack(U.ptr(U.dev(Wg)), F, K, U.ptr(gb), st) == 0
+    assert L.snk_q4_repack(U.ptr(U.dev(Wu)), F, K, U.ptr(ub), st) == 0
+    per = sb // (F // 16)
+    g = U.host(gb, np.uint8)[:sb].reshape(F // 16, per)
+    u = U.host(ub, np.uint8)[:sb].reshape(F // 16, per)
+    inter = np.stack([g, u], axis=1).reshape(-1)
+    Y, _ = gemm_gpu(None, 2 * F, K, X, epi=2, wbuf=U.dev(inter))
+    gg = O.mul_mat_q4_0(Wg, K, X).astype(np.float64)
+    uu = O.mul_mat_q4_0(Wu, K, X).astype(np.float64)
+    ref = gg / (1 + np.exp(-gg)) * uu
+    assert np.all(np.abs(Y - ref) <= ATOL + RTOL * np.abs(ref))
+
+
+def test_row_invariance_bitwise():
+    # a row's result is the same whatever the other rows of the step (sn.h:1-3; qbench.m's b1 == b8 == b32)
+    r = np.random.default_rng(4)
+    N, K = 1536, 2560
+    Wq = O.quantize_q4_0(r.normal(0, 0.02, (N, K)).astype(np.float32))
+    X = r.normal(0, 1, (40, K)).astype(np.float32)
+    L = S.lib()
+    wbuf = U.empty(L.snk_q4_stripes_bytes(N, K))
+    assert L.snk_q4_repack(U.ptr(U.dev(Wq)), N, K, U.ptr(wbuf), U.stream()) == 0
+    full, _ = gemm_gpu(None, N, K, X, wbuf=wbuf)
+    for rows in ([0], [5, 6, 7], list(range(17)), list(range(8, 40))):
+        part, _ = gemm_gpu(None, N, K, X[rows], wbuf=wbuf)
+        assert np.array_equal(part.view(np.uint32), full[rows].view(np.uint32))

@@ -1,0 +1,72 @@
+"""Row kernels of the step on the GPU against the oracle: the RMSNorm fused in front of the Q8_0 activation quantizer,
+and per-head QK-norm + NEOX RoPE + the fp16 K/V cache write, through the C ABI (include/sn_kernels.h)."""
+import numpy as np
+import pytest
+
+import sllm_next as S
+from oracle import oracle as O
+from tests import gpu_util as U
+
+pytestmark = pytest.mark.gpu
+
+
+def setup_module(module):
+    U.torch().cuda.init()
+
+
+def test_rmsnorm_then_q8_0():
+    r = np.random.default_rng(20)
+    M, K, eps = 24, 2560, 1e-6
+    X = (r.normal(0, 1, (M, K)) * r.uniform(0.01, 5, (M, 1))).astype(np.float32)
+    w = r.normal(1, 0.1, K).astype(np.float32)
+    L = S.lib()
+    x, dw = U.dev(X), U.dev(w)
+    xa = U.empty(L.snk_xa_bytes(M, K))
+    assert L.snk_quant_act(U.ptr(x), M, K, K, U.ptr(dw), eps, U.ptr(xa), U.stream()) == 0
+    got = U.xa_decode(U.host(xa, np.uint8), M, K)
+    xn = O.rmsnorm(X, w, eps)
+    want = O.dequantize_q8_0(O.quantize_q8_0(xn), K)
+    # the norm's sum of squares runs in another order, so a value may sit one rounding step to the other side of a
+    # quantization boundary; every value is within one Q8_0 step and nearly all are identical
+    step = np.repeat(np.abs(O.quantize_q8_0(xn).reshape(M, -1, 34)[:, :, :2].copy().view(np.float16)[..., 0]
+                            .astype(np.float32)), 32, axis=1)
+    assert np.all(np.abs(got - want) <= step * 1.001 + 1e-30)
+    assert np.mean(got == want) > 0.999
+
+
+@pytest.mark.parametrize("page", [32, 64])
+def test_qk_norm_rope_and_cache_write(page):
+    r = np.random.default_rng(21)
+    H, KVH, D, eps, base = 32, 8, 128, 1e-6, 1e6
+    R = 7
+    seq = np.array([0, 0, 1, 2, 2, 2, 3], np.int32)
+    pos = np.array([0, 1, 5, 4095, 100, 33, 2048], np.int32)
+    maxp = 4096 // page
+    npg = 4 * maxp
+    pt = r.permutation(npg).astype(np.int32).reshape(4, maxp)
+    qkv = r.normal(0, 2, (R, (H + 2 * KVH) * D)).astype(np.float32)
+    qw = r.normal(1, 0.1, D).astype(np.float32)
+    kw = r.normal(1, 0.1, D).astype(np.float32)
+    ts = np.float32(np.power(np.float32(base), np.float32(-2.0 / D)))
+    L = S.lib()
+    d_qkv = U.dev(qkv)
+    kp = U.empty(npg * KVH * page * D * 2)
+    vp = U.empty(npg * KVH * page * D * 2)
+    assert L.snk_qk_rope(U.ptr(d_qkv), (H + 2 * KVH) * D, R, H, KVH, U.ptr(U.dev(qw)), U.ptr(U.dev(kw)), eps, float(ts),
+                         U.ptr(U.dev(seq)), U.ptr(U.dev(pos)), U.ptr(U.dev(pt)), maxp, page, U.ptr(kp), U.ptr(vp),
+                         U.stream()) == 0
+    q_out = U.host(d_qkv, np.float32)[:qkv.size].reshape(qkv.shape)
+    kpool = U.host(kp, np.uint16)[:npg * KVH * page * D].reshape(npg, KVH, page, D)
+    vpool = U.host(vp, np.uint16)[:npg * KVH * page * D].reshape(npg, KVH, page, D)
+    for i in range(R):
+        cs = O.rope_cache(int(pos[i]), ts, D)
+        pg, off = pt[seq[i], pos[i] // page], pos[i] % page
+        for h in range(H):
+            want = O.qk_norm_rope(qkv[i, h * D:(h + 1) * D], qw, eps, cs)
+            assert np.allclose(q_out[i, h * D:(h + 1) * D], want, rtol=2e-5, atol=2e-6), (i, h)
+        for h in range(KVH):
+            k = O.qk_norm_rope(qkv[i, (H + h) * D:(H + h + 1) * D], kw, eps, cs)
+            got = kpool[pg, h, off].view(np.float16).astype(np.float32)
+            assert np.allclose(got, k.astype(np.float16).astype(np.float32), rtol=2e-3, atol=1e-3), (i, h)
+            v = qkv[i, (H + KVH + h) * D:(H + KVH + h + 1) * D]
+            assert np.array_equal(vpool[pg, h, off], v.astype(np.float16).view(np.uint16)), (i, h)
