@@ -58,27 +58,39 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
             }
     }
 
-    // cell addresses: K rows for S (cell = cbase + 16 jg + n), V rows for O (cells cbase + 32 st + 16 jg + 4 g + v)
+    // The wavefront's 64 cells lie in one page (64-cell pages) or two (32-cell pages): their page ids are uniform, read
+    // once. Every K and V load of the wavefront is issued here, before any arithmetic, so the whole 32 KB is in flight
+    // at once (V does not depend on the scores).
     const int32_t* ptrow = a.pt + (size_t) gr.seq * a.max_pages;
-    auto cell_ptr = [&](const uint16_t* pool, int c) -> const uint16_t* {
-        const int p = ptrow[c / a.page_cells];
-        return pool + ((size_t) p * a.KVH + kvh) * head_stride + (size_t) (c % a.page_cells) * ATT_D;
-    };
+    const int pc = a.page_cells;
+    const int p_lo = cbase <= pos_last ? ptrow[cbase / pc] : 0;
+    const int p_hi = cbase + 32 <= pos_last ? ptrow[(cbase + 32) / pc] : p_lo;
+    const uint16_t* kbase0 = a.kpool + ((size_t) p_lo * a.KVH + kvh) * head_stride;
+    const uint16_t* kbase1 = a.kpool + ((size_t) p_hi * a.KVH + kvh) * head_stride;
+    const uint16_t* vbase0 = a.vpool + ((size_t) p_lo * a.KVH + kvh) * head_stride;
+    const uint16_t* vbase1 = a.vpool + ((size_t) p_hi * a.KVH + kvh) * head_stride;
+    auto cell_off = [&](int c) { return (size_t) (c % pc) * ATT_D; };  // c - cbase < 64
+    u32x4 kf[4][4], vf[2][8];
+    for (int jg = 0; jg < 4; ++jg) {
+        const int c = cbase + 16 * jg + n;
+        const uint16_t* kp = (c - cbase < 32 ? kbase0 : kbase1) + cell_off(c);
+        for (int t = 0; t < 4; ++t)
+            kf[jg][t] = c <= pos_last ? *(const u32x4*) (kp + 32 * t + 8 * g) : (u32x4){0u, 0u, 0u, 0u};
+    }
+    for (int st = 0; st < 2; ++st)
+        for (int jj = 0; jj < 2; ++jj)
+            for (int v = 0; v < 4; ++v) {
+                const int c = cbase + 32 * st + 16 * jj + 4 * g + v;
+                const uint16_t* vp = (st == 0 ? vbase0 : vbase1) + cell_off(c);
+                vf[st][4 * jj + v] = c <= pos_last ? *(const u32x4*) (vp + 8 * n) : (u32x4){0u, 0u, 0u, 0u};
+            }
 
     // ---- scores for the wavefront's 64 cells: 4 groups of 16 cells
     floatx4 s[4];
     for (int jg = 0; jg < 4; ++jg) {
-        const int c = cbase + 16 * jg + n;
-        u32x4 kf[4];
-        if (c <= pos_last) {
-            const uint16_t* kp = cell_ptr(a.kpool, c);
-            for (int t = 0; t < 4; ++t) kf[t] = *(const u32x4*) (kp + 32 * t + 8 * g);
-        } else {
-            for (int t = 0; t < 4; ++t) kf[t] = (u32x4){0u, 0u, 0u, 0u};
-        }
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
         for (int t = 0; t < 4; ++t) {
-            const half8 kh = __builtin_bit_cast(half8, kf[t]);
+            const half8 kh = __builtin_bit_cast(half8, kf[jg][t]);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[t], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[t], acc, 0, 0, 0);
         }
@@ -114,15 +126,9 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
         half8 ph, pl;
         for (int jj = 0; jj < 2; ++jj)
             for (int v = 0; v < 4; ++v) split_hl(s[2 * st + jj][v], ph, pl, 4 * jj + v);
-        u32x4 vf[8];
-        for (int jj = 0; jj < 2; ++jj)
-            for (int v = 0; v < 4; ++v) {
-                const int c = cbase + 32 * st + 16 * jj + 4 * g + v;
-                vf[4 * jj + v] = c <= pos_last ? *(const u32x4*) (cell_ptr(a.vpool, c) + 8 * n) : (u32x4){0u, 0u, 0u, 0u};
-            }
         for (int t = 0; t < 8; ++t) {
             u32x4 bw;
-            for (int i = 0; i < 4; ++i) bw[i] = pick_half(vf[2 * i][t >> 1], vf[2 * i + 1][t >> 1], t & 1);
+            for (int i = 0; i < 4; ++i) bw[i] = pick_half(vf[st][2 * i][t >> 1], vf[st][2 * i + 1][t >> 1], t & 1);
             const half8 vb = __builtin_bit_cast(half8, bw);
             o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vb, o[t], 0, 0, 0);
             o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, o[t], 0, 0, 0);
@@ -160,7 +166,9 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
     }
 }
 
-// per (row, head): the chunks' partials in chunk order; out = acc / l. One wavefront, 2 dims a lane.
+// per (row, head): the chunks' partials in chunk order; out = acc / l. One wavefront, 2 dims a lane. With a.xa the
+// head's 128 outputs (4 Q8_0 blocks of the o-projection's input row) are also quantized there, exactly as the
+// activation quantizer does (ggml x86 quantize_row_q8_0), into the xa operand of K = H * 128.
 __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
     const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const int nc = a.row_pos[r] / ATT_CHUNK + 1;
@@ -178,9 +186,30 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
         M = mn;
     }
     const float il = L > 0.0f ? 1.0f / L : 0.0f;
-    float* out = a.out + (size_t) r * a.ldo + (size_t) h * ATT_D;
-    out[2 * lane] = o0 * il;
-    out[2 * lane + 1] = o1 * il;
+    o0 *= il;
+    o1 *= il;
+    if (a.out) {
+        float* out = a.out + (size_t) r * a.ldo + (size_t) h * ATT_D;
+        out[2 * lane] = o0;
+        out[2 * lane + 1] = o1;
+    }
+    if (a.xa) {
+        // block b = lane / 16 holds dims 32 b + 2 (lane % 16) and + 1
+        float amax = fmaxf(fabsf(o0), fabsf(o1));
+        for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        const float d = amax / 127.f;
+        const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+        const float dh = (float) (_Float16) d;
+        const int b = lane >> 4, e = 2 * (lane & 15);
+        const int gg = e < 16 ? e / 4 : (e - 16) / 4, j = e < 16 ? e % 4 : 4 + (e - 16) % 4;
+        const int nb = a.H * ATT_D / 32;
+        uint8_t* base = a.xa + ((size_t) ((r >> 4) * nb + h * 4 + b)) * XA_BLOCK_BYTES + 16 * ((r & 15) + 16 * gg) + 2 * j;
+        const float x0 = dh * __builtin_rintf(o0 * id), x1 = dh * __builtin_rintf(o1 * id);
+        const _Float16 h0 = (_Float16) x0, h1 = (_Float16) x1;
+        half2v hi = {h0, h1}, lo = {(_Float16) (x0 - (float) h0), (_Float16) (x1 - (float) h1)};
+        *(half2v*) base = hi;
+        *(half2v*) (base + 1024) = lo;
+    }
 }
 
 int paged_attention(const AttnArgs& a, hipStream_t st) {

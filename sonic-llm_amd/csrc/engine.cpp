@@ -553,8 +553,8 @@ extern "C" int sn_step(sn_engine* e, int R, const int32_t* tok, const int32_t* s
         });
         aa.kpool = kp;
         aa.vpool = vp;
+        aa.xa = e->xa;  // the merge writes the o-projection's Q8_0 operand itself
         rc |= e->launch(SNX_K_ATTN, attn_bytes, [&] { return paged_attention(aa, st); });
-        rc |= quant(e->ao, nullptr, R, QD, nullptr);
         rc |= gemm(l.wo, R, E, QD, e->x, E, EPI_ADD);
         rc |= quant(e->x, nullptr, R, E, l.ffn_norm);
         rc |= gemm(l.wgu, R, 2 * F, E, e->hb, F, EPI_SWIGLU);

@@ -14,7 +14,8 @@ void embed_rows(const float* table, int E, const int32_t* tok, int R, float* x, 
 }
 
 // ---- QK-norm + RoPE + K/V into the cache (qk_rope, kernels.metal:149-197) -------------------------------------------
-// One workgroup (4 wavefronts) per row; a wavefront takes one head at a time, lane i the rotation pair (i, i + 64).
+// Workgroup (row, y): wavefront w takes head 4 y + w, lane i the rotation pair (i, i + 64); workgroups y = 0 also
+// write the row's V.
 // Per head: RMSNorm over 128 dims with weight w, then y_i = x_i cos - x_{i+64} sin, y_{i+64} = x_i sin + x_{i+64} cos
 // with theta_i = p * s^i formed by i successive fp32 multiplies from p (ggml_rope_cache_init's loop), s = base^(-2/128)
 // computed on the host. q stays in place (fp32); k and v go to the row's cell in fp16.
@@ -32,7 +33,8 @@ __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ld
     float* row = qkv + (size_t) r * ldqkv;
     const int page = pt[(size_t) seq[r] * max_pages + p / page_cells];
     const int off = p % page_cells;
-    for (int h = wave; h < H + KVH; h += 4) {
+    const int h = 4 * blockIdx.y + wave;
+    if (h < H + KVH) {
         const bool isq = h < H;
         float* x = row + (size_t) h * 128;  // q heads then k heads, contiguous
         const float* w = isq ? qw : kw;
@@ -52,6 +54,7 @@ __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ld
             kc[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16) y1);
         }
     }
+    if (blockIdx.y != 0) return;
     const float* v = row + (size_t) (H + KVH) * 128;
     for (int i = threadIdx.x; i < KVH * 128; i += 256) {
         const int hh = i / 128, d = i % 128;
@@ -63,8 +66,8 @@ void qk_norm_rope_kv(float* qkv, int ldqkv, int R, int H, int KVH, const float* 
                      float theta_scale, const int32_t* seq, const int32_t* pos, const int32_t* pt, int max_pages,
                      int page_cells, uint16_t* kpool, uint16_t* vpool, hipStream_t st) {
     if (R > 0)
-        hipLaunchKernelGGL(k_qk_rope, dim3(R), dim3(256), 0, st, qkv, ldqkv, H, KVH, qw, kw, eps, theta_scale, seq, pos,
-                           pt, max_pages, page_cells, kpool, vpool);
+        hipLaunchKernelGGL(k_qk_rope, dim3(R, (H + KVH + 3) / 4), dim3(256), 0, st, qkv, ldqkv, H, KVH, qw, kw, eps,
+                           theta_scale, seq, pos, pt, max_pages, page_cells, kpool, vpool);
 }
 
 // ---- greedy argmax (argmax / argmax_p, kernels.metal:327-442) -------------------------------------------------------

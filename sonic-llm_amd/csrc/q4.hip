@@ -51,53 +51,55 @@ __device__ __forceinline__ float block_reduce_sum256(float v, float* red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-__device__ __forceinline__ void quant_block_store(const float* v, int m, int b, int nb, uint8_t* __restrict__ xa) {
-    // v: the block's 32 values (already normed). ggml x86 quantize_row_q8_0.
-    float amax = 0.0f;
-    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    const float d = amax / 127.f;
-    const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
-    const float dh = (float) (_Float16) d;
-    uint8_t* base = xa + ((size_t) ((m >> 4) * nb + b)) * XA_BLOCK_BYTES;
-    for (int g = 0; g < 4; ++g) {
-        half8 hi, lo;
-        for (int j = 0; j < 8; ++j) {
-            const int e = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
-            const float q = __builtin_rintf(v[e] * id);
-            const float x = dh * q;  // exact
-            const _Float16 h = (_Float16) x;
-            hi[j] = h;
-            lo[j] = (_Float16) (x - (float) h);
-        }
-        const int lane = (m & 15) + 16 * g;
-        *(half8*) (base + 16 * lane) = hi;
-        *(half8*) (base + 1024 + 16 * lane) = lo;
-    }
-}
-
+// Four lanes per 32-block: lane part g holds the block's elements {4g..4g+3, 16+4g..16+4g+3}, which is exactly its
+// 8-value fragment of the MFMA operand, so each lane writes one 16-byte hi and one 16-byte lo fragment. The block's
+// amax is a max over the 4 lanes. Workgroup (row m, block group y): 64 blocks; with a norm weight every workgroup of
+// the row first sums the row's squares (the row is read from L2 once per workgroup).
 __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, const int32_t* __restrict__ rows,
                                                    int K, int ldx, const float* __restrict__ nw, float eps,
                                                    uint8_t* __restrict__ xa, float* __restrict__ xn, int ldn) {
     __shared__ float red[4];
-    const int m = blockIdx.x, nb = K / 32;
+    const int m = blockIdx.x, nb = K / 32, t = threadIdx.x;
     const float* x = X + (size_t) (rows ? rows[m] : m) * ldx;
     float scale = 1.0f;
     if (nw) {
         float s = 0.0f;
-        for (int i = threadIdx.x; i < K; i += 256) s += x[i] * x[i];
+        for (int i = t; i < K; i += 256) s += x[i] * x[i];
         s = block_reduce_sum256(s, red);
         scale = 1.0f / sqrtf(s / (float) K + eps);
     }
-    for (int b = threadIdx.x; b < nb; b += 256) {
-        float v[32];
-        for (int j = 0; j < 32; ++j) {
-            const float t = x[32 * b + j];
-            v[j] = nw ? (t * scale) * nw[32 * b + j] : t;
-        }
-        if (xn)
-            for (int j = 0; j < 32; ++j) xn[(size_t) m * ldn + 32 * b + j] = v[j];
-        quant_block_store(v, m, b, nb, xa);
+    const int b = blockIdx.y * 64 + (t >> 2), g = t & 3;
+    if (b >= nb) return;  // (whole 4-lane groups leave together: the shuffles below stay within a group)
+    const float4 lo4 = *(const float4*) (x + 32 * b + 4 * g), hi4 = *(const float4*) (x + 32 * b + 16 + 4 * g);
+    float v[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+    if (nw) {
+        const float4 wl = *(const float4*) (nw + 32 * b + 4 * g), wh = *(const float4*) (nw + 32 * b + 16 + 4 * g);
+        const float w[8] = {wl.x, wl.y, wl.z, wl.w, wh.x, wh.y, wh.z, wh.w};
+        for (int j = 0; j < 8; ++j) v[j] = (v[j] * scale) * w[j];
     }
+    if (xn) {
+        float* o = xn + (size_t) m * ldn + 32 * b;
+        *(float4*) (o + 4 * g) = (float4){v[0], v[1], v[2], v[3]};
+        *(float4*) (o + 16 + 4 * g) = (float4){v[4], v[5], v[6], v[7]};
+    }
+    // ggml x86 quantize_row_q8_0: d = amax / 127 (stored fp16), q = round-half-even(x * 127 / amax)
+    float amax = 0.0f;
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const float d = amax / 127.f;
+    const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+    const float dh = (float) (_Float16) d;
+    half8 hi, lo;
+    for (int j = 0; j < 8; ++j) {
+        const float q = dh * __builtin_rintf(v[j] * id);  // exact
+        const _Float16 h = (_Float16) q;
+        hi[j] = h;
+        lo[j] = (_Float16) (q - (float) h);
+    }
+    uint8_t* base = xa + ((size_t) ((m >> 4) * nb + b)) * XA_BLOCK_BYTES + 16 * ((m & 15) + 16 * g);
+    *(half8*) base = hi;
+    *(half8*) (base + 1024) = lo;
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -297,7 +299,8 @@ void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int 
 void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const float* nw, float eps, uint8_t* xa,
                float* xn, int ldn, hipStream_t st) {
     if (M <= 0) return;
-    hipLaunchKernelGGL(k_quant_act, dim3(M), dim3(256), 0, st, x, rows, K, ldx, nw, eps, xa, xn, ldn);
+    hipLaunchKernelGGL(k_quant_act, dim3(M, (K / 32 + 63) / 64), dim3(256), 0, st, x, rows, K, ldx, nw, eps, xa, xn,
+                       ldn);
 }
 
 // ---------------------------------------------------------------------------------------------------------------------

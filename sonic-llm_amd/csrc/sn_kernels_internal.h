@@ -57,7 +57,7 @@ struct AttnArgs {
     int max_chunks;
     float* out;              // [rows][ldo] fp32 (merge output), or NULL
     int ldo;
-    uint8_t* xa;             // merge output as an xa operand (K = H*D), or NULL
+    uint8_t* xa;             // merge output also as the o-projection's xa operand (K = H*D), or NULL
     int H, KVH;
     float scale;
     int n_rows;

@@ -20,7 +20,7 @@ extern "C" size_t snk_xa_bytes(int M, int K) { return xa_bytes(M, K); }
 
 extern "C" int snk_quant_act(const float* d_x, int M, int K, int ldx, const float* d_norm_w, float eps, void* d_xa,
                              void* stream) {
-    if (M <= 0 || K <= 0 || K % 32 || ldx < K) return -1;
+    if (M <= 0 || K <= 0 || K % 32 || ldx < K || ldx % 4) return -1;
     quant_act(d_x, nullptr, M, K, ldx, d_norm_w, eps, (uint8_t*) d_xa, nullptr, 0, (hipStream_t) stream);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
