@@ -47,15 +47,17 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
     const bool qvalid = qrow < gr.nrows;
     const int qpos = gr.pos0 + qrow;
 
-    // Q^T fragments: MFMA t covers dims 32t .. 32t+31; lane (n, g) holds dims 32t + 8g .. +7 of query n
+    // Q^T fragments: MFMA t covers dims 32t .. 32t+31; lane (n, g) holds dims 32t + 8g .. +7 of query n. Loaded as
+    // 16-byte pieces from a valid row (an unused column reads the group's first row) and zeroed by a select, so no load
+    // sits behind a branch.
     half8 qh[4], ql[4];
     {
         const float* qp = a.q + (size_t) (gr.row0 + (qvalid ? qrow : 0)) * a.ldq + (size_t) qhead * ATT_D;
-        for (int t = 0; t < 4; ++t)
-            for (int j = 0; j < 8; ++j) {
-                const float v = qvalid ? qp[32 * t + 8 * g + j] * a.scale : 0.0f;
-                split_hl(v, qh[t], ql[t], j);
-            }
+        for (int t = 0; t < 4; ++t) {
+            const float4 x0 = *(const float4*) (qp + 32 * t + 8 * g), x1 = *(const float4*) (qp + 32 * t + 8 * g + 4);
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            for (int j = 0; j < 8; ++j) split_hl(qvalid ? xs[j] * a.scale : 0.0f, qh[t], ql[t], j);
+        }
     }
 
     // The wavefront's 64 cells lie in one page (64-cell pages) or two (32-cell pages): their page ids are uniform, read
@@ -70,20 +72,28 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
     const uint16_t* vbase0 = a.vpool + ((size_t) p_lo * a.KVH + kvh) * head_stride;
     const uint16_t* vbase1 = a.vpool + ((size_t) p_hi * a.KVH + kvh) * head_stride;
     auto cell_off = [&](int c) { return (size_t) (c % pc) * ATT_D; };  // c - cbase < 64
+    // Cells past the group's last position are read from the same pages (memory that exists: a page holds whole
+    // cells) and then zeroed by a select (a masked cell's p is exactly 0, and 0 * V must not meet a NaN).
     u32x4 kf[4][4], vf[2][8];
+    const u32x4 z4 = {0u, 0u, 0u, 0u};
     for (int jg = 0; jg < 4; ++jg) {
         const int c = cbase + 16 * jg + n;
         const uint16_t* kp = (c - cbase < 32 ? kbase0 : kbase1) + cell_off(c);
-        for (int t = 0; t < 4; ++t)
-            kf[jg][t] = c <= pos_last ? *(const u32x4*) (kp + 32 * t + 8 * g) : (u32x4){0u, 0u, 0u, 0u};
+        for (int t = 0; t < 4; ++t) kf[jg][t] = *(const u32x4*) (kp + 32 * t + 8 * g);
     }
     for (int st = 0; st < 2; ++st)
         for (int jj = 0; jj < 2; ++jj)
             for (int v = 0; v < 4; ++v) {
                 const int c = cbase + 32 * st + 16 * jj + 4 * g + v;
-                const uint16_t* vp = (st == 0 ? vbase0 : vbase1) + cell_off(c);
-                vf[st][4 * jj + v] = c <= pos_last ? *(const u32x4*) (vp + 8 * n) : (u32x4){0u, 0u, 0u, 0u};
+                vf[st][4 * jj + v] = *(const u32x4*) ((st == 0 ? vbase0 : vbase1) + cell_off(c) + 8 * n);
             }
+    for (int jg = 0; jg < 4; ++jg)
+        if (cbase + 16 * jg + n > pos_last)
+            for (int t = 0; t < 4; ++t) kf[jg][t] = z4;
+    for (int st = 0; st < 2; ++st)
+        for (int jj = 0; jj < 2; ++jj)
+            for (int v = 0; v < 4; ++v)
+                if (cbase + 32 * st + 16 * jj + 4 * g + v > pos_last) vf[st][4 * jj + v] = z4;
 
     // ---- scores for the wavefront's 64 cells: 4 groups of 16 cells
     floatx4 s[4];
@@ -202,8 +212,8 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
         const float dh = (float) (_Float16) d;
         const int b = lane >> 4, e = 2 * (lane & 15);
         const int gg = e < 16 ? e / 4 : (e - 16) / 4, j = e < 16 ? e % 4 : 4 + (e - 16) % 4;
-        const int nb = a.H * ATT_D / 32;
-        uint8_t* base = a.xa + ((size_t) ((r >> 4) * nb + h * 4 + b)) * XA_BLOCK_BYTES + 16 * ((r & 15) + 16 * gg) + 2 * j;
+        const int nbp = xa_nbp(a.H * ATT_D);
+        uint8_t* base = a.xa + ((size_t) ((r >> 4) * nbp + h * 4 + b)) * XA_BLOCK_BYTES + 16 * ((r & 15) + 16 * gg) + 2 * j;
         const float x0 = dh * __builtin_rintf(o0 * id), x1 = dh * __builtin_rintf(o1 * id);
         const _Float16 h0 = (_Float16) x0, h1 = (_Float16) x1;
         half2v hi = {h0, h1}, lo = {(_Float16) (x0 - (float) h0), (_Float16) (x1 - (float) h1)};

@@ -68,8 +68,15 @@ __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, 
         s = block_reduce_sum256(s, red);
         scale = 1.0f / sqrtf(s / (float) K + eps);
     }
+    const int nbp = xa_nbp(K);
     const int b = blockIdx.y * 64 + (t >> 2), g = t & 3;
-    if (b >= nb) return;  // (whole 4-lane groups leave together: the shuffles below stay within a group)
+    if (b >= nbp) return;  // (whole 4-lane groups leave together: the shuffles below stay within a group)
+    uint8_t* base = xa + ((size_t) ((m >> 4) * nbp + b)) * XA_BLOCK_BYTES + 16 * ((m & 15) + 16 * g);
+    if (b >= nb) {  // a padding block of the last 4-block group: zero
+        *(half8*) base = (half8){};
+        *(half8*) (base + 1024) = (half8){};
+        return;
+    }
     const float4 lo4 = *(const float4*) (x + 32 * b + 4 * g), hi4 = *(const float4*) (x + 32 * b + 16 + 4 * g);
     float v[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
     if (nw) {
@@ -97,7 +104,6 @@ __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, 
         hi[j] = h;
         lo[j] = (_Float16) (q - (float) h);
     }
-    uint8_t* base = xa + ((size_t) ((m >> 4) * nb + b)) * XA_BLOCK_BYTES + 16 * ((m & 15) + 16 * g);
     *(half8*) base = hi;
     *(half8*) (base + 1024) = lo;
 }
@@ -125,88 +131,115 @@ __device__ __forceinline__ half8 q4_unpack(uint32_t w) {
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
-// One workgroup = 4 wavefronts; wavefront w owns NT 16-row stripes (consecutive) and sweeps the groups of its k-slice.
-// MT 16-row tiles of activation rows (M <= 16 MT; grid.z walks further row tiles for bigger M).
-template <int MT, int NT>
+// One workgroup (4 wavefronts) owns NT consecutive 16-row stripes (16 NT output columns) of a k-slice; the 4
+// wavefronts split the slice's 4-block groups between them (wavefront w takes groups w, w + 4, ...) and their fp32
+// sums are added in LDS in wavefront order. A wavefront streams its groups with a ring of D groups of weight tiles in
+// flight; the activation fragments of a group (hi and lo, MT row tiles) are loaded with it. Every load is
+// unconditional: stripes past the matrix are clamped to its last stripe (their sums are never stored) and the xa
+// operand is padded (sn_common.h), so no load waits behind a branch.
+template <int MT, int NT, int D>
 __global__ __launch_bounds__(256) void k_q4_gemm(GemmArgs a) {
+    __shared__ floatx4 red[4][NT][MT][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int stripe0 = (blockIdx.x * 4 + wave) * NT;
-    if (stripe0 >= a.nstripes) return;
-    const int slice = blockIdx.y, mt0 = blockIdx.z * MT;
+    const int n_in = lane & 15, g = lane >> 4;
+    const int s0 = blockIdx.x * NT, slice = blockIdx.y, mt0 = blockIdx.z * MT;
     const int c0 = slice * a.gps, c1 = min(c0 + a.gps, a.ngroups);
-    const int nb = a.K / 32;
-    const int n_in = lane & 15;
+    const int ng = c1 - c0 > wave ? (c1 - c0 - wave + 3) / 4 : 0;  // this wavefront's groups: c0 + wave + 4 i
+    const int nbp = a.ngroups * 4;
+    const uint8_t* wp[NT];
+    for (int t = 0; t < NT; ++t) wp[t] = a.w + (size_t) min(s0 + t, a.nstripes - 1) * a.ngroups * Q4T_BYTES;
+    const uint8_t* xp = a.xa + (size_t) mt0 * nbp * XA_BLOCK_BYTES + 16 * lane;
 
     floatx4 acc[NT][MT];
     for (int t = 0; t < NT; ++t)
         for (int mt = 0; mt < MT; ++mt) acc[t][mt] = (floatx4){0.f, 0.f, 0.f, 0.f};
     const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
 
-    for (int c = c0; c < c1; ++c) {
-        half8 ahi[4][MT], alo[4][MT];
-        for (int b = 0; b < 4; ++b) {
-            const int blk = 4 * c + b;
-            for (int mt = 0; mt < MT; ++mt) {
-                if (blk < nb && mt0 + mt < a.mtiles) {
-                    const uint8_t* p = a.xa + ((size_t) (mt0 + mt) * nb + blk) * XA_BLOCK_BYTES + 16 * lane;
-                    ahi[b][mt] = *(const half8*) p;
-                    alo[b][mt] = *(const half8*) (p + 1024);
-                } else {
-                    ahi[b][mt] = (half8){};
-                    alo[b][mt] = (half8){};
-                }
-            }
-        }
+    u32x4 wq[D][NT];
+    half4v ws[D][NT];
+    // group index of the wavefront's i-th group, clamped to its last one (loads past the end repeat it, unused)
+    auto grp = [&](int i) { return c0 + wave + 4 * min(i, max(ng - 1, 0)); };
+    auto load_w = [&](int slot, int i) {
+        const size_t off = (size_t) grp(i) * Q4T_BYTES;
         for (int t = 0; t < NT; ++t) {
-            const int s = stripe0 + t;
-            if (s >= a.nstripes) break;
-            const uint8_t* tp = a.w + ((size_t) s * a.ngroups + c) * Q4T_BYTES;
-            const u32x4 wq = *(const u32x4*) (tp + 16 * lane);
-            // the 4 scales as one 8-byte load of fp16 (a bit_cast of a u32x2 element here lost the second word)
-            const half4v sc = *(const half4v*) (tp + Q4T_SCALE_OFF + 8 * n_in);
-            const float dw[4] = {(float) sc[0], (float) sc[1], (float) sc[2], (float) sc[3]};
-            for (int b = 0; b < 4; ++b) {
-                const half8 bw = q4_unpack(wq[b]);
-                for (int mt = 0; mt < MT; ++mt) {
-                    floatx4 r = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[b][mt], bw, zero, 0, 0, 0);
-                    r = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[b][mt], bw, r, 0, 0, 0);
-                    for (int v = 0; v < 4; ++v) acc[t][mt][v] = __builtin_fmaf(r[v], dw[b], acc[t][mt][v]);
+            wq[slot][t] = *(const u32x4*) (wp[t] + off + 16 * lane);
+            ws[slot][t] = *(const half4v*) (wp[t] + off + Q4T_SCALE_OFF + 8 * n_in);
+        }
+    };
+    if (ng > 0) {
+        for (int j = 0; j < D; ++j) load_w(j, j);
+        for (int i0 = 0; i0 < ng; i0 += D) {
+            for (int j = 0; j < D; ++j) {
+                const int i = i0 + j;
+                if (i >= ng) break;
+                const int c = grp(i);
+                half8 ahi[4][MT], alo[4][MT];
+                for (int b = 0; b < 4; ++b)
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const uint8_t* p = xp + ((size_t) mt * nbp + 4 * c + b) * XA_BLOCK_BYTES;
+                        ahi[b][mt] = *(const half8*) p;
+                        alo[b][mt] = *(const half8*) (p + 1024);
+                    }
+                for (int t = 0; t < NT; ++t) {
+                    const u32x4 w4 = wq[j][t];
+                    const half4v sc = ws[j][t];
+                    for (int b = 0; b < 4; ++b) {
+                        const half8 bw = q4_unpack(w4[b]);
+                        const float dw = (float) sc[b];
+                        for (int mt = 0; mt < MT; ++mt) {
+                            floatx4 r = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[b][mt], bw, zero, 0, 0, 0);
+                            r = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[b][mt], bw, r, 0, 0, 0);
+                            for (int v = 0; v < 4; ++v) acc[t][mt][v] = __builtin_fmaf(r[v], dw, acc[t][mt][v]);
+                        }
+                    }
                 }
+                load_w(j, i + D);  // refill the slot (past the end: the last group again, never used)
             }
         }
     }
 
-    // lane (n, g) holds rows 4g+v of each row tile, column n of each stripe
-    const int g = lane >> 4;
-    for (int t = 0; t < NT; ++t) {
-        const int s = stripe0 + t;
-        if (s >= a.nstripes) break;
-        const int col = s * 16 + n_in;
-        for (int mt = 0; mt < MT; ++mt)
-            for (int v = 0; v < 4; ++v) {
-                const int row = (mt0 + mt) * 16 + 4 * g + v;
-                if (row >= a.M || col >= a.N) continue;
-                const float val = acc[t][mt][v];
-                if (a.ks > 1) {
-                    a.part[((size_t) slice * a.M + row) * a.N + col] = val;
-                } else if (a.epi == EPI_STORE) {
-                    a.y[(size_t) row * a.ldy + col] = val;
-                } else if (a.epi == EPI_ADD) {
-                    a.y[(size_t) row * a.ldy + col] += val;
-                }
+    // the 4 wavefronts' sums, added in wavefront order; wavefront w then finishes stripe(s) of its own
+    for (int t = 0; t < NT; ++t)
+        for (int mt = 0; mt < MT; ++mt) red[wave][t][mt][lane] = acc[t][mt];
+    __syncthreads();
+    for (int t = wave; t < NT; t += 4)
+        for (int mt = 0; mt < MT; ++mt) {
+            floatx4 v4 = red[0][t][mt][lane];
+            for (int w = 1; w < 4; ++w) {
+                const floatx4 o = red[w][t][mt][lane];
+                for (int v = 0; v < 4; ++v) v4[v] += o[v];
             }
-    }
-    if (a.ks == 1 && a.epi == EPI_SWIGLU) {
-        // stripes 2p (gate) and 2p+1 (up) of a pair are in the same wavefront (NT even, stripe0 even)
-        for (int t = 0; t + 1 < NT; t += 2) {
-            const int s = stripe0 + t;
-            if (s + 1 >= a.nstripes) break;
+            red[0][t][mt][lane] = v4;
+        }
+    __syncthreads();
+
+    // lane (n, g) holds rows 4g+v of each row tile, column n of each stripe
+    if (a.ks > 1 || a.epi != EPI_SWIGLU) {
+        for (int t = wave; t < NT; t += 4) {
+            const int s = s0 + t;
+            const int col = s * 16 + n_in;
+            if (s >= a.nstripes || col >= a.N) continue;
+            for (int mt = 0; mt < MT; ++mt)
+                for (int v = 0; v < 4; ++v) {
+                    const int row = (mt0 + mt) * 16 + 4 * g + v;
+                    if (row >= a.M) continue;
+                    const float val = red[0][t][mt][lane][v];
+                    if (a.ks > 1) a.part[((size_t) slice * a.M + row) * a.N + col] = val;
+                    else if (a.epi == EPI_STORE) a.y[(size_t) row * a.ldy + col] = val;
+                    else a.y[(size_t) row * a.ldy + col] += val;
+                }
+        }
+    } else {
+        // stripes 2p (gate) and 2p + 1 (up) of a pair are both in this workgroup (NT even, s0 even)
+        for (int t = 2 * wave; t + 1 < NT; t += 8) {
+            const int s = s0 + t;
+            if (s + 1 >= a.nstripes) continue;
             const int col = (s / 2) * 16 + n_in;
             for (int mt = 0; mt < MT; ++mt)
                 for (int v = 0; v < 4; ++v) {
                     const int row = (mt0 + mt) * 16 + 4 * g + v;
                     if (row >= a.M || col >= a.N / 2) continue;
-                    a.y[(size_t) row * a.ldy + col] = silu(acc[t][mt][v]) * acc[t + 1][mt][v];
+                    a.y[(size_t) row * a.ldy + col] = silu(red[0][t][mt][lane][v]) * red[0][t + 1][mt][lane][v];
                 }
         }
     }
@@ -237,17 +270,17 @@ __global__ void k_q4_reduce(GemmArgs a) {
 // ---------------------------------------------------------------------------------------------------------------------
 // host side
 
-// The launch shape of a matrix depends on (N, K) only, never on the rows (row invariance).
+// The launch shape of a matrix depends on (N, K) only, never on the rows (row invariance): NT = 4 stripes per
+// workgroup, and k-slices across workgroups only while there are fewer than 1024 wavefronts and each slice keeps at
+// least 16 groups (2048 values), so the slices' partial sums stay a small fraction of the weight bytes.
 GemmPlan q4_plan(int N, int K) {
     GemmPlan p;
     p.nstripes = (N + 15) / 16;
     p.ngroups = (K / 32 + 3) / 4;
-    p.nt = p.nstripes >= 4096 ? 2 : 1;
-    const int waves = (p.nstripes + p.nt - 1) / p.nt;
-    // k-slices of at least 4 groups (512 values) until there are about 2048 wavefronts
+    p.nt = 4;
+    const int wgs = (p.nstripes + p.nt - 1) / p.nt;
     int ks = 1;
-    while (waves * ks < 2048 && (p.ngroups + ks) / (ks + 1) >= 4) ++ks;
-    p.ks = ks;
+    while (wgs * ks * 4 < 1024 && p.ngroups / (ks + 1) >= 16) ++ks;
     p.gps = (p.ngroups + ks - 1) / ks;
     p.ks = (p.ngroups + p.gps - 1) / p.gps;
     return p;
@@ -258,10 +291,10 @@ size_t q4_workspace_bytes(int M, int N, int K) {
     return p.ks > 1 ? (size_t) p.ks * M * N * sizeof(float) : 0;
 }
 
-template <int MT, int NT>
+template <int MT>
 static void launch_mt(const GemmArgs& a, int mblocks, hipStream_t st) {
-    dim3 grid((a.nstripes + 4 * NT - 1) / (4 * NT), a.ks, mblocks);
-    hipLaunchKernelGGL((k_q4_gemm<MT, NT>), grid, dim3(256), 0, st, a);
+    dim3 grid((a.nstripes + 3) / 4, a.ks, mblocks);
+    hipLaunchKernelGGL((k_q4_gemm<MT, 4, 3>), grid, dim3(256), 0, st, a);
 }
 
 int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* part,
@@ -273,16 +306,9 @@ int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, 
     a.M = M; a.N = N; a.K = K; a.ldy = ldy; a.epi = epi;
     a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
     a.mtiles = (M + 15) / 16;
-    int nt = p.nt;
-    if (epi == EPI_SWIGLU && nt < 2) nt = 2;  // a gate/up stripe pair in one wavefront
     if (p.ks > 1 && (part == nullptr || part_bytes < (size_t) p.ks * M * N * sizeof(float))) return -1;
-    const int MT = a.mtiles == 1 ? 1 : 2;
-    const int mblocks = (a.mtiles + MT - 1) / MT;
-    if (MT == 1) {
-        if (nt == 1) launch_mt<1, 1>(a, mblocks, st); else launch_mt<1, 2>(a, mblocks, st);
-    } else {
-        if (nt == 1) launch_mt<2, 1>(a, mblocks, st); else launch_mt<2, 2>(a, mblocks, st);
-    }
+    if (a.mtiles == 1) launch_mt<1>(a, 1, st);
+    else launch_mt<2>(a, (a.mtiles + 1) / 2, st);
     if (p.ks > 1) {
         const int outN = epi == EPI_SWIGLU ? N / 2 : N;
         const int tot = M * outN;
@@ -299,7 +325,7 @@ void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int 
 void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const float* nw, float eps, uint8_t* xa,
                float* xn, int ldn, hipStream_t st) {
     if (M <= 0) return;
-    hipLaunchKernelGGL(k_quant_act, dim3(M, (K / 32 + 63) / 64), dim3(256), 0, st, x, rows, K, ldx, nw, eps, xa, xn,
+    hipLaunchKernelGGL(k_quant_act, dim3(M, (xa_nbp(K) + 63) / 64), dim3(256), 0, st, x, rows, K, ldx, nw, eps, xa, xn,
                        ldn);
 }
 

@@ -45,8 +45,11 @@ void sn_set_err(char* err, int err_len, const char* fmt, ...);
 // stored as two fp16 values hi = fp16(v), lo = fp16(v - hi), which together hold v to within 2^-25 absolute.
 // Layout for row tile mt (16 rows) and block b: 2048 bytes = [hi: 64 lanes x 8 halves][lo: 64 lanes x 8 halves];
 // lane l = m + 16 g holds elements {4g..4g+3, 16+4g..16+4g+3} of row m (the same order as the weight tile lanes),
-// so one 16-byte load per lane gives the A operand of v_mfma_f32_16x16x32_f16.
+// so one 16-byte load per lane gives the A operand of v_mfma_f32_16x16x32_f16. A row tile holds xa_nbp(K) blocks (K/32
+// rounded up to a multiple of 4; the extra blocks are zero) and the row tiles are rounded up to an even count, so the
+// matmul's loads of a 4-block group of 2 row tiles never leave the buffer.
 #define XA_BLOCK_BYTES 2048
 
-static inline size_t xa_bytes(int M, int K) { return (size_t) ((M + 15) / 16) * (K / 32) * XA_BLOCK_BYTES; }
+__host__ __device__ static inline int xa_nbp(int K) { return (K / 32 + 3) / 4 * 4; }
+static inline size_t xa_bytes(int M, int K) { return (size_t) ((M + 31) / 32 * 2) * xa_nbp(K) * XA_BLOCK_BYTES; }
 static inline size_t q4t_bytes(int N, int K) { return (size_t) ((N + 15) / 16) * ((K / 32 + 3) / 4) * Q4T_BYTES; }

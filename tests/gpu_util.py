@@ -41,8 +41,9 @@ def stream():
 def xa_decode(xa: np.ndarray, M: int, K: int) -> np.ndarray:
     """The activation operand (hi + lo fp16 fragments) back to fp32 rows [M][K], undoing the lane layout."""
     nb = K // 32
+    nbp = (nb + 3) // 4 * 4  # blocks per row tile (padded to whole 4-block groups)
     mt = (M + 15) // 16
-    a = xa.view(np.float16).reshape(mt, nb, 2, 4, 16, 8).astype(np.float32)  # [mt][b][hi/lo][g][m][j]
+    a = xa.view(np.float16)[:mt * nbp * 1024].reshape(mt, nbp, 2, 4, 16, 8)[:, :nb].astype(np.float32)
     v = a[:, :, 0] + a[:, :, 1]  # [mt][b][g][m][j]
     out = np.zeros((mt * 16, K), np.float32)
     for g in range(4):
