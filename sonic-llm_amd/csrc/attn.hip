@@ -209,16 +209,13 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
         for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
         const float d = amax / 127.f;
         const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
-        const float dh = (float) (_Float16) d;
         const int b = lane >> 4, e = 2 * (lane & 15);
         const int gg = e < 16 ? e / 4 : (e - 16) / 4, j = e < 16 ? e % 4 : 4 + (e - 16) % 4;
-        const int nbp = xa_nbp(a.H * ATT_D);
-        uint8_t* base = a.xa + ((size_t) ((r >> 4) * nbp + h * 4 + b)) * XA_BLOCK_BYTES + 16 * ((r & 15) + 16 * gg) + 2 * j;
-        const float x0 = dh * __builtin_rintf(o0 * id), x1 = dh * __builtin_rintf(o1 * id);
-        const _Float16 h0 = (_Float16) x0, h1 = (_Float16) x1;
-        half2v hi = {h0, h1}, lo = {(_Float16) (x0 - (float) h0), (_Float16) (x1 - (float) h1)};
-        *(half2v*) base = hi;
-        *(half2v*) (base + 1024) = lo;
+        const int K = a.H * ATT_D, blk = h * 4 + b;
+        uint8_t* frag = a.xa + xa_frag_off(K, r >> 4, blk) + 16 * ((r & 15) + 16 * gg) + 2 * j;
+        const half2v q = {(_Float16) __builtin_rintf(o0 * id), (_Float16) __builtin_rintf(o1 * id)};
+        *(half2v*) frag = q;
+        if ((lane & 15) == 0) *((_Float16*) (a.xa + xa_scale_off(a.n_rows, K, r >> 4, blk)) + (r & 15)) = (_Float16) d;
     }
 }
 

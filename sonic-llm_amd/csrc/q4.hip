@@ -4,11 +4,12 @@
 // mvm_q4_0_*, :746-1007 qmm_ks/qmmh_ks_q4_0_*, dispatched by mm() in core_mm.inc.h:307-325), with ggml's CPU numerics
 // (Q8_0-quantized activations, integer block sums scaled by dw*dx) instead of the reference's fp16 weights.
 //
-// How a block's sum is formed: the weights' (q-8) are exact in fp16, the activation's dx*q8 is exact as an fp16
-// hi + lo pair, and v_mfma_f32_16x16x32_f16 multiplies exactly and accumulates in fp32, so the two MFMAs of a block
-// give dx*isum (to fp32 rounding); one fma per output then adds dw * that to the fp32 accumulator. Each output's sum
-// runs over blocks in K order within a k-slice, and k-slices are added in slice order; neither depends on the number
-// of rows, so a row's result is the same in any step (sn.h:1-3).
+// How a block's sum is formed: the weights' (q4 - 8) and the activations' q8 are exact in fp16, and
+// v_mfma_f32_16x16x32_f16 multiplies exactly and accumulates in fp32, where every partial sum of a block (|sum| <=
+// 32512) is an exact integer: the MFMA gives ggml's integer block sum isum. One fma per output then adds
+// isum * (dw * dx) (the product of two fp16 values is exact in fp32) to the fp32 accumulator. The order of the sums
+// of an output is fixed by (N, K) alone, never by the number of rows, so a row's result is the same in any step
+// (sn.h:1-3).
 #include "sn_kernels_internal.h"
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -56,7 +57,7 @@ __device__ __forceinline__ float block_reduce_sum256(float v, float* red) {
 // amax is a max over the 4 lanes. Workgroup (row m, block group y): 64 blocks; with a norm weight every workgroup of
 // the row first sums the row's squares (the row is read from L2 once per workgroup).
 __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, const int32_t* __restrict__ rows,
-                                                   int K, int ldx, const float* __restrict__ nw, float eps,
+                                                   int M, int K, int ldx, const float* __restrict__ nw, float eps,
                                                    uint8_t* __restrict__ xa, float* __restrict__ xn, int ldn) {
     __shared__ float red[4];
     const int m = blockIdx.x, nb = K / 32, t = threadIdx.x;
@@ -71,10 +72,11 @@ __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, 
     const int nbp = xa_nbp(K);
     const int b = blockIdx.y * 64 + (t >> 2), g = t & 3;
     if (b >= nbp) return;  // (whole 4-lane groups leave together: the shuffles below stay within a group)
-    uint8_t* base = xa + ((size_t) ((m >> 4) * nbp + b)) * XA_BLOCK_BYTES + 16 * ((m & 15) + 16 * g);
+    uint8_t* frag = xa + xa_frag_off(K, m >> 4, b) + 16 * ((m & 15) + 16 * g);
+    _Float16* dsl = (_Float16*) (xa + xa_scale_off(M, K, m >> 4, b)) + (m & 15);
     if (b >= nb) {  // a padding block of the last 4-block group: zero
-        *(half8*) base = (half8){};
-        *(half8*) (base + 1024) = (half8){};
+        *(half8*) frag = (half8){};
+        if (g == 0) *dsl = (_Float16) 0.0f;
         return;
     }
     const float4 lo4 = *(const float4*) (x + 32 * b + 4 * g), hi4 = *(const float4*) (x + 32 * b + 16 + 4 * g);
@@ -96,16 +98,10 @@ __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, 
     amax = fmaxf(amax, __shfl_xor(amax, 2));
     const float d = amax / 127.f;
     const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
-    const float dh = (float) (_Float16) d;
-    half8 hi, lo;
-    for (int j = 0; j < 8; ++j) {
-        const float q = dh * __builtin_rintf(v[j] * id);  // exact
-        const _Float16 h = (_Float16) q;
-        hi[j] = h;
-        lo[j] = (_Float16) (q - (float) h);
-    }
-    *(half8*) base = hi;
-    *(half8*) (base + 1024) = lo;
+    half8 q;
+    for (int j = 0; j < 8; ++j) q[j] = (_Float16) __builtin_rintf(v[j] * id);
+    *(half8*) frag = q;
+    if (g == 0) *dsl = (_Float16) d;
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -133,22 +129,25 @@ __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
 // One workgroup (4 wavefronts) owns NT consecutive 16-row stripes (16 NT output columns) of a k-slice; the 4
 // wavefronts split the slice's 4-block groups between them (wavefront w takes groups w, w + 4, ...) and their fp32
-// sums are added in LDS in wavefront order. A wavefront streams its groups with a ring of D groups of weight tiles in
-// flight; the activation fragments of a group (hi and lo, MT row tiles) are loaded with it. Every load is
-// unconditional: stripes past the matrix are clamped to its last stripe (their sums are never stored) and the xa
-// operand is padded (sn_common.h), so no load waits behind a branch.
+// sums are added in LDS in wavefront order. A wavefront streams its groups with a ring of D groups of weight tiles;
+// the activation fragments and scales of a group are loaded one group ahead, before the weight refill of the group
+// being computed, so that waiting for them (vmcnt counts in issue order) leaves the newer weight loads in flight.
+// Every load is unconditional: stripes past the matrix are clamped to its last stripe (their sums are never stored),
+// groups past a wavefront's last repeat it, and the xa operand is padded (sn_common.h), so no load waits on a branch.
 template <int MT, int NT, int D>
 __global__ __launch_bounds__(256) void k_q4_gemm(GemmArgs a) {
+    constexpr int U = D % 2 ? 2 * D : D;  // unroll: a multiple of both ring sizes
     __shared__ floatx4 red[4][NT][MT][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n_in = lane & 15, g = lane >> 4;
     const int s0 = blockIdx.x * NT, slice = blockIdx.y, mt0 = blockIdx.z * MT;
     const int c0 = slice * a.gps, c1 = min(c0 + a.gps, a.ngroups);
     const int ng = c1 - c0 > wave ? (c1 - c0 - wave + 3) / 4 : 0;  // this wavefront's groups: c0 + wave + 4 i
-    const int nbp = a.ngroups * 4;
     const uint8_t* wp[NT];
     for (int t = 0; t < NT; ++t) wp[t] = a.w + (size_t) min(s0 + t, a.nstripes - 1) * a.ngroups * Q4T_BYTES;
-    const uint8_t* xp = a.xa + (size_t) mt0 * nbp * XA_BLOCK_BYTES + 16 * lane;
+    const uint8_t* xf = a.xa + xa_frag_off(a.K, mt0, 0) + 16 * lane;
+    const uint8_t* xs = a.xa + xa_scale_off(a.M, a.K, mt0, 0) + 8 * g;
+    const int nbp = a.ngroups * 4;
 
     floatx4 acc[NT][MT];
     for (int t = 0; t < NT; ++t)
@@ -157,7 +156,8 @@ __global__ __launch_bounds__(256) void k_q4_gemm(GemmArgs a) {
 
     u32x4 wq[D][NT];
     half4v ws[D][NT];
-    // group index of the wavefront's i-th group, clamped to its last one (loads past the end repeat it, unused)
+    half8 aq[2][4][MT];
+    half4v ad[2][4][MT];
     auto grp = [&](int i) { return c0 + wave + 4 * min(i, max(ng - 1, 0)); };
     auto load_w = [&](int slot, int i) {
         const size_t off = (size_t) grp(i) * Q4T_BYTES;
@@ -166,34 +166,41 @@ __global__ __launch_bounds__(256) void k_q4_gemm(GemmArgs a) {
             ws[slot][t] = *(const half4v*) (wp[t] + off + Q4T_SCALE_OFF + 8 * n_in);
         }
     };
+    auto load_a = [&](int buf, int i) {
+        const int c = grp(i);
+        for (int b = 0; b < 4; ++b)
+            for (int mt = 0; mt < MT; ++mt) {
+                const size_t blk = (size_t) mt * nbp + 4 * c + b;
+                aq[buf][b][mt] = *(const half8*) (xf + blk * XA_FRAG_BYTES);
+                ad[buf][b][mt] = *(const half4v*) (xs + blk * 32);
+            }
+    };
+    auto compute = [&](int slot, int buf) {
+        for (int t = 0; t < NT; ++t) {
+            const u32x4 w4 = wq[slot][t];
+            const half4v sc = ws[slot][t];
+            for (int b = 0; b < 4; ++b) {
+                const half8 bw = q4_unpack(w4[b]);
+                const float dw = (float) sc[b];
+                for (int mt = 0; mt < MT; ++mt) {
+                    const floatx4 isum = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[buf][b][mt], bw, zero, 0, 0, 0);
+                    const half4v dx = ad[buf][b][mt];
+                    for (int v = 0; v < 4; ++v) acc[t][mt][v] = __builtin_fmaf(isum[v], dw * (float) dx[v], acc[t][mt][v]);
+                }
+            }
+        }
+    };
     if (ng > 0) {
-        for (int j = 0; j < D; ++j) load_w(j, j);
-        for (int i0 = 0; i0 < ng; i0 += D) {
-            for (int j = 0; j < D; ++j) {
+        load_w(0, 0);
+        load_a(0, 0);
+        for (int j = 1; j < D; ++j) load_w(j, j);
+        for (int i0 = 0; i0 < ng; i0 += U) {
+            for (int j = 0; j < U; ++j) {
                 const int i = i0 + j;
                 if (i >= ng) break;
-                const int c = grp(i);
-                half8 ahi[4][MT], alo[4][MT];
-                for (int b = 0; b < 4; ++b)
-                    for (int mt = 0; mt < MT; ++mt) {
-                        const uint8_t* p = xp + ((size_t) mt * nbp + 4 * c + b) * XA_BLOCK_BYTES;
-                        ahi[b][mt] = *(const half8*) p;
-                        alo[b][mt] = *(const half8*) (p + 1024);
-                    }
-                for (int t = 0; t < NT; ++t) {
-                    const u32x4 w4 = wq[j][t];
-                    const half4v sc = ws[j][t];
-                    for (int b = 0; b < 4; ++b) {
-                        const half8 bw = q4_unpack(w4[b]);
-                        const float dw = (float) sc[b];
-                        for (int mt = 0; mt < MT; ++mt) {
-                            floatx4 r = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[b][mt], bw, zero, 0, 0, 0);
-                            r = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[b][mt], bw, r, 0, 0, 0);
-                            for (int v = 0; v < 4; ++v) acc[t][mt][v] = __builtin_fmaf(r[v], dw, acc[t][mt][v]);
-                        }
-                    }
-                }
-                load_w(j, i + D);  // refill the slot (past the end: the last group again, never used)
+                load_a((j + 1) % 2, i + 1);
+                compute(j % D, j % 2);
+                load_w(j % D, i + D);
             }
         }
     }
@@ -294,7 +301,7 @@ size_t q4_workspace_bytes(int M, int N, int K) {
 template <int MT>
 static void launch_mt(const GemmArgs& a, int mblocks, hipStream_t st) {
     dim3 grid((a.nstripes + 3) / 4, a.ks, mblocks);
-    hipLaunchKernelGGL((k_q4_gemm<MT, 4, 3>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((k_q4_gemm<MT, 4, 2>), grid, dim3(256), 0, st, a);
 }
 
 int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* part,
@@ -325,8 +332,8 @@ void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int 
 void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const float* nw, float eps, uint8_t* xa,
                float* xn, int ldn, hipStream_t st) {
     if (M <= 0) return;
-    hipLaunchKernelGGL(k_quant_act, dim3(M, (xa_nbp(K) + 63) / 64), dim3(256), 0, st, x, rows, K, ldx, nw, eps, xa, xn,
-                       ldn);
+    hipLaunchKernelGGL(k_quant_act, dim3(M, (xa_nbp(K) + 63) / 64), dim3(256), 0, st, x, rows, M, K, ldx, nw, eps, xa,
+                       xn, ldn);
 }
 
 // ---------------------------------------------------------------------------------------------------------------------

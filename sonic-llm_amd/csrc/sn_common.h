@@ -41,15 +41,23 @@ void sn_set_err(char* err, int err_len, const char* fmt, ...);
 
 // ---- activation operand ("xa"): Q8_0-quantized rows as fp16 MFMA fragments -----------------------------------------
 // Rows are quantized to Q8_0 exactly as ggml's x86 CPU backend does (per 32-block: d = amax/127 stored fp16,
-// q = round-half-even(x * 127/amax)). The dequantized value v = fp16(d) * q is exact in fp32 (11 x 7 bits) and is
-// stored as two fp16 values hi = fp16(v), lo = fp16(v - hi), which together hold v to within 2^-25 absolute.
-// Layout for row tile mt (16 rows) and block b: 2048 bytes = [hi: 64 lanes x 8 halves][lo: 64 lanes x 8 halves];
-// lane l = m + 16 g holds elements {4g..4g+3, 16+4g..16+4g+3} of row m (the same order as the weight tile lanes),
-// so one 16-byte load per lane gives the A operand of v_mfma_f32_16x16x32_f16. A row tile holds xa_nbp(K) blocks (K/32
-// rounded up to a multiple of 4; the extra blocks are zero) and the row tiles are rounded up to an even count, so the
-// matmul's loads of a 4-block group of 2 row tiles never leave the buffer.
-#define XA_BLOCK_BYTES 2048
+// q = round-half-even(x * 127/amax)). The integers q (|q| <= 127) are held as fp16, which is exact, so an fp16 MFMA of
+// them against the weights' (q4 - 8) forms the block's integer sum exactly (every partial sum < 2^24); the scale d is
+// kept beside them in fp16.
+// Fragments: for row tile mt (16 rows) and block b, 1024 bytes; lane l = m + 16 g holds the q of elements
+// {4g..4g+3, 16+4g..16+4g+3} of row m (the same order as the weight tile lanes), so one 16-byte load per lane is the A
+// operand of v_mfma_f32_16x16x32_f16. Scales: for (mt, b), the 16 rows' d as fp16 (32 bytes), after all fragments.
+// A row tile holds xa_nbp(K) blocks (K/32 rounded up to a multiple of 4; the extra blocks are zero) and row tiles are
+// rounded up to an even count, so the matmul's loads of a 4-block group of 2 row tiles never leave the buffer.
+#define XA_FRAG_BYTES 1024
 
 __host__ __device__ static inline int xa_nbp(int K) { return (K / 32 + 3) / 4 * 4; }
-static inline size_t xa_bytes(int M, int K) { return (size_t) ((M + 31) / 32 * 2) * xa_nbp(K) * XA_BLOCK_BYTES; }
+__host__ __device__ static inline int xa_mtp(int M) { return (M + 31) / 32 * 2; }
+__host__ __device__ static inline size_t xa_frag_off(int K, int mt, int b) {
+    return ((size_t) mt * xa_nbp(K) + b) * XA_FRAG_BYTES;
+}
+__host__ __device__ static inline size_t xa_scale_off(int M, int K, int mt, int b) {
+    return (size_t) xa_mtp(M) * xa_nbp(K) * XA_FRAG_BYTES + ((size_t) mt * xa_nbp(K) + b) * 32;
+}
+static inline size_t xa_bytes(int M, int K) { return (size_t) xa_mtp(M) * xa_nbp(K) * (XA_FRAG_BYTES + 32); }
 static inline size_t q4t_bytes(int N, int K) { return (size_t) ((N + 15) / 16) * ((K / 32 + 3) / 4) * Q4T_BYTES; }

@@ -38,18 +38,24 @@ def stream():
     return C.c_void_p(T.cuda.current_stream().cuda_stream)
 
 
-def xa_decode(xa: np.ndarray, M: int, K: int) -> np.ndarray:
-    """The activation operand (hi + lo fp16 fragments) back to fp32 rows [M][K], undoing the lane layout."""
+def xa_decode(xa: np.ndarray, M: int, K: int):
+    """The activation operand back to (q [M][K] as int, d [M][K/32] as float32): undoes the fragment lane layout."""
     nb = K // 32
     nbp = (nb + 3) // 4 * 4  # blocks per row tile (padded to whole 4-block groups)
+    mtp = (M + 31) // 32 * 2  # row tiles, rounded up to an even count
     mt = (M + 15) // 16
-    a = xa.view(np.float16)[:mt * nbp * 1024].reshape(mt, nbp, 2, 4, 16, 8)[:, :nb].astype(np.float32)
-    v = a[:, :, 0] + a[:, :, 1]  # [mt][b][g][m][j]
-    out = np.zeros((mt * 16, K), np.float32)
+    frag = xa.view(np.float16)[:mtp * nbp * 512].reshape(mtp, nbp, 4, 16, 8)[:mt, :nb]  # [mt][b][g][m][j]
+    q = np.zeros((mt * 16, K), np.float32)
     for g in range(4):
         for j in range(8):
             e = 4 * g + j if j < 4 else 16 + 4 * g + (j - 4)
-            # rows mt*16 + m, columns 32 b + e
-            blockvals = v[:, :, g, :, j]  # [mt][b][m]
-            out[:, e::32] = blockvals.transpose(0, 2, 1).reshape(mt * 16, nb)
-    return out[:M]
+            q[:, e::32] = frag[:, :, g, :, j].astype(np.float32).transpose(0, 2, 1).reshape(mt * 16, nb)
+    sc = xa.view(np.uint8)[mtp * nbp * 1024:mtp * nbp * 1056].view(np.float16).reshape(mtp, nbp, 16)[:mt, :nb]
+    d = sc.astype(np.float32).transpose(0, 2, 1).reshape(mt * 16, nb)
+    return q[:M], d[:M]
+
+
+def xa_values(xa: np.ndarray, M: int, K: int) -> np.ndarray:
+    """The operand's values d * q as fp32 [M][K] (exact: fp16 d times an integer |q| <= 127)."""
+    q, d = xa_decode(xa, M, K)
+    return q * np.repeat(d, 32, axis=1)

@@ -89,12 +89,13 @@ def test_activation_quantization_bit_exact():
     X[5] *= 1e-3
     Wq = O.quantize_q4_0(r.normal(0, 0.02, (16, K)).astype(np.float32))
     _, xa = gemm_gpu(Wq, 16, K, X)
-    got = U.xa_decode(xa, M, K)
-    want = O.dequantize_q8_0(O.quantize_q8_0(X), K)
-    # the same Q8_0 blocks; each value held as fp16 hi + lo, exact except below fp16's normal range (2^-25 absolute)
-    normal = [m for m in range(M) if m != 5]
-    assert np.array_equal(got[normal], want[normal])
-    assert np.all(np.abs(got - want) <= 2.0 ** -25)
+    q, d = U.xa_decode(xa, M, K)
+    blocks = O.quantize_q8_0(X).reshape(M, K // 32, 34)
+    want_d = blocks[:, :, :2].copy().view(np.float16)[..., 0].astype(np.float32)
+    want_q = blocks[:, :, 2:].view(np.int8).astype(np.float32).reshape(M, K)
+    # the same Q8_0 blocks, bit for bit: every scale and every integer
+    assert np.array_equal(d, want_d)
+    assert np.array_equal(q, want_q)
 
 
 def test_config1_q4_matmul_4096x4096_b8():

@@ -23,7 +23,7 @@ def test_rmsnorm_then_q8_0():
     x, dw = U.dev(X), U.dev(w)
     xa = U.empty(L.snk_xa_bytes(M, K))
     assert L.snk_quant_act(U.ptr(x), M, K, K, U.ptr(dw), eps, U.ptr(xa), U.stream()) == 0
-    got = U.xa_decode(U.host(xa, np.uint8), M, K)
+    got = U.xa_values(U.host(xa, np.uint8), M, K)
     xn = O.rmsnorm(X, w, eps)
     want = O.dequantize_q8_0(O.quantize_q8_0(xn), K)
     # the norm's sum of squares runs in another order, so a value may sit one rounding step to the other side of a
