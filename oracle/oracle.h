@@ -16,6 +16,15 @@
 //     (sn_attn.inc.h:216-231) and the output stage (sn_encode.inc.h:248-317).
 //   * MoE routing softmax -> top-k (ties: lower id) -> renormalise with the sum floored at 6.1035e-5 (kernels.metal:3419-3467).
 //   * Draft acceptance: rows checked in order, kept while draft == target argmax (next_engine/take.rs:339-357).
+//
+// How each function is pinned (tests/test_oracle.py, tests/test_golden.py): dequant by the closed form on every nibble
+// and fp16 specials; fp16 conversion against numpy; mul_mat against an fp64 product of the dequantized operands and
+// against the integer block sum; RMSNorm, RoPE, argmax/top-2, MoE routing and acceptance against closed forms or brute
+// force; paged attention against an fp64 dense softmax over page-gathered cells, chunked == monolithic, page-placement
+// and shared-prefix invariance; the model writer's GGUF layout against the reference's own GGUF fixture.
+// Parity unpinned against ggml itself (no ggml vector exists offline): the exact bytes of quantize_row_q4_0_ref and of
+// x86 quantize_row_q8_0 (their rounding rules are restated from ggml's published source and checked by invariants
+// only), and ggml's fp32 summation order inside mul_mat (checked to tolerance only).
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
