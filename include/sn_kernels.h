@@ -26,13 +26,14 @@ int snk_q4_dequant(const void* d_stripes, int N, int K, float* d_w, void* stream
 size_t snk_xa_bytes(int M, int K);
 int snk_quant_act(const float* d_x, int M, int K, int ldx, const float* d_norm_w, float eps, void* d_xa, void* stream);
 // the matmul; epi: store, add into d_y, or SwiGLU over interleaved gate/up stripe pairs (N = 2F, output F columns).
-// d_ws: k-slice partials of snk_q4_workspace_bytes(M, N, K) bytes (may be 0). 0, or -1 (workspace too small).
+// d_ws: k-slice partial sums of snk_q4_workspace_bytes(M, N, K) bytes (may be 0). 0, or -1 (workspace too small).
 size_t snk_q4_workspace_bytes(int M, int N, int K);
 int snk_q4_gemm(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi, void* d_ws,
                 size_t ws_bytes, void* stream);
-// average device time (microseconds) of one matmul launch over `iters` launches timed with HIP events on `stream`,
-// the weights taken from n_copies stripe copies in turn (copies beyond the 256 MB Infinity Cache keep the reads in HBM).
-// Synchronous.
+// average device time (microseconds) of one raw matmul launch (the k-slice sums into d_ws, as a decode step runs it:
+// the step's row kernels add the slices) over `iters` launches timed with HIP events on `stream`, the weights taken
+// from n_copies stripe copies in turn (copies beyond the 256 MB Infinity Cache keep the reads in HBM). d_y and ldy are
+// not used. Synchronous; -1 when d_ws is too small.
 double snk_q4_gemm_time(const void* const* d_stripes, int n_copies, const void* d_xa, int M, int N, int K, float* d_y,
                         int ldy, void* d_ws, size_t ws_bytes, int iters, void* stream);
 

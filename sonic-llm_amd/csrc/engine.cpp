@@ -535,36 +535,55 @@ extern "C" int sn_step(sn_engine* e, int R, const int32_t* tok, const int32_t* s
             return 0;
         });
     };
-    auto gemm = [&](const uint8_t* w, int M, int N, int K, float* y, int ldy, int epi) {
+    // Matmuls leave their k-slice sums in the workspace; the next row kernel adds them in slice order and applies the
+    // epilogue (RoPE for q|k|v, residual add + RMSNorm + Q8_0 for o and down, SwiGLU + Q8_0 for gate/up).
+    float* part = e->gemm_ws;
+    int ks = 0;  // k-slices of the last matmul
+    auto gemm = [&](const uint8_t* w, int M, int N, int K) {
         return e->launch(SNX_K_GEMM, gemm_bytes(M, N, K), [&] {
-            return q4_gemm(w, e->xa, M, N, K, y, ldy, epi, e->gemm_ws, e->gemm_ws_bytes, st);
+            ks = q4_gemm_raw(w, e->xa, M, N, K, part, e->gemm_ws_bytes, st);
+            return ks < 0 ? -1 : 0;
         });
     };
+    auto resid = [&](const float* nw, bool quantize) {
+        return e->launch(SNX_K_QUANT, (double) R * E * (8 + 4 * ks) + (quantize ? (double) R * E * 2 : 0.0), [&] {
+            return resid_quant(e->x, part, ks, R, E, nw, e->eps, quantize ? e->xa : nullptr, st);
+        });
+    };
+    rc |= quant(e->x, nullptr, R, E, e->ly[0].attn_norm);  // layer 0: x is the embedding
     for (int i = 0; i < e->L && rc == 0; ++i) {
         const DevLayer& l = e->ly[i];
         uint16_t* kp = e->kbase + (size_t) i * e->layer_halves;
         uint16_t* vp = e->vbase + (size_t) i * e->layer_halves;
-        rc |= quant(e->x, nullptr, R, E, l.attn_norm);
-        rc |= gemm(l.wqkv, R, e->NQKV, E, e->qkv, e->NQKV, EPI_STORE);
-        rc |= e->launch(SNX_K_ROPE, (double) R * (e->NQKV * 4 + QD * 4 + 2 * KD * 2), [&] {
-            qk_norm_rope_kv(e->qkv, e->NQKV, R, e->H, e->KVH, l.q_norm, l.k_norm, e->eps, e->theta_scale, d_seq, d_pos,
-                            e->d_pt, e->max_pages, e->page_cells, kp, vp, st);
+        if (i > 0) rc |= resid(l.attn_norm, true);  // x += the previous layer's down projection
+        rc |= gemm(l.wqkv, R, e->NQKV, E);
+        rc |= e->launch(SNX_K_ROPE, (double) R * (e->NQKV * 4.0 * (ks + 1) + QD * 4 + 2 * KD * 2), [&] {
+            qk_norm_rope_kv(e->qkv, e->NQKV, part, ks, R, e->H, e->KVH, l.q_norm, l.k_norm, e->eps, e->theta_scale,
+                            d_seq, d_pos, e->d_pt, e->max_pages, e->page_cells, kp, vp, st);
             return 0;
         });
         aa.kpool = kp;
         aa.vpool = vp;
         aa.xa = e->xa;  // the merge writes the o-projection's Q8_0 operand itself
         rc |= e->launch(SNX_K_ATTN, attn_bytes, [&] { return paged_attention(aa, st); });
-        rc |= gemm(l.wo, R, E, QD, e->x, E, EPI_ADD);
-        rc |= quant(e->x, nullptr, R, E, l.ffn_norm);
-        rc |= gemm(l.wgu, R, 2 * F, E, e->hb, F, EPI_SWIGLU);
-        rc |= quant(e->hb, nullptr, R, F, nullptr);
-        rc |= gemm(l.wd, R, E, F, e->x, E, EPI_ADD);
+        rc |= gemm(l.wo, R, E, QD);
+        rc |= resid(l.ffn_norm, true);
+        rc |= gemm(l.wgu, R, 2 * F, E);
+        rc |= e->launch(SNX_K_QUANT, (double) R * 2 * F * 4 * ks + (double) R * F * 6, [&] {
+            swiglu_quant(part, ks, R, F, e->hb, e->xa, st);
+            return 0;
+        });
+        rc |= gemm(l.wd, R, E, F);
     }
+    if (rc == 0) rc |= resid(nullptr, false);  // x += the last layer's down projection
     // ---- outputs (sn_encode.inc.h:304-317): final norm of the output rows, LM head, argmax
     if (n_out > 0 && rc == 0) {
         rc |= quant(e->x, d_out, n_out, E, e->out_norm);
-        rc |= gemm(e->head, n_out, e->V, E, e->logits, e->V, EPI_STORE);
+        rc |= e->launch(SNX_K_GEMM, gemm_bytes(n_out, e->V, E), [&] {
+            if (q4_plan(e->V, E).ks == 1)  // one slice: the sums are the logits
+                return q4_gemm_raw(e->head, e->xa, n_out, e->V, E, e->logits, (size_t) n_out * e->V * 4, st) < 0 ? -1 : 0;
+            return q4_gemm(e->head, e->xa, n_out, e->V, E, e->logits, e->V, EPI_STORE, e->gemm_ws, e->gemm_ws_bytes, st);
+        });
         const int nban = (int) e->eog.size();
         rc |= e->launch(SNX_K_OTHER, (double) n_out * e->V * 4, [&] {
             argmax_rows(e->logits, e->V, n_out, e->d_ban, nban, d_skip, e->d_otok, e->want_probs ? e->d_rec : nullptr,

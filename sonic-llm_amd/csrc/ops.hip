@@ -19,18 +19,24 @@ void embed_rows(const float* table, int E, const int32_t* tok, int R, float* x, 
 // Per head: RMSNorm over 128 dims with weight w, then y_i = x_i cos - x_{i+64} sin, y_{i+64} = x_i sin + x_{i+64} cos
 // with theta_i = p * s^i formed by i successive fp32 multiplies from p (ggml_rope_cache_init's loop), s = base^(-2/128)
 // computed on the host. q stays in place (fp32); k and v go to the row's cell in fp16.
-__global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ldqkv, int H, int KVH,
-                                                 const float* __restrict__ qw, const float* __restrict__ kw, float eps,
-                                                 float theta_scale, const int32_t* __restrict__ seq,
-                                                 const int32_t* __restrict__ pos, const int32_t* __restrict__ pt,
-                                                 int max_pages, int page_cells, uint16_t* __restrict__ kpool,
-                                                 uint16_t* __restrict__ vpool) {
+__global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ldqkv, const float* __restrict__ part,
+                                                 int ks, int R, int H, int KVH, const float* __restrict__ qw,
+                                                 const float* __restrict__ kw, float eps, float theta_scale,
+                                                 const int32_t* __restrict__ seq, const int32_t* __restrict__ pos,
+                                                 const int32_t* __restrict__ pt, int max_pages, int page_cells,
+                                                 uint16_t* __restrict__ kpool, uint16_t* __restrict__ vpool) {
     const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int p = pos[r];
     float theta = (float) p;
     for (int i = 0; i < lane; ++i) theta *= theta_scale;
     const float c = cosf(theta), s = sinf(theta);
     float* row = qkv + (size_t) r * ldqkv;
+    const int N = (H + 2 * KVH) * 128;
+    auto sum = [&](int c) {
+        float v = part[(size_t) r * N + c];
+        for (int k = 1; k < ks; ++k) v += part[((size_t) k * R + r) * N + c];
+        return v;
+    };
     const int page = pt[(size_t) seq[r] * max_pages + p / page_cells];
     const int off = p % page_cells;
     const int h = 4 * blockIdx.y + wave;
@@ -38,7 +44,18 @@ __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ld
         const bool isq = h < H;
         float* x = row + (size_t) h * 128;  // q heads then k heads, contiguous
         const float* w = isq ? qw : kw;
-        float x0 = x[lane], x1 = x[lane + 64];
+        float x0, x1;
+        if (part) {  // the q|k|v matmul's k-slice sums, added in slice order
+            x0 = sum(h * 128 + lane);
+            x1 = sum(h * 128 + lane + 64);
+            if (!isq) {  // k as the matmul made it (q is overwritten below)
+                x[lane] = x0;
+                x[lane + 64] = x1;
+            }
+        } else {
+            x0 = x[lane];
+            x1 = x[lane + 64];
+        }
         float ss = x0 * x0 + x1 * x1;
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
         const float sc = 1.0f / sqrtf(ss / 128.f + eps);
@@ -55,19 +72,27 @@ __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ld
         }
     }
     if (blockIdx.y != 0) return;
-    const float* v = row + (size_t) (H + KVH) * 128;
+    float* v = row + (size_t) (H + KVH) * 128;
     for (int i = threadIdx.x; i < KVH * 128; i += 256) {
         const int hh = i / 128, d = i % 128;
-        vpool[(((size_t) page * KVH + hh) * page_cells + off) * 128 + d] = __builtin_bit_cast(uint16_t, (_Float16) v[i]);
+        float vi;
+        if (part) {
+            vi = sum((H + KVH) * 128 + i);
+            v[i] = vi;
+        } else {
+            vi = v[i];
+        }
+        vpool[(((size_t) page * KVH + hh) * page_cells + off) * 128 + d] = __builtin_bit_cast(uint16_t, (_Float16) vi);
     }
 }
 
-void qk_norm_rope_kv(float* qkv, int ldqkv, int R, int H, int KVH, const float* qw, const float* kw, float eps,
-                     float theta_scale, const int32_t* seq, const int32_t* pos, const int32_t* pt, int max_pages,
-                     int page_cells, uint16_t* kpool, uint16_t* vpool, hipStream_t st) {
+void qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, int H, int KVH, const float* qw,
+                     const float* kw, float eps, float theta_scale, const int32_t* seq, const int32_t* pos,
+                     const int32_t* pt, int max_pages, int page_cells, uint16_t* kpool, uint16_t* vpool,
+                     hipStream_t st) {
     if (R > 0)
-        hipLaunchKernelGGL(k_qk_rope, dim3(R, (H + KVH + 3) / 4), dim3(256), 0, st, qkv, ldqkv, H, KVH, qw, kw, eps,
-                           theta_scale, seq, pos, pt, max_pages, page_cells, kpool, vpool);
+        hipLaunchKernelGGL(k_qk_rope, dim3(R, (H + KVH + 3) / 4), dim3(256), 0, st, qkv, ldqkv, part, ks, R, H, KVH, qw,
+                           kw, eps, theta_scale, seq, pos, pt, max_pages, page_cells, kpool, vpool);
 }
 
 // ---- greedy argmax (argmax / argmax_p, kernels.metal:327-442) -------------------------------------------------------

@@ -10,6 +10,8 @@
 // isum * (dw * dx) (the product of two fp16 values is exact in fp32) to the fp32 accumulator. The order of the sums
 // of an output is fixed by (N, K) alone, never by the number of rows, so a row's result is the same in any step
 // (sn.h:1-3).
+#include <algorithm>
+
 #include "sn_kernels_internal.h"
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -43,6 +45,8 @@ __global__ void k_q4_repack(const uint8_t* __restrict__ src, int N, int K, uint8
 // ---------------------------------------------------------------------------------------------------------------------
 // activation quantizer: fp32 rows (optionally RMS-normed by weight nw first) -> xa operand (sn_common.h).
 // One workgroup of 256 threads per row. The norm is ggml's: y = (x * scale) * w, scale = 1/sqrt(mean(x^2) + eps).
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
 __device__ __forceinline__ float block_reduce_sum256(float v, float* red) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
     const int w = threadIdx.x >> 6;
@@ -51,6 +55,8 @@ __device__ __forceinline__ float block_reduce_sum256(float v, float* red) {
     __syncthreads();
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
+
+__device__ __forceinline__ void q8_store(const float* v, int g, uint8_t* frag, _Float16* dsl);
 
 // Four lanes per 32-block: lane part g holds the block's elements {4g..4g+3, 16+4g..16+4g+3}, which is exactly its
 // 8-value fragment of the MFMA operand, so each lane writes one 16-byte hi and one 16-byte lo fragment. The block's
@@ -91,7 +97,13 @@ __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, 
         *(float4*) (o + 4 * g) = (float4){v[0], v[1], v[2], v[3]};
         *(float4*) (o + 16 + 4 * g) = (float4){v[4], v[5], v[6], v[7]};
     }
-    // ggml x86 quantize_row_q8_0: d = amax / 127 (stored fp16), q = round-half-even(x * 127 / amax)
+    q8_store(v, g, frag, dsl);
+}
+
+// Row m, block b of a Q8_0 operand from its 32 fp32 values (this lane's 8: elements 4g..4g+3, 16+4g..16+4g+3):
+// ggml x86 quantize_row_q8_0, d = amax / 127 (stored fp16), q = round-half-even(x * 127 / amax). The 4 lanes of a
+// block are adjacent (the shuffles stay within them).
+__device__ __forceinline__ void q8_store(const float* v, int g, uint8_t* frag, _Float16* dsl) {
     float amax = 0.0f;
     for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
     amax = fmaxf(amax, __shfl_xor(amax, 1));
@@ -102,6 +114,101 @@ __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, 
     for (int j = 0; j < 8; ++j) q[j] = (_Float16) __builtin_rintf(v[j] * id);
     *(half8*) frag = q;
     if (g == 0) *dsl = (_Float16) d;
+}
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *(const float4*) p; }
+__device__ __forceinline__ float4 add4(float4 a, float4 b) { return (float4){a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w}; }
+
+// Residual rows: x[m] += the k-slice sums of a matmul (part[ks][M][K], slices added in order), written back; then,
+// when xa is given, the RMSNorm (weight nw) and Q8_0 operand of the new row. One workgroup per row (the norm needs the
+// whole row before any value is quantized); lane t covers blocks t / 4 + 64 i.
+template <int IT>
+__global__ __launch_bounds__(256) void k_resid_quant(float* __restrict__ X, const float* __restrict__ part, int ks,
+                                                     int M, int K, const float* __restrict__ nw, float eps,
+                                                     uint8_t* __restrict__ xa) {
+    __shared__ float red[4];
+    const int m = blockIdx.x, t = threadIdx.x, g = t & 3;
+    const int nb = K / 32, nbp = xa_nbp(K);
+    float* x = X + (size_t) m * K;
+    float v[IT][8];
+    float ss = 0.0f;
+    for (int it = 0; it < IT; ++it) {
+        const int b = t / 4 + 64 * it;
+        if (b >= nb) continue;
+        const int e0 = 32 * b + 4 * g, e1 = e0 + 16;
+        float4 lo = ld4(x + e0), hi = ld4(x + e1);
+        float4 slo = ld4(part + (size_t) m * K + e0), shi = ld4(part + (size_t) m * K + e1);
+        for (int k = 1; k < ks; ++k) {
+            slo = add4(slo, ld4(part + ((size_t) k * M + m) * K + e0));
+            shi = add4(shi, ld4(part + ((size_t) k * M + m) * K + e1));
+        }
+        lo = add4(lo, slo);
+        hi = add4(hi, shi);
+        *(float4*) (x + e0) = lo;
+        *(float4*) (x + e1) = hi;
+        const float w8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        for (int j = 0; j < 8; ++j) {
+            v[it][j] = w8[j];
+            ss += w8[j] * w8[j];
+        }
+    }
+    if (!xa) return;
+    const float scale = nw ? 1.0f / sqrtf(block_reduce_sum256(ss, red) / (float) K + eps) : 1.0f;
+    for (int it = 0; it < IT; ++it) {
+        const int b = t / 4 + 64 * it;
+        if (b >= nbp) continue;
+        uint8_t* frag = xa + xa_frag_off(K, m >> 4, b) + 16 * ((m & 15) + 16 * g);
+        _Float16* dsl = (_Float16*) (xa + xa_scale_off(M, K, m >> 4, b)) + (m & 15);
+        if (b >= nb) {  // a padding block of the last 4-block group: zero
+            *(half8*) frag = (half8){};
+            if (g == 0) *dsl = (_Float16) 0.0f;
+            continue;
+        }
+        float y[8];
+        if (nw) {
+            const float4 wl = ld4(nw + 32 * b + 4 * g), wh = ld4(nw + 32 * b + 16 + 4 * g);
+            const float w8[8] = {wl.x, wl.y, wl.z, wl.w, wh.x, wh.y, wh.z, wh.w};
+            for (int j = 0; j < 8; ++j) y[j] = (v[it][j] * scale) * w8[j];
+        } else {
+            for (int j = 0; j < 8; ++j) y[j] = v[it][j];
+        }
+        q8_store(y, g, frag, dsl);
+    }
+}
+
+// SwiGLU of a stripe-interleaved gate/up matmul's k-slice sums (part[ks][M][2F]: output column 16p + n is
+// silu(column 32p + n) * column 32p + 16 + n), written as fp32 rows h (when given) and as the Q8_0 operand of the next
+// matmul. Workgroup (row m, 64 blocks), 4 lanes per block as in k_quant_act.
+__global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ part, int ks, int M, int F,
+                                                      float* __restrict__ h, uint8_t* __restrict__ xa) {
+    const int m = blockIdx.x, t = threadIdx.x;
+    const int nb = F / 32, nbp = xa_nbp(F);
+    const int b = blockIdx.y * 64 + (t >> 2), g = t & 3;
+    if (b >= nbp) return;
+    uint8_t* frag = xa + xa_frag_off(F, m >> 4, b) + 16 * ((m & 15) + 16 * g);
+    _Float16* dsl = (_Float16*) (xa + xa_scale_off(M, F, m >> 4, b)) + (m & 15);
+    if (b >= nb) {
+        *(half8*) frag = (half8){};
+        if (g == 0) *dsl = (_Float16) 0.0f;
+        return;
+    }
+    // elements 32b + 4g + j (pair 2b) and 32b + 16 + 4g + j (pair 2b + 1): gate at 64b + 4g (+32), up 16 further
+    const size_t N = 2 * (size_t) F;
+    auto sum4 = [&](int c) {
+        float4 s4 = ld4(part + (size_t) m * N + c);
+        for (int k = 1; k < ks; ++k) s4 = add4(s4, ld4(part + ((size_t) k * M + m) * N + c));
+        return s4;
+    };
+    const float4 g0 = sum4(64 * b + 4 * g), u0 = sum4(64 * b + 16 + 4 * g);
+    const float4 g1 = sum4(64 * b + 32 + 4 * g), u1 = sum4(64 * b + 48 + 4 * g);
+    float v[8] = {silu(g0.x) * u0.x, silu(g0.y) * u0.y, silu(g0.z) * u0.z, silu(g0.w) * u0.w,
+                  silu(g1.x) * u1.x, silu(g1.y) * u1.y, silu(g1.z) * u1.z, silu(g1.w) * u1.w};
+    if (h) {
+        float* o = h + (size_t) m * F + 32 * b;
+        *(float4*) (o + 4 * g) = (float4){v[0], v[1], v[2], v[3]};
+        *(float4*) (o + 16 + 4 * g) = (float4){v[4], v[5], v[6], v[7]};
+    }
+    q8_store(v, g, frag, dsl);
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -125,134 +232,103 @@ __device__ __forceinline__ half8 q4_unpack(uint32_t w) {
     return r;
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
-
-// One workgroup (4 wavefronts) owns NT consecutive 16-row stripes (16 NT output columns) of a k-slice; the 4
-// wavefronts split the slice's 4-block groups between them (wavefront w takes groups w, w + 4, ...) and their fp32
-// sums are added in LDS in wavefront order. A wavefront streams its groups with a ring of D groups of weight tiles;
-// the activation fragments and scales of a group are loaded one group ahead, before the weight refill of the group
-// being computed, so that waiting for them (vmcnt counts in issue order) leaves the newer weight loads in flight.
-// Every load is unconditional: stripes past the matrix are clamped to its last stripe (their sums are never stored),
-// groups past a wavefront's last repeat it, and the xa operand is padded (sn_common.h), so no load waits on a branch.
-template <int MT, int NT, int D>
+// One workgroup (4 wavefronts) owns a set of 4 consecutive 16-row stripes (wavefront w: stripe 4 set + w) and a
+// k-slice of consecutive 4-block groups; the four wavefronts walk the slice's groups together, so a group's activation
+// operand (MT row tiles x 4 blocks: 1 KB fragments and fp16 scales) is loaded from global memory once per workgroup:
+// each wavefront loads MT fragments of it (wavefront 0 also the scales) into a register ring D groups ahead and stages
+// them into an LDS double buffer one group ahead (scales as fp32). The weight tiles go straight from global memory into
+// a ring of D groups of registers, so each wavefront keeps D tiles of its stripe in flight. Loads are issued in group
+// order (activations before weights), the order they are used in: vmcnt counts in issue order, so waiting for the
+// oldest group leaves the newer ones in flight. Every load is unconditional: stripes past the matrix are clamped to its
+// last stripe (their sums are never stored) and groups past the slice repeat its last group (cache hits), so no load
+// sits behind a branch.
+//
+// The kernel writes each slice's raw fp32 sums, part[slice][M][N]; whoever consumes them adds the slices in slice
+// order (k_q4_reduce here; the row kernels of the step), so the order of every sum is fixed by (N, K) alone.
+template <int MT, int D>
 __global__ __launch_bounds__(256) void k_q4_gemm(GemmArgs a) {
-    constexpr int U = D % 2 ? 2 * D : D;  // unroll: a multiple of both ring sizes
-    __shared__ floatx4 red[4][NT][MT][64];
+    static_assert(D >= 2, "ring of at least two groups");
+    constexpr int U = D % 2 ? 2 * D : D;  // unroll: a multiple of the ring and of the LDS double buffer
+    __shared__ __attribute__((aligned(16))) uint8_t s_act[2][MT * 4][1024];
+    __shared__ __attribute__((aligned(16))) float s_sc[2][MT * 64];  // tile mt: [block][row] as fp32
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n_in = lane & 15, g = lane >> 4;
-    const int s0 = blockIdx.x * NT, slice = blockIdx.y, mt0 = blockIdx.z * MT;
-    const int c0 = slice * a.gps, c1 = min(c0 + a.gps, a.ngroups);
-    const int ng = c1 - c0 > wave ? (c1 - c0 - wave + 3) / 4 : 0;  // this wavefront's groups: c0 + wave + 4 i
-    const uint8_t* wp[NT];
-    for (int t = 0; t < NT; ++t) wp[t] = a.w + (size_t) min(s0 + t, a.nstripes - 1) * a.ngroups * Q4T_BYTES;
-    const uint8_t* xf = a.xa + xa_frag_off(a.K, mt0, 0) + 16 * lane;
-    const uint8_t* xs = a.xa + xa_scale_off(a.M, a.K, mt0, 0) + 8 * g;
-    const int nbp = a.ngroups * 4;
+    const int set = blockIdx.x, slice = blockIdx.y, mt0 = blockIdx.z * MT;
+    const int stripe = set * 4 + wave;
+    const int c0 = slice * a.gps, ng = min(a.gps, a.ngroups - c0);  // groups c0 .. c0 + ng - 1 (ng >= 1)
 
-    floatx4 acc[NT][MT];
-    for (int t = 0; t < NT; ++t)
-        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    const uint8_t* wp = a.w + (size_t) min(stripe, a.nstripes - 1) * a.ngroups * Q4T_BYTES;
+    // activation fragment f = wave * MT + j of a group: row tile mt0 + f / 4, block f % 4
+    const uint8_t* af[MT];
+    for (int j = 0; j < MT; ++j) {
+        const int f = wave * MT + j;
+        af[j] = a.xa + xa_frag_off(a.K, mt0 + f / 4, f % 4) + 16 * lane;
+    }
+    // scales: lane l < 32 MT loads dword l % 32 of row tile mt0 + l / 32 (its 4 blocks' 128 B are contiguous)
+    const int sl = lane < 32 * MT ? lane : 0;
+    const uint8_t* asp = a.xa + xa_scale_off(a.M, a.K, mt0 + sl / 32, 0) + 4 * (sl % 32);
+
+    u32x4 wq[D];
+    half4v ws[D];
+    u32x4 ra[D][MT];
+    uint32_t rs[D];
+    floatx4 acc[MT];
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = (floatx4){0.f, 0.f, 0.f, 0.f};
     const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
 
-    u32x4 wq[D][NT];
-    half4v ws[D][NT];
-    half8 aq[2][4][MT];
-    half4v ad[2][4][MT];
-    auto grp = [&](int i) { return c0 + wave + 4 * min(i, max(ng - 1, 0)); };
-    auto load_w = [&](int slot, int i) {
-        const size_t off = (size_t) grp(i) * Q4T_BYTES;
-        for (int t = 0; t < NT; ++t) {
-            wq[slot][t] = *(const u32x4*) (wp[t] + off + 16 * lane);
-            ws[slot][t] = *(const half4v*) (wp[t] + off + Q4T_SCALE_OFF + 8 * n_in);
-        }
+    auto load = [&](int slot, int i) {
+        const int c = c0 + min(i, ng - 1);
+        for (int j = 0; j < MT; ++j) ra[slot][j] = *(const u32x4*) (af[j] + (size_t) c * 4 * XA_FRAG_BYTES);
+        rs[slot] = *(const uint32_t*) (asp + (size_t) c * 128);
+        const size_t off = (size_t) c * Q4T_BYTES;
+        wq[slot] = *(const u32x4*) (wp + off + 16 * lane);
+        ws[slot] = *(const half4v*) (wp + off + Q4T_SCALE_OFF + 8 * n_in);
     };
-    auto load_a = [&](int buf, int i) {
-        const int c = grp(i);
-        for (int b = 0; b < 4; ++b)
-            for (int mt = 0; mt < MT; ++mt) {
-                const size_t blk = (size_t) mt * nbp + 4 * c + b;
-                aq[buf][b][mt] = *(const half8*) (xf + blk * XA_FRAG_BYTES);
-                ad[buf][b][mt] = *(const half4v*) (xs + blk * 32);
-            }
+    auto stage = [&](int buf, int slot) {
+        for (int j = 0; j < MT; ++j) *(u32x4*) (&s_act[buf][wave * MT + j][16 * lane]) = ra[slot][j];
+        if (wave == 0 && lane < 32 * MT) {
+            // dword l % 32 of tile l / 32 holds fp16 [block][row] entries 2 (l % 32) and 2 (l % 32) + 1
+            const half2v h = __builtin_bit_cast(half2v, rs[slot]);
+            *(float2*) &s_sc[buf][(lane / 32) * 64 + 2 * (lane % 32)] = (float2){(float) h[0], (float) h[1]};
+        }
     };
     auto compute = [&](int slot, int buf) {
-        for (int t = 0; t < NT; ++t) {
-            const u32x4 w4 = wq[slot][t];
-            const half4v sc = ws[slot][t];
-            for (int b = 0; b < 4; ++b) {
-                const half8 bw = q4_unpack(w4[b]);
-                const float dw = (float) sc[b];
-                for (int mt = 0; mt < MT; ++mt) {
-                    const floatx4 isum = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[buf][b][mt], bw, zero, 0, 0, 0);
-                    const half4v dx = ad[buf][b][mt];
-                    for (int v = 0; v < 4; ++v) acc[t][mt][v] = __builtin_fmaf(isum[v], dw * (float) dx[v], acc[t][mt][v]);
-                }
+        for (int b = 0; b < 4; ++b) {
+            const half8 bw = q4_unpack(wq[slot][b]);
+            const float dw = (float) ws[slot][b];
+            for (int mt = 0; mt < MT; ++mt) {
+                const half8 A = *(const half8*) (&s_act[buf][mt * 4 + b][16 * lane]);
+                const floatx4 dx = *(const floatx4*) &s_sc[buf][mt * 64 + b * 16 + 4 * g];
+                const floatx4 isum = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bw, zero, 0, 0, 0);
+                for (int v = 0; v < 4; ++v) acc[mt][v] = __builtin_fmaf(isum[v], dw * dx[v], acc[mt][v]);
             }
         }
     };
-    if (ng > 0) {
-        load_w(0, 0);
-        load_a(0, 0);
-        for (int j = 1; j < D; ++j) load_w(j, j);
-        for (int i0 = 0; i0 < ng; i0 += U) {
-            for (int j = 0; j < U; ++j) {
-                const int i = i0 + j;
-                if (i >= ng) break;
-                load_a((j + 1) % 2, i + 1);
-                compute(j % D, j % 2);
-                load_w(j % D, i + D);
-            }
+
+    for (int j = 0; j < D; ++j) load(j, j);
+    stage(0, 0);
+    for (int i0 = 0; i0 < ng; i0 += U) {
+        for (int j = 0; j < U; ++j) {
+            const int i = i0 + j;
+            if (i >= ng) break;
+            __syncthreads();  // group i is staged; everyone is done reading the buffer group i + 1 goes to
+            stage((j + 1) % 2, (j + 1) % D);
+            compute(j % D, j % 2);
+            load(j % D, i + D);
         }
     }
 
-    // the 4 wavefronts' sums, added in wavefront order; wavefront w then finishes stripe(s) of its own
-    for (int t = 0; t < NT; ++t)
-        for (int mt = 0; mt < MT; ++mt) red[wave][t][mt][lane] = acc[t][mt];
-    __syncthreads();
-    for (int t = wave; t < NT; t += 4)
-        for (int mt = 0; mt < MT; ++mt) {
-            floatx4 v4 = red[0][t][mt][lane];
-            for (int w = 1; w < 4; ++w) {
-                const floatx4 o = red[w][t][mt][lane];
-                for (int v = 0; v < 4; ++v) v4[v] += o[v];
-            }
-            red[0][t][mt][lane] = v4;
+    // lane (n, g) holds rows 4g + v of each row tile, column n of the stripe
+    const int col = stripe * 16 + n_in;
+    if (stripe >= a.nstripes || col >= a.N) return;
+    for (int mt = 0; mt < MT; ++mt)
+        for (int v = 0; v < 4; ++v) {
+            const int row = (mt0 + mt) * 16 + 4 * g + v;
+            if (row < a.M) a.part[((size_t) slice * a.M + row) * a.N + col] = acc[mt][v];
         }
-    __syncthreads();
-
-    // lane (n, g) holds rows 4g+v of each row tile, column n of each stripe
-    if (a.ks > 1 || a.epi != EPI_SWIGLU) {
-        for (int t = wave; t < NT; t += 4) {
-            const int s = s0 + t;
-            const int col = s * 16 + n_in;
-            if (s >= a.nstripes || col >= a.N) continue;
-            for (int mt = 0; mt < MT; ++mt)
-                for (int v = 0; v < 4; ++v) {
-                    const int row = (mt0 + mt) * 16 + 4 * g + v;
-                    if (row >= a.M) continue;
-                    const float val = red[0][t][mt][lane][v];
-                    if (a.ks > 1) a.part[((size_t) slice * a.M + row) * a.N + col] = val;
-                    else if (a.epi == EPI_STORE) a.y[(size_t) row * a.ldy + col] = val;
-                    else a.y[(size_t) row * a.ldy + col] += val;
-                }
-        }
-    } else {
-        // stripes 2p (gate) and 2p + 1 (up) of a pair are both in this workgroup (NT even, s0 even)
-        for (int t = 2 * wave; t + 1 < NT; t += 8) {
-            const int s = s0 + t;
-            if (s + 1 >= a.nstripes) continue;
-            const int col = (s / 2) * 16 + n_in;
-            for (int mt = 0; mt < MT; ++mt)
-                for (int v = 0; v < 4; ++v) {
-                    const int row = (mt0 + mt) * 16 + 4 * g + v;
-                    if (row >= a.M || col >= a.N / 2) continue;
-                    a.y[(size_t) row * a.ldy + col] = silu(red[0][t][mt][lane][v]) * red[0][t + 1][mt][lane][v];
-                }
-        }
-    }
 }
 
-// k-slice partials added in slice order, then the epilogue
+// k-slice partial sums added in slice order, then the epilogue
 __global__ void k_q4_reduce(GemmArgs a) {
     const int outN = a.epi == EPI_SWIGLU ? a.N / 2 : a.N;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -264,7 +340,7 @@ __global__ void k_q4_reduce(GemmArgs a) {
         return s;
     };
     if (a.epi == EPI_SWIGLU) {
-        // output column col = 16 p + n is gate column 32 p + n and up column 32 p + 16 + n
+        // output column 16 p + n: gate column 32 p + n, up column 32 p + 16 + n of the interleaved matrix
         const int p = col / 16, n = col % 16;
         a.y[(size_t) row * a.ldy + col] = silu(sum(32 * p + n)) * sum(32 * p + 16 + n);
     } else if (a.epi == EPI_ADD) {
@@ -277,56 +353,70 @@ __global__ void k_q4_reduce(GemmArgs a) {
 // ---------------------------------------------------------------------------------------------------------------------
 // host side
 
-// The launch shape of a matrix depends on (N, K) only, never on the rows (row invariance): NT = 4 stripes per
-// workgroup, and k-slices across workgroups only while there are fewer than 1024 wavefronts and each slice keeps at
-// least 16 groups (2048 values), so the slices' partial sums stay a small fraction of the weight bytes.
+// The launch shape depends on (N, K) only, never on the rows (row invariance): 4 stripes per workgroup, and k-slices
+// across workgroups while there are fewer than 256 workgroups (an MI355X round is 1024 of them: fewer, longer
+// workgroups keep the slices' partial sums small).
 GemmPlan q4_plan(int N, int K) {
     GemmPlan p;
     p.nstripes = (N + 15) / 16;
     p.ngroups = (K / 32 + 3) / 4;
-    p.nt = 4;
-    const int wgs = (p.nstripes + p.nt - 1) / p.nt;
+    p.sets = (p.nstripes + 3) / 4;
     int ks = 1;
-    while (wgs * ks * 4 < 1024 && p.ngroups / (ks + 1) >= 16) ++ks;
+    while (p.sets * ks < 256 && ks < p.ngroups) ++ks;
     p.gps = (p.ngroups + ks - 1) / ks;
     p.ks = (p.ngroups + p.gps - 1) / p.gps;
     return p;
 }
 
-size_t q4_workspace_bytes(int M, int N, int K) {
-    const GemmPlan p = q4_plan(N, K);
-    return p.ks > 1 ? (size_t) p.ks * M * N * sizeof(float) : 0;
-}
+size_t q4_workspace_bytes(int M, int N, int K) { return (size_t) q4_plan(N, K).ks * M * N * sizeof(float); }
 
-template <int MT>
-static void launch_mt(const GemmArgs& a, int mblocks, hipStream_t st) {
-    dim3 grid((a.nstripes + 3) / 4, a.ks, mblocks);
-    hipLaunchKernelGGL((k_q4_gemm<MT, 4, 2>), grid, dim3(256), 0, st, a);
-}
-
-int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* part,
-            size_t part_bytes, hipStream_t st) {
+int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
+                hipStream_t st) {
     if (M <= 0) return 0;
     const GemmPlan p = q4_plan(N, K);
+    if (part == nullptr || part_bytes < (size_t) p.ks * M * N * sizeof(float)) return -1;
     GemmArgs a;
-    a.w = w; a.xa = xa; a.y = y; a.part = part;
-    a.M = M; a.N = N; a.K = K; a.ldy = ldy; a.epi = epi;
+    a.w = w; a.xa = xa; a.part = part; a.y = nullptr;
+    a.M = M; a.N = N; a.K = K; a.ldy = 0; a.epi = EPI_STORE;
     a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
     a.mtiles = (M + 15) / 16;
-    if (p.ks > 1 && (part == nullptr || part_bytes < (size_t) p.ks * M * N * sizeof(float))) return -1;
-    if (a.mtiles == 1) launch_mt<1>(a, 1, st);
-    else launch_mt<2>(a, (a.mtiles + 1) / 2, st);
-    if (p.ks > 1) {
-        const int outN = epi == EPI_SWIGLU ? N / 2 : N;
-        const int tot = M * outN;
-        hipLaunchKernelGGL(k_q4_reduce, dim3((tot + 255) / 256), dim3(256), 0, st, a);
-    }
+    if (a.mtiles == 1) hipLaunchKernelGGL((k_q4_gemm<1, 4>), dim3(p.sets, p.ks, 1), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_q4_gemm<2, 4>), dim3(p.sets, p.ks, (a.mtiles + 1) / 2), dim3(256), 0, st, a);
+    return p.ks;
+}
+
+int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* ws,
+            size_t ws_bytes, hipStream_t st) {
+    if (M <= 0) return 0;
+    const int ks = q4_gemm_raw(w, xa, M, N, K, ws, ws_bytes, st);
+    if (ks < 0) return -1;
+    GemmArgs a;
+    a.part = ws; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.ldy = ldy; a.epi = epi; a.ks = ks;
+    const int tot = M * (epi == EPI_SWIGLU ? N / 2 : N);
+    hipLaunchKernelGGL(k_q4_reduce, dim3((tot + 255) / 256), dim3(256), 0, st, a);
     return 0;
 }
 
 void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int soff, hipStream_t st) {
     const int tiles = ((N + 15) / 16) * ((K / 32 + 3) / 4);
     hipLaunchKernelGGL(k_q4_repack, dim3(tiles), dim3(64), 0, st, src, N, K, dst, sstride, soff);
+}
+
+int resid_quant(float* x, const float* part, int ks, int M, int K, const float* nw, float eps, uint8_t* xa,
+                hipStream_t st) {
+    if (M <= 0) return 0;
+    const int it = (xa_nbp(K) + 63) / 64;
+    if (K % 32 || it > 4) return -1;
+    if (it == 1) hipLaunchKernelGGL((k_resid_quant<1>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa);
+    else if (it == 2) hipLaunchKernelGGL((k_resid_quant<2>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa);
+    else hipLaunchKernelGGL((k_resid_quant<4>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa);
+    return 0;
+}
+
+void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st) {
+    if (M > 0)
+        hipLaunchKernelGGL(k_swiglu_quant, dim3(M, (xa_nbp(F) + 63) / 64), dim3(256), 0, st, part, ks, M, F, h, xa);
 }
 
 void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const float* nw, float eps, uint8_t* xa,

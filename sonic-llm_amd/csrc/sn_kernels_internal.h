@@ -8,25 +8,41 @@ struct GemmArgs {
     const uint8_t* w;
     const uint8_t* xa;
     float* y;
-    float* part;
+    float* part;  // k-slice partial sums [ks][M][N]
     int M, N, K, ldy, epi;
     int nstripes, ngroups, ks, gps, mtiles;
 };
 
+// Launch shape of one matrix: a workgroup owns 4 stripes (a "set") and gps consecutive 4-block groups (a slice).
 struct GemmPlan {
-    int nstripes, ngroups, nt, ks, gps;
+    int nstripes, ngroups, sets, ks, gps;
 };
 
+// Depends on (N, K) only, never on the rows.
 GemmPlan q4_plan(int N, int K);
+// The k-slice sums of a matmul of M rows: ks * M * N floats.
 size_t q4_workspace_bytes(int M, int N, int K);
+// Raw matmul: part[slice][M][N] = the slice's sums (the consumer adds the slices in order). Returns the slice count,
+// or -1 when part_bytes is too small.
+int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
+                hipStream_t st);
 // GGUF Q4_0 rows -> stripes; source stripe s lands at destination stripe s * sstride + soff.
 void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int soff, hipStream_t st);
 // rows (optional): row m of the operand is row rows[m] of x. nw (optional): RMSNorm weight applied first.
 // xn (optional): the normed fp32 rows, ldn apart.
 void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const float* nw, float eps, uint8_t* xa,
                float* xn, int ldn, hipStream_t st);
-int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* part,
-            size_t part_bytes, hipStream_t st);
+// Raw matmul into the workspace, then the slices added in order with an epilogue into y (ldy apart): store, add, or
+// SwiGLU of the stripe-interleaved gate/up pair (output column 16p + n = silu(column 32p + n) * column 32p + 16 + n).
+// x[m] += the k-slice sums part[ks][M][K] (added in slice order); then, with xa, the Q8_0 operand of the new rows
+// (RMS-normed by nw when given). K <= 8192. 0, or -1 (shape).
+int resid_quant(float* x, const float* part, int ks, int M, int K, const float* nw, float eps, uint8_t* xa,
+                hipStream_t st);
+// h (optional) and the Q8_0 operand of silu(gate) * up from a stripe-interleaved gate/up matmul's k-slice sums
+// part[ks][M][2F].
+void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st);
+int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* ws,
+            size_t ws_bytes, hipStream_t st);
 
 // ---- paged attention ----
 // One work item = (query group, KV head, chunk of ATT_CHUNK cells). A query group is up to 16/G rows of one
@@ -67,9 +83,12 @@ int paged_attention(const AttnArgs& a, hipStream_t st);
 
 // ---- elementwise / row kernels ----
 void embed_rows(const float* table, int E, const int32_t* tok, int R, float* x, hipStream_t st);
-void qk_norm_rope_kv(float* qkv, int ldqkv, int R, int H, int KVH, const float* qw, const float* kw, float eps,
-                     float theta_scale, const int32_t* seq, const int32_t* pos, const int32_t* pt, int max_pages,
-                     int page_cells, uint16_t* kpool, uint16_t* vpool, hipStream_t st);
+// q|k|v rows: from qkv (part NULL) or from the q|k|v matmul's k-slice sums part[ks][R][(H + 2 KVH) 128], which are
+// then also written to qkv (k and v as summed, q after QK-norm and RoPE); k and v go to the rows' cache cells.
+void qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, int H, int KVH, const float* qw,
+                     const float* kw, float eps, float theta_scale, const int32_t* seq, const int32_t* pos,
+                     const int32_t* pt, int max_pages, int page_cells, uint16_t* kpool, uint16_t* vpool,
+                     hipStream_t st);
 // cells [a, b) of page `dst` in every layer: copied from page `src` (src >= 0) or zeroed (src < 0)
 void kv_page_op(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L, int KVH, int page_cells, int src, int dst,
                 int a, int b, hipStream_t st);

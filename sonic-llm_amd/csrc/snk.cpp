@@ -41,14 +41,16 @@ extern "C" double snk_q4_gemm_time(const void* const* d_stripes, int n_copies, c
     hipStream_t st = (hipStream_t) stream;
     hipEvent_t a, b;
     if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return -1.0;
-    // one untimed launch per copy
+    // the raw matmul (the k-slice sums), as a step runs it; one untimed launch per copy
+    (void) d_y;
+    (void) ldy;
     for (int c = 0; c < n_copies; ++c)
-        q4_gemm((const uint8_t*) d_stripes[c], (const uint8_t*) d_xa, M, N, K, d_y, ldy, EPI_STORE, (float*) d_ws,
-                ws_bytes, st);
+        if (q4_gemm_raw((const uint8_t*) d_stripes[c], (const uint8_t*) d_xa, M, N, K, (float*) d_ws, ws_bytes, st) < 0)
+            return -1.0;
     hipEventRecord(a, st);
     for (int i = 0; i < iters; ++i)
-        q4_gemm((const uint8_t*) d_stripes[i % n_copies], (const uint8_t*) d_xa, M, N, K, d_y, ldy, EPI_STORE,
-                (float*) d_ws, ws_bytes, st);
+        q4_gemm_raw((const uint8_t*) d_stripes[i % n_copies], (const uint8_t*) d_xa, M, N, K, (float*) d_ws, ws_bytes,
+                    st);
     hipEventRecord(b, st);
     hipEventSynchronize(b);
     float ms = 0.0f;
@@ -177,7 +179,7 @@ extern "C" int snk_qk_rope(float* d_qkv, int ldqkv, int R, int H, int KVH, const
                            float eps, float theta_scale, const int32_t* d_seq, const int32_t* d_pos, const int32_t* d_pt,
                            int max_pages, int page_cells, void* d_kpool, void* d_vpool, void* stream) {
     if (R <= 0 || H <= 0 || KVH <= 0 || ldqkv < (H + 2 * KVH) * 128 || (page_cells != 32 && page_cells != 64)) return -1;
-    qk_norm_rope_kv(d_qkv, ldqkv, R, H, KVH, d_qw, d_kw, eps, theta_scale, d_seq, d_pos, d_pt, max_pages, page_cells,
+    qk_norm_rope_kv(d_qkv, ldqkv, nullptr, 1, R, H, KVH, d_qw, d_kw, eps, theta_scale, d_seq, d_pos, d_pt, max_pages, page_cells,
                     (uint16_t*) d_kpool, (uint16_t*) d_vpool, (hipStream_t) stream);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
