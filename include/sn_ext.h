@@ -39,6 +39,20 @@ int snx_fill_kv(sn_engine* e, int slot, int n, uint64_t seed, char* err, int err
 // [R][F]. n floats into dst. 0, or -1.
 int snx_debug_read(sn_engine* e, int which, float* dst, size_t n);
 
+// The fused draft-verify step of a guess-head model (guessing on): for each of n sequences (slot seq[s], its pending
+// token last[s] at position pos[s], its cells before pos[s] in the cache) the guess head drafts k tokens (1 .. 4;
+// sn_guess's rows, batched over the sequences), the model runs the verify rows [last, d1 .. dk] at pos .. pos + k
+// (every sequence in one pass), and greedy acceptance keeps the leading drafts equal to their row's argmax
+// (next_engine/draft.rs:135-178, take.rs:339-357) — all on the GPU in one submission, one wait. Per sequence: out_n[s]
+// = accepted + 1 tokens in out_tok[s * (k + 1) ..]: the accepted drafts, then the correction (bonus) token, which is
+// the sequence's next pending token at pos[s] + out_n[s]; the rest of its row is -1. The cells of the refused rows
+// are zeroed in every layer (as sn_clear would leave them; their pages stay with the slot) and the head's state moves
+// to the last kept row. force (optional, [n][k] bytes): verify row i of sequence s with force[s * k + i] set takes
+// draft i + 1 as its argmax (a seeded acceptance rate for benchmarks; the rows still run in full). 0, -2 out of
+// pages (nothing ran), or -1 (err).
+int snx_spec_step(sn_engine* e, int n, const int32_t* seq, const int32_t* last, const int32_t* pos, int k,
+                  const uint8_t* force, int32_t* out_n, int32_t* out_tok, char* err, int err_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -384,99 +384,163 @@ static void mm(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M
     or_mul_mat_q4_0(W, N, K, X, M, Y, nt);
 }
 
-void or_qwen3_step(const or_qwen3* m, or_kv* kv, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos,
-                   int n_out, const int32_t* out_rows, float* logits, float* hidden, int32_t* out_tok, int nthreads) {
-    const int E = m->n_embd, H = m->n_head, KVH = m->n_head_kv, D = m->head_dim, F = m->n_ff, V = m->n_vocab;
+// One Qwen3 block over R rows, in place on the residual rows x [R][E] (the rows' rope tables in cs [R][D]). The block's
+// K/V cells go to layer `kl` of the cache. kv_only: stop after writing them (the guess head's cache fill).
+static void block(const or_qwen3* m, const or_layer* L, or_kv* kv, int kl, int R, const int32_t* seq,
+                  const int32_t* pos, float* x, const float* cs, int kv_only, int nthreads) {
+    const int E = m->n_embd, H = m->n_head, KVH = m->n_head_kv, D = m->head_dim, F = m->n_ff;
     const int QD = H * D, KD = KVH * D, G = H / KVH;
-    const float theta_scale = powf(m->rope_base, -2.0f / D);
     const float scale = 1.0f / sqrtf((float) D);
-    float* x = (float*) malloc((size_t) R * E * 4);
-    float* h = (float*) malloc((size_t) R * E * 4);
+    const int FF = F > m->n_ff_exp ? F : m->n_ff_exp;
+    float* h = (float*) calloc((size_t) R * E, 4);
     float* q = (float*) malloc((size_t) R * QD * 4);
     float* k = (float*) malloc((size_t) R * KD * 4);
     float* v = (float*) malloc((size_t) R * KD * 4);
     float* ao = (float*) malloc((size_t) R * QD * 4);
     float* y = (float*) malloc((size_t) R * (E > QD ? E : QD) * 4);
-    const int FF = F > m->n_ff_exp ? F : m->n_ff_exp;
     float* g = (float*) malloc((size_t) R * FF * 4);
     float* u = (float*) malloc((size_t) R * FF * 4);
+    const size_t lstride = (size_t) kv->ctx * KD;  // one layer of one sequence
+    for (int r = 0; r < R; ++r) or_rmsnorm(x + (size_t) r * E, L->attn_norm, E, m->eps, h + (size_t) r * E);
+    if (!kv_only) mm(L->wq, QD, E, h, R, q, nthreads);
+    mm(L->wk, KD, E, h, R, k, nthreads);
+    mm(L->wv, KD, E, h, R, v, nthreads);
+    for (int r = 0; r < R; ++r) {
+        if (!kv_only)
+            for (int hh = 0; hh < H; ++hh)
+                or_qk_norm_rope(q + (size_t) r * QD + hh * D, L->q_norm, D, m->eps, cs + (size_t) r * D, 1);
+        for (int hh = 0; hh < KVH; ++hh)
+            or_qk_norm_rope(k + (size_t) r * KD + hh * D, L->k_norm, D, m->eps, cs + (size_t) r * D, 1);
+        // the row's cell: K and V in fp16
+        const size_t base = ((size_t) seq[r] * kv->n_layer + kl) * lstride + (size_t) pos[r] * KD;
+        for (int i = 0; i < KD; ++i) {
+            kv->k[base + i] = or_f32_to_f16(k[(size_t) r * KD + i]);
+            kv->v[base + i] = or_f32_to_f16(v[(size_t) r * KD + i]);
+        }
+    }
+    if (kv_only) goto done;
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(dynamic, 1)
+    for (int rh = 0; rh < R * H; ++rh) {
+        const int r = rh / H, hh = rh % H, kh = hh / G, n = pos[r] + 1;
+        const size_t base = ((size_t) seq[r] * kv->n_layer + kl) * lstride;
+        const uint16_t** kp = (const uint16_t**) malloc((size_t) n * sizeof(void*));
+        const uint16_t** vp = (const uint16_t**) malloc((size_t) n * sizeof(void*));
+        for (int c = 0; c < n; ++c) {
+            kp[c] = kv->k + base + (size_t) c * KD + (size_t) kh * D;
+            vp[c] = kv->v + base + (size_t) c * KD + (size_t) kh * D;
+        }
+        attn_cells(q + (size_t) r * QD + hh * D, D, n, kp, vp, scale, ao + (size_t) r * QD + hh * D, 0);
+        free(kp);
+        free(vp);
+    }
+    mm(L->wo, E, QD, ao, R, y, nthreads);
+    for (size_t i = 0; i < (size_t) R * E; ++i) x[i] += y[i];
+    for (int r = 0; r < R; ++r) or_rmsnorm(x + (size_t) r * E, L->ffn_norm, E, m->eps, h + (size_t) r * E);
+    if (m->n_expert > 0) {
+        const int NE = m->n_expert, K = m->n_expert_used, FE = m->n_ff_exp;
+        const size_t gsz = (size_t) FE * (E / QK) * 18, dsz = (size_t) E * (FE / QK) * 18;
+        for (int r = 0; r < R; ++r) {
+            float* lg = (float*) malloc((size_t) NE * 4);
+            int32_t ids[64];
+            float w[64];
+            for (int e = 0; e < NE; ++e) {
+                float s = 0.0f;
+                for (int i = 0; i < E; ++i) s += L->router[(size_t) e * E + i] * h[(size_t) r * E + i];
+                lg[e] = s;
+            }
+            or_moe_route(lg, NE, K, ids, w);
+            float* acc = (float*) calloc((size_t) E, 4);
+            for (int j = 0; j < K; ++j) {
+                mm(L->eg + ids[j] * gsz, FE, E, h + (size_t) r * E, 1, g, nthreads);
+                mm(L->eu + ids[j] * gsz, FE, E, h + (size_t) r * E, 1, u, nthreads);
+                for (int i = 0; i < FE; ++i) g[i] = or_silu(g[i]) * u[i];
+                mm(L->ed + ids[j] * dsz, E, FE, g, 1, y, nthreads);
+                for (int i = 0; i < E; ++i) acc[i] += w[j] * y[i];
+            }
+            for (int i = 0; i < E; ++i) x[(size_t) r * E + i] += acc[i];
+            free(acc);
+            free(lg);
+        }
+    } else {
+        mm(L->wg, F, E, h, R, g, nthreads);
+        mm(L->wu, F, E, h, R, u, nthreads);
+        for (size_t i = 0; i < (size_t) R * F; ++i) g[i] = or_silu(g[i]) * u[i];
+        mm(L->wd, E, F, g, R, y, nthreads);
+        for (size_t i = 0; i < (size_t) R * E; ++i) x[i] += y[i];
+    }
+done:
+    free(h); free(q); free(k); free(v); free(ao); free(y); free(g); free(u);
+}
+
+void or_qwen3_step(const or_qwen3* m, or_kv* kv, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos,
+                   int n_out, const int32_t* out_rows, float* logits, float* hidden, int32_t* out_tok, float* hn_all,
+                   int nthreads) {
+    const int E = m->n_embd, D = m->head_dim, V = m->n_vocab;
+    const float theta_scale = powf(m->rope_base, -2.0f / D);
+    float* x = (float*) malloc((size_t) R * E * 4);
     float* cs = (float*) malloc((size_t) R * D * 4);
     for (int r = 0; r < R; ++r) {
         memcpy(x + (size_t) r * E, m->tok_embd + (size_t) tok[r] * E, (size_t) E * 4);
         or_rope_cache(pos[r], theta_scale, D, cs + (size_t) r * D);
     }
-    const size_t lstride = (size_t) kv->ctx * KD;  // one layer of one sequence
-    for (int il = 0; il < m->n_layer; ++il) {
-        const or_layer* L = &m->layers[il];
-        for (int r = 0; r < R; ++r) or_rmsnorm(x + (size_t) r * E, L->attn_norm, E, m->eps, h + (size_t) r * E);
-        mm(L->wq, QD, E, h, R, q, nthreads);
-        mm(L->wk, KD, E, h, R, k, nthreads);
-        mm(L->wv, KD, E, h, R, v, nthreads);
-        for (int r = 0; r < R; ++r) {
-            for (int hh = 0; hh < H; ++hh) or_qk_norm_rope(q + (size_t) r * QD + hh * D, L->q_norm, D, m->eps, cs + (size_t) r * D, 1);
-            for (int hh = 0; hh < KVH; ++hh) or_qk_norm_rope(k + (size_t) r * KD + hh * D, L->k_norm, D, m->eps, cs + (size_t) r * D, 1);
-            // the row's cell: K and V in fp16
-            const size_t base = ((size_t) seq[r] * m->n_layer + il) * lstride + (size_t) pos[r] * KD;
-            for (int i = 0; i < KD; ++i) {
-                kv->k[base + i] = or_f32_to_f16(k[(size_t) r * KD + i]);
-                kv->v[base + i] = or_f32_to_f16(v[(size_t) r * KD + i]);
-            }
-        }
-#pragma omp parallel for num_threads(nthr(nthreads)) schedule(dynamic, 1)
-        for (int rh = 0; rh < R * H; ++rh) {
-            const int r = rh / H, hh = rh % H, kh = hh / G, n = pos[r] + 1;
-            const size_t base = ((size_t) seq[r] * m->n_layer + il) * lstride;
-            const uint16_t** kp = (const uint16_t**) malloc((size_t) n * sizeof(void*));
-            const uint16_t** vp = (const uint16_t**) malloc((size_t) n * sizeof(void*));
-            for (int c = 0; c < n; ++c) {
-                kp[c] = kv->k + base + (size_t) c * KD + (size_t) kh * D;
-                vp[c] = kv->v + base + (size_t) c * KD + (size_t) kh * D;
-            }
-            attn_cells(q + (size_t) r * QD + hh * D, D, n, kp, vp, scale, ao + (size_t) r * QD + hh * D, 0);
-            free(kp);
-            free(vp);
-        }
-        mm(L->wo, E, QD, ao, R, y, nthreads);
-        for (size_t i = 0; i < (size_t) R * E; ++i) x[i] += y[i];
-        for (int r = 0; r < R; ++r) or_rmsnorm(x + (size_t) r * E, L->ffn_norm, E, m->eps, h + (size_t) r * E);
-        if (m->n_expert > 0) {
-            const int NE = m->n_expert, K = m->n_expert_used, FE = m->n_ff_exp;
-            const size_t gsz = (size_t) FE * (E / QK) * 18, dsz = (size_t) E * (FE / QK) * 18;
-            for (int r = 0; r < R; ++r) {
-                float* lg = (float*) malloc((size_t) NE * 4);
-                int32_t ids[64];
-                float w[64];
-                for (int e = 0; e < NE; ++e) {
-                    float s = 0.0f;
-                    for (int i = 0; i < E; ++i) s += m->layers[il].router[(size_t) e * E + i] * h[(size_t) r * E + i];
-                    lg[e] = s;
-                }
-                or_moe_route(lg, NE, K, ids, w);
-                float* acc = (float*) calloc((size_t) E, 4);
-                for (int j = 0; j < K; ++j) {
-                    mm(L->eg + ids[j] * gsz, FE, E, h + (size_t) r * E, 1, g, nthreads);
-                    mm(L->eu + ids[j] * gsz, FE, E, h + (size_t) r * E, 1, u, nthreads);
-                    for (int i = 0; i < FE; ++i) g[i] = or_silu(g[i]) * u[i];
-                    mm(L->ed + ids[j] * dsz, E, FE, g, 1, y, nthreads);
-                    for (int i = 0; i < E; ++i) acc[i] += w[j] * y[i];
-                }
-                for (int i = 0; i < E; ++i) x[(size_t) r * E + i] += acc[i];
-                free(acc);
-                free(lg);
-            }
-        } else {
-            mm(L->wg, F, E, h, R, g, nthreads);
-            mm(L->wu, F, E, h, R, u, nthreads);
-            for (size_t i = 0; i < (size_t) R * F; ++i) g[i] = or_silu(g[i]) * u[i];
-            mm(L->wd, E, F, g, R, y, nthreads);
-            for (size_t i = 0; i < (size_t) R * E; ++i) x[i] += y[i];
-        }
-    }
+    for (int il = 0; il < m->n_layer; ++il) block(m, &m->layers[il], kv, il, R, seq, pos, x, cs, 0, nthreads);
+    if (hn_all)
+        for (int r = 0; r < R; ++r) or_rmsnorm(x + (size_t) r * E, m->output_norm, E, m->eps, hn_all + (size_t) r * E);
     float* ho = (float*) malloc((size_t) (n_out > 0 ? n_out : 1) * E * 4);
     for (int j = 0; j < n_out; ++j) or_rmsnorm(x + (size_t) out_rows[j] * E, m->output_norm, E, m->eps, ho + (size_t) j * E);
     if (hidden) memcpy(hidden, ho, (size_t) n_out * E * 4);
     if (n_out > 0) mm(m->output, V, E, ho, n_out, logits, nthreads);
     for (int j = 0; j < n_out; ++j) out_tok[j] = or_argmax(logits + (size_t) j * V, V, NULL, 0);
     free(ho);
-    free(x); free(h); free(q); free(k); free(v); free(ao); free(y); free(g); free(u); free(cs);
+    free(x);
+    free(cs);
+}
+
+// the guess head's input rows: eh_proj([enorm(embed(tok)); hnorm(hprev)]) (sn_cache.inc.h:357-363, sn_state.inc.h:294-305)
+static void mtp_in(const or_qwen3* m, int R, const int32_t* tok, const float* hprev, float* x, int nthreads) {
+    const int E = m->n_embd;
+    float* cat = (float*) malloc((size_t) R * 2 * E * 4);
+    for (int r = 0; r < R; ++r) {
+        or_rmsnorm(m->tok_embd + (size_t) tok[r] * E, m->mtp_enorm, E, m->eps, cat + (size_t) r * 2 * E);
+        or_rmsnorm(hprev + (size_t) r * E, m->mtp_hnorm, E, m->eps, cat + (size_t) r * 2 * E + E);
+    }
+    mm(m->mtp_eh, E, 2 * E, cat, R, x, nthreads);
+    free(cat);
+}
+
+void or_mtp_fill(const or_qwen3* m, or_kv* kv, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos,
+                 const float* hprev, int nthreads) {
+    const int E = m->n_embd, D = m->head_dim;
+    const float theta_scale = powf(m->rope_base, -2.0f / D);
+    float* x = (float*) malloc((size_t) R * E * 4);
+    float* cs = (float*) malloc((size_t) R * D * 4);
+    for (int r = 0; r < R; ++r) or_rope_cache(pos[r], theta_scale, D, cs + (size_t) r * D);
+    mtp_in(m, R, tok, hprev, x, nthreads);
+    block(m, m->mtp, kv, m->n_layer, R, seq, pos, x, cs, 1, nthreads);
+    free(x);
+    free(cs);
+}
+
+void or_mtp_guess(const or_qwen3* m, or_kv* kv, int seq, int32_t tok, int pos, int k, const float* hprev,
+                  int32_t* out_tok, float* logits, int nthreads) {
+    const int E = m->n_embd, D = m->head_dim, V = m->n_vocab;
+    const float theta_scale = powf(m->rope_base, -2.0f / D);
+    float* h = (float*) malloc((size_t) E * 4);
+    float* x = (float*) malloc((size_t) E * 4);
+    float* cs = (float*) malloc((size_t) D * 4);
+    float* lg = (float*) malloc((size_t) V * 4);
+    memcpy(h, hprev, (size_t) E * 4);
+    int32_t t = tok;
+    for (int j = 0; j < k; ++j) {
+        const int32_t p = pos + j;
+        or_rope_cache(p, theta_scale, D, cs);
+        mtp_in(m, 1, &t, h, x, nthreads);
+        block(m, m->mtp, kv, m->n_layer, 1, &seq, &p, x, cs, 0, nthreads);
+        or_rmsnorm(x, m->mtp_head_norm, E, m->eps, h);  // the head's output state: the next row's hprev
+        mm(m->output, V, E, h, 1, lg, nthreads);
+        t = or_argmax(lg, V, NULL, 0);
+        out_tok[j] = t;
+        if (logits) memcpy(logits + (size_t) j * V, lg, (size_t) V * 4);
+    }
+    free(h); free(x); free(cs); free(lg);
 }

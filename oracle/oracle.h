@@ -110,9 +110,14 @@ typedef struct {
     const float* output_norm;  // [E]
     const uint8_t* output;     // Q4_0 [V][E]
     const or_layer* layers;    // n_layer
+    // the guess head (MTP; NULL when absent): one more block, eh_proj Q4_0 [E][2E], its norms [E]
+    const or_layer* mtp;
+    const uint8_t* mtp_eh;
+    const float *mtp_enorm, *mtp_hnorm, *mtp_head_norm;  // head_norm: shared_head_norm, else output_norm
 } or_qwen3;
 
-// The oracle's KV cache: contiguous per (sequence, layer): K and V fp16 [ctx][KVH][D].
+// The oracle's KV cache: contiguous per (sequence, layer): K and V fp16 [ctx][KVH][D]. n_layer counts the guess
+// head's block too (its cells are layer n_layer - 1 of the model's n_layer + 1).
 typedef struct {
     int n_seq, ctx, n_layer, n_kv, head_dim;
     uint16_t* k;  // [n_seq][n_layer][ctx][KVH][D]
@@ -122,9 +127,22 @@ typedef struct {
 // One step of R rows (tok, seq, pos): every layer writes each row's K/V at (seq, pos) before any row of that layer
 // attends, so rows of one sequence at consecutive positions see each other causally (prompt rows, draft rows).
 // logits: [n_out][V] of rows out_rows; hidden (optional): [n_out][E] of those rows after the final norm;
-// out_tok: the greedy token of each output row. nthreads <= 0: all cores.
+// out_tok: the greedy token of each output row; hn_all (optional): [R][E] every row after the final norm (what the guess
+// head pairs with the next position's token). nthreads <= 0: all cores.
 void or_qwen3_step(const or_qwen3* m, or_kv* kv, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos,
-                   int n_out, const int32_t* out_rows, float* logits, float* hidden, int32_t* out_tok, int nthreads);
+                   int n_out, const int32_t* out_rows, float* logits, float* hidden, int32_t* out_tok, float* hn_all,
+                   int nthreads);
+
+// The guess head's cache cells of R rows (mtp_fill, sn_state.inc.h:283-313): row r's cell at (seq, pos) from its token
+// and hprev [R][E], the model's hidden state after the output norm at pos - 1 (zeros at position 0): eh_proj of
+// [enorm(embed(tok)); hnorm(hprev)], the head block's attn_norm, k (QK-norm, RoPE) and v.
+void or_mtp_fill(const or_qwen3* m, or_kv* kv, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos,
+                 const float* hprev, int nthreads);
+// k guesses of one sequence (sn_guess / guess_row, sn_cache.inc.h:300-388): row j at position pos + j takes token tok
+// (then guess j - 1) and hprev (then the head's own output state), runs the head block (writing its cell), the head
+// norm, the LM head and argmax. logits (optional): [k][V].
+void or_mtp_guess(const or_qwen3* m, or_kv* kv, int seq, int32_t tok, int pos, int k, const float* hprev,
+                  int32_t* out_tok, float* logits, int nthreads);
 
 // MoE FFN routing of one row: softmax over n_expert router logits, the k largest (ties: lower id), weights
 // renormalised by their sum floored at 6.103515625e-5 (kernels.metal:3419-3467).

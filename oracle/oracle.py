@@ -63,7 +63,9 @@ def _declare(L):
     L.or_moe_route.argtypes = [P, C.c_int, C.c_int, P, P]
     L.or_accept.argtypes = [P, P, C.c_int]
     L.or_accept.restype = C.c_int
-    L.or_qwen3_step.argtypes = [P, P, C.c_int, P, P, P, C.c_int, P, P, P, P, C.c_int]
+    L.or_qwen3_step.argtypes = [P, P, C.c_int, P, P, P, C.c_int, P, P, P, P, P, C.c_int]
+    L.or_mtp_fill.argtypes = [P, P, C.c_int, P, P, P, P, C.c_int]
+    L.or_mtp_guess.argtypes = [P, P, C.c_int, C.c_int32, C.c_int, C.c_int, P, P, P, C.c_int]
 
 
 def _p(a: np.ndarray):
@@ -221,7 +223,8 @@ class _Model(C.Structure):
                 ("head_dim", C.c_int), ("n_ff", C.c_int), ("n_vocab", C.c_int), ("n_expert", C.c_int),
                 ("n_expert_used", C.c_int), ("n_ff_exp", C.c_int), ("eps", C.c_float), ("rope_base", C.c_float),
                 ("tok_embd", C.c_void_p), ("output_norm", C.c_void_p), ("output", C.c_void_p),
-                ("layers", C.POINTER(_Layer))]
+                ("layers", C.POINTER(_Layer)), ("mtp", C.POINTER(_Layer)), ("mtp_eh", C.c_void_p),
+                ("mtp_enorm", C.c_void_p), ("mtp_hnorm", C.c_void_p), ("mtp_head_norm", C.c_void_p)]
 
 
 class _KV(C.Structure):
@@ -237,7 +240,8 @@ class Qwen3:
         a = g.kv["general.architecture"]
         self.arch = a
         self.E = int(g.kv[f"{a}.embedding_length"])
-        self.L = int(g.kv[f"{a}.block_count"])
+        self.n_mtp = int(g.kv.get(f"{a}.nextn_predict_layers", 0))  # block_count counts the guess head's block too
+        self.L = int(g.kv[f"{a}.block_count"]) - self.n_mtp
         self.H = int(g.kv[f"{a}.attention.head_count"])
         self.KVH = int(g.kv[f"{a}.attention.head_count_kv"])
         self.D = int(g.kv.get(f"{a}.attention.key_length", self.E // self.H))
@@ -257,8 +261,8 @@ class Qwen3:
             self._keep.append(t)
             return t.ctypes.data
 
-        layers = (_Layer * self.L)()
-        for i in range(self.L):
+        layers = (_Layer * (self.L + self.n_mtp))()
+        for i in range(self.L + self.n_mtp):
             p = f"blk.{i}."
             ly = layers[i]
             for f, n in (("attn_norm", "attn_norm"), ("q_norm", "attn_q_norm"), ("k_norm", "attn_k_norm"),
@@ -278,13 +282,22 @@ class Qwen3:
         self.m = _Model(self.L, self.E, self.H, self.KVH, self.D, self.F, self.V, self.NE, self.NEU, self.FE,
                         self.eps, self.base, ptr("token_embd.weight"), ptr("output_norm.weight"),
                         ptr("output.weight"), layers)
+        if self.n_mtp:
+            p = f"blk.{self.L}.nextn."
+            self.m.mtp = C.cast(C.byref(layers, self.L * C.sizeof(_Layer)), C.POINTER(_Layer))
+            self.m.mtp_eh = ptr(p + "eh_proj.weight")
+            self.m.mtp_enorm = ptr(p + "enorm.weight")
+            self.m.mtp_hnorm = ptr(p + "hnorm.weight")
+            hn = p + "shared_head_norm.weight"
+            self.m.mtp_head_norm = ptr(hn if hn in g.tinfo else "output_norm.weight")
         self.n_seq, self.ctx = n_seq, ctx
-        shape = (n_seq, self.L, ctx, self.KVH, self.D)
+        shape = (n_seq, self.L + self.n_mtp, ctx, self.KVH, self.D)
         self.k = np.zeros(shape, np.uint16)
         self.v = np.zeros(shape, np.uint16)
-        self.kv = _KV(n_seq, ctx, self.L, self.KVH, self.D, self.k.ctypes.data, self.v.ctypes.data)
+        self.kv = _KV(n_seq, ctx, self.L + self.n_mtp, self.KVH, self.D, self.k.ctypes.data, self.v.ctypes.data)
 
-    def step(self, tok, seq, pos, out_rows, want_hidden=False, nthreads=0):
+    def step(self, tok, seq, pos, out_rows, want_hidden=False, nthreads=0, hn_all=None):
+        """hn_all (optional float32 [R][E]): receives every row's hidden state after the output norm."""
         tok = np.ascontiguousarray(tok, np.int32)
         seq = np.ascontiguousarray(seq, np.int32)
         pos = np.ascontiguousarray(pos, np.int32)
@@ -294,5 +307,23 @@ class Qwen3:
         hidden = np.empty((max(n_out, 1), self.E), np.float32) if want_hidden else None
         out_tok = np.empty(max(n_out, 1), np.int32)
         lib().or_qwen3_step(C.byref(self.m), C.byref(self.kv), tok.size, _p(tok), _p(seq), _p(pos), n_out,
-                            _p(out_rows), _p(logits), _p(hidden) if want_hidden else None, _p(out_tok), nthreads)
+                            _p(out_rows), _p(logits), _p(hidden) if want_hidden else None, _p(out_tok),
+                            _p(hn_all) if hn_all is not None else None, nthreads)
         return out_tok[:n_out], logits[:n_out], (hidden[:n_out] if want_hidden else None)
+
+    def mtp_fill(self, tok, seq, pos, hprev, nthreads=0):
+        """The guess head's cache cells of rows (tok, seq, pos); hprev [R][E]: the model's normed hidden state at pos - 1."""
+        tok = np.ascontiguousarray(tok, np.int32)
+        seq = np.ascontiguousarray(seq, np.int32)
+        pos = np.ascontiguousarray(pos, np.int32)
+        hp = np.ascontiguousarray(hprev, np.float32)
+        lib().or_mtp_fill(C.byref(self.m), C.byref(self.kv), tok.size, _p(tok), _p(seq), _p(pos), _p(hp), nthreads)
+
+    def mtp_guess(self, seq, tok, pos, k, hprev, nthreads=0):
+        """k guesses of one sequence; returns (tokens [k], logits [k][V])."""
+        out = np.empty(k, np.int32)
+        lg = np.empty((k, self.V), np.float32)
+        hp = np.ascontiguousarray(hprev, np.float32)
+        lib().or_mtp_guess(C.byref(self.m), C.byref(self.kv), int(seq), int(tok), int(pos), int(k), _p(hp), _p(out),
+                           _p(lg), nthreads)
+        return out, lg

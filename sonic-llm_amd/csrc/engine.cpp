@@ -40,7 +40,7 @@ struct DevLayer {
 struct sn_engine {
     GgufFile gg;
     std::string arch;
-    int E = 0, L = 0, H = 0, KVH = 0, D = 128, F = 0, V = 0, QD = 0, KD = 0, NQKV = 0, n_ctx_train = 0;
+    int E = 0, L = 0, CL = 0, H = 0, KVH = 0, D = 128, F = 0, V = 0, QD = 0, KD = 0, NQKV = 0, n_ctx_train = 0;
     float eps = 1e-6f, rope_base = 1e6f, theta_scale = 1.0f;
     int slots = 0, ctx = 0, max_rows = 0, n_pages = 0, page_cells = 64, max_pages = 0, max_out = 0;
     bool has_nextn = false;
@@ -52,6 +52,16 @@ struct sn_engine {
     float *tok_embd = nullptr, *out_norm = nullptr;
     uint8_t* head = nullptr;
     std::vector<DevLayer> ly;
+    // the guess head (MTP): its block, eh_proj stripes [E][2E], enorm, hnorm, the norm before the LM head
+    DevLayer mtp;
+    uint8_t* mtp_eh = nullptr;
+    float *mtp_enorm = nullptr, *mtp_hnorm = nullptr, *mtp_hdnorm = nullptr;
+    // its rows' buffers: mhn the step's rows after the output norm, mpend each slot's last one (the next head row's
+    // hidden state), mhg the head rows' own output states, mx their residual rows, mcat [enorm(embed); hnorm(h)] rows
+    float *mhn = nullptr, *mpend = nullptr, *mhg = nullptr, *mx = nullptr, *mcat = nullptr;
+    int32_t* d_gtok = nullptr;  // guesses [4][slots]
+    // the last step's run of rows of each slot (first row, its position, rows): sn_clear keeps mpend at the cut
+    std::vector<int> run_row, run_pos, run_n;
     uint16_t *kbase = nullptr, *vbase = nullptr;
     size_t layer_halves = 0;  // one layer's K (or V) pool, in fp16 values
     int32_t* d_pt = nullptr;
@@ -199,6 +209,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     const int nextn = (int) g.num(a + ".nextn_predict_layers", 0);
     e->has_nextn = nextn > 0;
     e->L = (int) g.num(a + ".block_count", 0) - nextn;
+    e->CL = e->L + (nextn > 0 ? 1 : 0);  // cache layers: the model's, then the guess head's
     e->E = (int) g.num(a + ".embedding_length", 0);
     e->H = (int) g.num(a + ".attention.head_count", 0);
     e->KVH = (int) g.num(a + ".attention.head_count_kv", 0);
@@ -220,7 +231,9 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->max_pages = e->ctx / e->page_cells;
     e->n_pages = pages > 0 ? pages : slots * e->max_pages;
     e->max_rows = max_rows;
-    e->max_out = slots + 4;
+    // output rows a step may ask for: a write row per slot and a few drafts (sn_step.inc.h:97-99); with a guess head the
+    // fused draft-verify step reads every verify row (up to 5 a slot)
+    e->max_out = std::max(slots + 4, e->has_nextn ? std::min(max_rows, 5 * slots) : 0);
     e->max_chunks = (e->ctx + ATT_CHUNK - 1) / ATT_CHUNK;
     if (hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking) != hipSuccess || hipEventCreate(&e->ev0) != hipSuccess ||
         hipEventCreate(&e->ev1) != hipSuccess)
@@ -258,9 +271,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
         e->head = e->dalloc<uint8_t>(q4t_bytes(e->V, E), err, err_len);
         ok = e->head && upload_q4(e, t, tmp, e->head, 1, 0, err, err_len);
     }
-    e->ly.resize(e->L);
-    for (int i = 0; i < e->L && ok; ++i) {
-        DevLayer& l = e->ly[i];
+    auto load_layer = [&](int i, DevLayer& l) {
         const std::string p = "blk." + std::to_string(i) + ".";
         l.attn_norm = f32(p + "attn_norm.weight", E);
         l.q_norm = f32(p + "attn_q_norm.weight", e->D);
@@ -270,7 +281,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
                          *tv = q4(p + "attn_v.weight", KD, E), *to = q4(p + "attn_output.weight", E, QD),
                          *tg = q4(p + "ffn_gate.weight", F, E), *tu = q4(p + "ffn_up.weight", F, E),
                          *td = q4(p + "ffn_down.weight", E, F);
-        if (!ok) break;
+        if (!ok) return;
         l.wqkv = e->dalloc<uint8_t>(q4t_bytes(e->NQKV, E), err, err_len);
         l.wo = e->dalloc<uint8_t>(q4t_bytes(E, QD), err, err_len);
         l.wgu = e->dalloc<uint8_t>(q4t_bytes(2 * F, E), err, err_len);
@@ -282,16 +293,31 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
              upload_q4(e, tv, tmp, l.wqkv + q4t_bytes(QD + KD, E), 1, 0, err, err_len) &&
              upload_q4(e, to, tmp, l.wo, 1, 0, err, err_len) && upload_q4(e, tg, tmp, l.wgu, 2, 0, err, err_len) &&
              upload_q4(e, tu, tmp, l.wgu, 2, 1, err, err_len) && upload_q4(e, td, tmp, l.wd, 1, 0, err, err_len);
+    };
+    e->ly.resize(e->L);
+    for (int i = 0; i < e->L && ok; ++i) load_layer(i, e->ly[i]);
+    if (e->has_nextn && ok) {
+        // the guess head (sn_load.inc.h:134-147): block L, eh_proj [E][2E], its norms; shared_head_norm falls back to
+        // the model's output norm
+        load_layer(e->L, e->mtp);
+        const std::string p = "blk." + std::to_string(e->L) + ".nextn.";
+        if (const GgufTensor* t = ok ? q4(p + "eh_proj.weight", E, 2 * E) : nullptr) {
+            e->mtp_eh = e->dalloc<uint8_t>(q4t_bytes(E, 2 * E), err, err_len);
+            ok = e->mtp_eh && upload_q4(e, t, tmp, e->mtp_eh, 1, 0, err, err_len);
+        }
+        if (ok) e->mtp_enorm = f32(p + "enorm.weight", E);
+        if (ok) e->mtp_hnorm = f32(p + "hnorm.weight", E);
+        if (ok) e->mtp_hdnorm = g.find(p + "shared_head_norm.weight") ? f32(p + "shared_head_norm.weight", E) : e->out_norm;
     }
     hipFree(tmp);
     if (!ok) return fail(why.empty() ? std::string() : why);
 
     // ---- the KV pool: per layer, K then V, pages of [KVH][page_cells][128] fp16, zeroed
     e->layer_halves = (size_t) e->n_pages * e->KVH * e->page_cells * e->D;
-    e->kbase = e->dalloc<uint16_t>(e->layer_halves * 2 * e->L * sizeof(uint16_t), err, err_len);
+    e->kbase = e->dalloc<uint16_t>(e->layer_halves * 2 * e->CL * sizeof(uint16_t), err, err_len);
     if (!e->kbase) return fail("");
-    e->vbase = e->kbase + e->layer_halves * e->L;
-    if (hipMemset(e->kbase, 0, e->layer_halves * 2 * e->L * 2) != hipSuccess) return fail("KV pool clear failed");
+    e->vbase = e->kbase + e->layer_halves * e->CL;
+    if (hipMemset(e->kbase, 0, e->layer_halves * 2 * e->CL * 2) != hipSuccess) return fail("KV pool clear failed");
     e->pt.assign((size_t) slots * e->max_pages, -1);
     e->ref.assign(e->n_pages, 0);
     for (int p = e->n_pages - 1; p >= 0; --p) e->freel.push_back(p);
@@ -299,7 +325,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
 
     // ---- step buffers
     const int R = max_rows, MO = e->max_out;
-    const int KMAX = std::max(std::max(E, QD), F);
+    const int KMAX = std::max(std::max(E, QD), std::max(F, e->has_nextn ? 2 * E : 0));
     e->d_pt = e->dalloc<int32_t>(e->pt.size() * 4, err, err_len);
     e->x = e->dalloc<float>((size_t) R * E * 4, err, err_len);
     e->qkv = e->dalloc<float>((size_t) R * e->NQKV * 4, err, err_len);
@@ -313,12 +339,20 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     ws = std::max(ws, q4_workspace_bytes(R, 2 * F, E));
     ws = std::max(ws, q4_workspace_bytes(R, E, F));
     ws = std::max(ws, q4_workspace_bytes(MO, e->V, E));
+    if (e->has_nextn) {
+        ws = std::max(ws, q4_workspace_bytes(R, E, 2 * E));    // eh_proj
+        ws = std::max(ws, q4_workspace_bytes(R, 2 * KD, E));   // the head's k|v (its cache fill)
+    }
     e->gemm_ws_bytes = ws;
     e->gemm_ws = e->dalloc<float>(ws, err, err_len);
     e->apart = e->dalloc<float>((size_t) R * e->H * e->max_chunks * (e->D + 2) * 4, err, err_len);
     // staging: tok, seq, pos (R each), out_rows (MO), skip (MO bytes, padded), groups (R), items (R * max_chunks), pt
+    // (+ with a guess head: 4 rounds of head rows, one a slot, their groups and items; row sources and keep lists)
     e->stage_bytes = (size_t) 3 * R * 4 + (size_t) MO * 4 + ((MO + 15) / 16 * 16) + (size_t) R * sizeof(AttnGroup) +
                      (size_t) R * e->max_chunks * sizeof(AttnItem) + e->pt.size() * 4 + 256;
+    if (e->has_nextn)
+        e->stage_bytes += (size_t) 4 * slots * (sizeof(AttnGroup) + e->max_chunks * sizeof(AttnItem) + 64) +
+                          (size_t) 16 * R * 4 + 4096;
     e->d_stage = e->dalloc<uint8_t>(e->stage_bytes, err, err_len);
     e->d_otok = e->dalloc<int32_t>((size_t) MO * 4, err, err_len);
     e->d_rec = e->dalloc<float>((size_t) MO * 32, err, err_len);
@@ -326,6 +360,20 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     if (!e->d_pt || !e->x || !e->qkv || !e->ao || !e->hb || !e->logits || !e->xa || !e->gemm_ws || !e->apart ||
         !e->d_stage || !e->d_otok || !e->d_rec || !e->d_ban)
         return fail("");
+    if (e->has_nextn) {
+        const int RS = std::max(R, slots);
+        e->mhn = e->dalloc<float>((size_t) R * E * 4, err, err_len);
+        e->mpend = e->dalloc<float>((size_t) slots * E * 4, err, err_len);
+        e->mhg = e->dalloc<float>((size_t) RS * E * 4, err, err_len);
+        e->mx = e->dalloc<float>((size_t) RS * E * 4, err, err_len);
+        e->mcat = e->dalloc<float>((size_t) RS * 2 * E * 4, err, err_len);
+        e->d_gtok = e->dalloc<int32_t>((size_t) 4 * slots * 4, err, err_len);
+        if (!e->mhn || !e->mpend || !e->mhg || !e->mx || !e->mcat || !e->d_gtok) return fail("");
+        if (hipMemset(e->mpend, 0, (size_t) slots * E * 4) != hipSuccess) return fail("guess-head state clear failed");
+        e->run_row.assign(slots, -1);
+        e->run_pos.assign(slots, 0);
+        e->run_n.assign(slots, 0);
+    }
     if (hipHostMalloc((void**) &e->h_stage, e->stage_bytes, 0) != hipSuccess ||
         hipHostMalloc((void**) &e->h_otok, (size_t) MO * 4, 0) != hipSuccess ||
         hipHostMalloc((void**) &e->h_rec, (size_t) MO * 32, 0) != hipSuccess)
@@ -382,7 +430,7 @@ int page_new(sn_engine* e) {
 void page_drop(sn_engine* e, int p) {
     if (p < 0) return;
     if (--e->ref[p] == 0) {
-        kv_page_op(e->kbase, e->vbase, e->layer_halves, e->L, e->KVH, e->page_cells, -1, p, 0, e->page_cells, e->st);
+        kv_page_op(e->kbase, e->vbase, e->layer_halves, e->CL, e->KVH, e->page_cells, -1, p, 0, e->page_cells, e->st);
         e->freel.push_back(p);
     }
 }
@@ -405,64 +453,40 @@ bool step_shape_bad(const sn_engine* e, int R, int n_write, int n_fast, int n_ou
 
 }  // namespace
 
-extern "C" int sn_step(sn_engine* e, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos, int n_write,
-                       int n_fast, int n_out, const int32_t* out_rows, int32_t* out_tok, int chain, char* err,
-                       int err_len) {
-    (void) chain;  // a chained step is run as an ordinary step: the same tokens (sn.h:36-38)
-    if (step_shape_bad(e, R, n_write, n_fast, n_out)) {
-        sn_set_err(err, err_len, "bad step shape");
-        return -1;
-    }
-    for (int r = 0; r < R; ++r)
-        if (seq[r] < 0 || seq[r] >= e->slots || pos[r] < 0 || pos[r] >= e->ctx || tok[r] < 0 || tok[r] >= e->V) {
-            sn_set_err(err, err_len, "a row is out of range (slot, position or token)");
-            return -1;
-        }
-    for (int j = 0; j < n_out; ++j)
-        if (out_rows[j] < 0 || out_rows[j] >= R) {
-            sn_set_err(err, err_len, "an output row is outside the step");
-            return -1;
-        }
-    // a page for every cell a row reads or writes (pages_for gives the row's own chunk; here also any earlier chunk a
-    // sequence never wrote, as a zero page: the attention reads cells 0 .. pos of every row, and unwritten cells are
-    // zero). Out of pages: -2 with nothing run.
-    std::vector<std::pair<int, int>> fresh;
-    for (int r = 0; r < R; ++r)
-        for (int c = 0; c <= pos[r] / e->page_cells; ++c) {
-        int32_t* t = e->seq_pages(seq[r]) + c;
-        if (*t < 0) {
-            const int p = page_new(e);
-            if (p < 0) {
-                for (auto& f : fresh) {  // give back what this step took (never written, so still zero)
-                    int32_t* tp = e->seq_pages(f.first) + f.second;
-                    e->ref[*tp] = 0;
-                    e->freel.push_back(*tp);
-                    *tp = -1;
-                }
-                sn_set_err(err, err_len, "out of cache pages");
-                return -2;
-            }
-            *t = p;
-            fresh.push_back({seq[r], c});
-            e->pt_dirty = true;
-        }
-        }
+namespace {
 
-    // ---- the step's rows, attention work list and page table into one staging copy
-    const int G = e->H / e->KVH, gmax = 16 / G;
-    uint8_t* hs = e->h_stage;
+// One staging copy of a step's inputs: pieces 16-byte aligned in the pinned host buffer, copied to the device at once.
+struct Stage {
+    sn_engine* e;
     size_t off = 0;
-    auto put = [&](const void* src, size_t n) {
+    bool over = false;
+    size_t put(const void* src, size_t n) {
         const size_t at = off;
-        memcpy(hs + at, src, n);
+        if (at + n > e->stage_bytes) {
+            over = true;
+            return 0;
+        }
+        if (n) memcpy(e->h_stage + at, src, n);
         off = (off + n + 15) / 16 * 16;
         return at;
-    };
-    const size_t o_tok = put(tok, (size_t) R * 4), o_seq = put(seq, (size_t) R * 4), o_pos = put(pos, (size_t) R * 4);
-    const size_t o_out = put(out_rows, (size_t) n_out * 4);
-    std::vector<uint8_t> skip(n_out + 1, 0);
-    for (int j = 0; j < n_out; ++j) skip[j] = e->no_end[seq[out_rows[j]]];
-    const size_t o_skip = put(skip.data(), (size_t) n_out + 1);
+    }
+    template <class T>
+    size_t put(const std::vector<T>& v) { return put(v.data(), v.size() * sizeof(T)); }
+    template <class T>
+    T* dev(size_t at) const { return (T*) (e->d_stage + at); }
+};
+
+// The attention work of R rows: consecutive rows of one sequence at consecutive positions share a group (up to 16/G
+// rows: their K/V loads are shared), a group has one item per 256-cell chunk of its last row. bytes: each (sequence,
+// KV head) reads its cells once, q in and the output out, page-table entries.
+struct AttnList {
+    size_t o_grp = 0, o_itm = 0;
+    int n_items = 0;
+    double bytes = 0.0;
+};
+
+AttnList attn_list(sn_engine* e, Stage& S, int R, const int32_t* seq, const int32_t* pos) {
+    const int gmax = 16 / (e->H / e->KVH);
     std::vector<AttnGroup> groups;
     std::vector<AttnItem> items;
     for (int r = 0; r < R;) {
@@ -474,128 +498,267 @@ extern "C" int sn_step(sn_engine* e, int R, const int32_t* tok, const int32_t* s
         for (int c = 0; c <= last / ATT_CHUNK; ++c) items.push_back({gi, c});
         r += n;
     }
-    const size_t o_grp = put(groups.data(), groups.size() * sizeof(AttnGroup));
-    const size_t o_itm = put(items.data(), items.size() * sizeof(AttnItem));
+    AttnList al;
+    al.o_grp = S.put(groups);
+    al.o_itm = S.put(items);
+    al.n_items = (int) items.size();
+    al.bytes = (double) R * e->QD * 8;
+    std::vector<int> seen;
+    for (const AttnGroup& g : groups) {
+        if (std::find(seen.begin(), seen.end(), g.seq) != seen.end()) continue;
+        seen.push_back(g.seq);
+        int last = 0;
+        for (const AttnGroup& h : groups)
+            if (h.seq == g.seq) last = std::max(last, h.pos0 + h.nrows - 1);
+        al.bytes += (double) (last + 1) * e->KD * 2 * 2 + 4.0 * (last / e->page_cells + 1);
+    }
+    return al;
+}
+
+// A page for every cell the rows read or write: the attention reads cells 0 .. pos of every row, and a chunk a
+// sequence never wrote is a zero page. Out of pages: -2 with nothing taken.
+int take_pages(sn_engine* e, int R, const int32_t* seq, const int32_t* pos) {
+    std::vector<std::pair<int, int>> fresh;
+    for (int r = 0; r < R; ++r)
+        for (int c = 0; c <= pos[r] / e->page_cells; ++c) {
+            int32_t* t = e->seq_pages(seq[r]) + c;
+            if (*t >= 0) continue;
+            const int p = page_new(e);
+            if (p < 0) {
+                for (auto& f : fresh) {  // give back what this call took (never written, so still zero)
+                    int32_t* tp = e->seq_pages(f.first) + f.second;
+                    e->ref[*tp] = 0;
+                    e->freel.push_back(*tp);
+                    *tp = -1;
+                }
+                return -2;
+            }
+            *t = p;
+            fresh.push_back({seq[r], c});
+            e->pt_dirty = true;
+        }
+    return 0;
+}
+
+// the staged inputs to the device (and the page table when it changed); starts the step's GPU clock
+int stage_copy(sn_engine* e, Stage& S) {
     const bool send_pt = e->pt_dirty;
-    const size_t o_pt = send_pt ? put(e->pt.data(), e->pt.size() * 4) : 0;
-    const size_t copy_bytes = off;
-    hipStream_t st = e->st;
-    SN_HIP_TRY(hipEventRecord(e->ev0, st), -1);
-    SN_HIP_TRY(hipMemcpyAsync(e->d_stage, hs, copy_bytes, hipMemcpyHostToDevice, st), -1);
+    const size_t o_pt = send_pt ? S.put(e->pt) : 0;
+    if (S.over) return -1;
+    if (hipEventRecord(e->ev0, e->st) != hipSuccess ||
+        hipMemcpyAsync(e->d_stage, e->h_stage, S.off, hipMemcpyHostToDevice, e->st) != hipSuccess)
+        return -1;
     if (send_pt) {
-        SN_HIP_TRY(hipMemcpyAsync(e->d_pt, e->d_stage + o_pt, e->pt.size() * 4, hipMemcpyDeviceToDevice, st), -1);
+        if (hipMemcpyAsync(e->d_pt, e->d_stage + o_pt, e->pt.size() * 4, hipMemcpyDeviceToDevice, e->st) != hipSuccess)
+            return -1;
         e->pt_dirty = false;
     }
-    const int32_t* d_tok = (const int32_t*) (e->d_stage + o_tok);
-    const int32_t* d_seq = (const int32_t*) (e->d_stage + o_seq);
-    const int32_t* d_pos = (const int32_t*) (e->d_stage + o_pos);
-    const int32_t* d_out = (const int32_t*) (e->d_stage + o_out);
-    const uint8_t* d_skip = e->d_stage + o_skip;
+    return 0;
+}
 
-    // ---- the layers (qwen_layers, sn_attn.inc.h:216-231)
-    const int E = e->E, QD = e->QD, KD = e->KD, F = e->F;
-    e->prof_recs.clear();
-    auto gemm_bytes = [](int M, int N, int K) { return (double) N * (K / 32) * 18 + (double) M * K * 4 + (double) M * N * 4; };
-    // attention: each (sequence, KV head) reads its cells once; q in, output out, page-table entries
-    double attn_bytes = (double) R * QD * 8;
-    {
-        std::vector<int> seen;
-        for (const AttnGroup& g : groups) {
-            int last = g.pos0 + g.nrows - 1;
-            for (const AttnGroup& h : groups)
-                if (h.seq == g.seq) last = std::max(last, h.pos0 + h.nrows - 1);
-            if (std::find(seen.begin(), seen.end(), g.seq) != seen.end()) continue;
-            seen.push_back(g.seq);
-            attn_bytes += (double) (last + 1) * KD * 2 * 2 + 4.0 * (last / e->page_cells + 1);
-        }
-    }
-    int rc = 0;
-    rc |= e->launch(SNX_K_OTHER, (double) R * E * 8, [&] { embed_rows(e->tok_embd, E, d_tok, R, e->x, st); return 0; });
-    AttnArgs aa{};
-    aa.q = e->qkv;
-    aa.ldq = e->NQKV;
-    aa.pt = e->d_pt;
-    aa.max_pages = e->max_pages;
-    aa.page_cells = e->page_cells;
-    aa.groups = (const AttnGroup*) (e->d_stage + o_grp);
-    aa.items = (const AttnItem*) (e->d_stage + o_itm);
-    aa.n_items = (int) items.size();
-    aa.part = e->apart;
-    aa.max_chunks = e->max_chunks;
-    aa.out = e->ao;
-    aa.ldo = QD;
-    aa.H = e->H;
-    aa.KVH = e->KVH;
-    aa.scale = 1.0f / sqrtf((float) e->D);
-    aa.n_rows = R;
-    aa.row_pos = d_pos;
-    auto quant = [&](const float* x, const int32_t* rows, int M, int K, const float* nw) {
-        return e->launch(SNX_K_QUANT, (double) M * K * 8, [&] {
-            quant_act(x, rows, M, K, K, nw, e->eps, e->xa, nullptr, 0, st);
-            return 0;
-        });
-    };
-    // Matmuls leave their k-slice sums in the workspace; the next row kernel adds them in slice order and applies the
-    // epilogue (RoPE for q|k|v, residual add + RMSNorm + Q8_0 for o and down, SwiGLU + Q8_0 for gate/up).
-    float* part = e->gemm_ws;
+double gemm_bytes(int M, int N, int K) { return (double) N * (K / 32) * 18 + (double) M * K * 4 + (double) M * N * 4; }
+
+// Device work of a step, all on the engine's stream. Matmuls leave their k-slice sums in the workspace; the next row
+// kernel adds them in slice order and applies the epilogue (RoPE for q|k|v, residual add + RMSNorm + Q8_0 for o and
+// down, SwiGLU + Q8_0 for gate/up).
+struct Dev {
+    sn_engine* e;
+    hipStream_t st;
     int ks = 0;  // k-slices of the last matmul
-    auto gemm = [&](const uint8_t* w, int M, int N, int K) {
-        return e->launch(SNX_K_GEMM, gemm_bytes(M, N, K), [&] {
-            ks = q4_gemm_raw(w, e->xa, M, N, K, part, e->gemm_ws_bytes, st);
+    int rc = 0;
+
+    void gemm(const uint8_t* w, int M, int N, int K) {
+        rc |= e->launch(SNX_K_GEMM, gemm_bytes(M, N, K), [&] {
+            ks = q4_gemm_raw(w, e->xa, M, N, K, e->gemm_ws, e->gemm_ws_bytes, st);
             return ks < 0 ? -1 : 0;
         });
-    };
-    auto resid = [&](const float* nw, bool quantize) {
-        return e->launch(SNX_K_QUANT, (double) R * E * (8 + 4 * ks) + (quantize ? (double) R * E * 2 : 0.0), [&] {
-            return resid_quant(e->x, part, ks, R, E, nw, e->eps, quantize ? e->xa : nullptr, st);
+    }
+    void quant(const float* x, const int32_t* rows, int M, int K, const float* nw, float* xn = nullptr) {
+        rc |= e->launch(SNX_K_QUANT, (double) M * K * 8, [&] {
+            quant_act(x, rows, M, K, K, nw, e->eps, e->xa, xn, K, st);
+            return 0;
         });
-    };
-    rc |= quant(e->x, nullptr, R, E, e->ly[0].attn_norm);  // layer 0: x is the embedding
-    for (int i = 0; i < e->L && rc == 0; ++i) {
-        const DevLayer& l = e->ly[i];
-        uint16_t* kp = e->kbase + (size_t) i * e->layer_halves;
-        uint16_t* vp = e->vbase + (size_t) i * e->layer_halves;
-        if (i > 0) rc |= resid(l.attn_norm, true);  // x += the previous layer's down projection
-        rc |= gemm(l.wqkv, R, e->NQKV, E);
-        rc |= e->launch(SNX_K_ROPE, (double) R * (e->NQKV * 4.0 * (ks + 1) + QD * 4 + 2 * KD * 2), [&] {
-            qk_norm_rope_kv(e->qkv, e->NQKV, part, ks, R, e->H, e->KVH, l.q_norm, l.k_norm, e->eps, e->theta_scale,
+    }
+    // x (R rows of E) += the last matmul's sums (add false: x = the sums); then the Q8_0 operand of norm(x) when asked
+    void resid(float* x, int R, const float* nw, bool quantize, bool add = true) {
+        const int E = e->E;
+        rc |= e->launch(SNX_K_QUANT, (double) R * E * (8 + 4 * ks) + (quantize ? (double) R * E * 2 : 0.0), [&] {
+            return resid_quant(x, e->gemm_ws, ks, R, E, nw, e->eps, quantize ? e->xa : nullptr, st, add);
+        });
+    }
+    void swiglu(int R) {
+        const int F = e->F;
+        rc |= e->launch(SNX_K_QUANT, (double) R * 2 * F * 4 * ks + (double) R * F * 6, [&] {
+            swiglu_quant(e->gemm_ws, ks, R, F, e->hb, e->xa, st);
+            return 0;
+        });
+    }
+    void rope(const DevLayer& l, int R, int H, const int32_t* d_seq, const int32_t* d_pos, uint16_t* kp, uint16_t* vp) {
+        const int N = (H + 2 * e->KVH) * e->D;
+        rc |= e->launch(SNX_K_ROPE, (double) R * (N * 4.0 * (ks + 1) + H * e->D * 4 + 2 * e->KD * 2), [&] {
+            qk_norm_rope_kv(e->qkv, e->NQKV, e->gemm_ws, ks, R, H, e->KVH, l.q_norm, l.k_norm, e->eps, e->theta_scale,
                             d_seq, d_pos, e->d_pt, e->max_pages, e->page_cells, kp, vp, st);
             return 0;
         });
+    }
+    void attention(const Stage& S, const AttnList& al, int R, const int32_t* d_pos, uint16_t* kp, uint16_t* vp) {
+        AttnArgs aa{};
+        aa.q = e->qkv;
+        aa.ldq = e->NQKV;
         aa.kpool = kp;
         aa.vpool = vp;
+        aa.pt = e->d_pt;
+        aa.max_pages = e->max_pages;
+        aa.page_cells = e->page_cells;
+        aa.groups = S.dev<const AttnGroup>(al.o_grp);
+        aa.items = S.dev<const AttnItem>(al.o_itm);
+        aa.n_items = al.n_items;
+        aa.part = e->apart;
+        aa.max_chunks = e->max_chunks;
+        aa.out = e->ao;
+        aa.ldo = e->QD;
         aa.xa = e->xa;  // the merge writes the o-projection's Q8_0 operand itself
-        rc |= e->launch(SNX_K_ATTN, attn_bytes, [&] { return paged_attention(aa, st); });
-        rc |= gemm(l.wo, R, E, QD);
-        rc |= resid(l.ffn_norm, true);
-        rc |= gemm(l.wgu, R, 2 * F, E);
-        rc |= e->launch(SNX_K_QUANT, (double) R * 2 * F * 4 * ks + (double) R * F * 6, [&] {
-            swiglu_quant(part, ks, R, F, e->hb, e->xa, st);
-            return 0;
-        });
-        rc |= gemm(l.wd, R, E, F);
+        aa.H = e->H;
+        aa.KVH = e->KVH;
+        aa.scale = 1.0f / sqrtf((float) e->D);
+        aa.n_rows = R;
+        aa.row_pos = d_pos;
+        rc |= e->launch(SNX_K_ATTN, al.bytes, [&] { return paged_attention(aa, st); });
     }
-    if (rc == 0) rc |= resid(nullptr, false);  // x += the last layer's down projection
-    // ---- outputs (sn_encode.inc.h:304-317): final norm of the output rows, LM head, argmax
-    if (n_out > 0 && rc == 0) {
-        rc |= quant(e->x, d_out, n_out, E, e->out_norm);
-        rc |= e->launch(SNX_K_GEMM, gemm_bytes(n_out, e->V, E), [&] {
-            if (q4_plan(e->V, E).ks == 1)  // one slice: the sums are the logits
-                return q4_gemm_raw(e->head, e->xa, n_out, e->V, E, e->logits, (size_t) n_out * e->V * 4, st) < 0 ? -1 : 0;
-            return q4_gemm(e->head, e->xa, n_out, e->V, E, e->logits, e->V, EPI_STORE, e->gemm_ws, e->gemm_ws_bytes, st);
-        });
+    uint16_t* kp(int layer) { return e->kbase + (size_t) layer * e->layer_halves; }
+    uint16_t* vp(int layer) { return e->vbase + (size_t) layer * e->layer_halves; }
+
+    // one block over R rows whose Q8_0 operand of attn_norm(x) is in xa; x (residual) updated through its down
+    // projection's sums (left in the workspace, not yet added)
+    void block(const DevLayer& l, int layer, float* x, int R, const Stage& S, const AttnList& al, const int32_t* d_seq,
+               const int32_t* d_pos) {
+        const int E = e->E, F = e->F;
+        gemm(l.wqkv, R, e->NQKV, E);
+        rope(l, R, e->H, d_seq, d_pos, kp(layer), vp(layer));
+        attention(S, al, R, d_pos, kp(layer), vp(layer));
+        gemm(l.wo, R, E, e->QD);
+        resid(x, R, l.ffn_norm, true);
+        gemm(l.wgu, R, 2 * F, E);
+        swiglu(R);
+        gemm(l.wd, R, E, F);
+    }
+
+    // the model's layers over R rows (qwen_layers, sn_attn.inc.h:216-231); leaves x = the final residual rows
+    void model(int R, const int32_t* d_tok, const int32_t* d_seq, const int32_t* d_pos, const Stage& S,
+               const AttnList& al) {
+        const int E = e->E;
+        rc |= e->launch(SNX_K_OTHER, (double) R * E * 8, [&] { embed_rows(e->tok_embd, E, d_tok, R, e->x, st); return 0; });
+        quant(e->x, nullptr, R, E, e->ly[0].attn_norm);
+        for (int i = 0; i < e->L && rc == 0; ++i) {
+            if (i > 0) resid(e->x, R, e->ly[i].attn_norm, true);  // x += the previous layer's down projection
+            block(e->ly[i], i, e->x, R, S, al, d_seq, d_pos);
+        }
+        if (rc == 0) resid(e->x, R, nullptr, false);  // x += the last layer's down projection
+    }
+
+    // output stage (sn_encode.inc.h:304-317): final norm of rows d_rows (n of them) of `x`, LM head, optional forced
+    // drafts, greedy argmax into d_otok (and the probability records when on)
+    void outputs(const float* x, int n, const int32_t* d_rows, const uint8_t* d_skip, const uint8_t* d_force = nullptr,
+                 const int32_t* d_ftok = nullptr, int32_t* d_otok = nullptr, const float* hdnorm = nullptr) {
+        const int E = e->E, V = e->V;
+        quant(x, d_rows, n, E, hdnorm ? hdnorm : e->out_norm);
+        head_logits(n);
+        if (d_force) force_rows(e->logits, V, n, d_force, d_ftok, st);
         const int nban = (int) e->eog.size();
-        rc |= e->launch(SNX_K_OTHER, (double) n_out * e->V * 4, [&] {
-            argmax_rows(e->logits, e->V, n_out, e->d_ban, nban, d_skip, e->d_otok, e->want_probs ? e->d_rec : nullptr,
-                        st);
+        int32_t* out = d_otok ? d_otok : e->d_otok;
+        rc |= e->launch(SNX_K_OTHER, (double) n * V * 4, [&] {
+            argmax_rows(e->logits, V, n, e->d_ban, nban, d_skip, out, e->want_probs && !d_otok ? e->d_rec : nullptr, st);
             return 0;
         });
-        SN_HIP_TRY(hipMemcpyAsync(e->h_otok, e->d_otok, (size_t) n_out * 4, hipMemcpyDeviceToHost, st), -1);
-        if (e->want_probs)
-            SN_HIP_TRY(hipMemcpyAsync(e->h_rec, e->d_rec, (size_t) n_out * 32, hipMemcpyDeviceToHost, st), -1);
     }
-    SN_HIP_TRY(hipEventRecord(e->ev1, st), -1);
-    SN_HIP_TRY(hipStreamSynchronize(st), -1);
+    void head_logits(int n) {
+        const int E = e->E, V = e->V;
+        rc |= e->launch(SNX_K_GEMM, gemm_bytes(n, V, E), [&] {
+            if (q4_plan(V, E).ks == 1)  // one slice: the sums are the logits
+                return q4_gemm_raw(e->head, e->xa, n, V, E, e->logits, (size_t) n * V * 4, st) < 0 ? -1 : 0;
+            return q4_gemm(e->head, e->xa, n, V, E, e->logits, V, EPI_STORE, e->gemm_ws, e->gemm_ws_bytes, st);
+        });
+    }
+
+    // the guess head's cache cells of R rows (mtp_fill, sn_state.inc.h:283-313): mhn = the rows after the output norm;
+    // row r pairs its token with src[r]'s hidden state (an earlier row of mhn, its slot's mpend, or none); eh_proj, the
+    // head block's attn_norm, its k (QK-norm, RoPE) and v into the head's cache layer. keep: (slot, row) pairs whose
+    // mhn row becomes the slot's mpend.
+    void head_fill(int R, const int32_t* d_tok, const int32_t* d_seq, const int32_t* d_pos, const int32_t* d_src,
+                   int nkeep, const int32_t* d_keep) {
+        const int E = e->E;
+        quant(e->x, nullptr, R, E, e->out_norm, e->mhn);
+        rc |= e->launch(SNX_K_OTHER, (double) R * E * 16, [&] {
+            mtp_cat(e->tok_embd, E, d_tok, e->mhn, e->mpend, d_src, d_seq, e->mtp_enorm, e->mtp_hnorm, e->eps, e->mcat, R,
+                    st);
+            return 0;
+        });
+        quant(e->mcat, nullptr, R, 2 * E, nullptr);
+        gemm(e->mtp_eh, R, E, 2 * E);
+        resid(e->mx, R, e->mtp.attn_norm, true, false);
+        // the head's k|v stripes (rows QD .. QD + 2 KD of its q|k|v matrix)
+        gemm(e->mtp.wqkv + q4t_bytes(e->QD, E), R, 2 * e->KD, E);
+        rope(e->mtp, R, 0, d_seq, d_pos, kp(e->L), vp(e->L));
+        if (nkeep > 0) rows_keep(e->mhn, d_keep, nkeep, E, e->mpend, st);
+    }
+
+    // n head rows (sn_cache.inc.h:357-369), row r at position d_pos[r] of slot d_seq[r], token d_tok[r], paired with its
+    // slot's mpend (first) or with mhg row r (the head's previous output state): the head block (writing its cell),
+    // the head norm (mhg), the LM head and argmax into d_gout
+    void head_rows(int n, const int32_t* d_tok, const int32_t* d_seq, const int32_t* d_pos, bool first, const Stage& S,
+                   const AttnList& al, int32_t* d_gout) {
+        const int E = e->E;
+        rc |= e->launch(SNX_K_OTHER, (double) n * E * 16, [&] {
+            mtp_cat(e->tok_embd, E, d_tok, first ? nullptr : e->mhg, e->mpend, nullptr, d_seq, e->mtp_enorm,
+                    e->mtp_hnorm, e->eps, e->mcat, n, st);
+            return 0;
+        });
+        quant(e->mcat, nullptr, n, 2 * E, nullptr);
+        gemm(e->mtp_eh, n, E, 2 * E);
+        resid(e->mx, n, e->mtp.attn_norm, true, false);
+        block(e->mtp, e->L, e->mx, n, S, al, d_seq, d_pos);
+        resid(e->mx, n, nullptr, false);
+        quant(e->mx, nullptr, n, E, e->mtp_hdnorm, e->mhg);
+        head_logits(n);
+        rc |= e->launch(SNX_K_OTHER, (double) n * e->V * 4, [&] {
+            argmax_rows(e->logits, e->V, n, e->d_ban, 0, nullptr, d_gout, nullptr, st);
+            return 0;
+        });
+    }
+};
+
+// the row sources of the guess head's fill (sn_state.inc.h:292): the row before in the step (same slot, position
+// before), else the slot's kept state, none at position 0; and each run's last row kept as its slot's state
+void head_sources(const sn_engine* e, int R, const int32_t* seq, const int32_t* pos, std::vector<int32_t>& src,
+                  std::vector<int32_t>& keep) {
+    (void) e;
+    src.resize(R);
+    keep.clear();
+    for (int r = 0; r < R; ++r) {
+        src[r] = r > 0 && seq[r] == seq[r - 1] && pos[r] == pos[r - 1] + 1 ? r - 1 : pos[r] == 0 ? -2 : -1;
+        if (r + 1 == R || !(seq[r + 1] == seq[r] && pos[r + 1] == pos[r] + 1)) {
+            keep.push_back(seq[r]);
+            keep.push_back(r);
+        }
+    }
+}
+
+// the runs of the last step, for sn_clear's cut of the guess head's state
+void note_runs(sn_engine* e, int R, const int32_t* seq, const int32_t* pos) {
+    for (int r = 0; r < R;) {
+        int n = 1;
+        while (r + n < R && seq[r + n] == seq[r] && pos[r + n] == pos[r] + n) ++n;
+        e->run_row[seq[r]] = r;
+        e->run_pos[seq[r]] = pos[r];
+        e->run_n[seq[r]] = n;
+        r += n;
+    }
+}
+
+// waits for the step; the GPU time and profiling records
+int finish(sn_engine* e, int rc, char* err, int err_len) {
+    SN_HIP_TRY(hipEventRecord(e->ev1, e->st), -1);
+    SN_HIP_TRY(hipStreamSynchronize(e->st), -1);
     if (rc != 0) {
         sn_set_err(err, err_len, "a kernel launch was refused (workspace or shape)");
         return -1;
@@ -615,10 +778,218 @@ extern "C" int sn_step(sn_engine* e, int R, const int32_t* tok, const int32_t* s
         e->prof_bytes[pr.kind] += pr.bytes;
         e->prof_n[pr.kind] += 1;
     }
+    return 0;
+}
+
+bool rows_bad(const sn_engine* e, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos) {
+    for (int r = 0; r < R; ++r)
+        if (seq[r] < 0 || seq[r] >= e->slots || pos[r] < 0 || pos[r] >= e->ctx || tok[r] < 0 || tok[r] >= e->V)
+            return true;
+    return false;
+}
+
+}  // namespace
+
+extern "C" int sn_step(sn_engine* e, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos, int n_write,
+                       int n_fast, int n_out, const int32_t* out_rows, int32_t* out_tok, int chain, char* err,
+                       int err_len) {
+    (void) chain;  // a chained step is run as an ordinary step: the same tokens (sn.h:36-38)
+    if (step_shape_bad(e, R, n_write, n_fast, n_out)) {
+        sn_set_err(err, err_len, "bad step shape");
+        return -1;
+    }
+    if (rows_bad(e, R, tok, seq, pos)) {
+        sn_set_err(err, err_len, "a row is out of range (slot, position or token)");
+        return -1;
+    }
+    for (int j = 0; j < n_out; ++j)
+        if (out_rows[j] < 0 || out_rows[j] >= R) {
+            sn_set_err(err, err_len, "an output row is outside the step");
+            return -1;
+        }
+    if (take_pages(e, R, seq, pos) != 0) {
+        sn_set_err(err, err_len, "out of cache pages");
+        return -2;
+    }
+    const bool fill = e->has_nextn && e->guess_on;
+
+    // ---- the step's rows, attention work list and page table into one staging copy
+    Stage S{e};
+    const size_t o_tok = S.put(tok, (size_t) R * 4), o_seq = S.put(seq, (size_t) R * 4), o_pos = S.put(pos, (size_t) R * 4);
+    const size_t o_out = S.put(out_rows, (size_t) n_out * 4);
+    std::vector<uint8_t> skip(n_out + 1, 0);
+    for (int j = 0; j < n_out; ++j) skip[j] = e->no_end[seq[out_rows[j]]];
+    const size_t o_skip = S.put(skip);
+    const AttnList al = attn_list(e, S, R, seq, pos);
+    std::vector<int32_t> src, keep;
+    size_t o_src = 0, o_keep = 0;
+    if (fill) {
+        head_sources(e, R, seq, pos, src, keep);
+        o_src = S.put(src);
+        o_keep = S.put(keep);
+    }
+    e->prof_recs.clear();
+    if (stage_copy(e, S) != 0) {
+        sn_set_err(err, err_len, "step staging failed");
+        return -1;
+    }
+    const int32_t* d_tok = S.dev<const int32_t>(o_tok);
+    const int32_t* d_seq = S.dev<const int32_t>(o_seq);
+    const int32_t* d_pos = S.dev<const int32_t>(o_pos);
+
+    Dev d{e, e->st};
+    d.model(R, d_tok, d_seq, d_pos, S, al);
+    if (fill && d.rc == 0)
+        d.head_fill(R, d_tok, d_seq, d_pos, S.dev<const int32_t>(o_src), (int) keep.size() / 2, S.dev<const int32_t>(o_keep));
+    if (n_out > 0 && d.rc == 0) {
+        d.outputs(e->x, n_out, S.dev<const int32_t>(o_out), S.dev<const uint8_t>(o_skip));
+        SN_HIP_TRY(hipMemcpyAsync(e->h_otok, e->d_otok, (size_t) n_out * 4, hipMemcpyDeviceToHost, e->st), -1);
+        if (e->want_probs)
+            SN_HIP_TRY(hipMemcpyAsync(e->h_rec, e->d_rec, (size_t) n_out * 32, hipMemcpyDeviceToHost, e->st), -1);
+    }
+    if (finish(e, d.rc, err, err_len) != 0) return -1;
+    if (fill) note_runs(e, R, seq, pos);
     if (n_out > 0) memcpy(out_tok, e->h_otok, (size_t) n_out * 4);
     e->last_n_out = n_out;
     e->last_pn = e->want_probs ? n_out : 0;
     if (e->want_probs) e->last_probs.assign(e->h_rec, e->h_rec + (size_t) n_out * 8);
+    return 0;
+}
+
+// k guesses of one sequence (sn_guess, sn_cache.inc.h:357-388): k head rows, each fed the guess before it on the GPU
+extern "C" int sn_guess(sn_engine* e, int seq, int32_t tok, int pos, int k, int32_t* out_tok, char* err, int err_len) {
+    if (!e->has_nextn || !e->guess_on) {
+        sn_set_err(err, err_len, "sn_guess: no guess head, or guessing is off (sn_guess_on)");
+        return -1;
+    }
+    if (seq < 0 || seq >= e->slots || pos < 0 || k < 1 || k > 4 || pos + k > e->ctx || tok < 0 || tok >= e->V) {
+        sn_set_err(err, err_len, "sn_guess: slot, position, token or count out of range");
+        return -1;
+    }
+    std::vector<int32_t> sq(k, seq), ps(k);
+    for (int j = 0; j < k; ++j) ps[j] = pos + j;
+    if (take_pages(e, k, sq.data(), ps.data()) != 0) {
+        sn_set_err(err, err_len, "out of cache pages");
+        return -2;
+    }
+    Stage S{e};
+    const size_t o_tok = S.put(&tok, 4), o_seq = S.put(&seq, 4), o_pos = S.put(ps);
+    std::vector<AttnList> al;
+    for (int j = 0; j < k; ++j) al.push_back(attn_list(e, S, 1, &seq, &ps[j]));
+    e->prof_recs.clear();
+    if (stage_copy(e, S) != 0) {
+        sn_set_err(err, err_len, "sn_guess: staging failed");
+        return -1;
+    }
+    Dev d{e, e->st};
+    for (int j = 0; j < k && d.rc == 0; ++j)
+        d.head_rows(1, j ? e->d_gtok + (j - 1) * e->slots : S.dev<const int32_t>(o_tok), S.dev<const int32_t>(o_seq),
+                    S.dev<const int32_t>(o_pos) + j, j == 0, S, al[j], e->d_gtok + j * e->slots);
+    for (int j = 0; j < k; ++j)
+        SN_HIP_TRY(hipMemcpyAsync(e->h_otok + j, e->d_gtok + j * e->slots, 4, hipMemcpyDeviceToHost, e->st), -1);
+    if (finish(e, d.rc, err, err_len) != 0) return -1;
+    memcpy(out_tok, e->h_otok, (size_t) k * 4);
+    return 0;
+}
+
+// The fused draft-verify step (sn_ext.h): drafts, verify rows, acceptance and the cut, in one submission.
+extern "C" int snx_spec_step(sn_engine* e, int n, const int32_t* seq, const int32_t* last, const int32_t* pos, int k,
+                             const uint8_t* force, int32_t* out_n, int32_t* out_tok, char* err, int err_len) {
+    if (!e->has_nextn || !e->guess_on) {
+        sn_set_err(err, err_len, "snx_spec_step: no guess head, or guessing is off (sn_guess_on)");
+        return -1;
+    }
+    const int R = n * (k + 1);
+    if (n < 1 || n > e->slots || k < 1 || k > 4 || R > e->max_rows || R > e->max_out) {
+        sn_set_err(err, err_len, "snx_spec_step: bad sequence count or draft length");
+        return -1;
+    }
+    std::vector<int32_t> vtok(R), vseq(R), vpos(R), rows(R), hpos((size_t) k * n);
+    for (int s = 0; s < n; ++s) {
+        if (seq[s] < 0 || seq[s] >= e->slots || pos[s] < 0 || pos[s] + k >= e->ctx || last[s] < 0 || last[s] >= e->V) {
+            sn_set_err(err, err_len, "snx_spec_step: a sequence is out of range (slot, position or token)");
+            return -1;
+        }
+        for (int t = 0; t < s; ++t)
+            if (seq[t] == seq[s]) {
+                sn_set_err(err, err_len, "snx_spec_step: a slot appears twice");
+                return -1;
+            }
+        for (int i = 0; i <= k; ++i) {
+            const int r = s * (k + 1) + i;
+            vtok[r] = i == 0 ? last[s] : 0;  // the drafts are filled in on the GPU
+            vseq[r] = seq[s];
+            vpos[r] = pos[s] + i;
+            rows[r] = r;
+        }
+        for (int j = 0; j < k; ++j) hpos[(size_t) j * n + s] = pos[s] + j;
+    }
+    if (take_pages(e, R, vseq.data(), vpos.data()) != 0) {
+        sn_set_err(err, err_len, "out of cache pages");
+        return -2;
+    }
+    Stage S{e};
+    const size_t o_vtok = S.put(vtok), o_vseq = S.put(vseq), o_vpos = S.put(vpos), o_rows = S.put(rows);
+    std::vector<uint8_t> skip(R + 1, 0), frc(R + 1, 0);
+    for (int r = 0; r < R; ++r) skip[r] = e->no_end[vseq[r]];
+    if (force)
+        for (int s = 0; s < n; ++s)
+            for (int i = 0; i < k; ++i) frc[s * (k + 1) + i] = force[s * k + i] != 0;
+    const size_t o_skip = S.put(skip), o_force = S.put(frc);
+    const size_t o_last = S.put(last, (size_t) n * 4), o_hseq = S.put(seq, (size_t) n * 4), o_hpos = S.put(hpos);
+    std::vector<AttnList> hal;
+    for (int j = 0; j < k; ++j) hal.push_back(attn_list(e, S, n, seq, &hpos[(size_t) j * n]));
+    const AttnList al = attn_list(e, S, R, vseq.data(), vpos.data());
+    std::vector<int32_t> src, keep;
+    head_sources(e, R, vseq.data(), vpos.data(), src, keep);
+    const size_t o_src = S.put(src);
+    // device scratch in the staging buffer: draft checks, results, kept rows, accepted counts
+    std::vector<int32_t> zeros((size_t) R + 2 * n + R + 2 * n + n, 0);
+    const size_t o_ftok = S.put(zeros.data(), (size_t) R * 4), o_outn = S.put(zeros.data(), (size_t) n * 4),
+                 o_outt = S.put(zeros.data(), (size_t) R * 4), o_keep = S.put(zeros.data(), (size_t) 2 * n * 4),
+                 o_acc = S.put(zeros.data(), (size_t) n * 4);
+    e->prof_recs.clear();
+    if (stage_copy(e, S) != 0) {
+        sn_set_err(err, err_len, "snx_spec_step: staging failed");
+        return -1;
+    }
+    hipStream_t st = e->st;
+    int32_t* d_vtok = S.dev<int32_t>(o_vtok);
+    const int32_t* d_vseq = S.dev<const int32_t>(o_vseq);
+    const int32_t* d_vpos = S.dev<const int32_t>(o_vpos);
+    int32_t* d_ftok = S.dev<int32_t>(o_ftok);
+    int32_t* d_outn = S.dev<int32_t>(o_outn);
+    int32_t* d_outt = S.dev<int32_t>(o_outt);
+    int32_t* d_keep = S.dev<int32_t>(o_keep);
+    int32_t* d_acc = S.dev<int32_t>(o_acc);
+    Dev d{e, st};
+    // drafts: k rounds of n head rows (one a sequence), each round fed the guesses before it
+    for (int j = 0; j < k && d.rc == 0; ++j)
+        d.head_rows(n, j ? e->d_gtok + (j - 1) * e->slots : S.dev<const int32_t>(o_last), S.dev<const int32_t>(o_hseq),
+                    S.dev<const int32_t>(o_hpos) + (size_t) j * n, j == 0, S, hal[j], e->d_gtok + j * e->slots);
+    // verify rows [last, d1 .. dk] of every sequence through the model; the head's cells of those rows
+    spec_rows(n, k, e->slots, e->d_gtok, d_vtok, d_ftok, st);
+    d.model(R, d_vtok, d_vseq, d_vpos, S, al);
+    if (d.rc == 0) d.head_fill(R, d_vtok, d_vseq, d_vpos, S.dev<const int32_t>(o_src), 0, nullptr);
+    if (d.rc == 0)
+        d.outputs(e->x, R, S.dev<const int32_t>(o_rows), S.dev<const uint8_t>(o_skip),
+                  force ? S.dev<const uint8_t>(o_force) : nullptr, d_ftok);
+    // acceptance, the refused rows' cells cut in every layer, the head's state at the last kept row
+    accept_rows(n, k, e->slots, e->d_gtok, e->d_otok, d_vseq, d_outn, d_outt, d_keep, d_acc, st);
+    cut_cells(e->kbase, e->vbase, e->layer_halves, e->CL, e->KVH, e->page_cells, e->d_pt, e->max_pages, n, k, d_vseq,
+              d_vpos, d_acc, st);
+    rows_keep(e->mhn, d_keep, n, e->E, e->mpend, st);
+    SN_HIP_TRY(hipMemcpyAsync(e->h_otok, d_outt, (size_t) R * 4, hipMemcpyDeviceToHost, st), -1);
+    SN_HIP_TRY(hipMemcpyAsync(e->h_rec, d_outn, (size_t) n * 4, hipMemcpyDeviceToHost, st), -1);
+    if (finish(e, d.rc, err, err_len) != 0) return -1;
+    memcpy(out_tok, e->h_otok, (size_t) R * 4);
+    memcpy(out_n, e->h_rec, (size_t) n * 4);
+    for (int s = 0; s < n; ++s) {  // the run each sequence keeps (sn_clear's cut of the head state)
+        e->run_row[seq[s]] = s * (k + 1);
+        e->run_pos[seq[s]] = pos[s];
+        e->run_n[seq[s]] = out_n[s];
+    }
+    e->last_n_out = 0;  // the verify rows' logits are not kept for sn_logits
     return 0;
 }
 
@@ -717,7 +1088,7 @@ extern "C" int sn_copy(sn_engine* e, int from, int to, int n, char* err, int err
             return -2;
         }
         tt[c] = np;
-        if (tf[c] >= 0) kv_page_op(e->kbase, e->vbase, e->layer_halves, e->L, e->KVH, pc, tf[c], np, 0, n % pc, e->st);
+        if (tf[c] >= 0) kv_page_op(e->kbase, e->vbase, e->layer_halves, e->CL, e->KVH, pc, tf[c], np, 0, n % pc, e->st);
     }
     e->pt_dirty = true;
     SN_HIP_TRY(hipStreamSynchronize(e->st), -1);
@@ -731,6 +1102,18 @@ extern "C" int sn_clear(sn_engine* e, int slot, int from, int to, char* err, int
     }
     const int pc = e->page_cells;
     int32_t* t = e->seq_pages(slot);
+    if (e->has_nextn && e->guess_on) {
+        // the guess head's state of the slot: the hidden state of its last kept cell when the last step's run holds
+        // it (sn_seq.inc.h:72), none at 0
+        const size_t EB = (size_t) e->E * 4;
+        if (from == 0) {
+            SN_HIP_TRY(hipMemsetAsync(e->mpend + (size_t) slot * e->E, 0, EB, e->st), -1);
+        } else if (e->run_row[slot] >= 0 && from - 1 >= e->run_pos[slot] && from - 1 < e->run_pos[slot] + e->run_n[slot]) {
+            const int row = e->run_row[slot] + (from - 1 - e->run_pos[slot]);
+            SN_HIP_TRY(hipMemcpyAsync(e->mpend + (size_t) slot * e->E, e->mhn + (size_t) row * e->E, EB,
+                                      hipMemcpyDeviceToDevice, e->st), -1);
+        }
+    }
     const int c1 = (from + pc - 1) / pc;  // every chunk from the first wholly at or past `from` goes
     for (int c = c1; c < e->max_pages; ++c) {
         page_drop(e, t[c]);
@@ -747,9 +1130,9 @@ extern "C" int sn_clear(sn_engine* e, int slot, int from, int to, char* err, int
             }
             --e->ref[p];
             t[c] = np;
-            kv_page_op(e->kbase, e->vbase, e->layer_halves, e->L, e->KVH, pc, p, np, 0, from % pc, e->st);
+            kv_page_op(e->kbase, e->vbase, e->layer_halves, e->CL, e->KVH, pc, p, np, 0, from % pc, e->st);
         } else {
-            kv_page_op(e->kbase, e->vbase, e->layer_halves, e->L, e->KVH, pc, -1, p, from % pc,
+            kv_page_op(e->kbase, e->vbase, e->layer_halves, e->CL, e->KVH, pc, -1, p, from % pc,
                        std::min(pc, to - c * pc), e->st);
         }
     }
@@ -757,7 +1140,7 @@ extern "C" int sn_clear(sn_engine* e, int slot, int from, int to, char* err, int
     return 0;
 }
 
-extern "C" size_t sn_kv_bytes(const sn_engine* e, int n) { return (size_t) e->L * 2 * n * e->KD * 2; }
+extern "C" size_t sn_kv_bytes(const sn_engine* e, int n) { return (size_t) e->CL * 2 * n * e->KD * 2; }
 
 static int kv_xfer(sn_engine* e, int slot, int n, void* host, int save, char* err, int err_len) {
     if (!slot_ok(e, slot, 0, n)) {
@@ -790,7 +1173,7 @@ static int kv_xfer(sn_engine* e, int slot, int n, void* host, int save, char* er
     }
     hipMemcpy(dp, t, (size_t) np * 4, hipMemcpyHostToDevice);
     if (!save) hipMemcpy(stg, host, bytes, hipMemcpyHostToDevice);
-    kv_stage(e->kbase, e->vbase, e->layer_halves, e->L, e->KVH, e->page_cells, dp, n, stg, save, e->st);
+    kv_stage(e->kbase, e->vbase, e->layer_halves, e->CL, e->KVH, e->page_cells, dp, n, stg, save, e->st);
     hipStreamSynchronize(e->st);
     if (save) hipMemcpy(host, stg, bytes, hipMemcpyDeviceToHost);
     const hipError_t ke = hipGetLastError();
@@ -821,7 +1204,7 @@ extern "C" int snx_fill_kv(sn_engine* e, int slot, int n, uint64_t seed, char* e
     int32_t* dp = nullptr;
     SN_HIP_TRY(hipMalloc(&dp, (size_t) np * 4), -1);
     hipMemcpy(dp, t, (size_t) np * 4, hipMemcpyHostToDevice);
-    kv_fill_normal(e->kbase, e->vbase, e->layer_halves, e->L, e->KVH, e->page_cells, dp, n,
+    kv_fill_normal(e->kbase, e->vbase, e->layer_halves, e->CL, e->KVH, e->page_cells, dp, n,
                    seed ^ (0x9E3779B97F4A7C15ull * (uint64_t) (slot + 1)), e->st);
     hipStreamSynchronize(e->st);
     const hipError_t ke = hipGetLastError();
@@ -849,7 +1232,7 @@ extern "C" const char* sn_arch(const sn_engine* e) { return e->arch.c_str(); }
 extern "C" int sn_n_embd(const sn_engine* e) { return e->E; }
 extern "C" int sn_pages_total(const sn_engine* e) { return e->n_pages; }
 extern "C" int sn_pages_free(const sn_engine* e) { return (int) e->freel.size(); }
-extern "C" size_t sn_page_bytes(const sn_engine* e) { return (size_t) e->page_cells * e->KD * 2 * 2 * e->L; }
+extern "C" size_t sn_page_bytes(const sn_engine* e) { return (size_t) e->page_cells * e->KD * 2 * 2 * e->CL; }
 extern "C" int sn_seq_pages(const sn_engine* e, int seq, int* own) {
     if (seq < 0 || seq >= e->slots) return 0;
     int n = 0, o = 0;
@@ -968,18 +1351,10 @@ extern "C" float sn_embd_norm(sn_engine* e) {
     return 0.0f;
 }
 
-// guess head: declared here, served once the nextn layer is loaded (see sn_guess_head)
-extern "C" int sn_guess_head(const sn_engine* e) {
-    (void) e;
-    return 0;
-}
+// the guess head (sn_cache.inc.h:288-298): there when the GGUF carries a nextn block the engine loaded
+extern "C" int sn_guess_head(const sn_engine* e) { return e->has_nextn ? 1 : 0; }
 extern "C" int sn_guess_on(sn_engine* e, int on) {
-    (void) on;
-    e->guess_on = 0;
-    return 0;
-}
-extern "C" int sn_guess(sn_engine* e, int seq, int32_t tok, int pos, int k, int32_t* out_tok, char* err, int err_len) {
-    (void) e; (void) seq; (void) tok; (void) pos; (void) k; (void) out_tok;
-    sn_set_err(err, err_len, "sn_guess: no guess head, or guessing is off (sn_guess_on)");
-    return -1;
+    if (!e->has_nextn) return 0;
+    e->guess_on = on != 0;
+    return e->guess_on;
 }

@@ -279,3 +279,134 @@ void kv_fill_normal(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L
         hipLaunchKernelGGL(k_kv_fill, dim3(n, L, 2), dim3(256), 0, st, kbase, vbase, layer_halves, KVH, page_cells, pages,
                            n, seed);
 }
+
+// ---- the guess head (MTP) and the fused draft-verify step ----------------------------------------------------------
+
+__device__ __forceinline__ float row_sumsq256(const float* x, int n, float* red) {
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) s += x[i] * x[i];
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// The head's input rows [enorm(embed(tok)); hnorm(h)] (sn_cache.inc.h:357-363, sn_state.inc.h:294-305), h the row's
+// hidden state before it: src NULL: hrows row r when hrows is given, else the slot's kept state pend[seq]; with src:
+// src[r] >= 0 row src[r] of hrows, -1 pend[seq[r]], -2 none (zeros: a sequence's first cell).
+__global__ __launch_bounds__(256) void k_mtp_cat(const float* __restrict__ table, int E, const int32_t* __restrict__ tok,
+                                                 const float* __restrict__ hrows, const float* __restrict__ pend,
+                                                 const int32_t* __restrict__ src, const int32_t* __restrict__ seq,
+                                                 const float* __restrict__ enorm, const float* __restrict__ hnorm,
+                                                 float eps, float* __restrict__ cat) {
+    __shared__ float red[4];
+    const int r = blockIdx.x;
+    const float* em = table + (size_t) tok[r] * E;
+    const int s = src ? src[r] : (hrows ? r : -1);
+    const float* h = s >= 0 ? hrows + (size_t) s * E : s == -1 ? pend + (size_t) seq[r] * E : nullptr;
+    float* y = cat + (size_t) r * 2 * E;
+    const float se = 1.0f / sqrtf(row_sumsq256(em, E, red) / (float) E + eps);
+    for (int i = threadIdx.x; i < E; i += 256) y[i] = (em[i] * se) * enorm[i];
+    if (!h) {
+        for (int i = threadIdx.x; i < E; i += 256) y[E + i] = 0.0f;
+        return;
+    }
+    const float sh = 1.0f / sqrtf(row_sumsq256(h, E, red) / (float) E + eps);
+    for (int i = threadIdx.x; i < E; i += 256) y[E + i] = (h[i] * sh) * hnorm[i];
+}
+
+void mtp_cat(const float* table, int E, const int32_t* tok, const float* hrows, const float* pend, const int32_t* src,
+             const int32_t* seq, const float* enorm, const float* hnorm, float eps, float* cat, int R, hipStream_t st) {
+    if (R > 0)
+        hipLaunchKernelGGL(k_mtp_cat, dim3(R), dim3(256), 0, st, table, E, tok, hrows, pend, src, seq, enorm, hnorm, eps,
+                           cat);
+}
+
+// keep[j] = (slot, row): dst row `slot` = src row `row` (mtp_keep: a slot's last hidden state of the step)
+__global__ void k_rows_keep(const float* __restrict__ src, const int32_t* __restrict__ keep, int E,
+                            float* __restrict__ dst) {
+    const int slot = keep[2 * blockIdx.x], row = keep[2 * blockIdx.x + 1];
+    if (slot < 0) return;
+    for (int i = threadIdx.x; i < E; i += 256) dst[(size_t) slot * E + i] = src[(size_t) row * E + i];
+}
+
+void rows_keep(const float* src, const int32_t* keep, int n, int E, float* dst, hipStream_t st) {
+    if (n > 0) hipLaunchKernelGGL(k_rows_keep, dim3(n), dim3(256), 0, st, src, keep, E, dst);
+}
+
+// Verify rows (sequence s, row i = 0 .. k at position pos_s + i) from the drafts gtok[j][s] (round j's guess of s):
+// row i > 0 takes draft i - 1; ftok[row] = the draft the row's argmax is checked against (row i < k: draft i).
+__global__ void k_spec_rows(int n, int k, int slots, const int32_t* __restrict__ gtok, int32_t* __restrict__ vtok,
+                            int32_t* __restrict__ ftok) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n * (k + 1)) return;
+    const int s = t / (k + 1), i = t % (k + 1);
+    if (i > 0) vtok[t] = gtok[(i - 1) * slots + s];
+    ftok[t] = i < k ? gtok[i * slots + s] : 0;
+}
+
+// rows with force[r]: the draft ftok[r] becomes the row's greedy token (a seeded acceptance rate for benchmarks)
+__global__ void k_force(float* __restrict__ logits, int V, int R, const uint8_t* __restrict__ force,
+                        const int32_t* __restrict__ ftok) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r < R && force[r]) logits[(size_t) r * V + ftok[r]] = 3.0e38f;
+}
+
+// Greedy acceptance (next_engine/take.rs:339-357) per sequence: a = the leading drafts equal to their row's argmax;
+// the sequence takes drafts 1 .. a and then row a's argmax. out_n[s] = a + 1, out_tok[s][0 .. a]; keep[s] = (slot,
+// row of the last kept cell) for the guess head's state; acc[s] = a.
+__global__ void k_accept(int n, int k, int slots, const int32_t* __restrict__ gtok, const int32_t* __restrict__ otok,
+                         const int32_t* __restrict__ seq, int32_t* __restrict__ out_n, int32_t* __restrict__ out_tok,
+                         int32_t* __restrict__ keep, int32_t* __restrict__ acc) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    const int r0 = s * (k + 1);
+    int a = 0;
+    while (a < k && gtok[a * slots + s] == otok[r0 + a]) ++a;
+    for (int i = 0; i < a; ++i) out_tok[s * (k + 1) + i] = gtok[i * slots + s];
+    out_tok[s * (k + 1) + a] = otok[r0 + a];
+    for (int i = a + 1; i <= k; ++i) out_tok[s * (k + 1) + i] = -1;
+    out_n[s] = a + 1;
+    keep[2 * s] = seq[r0];
+    keep[2 * s + 1] = r0 + a;
+    acc[s] = a;
+}
+
+// the cells of the refused rows (positions pos_s + acc_s + 1 .. pos_s + k) zeroed in every cache layer
+__global__ void k_cut_cells(uint16_t* __restrict__ kbase, uint16_t* __restrict__ vbase, size_t layer_halves, int KVH,
+                            int page_cells, const int32_t* __restrict__ pt, int max_pages, int k,
+                            const int32_t* __restrict__ seq, const int32_t* __restrict__ pos,
+                            const int32_t* __restrict__ acc) {
+    const int s = blockIdx.x, i = blockIdx.y + 1, layer = blockIdx.z;
+    if (i <= acc[s]) return;
+    const int r0 = s * (k + 1), c = pos[r0] + i;
+    const int page = pt[(size_t) seq[r0] * max_pages + c / page_cells];
+    if (page < 0) return;
+    const size_t base = (size_t) layer * layer_halves;
+    for (int t = threadIdx.x; t < KVH * 128; t += 256) {
+        const int h = t / 128, d = t % 128;
+        const size_t at = base + (((size_t) page * KVH + h) * page_cells + c % page_cells) * 128 + d;
+        kbase[at] = 0;
+        vbase[at] = 0;
+    }
+}
+
+void spec_rows(int n, int k, int slots, const int32_t* gtok, int32_t* vtok, int32_t* ftok, hipStream_t st) {
+    const int R = n * (k + 1);
+    hipLaunchKernelGGL(k_spec_rows, dim3((R + 255) / 256), dim3(256), 0, st, n, k, slots, gtok, vtok, ftok);
+}
+void force_rows(float* logits, int V, int R, const uint8_t* force, const int32_t* ftok, hipStream_t st) {
+    hipLaunchKernelGGL(k_force, dim3((R + 255) / 256), dim3(256), 0, st, logits, V, R, force, ftok);
+}
+void accept_rows(int n, int k, int slots, const int32_t* gtok, const int32_t* otok, const int32_t* seq, int32_t* out_n,
+                 int32_t* out_tok, int32_t* keep, int32_t* acc, hipStream_t st) {
+    hipLaunchKernelGGL(k_accept, dim3((n + 63) / 64), dim3(64), 0, st, n, k, slots, gtok, otok, seq, out_n, out_tok, keep,
+                       acc);
+}
+void cut_cells(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int CL, int KVH, int page_cells, const int32_t* pt,
+               int max_pages, int n, int k, const int32_t* seq, const int32_t* pos, const int32_t* acc, hipStream_t st) {
+    if (k > 0)
+        hipLaunchKernelGGL(k_cut_cells, dim3(n, k, CL), dim3(256), 0, st, kbase, vbase, layer_halves, KVH, page_cells, pt,
+                           max_pages, k, seq, pos, acc);
+}

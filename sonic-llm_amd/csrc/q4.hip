@@ -119,13 +119,14 @@ __device__ __forceinline__ void q8_store(const float* v, int g, uint8_t* frag, _
 __device__ __forceinline__ float4 ld4(const float* p) { return *(const float4*) p; }
 __device__ __forceinline__ float4 add4(float4 a, float4 b) { return (float4){a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w}; }
 
-// Residual rows: x[m] += the k-slice sums of a matmul (part[ks][M][K], slices added in order), written back; then,
+// Residual rows: x[m] += the k-slice sums of a matmul (part[ks][M][K], slices added in order; add 0: x[m] = the
+// sums), written back; then,
 // when xa is given, the RMSNorm (weight nw) and Q8_0 operand of the new row. One workgroup per row (the norm needs the
 // whole row before any value is quantized); lane t covers blocks t / 4 + 64 i.
 template <int IT>
 __global__ __launch_bounds__(256) void k_resid_quant(float* __restrict__ X, const float* __restrict__ part, int ks,
                                                      int M, int K, const float* __restrict__ nw, float eps,
-                                                     uint8_t* __restrict__ xa) {
+                                                     uint8_t* __restrict__ xa, int add) {
     __shared__ float red[4];
     const int m = blockIdx.x, t = threadIdx.x, g = t & 3;
     const int nb = K / 32, nbp = xa_nbp(K);
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(256) void k_resid_quant(float* __restrict__ X, cons
         const int b = t / 4 + 64 * it;
         if (b >= nb) continue;
         const int e0 = 32 * b + 4 * g, e1 = e0 + 16;
-        float4 lo = ld4(x + e0), hi = ld4(x + e1);
+        float4 lo = add ? ld4(x + e0) : (float4){0.f, 0.f, 0.f, 0.f}, hi = add ? ld4(x + e1) : (float4){0.f, 0.f, 0.f, 0.f};
         float4 slo = ld4(part + (size_t) m * K + e0), shi = ld4(part + (size_t) m * K + e1);
         for (int k = 1; k < ks; ++k) {
             slo = add4(slo, ld4(part + ((size_t) k * M + m) * K + e0));
@@ -404,13 +405,14 @@ void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int 
 }
 
 int resid_quant(float* x, const float* part, int ks, int M, int K, const float* nw, float eps, uint8_t* xa,
-                hipStream_t st) {
+                hipStream_t st, bool add) {
     if (M <= 0) return 0;
     const int it = (xa_nbp(K) + 63) / 64;
     if (K % 32 || it > 4) return -1;
-    if (it == 1) hipLaunchKernelGGL((k_resid_quant<1>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa);
-    else if (it == 2) hipLaunchKernelGGL((k_resid_quant<2>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa);
-    else hipLaunchKernelGGL((k_resid_quant<4>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa);
+    const int ad = add ? 1 : 0;
+    if (it == 1) hipLaunchKernelGGL((k_resid_quant<1>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad);
+    else if (it == 2) hipLaunchKernelGGL((k_resid_quant<2>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad);
+    else hipLaunchKernelGGL((k_resid_quant<4>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad);
     return 0;
 }
 

@@ -34,10 +34,10 @@ void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const
                float* xn, int ldn, hipStream_t st);
 // Raw matmul into the workspace, then the slices added in order with an epilogue into y (ldy apart): store, add, or
 // SwiGLU of the stripe-interleaved gate/up pair (output column 16p + n = silu(column 32p + n) * column 32p + 16 + n).
-// x[m] += the k-slice sums part[ks][M][K] (added in slice order); then, with xa, the Q8_0 operand of the new rows
-// (RMS-normed by nw when given). K <= 8192. 0, or -1 (shape).
+// x[m] += the k-slice sums part[ks][M][K] (added in slice order; add false: x[m] = the sums); then, with xa, the Q8_0
+// operand of the new rows (RMS-normed by nw when given). K <= 8192. 0, or -1 (shape).
 int resid_quant(float* x, const float* part, int ks, int M, int K, const float* nw, float eps, uint8_t* xa,
-                hipStream_t st);
+                hipStream_t st, bool add = true);
 // h (optional) and the Q8_0 operand of silu(gate) * up from a stripe-interleaved gate/up matmul's k-slice sums
 // part[ks][M][2F].
 void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st);
@@ -101,3 +101,18 @@ void kv_fill_normal(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L
                     const int32_t* pages, int n, uint64_t seed, hipStream_t st);
 void argmax_rows(const float* logits, int V, int n, const int32_t* ban, int nban, const uint8_t* skip, int32_t* out,
                  float* rec, hipStream_t st);
+
+// ---- the guess head (MTP) and the fused draft-verify step
+// [enorm(embed(tok)); hnorm(h)] rows into cat [R][2E]; h: src NULL: hrows row r (hrows given) or pend[seq[r]];
+// src[r] >= 0: hrows row src[r], -1: pend[seq[r]], -2: zeros
+void mtp_cat(const float* table, int E, const int32_t* tok, const float* hrows, const float* pend, const int32_t* src,
+             const int32_t* seq, const float* enorm, const float* hnorm, float eps, float* cat, int R, hipStream_t st);
+// keep [n][2] = (slot, row): dst[slot] = src[row] (E floats); slot < 0 skips
+void rows_keep(const float* src, const int32_t* keep, int n, int E, float* dst, hipStream_t st);
+// verify rows of n sequences x (k + 1) from the drafts gtok [k][slots]: vtok rows i > 0, ftok (row i < k: draft i)
+void spec_rows(int n, int k, int slots, const int32_t* gtok, int32_t* vtok, int32_t* ftok, hipStream_t st);
+void force_rows(float* logits, int V, int R, const uint8_t* force, const int32_t* ftok, hipStream_t st);
+void accept_rows(int n, int k, int slots, const int32_t* gtok, const int32_t* otok, const int32_t* seq, int32_t* out_n,
+                 int32_t* out_tok, int32_t* keep, int32_t* acc, hipStream_t st);
+void cut_cells(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int CL, int KVH, int page_cells, const int32_t* pt,
+               int max_pages, int n, int k, const int32_t* seq, const int32_t* pos, const int32_t* acc, hipStream_t st);

@@ -113,6 +113,7 @@ EXT_API = [
     ("snx_prof_read", I, [P, I, C.POINTER(C.c_double), C.POINTER(I), C.POINTER(C.c_double)]),
     ("snx_fill_kv", I, [P, I, I, C.c_uint64, CH, I]),
     ("snx_debug_read", I, [P, I, P, C.c_size_t]),
+    ("snx_spec_step", I, [P, I, P, P, P, I, P, P, P, CH, I]),
 ]
 SYNTH_API = [
     ("snx_write_model", I, [CH, P, C.c_uint64, I, CH, I]),
@@ -263,6 +264,31 @@ class Engine:
 
     def fill_kv(self, slot, n, seed):
         call(self.L.snx_fill_kv, self.e, slot, n, seed)
+
+    # ---- the guess head (sn_guess_head / sn_guess_on / sn_guess) and the fused draft-verify step
+    def guess_head(self) -> bool:
+        return bool(self.L.sn_guess_head(self.e))
+
+    def guess_on(self, on: bool) -> bool:
+        return bool(self.L.sn_guess_on(self.e, int(on)))
+
+    def guess(self, seq, tok, pos, k) -> np.ndarray:
+        out = np.empty(k, np.int32)
+        call(self.L.sn_guess, self.e, int(seq), int(tok), int(pos), int(k), _p(out))
+        return out
+
+    def spec_step(self, seq, last, pos, k, force=None):
+        """snx_spec_step: per sequence (accepted + 1, tokens [k + 1] with -1 after the bonus)."""
+        seq = np.ascontiguousarray(seq, np.int32)
+        last = np.ascontiguousarray(last, np.int32)
+        pos = np.ascontiguousarray(pos, np.int32)
+        n = seq.size
+        fr = None if force is None else np.ascontiguousarray(force, np.uint8).reshape(n, k)
+        out_n = np.empty(n, np.int32)
+        out_tok = np.empty((n, k + 1), np.int32)
+        call(self.L.snx_spec_step, self.e, n, _p(seq), _p(last), _p(pos), int(k), _p(fr) if fr is not None else None,
+             _p(out_n), _p(out_tok))
+        return out_n, out_tok
 
     def prof(self, on: bool):
         self.L.snx_prof(self.e, int(on))
