@@ -34,7 +34,8 @@ def log(msg):
 def model_file(cfg_kw, seed, path=None):
     import sllm_next as S
     d = os.environ.get("SN_BENCH_DIR") or "/tmp"
-    path = path or os.path.join(d, f"sonic_qwen3_{cfg_kw['n_layer']}L_{cfg_kw['n_embd']}_{seed}.gguf")
+    tag = "_mtp" if cfg_kw.get("nextn") else ""
+    path = path or os.path.join(d, f"sonic_qwen3_{cfg_kw['n_layer']}L_{cfg_kw['n_embd']}{tag}_{seed}.gguf")
     done = path + ".done"
     if not (os.path.exists(path) and os.path.exists(done)):
         t = time.time()
@@ -82,6 +83,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--model", default=None, help="GGUF path (generated when missing)")
     ap.add_argument("--seed", type=int, default=42)
+    ap.add_argument("--config", default="decode", choices=("decode", "mtp"),
+                    help="decode: the headline (configs[2]); mtp: the fused draft-verify step (configs[3])")
+    ap.add_argument("--accept", type=float, default=0.6, help="mtp: the seeded share of drafts forced to match")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (sequences would shard "
@@ -93,6 +97,8 @@ def main():
 
     import sllm_next as S
 
+    if args.config == "mtp":
+        return bench_mtp(args)
     cfg = dict(S.QWEN3_4B)
     path = model_file(cfg, args.seed, args.model)
     B, ctx = args.seqs, args.ctx
@@ -167,6 +173,79 @@ def main():
         "roofline_gemm": roof("gemm") if "gemm" in kernels else None,
         "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_mtp(args):
+    """the fused draft-verify step (snx_spec_step) of the Qwen3-4B-arch model with one Q4_0 guess-head
+    block: 8 sequences at 4096 cells, k = 3 drafts each, verify rows [last, d1, d2, d3]; a seeded mask forces each draft
+    to equal its row's argmax with probability --accept (the rows still run in full). value = tokens kept per second."""
+    import numpy as np
+    import torch
+
+    import sllm_next as S
+
+    cfg = dict(S.QWEN3_4B, nextn=1)
+    path = model_file(cfg, args.seed, args.model)
+    B, ctx, k = 8, 4096, 3
+    total = ctx + (args.warmup + args.steps + args.prof_steps) * (k + 1) + 8
+    t = time.time()
+    eng = S.Engine(path, slots=B, ctx=total, max_rows=B * (k + 1))
+    assert eng.guess_head() and eng.guess_on(True)
+    for s in range(B):
+        eng.fill_kv(s, ctx, args.seed)
+    log(f"[bench] engine open + {B} x {ctx} cells in {time.time() - t:.1f}s")
+    rng = np.random.default_rng(args.seed)
+    seqs = np.arange(B, dtype=np.int32)
+    last = rng.integers(0, eng.V, B).astype(np.int32)
+    pos = np.full(B, ctx, np.int32)
+    kept = 0
+
+    def step():
+        nonlocal last, kept
+        force = (rng.random((B, k)) < args.accept).astype(np.uint8)
+        n, tok = eng.spec_step(seqs, last, pos, k, force=force)
+        last = tok[np.arange(B), n - 1].astype(np.int32)
+        pos[:] += n
+        kept += int(n.sum())
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    kept = 0
+    t0 = time.perf_counter()
+    gpu_ms = 0.0
+    for _ in range(args.steps):
+        step()
+        gpu_ms += eng.last_gpu_ms()
+    dt = time.perf_counter() - t0
+    toks = kept
+    log(f"[bench] {args.steps} spec steps: {dt * 1e3 / args.steps:.3f} ms/step, {toks / args.steps:.2f} tokens/step")
+    eng.prof(True)
+    for _ in range(args.prof_steps):
+        step()
+    prof = eng.prof_read()
+    eng.prof(False)
+    eng.close()
+    kernels = {}
+    for name, p in prof.items():
+        if p["launches"]:
+            gbs = p["bytes"] / (p["ms"] * 1e-3) / 1e9
+            kernels[name] = {"ms_per_step": round(p["ms"] / args.prof_steps, 4),
+                             "launches_per_step": p["launches"] / args.prof_steps,
+                             "GBps": round(gbs, 1), "frac": round(gbs * 1e9 / HBM_PEAK, 4)}
+    line = {
+        "metric": "MTP draft+verify tok/s, Qwen3-4B-arch Q4_0 + 1 Q4_0 guess-head block, 8 seqs x 4096, k=3",
+        "value": round(toks / dt, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "q4_0 x q8_0 -> f32 (fp16 MFMA); f16 KV, f32 softmax",
+        "data": f"synthetic: random-init weights (seeded), seeded N(0,1) fp16 context cells, seeded draft mask "
+                f"(p={args.accept})",
+        "config": {"workload": "fused MTP draft+verify step (BASELINE.json configs[3])", "seqs": B, "ctx": ctx,
+                   "drafts": k, "verify_rows": B * (k + 1), "tokens_per_step": round(toks / args.steps, 3),
+                   "gpu_ms_per_step": round(gpu_ms / args.steps, 4)},
+        "kernels": kernels,
     }
     print(json.dumps(line), flush=True)
 
