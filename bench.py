@@ -34,7 +34,7 @@ def log(msg):
 def model_file(cfg_kw, seed, path=None):
     import sllm_next as S
     d = os.environ.get("SN_BENCH_DIR") or "/tmp"
-    tag = "_mtp" if cfg_kw.get("nextn") else ""
+    tag = ("_mtp" if cfg_kw.get("nextn") else "") + (f"_moe{cfg_kw['n_expert']}" if cfg_kw.get("n_expert") else "")
     path = path or os.path.join(d, f"sonic_qwen3_{cfg_kw['n_layer']}L_{cfg_kw['n_embd']}{tag}_{seed}.gguf")
     done = path + ".done"
     if not (os.path.exists(path) and os.path.exists(done)):
@@ -83,8 +83,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--model", default=None, help="GGUF path (generated when missing)")
     ap.add_argument("--seed", type=int, default=42)
-    ap.add_argument("--config", default="decode", choices=("decode", "mtp"),
-                    help="decode: the headline (configs[2]); mtp: the fused draft-verify step (configs[3])")
+    ap.add_argument("--config", default="decode", choices=("decode", "mtp", "moe"),
+                    help="decode: the headline (configs[2]); mtp: the fused draft-verify step (configs[3]); "
+                         "moe: Qwen3-30B-A3B-arch batched decode (configs[4])")
     ap.add_argument("--accept", type=float, default=0.6, help="mtp: the seeded share of drafts forced to match")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -99,7 +100,8 @@ def main():
 
     if args.config == "mtp":
         return bench_mtp(args)
-    cfg = dict(S.QWEN3_4B)
+    moe = args.config == "moe"
+    cfg = dict(S.QWEN3_30B_A3B if moe else S.QWEN3_4B)
     path = model_file(cfg, args.seed, args.model)
     B, ctx = args.seqs, args.ctx
     total = ctx + args.warmup + args.steps + args.prof_steps + 1
@@ -155,19 +157,25 @@ def main():
 
     eng.close()
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not moe:
         t = time.time()
         cpu = cpu_baseline(path, B, ctx, args.seed)
         log(f"[bench] cpu baseline in {time.time() - t:.1f}s: {cpu['value']:.2f} tok/s")
+    metric = ("agg decode tok/s, Qwen3-30B-A3B-arch Q4_0 MoE x32 seqs" if moe else
+              "agg decode tok/s, Qwen3-4B-arch Q4_0 x32 seqs; Q4_0 GEMV % HBM peak")
+    workload = ("Qwen3-30B-A3B-arch Q4_0 MoE batched decode step (BASELINE.json configs[4])" if moe else
+                "Qwen3-4B-arch Q4_0 batched decode step (BASELINE.json configs[2])")
     line = {
-        "metric": "agg decode tok/s, Qwen3-4B-arch Q4_0 x32 seqs; Q4_0 GEMV % HBM peak",
+        "metric": metric,
         "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "q4_0 x q8_0 -> f32 (fp16 MFMA); f16 KV, f32 softmax",
         "data": "synthetic: random-init weights (seeded), random token ids, seeded N(0,1) fp16 context cells",
-        "config": {"workload": "Qwen3-4B-arch Q4_0 batched decode step (BASELINE.json configs[2])", "seqs": B,
+        "config": {"workload": workload, "seqs": B,
                    "ctx": ctx, "layers": cfg["n_layer"], "hidden": cfg["n_embd"], "heads": cfg["n_head"],
                    "kv_heads": cfg["n_head_kv"], "ffn": cfg["n_ff"], "vocab": cfg["n_vocab"], "page_cells": 64,
+                   **({"experts": cfg["n_expert"], "experts_used": cfg["n_expert_used"], "expert_ffn": cfg["n_ff_exp"]}
+                      if moe else {}),
                    "gpu_ms_per_step": round(gpu_ms / args.steps, 4)},
         "roofline": roof(dom),
         "roofline_gemm": roof("gemm") if "gemm" in kernels else None,

@@ -33,6 +33,9 @@ namespace {
 struct DevLayer {
     float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *ffn_norm = nullptr;
     uint8_t *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wd = nullptr;
+    // a MoE layer: fp32 router [NE][E]; per expert, gate/up stripes interleaved in pairs [2 FE][E] and down [E][FE]
+    float* router = nullptr;
+    uint8_t *egu = nullptr, *ed = nullptr;
 };
 
 }  // namespace
@@ -44,6 +47,11 @@ struct sn_engine {
     float eps = 1e-6f, rope_base = 1e6f, theta_scale = 1.0f;
     int slots = 0, ctx = 0, max_rows = 0, n_pages = 0, page_cells = 64, max_pages = 0, max_out = 0;
     bool has_nextn = false;
+    // qwen3moe: experts, experts a token uses, an expert's FFN width; the tile bound of a step's expert rows
+    int NE = 0, NEU = 0, FE = 0, moe_tiles = 0;
+    size_t egu_stride = 0, ed_stride = 0;
+    float *hn = nullptr, *rlog = nullptr, *mw = nullptr;  // normed rows, router logits, routing weights
+    int32_t *mid = nullptr, *prow = nullptr, *rsrc = nullptr, *gitems = nullptr, *gcount = nullptr;
 
     hipStream_t st = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -149,6 +157,16 @@ bool upload_q4(sn_engine* e, const GgufTensor* t, uint8_t* tmp, uint8_t* dst, in
     return true;
 }
 
+// a GGUF Q4_0 expert tensor (ne = [K, N, NE]) into per-expert stripes, expert x at dst + x * dst_stride
+bool upload_q4_experts(sn_engine* e, const GgufTensor* t, uint8_t* tmp, uint8_t* dst, int NE, int N, int K,
+                       size_t dst_stride, int sstride, int soff, char* err, int err_len) {
+    SN_HIP_TRY(hipMemcpyAsync(tmp, t->data, t->nbytes, hipMemcpyHostToDevice, e->st), false);
+    const size_t src_stride = (size_t) N * (K / 32) * 18;
+    for (int x = 0; x < NE; ++x) q4_repack(tmp + x * src_stride, N, K, dst + x * dst_stride, sstride, soff, e->st);
+    SN_HIP_TRY(hipStreamSynchronize(e->st), false);
+    return true;
+}
+
 float* upload_f32(sn_engine* e, const GgufTensor* t, char* err, int err_len) {
     float* d = e->dalloc<float>(t->nbytes, err, err_len);
     if (!d) return nullptr;
@@ -161,9 +179,17 @@ float* upload_f32(sn_engine* e, const GgufTensor* t, char* err, int err_len) {
 
 bool model_check(const GgufFile& g, std::string* why) {
     const std::string a = g.str("general.architecture");
-    if (a != "qwen3") {
-        *why = "architecture '" + a + "': this engine serves qwen3 models";
+    if (a != "qwen3" && a != "qwen3moe") {
+        *why = "architecture '" + a + "': this engine serves qwen3 and qwen3moe models";
         return false;
+    }
+    if (a == "qwen3moe") {
+        const int ne = (int) g.num(a + ".expert_count", 0), nu = (int) g.num(a + ".expert_used_count", 0);
+        const int fe = (int) g.num(a + ".expert_feed_forward_length", 0);
+        if (ne < 1 || ne > 256 || nu < 1 || nu > 8 || nu > ne || fe <= 0 || fe % 128) {
+            *why = "experts: 1 .. 256 experts, 1 .. 8 used, expert FFN width a multiple of 128";
+            return false;
+        }
     }
     const int H = (int) g.num(a + ".attention.head_count", 0), KVH = (int) g.num(a + ".attention.head_count_kv", 0);
     const int E = (int) g.num(a + ".embedding_length", 0);
@@ -214,6 +240,11 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->H = (int) g.num(a + ".attention.head_count", 0);
     e->KVH = (int) g.num(a + ".attention.head_count_kv", 0);
     e->F = (int) g.num(a + ".feed_forward_length", 0);
+    if (a == "qwen3moe") {
+        e->NE = (int) g.num(a + ".expert_count", 0);
+        e->NEU = (int) g.num(a + ".expert_used_count", 0);
+        e->FE = (int) g.num(a + ".expert_feed_forward_length", 0);
+    }
     e->eps = (float) g.num(a + ".attention.layer_norm_rms_epsilon", 1e-6);
     e->rope_base = (float) g.num(a + ".rope.freq_base", 1e6);
     e->n_ctx_train = (int) g.num(a + ".context_length", 0);
@@ -278,22 +309,57 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
         l.k_norm = f32(p + "attn_k_norm.weight", e->D);
         l.ffn_norm = f32(p + "ffn_norm.weight", E);
         const GgufTensor *tq = q4(p + "attn_q.weight", QD, E), *tk = q4(p + "attn_k.weight", KD, E),
-                         *tv = q4(p + "attn_v.weight", KD, E), *to = q4(p + "attn_output.weight", E, QD),
-                         *tg = q4(p + "ffn_gate.weight", F, E), *tu = q4(p + "ffn_up.weight", F, E),
-                         *td = q4(p + "ffn_down.weight", E, F);
+                         *tv = q4(p + "attn_v.weight", KD, E), *to = q4(p + "attn_output.weight", E, QD);
         if (!ok) return;
         l.wqkv = e->dalloc<uint8_t>(q4t_bytes(e->NQKV, E), err, err_len);
         l.wo = e->dalloc<uint8_t>(q4t_bytes(E, QD), err, err_len);
-        l.wgu = e->dalloc<uint8_t>(q4t_bytes(2 * F, E), err, err_len);
-        l.wd = e->dalloc<uint8_t>(q4t_bytes(E, F), err, err_len);
-        ok = l.wqkv && l.wo && l.wgu && l.wd;
-        // q, k, v stripes one after another (one matmul for all three); gate and up stripes interleaved in pairs
+        ok = l.wqkv && l.wo;
+        // q, k, v stripes one after another (one matmul for all three)
         ok = ok && upload_q4(e, tq, tmp, l.wqkv, 1, 0, err, err_len) &&
              upload_q4(e, tk, tmp, l.wqkv + q4t_bytes(QD, E), 1, 0, err, err_len) &&
              upload_q4(e, tv, tmp, l.wqkv + q4t_bytes(QD + KD, E), 1, 0, err, err_len) &&
-             upload_q4(e, to, tmp, l.wo, 1, 0, err, err_len) && upload_q4(e, tg, tmp, l.wgu, 2, 0, err, err_len) &&
-             upload_q4(e, tu, tmp, l.wgu, 2, 1, err, err_len) && upload_q4(e, td, tmp, l.wd, 1, 0, err, err_len);
+             upload_q4(e, to, tmp, l.wo, 1, 0, err, err_len);
+        if (!ok) return;
+        if (e->NE > 0 && i < e->L) {  // experts (the guess head's block stays dense)
+            const int NE = e->NE, FE = e->FE;
+            const GgufTensor* tr = need(g, p + "ffn_gate_inp.weight", GGML_F32, &why);
+            if (tr && (tr->ne[0] != E || tr->ne[1] != NE)) tr = nullptr, why = "router " + p + " has unexpected dims";
+            auto q4e = [&](const std::string& n, int N, int K) -> const GgufTensor* {
+                const GgufTensor* t = need(g, n, GGML_Q4_0, &why);
+                if (t && (t->ne[0] != K || t->ne[1] != N || t->ne[2] != NE)) {
+                    why = "tensor " + n + " has unexpected dimensions";
+                    t = nullptr;
+                }
+                return t;
+            };
+            const GgufTensor *tg = q4e(p + "ffn_gate_exps.weight", FE, E), *tu = q4e(p + "ffn_up_exps.weight", FE, E),
+                             *td = q4e(p + "ffn_down_exps.weight", E, FE);
+            ok = tr && tg && tu && td;
+            if (!ok) return;
+            l.router = upload_f32(e, tr, err, err_len);
+            l.egu = e->dalloc<uint8_t>(e->egu_stride * NE, err, err_len);
+            l.ed = e->dalloc<uint8_t>(e->ed_stride * NE, err, err_len);
+            ok = l.router && l.egu && l.ed;
+            // per expert: gate and up stripes interleaved in pairs, down stripes; experts one after another
+            ok = ok && upload_q4_experts(e, tg, tmp, l.egu, NE, FE, E, e->egu_stride, 2, 0, err, err_len) &&
+                 upload_q4_experts(e, tu, tmp, l.egu, NE, FE, E, e->egu_stride, 2, 1, err, err_len) &&
+                 upload_q4_experts(e, td, tmp, l.ed, NE, E, FE, e->ed_stride, 1, 0, err, err_len);
+            return;
+        }
+        const GgufTensor *tg = q4(p + "ffn_gate.weight", F, E), *tu = q4(p + "ffn_up.weight", F, E),
+                         *td = q4(p + "ffn_down.weight", E, F);
+        if (!ok) return;
+        l.wgu = e->dalloc<uint8_t>(q4t_bytes(2 * F, E), err, err_len);
+        l.wd = e->dalloc<uint8_t>(q4t_bytes(E, F), err, err_len);
+        ok = l.wgu && l.wd;
+        // gate and up stripes interleaved in pairs
+        ok = ok && upload_q4(e, tg, tmp, l.wgu, 2, 0, err, err_len) && upload_q4(e, tu, tmp, l.wgu, 2, 1, err, err_len) &&
+             upload_q4(e, td, tmp, l.wd, 1, 0, err, err_len);
     };
+    if (e->NE > 0) {
+        e->egu_stride = q4t_bytes(2 * e->FE, E);
+        e->ed_stride = q4t_bytes(E, e->FE);
+    }
     e->ly.resize(e->L);
     for (int i = 0; i < e->L && ok; ++i) load_layer(i, e->ly[i]);
     if (e->has_nextn && ok) {
@@ -332,13 +398,35 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->ao = e->dalloc<float>((size_t) R * QD * 4, err, err_len);
     e->hb = e->dalloc<float>((size_t) R * F * 4, err, err_len);
     e->logits = e->dalloc<float>((size_t) MO * e->V * 4, err, err_len);
-    e->xa = e->dalloc<uint8_t>(xa_bytes(R, KMAX), err, err_len);
+    // MoE: a step's (row, expert) pairs in expert-major tiles of 16 rows: at most one partial tile per expert used
+    const int RK = R * e->NEU;
+    if (RK > 4096) return fail("a MoE model's steps take at most 4096 / experts-used rows (max_rows)");
+    e->moe_tiles = e->NE > 0 ? std::min(e->NE, RK) + (RK + 15) / 16 : 0;
+    const int P = e->moe_tiles * 16;
+    e->xa = e->dalloc<uint8_t>(std::max(xa_bytes(R, KMAX), e->NE > 0 ? xa_bytes(P, std::max(E, e->FE)) : 0), err,
+                               err_len);
     size_t ws = 0;
     ws = std::max(ws, q4_workspace_bytes(R, e->NQKV, E));
     ws = std::max(ws, q4_workspace_bytes(R, E, QD));
-    ws = std::max(ws, q4_workspace_bytes(R, 2 * F, E));
-    ws = std::max(ws, q4_workspace_bytes(R, E, F));
+    if (F > 0) {
+        ws = std::max(ws, q4_workspace_bytes(R, 2 * F, E));
+        ws = std::max(ws, q4_workspace_bytes(R, E, F));
+    }
     ws = std::max(ws, q4_workspace_bytes(MO, e->V, E));
+    if (e->NE > 0) {
+        ws = std::max(ws, (size_t) P * 2 * e->FE * 4);  // grouped expert matmuls: one slice
+        ws = std::max(ws, (size_t) P * E * 4);
+        const int NU = e->NEU;
+        e->hn = e->dalloc<float>((size_t) R * E * 4, err, err_len);
+        e->rlog = e->dalloc<float>((size_t) R * e->NE * 4, err, err_len);
+        e->mw = e->dalloc<float>((size_t) R * NU * 4, err, err_len);
+        e->mid = e->dalloc<int32_t>((size_t) R * NU * 4, err, err_len);
+        e->prow = e->dalloc<int32_t>((size_t) R * NU * 4, err, err_len);
+        e->rsrc = e->dalloc<int32_t>((size_t) P * 4, err, err_len);
+        e->gitems = e->dalloc<int32_t>((size_t) e->moe_tiles * 2 * 4, err, err_len);
+        e->gcount = e->dalloc<int32_t>(4, err, err_len);
+        if (!e->hn || !e->rlog || !e->mw || !e->mid || !e->prow || !e->rsrc || !e->gitems || !e->gcount) return fail("");
+    }
     if (e->has_nextn) {
         ws = std::max(ws, q4_workspace_bytes(R, E, 2 * E));    // eh_proj
         ws = std::max(ws, q4_workspace_bytes(R, 2 * KD, E));   // the head's k|v (its cache fill)
@@ -628,19 +716,69 @@ struct Dev {
     uint16_t* kp(int layer) { return e->kbase + (size_t) layer * e->layer_halves; }
     uint16_t* vp(int layer) { return e->vbase + (size_t) layer * e->layer_halves; }
 
-    // one block over R rows whose Q8_0 operand of attn_norm(x) is in xa; x (residual) updated through its down
-    // projection's sums (left in the workspace, not yet added)
-    void block(const DevLayer& l, int layer, float* x, int R, const Stage& S, const AttnList& al, const int32_t* d_seq,
+    // one block over R rows whose Q8_0 operand of attn_norm(x) is in xa. Returns whether x still awaits its down
+    // projection's sums (left in the workspace): a dense FFN; a MoE layer adds its experts itself.
+    bool block(const DevLayer& l, int layer, float* x, int R, const Stage& S, const AttnList& al, const int32_t* d_seq,
                const int32_t* d_pos) {
         const int E = e->E, F = e->F;
         gemm(l.wqkv, R, e->NQKV, E);
         rope(l, R, e->H, d_seq, d_pos, kp(layer), vp(layer));
         attention(S, al, R, d_pos, kp(layer), vp(layer));
         gemm(l.wo, R, E, e->QD);
+        if (l.egu) {
+            moe(l, x, R);
+            return false;
+        }
         resid(x, R, l.ffn_norm, true);
         gemm(l.wgu, R, 2 * F, E);
         swiglu(R);
         gemm(l.wd, R, E, F);
+        return true;
+    }
+
+    // MoE FFN (moe_ffn, sn_layers.inc.h:129-144): x += o's sums, ffn norm (the rows kept as hn); router, top-k and
+    // renormalised weights; the (row, expert) pairs in expert-major 16-row tiles; their Q8_0 operand gathered from hn;
+    // grouped gate/up (SwiGLU + Q8_0) and down matmuls over the used experts; the weighted sum in slot order into x
+    void moe(const DevLayer& l, float* x, int R) {
+        const int E = e->E, NE = e->NE, NU = e->NEU, FE = e->FE, T = e->moe_tiles, P = T * 16;
+        rc |= e->launch(SNX_K_QUANT, (double) R * E * (8 + 4 * ks) + (double) R * E * 6, [&] {
+            return resid_quant(x, e->gemm_ws, ks, R, E, l.ffn_norm, e->eps, e->xa, st, true, e->hn);
+        });
+        rc |= e->launch(SNX_K_OTHER, (double) NE * E * 4 + (double) R * E * 4, [&] {
+            moe_route(e->hn, l.router, R, E, NE, NU, e->rlog, e->mid, e->mw, st);
+            return moe_group(e->mid, R, NU, NE, P, e->prow, e->rsrc, e->gitems, e->gcount, st);
+        });
+        // the experts used (a host read only while profiling: the matmuls' algorithmic bytes)
+        double used = std::min(NE, R * NU);
+        if (e->prof_on) {
+            std::vector<int32_t> it(2 * (size_t) T);
+            int32_t n = 0;
+            if (hipMemcpyAsync(&n, e->gcount, 4, hipMemcpyDeviceToHost, st) == hipSuccess &&
+                hipMemcpyAsync(it.data(), e->gitems, it.size() * 4, hipMemcpyDeviceToHost, st) == hipSuccess &&
+                hipStreamSynchronize(st) == hipSuccess) {
+                std::vector<bool> seen(NE, false);
+                used = 0;
+                for (int i = 0; i < n && i < T; ++i)
+                    if (!seen[it[2 * i]]) seen[it[2 * i]] = true, used += 1;
+            }
+        }
+        quant(e->hn, e->rsrc, P, E, nullptr);
+        rc |= e->launch(SNX_K_GEMM, used * e->egu_stride + (double) R * NU * E * 4 + (double) R * NU * 2 * FE * 4, [&] {
+            return q4_gemm_grouped(l.egu, e->egu_stride, e->gitems, e->gcount, T, e->xa, P, 2 * FE, E, e->gemm_ws,
+                                   e->gemm_ws_bytes, st) < 0 ? -1 : 0;
+        });
+        rc |= e->launch(SNX_K_QUANT, (double) R * NU * FE * 14, [&] {
+            swiglu_quant(e->gemm_ws, 1, P, FE, nullptr, e->xa, st);
+            return 0;
+        });
+        rc |= e->launch(SNX_K_GEMM, used * e->ed_stride + (double) R * NU * FE * 4 + (double) R * NU * E * 4, [&] {
+            return q4_gemm_grouped(l.ed, e->ed_stride, e->gitems, e->gcount, T, e->xa, P, E, FE, e->gemm_ws,
+                                   e->gemm_ws_bytes, st) < 0 ? -1 : 0;
+        });
+        rc |= e->launch(SNX_K_OTHER, (double) R * NU * E * 4 + (double) R * E * 8, [&] {
+            moe_out(x, e->gemm_ws, e->prow, e->mw, R, E, NU, st);
+            return 0;
+        });
     }
 
     // the model's layers over R rows (qwen_layers, sn_attn.inc.h:216-231); leaves x = the final residual rows
@@ -648,12 +786,13 @@ struct Dev {
                const AttnList& al) {
         const int E = e->E;
         rc |= e->launch(SNX_K_OTHER, (double) R * E * 8, [&] { embed_rows(e->tok_embd, E, d_tok, R, e->x, st); return 0; });
-        quant(e->x, nullptr, R, E, e->ly[0].attn_norm);
+        bool pending = false;  // x awaits the previous layer's down projection sums
         for (int i = 0; i < e->L && rc == 0; ++i) {
-            if (i > 0) resid(e->x, R, e->ly[i].attn_norm, true);  // x += the previous layer's down projection
-            block(e->ly[i], i, e->x, R, S, al, d_seq, d_pos);
+            if (pending) resid(e->x, R, e->ly[i].attn_norm, true);  // x += them, then the attn_norm operand
+            else quant(e->x, nullptr, R, E, e->ly[i].attn_norm);
+            pending = block(e->ly[i], i, e->x, R, S, al, d_seq, d_pos);
         }
-        if (rc == 0) resid(e->x, R, nullptr, false);  // x += the last layer's down projection
+        if (rc == 0 && pending) resid(e->x, R, nullptr, false);  // x += the last layer's down projection
     }
 
     // output stage (sn_encode.inc.h:304-317): final norm of rows d_rows (n of them) of `x`, LM head, optional forced
@@ -716,8 +855,7 @@ struct Dev {
         quant(e->mcat, nullptr, n, 2 * E, nullptr);
         gemm(e->mtp_eh, n, E, 2 * E);
         resid(e->mx, n, e->mtp.attn_norm, true, false);
-        block(e->mtp, e->L, e->mx, n, S, al, d_seq, d_pos);
-        resid(e->mx, n, nullptr, false);
+        if (block(e->mtp, e->L, e->mx, n, S, al, d_seq, d_pos)) resid(e->mx, n, nullptr, false);
         quant(e->mx, nullptr, n, E, e->mtp_hdnorm, e->mhg);
         head_logits(n);
         rc |= e->launch(SNX_K_OTHER, (double) n * e->V * 4, [&] {

@@ -410,3 +410,172 @@ void cut_cells(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int CL, in
         hipLaunchKernelGGL(k_cut_cells, dim3(n, k, CL), dim3(256), 0, st, kbase, vbase, layer_halves, KVH, page_cells, pt,
                            max_pages, k, seq, pos, acc);
 }
+
+// ---- mixture of experts (moe_ffn, sn_layers.inc.h:129-144) -----------------------------------------------------------
+
+// Router logits [R][NE] = hn [R][E] (the normed rows) x router [NE][E] (fp32). Workgroup per expert, its router row in
+// LDS; thread (row r, segment g of 8) sums its segment's E / 8 products with float4 loads all in flight, then the 8
+// segments are added by a fixed xor tree: the order of a row's sum depends on E alone, not on the other rows.
+__global__ __launch_bounds__(256) void k_router(const float* __restrict__ hn, const float* __restrict__ router, int R,
+                                                int E, int NE, float* __restrict__ out) {
+    extern __shared__ float wrow[];
+    const int x = blockIdx.x, t = threadIdx.x, seg = t & 7;
+    for (int i = t; i < E; i += 256) wrow[i] = router[(size_t) x * E + i];
+    __syncthreads();
+    const int SL = E / 8;  // a segment (E % 32 == 0)
+    for (int r0 = 0; r0 < R; r0 += 32) {
+        const int r = r0 + (t >> 3);
+        const float* h = hn + (size_t) min(r, R - 1) * E + seg * SL;
+        const float* w = wrow + seg * SL;
+        float s = 0.0f;
+        for (int i0 = 0; i0 < SL; i0 += 64) {
+            float4 hv[16];
+            for (int u = 0; u < 16; ++u) hv[u] = i0 + 4 * u < SL ? *(const float4*) (h + i0 + 4 * u) : (float4){};
+            for (int u = 0; u < 16; ++u)
+                if (i0 + 4 * u < SL) {
+                    const float4 wv = *(const float4*) (w + i0 + 4 * u);
+                    s += hv[u].x * wv.x + hv[u].y * wv.y + hv[u].z * wv.z + hv[u].w * wv.w;
+                }
+        }
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        s += __shfl_xor(s, 4);
+        if (seg == 0 && r < R) out[(size_t) r * NE + x] = s;
+    }
+}
+
+// Routing of a row (moe_topk1, kernels.metal:3419-3467): softmax of its NE logits, the k largest (ties: the lower id),
+// weights p / sum(p) renormalised by their own sum floored at 6.103515625e-5. A wavefront per row.
+__global__ __launch_bounds__(64) void k_moe_topk(const float* __restrict__ lg, int NE, int k, int32_t* __restrict__ ids,
+                                                 float* __restrict__ w) {
+    const int r = blockIdx.x, lane = threadIdx.x;
+    const float* l = lg + (size_t) r * NE;
+    float p[4];
+    float m = -INFINITY;
+    for (int g = 0; g < 4; ++g) {
+        const int i = lane + 64 * g;
+        p[g] = i < NE ? l[i] : -INFINITY;
+        m = fmaxf(m, p[g]);
+    }
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    float tot = 0.0f;
+    for (int g = 0; g < 4; ++g) {
+        const bool in = lane + 64 * g < NE;
+        const float e = in ? expf(p[g] - m) : 0.0f;
+        p[g] = in ? e : -INFINITY;
+        tot += e;
+    }
+    for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o);
+    float pk[8];
+    int pick[8];
+    for (int j = 0; j < k; ++j) {
+        float bv = -INFINITY;
+        int bi = 1 << 30;
+        for (int g = 0; g < 4; ++g)
+            if (p[g] > bv) {
+                bv = p[g];
+                bi = lane + 64 * g;
+            }
+        float mv = bv;
+        for (int o = 32; o > 0; o >>= 1) mv = fmaxf(mv, __shfl_xor(mv, o));
+        int mi = bv == mv ? bi : 1 << 30;
+        for (int o = 32; o > 0; o >>= 1) mi = min(mi, __shfl_xor(mi, o));
+        for (int g = 0; g < 4; ++g)
+            if (lane + 64 * g == mi) p[g] = -INFINITY;
+        pk[j] = mv;
+        pick[j] = mi;
+    }
+    if (lane == 0) {
+        float sel = 0.0f;
+        for (int j = 0; j < k; ++j) {
+            pk[j] /= tot;
+            sel += pk[j];
+        }
+        sel = fmaxf(sel, 6.103515625e-5f);
+        for (int j = 0; j < k; ++j) {
+            ids[r * k + j] = pick[j];
+            w[r * k + j] = pk[j] / sel;
+        }
+    }
+}
+
+// The (row, slot) pairs in expert-major tiles of 16 rows (moe_lists, kernels.metal:3468-3497), deterministically: expert
+// x's pairs take tiles toff[x] .. in (row, slot) order. prow[r][j] = the pair's row in that layout; rsrc[p] = the row
+// whose operand tile row p carries (-1: padding); items = (expert, tile) of every tile, count = their number. One
+// workgroup of 1024 threads: the pairs' experts in LDS, a wavefront per expert ranks its pairs with ballots.
+#define MOE_MAX_PAIRS 4096
+__global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ ids, int RK, int NE, int P,
+                                                    int32_t* __restrict__ prow, int32_t* __restrict__ rsrc,
+                                                    int32_t* __restrict__ items, int32_t* __restrict__ count, int k) {
+    __shared__ int cnt[256], toff[257];
+    __shared__ int sid[MOE_MAX_PAIRS];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    for (int x = t; x < NE; x += 1024) cnt[x] = 0;
+    for (int p = t; p < P; p += 1024) rsrc[p] = -1;
+    for (int q = t; q < RK; q += 1024) sid[q] = ids[q];
+    __syncthreads();
+    for (int q = t; q < RK; q += 1024) atomicAdd(&cnt[sid[q]], 1);
+    __syncthreads();
+    if (t == 0) {
+        int o = 0;
+        for (int x = 0; x < NE; ++x) {
+            toff[x] = o;
+            o += (cnt[x] + 15) / 16;
+        }
+        toff[NE] = o;
+        *count = o;
+    }
+    __syncthreads();
+    for (int x = wave; x < NE; x += 16) {
+        if (cnt[x] == 0) continue;
+        int base = 0;
+        for (int u0 = 0; u0 < RK; u0 += 64) {
+            const int u = u0 + lane;
+            const bool hit = u < RK && sid[u] == x;
+            const unsigned long long m = __ballot(hit);
+            if (hit) {
+                const int p = toff[x] * 16 + base + __popcll(m & ((1ull << lane) - 1));
+                prow[u] = p;
+                rsrc[p] = u / k;
+            }
+            base += __popcll(m);
+        }
+        for (int i = toff[x] + lane; i < toff[x + 1]; i += 64) {
+            items[2 * i] = x;
+            items[2 * i + 1] = i;
+        }
+    }
+}
+
+// x[r] += sum_j w[r][j] * y[prow[r][j]] in slot order (moe_out, kernels.metal:3520-3538); y = the down matmul's sums.
+// Workgroup (row, 256 elements).
+__global__ __launch_bounds__(256) void k_moe_out(float* __restrict__ x, const float* __restrict__ y,
+                                                 const int32_t* __restrict__ prow, const float* __restrict__ w, int E,
+                                                 int k) {
+    const int r = blockIdx.x, i = blockIdx.y * 256 + threadIdx.x;
+    if (i >= E) return;
+    float yv[8], wv[8];
+    for (int j = 0; j < k; ++j) {
+        wv[j] = w[r * k + j];
+        yv[j] = y[(size_t) prow[r * k + j] * E + i];
+    }
+    float acc = 0.0f;
+    for (int j = 0; j < k; ++j) acc += wv[j] * yv[j];
+    x[(size_t) r * E + i] += acc;
+}
+
+void moe_route(const float* hn, const float* router, int R, int E, int NE, int k, float* lg, int32_t* ids, float* w,
+               hipStream_t st) {
+    if (R <= 0) return;
+    hipLaunchKernelGGL(k_router, dim3(NE), dim3(256), (size_t) E * 4, st, hn, router, R, E, NE, lg);
+    hipLaunchKernelGGL(k_moe_topk, dim3(R), dim3(64), 0, st, lg, NE, k, ids, w);
+}
+int moe_group(const int32_t* ids, int R, int k, int NE, int P, int32_t* prow, int32_t* rsrc, int32_t* items,
+              int32_t* count, hipStream_t st) {
+    if (R * k > MOE_MAX_PAIRS) return -1;
+    hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(1024), 0, st, ids, R * k, NE, P, prow, rsrc, items, count, k);
+    return 0;
+}
+void moe_out(float* x, const float* y, const int32_t* prow, const float* w, int R, int E, int k, hipStream_t st) {
+    if (R > 0) hipLaunchKernelGGL(k_moe_out, dim3(R, (E + 255) / 256), dim3(256), 0, st, x, y, prow, w, E, k);
+}

@@ -67,7 +67,15 @@ __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, 
                                                    uint8_t* __restrict__ xa, float* __restrict__ xn, int ldn) {
     __shared__ float red[4];
     const int m = blockIdx.x, nb = K / 32, t = threadIdx.x;
-    const float* x = X + (size_t) (rows ? rows[m] : m) * ldx;
+    const int src = rows ? rows[m] : m;
+    if (src < 0) {  // a zero row (padding of an expert's tile)
+        const int b = blockIdx.y * 64 + (t >> 2), g = t & 3;
+        if (b >= xa_nbp(K)) return;
+        *(half8*) (xa + xa_frag_off(K, m >> 4, b) + 16 * ((m & 15) + 16 * g)) = (half8){};
+        if (g == 0) *((_Float16*) (xa + xa_scale_off(M, K, m >> 4, b)) + (m & 15)) = (_Float16) 0.0f;
+        return;
+    }
+    const float* x = X + (size_t) src * ldx;
     float scale = 1.0f;
     if (nw) {
         float s = 0.0f;
@@ -126,7 +134,7 @@ __device__ __forceinline__ float4 add4(float4 a, float4 b) { return (float4){a.x
 template <int IT>
 __global__ __launch_bounds__(256) void k_resid_quant(float* __restrict__ X, const float* __restrict__ part, int ks,
                                                      int M, int K, const float* __restrict__ nw, float eps,
-                                                     uint8_t* __restrict__ xa, int add) {
+                                                     uint8_t* __restrict__ xa, int add, float* __restrict__ xn) {
     __shared__ float red[4];
     const int m = blockIdx.x, t = threadIdx.x, g = t & 3;
     const int nb = K / 32, nbp = xa_nbp(K);
@@ -172,6 +180,11 @@ __global__ __launch_bounds__(256) void k_resid_quant(float* __restrict__ X, cons
             for (int j = 0; j < 8; ++j) y[j] = (v[it][j] * scale) * w8[j];
         } else {
             for (int j = 0; j < 8; ++j) y[j] = v[it][j];
+        }
+        if (xn) {  // the normed rows themselves (the MoE router's input)
+            float* o = xn + (size_t) m * K + 32 * b;
+            *(float4*) (o + 4 * g) = (float4){y[0], y[1], y[2], y[3]};
+            *(float4*) (o + 16 + 4 * g) = (float4){y[4], y[5], y[6], y[7]};
         }
         q8_store(y, g, frag, dsl);
     }
@@ -254,11 +267,18 @@ __global__ __launch_bounds__(256) void k_q4_gemm(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) float s_sc[2][MT * 64];  // tile mt: [block][row] as fp32
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n_in = lane & 15, g = lane >> 4;
-    const int set = blockIdx.x, slice = blockIdx.y, mt0 = blockIdx.z * MT;
+    const int set = blockIdx.x, slice = blockIdx.y;
+    int mt0 = blockIdx.z * MT;
+    const uint8_t* wbase = a.w;
+    if (a.items) {  // grouped: this workgroup's (expert, row tile)
+        if ((int) blockIdx.z >= *a.count) return;
+        wbase = a.w + (size_t) a.items[2 * blockIdx.z] * a.wstride;
+        mt0 = a.items[2 * blockIdx.z + 1];
+    }
     const int stripe = set * 4 + wave;
     const int c0 = slice * a.gps, ng = min(a.gps, a.ngroups - c0);  // groups c0 .. c0 + ng - 1 (ng >= 1)
 
-    const uint8_t* wp = a.w + (size_t) min(stripe, a.nstripes - 1) * a.ngroups * Q4T_BYTES;
+    const uint8_t* wp = wbase + (size_t) min(stripe, a.nstripes - 1) * a.ngroups * Q4T_BYTES;
     // activation fragment f = wave * MT + j of a group: row tile mt0 + f / 4, block f % 4
     const uint8_t* af[MT];
     for (int j = 0; j < MT; ++j) {
@@ -376,7 +396,7 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
     if (M <= 0) return 0;
     const GemmPlan p = q4_plan(N, K);
     if (part == nullptr || part_bytes < (size_t) p.ks * M * N * sizeof(float)) return -1;
-    GemmArgs a;
+    GemmArgs a{};
     a.w = w; a.xa = xa; a.part = part; a.y = nullptr;
     a.M = M; a.N = N; a.K = K; a.ldy = 0; a.epi = EPI_STORE;
     a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
@@ -386,12 +406,26 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
     return p.ks;
 }
 
+int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
+                    const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st) {
+    if (M <= 0 || max_items <= 0) return 0;
+    if (part == nullptr || part_bytes < (size_t) M * N * sizeof(float)) return -1;
+    GemmArgs a{};
+    a.w = w; a.xa = xa; a.part = part;
+    a.items = items; a.count = count; a.wstride = wstride;
+    a.M = M; a.N = N; a.K = K; a.epi = EPI_STORE;
+    a.nstripes = (N + 15) / 16; a.ngroups = (K / 32 + 3) / 4; a.ks = 1; a.gps = a.ngroups;
+    a.mtiles = (M + 15) / 16;
+    hipLaunchKernelGGL((k_q4_gemm<1, 4>), dim3((a.nstripes + 3) / 4, 1, max_items), dim3(256), 0, st, a);
+    return 1;
+}
+
 int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* ws,
             size_t ws_bytes, hipStream_t st) {
     if (M <= 0) return 0;
     const int ks = q4_gemm_raw(w, xa, M, N, K, ws, ws_bytes, st);
     if (ks < 0) return -1;
-    GemmArgs a;
+    GemmArgs a{};
     a.part = ws; a.y = y;
     a.M = M; a.N = N; a.K = K; a.ldy = ldy; a.epi = epi; a.ks = ks;
     const int tot = M * (epi == EPI_SWIGLU ? N / 2 : N);
@@ -405,14 +439,14 @@ void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int 
 }
 
 int resid_quant(float* x, const float* part, int ks, int M, int K, const float* nw, float eps, uint8_t* xa,
-                hipStream_t st, bool add) {
+                hipStream_t st, bool add, float* xn) {
     if (M <= 0) return 0;
     const int it = (xa_nbp(K) + 63) / 64;
-    if (K % 32 || it > 4) return -1;
+    if (K % 32 || it > 4 || (xn && !xa)) return -1;
     const int ad = add ? 1 : 0;
-    if (it == 1) hipLaunchKernelGGL((k_resid_quant<1>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad);
-    else if (it == 2) hipLaunchKernelGGL((k_resid_quant<2>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad);
-    else hipLaunchKernelGGL((k_resid_quant<4>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad);
+    if (it == 1) hipLaunchKernelGGL((k_resid_quant<1>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
+    else if (it == 2) hipLaunchKernelGGL((k_resid_quant<2>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
+    else hipLaunchKernelGGL((k_resid_quant<4>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
     return 0;
 }
 

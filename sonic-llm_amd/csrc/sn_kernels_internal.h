@@ -9,6 +9,11 @@ struct GemmArgs {
     const uint8_t* xa;
     float* y;
     float* part;  // k-slice partial sums [ks][M][N]
+    // grouped (experts): z-block i runs item (expert, row tile) items[2i], items[2i + 1] for i < *count, its weights at
+    // w + expert * wstride; one slice, one row tile a workgroup
+    const int32_t* items;
+    const int32_t* count;
+    size_t wstride;
     int M, N, K, ldy, epi;
     int nstripes, ngroups, ks, gps, mtiles;
 };
@@ -26,9 +31,14 @@ size_t q4_workspace_bytes(int M, int N, int K);
 // or -1 when part_bytes is too small.
 int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
                 hipStream_t st);
+// Grouped raw matmul of expert matrices (moe: qmm_grouped, sn_attn.inc.h:352-359): up to max_items (expert, row tile)
+// items, the device count in `count`; part[M][N] rows of each item's tile (one slice).
+int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
+                    const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st);
 // GGUF Q4_0 rows -> stripes; source stripe s lands at destination stripe s * sstride + soff.
 void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int soff, hipStream_t st);
-// rows (optional): row m of the operand is row rows[m] of x. nw (optional): RMSNorm weight applied first.
+// rows (optional): row m of the operand is row rows[m] of x (rows[m] < 0: a zero row). nw (optional): RMSNorm weight
+// applied first.
 // xn (optional): the normed fp32 rows, ldn apart.
 void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const float* nw, float eps, uint8_t* xa,
                float* xn, int ldn, hipStream_t st);
@@ -37,7 +47,7 @@ void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const
 // x[m] += the k-slice sums part[ks][M][K] (added in slice order; add false: x[m] = the sums); then, with xa, the Q8_0
 // operand of the new rows (RMS-normed by nw when given). K <= 8192. 0, or -1 (shape).
 int resid_quant(float* x, const float* part, int ks, int M, int K, const float* nw, float eps, uint8_t* xa,
-                hipStream_t st, bool add = true);
+                hipStream_t st, bool add = true, float* xn = nullptr);
 // h (optional) and the Q8_0 operand of silu(gate) * up from a stripe-interleaved gate/up matmul's k-slice sums
 // part[ks][M][2F].
 void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st);
@@ -116,3 +126,14 @@ void accept_rows(int n, int k, int slots, const int32_t* gtok, const int32_t* ot
                  int32_t* out_tok, int32_t* keep, int32_t* acc, hipStream_t st);
 void cut_cells(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int CL, int KVH, int page_cells, const int32_t* pt,
                int max_pages, int n, int k, const int32_t* seq, const int32_t* pos, const int32_t* acc, hipStream_t st);
+
+// ---- mixture of experts
+// router logits lg [R][NE] of the normed rows hn, then each row's k experts ids [R][k] and weights w [R][k]
+void moe_route(const float* hn, const float* router, int R, int E, int NE, int k, float* lg, int32_t* ids, float* w,
+               hipStream_t st);
+// the pairs in expert-major 16-row tiles: prow [R][k], rsrc [P] (-1 padding), items [2 x tiles] (expert, tile), count.
+// R * k <= 4096; -1 beyond.
+int moe_group(const int32_t* ids, int R, int k, int NE, int P, int32_t* prow, int32_t* rsrc, int32_t* items,
+               int32_t* count, hipStream_t st);
+// x[r] += sum_j w[r][j] y[prow[r][j]] (slot order)
+void moe_out(float* x, const float* y, const int32_t* prow, const float* w, int R, int E, int k, hipStream_t st);

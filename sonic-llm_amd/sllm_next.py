@@ -161,6 +161,8 @@ def model_cfg(n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, head_dim=128, n
 
 # The configs' models
 QWEN3_4B = dict(n_layer=36, n_embd=2560, n_head=32, n_head_kv=8, n_ff=9728, n_vocab=151936)
+QWEN3_30B_A3B = dict(n_layer=48, n_embd=2048, n_head=32, n_head_kv=4, n_ff=6144, n_vocab=151936, n_expert=128,
+                     n_expert_used=8, n_ff_exp=768)
 
 
 def write_model(path: str, cfg: ModelCfg, seed: int, nthreads: int = 0) -> None:
