@@ -19,6 +19,7 @@ void embed_rows(const float* table, int E, const int32_t* tok, int R, float* x, 
 // Per head: RMSNorm over 128 dims with weight w, then y_i = x_i cos - x_{i+64} sin, y_{i+64} = x_i sin + x_{i+64} cos
 // with theta_i = p * s^i formed by i successive fp32 multiplies from p (ggml_rope_cache_init's loop), s = base^(-2/128)
 // computed on the host. q stays in place (fp32); k and v go to the row's cell in fp16.
+template <int KM>
 __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ldqkv, const float* __restrict__ part,
                                                  int ks, int R, int H, int KVH, const float* __restrict__ qw,
                                                  const float* __restrict__ kw, float eps, float theta_scale,
@@ -32,11 +33,7 @@ __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ld
     const float c = cosf(theta), s = sinf(theta);
     float* row = qkv + (size_t) r * ldqkv;
     const int N = (H + 2 * KVH) * 128;
-    auto sum = [&](int c) {
-        float v = part[(size_t) r * N + c];
-        for (int k = 1; k < ks; ++k) v += part[((size_t) k * R + r) * N + c];
-        return v;
-    };
+    auto sum = [&](int c) { return slices_sum1<KM>(part + (size_t) r * N + c, (size_t) R * N, ks); };
     const int page = pt[(size_t) seq[r] * max_pages + p / page_cells];
     const int off = p % page_cells;
     const int h = 4 * blockIdx.y + wave;
@@ -90,9 +87,18 @@ void qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, in
                      const float* kw, float eps, float theta_scale, const int32_t* seq, const int32_t* pos,
                      const int32_t* pt, int max_pages, int page_cells, uint16_t* kpool, uint16_t* vpool,
                      hipStream_t st) {
-    if (R > 0)
-        hipLaunchKernelGGL(k_qk_rope, dim3(R, (H + KVH + 3) / 4), dim3(256), 0, st, qkv, ldqkv, part, ks, R, H, KVH, qw,
-                           kw, eps, theta_scale, seq, pos, pt, max_pages, page_cells, kpool, vpool);
+    if (R <= 0) return;
+    const dim3 grid(R, (H + KVH + 3) / 4);
+    const int km = part ? ks_bound(ks) : 1;
+    if (km == 0) return;
+#define QKR(KM_)                                                                                                 \
+    hipLaunchKernelGGL((k_qk_rope<KM_>), grid, dim3(256), 0, st, qkv, ldqkv, part, ks, R, H, KVH, qw, kw, eps, \
+                       theta_scale, seq, pos, pt, max_pages, page_cells, kpool, vpool)
+    if (km == 1) QKR(1);
+    else if (km == 2) QKR(2);
+    else if (km == 4) QKR(4);
+    else QKR(8);
+#undef QKR
 }
 
 // ---- greedy argmax (argmax / argmax_p, kernels.metal:327-442) -------------------------------------------------------

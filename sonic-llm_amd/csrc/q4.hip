@@ -131,7 +131,7 @@ __device__ __forceinline__ float4 add4(float4 a, float4 b) { return (float4){a.x
 // sums), written back; then,
 // when xa is given, the RMSNorm (weight nw) and Q8_0 operand of the new row. One workgroup per row (the norm needs the
 // whole row before any value is quantized); lane t covers blocks t / 4 + 64 i.
-template <int IT>
+template <int IT, int KM>
 __global__ __launch_bounds__(256) void k_resid_quant(float* __restrict__ X, const float* __restrict__ part, int ks,
                                                      int M, int K, const float* __restrict__ nw, float eps,
                                                      uint8_t* __restrict__ xa, int add, float* __restrict__ xn) {
@@ -146,11 +146,8 @@ __global__ __launch_bounds__(256) void k_resid_quant(float* __restrict__ X, cons
         if (b >= nb) continue;
         const int e0 = 32 * b + 4 * g, e1 = e0 + 16;
         float4 lo = add ? ld4(x + e0) : (float4){0.f, 0.f, 0.f, 0.f}, hi = add ? ld4(x + e1) : (float4){0.f, 0.f, 0.f, 0.f};
-        float4 slo = ld4(part + (size_t) m * K + e0), shi = ld4(part + (size_t) m * K + e1);
-        for (int k = 1; k < ks; ++k) {
-            slo = add4(slo, ld4(part + ((size_t) k * M + m) * K + e0));
-            shi = add4(shi, ld4(part + ((size_t) k * M + m) * K + e1));
-        }
+        const float4 slo = slices_sum4<KM>(part + (size_t) m * K + e0, (size_t) M * K, ks);
+        const float4 shi = slices_sum4<KM>(part + (size_t) m * K + e1, (size_t) M * K, ks);
         lo = add4(lo, slo);
         hi = add4(hi, shi);
         *(float4*) (x + e0) = lo;
@@ -193,6 +190,7 @@ __global__ __launch_bounds__(256) void k_resid_quant(float* __restrict__ X, cons
 // SwiGLU of a stripe-interleaved gate/up matmul's k-slice sums (part[ks][M][2F]: output column 16p + n is
 // silu(column 32p + n) * column 32p + 16 + n), written as fp32 rows h (when given) and as the Q8_0 operand of the next
 // matmul. Workgroup (row m, 64 blocks), 4 lanes per block as in k_quant_act.
+template <int KM>
 __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ part, int ks, int M, int F,
                                                       float* __restrict__ h, uint8_t* __restrict__ xa) {
     const int m = blockIdx.x, t = threadIdx.x;
@@ -208,11 +206,7 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ 
     }
     // elements 32b + 4g + j (pair 2b) and 32b + 16 + 4g + j (pair 2b + 1): gate at 64b + 4g (+32), up 16 further
     const size_t N = 2 * (size_t) F;
-    auto sum4 = [&](int c) {
-        float4 s4 = ld4(part + (size_t) m * N + c);
-        for (int k = 1; k < ks; ++k) s4 = add4(s4, ld4(part + ((size_t) k * M + m) * N + c));
-        return s4;
-    };
+    auto sum4 = [&](int c) { return slices_sum4<KM>(part + (size_t) m * N + c, (size_t) M * N, ks); };
     const float4 g0 = sum4(64 * b + 4 * g), u0 = sum4(64 * b + 16 + 4 * g);
     const float4 g1 = sum4(64 * b + 32 + 4 * g), u1 = sum4(64 * b + 48 + 4 * g);
     float v[8] = {silu(g0.x) * u0.x, silu(g0.y) * u0.y, silu(g0.z) * u0.z, silu(g0.w) * u0.w,
@@ -376,14 +370,14 @@ __global__ void k_q4_reduce(GemmArgs a) {
 
 // The launch shape depends on (N, K) only, never on the rows (row invariance): 4 stripes per workgroup, and k-slices
 // across workgroups while there are fewer than 256 workgroups (an MI355X round is 1024 of them: fewer, longer
-// workgroups keep the slices' partial sums small).
+// workgroups keep the slices' partial sums small), at most KS_MAX slices.
 GemmPlan q4_plan(int N, int K) {
     GemmPlan p;
     p.nstripes = (N + 15) / 16;
     p.ngroups = (K / 32 + 3) / 4;
     p.sets = (p.nstripes + 3) / 4;
     int ks = 1;
-    while (p.sets * ks < 256 && ks < p.ngroups) ++ks;
+    while (p.sets * ks < 256 && ks < p.ngroups && ks < KS_MAX) ++ks;
     p.gps = (p.ngroups + ks - 1) / ks;
     p.ks = (p.ngroups + p.gps - 1) / p.gps;
     return p;
@@ -438,21 +432,36 @@ void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int 
     hipLaunchKernelGGL(k_q4_repack, dim3(tiles), dim3(64), 0, st, src, N, K, dst, sstride, soff);
 }
 
+template <int IT>
+static void launch_resid(int km, float* x, const float* part, int ks, int M, int K, const float* nw, float eps,
+                         uint8_t* xa, int ad, float* xn, hipStream_t st) {
+    if (km == 1) hipLaunchKernelGGL((k_resid_quant<IT, 1>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
+    else if (km == 2) hipLaunchKernelGGL((k_resid_quant<IT, 2>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
+    else if (km == 4) hipLaunchKernelGGL((k_resid_quant<IT, 4>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
+    else hipLaunchKernelGGL((k_resid_quant<IT, 8>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
+}
+
 int resid_quant(float* x, const float* part, int ks, int M, int K, const float* nw, float eps, uint8_t* xa,
                 hipStream_t st, bool add, float* xn) {
     if (M <= 0) return 0;
-    const int it = (xa_nbp(K) + 63) / 64;
-    if (K % 32 || it > 4 || (xn && !xa)) return -1;
+    const int it = (xa_nbp(K) + 63) / 64, km = ks_bound(ks);
+    if (K % 32 || it > 4 || (xn && !xa) || km == 0) return -1;
     const int ad = add ? 1 : 0;
-    if (it == 1) hipLaunchKernelGGL((k_resid_quant<1>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
-    else if (it == 2) hipLaunchKernelGGL((k_resid_quant<2>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
-    else hipLaunchKernelGGL((k_resid_quant<4>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
+    if (it == 1) launch_resid<1>(km, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
+    else if (it == 2) launch_resid<2>(km, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
+    else launch_resid<4>(km, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
     return 0;
 }
 
 void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st) {
-    if (M > 0)
-        hipLaunchKernelGGL(k_swiglu_quant, dim3(M, (xa_nbp(F) + 63) / 64), dim3(256), 0, st, part, ks, M, F, h, xa);
+    if (M <= 0) return;
+    const dim3 grid(M, (xa_nbp(F) + 63) / 64);
+    const int km = ks_bound(ks);
+    if (km == 0) return;
+    if (km == 1) hipLaunchKernelGGL((k_swiglu_quant<1>), grid, dim3(256), 0, st, part, ks, M, F, h, xa);
+    else if (km == 2) hipLaunchKernelGGL((k_swiglu_quant<2>), grid, dim3(256), 0, st, part, ks, M, F, h, xa);
+    else if (km == 4) hipLaunchKernelGGL((k_swiglu_quant<4>), grid, dim3(256), 0, st, part, ks, M, F, h, xa);
+    else hipLaunchKernelGGL((k_swiglu_quant<8>), grid, dim3(256), 0, st, part, ks, M, F, h, xa);
 }
 
 void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const float* nw, float eps, uint8_t* xa,

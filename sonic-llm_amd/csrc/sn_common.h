@@ -61,3 +61,27 @@ __host__ __device__ static inline size_t xa_scale_off(int M, int K, int mt, int 
 }
 static inline size_t xa_bytes(int M, int K) { return (size_t) xa_mtp(M) * xa_nbp(K) * (XA_FRAG_BYTES + 32); }
 static inline size_t q4t_bytes(int N, int K) { return (size_t) ((N + 15) / 16) * ((K / 32 + 3) / 4) * Q4T_BYTES; }
+
+// The sum, in slice order, of ks <= KM k-slices of a matmul (slice k at p + k * stride). Every load is issued before
+// any is used (the slice index is clamped, so no load sits behind a branch); the slices past ks are not added.
+#define KS_MAX 8
+template <int KM>
+__device__ __forceinline__ float4 slices_sum4(const float* p, size_t stride, int ks) {
+    float4 v[KM];
+    for (int k = 0; k < KM; ++k) v[k] = *(const float4*) (p + (size_t) (k < ks ? k : ks - 1) * stride);
+    float4 s = v[0];
+    for (int k = 1; k < KM; ++k)
+        if (k < ks) s = (float4){s.x + v[k].x, s.y + v[k].y, s.z + v[k].z, s.w + v[k].w};
+    return s;
+}
+template <int KM>
+__device__ __forceinline__ float slices_sum1(const float* p, size_t stride, int ks) {
+    float v[KM];
+    for (int k = 0; k < KM; ++k) v[k] = p[(size_t) (k < ks ? k : ks - 1) * stride];
+    float s = v[0];
+    for (int k = 1; k < KM; ++k)
+        if (k < ks) s += v[k];
+    return s;
+}
+// the smallest slice bound of the kernels' instances that holds ks (0: ks out of range)
+static inline int ks_bound(int ks) { return ks < 1 ? 0 : ks == 1 ? 1 : ks <= 2 ? 2 : ks <= 4 ? 4 : ks <= KS_MAX ? 8 : 0; }
