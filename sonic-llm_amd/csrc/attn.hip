@@ -176,7 +176,8 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
     }
 }
 
-// per (row, head): the chunks' partials in chunk order; out = acc / l. One wavefront, 2 dims a lane. With a.xa the
+// per (row, head): the chunks' partials in chunk order; out = acc / l. One wavefront, 2 dims a lane; the loads of 8
+// chunks are issued together (chunk index clamped, no load behind a branch), then combined in order. With a.xa the
 // head's 128 outputs (4 Q8_0 blocks of the o-projection's input row) are also quantized there, exactly as the
 // activation quantizer does (ggml x86 quantize_row_q8_0), into the xa operand of K = H * 128.
 __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
@@ -184,16 +185,24 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
     const int nc = a.row_pos[r] / ATT_CHUNK + 1;
     const float* p0 = a.part + ((size_t) r * a.H + h) * a.max_chunks * (ATT_D + 2);
     float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-    for (int c = 0; c < nc; ++c) {
-        const float* pc = p0 + (size_t) c * (ATT_D + 2);
-        const float mc = pc[ATT_D], lc = pc[ATT_D + 1];
-        if (mc == -INFINITY) continue;  // a chunk with no cell for this row
-        const float mn = fmaxf(M, mc);
-        const float e0 = M == -INFINITY ? 0.0f : __expf(M - mn), e1 = __expf(mc - mn);
-        o0 = o0 * e0 + pc[2 * lane] * e1;
-        o1 = o1 * e0 + pc[2 * lane + 1] * e1;
-        L = L * e0 + lc * e1;
-        M = mn;
+    for (int c0 = 0; c0 < nc; c0 += 8) {
+        float2 ov[8], ml[8];
+        for (int j = 0; j < 8; ++j) {
+            const float* pc = p0 + (size_t) (c0 + j < nc ? c0 + j : nc - 1) * (ATT_D + 2);
+            ov[j] = *(const float2*) (pc + 2 * lane);
+            ml[j] = *(const float2*) (pc + ATT_D);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {  // (a fixed trip count keeps ov and ml in registers)
+            const float mc = ml[j].x, lc = ml[j].y;
+            if (c0 + j >= nc || mc == -INFINITY) continue;  // past the row's chunks, or a chunk with no cell for it
+            const float mn = fmaxf(M, mc);
+            const float e0 = M == -INFINITY ? 0.0f : __expf(M - mn), e1 = __expf(mc - mn);
+            o0 = o0 * e0 + ov[j].x * e1;
+            o1 = o1 * e0 + ov[j].y * e1;
+            L = L * e0 + lc * e1;
+            M = mn;
+        }
     }
     const float il = L > 0.0f ? 1.0f / L : 0.0f;
     o0 *= il;

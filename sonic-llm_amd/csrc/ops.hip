@@ -14,11 +14,12 @@ void embed_rows(const float* table, int E, const int32_t* tok, int R, float* x, 
 }
 
 // ---- QK-norm + RoPE + K/V into the cache (qk_rope, kernels.metal:149-197) -------------------------------------------
-// Workgroup (row, y): wavefront w takes head 4 y + w, lane i the rotation pair (i, i + 64); workgroups y = 0 also
-// write the row's V.
-// Per head: RMSNorm over 128 dims with weight w, then y_i = x_i cos - x_{i+64} sin, y_{i+64} = x_i sin + x_{i+64} cos
-// with theta_i = p * s^i formed by i successive fp32 multiplies from p (ggml_rope_cache_init's loop), s = base^(-2/128)
-// computed on the host. q stays in place (fp32); k and v go to the row's cell in fp16.
+// Workgroup (row, y): wavefront w takes head 4 y + w of the row's q heads, k heads and v heads in that order; lane i
+// the dims (i, i + 64), which are a rotation pair for q and k.
+// Per q/k head: RMSNorm over 128 dims with weight w, then y_i = x_i cos - x_{i+64} sin, y_{i+64} = x_i sin +
+// x_{i+64} cos with theta_i = p * s^i formed by i successive fp32 multiplies from p (ggml_rope_cache_init's loop),
+// s = base^(-2/128) computed on the host. q stays in place (fp32); k and v go to the row's cell in fp16 (with part
+// given, k and v as the matmul made them are also written into the row).
 template <int KM>
 __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ldqkv, const float* __restrict__ part,
                                                  int ks, int R, int H, int KVH, const float* __restrict__ qw,
@@ -27,59 +28,50 @@ __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ld
                                                  const int32_t* __restrict__ pt, int max_pages, int page_cells,
                                                  uint16_t* __restrict__ kpool, uint16_t* __restrict__ vpool) {
     const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = 4 * blockIdx.y + wave;
+    if (h >= H + 2 * KVH) return;
+    const bool isq = h < H, isv = h >= H + KVH;
+    const int N = (H + 2 * KVH) * 128;
+    float* x = qkv + (size_t) r * ldqkv + (size_t) h * 128;  // q heads, k heads, v heads: contiguous
+    const float* w = isq ? qw : kw;
+    const float w0 = isv ? 0.0f : w[lane], w1 = isv ? 0.0f : w[lane + 64];
     const int p = pos[r];
+    const int page = pt[(size_t) seq[r] * max_pages + p / page_cells];
+    const int off = p % page_cells;
+    float x0, x1;
+    if (part) {  // the q|k|v matmul's k-slice sums, added in slice order
+        x0 = slices_sum1<KM>(part + (size_t) r * N + h * 128 + lane, (size_t) R * N, ks);
+        x1 = slices_sum1<KM>(part + (size_t) r * N + h * 128 + lane + 64, (size_t) R * N, ks);
+        if (!isq) {  // k and v as the matmul made them (q is overwritten below)
+            x[lane] = x0;
+            x[lane + 64] = x1;
+        }
+    } else {
+        x0 = x[lane];
+        x1 = x[lane + 64];
+    }
+    if (isv) {
+        uint16_t* vc = vpool + (((size_t) page * KVH + (h - H - KVH)) * page_cells + off) * 128;
+        vc[lane] = __builtin_bit_cast(uint16_t, (_Float16) x0);
+        vc[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16) x1);
+        return;
+    }
     float theta = (float) p;
     for (int i = 0; i < lane; ++i) theta *= theta_scale;
     const float c = cosf(theta), s = sinf(theta);
-    float* row = qkv + (size_t) r * ldqkv;
-    const int N = (H + 2 * KVH) * 128;
-    auto sum = [&](int c) { return slices_sum1<KM>(part + (size_t) r * N + c, (size_t) R * N, ks); };
-    const int page = pt[(size_t) seq[r] * max_pages + p / page_cells];
-    const int off = p % page_cells;
-    const int h = 4 * blockIdx.y + wave;
-    if (h < H + KVH) {
-        const bool isq = h < H;
-        float* x = row + (size_t) h * 128;  // q heads then k heads, contiguous
-        const float* w = isq ? qw : kw;
-        float x0, x1;
-        if (part) {  // the q|k|v matmul's k-slice sums, added in slice order
-            x0 = sum(h * 128 + lane);
-            x1 = sum(h * 128 + lane + 64);
-            if (!isq) {  // k as the matmul made it (q is overwritten below)
-                x[lane] = x0;
-                x[lane + 64] = x1;
-            }
-        } else {
-            x0 = x[lane];
-            x1 = x[lane + 64];
-        }
-        float ss = x0 * x0 + x1 * x1;
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-        const float sc = 1.0f / sqrtf(ss / 128.f + eps);
-        x0 = (x0 * sc) * w[lane];
-        x1 = (x1 * sc) * w[lane + 64];
-        const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
-        if (isq) {
-            x[lane] = y0;
-            x[lane + 64] = y1;
-        } else {
-            uint16_t* kc = kpool + (((size_t) page * KVH + (h - H)) * page_cells + off) * 128;
-            kc[lane] = __builtin_bit_cast(uint16_t, (_Float16) y0);
-            kc[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16) y1);
-        }
-    }
-    if (blockIdx.y != 0) return;
-    float* v = row + (size_t) (H + KVH) * 128;
-    for (int i = threadIdx.x; i < KVH * 128; i += 256) {
-        const int hh = i / 128, d = i % 128;
-        float vi;
-        if (part) {
-            vi = sum((H + KVH) * 128 + i);
-            v[i] = vi;
-        } else {
-            vi = v[i];
-        }
-        vpool[(((size_t) page * KVH + hh) * page_cells + off) * 128 + d] = __builtin_bit_cast(uint16_t, (_Float16) vi);
+    float ss = x0 * x0 + x1 * x1;
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    const float sc = 1.0f / sqrtf(ss / 128.f + eps);
+    x0 = (x0 * sc) * w0;
+    x1 = (x1 * sc) * w1;
+    const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
+    if (isq) {
+        x[lane] = y0;
+        x[lane + 64] = y1;
+    } else {
+        uint16_t* kc = kpool + (((size_t) page * KVH + (h - H)) * page_cells + off) * 128;
+        kc[lane] = __builtin_bit_cast(uint16_t, (_Float16) y0);
+        kc[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16) y1);
     }
 }
 
@@ -88,7 +80,7 @@ void qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, in
                      const int32_t* pt, int max_pages, int page_cells, uint16_t* kpool, uint16_t* vpool,
                      hipStream_t st) {
     if (R <= 0) return;
-    const dim3 grid(R, (H + KVH + 3) / 4);
+    const dim3 grid(R, (H + 2 * KVH + 3) / 4);
     const int km = part ? ks_bound(ks) : 1;
     if (km == 0) return;
 #define QKR(KM_)                                                                                                 \

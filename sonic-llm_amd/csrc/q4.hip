@@ -127,24 +127,39 @@ __device__ __forceinline__ void q8_store(const float* v, int g, uint8_t* frag, _
 __device__ __forceinline__ float4 ld4(const float* p) { return *(const float4*) p; }
 __device__ __forceinline__ float4 add4(float4 a, float4 b) { return (float4){a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w}; }
 
+// the workgroup's sum of v, the wavefronts' sums added in wavefront order (at most 16 wavefronts)
+__device__ __forceinline__ float block_reduce_sum(float v, float* red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = red[0];
+    for (int w = 1; w < (int) (blockDim.x >> 6); ++w) s += red[w];
+    return s;
+}
+
 // Residual rows: x[m] += the k-slice sums of a matmul (part[ks][M][K], slices added in order; add 0: x[m] = the
-// sums), written back; then,
-// when xa is given, the RMSNorm (weight nw) and Q8_0 operand of the new row. One workgroup per row (the norm needs the
-// whole row before any value is quantized); lane t covers blocks t / 4 + 64 i.
+// sums), written back; then, when xa is given, the RMSNorm (weight nw) and Q8_0 operand of the new row. One workgroup
+// per row (the norm needs the whole row before any value is quantized), 4 lanes per 32-block: lane t covers blocks
+// t / 4 + (blockDim / 4) i, i < IT. Every load (residual, slices, norm weight) is issued before the row's reduction.
 template <int IT, int KM>
-__global__ __launch_bounds__(256) void k_resid_quant(float* __restrict__ X, const float* __restrict__ part, int ks,
-                                                     int M, int K, const float* __restrict__ nw, float eps,
-                                                     uint8_t* __restrict__ xa, int add, float* __restrict__ xn) {
-    __shared__ float red[4];
-    const int m = blockIdx.x, t = threadIdx.x, g = t & 3;
+__global__ __launch_bounds__(1024) void k_resid_quant(float* __restrict__ X, const float* __restrict__ part, int ks,
+                                                      int M, int K, const float* __restrict__ nw, float eps,
+                                                      uint8_t* __restrict__ xa, int add, float* __restrict__ xn) {
+    __shared__ float red[16];
+    const int m = blockIdx.x, t = threadIdx.x, g = t & 3, bstep = blockDim.x >> 2;
     const int nb = K / 32, nbp = xa_nbp(K);
     float* x = X + (size_t) m * K;
-    float v[IT][8];
+    float v[IT][8], w[IT][8];
     float ss = 0.0f;
     for (int it = 0; it < IT; ++it) {
-        const int b = t / 4 + 64 * it;
+        const int b = t / 4 + bstep * it;
         if (b >= nb) continue;
         const int e0 = 32 * b + 4 * g, e1 = e0 + 16;
+        if (xa && nw) {
+            const float4 wl = ld4(nw + e0), wh = ld4(nw + e1);
+            const float w8[8] = {wl.x, wl.y, wl.z, wl.w, wh.x, wh.y, wh.z, wh.w};
+            for (int j = 0; j < 8; ++j) w[it][j] = w8[j];
+        }
         float4 lo = add ? ld4(x + e0) : (float4){0.f, 0.f, 0.f, 0.f}, hi = add ? ld4(x + e1) : (float4){0.f, 0.f, 0.f, 0.f};
         const float4 slo = slices_sum4<KM>(part + (size_t) m * K + e0, (size_t) M * K, ks);
         const float4 shi = slices_sum4<KM>(part + (size_t) m * K + e1, (size_t) M * K, ks);
@@ -152,16 +167,16 @@ __global__ __launch_bounds__(256) void k_resid_quant(float* __restrict__ X, cons
         hi = add4(hi, shi);
         *(float4*) (x + e0) = lo;
         *(float4*) (x + e1) = hi;
-        const float w8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        const float r8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         for (int j = 0; j < 8; ++j) {
-            v[it][j] = w8[j];
-            ss += w8[j] * w8[j];
+            v[it][j] = r8[j];
+            ss += r8[j] * r8[j];
         }
     }
     if (!xa) return;
-    const float scale = nw ? 1.0f / sqrtf(block_reduce_sum256(ss, red) / (float) K + eps) : 1.0f;
+    const float scale = nw ? 1.0f / sqrtf(block_reduce_sum(ss, red) / (float) K + eps) : 1.0f;
     for (int it = 0; it < IT; ++it) {
-        const int b = t / 4 + 64 * it;
+        const int b = t / 4 + bstep * it;
         if (b >= nbp) continue;
         uint8_t* frag = xa + xa_frag_off(K, m >> 4, b) + 16 * ((m & 15) + 16 * g);
         _Float16* dsl = (_Float16*) (xa + xa_scale_off(M, K, m >> 4, b)) + (m & 15);
@@ -172,9 +187,7 @@ __global__ __launch_bounds__(256) void k_resid_quant(float* __restrict__ X, cons
         }
         float y[8];
         if (nw) {
-            const float4 wl = ld4(nw + 32 * b + 4 * g), wh = ld4(nw + 32 * b + 16 + 4 * g);
-            const float w8[8] = {wl.x, wl.y, wl.z, wl.w, wh.x, wh.y, wh.z, wh.w};
-            for (int j = 0; j < 8; ++j) y[j] = (v[it][j] * scale) * w8[j];
+            for (int j = 0; j < 8; ++j) y[j] = (v[it][j] * scale) * w[it][j];
         } else {
             for (int j = 0; j < 8; ++j) y[j] = v[it][j];
         }
@@ -369,15 +382,16 @@ __global__ void k_q4_reduce(GemmArgs a) {
 // host side
 
 // The launch shape depends on (N, K) only, never on the rows (row invariance): 4 stripes per workgroup, and k-slices
-// across workgroups while there are fewer than 256 workgroups (an MI355X round is 1024 of them: fewer, longer
-// workgroups keep the slices' partial sums small), at most KS_MAX slices.
+// across workgroups while there are fewer than 512 workgroups, at most KS_MAX slices. 512 is two workgroups per CU:
+// a launch of 256-511 workgroups leaves CUs holding one next to CUs holding two (gate/up at 304 sets: 19.6 us at
+// one slice, 15.5 us at two, M = 32 on MI355X), while more slices mean more partial sums for the consumer to add.
 GemmPlan q4_plan(int N, int K) {
     GemmPlan p;
     p.nstripes = (N + 15) / 16;
     p.ngroups = (K / 32 + 3) / 4;
     p.sets = (p.nstripes + 3) / 4;
     int ks = 1;
-    while (p.sets * ks < 256 && ks < p.ngroups && ks < KS_MAX) ++ks;
+    while (p.sets * ks < 512 && ks < p.ngroups && ks < KS_MAX) ++ks;
     p.gps = (p.ngroups + ks - 1) / ks;
     p.ks = (p.ngroups + p.gps - 1) / p.gps;
     return p;
@@ -433,23 +447,27 @@ void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int 
 }
 
 template <int IT>
-static void launch_resid(int km, float* x, const float* part, int ks, int M, int K, const float* nw, float eps,
+static void launch_resid(int km, int nt, float* x, const float* part, int ks, int M, int K, const float* nw, float eps,
                          uint8_t* xa, int ad, float* xn, hipStream_t st) {
-    if (km == 1) hipLaunchKernelGGL((k_resid_quant<IT, 1>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
-    else if (km == 2) hipLaunchKernelGGL((k_resid_quant<IT, 2>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
-    else if (km == 4) hipLaunchKernelGGL((k_resid_quant<IT, 4>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
-    else hipLaunchKernelGGL((k_resid_quant<IT, 8>), dim3(M), dim3(256), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn);
+#define RQ(KM_) hipLaunchKernelGGL((k_resid_quant<IT, KM_>), dim3(M), dim3(nt), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn)
+    if (km == 1) RQ(1);
+    else if (km == 2) RQ(2);
+    else if (km == 4) RQ(4);
+    else RQ(8);
+#undef RQ
 }
 
 int resid_quant(float* x, const float* part, int ks, int M, int K, const float* nw, float eps, uint8_t* xa,
                 hipStream_t st, bool add, float* xn) {
     if (M <= 0) return 0;
-    const int it = (xa_nbp(K) + 63) / 64, km = ks_bound(ks);
+    // 4 lanes per block of the padded row, in whole wavefronts, at most 1024 lanes (then IT passes)
+    const int lanes = 4 * xa_nbp(K), nt = std::min(1024, (lanes + 63) / 64 * 64), it = (lanes + nt - 1) / nt;
+    const int km = ks_bound(ks);
     if (K % 32 || it > 4 || (xn && !xa) || km == 0) return -1;
     const int ad = add ? 1 : 0;
-    if (it == 1) launch_resid<1>(km, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
-    else if (it == 2) launch_resid<2>(km, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
-    else launch_resid<4>(km, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
+    if (it == 1) launch_resid<1>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
+    else if (it == 2) launch_resid<2>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
+    else launch_resid<4>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
     return 0;
 }
 
