@@ -213,18 +213,29 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
         out[2 * lane + 1] = o1;
     }
     if (a.xa) {
-        // block b = lane / 16 holds dims 32 b + 2 (lane % 16) and + 1
+        // block b = lane / 16 holds dims 32 b + 2 (lane % 16) and + 1: elements e, e + 1 of block 4 h + b, stored in
+        // the operand's fragment order (q / 16 for elements 16..31), with the block's scale and correction
         float amax = fmaxf(fabsf(o0), fabsf(o1));
         for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
         const float d = amax / 127.f;
         const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
         const int b = lane >> 4, e = 2 * (lane & 15);
-        const int gg = e < 16 ? e / 4 : (e - 16) / 4, j = e < 16 ? e % 4 : 4 + (e - 16) % 4;
+        const bool hi = e >= 16;
+        const int gg = (hi ? e - 16 : e) / 4, j = (hi ? 4 : 0) + e % 4;
         const int K = a.H * ATT_D, blk = h * 4 + b;
-        uint8_t* frag = a.xa + xa_frag_off(K, r >> 4, blk) + 16 * ((r & 15) + 16 * gg) + 2 * j;
-        const half2v q = {(_Float16) __builtin_rintf(o0 * id), (_Float16) __builtin_rintf(o1 * id)};
-        *(half2v*) frag = q;
-        if ((lane & 15) == 0) *((_Float16*) (a.xa + xa_scale_off(a.n_rows, K, r >> 4, blk)) + (r & 15)) = (_Float16) d;
+        const float q0 = __builtin_rintf(o0 * id), q1 = __builtin_rintf(o1 * id);
+        const float sc = hi ? 0.0625f : 1.0f;
+        uint8_t* rec = a.xa + xa_rec_off(K, r, blk);
+        *(half2v*) (rec + b * 1024 + 16 * ((r & 15) + 16 * gg) + 2 * j) = (half2v){(_Float16) (q0 * sc), (_Float16) (q1 * sc)};
+        float slo = hi ? 0.0f : q0 + q1, shi = hi ? q0 + q1 : 0.0f;
+        for (int off = 1; off < 16; off <<= 1) {
+            slo += __shfl_xor(slo, off);
+            shi += __shfl_xor(shi, off);
+        }
+        if ((lane & 15) == 0) {
+            *(float*) (rec + XA_DX_OFF + b * 64 + 4 * (r & 15)) = (float) (_Float16) d;
+            *(float*) (rec + XA_CORR_OFF + b * 64 + 4 * (r & 15)) = -(1032.0f * slo + 72.0f * shi);
+        }
     }
 }
 

@@ -4,12 +4,13 @@
 // mvm_q4_0_*, :746-1007 qmm_ks/qmmh_ks_q4_0_*, dispatched by mm() in core_mm.inc.h:307-325), with ggml's CPU numerics
 // (Q8_0-quantized activations, integer block sums scaled by dw*dx) instead of the reference's fp16 weights.
 //
-// How a block's sum is formed: the weights' (q4 - 8) and the activations' q8 are exact in fp16, and
-// v_mfma_f32_16x16x32_f16 multiplies exactly and accumulates in fp32, where every partial sum of a block (|sum| <=
-// 32512) is an exact integer: the MFMA gives ggml's integer block sum isum. One fma per output then adds
-// isum * (dw * dx) (the product of two fp16 values is exact in fp32) to the fp32 accumulator. The order of the sums
-// of an output is fixed by (N, K) alone, never by the number of rows, so a row's result is the same in any step
-// (sn.h:1-3).
+// How a block's sum is formed: the activation operand holds the Q8_0 integers q as fp16 (exact; q / 16 for the
+// elements that pair with high nibbles), the weights are unpacked to fp16 (1024 + w) or (1024 + 16 w), and
+// v_mfma_f32_16x16x32_f16 multiplies exactly and accumulates in fp32 with a per-row integer correction as its C input;
+// every partial sum is an integer below 2^23, so the MFMA gives ggml's integer block sum isum = sum q (w - 8) exactly.
+// One fma per output then adds isum * (dw * dx) (the product of two fp16 values is exact in fp32) to the fp32
+// accumulator. The order of the sums of an output is fixed by (N, K) alone, never by the number of rows, so a row's
+// result is the same in any step (sn.h:1-3).
 #include <algorithm>
 
 #include "sn_kernels_internal.h"
@@ -56,7 +57,8 @@ __device__ __forceinline__ float block_reduce_sum256(float v, float* red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-__device__ __forceinline__ void q8_store(const float* v, int g, uint8_t* frag, _Float16* dsl);
+__device__ __forceinline__ void q8_store(const float* v, int g, uint8_t* xa, int K, int m, int b);
+__device__ __forceinline__ void q8_zero(int g, uint8_t* xa, int K, int m, int b);
 
 // Four lanes per 32-block: lane part g holds the block's elements {4g..4g+3, 16+4g..16+4g+3}, which is exactly its
 // 8-value fragment of the MFMA operand, so each lane writes one 16-byte hi and one 16-byte lo fragment. The block's
@@ -71,8 +73,7 @@ __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, 
     if (src < 0) {  // a zero row (padding of an expert's tile)
         const int b = blockIdx.y * 64 + (t >> 2), g = t & 3;
         if (b >= xa_nbp(K)) return;
-        *(half8*) (xa + xa_frag_off(K, m >> 4, b) + 16 * ((m & 15) + 16 * g)) = (half8){};
-        if (g == 0) *((_Float16*) (xa + xa_scale_off(M, K, m >> 4, b)) + (m & 15)) = (_Float16) 0.0f;
+        q8_zero(g, xa, K, m, b);
         return;
     }
     const float* x = X + (size_t) src * ldx;
@@ -86,11 +87,8 @@ __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, 
     const int nbp = xa_nbp(K);
     const int b = blockIdx.y * 64 + (t >> 2), g = t & 3;
     if (b >= nbp) return;  // (whole 4-lane groups leave together: the shuffles below stay within a group)
-    uint8_t* frag = xa + xa_frag_off(K, m >> 4, b) + 16 * ((m & 15) + 16 * g);
-    _Float16* dsl = (_Float16*) (xa + xa_scale_off(M, K, m >> 4, b)) + (m & 15);
     if (b >= nb) {  // a padding block of the last 4-block group: zero
-        *(half8*) frag = (half8){};
-        if (g == 0) *dsl = (_Float16) 0.0f;
+        q8_zero(g, xa, K, m, b);
         return;
     }
     const float4 lo4 = *(const float4*) (x + 32 * b + 4 * g), hi4 = *(const float4*) (x + 32 * b + 16 + 4 * g);
@@ -105,13 +103,14 @@ __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, 
         *(float4*) (o + 4 * g) = (float4){v[0], v[1], v[2], v[3]};
         *(float4*) (o + 16 + 4 * g) = (float4){v[4], v[5], v[6], v[7]};
     }
-    q8_store(v, g, frag, dsl);
+    q8_store(v, g, xa, K, m, b);
 }
 
 // Row m, block b of a Q8_0 operand from its 32 fp32 values (this lane's 8: elements 4g..4g+3, 16+4g..16+4g+3):
 // ggml x86 quantize_row_q8_0, d = amax / 127 (stored fp16), q = round-half-even(x * 127 / amax). The 4 lanes of a
-// block are adjacent (the shuffles stay within them).
-__device__ __forceinline__ void q8_store(const float* v, int g, uint8_t* frag, _Float16* dsl) {
+// block are adjacent (the shuffles stay within them). Writes the lane's fragment slice (q, and q / 16 for elements
+// 16..31) and, from lane part 0, the block's scale and correction (see sn_common.h).
+__device__ __forceinline__ void q8_store(const float* v, int g, uint8_t* xa, int K, int m, int b) {
     float amax = 0.0f;
     for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
     amax = fmaxf(amax, __shfl_xor(amax, 1));
@@ -119,9 +118,33 @@ __device__ __forceinline__ void q8_store(const float* v, int g, uint8_t* frag, _
     const float d = amax / 127.f;
     const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
     half8 q;
-    for (int j = 0; j < 8; ++j) q[j] = (_Float16) __builtin_rintf(v[j] * id);
-    *(half8*) frag = q;
-    if (g == 0) *dsl = (_Float16) d;
+    float slo = 0.0f, shi = 0.0f;  // integer sums (exact in fp32)
+    for (int j = 0; j < 8; ++j) {
+        const float r = __builtin_rintf(v[j] * id);
+        q[j] = (_Float16) (j < 4 ? r : r * 0.0625f);
+        if (j < 4) slo += r;
+        else shi += r;
+    }
+    slo += __shfl_xor(slo, 1);
+    shi += __shfl_xor(shi, 1);
+    slo += __shfl_xor(slo, 2);
+    shi += __shfl_xor(shi, 2);
+    uint8_t* rec = xa + xa_rec_off(K, m, b);
+    *(half8*) (rec + (b & 3) * 1024 + 16 * ((m & 15) + 16 * g)) = q;
+    if (g == 0) {
+        *(float*) (rec + XA_DX_OFF + (b & 3) * 64 + 4 * (m & 15)) = (float) (_Float16) d;
+        *(float*) (rec + XA_CORR_OFF + (b & 3) * 64 + 4 * (m & 15)) = -(1032.0f * slo + 72.0f * shi);
+    }
+}
+
+// a zero block (padding, or a zero row of an expert's tile)
+__device__ __forceinline__ void q8_zero(int g, uint8_t* xa, int K, int m, int b) {
+    uint8_t* rec = xa + xa_rec_off(K, m, b);
+    *(half8*) (rec + (b & 3) * 1024 + 16 * ((m & 15) + 16 * g)) = (half8){};
+    if (g == 0) {
+        *(float*) (rec + XA_DX_OFF + (b & 3) * 64 + 4 * (m & 15)) = 0.0f;
+        *(float*) (rec + XA_CORR_OFF + (b & 3) * 64 + 4 * (m & 15)) = 0.0f;
+    }
 }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *(const float4*) p; }
@@ -178,11 +201,8 @@ __global__ __launch_bounds__(1024) void k_resid_quant(float* __restrict__ X, con
     for (int it = 0; it < IT; ++it) {
         const int b = t / 4 + bstep * it;
         if (b >= nbp) continue;
-        uint8_t* frag = xa + xa_frag_off(K, m >> 4, b) + 16 * ((m & 15) + 16 * g);
-        _Float16* dsl = (_Float16*) (xa + xa_scale_off(M, K, m >> 4, b)) + (m & 15);
         if (b >= nb) {  // a padding block of the last 4-block group: zero
-            *(half8*) frag = (half8){};
-            if (g == 0) *dsl = (_Float16) 0.0f;
+            q8_zero(g, xa, K, m, b);
             continue;
         }
         float y[8];
@@ -196,7 +216,7 @@ __global__ __launch_bounds__(1024) void k_resid_quant(float* __restrict__ X, con
             *(float4*) (o + 4 * g) = (float4){y[0], y[1], y[2], y[3]};
             *(float4*) (o + 16 + 4 * g) = (float4){y[4], y[5], y[6], y[7]};
         }
-        q8_store(y, g, frag, dsl);
+        q8_store(y, g, xa, K, m, b);
     }
 }
 
@@ -210,11 +230,8 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ 
     const int nb = F / 32, nbp = xa_nbp(F);
     const int b = blockIdx.y * 64 + (t >> 2), g = t & 3;
     if (b >= nbp) return;
-    uint8_t* frag = xa + xa_frag_off(F, m >> 4, b) + 16 * ((m & 15) + 16 * g);
-    _Float16* dsl = (_Float16*) (xa + xa_scale_off(M, F, m >> 4, b)) + (m & 15);
     if (b >= nb) {
-        *(half8*) frag = (half8){};
-        if (g == 0) *dsl = (_Float16) 0.0f;
+        q8_zero(g, xa, F, m, b);
         return;
     }
     // elements 32b + 4g + j (pair 2b) and 32b + 16 + 4g + j (pair 2b + 1): gate at 64b + 4g (+32), up 16 further
@@ -229,50 +246,60 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ 
         *(float4*) (o + 4 * g) = (float4){v[0], v[1], v[2], v[3]};
         *(float4*) (o + 16 + 4 * g) = (float4){v[4], v[5], v[6], v[7]};
     }
-    q8_store(v, g, frag, dsl);
+    q8_store(v, g, xa, F, m, b);
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
 // the matmul
+
+// A weight lane's 4 bytes (one block: byte j holds element j in its low nibble, j + 16 in its high nibble) as the MFMA
+// operand in the lane order of the activation fragments: fp16 (1024 + w) for elements 4g..4g+3 and (1024 + 16 w) for
+// 16+4g..16+4g+3, built by two masks and four byte permutes (0x64 is the high byte of fp16 1024).
 __device__ __forceinline__ half8 q4_unpack(uint32_t w) {
-    // (q - 8) of the 8 nibbles of w as fp16: low nibbles are elements 4g..4g+3, high nibbles 16+4g..16+4g+3.
-    // 0x6400 | q is fp16(1024 + q); subtracting 1032 is exact.
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;
     const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u);
     const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u);
     const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u);
     const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u);
-    const half2v off = {(_Float16) 1032.0f, (_Float16) 1032.0f};
-    const half2v h0 = __builtin_bit_cast(half2v, p0) - off;
-    const half2v h1 = __builtin_bit_cast(half2v, p1) - off;
-    const half2v h2 = __builtin_bit_cast(half2v, p2) - off;
-    const half2v h3 = __builtin_bit_cast(half2v, p3) - off;
-    half8 r;
-    r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
-    r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
-    return r;
+    return __builtin_bit_cast(half8, (u32x4){p0, p1, p2, p3});
 }
 
-// One workgroup (4 wavefronts) owns a set of 4 consecutive 16-row stripes (wavefront w: stripe 4 set + w) and a
-// k-slice of consecutive 4-block groups; the four wavefronts walk the slice's groups together, so a group's activation
-// operand (MT row tiles x 4 blocks: 1 KB fragments and fp16 scales) is loaded from global memory once per workgroup:
-// each wavefront loads MT fragments of it (wavefront 0 also the scales) into a register ring D groups ahead and stages
-// them into an LDS double buffer one group ahead (scales as fp32). The weight tiles go straight from global memory into
-// a ring of D groups of registers, so each wavefront keeps D tiles of its stripe in flight. Loads are issued in group
-// order (activations before weights), the order they are used in: vmcnt counts in issue order, so waiting for the
-// oldest group leaves the newer ones in flight. Every load is unconditional: stripes past the matrix are clamped to its
-// last stripe (their sums are never stored) and groups past the slice repeat its last group (cache hits), so no load
-// sits behind a branch.
+#define RSRC_WORD3 0x00020000  // raw buffer resource, gfx9 data format
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short) 0, (int) bytes, RSRC_WORD3);
+}
+__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
+}
+__device__ __forceinline__ u32x2 bload8(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0));
+}
+__device__ __forceinline__ float bload4f(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
+}
+
+// One workgroup (4 wavefronts) owns a set of 4 S consecutive 16-row stripes (wavefront w: stripes S w .. S w + S - 1 of
+// the set; S = 2, or 1 for narrow matrices), MT row tiles and a k-slice of consecutive 4-block groups, which the 4 wavefronts walk together. Per group:
+//   - the activation records of the MT row tiles (MT x 4 KB of fragments, MT x 512 B of scales and corrections) are
+//     loaded from global memory once per workgroup, each wavefront a quarter, into a register slot, and staged into an
+//     LDS double buffer one group ahead;
+//   - each wavefront's S weight tiles go from global memory into a register slot; the ring has D = 2 slots, so the
+//     loads of the next group are in flight while a group is summed.
+// Every load is a buffer load with a per-lane offset and a wavefront-uniform (scalar) one, issued without a branch:
+// groups past the slice repeat its last group and are added with scale 0; stripes past the matrix read as zero (the
+// buffer's size stops them) and are not stored. Each block is one MFMA per (row tile, stripe) with the correction as
+// its C input, then acc += isum * (dw * dx) (an exact product of two fp16 values), the arithmetic of ggml's
+// vec_dot_q4_0_q8_0. Scheduling fences keep the loads of each ring slot in issue order, so the wait before a slot
+// leaves the other slot's loads in flight.
 //
 // The kernel writes each slice's raw fp32 sums, part[slice][M][N]; whoever consumes them adds the slices in slice
 // order (k_q4_reduce here; the row kernels of the step), so the order of every sum is fixed by (N, K) alone.
-template <int MT, int D>
-__global__ __launch_bounds__(256) void k_q4_gemm(GemmArgs a) {
-    static_assert(D >= 2, "ring of at least two groups");
-    constexpr int U = D % 2 ? 2 * D : D;  // unroll: a multiple of the ring and of the LDS double buffer
+template <int MT, int S>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_q4_gemm(GemmArgs a) {
+    constexpr int D = 2, FPW = MT;  // ring slots, fragments each wavefront stages
     __shared__ __attribute__((aligned(16))) uint8_t s_act[2][MT * 4][1024];
-    __shared__ __attribute__((aligned(16))) float s_sc[2][MT * 64];  // tile mt: [block][row] as fp32
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ __attribute__((aligned(16))) float s_k[2][MT][2][64];  // [buffer][row tile][dx, corr][block * 16 + row]
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n_in = lane & 15, g = lane >> 4;
     const int set = blockIdx.x, slice = blockIdx.y;
     int mt0 = blockIdx.z * MT;
@@ -282,78 +309,92 @@ __global__ __launch_bounds__(256) void k_q4_gemm(GemmArgs a) {
         wbase = a.w + (size_t) a.items[2 * blockIdx.z] * a.wstride;
         mt0 = a.items[2 * blockIdx.z + 1];
     }
-    const int stripe = set * 4 + wave;
+    mt0 = __builtin_amdgcn_readfirstlane(mt0);
     const int c0 = slice * a.gps, ng = min(a.gps, a.ngroups - c0);  // groups c0 .. c0 + ng - 1 (ng >= 1)
+    const int s0 = set * (4 * S) + wave * S;
+    const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(S, a.nstripes - s0)));
+    const int sbytes = a.ngroups * Q4T_BYTES;  // one stripe
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(wbase + (size_t) min(s0, a.nstripes - 1) * sbytes, (uint32_t) (nvalid * sbytes));
+    const size_t x0 = (size_t) mt0 * a.ngroups * XA_REC;
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xa + x0, (uint32_t) (xa_bytes(a.M, a.K) - x0));
+    const int rstride = a.ngroups * XA_REC;  // between row tiles' records
+    // what this wavefront stages: fragments f = wave * FPW + j (row tile f / 4, block f % 4); constant block kb =
+    // wave (row tile kb / 2; dx or corr) while kb < 2 MT
+    const int kb = min(wave, 2 * MT - 1);
 
-    const uint8_t* wp = wbase + (size_t) min(stripe, a.nstripes - 1) * a.ngroups * Q4T_BYTES;
-    // activation fragment f = wave * MT + j of a group: row tile mt0 + f / 4, block f % 4
-    const uint8_t* af[MT];
-    for (int j = 0; j < MT; ++j) {
-        const int f = wave * MT + j;
-        af[j] = a.xa + xa_frag_off(a.K, mt0 + f / 4, f % 4) + 16 * lane;
-    }
-    // scales: lane l < 32 MT loads dword l % 32 of row tile mt0 + l / 32 (its 4 blocks' 128 B are contiguous)
-    const int sl = lane < 32 * MT ? lane : 0;
-    const uint8_t* asp = a.xa + xa_scale_off(a.M, a.K, mt0 + sl / 32, 0) + 4 * (sl % 32);
-
-    u32x4 wq[D];
-    half4v ws[D];
-    u32x4 ra[D][MT];
-    uint32_t rs[D];
-    floatx4 acc[MT];
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = (floatx4){0.f, 0.f, 0.f, 0.f};
-    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+    u32x4 wq[D][S];
+    u32x2 ws[D][S];
+    u32x4 ra[D][FPW];
+    float rk[D];
+    floatx4 acc[S][MT];
+    for (int s = 0; s < S; ++s)
+        for (int mt = 0; mt < MT; ++mt) acc[s][mt] = (floatx4){0.f, 0.f, 0.f, 0.f};
 
     auto load = [&](int slot, int i) {
         const int c = c0 + min(i, ng - 1);
-        for (int j = 0; j < MT; ++j) ra[slot][j] = *(const u32x4*) (af[j] + (size_t) c * 4 * XA_FRAG_BYTES);
-        rs[slot] = *(const uint32_t*) (asp + (size_t) c * 128);
-        const size_t off = (size_t) c * Q4T_BYTES;
-        wq[slot] = *(const u32x4*) (wp + off + 16 * lane);
-        ws[slot] = *(const half4v*) (wp + off + Q4T_SCALE_OFF + 8 * n_in);
-    };
-    auto stage = [&](int buf, int slot) {
-        for (int j = 0; j < MT; ++j) *(u32x4*) (&s_act[buf][wave * MT + j][16 * lane]) = ra[slot][j];
-        if (wave == 0 && lane < 32 * MT) {
-            // dword l % 32 of tile l / 32 holds fp16 [block][row] entries 2 (l % 32) and 2 (l % 32) + 1
-            const half2v h = __builtin_bit_cast(half2v, rs[slot]);
-            *(float2*) &s_sc[buf][(lane / 32) * 64 + 2 * (lane % 32)] = (float2){(float) h[0], (float) h[1]};
+        for (int j = 0; j < FPW; ++j) {
+            const int f = wave * FPW + j;
+            ra[slot][j] = bload16(xr, 16 * lane, (f / 4) * rstride + c * XA_REC + (f % 4) * 1024);
+        }
+        rk[slot] = bload4f(xr, 4 * lane, (kb / 2) * rstride + c * XA_REC + XA_DX_OFF + (kb % 2) * 256);
+        for (int s = 0; s < S; ++s) {
+            const int so = s * sbytes + c * Q4T_BYTES;
+            wq[slot][s] = bload16(wr, 16 * lane, so);
+            ws[slot][s] = bload8(wr, Q4T_SCALE_OFF + 8 * n_in, so);
         }
     };
-    auto compute = [&](int slot, int buf) {
+    auto stage = [&](int buf, int slot) {
+        for (int j = 0; j < FPW; ++j) *(u32x4*) &s_act[buf][wave * FPW + j][16 * lane] = ra[slot][j];
+        if (wave < 2 * MT) s_k[buf][kb / 2][kb % 2][lane] = rk[slot];
+    };
+    auto compute = [&](int slot, int buf, float m) {
         for (int b = 0; b < 4; ++b) {
-            const half8 bw = q4_unpack(wq[slot][b]);
-            const float dw = (float) ws[slot][b];
+            half8 A[MT];
+            floatx4 dx[MT], cr[MT];
             for (int mt = 0; mt < MT; ++mt) {
-                const half8 A = *(const half8*) (&s_act[buf][mt * 4 + b][16 * lane]);
-                const floatx4 dx = *(const floatx4*) &s_sc[buf][mt * 64 + b * 16 + 4 * g];
-                const floatx4 isum = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bw, zero, 0, 0, 0);
-                for (int v = 0; v < 4; ++v) acc[mt][v] = __builtin_fmaf(isum[v], dw * dx[v], acc[mt][v]);
+                A[mt] = *(const half8*) &s_act[buf][mt * 4 + b][16 * lane];
+                dx[mt] = *(const floatx4*) &s_k[buf][mt][0][b * 16 + 4 * g];
+                cr[mt] = *(const floatx4*) &s_k[buf][mt][1][b * 16 + 4 * g];
+            }
+            for (int s = 0; s < S; ++s) {
+                const half8 bw = q4_unpack(wq[slot][s][b]);
+                const float dw = (float) __builtin_bit_cast(half4v, ws[slot][s])[b] * m;
+                for (int mt = 0; mt < MT; ++mt) {
+                    const floatx4 isum = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], bw, cr[mt], 0, 0, 0);
+                    for (int v = 0; v < 4; ++v) acc[s][mt][v] = __builtin_fmaf(isum[v], dw * dx[mt][v], acc[s][mt][v]);
+                }
             }
         }
     };
 
-    for (int j = 0; j < D; ++j) load(j, j);
-    stage(0, 0);
-    for (int i0 = 0; i0 < ng; i0 += U) {
-        for (int j = 0; j < U; ++j) {
-            const int i = i0 + j;
-            if (i >= ng) break;
-            __syncthreads();  // group i is staged; everyone is done reading the buffer group i + 1 goes to
-            stage((j + 1) % 2, (j + 1) % D);
-            compute(j % D, j % 2);
-            load(j % D, i + D);
-        }
+    for (int j = 0; j < D; ++j) {
+        load(j, j);
+        __builtin_amdgcn_sched_barrier(0);
     }
-
-    // lane (n, g) holds rows 4g + v of each row tile, column n of the stripe
-    const int col = stripe * 16 + n_in;
-    if (stripe >= a.nstripes || col >= a.N) return;
-    for (int mt = 0; mt < MT; ++mt)
-        for (int v = 0; v < 4; ++v) {
-            const int row = (mt0 + mt) * 16 + 4 * g + v;
-            if (row < a.M) a.part[((size_t) slice * a.M + row) * a.N + col] = acc[mt][v];
+    stage(0, 0);
+    const int trips = (ng + D - 1) / D;
+    for (int t = 0; t < trips; ++t)
+        for (int j = 0; j < D; ++j) {
+            const int i = t * D + j;
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();  // group i is staged in buffer j; everyone is done reading buffer j ^ 1
+            stage(j ^ 1, j ^ 1);  // group i + 1 (its registers: slot (i + 1) % D)
+            __builtin_amdgcn_sched_barrier(0);
+            compute(j, j, i < ng ? 1.0f : 0.0f);
+            __builtin_amdgcn_sched_barrier(0);
+            load(j, i + D);
         }
+
+    // lane (n, g) holds rows 4g + v of each row tile, column n of each of its stripes
+    for (int s = 0; s < S; ++s) {
+        const int stripe = s0 + s, col = stripe * 16 + n_in;
+        if (stripe >= a.nstripes || col >= a.N) continue;
+        for (int mt = 0; mt < MT; ++mt)
+            for (int v = 0; v < 4; ++v) {
+                const int row = (mt0 + mt) * 16 + 4 * g + v;
+                if (row < a.M) a.part[((size_t) slice * a.M + row) * a.N + col] = acc[s][mt][v];
+            }
+    }
 }
 
 // k-slice partial sums added in slice order, then the epilogue
@@ -381,19 +422,24 @@ __global__ void k_q4_reduce(GemmArgs a) {
 // ---------------------------------------------------------------------------------------------------------------------
 // host side
 
-// The launch shape depends on (N, K) only, never on the rows (row invariance): 4 stripes per workgroup, and k-slices
-// across workgroups while there are fewer than 512 workgroups, at most KS_MAX slices. 512 is two workgroups per CU:
-// a launch of 256-511 workgroups leaves CUs holding one next to CUs holding two (gate/up at 304 sets: 19.6 us at
-// one slice, 15.5 us at two, M = 32 on MI355X), while more slices mean more partial sums for the consumer to add.
+// The launch shape depends on (N, K) only, never on the rows (row invariance): 4 spw stripes per workgroup (spw = 1 for
+// matrices too narrow to give 64 sets of 8),
+// and the groups of K in slices across workgroups. A slice holds an even number of groups (the kernel walks groups in
+// pairs, one per ring slot; an odd count would add a masked pass), halved from the whole of K while the launch has
+// fewer than 768 workgroups, down to 4 groups and at most KS_MAX slices: on MI355X at 32 rows, short slices (a single
+// round of loads per workgroup) beat fewer, longer workgroups for the layer-sized matrices, while every slice costs
+// the consumer one more partial sum to read.
 GemmPlan q4_plan(int N, int K) {
     GemmPlan p;
     p.nstripes = (N + 15) / 16;
     p.ngroups = (K / 32 + 3) / 4;
-    p.sets = (p.nstripes + 3) / 4;
-    int ks = 1;
-    while (p.sets * ks < 512 && ks < p.ngroups && ks < KS_MAX) ++ks;
-    p.gps = (p.ngroups + ks - 1) / ks;
-    p.ks = (p.ngroups + p.gps - 1) / p.gps;
+    p.spw = p.nstripes >= 64 * 2 * 4 ? 2 : 1;  // stripes per wavefront: 1 while 2 would leave fewer than 64 sets
+    p.sets = (p.nstripes + 4 * p.spw - 1) / (4 * p.spw);
+    auto slices = [&](int gps) { return (p.ngroups + gps - 1) / gps; };
+    int gps = (p.ngroups + 1) / 2 * 2;
+    while (gps > 4 && p.sets * slices(gps) < 768 && slices(gps - 2) <= KS_MAX) gps -= 2;
+    p.gps = gps;
+    p.ks = slices(gps);
     return p;
 }
 
@@ -409,8 +455,14 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
     a.M = M; a.N = N; a.K = K; a.ldy = 0; a.epi = EPI_STORE;
     a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
     a.mtiles = (M + 15) / 16;
-    if (a.mtiles == 1) hipLaunchKernelGGL((k_q4_gemm<1, 4>), dim3(p.sets, p.ks, 1), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_q4_gemm<2, 4>), dim3(p.sets, p.ks, (a.mtiles + 1) / 2), dim3(256), 0, st, a);
+    const dim3 g1(p.sets, p.ks, 1), g2(p.sets, p.ks, (a.mtiles + 1) / 2);
+    if (a.mtiles == 1) {
+        if (p.spw == 2) hipLaunchKernelGGL((k_q4_gemm<1, 2>), g1, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_q4_gemm<1, 1>), g1, dim3(256), 0, st, a);
+    } else {
+        if (p.spw == 2) hipLaunchKernelGGL((k_q4_gemm<2, 2>), g2, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_q4_gemm<2, 1>), g2, dim3(256), 0, st, a);
+    }
     return p.ks;
 }
 
@@ -424,7 +476,7 @@ int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, cons
     a.M = M; a.N = N; a.K = K; a.epi = EPI_STORE;
     a.nstripes = (N + 15) / 16; a.ngroups = (K / 32 + 3) / 4; a.ks = 1; a.gps = a.ngroups;
     a.mtiles = (M + 15) / 16;
-    hipLaunchKernelGGL((k_q4_gemm<1, 4>), dim3((a.nstripes + 3) / 4, 1, max_items), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((k_q4_gemm<1, 1>), dim3((a.nstripes + 3) / 4, 1, max_items), dim3(256), 0, st, a);
     return 1;
 }
 
@@ -502,10 +554,11 @@ __global__ void k_q4_dequant(const uint8_t* __restrict__ w, int N, int K, float*
     for (int b = 0; b < 4; ++b) {
         const int blk = 4 * grp + b;
         if (row >= N || blk >= nb) continue;
-        const half8 q = q4_unpack(wq[b]);
+        const half8 q = q4_unpack(wq[b]);  // (1024 + w) for elements 4g.., (1024 + 16 w) for 16 + 4g..
         for (int j = 0; j < 8; ++j) {
             const int e = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
-            out[(size_t) row * K + 32 * blk + e] = (float) q[j] * dw[b];
+            const float w8 = j < 4 ? (float) q[j] - 1032.0f : ((float) q[j] - 1152.0f) * 0.0625f;  // w - 8, exactly
+            out[(size_t) row * K + 32 * blk + e] = w8 * dw[b];
         }
     }
 }

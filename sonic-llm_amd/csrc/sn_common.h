@@ -41,25 +41,29 @@ void sn_set_err(char* err, int err_len, const char* fmt, ...);
 
 // ---- activation operand ("xa"): Q8_0-quantized rows as fp16 MFMA fragments -----------------------------------------
 // Rows are quantized to Q8_0 exactly as ggml's x86 CPU backend does (per 32-block: d = amax/127 stored fp16,
-// q = round-half-even(x * 127/amax)). The integers q (|q| <= 127) are held as fp16, which is exact, so an fp16 MFMA of
-// them against the weights' (q4 - 8) forms the block's integer sum exactly (every partial sum < 2^24); the scale d is
-// kept beside them in fp16.
-// Fragments: for row tile mt (16 rows) and block b, 1024 bytes; lane l = m + 16 g holds the q of elements
-// {4g..4g+3, 16+4g..16+4g+3} of row m (the same order as the weight tile lanes), so one 16-byte load per lane is the A
-// operand of v_mfma_f32_16x16x32_f16. Scales: for (mt, b), the 16 rows' d as fp16 (32 bytes), after all fragments.
-// A row tile holds xa_nbp(K) blocks (K/32 rounded up to a multiple of 4; the extra blocks are zero) and row tiles are
-// rounded up to an even count, so the matmul's loads of a 4-block group of 2 row tiles never leave the buffer.
-#define XA_FRAG_BYTES 1024
+// q = round-half-even(x * 127/amax)). The operand is a sequence of records, one per (16-row tile mt, 4-block group c),
+// tile-major: record (mt, c) starts at (mt * xa_ngroups(K) + c) * XA_REC. A record holds, for blocks 4c + bb:
+//   [bb * 1024, +1024)   the fragment of block 4c + bb: lane l = m + 16 g holds row m's elements 4g..4g+3 as q and
+//                        16+4g..16+4g+3 as q / 16 (8 fp16, all exact; the order of the weight tile lanes);
+//   [4096 + bb * 64, +64) the 16 rows' scales d as fp32 (the fp16 value, exactly);
+//   [4352 + bb * 64, +64) the 16 rows' corrections -(1032 * sum of q over elements 0..15 + 72 * sum over 16..31), an
+//                        exact integer.
+// The matmul unpacks a weight nibble w to fp16 (1024 + w) for elements 0..15 and (1024 + 16 w) for 16..31; an fp16
+// MFMA of a fragment against them, with the correction as its C input, is sum q (w - 8), ggml's integer block sum,
+// exactly: every term and every partial sum is an integer below 2^23 in magnitude.
+// Row tiles are rounded up to an even count and blocks to whole groups; padding blocks are zero.
+#define XA_REC 4608
+#define XA_DX_OFF 4096
+#define XA_CORR_OFF 4352
 
 __host__ __device__ static inline int xa_nbp(int K) { return (K / 32 + 3) / 4 * 4; }
+__host__ __device__ static inline int xa_ngroups(int K) { return (K / 32 + 3) / 4; }
 __host__ __device__ static inline int xa_mtp(int M) { return (M + 31) / 32 * 2; }
-__host__ __device__ static inline size_t xa_frag_off(int K, int mt, int b) {
-    return ((size_t) mt * xa_nbp(K) + b) * XA_FRAG_BYTES;
+// the record holding row m, block b
+__host__ __device__ static inline size_t xa_rec_off(int K, int m, int b) {
+    return ((size_t) (m >> 4) * xa_ngroups(K) + (b >> 2)) * XA_REC;
 }
-__host__ __device__ static inline size_t xa_scale_off(int M, int K, int mt, int b) {
-    return (size_t) xa_mtp(M) * xa_nbp(K) * XA_FRAG_BYTES + ((size_t) mt * xa_nbp(K) + b) * 32;
-}
-static inline size_t xa_bytes(int M, int K) { return (size_t) xa_mtp(M) * xa_nbp(K) * (XA_FRAG_BYTES + 32); }
+__host__ __device__ static inline size_t xa_bytes(int M, int K) { return (size_t) xa_mtp(M) * xa_ngroups(K) * XA_REC; }
 static inline size_t q4t_bytes(int N, int K) { return (size_t) ((N + 15) / 16) * ((K / 32 + 3) / 4) * Q4T_BYTES; }
 
 // The sum, in slice order, of ks <= KM k-slices of a matmul (slice k at p + k * stride). Every load is issued before

@@ -18,9 +18,10 @@ struct GemmArgs {
     int nstripes, ngroups, ks, gps, mtiles;
 };
 
-// Launch shape of one matrix: a workgroup owns 4 stripes (a "set") and gps consecutive 4-block groups (a slice).
+// Launch shape of one matrix: a workgroup owns 4 spw stripes (a "set": spw per wavefront) and gps consecutive 4-block
+// groups (a slice).
 struct GemmPlan {
-    int nstripes, ngroups, sets, ks, gps;
+    int nstripes, ngroups, spw, sets, ks, gps;
 };
 
 // Depends on (N, K) only, never on the rows.
