@@ -131,7 +131,9 @@ def main():
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     value = B * args.steps / dt
-    log(f"[bench] {args.steps} steps: {dt * 1e3 / args.steps:.3f} ms/step wall, {gpu_ms / args.steps:.3f} ms/step GPU")
+    caps, reps = eng.graph_count()
+    log(f"[bench] {args.steps} steps: {dt * 1e3 / args.steps:.3f} ms/step wall, {gpu_ms / args.steps:.3f} ms/step GPU "
+        f"(graph captures {caps}, replays {reps})")
 
     # profiled pass: per-kernel-class time and algorithmic bytes
     eng.prof(True)

@@ -29,6 +29,14 @@ void snx_prof(sn_engine* e, int on);
 // (sequence, KV head) reads once + q + output + page-table entries). 0, or -1 for an unknown class.
 int snx_prof_read(const sn_engine* e, int kind, double* ms, int* launches, double* bytes);
 
+// Graph replay of steps on (the default) or off. While on, sn_step captures its device work as a HIP graph the first
+// time a step shape occurs (rows, outputs, attention work-list size, ...) and replays it while the shape repeats,
+// which saves the per-launch cost of ~370 launches a step; the launches and results are the same as with it off.
+// Profiling (snx_prof) runs steps without graphs.
+void snx_graphs(sn_engine* e, int on);
+// Steps captured as a new graph (replays 0) or replayed from the cached one (replays 1) since the engine opened.
+long snx_graph_count(const sn_engine* e, int replays);
+
 // Give slot `slot` the cells [0, n) (pages as a step would take them) holding seeded N(0, 1) fp16 K and V in every
 // layer: a context "already in the cache" for throughput runs (what the cells hold does not change what a step
 // costs). The values depend only on (seed, slot, layer, cell). 0, -2 out of pages, or -1 (err).

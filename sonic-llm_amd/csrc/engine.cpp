@@ -97,6 +97,14 @@ struct sn_engine {
     double last_ms = 0.0;
     int guess_on = 0;
 
+    // the device work of the last step shape, captured as a HIP graph and replayed while the shape repeats: its key is
+    // every host value a launch of the step takes (row counts, work-list sizes, staging offsets), so a replay issues
+    // exactly the launches an eager step would
+    bool graphs = true;
+    std::vector<int64_t> graph_key;
+    hipGraphExec_t graph_exec = nullptr;
+    long graph_replays = 0, graph_captures = 0;
+
     // per-kernel-class profiling (sn_ext.h): event pairs around each launch while on
     struct ProfRec {
         int kind, e0, e1;
@@ -479,6 +487,7 @@ extern "C" void sn_close(sn_engine* e) {
     if (e->ev0) hipEventDestroy(e->ev0);
     if (e->ev1) hipEventDestroy(e->ev1);
     for (auto& ev : e->prof_ev) hipEventDestroy(ev);
+    if (e->graph_exec) hipGraphExecDestroy(e->graph_exec);
     if (e->st) hipStreamDestroy(e->st);
     delete e;
 }
@@ -919,6 +928,44 @@ int finish(sn_engine* e, int rc, char* err, int err_len) {
     return 0;
 }
 
+// Run a step's device work on the engine's stream: replayed from the cached graph when the key matches, else captured
+// into a new graph (replacing the cached one) and launched; run eagerly while profiling (events around each launch)
+// or if capture is not available. The work issues kernels only: no copies, memsets or waits. Returns the work's rc.
+template <class Work>
+int run_device(sn_engine* e, std::vector<int64_t>&& key, Work work) {
+    if (e->graphs && !e->prof_on) {
+        if (e->graph_exec && e->graph_key == key) {
+            ++e->graph_replays;
+            return hipGraphLaunch(e->graph_exec, e->st) == hipSuccess ? 0 : -1;
+        }
+        if (hipStreamBeginCapture(e->st, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+            Dev d{e, e->st};
+            work(d);
+            hipGraph_t g = nullptr;
+            const bool ok = hipStreamEndCapture(e->st, &g) == hipSuccess && g != nullptr;
+            if (ok && d.rc != 0) {
+                hipGraphDestroy(g);
+                return d.rc;
+            }
+            hipGraphExec_t ex = nullptr;
+            if (ok && hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) == hipSuccess) {
+                hipGraphDestroy(g);
+                if (e->graph_exec) hipGraphExecDestroy(e->graph_exec);
+                e->graph_exec = ex;
+                e->graph_key = std::move(key);
+                ++e->graph_captures;
+                return hipGraphLaunch(e->graph_exec, e->st) == hipSuccess ? 0 : -1;
+            }
+            if (g) hipGraphDestroy(g);
+        }
+        (void) hipGetLastError();  // capture unavailable: eager from now on
+        e->graphs = false;
+    }
+    Dev d{e, e->st};
+    work(d);
+    return d.rc;
+}
+
 bool rows_bad(const sn_engine* e, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos) {
     for (int r = 0; r < R; ++r)
         if (seq[r] < 0 || seq[r] >= e->slots || pos[r] < 0 || pos[r] >= e->ctx || tok[r] < 0 || tok[r] >= e->V)
@@ -975,17 +1022,22 @@ extern "C" int sn_step(sn_engine* e, int R, const int32_t* tok, const int32_t* s
     const int32_t* d_seq = S.dev<const int32_t>(o_seq);
     const int32_t* d_pos = S.dev<const int32_t>(o_pos);
 
-    Dev d{e, e->st};
-    d.model(R, d_tok, d_seq, d_pos, S, al);
-    if (fill && d.rc == 0)
-        d.head_fill(R, d_tok, d_seq, d_pos, S.dev<const int32_t>(o_src), (int) keep.size() / 2, S.dev<const int32_t>(o_keep));
-    if (n_out > 0 && d.rc == 0) {
-        d.outputs(e->x, n_out, S.dev<const int32_t>(o_out), S.dev<const uint8_t>(o_skip));
+    std::vector<int64_t> key = {1, R, n_out, fill, e->want_probs, (int64_t) e->eog.size(), (int64_t) keep.size(),
+                                (int64_t) o_tok, (int64_t) o_seq, (int64_t) o_pos, (int64_t) o_out, (int64_t) o_skip,
+                                (int64_t) al.o_grp, (int64_t) al.o_itm, al.n_items, (int64_t) o_src, (int64_t) o_keep};
+    const int drc = run_device(e, std::move(key), [&](Dev& d) {
+        d.model(R, d_tok, d_seq, d_pos, S, al);
+        if (fill && d.rc == 0)
+            d.head_fill(R, d_tok, d_seq, d_pos, S.dev<const int32_t>(o_src), (int) keep.size() / 2,
+                        S.dev<const int32_t>(o_keep));
+        if (n_out > 0 && d.rc == 0) d.outputs(e->x, n_out, S.dev<const int32_t>(o_out), S.dev<const uint8_t>(o_skip));
+    });
+    if (drc == 0 && n_out > 0) {
         SN_HIP_TRY(hipMemcpyAsync(e->h_otok, e->d_otok, (size_t) n_out * 4, hipMemcpyDeviceToHost, e->st), -1);
         if (e->want_probs)
             SN_HIP_TRY(hipMemcpyAsync(e->h_rec, e->d_rec, (size_t) n_out * 32, hipMemcpyDeviceToHost, e->st), -1);
     }
-    if (finish(e, d.rc, err, err_len) != 0) return -1;
+    if (finish(e, drc, err, err_len) != 0) return -1;
     if (fill) note_runs(e, R, seq, pos);
     if (n_out > 0) memcpy(out_tok, e->h_otok, (size_t) n_out * 4);
     e->last_n_out = n_out;
@@ -1132,6 +1184,15 @@ extern "C" int snx_spec_step(sn_engine* e, int n, const int32_t* seq, const int3
 }
 
 extern "C" double sn_last_gpu_ms(const sn_engine* e) { return e->last_ms; }
+
+extern "C" long snx_graph_count(const sn_engine* e, int replays) { return replays ? e->graph_replays : e->graph_captures; }
+
+extern "C" void snx_graphs(sn_engine* e, int on) {
+    e->graphs = on != 0;
+    if (e->graph_exec) hipGraphExecDestroy(e->graph_exec);
+    e->graph_exec = nullptr;
+    e->graph_key.clear();
+}
 
 extern "C" void snx_prof(sn_engine* e, int on) {
     e->prof_on = on != 0;

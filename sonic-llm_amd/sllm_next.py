@@ -109,6 +109,8 @@ SNK_API = [
     ("snk_mfma_probe", I, [P, P, P, P]),
 ]
 EXT_API = [
+    ("snx_graphs", None, [P, I]),
+    ("snx_graph_count", C.c_long, [P, I]),
     ("snx_prof", None, [P, I]),
     ("snx_prof_read", I, [P, I, C.POINTER(C.c_double), C.POINTER(I), C.POINTER(C.c_double)]),
     ("snx_fill_kv", I, [P, I, I, C.c_uint64, CH, I]),
@@ -291,6 +293,14 @@ class Engine:
         call(self.L.snx_spec_step, self.e, n, _p(seq), _p(last), _p(pos), int(k), _p(fr) if fr is not None else None,
              _p(out_n), _p(out_tok))
         return out_n, out_tok
+
+    def graphs(self, on: bool):
+        """snx_graphs: replay each step shape's device work as a HIP graph (the default) or launch it eagerly."""
+        self.L.snx_graphs(self.e, int(on))
+
+    def graph_count(self) -> tuple:
+        """(steps captured as a new graph, steps replayed from the cached graph) since the engine opened."""
+        return self.L.snx_graph_count(self.e, 0), self.L.snx_graph_count(self.e, 1)
 
     def prof(self, on: bool):
         self.L.snx_prof(self.e, int(on))

@@ -200,3 +200,41 @@ def test_error_paths(tiny):
         assert eng.pages_free() == 0
         eng.clear(1, 0, 65)
         assert eng.pages_free() == 2
+
+
+def test_graph_replay_matches_eager(tiny):
+    """Steps replayed from the captured HIP graph give the same tokens and logits, bit for bit, as eager launches: over
+    repeated shapes (replays), shape changes (rows, outputs, a new 256-cell attention chunk: recaptures), with eager
+    cache operations (sn_copy, sn_clear) and host reads between the replays."""
+    r = np.random.default_rng(5)
+    V = TINY["n_vocab"]
+    with S.Engine(tiny, slots=4, ctx=512, max_rows=256) as ge, S.Engine(tiny, slots=4, ctx=512, max_rows=256) as ee:
+        ee.graphs(False)
+        prompt = r.integers(0, V, 250).astype(np.int32)
+        for eng in (ge, ee):  # a 250-cell prompt in slot 0 (one eager-equivalent step shape)
+            eng.step(prompt, np.zeros(250, np.int32), np.arange(250, dtype=np.int32), np.array([249], np.int32), n_write=0)
+        for eng in (ge, ee):
+            eng.copy(0, 1, 250)
+        pos = np.array([250, 250], np.int32)
+        tok = r.integers(0, V, 2).astype(np.int32)
+        n_steps = 0
+        for it in range(14):  # 2 rows crossing the 256-cell chunk boundary at position 256
+            seq = np.array([0, 1], np.int32)
+            outs = np.arange(2, dtype=np.int32) if it % 5 != 3 else np.array([1], np.int32)
+            tg = ge.step(tok, seq, pos, outs)
+            te = ee.step(tok, seq, pos, outs)
+            lg, le = ge.logits(list(range(len(outs)))), ee.logits(list(range(len(outs))))
+            assert np.array_equal(tg, te), (it, tg, te)
+            assert np.array_equal(lg.view(np.uint32), le.view(np.uint32)), it
+            n_steps += 1
+            if len(outs) == 2:
+                tok = tg.astype(np.int32)
+            pos = pos + 1
+            if it == 6:  # eager cache work between replays: cut slot 1 back one cell and rebuild it
+                for eng in (ge, ee):
+                    eng.clear(1, int(pos[1]) - 1, int(pos[1]))
+                pos[1] -= 1
+        assert n_steps == 14
+        caps, reps = ge.graph_count()
+        assert reps >= 5 and caps >= 3, (caps, reps)  # replays happened, and shape changes recaptured
+        assert ee.graph_count() == (0, 0)
