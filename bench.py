@@ -87,7 +87,21 @@ def main():
                     help="decode: the headline (configs[2]); mtp: the fused draft-verify step (configs[3]); "
                          "moe: Qwen3-30B-A3B-arch batched decode (configs[4])")
     ap.add_argument("--accept", type=float, default=0.6, help="mtp: the seeded share of drafts forced to match")
+    ap.add_argument("--no-graphs", action="store_true", help="launch every step eagerly (no HIP graph replay)")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device-to-device once (a plain copy kernel of known size, to scale "
+                         "rocprofv3's FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
+    if args.copy_calib:
+        import torch
+        n = args.copy_calib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copied {n} bytes device to device")
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (sequences would shard "
               f"across GPUs with no per-step exchange; see DESIGN.md)", file=sys.stderr)
@@ -107,6 +121,8 @@ def main():
     total = ctx + args.warmup + args.steps + args.prof_steps + 1
     t = time.time()
     eng = S.Engine(path, slots=B, ctx=total, max_rows=B)
+    if args.no_graphs:
+        eng.graphs(False)
     for s in range(B):
         eng.fill_kv(s, ctx, args.seed)
     log(f"[bench] engine open + {B} x {ctx} cells in {time.time() - t:.1f}s")
@@ -149,13 +165,21 @@ def main():
                              "bytes_per_launch": p["bytes"] / p["launches"], "us_per_launch": 1e3 * p["ms"] / p["launches"],
                              "GBps": gbs, "frac": gbs * 1e9 / HBM_PEAK}
     log("[bench] kernels " + json.dumps(kernels))
-    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
+    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"]) if kernels else None
+
+    # HBM bytes per launch of each class from the committed rocprofv3 counter runs of this workload (FETCH_SIZE and
+    # WRITE_SIZE, scaled by a copy of known size): profiles/decode_qwen3_4b_b32_ctx2048_traffic.md
+    traffic = {}
+    tpath = os.path.join(ROOT, "profiles", "decode_qwen3_4b_b32_ctx2048_traffic.json")
+    if not moe and (B, ctx) == (32, 2048) and os.path.exists(tpath):
+        traffic = json.load(open(tpath))
 
     def roof(k):
         c = kernels[k]
         return {"kernel": k, "bound": "hbm", "achieved": round(c["GBps"], 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": round(c["frac"], 4), "traffic": None, "bytes_per_launch": round(c["bytes_per_launch"]),
-                "us_per_launch": round(c["us_per_launch"], 2)}
+                "frac": round(c["frac"], 4), "traffic": round(traffic[k]) if k in traffic else None,
+                "bytes_per_launch": round(c["bytes_per_launch"]), "us_per_launch": round(c["us_per_launch"], 2),
+                **({"traffic_source": "profiles/decode_qwen3_4b_b32_ctx2048_traffic.md"} if k in traffic else {})}
 
     eng.close()
     cpu = None
@@ -179,7 +203,7 @@ def main():
                    **({"experts": cfg["n_expert"], "experts_used": cfg["n_expert_used"], "expert_ffn": cfg["n_ff_exp"]}
                       if moe else {}),
                    "gpu_ms_per_step": round(gpu_ms / args.steps, 4)},
-        "roofline": roof(dom),
+        "roofline": roof(dom) if dom else None,
         "roofline_gemm": roof("gemm") if "gemm" in kernels else None,
         "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
         "cpu_baseline": cpu,
