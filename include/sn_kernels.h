@@ -21,6 +21,17 @@ int snk_q4_repack(const void* d_q4, int N, int K, void* d_stripes, void* stream)
 // the stripes dequantized back to fp32 [N][K] with the matmul's own unpack (d * (q - 8)): for the bit-exactness check
 // against ggml's dequantize_row_q4_0
 int snk_q4_dequant(const void* d_stripes, int N, int K, float* d_w, void* stream);
+// Q8_0 weights (block_q8_0: fp16 d + 32 int8, w = d*q; the reference's mv_q8_0* kernels, kernels.metal:1995-2130,
+// and its Q8_0 cv_ks dequant, :597-609), with ggml's CPU numerics (vec_dot_q8_0_q8_0: Q8_0 activations, integer block
+// sums): bytes of the tile layout, GGUF Q8_0 rows -> tiles, the tiles dequantized back with the matmul's own unpack
+// (d * q, for the bit-exactness check against ggml's dequantize_row_q8_0), and the matmul (arguments as snk_q4_gemm).
+size_t snk_q8_tiles_bytes(int N, int K);
+int snk_q8_repack(const void* d_q8, int N, int K, void* d_tiles, void* stream);
+int snk_q8_dequant(const void* d_tiles, int N, int K, float* d_w, void* stream);
+size_t snk_q8_workspace_bytes(int M, int N, int K);
+int snk_q8_gemm(const void* d_tiles, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi, void* d_ws,
+                size_t ws_bytes, void* stream);
+
 // activation operand: M fp32 rows (ldx apart) quantized to Q8_0 (ggml x86 quantize_row_q8_0), RMS-normed by d_norm_w
 // first when it is not NULL (the rmsnorm of kernels.metal:121-140 fused in front)
 size_t snk_xa_bytes(int M, int K);

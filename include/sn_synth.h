@@ -13,16 +13,19 @@ typedef struct {
     int n_expert, n_expert_used, n_ff_exp;  // > 0: a qwen3moe model (experts in every layer)
     int nextn;                              // 1: one multi-token-prediction layer after the model's own (blk.<n_layer>)
     float rope_base, eps;
-    float w_std;    // std of the Q4_0 matrices before quantization (configs: 0.02)
+    float w_std;    // std of the matrices before quantization (configs: 0.02)
     float emb_std;  // std of the fp32 embedding table
+    int wtype;      // the matrices' block type: 2 (0 too) Q4_0, 8 Q8_0
 } snx_model_cfg;
 
-// Write the model to `path` (GGUF v3; Q4_0 matrices quantized with ggml's quantize_row_q4_0_ref; norms 1 + N(0, 0.1)).
-// nthreads <= 0: all cores. The bytes depend only on (cfg, seed). 0, or -1 with the reason in err.
+// Write the model to `path` (GGUF v3; matrices quantized with ggml's quantize_row_q4_0_ref or quantize_row_q8_0_ref;
+// norms 1 + N(0, 0.1)). nthreads <= 0: all cores. The bytes depend only on (cfg, seed). 0, or -1 with the reason in err.
 int snx_write_model(const char* path, const snx_model_cfg* cfg, uint64_t seed, int nthreads, char* err, int err_len);
 
 // ggml quantize_row_q4_0_ref of k values (k % 32 == 0): 18-byte blocks into y.
 void snx_quantize_q4_0(const float* x, uint8_t* y, int64_t k);
+// ggml quantize_row_q8_0_ref of k values (k % 32 == 0): 34-byte blocks into y.
+void snx_quantize_q8_0(const float* x, uint8_t* y, int64_t k);
 
 #ifdef __cplusplus
 }

@@ -108,6 +108,48 @@ void or_dequantize_row_q8_0(const uint8_t* x, float* y, int64_t k) {
     }
 }
 
+// ggml quantize_row_q8_0_ref (the quantizer of Q8_0 weights in a model file): d = amax / 127 stored fp16, id = 1/d (0
+// when d is 0), q = roundf(x * id) (halves away from zero). The activations of a mul_mat use or_quantize_row_q8_0.
+void or_quantize_row_q8_0_ref(const float* x, uint8_t* y, int64_t k) {
+    const int64_t nb = k / QK;
+    for (int64_t i = 0; i < nb; i++) {
+        const float* xb = x + i * QK;
+        uint8_t* yb = y + i * 34;
+        float amax = 0.0f;
+        for (int j = 0; j < QK; j++) amax = fmaxf(amax, fabsf(xb[j]));
+        const float d = amax / 127.f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        f2h_store(yb, d);
+        for (int j = 0; j < QK; ++j) yb[2 + j] = (uint8_t) (int8_t) (int) roundf(xb[j] * id);
+    }
+}
+
+// ggml_vec_dot_q8_0_q8_0 (generic form): per block the integer sum of qw * qx, then sumf += sumi * (dw * dx)
+float or_vec_dot_q8_0_q8_0(int64_t k, const uint8_t* w, const uint8_t* xq) {
+    const int64_t nb = k / QK;
+    float sumf = 0.0f;
+    for (int64_t ib = 0; ib < nb; ++ib) {
+        const uint8_t* bw = w + ib * 34;
+        const uint8_t* bx = xq + ib * 34;
+        int sumi = 0;
+        for (int j = 0; j < QK; ++j) sumi += (int8_t) bw[2 + j] * (int8_t) bx[2 + j];
+        sumf += (float) sumi * (h2f(bw) * h2f(bx));
+    }
+    return sumf;
+}
+
+// ggml CPU mul_mat of Q8_0 weights: the activation rows quantized to Q8_0 (x86 quantize_row_q8_0), then
+// vec_dot_q8_0_q8_0 per (row, output)
+void or_mul_mat_q8_0(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nthreads) {
+    const int64_t nb = K / QK;
+    uint8_t* xq = (uint8_t*) malloc((size_t) M * nb * 34);
+    for (int64_t m = 0; m < M; ++m) or_quantize_row_q8_0(X + m * K, xq + m * nb * 34, K);
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t m = 0; m < M; ++m) Y[m * N + n] = or_vec_dot_q8_0_q8_0(K, W + n * nb * 34, xq + m * nb * 34);
+    free(xq);
+}
+
 // ggml_vec_dot_q4_0_q8_0 (generic form): per block the integer sum of (q4 - 8) * q8, then sumf += sumi * dw * dx
 float or_vec_dot_q4_0_q8_0(int64_t k, const uint8_t* w, const uint8_t* xq) {
     const int64_t nb = k / QK;
@@ -380,9 +422,12 @@ int or_accept(const int32_t* draft, const int32_t* target, int k) {
 }
 
 // ---- the Qwen3 step ----
-static void mm(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nt) {
-    or_mul_mat_q4_0(W, N, K, X, M, Y, nt);
+static void mm(const or_qwen3* m, const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nt) {
+    if (m->wtype == 8) or_mul_mat_q8_0(W, N, K, X, M, Y, nt);
+    else or_mul_mat_q4_0(W, N, K, X, M, Y, nt);
 }
+// bytes of one block of the model's matrices
+static size_t wblock(const or_qwen3* m) { return m->wtype == 8 ? 34 : 18; }
 
 // One Qwen3 block over R rows, in place on the residual rows x [R][E] (the rows' rope tables in cs [R][D]). The block's
 // K/V cells go to layer `kl` of the cache. kv_only: stop after writing them (the guess head's cache fill).
@@ -402,9 +447,9 @@ static void block(const or_qwen3* m, const or_layer* L, or_kv* kv, int kl, int R
     float* u = (float*) malloc((size_t) R * FF * 4);
     const size_t lstride = (size_t) kv->ctx * KD;  // one layer of one sequence
     for (int r = 0; r < R; ++r) or_rmsnorm(x + (size_t) r * E, L->attn_norm, E, m->eps, h + (size_t) r * E);
-    if (!kv_only) mm(L->wq, QD, E, h, R, q, nthreads);
-    mm(L->wk, KD, E, h, R, k, nthreads);
-    mm(L->wv, KD, E, h, R, v, nthreads);
+    if (!kv_only) mm(m, L->wq, QD, E, h, R, q, nthreads);
+    mm(m, L->wk, KD, E, h, R, k, nthreads);
+    mm(m, L->wv, KD, E, h, R, v, nthreads);
     for (int r = 0; r < R; ++r) {
         if (!kv_only)
             for (int hh = 0; hh < H; ++hh)
@@ -433,12 +478,12 @@ static void block(const or_qwen3* m, const or_layer* L, or_kv* kv, int kl, int R
         free(kp);
         free(vp);
     }
-    mm(L->wo, E, QD, ao, R, y, nthreads);
+    mm(m, L->wo, E, QD, ao, R, y, nthreads);
     for (size_t i = 0; i < (size_t) R * E; ++i) x[i] += y[i];
     for (int r = 0; r < R; ++r) or_rmsnorm(x + (size_t) r * E, L->ffn_norm, E, m->eps, h + (size_t) r * E);
     if (m->n_expert > 0) {
         const int NE = m->n_expert, K = m->n_expert_used, FE = m->n_ff_exp;
-        const size_t gsz = (size_t) FE * (E / QK) * 18, dsz = (size_t) E * (FE / QK) * 18;
+        const size_t gsz = (size_t) FE * (E / QK) * wblock(m), dsz = (size_t) E * (FE / QK) * wblock(m);
         for (int r = 0; r < R; ++r) {
             float* lg = (float*) malloc((size_t) NE * 4);
             int32_t ids[64];
@@ -451,10 +496,10 @@ static void block(const or_qwen3* m, const or_layer* L, or_kv* kv, int kl, int R
             or_moe_route(lg, NE, K, ids, w);
             float* acc = (float*) calloc((size_t) E, 4);
             for (int j = 0; j < K; ++j) {
-                mm(L->eg + ids[j] * gsz, FE, E, h + (size_t) r * E, 1, g, nthreads);
-                mm(L->eu + ids[j] * gsz, FE, E, h + (size_t) r * E, 1, u, nthreads);
+                mm(m, L->eg + ids[j] * gsz, FE, E, h + (size_t) r * E, 1, g, nthreads);
+                mm(m, L->eu + ids[j] * gsz, FE, E, h + (size_t) r * E, 1, u, nthreads);
                 for (int i = 0; i < FE; ++i) g[i] = or_silu(g[i]) * u[i];
-                mm(L->ed + ids[j] * dsz, E, FE, g, 1, y, nthreads);
+                mm(m, L->ed + ids[j] * dsz, E, FE, g, 1, y, nthreads);
                 for (int i = 0; i < E; ++i) acc[i] += w[j] * y[i];
             }
             for (int i = 0; i < E; ++i) x[(size_t) r * E + i] += acc[i];
@@ -462,10 +507,10 @@ static void block(const or_qwen3* m, const or_layer* L, or_kv* kv, int kl, int R
             free(lg);
         }
     } else {
-        mm(L->wg, F, E, h, R, g, nthreads);
-        mm(L->wu, F, E, h, R, u, nthreads);
+        mm(m, L->wg, F, E, h, R, g, nthreads);
+        mm(m, L->wu, F, E, h, R, u, nthreads);
         for (size_t i = 0; i < (size_t) R * F; ++i) g[i] = or_silu(g[i]) * u[i];
-        mm(L->wd, E, F, g, R, y, nthreads);
+        mm(m, L->wd, E, F, g, R, y, nthreads);
         for (size_t i = 0; i < (size_t) R * E; ++i) x[i] += y[i];
     }
 done:
@@ -489,7 +534,7 @@ void or_qwen3_step(const or_qwen3* m, or_kv* kv, int R, const int32_t* tok, cons
     float* ho = (float*) malloc((size_t) (n_out > 0 ? n_out : 1) * E * 4);
     for (int j = 0; j < n_out; ++j) or_rmsnorm(x + (size_t) out_rows[j] * E, m->output_norm, E, m->eps, ho + (size_t) j * E);
     if (hidden) memcpy(hidden, ho, (size_t) n_out * E * 4);
-    if (n_out > 0) mm(m->output, V, E, ho, n_out, logits, nthreads);
+    if (n_out > 0) mm(m, m->output, V, E, ho, n_out, logits, nthreads);
     for (int j = 0; j < n_out; ++j) out_tok[j] = or_argmax(logits + (size_t) j * V, V, NULL, 0);
     free(ho);
     free(x);
@@ -504,7 +549,7 @@ static void mtp_in(const or_qwen3* m, int R, const int32_t* tok, const float* hp
         or_rmsnorm(m->tok_embd + (size_t) tok[r] * E, m->mtp_enorm, E, m->eps, cat + (size_t) r * 2 * E);
         or_rmsnorm(hprev + (size_t) r * E, m->mtp_hnorm, E, m->eps, cat + (size_t) r * 2 * E + E);
     }
-    mm(m->mtp_eh, E, 2 * E, cat, R, x, nthreads);
+    mm(m, m->mtp_eh, E, 2 * E, cat, R, x, nthreads);
     free(cat);
 }
 
@@ -537,7 +582,7 @@ void or_mtp_guess(const or_qwen3* m, or_kv* kv, int seq, int32_t tok, int pos, i
         mtp_in(m, 1, &t, h, x, nthreads);
         block(m, m->mtp, kv, m->n_layer, 1, &seq, &p, x, cs, 0, nthreads);
         or_rmsnorm(x, m->mtp_head_norm, E, m->eps, h);  // the head's output state: the next row's hprev
-        mm(m->output, V, E, h, 1, lg, nthreads);
+        mm(m, m->output, V, E, h, 1, lg, nthreads);
         t = or_argmax(lg, V, NULL, 0);
         out_tok[j] = t;
         if (logits) memcpy(logits + (size_t) j * V, lg, (size_t) V * 4);

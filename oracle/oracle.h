@@ -10,6 +10,8 @@
 //     and the GPU-side form kernels.metal:21-28, :461-469.
 //   * ggml's x86 CPU `quantize_row_q8_0` (activations of a Q4_0 mul_mat: d = amax/127 stored fp16, id = 127/amax,
 //     q = round-half-even(x*id)) and the generic `ggml_vec_dot_q4_0_q8_0` (integer block sums, fp32 sumi*dw*dx).
+//   * Q8_0 weights: ggml `quantize_row_q8_0_ref` (d = amax/127, q = roundf(x/d)), `dequantize_row_q8_0` (d*q) and the
+//     generic `ggml_vec_dot_q8_0_q8_0` (the reference's Q8_0 kernels: kernels.metal:9, :597-609, :1995-2130).
 //   * fp32 RMSNorm (kernels.metal:121-140; ggml rms_norm sums squares in double), per-head QK-norm + NEOX RoPE with ggml's
 //     iterative theta (kernels.metal:149-197), SwiGLU silu(g)*u (kernels.metal:564-568), greedy argmax with the lowest id on
 //     ties (kernels.metal:327-356), paged GQA decode attention (kernels.metal:1122-1192), the Qwen3 layer order
@@ -47,6 +49,11 @@ void or_dequantize_row_q8_0(const uint8_t* x, float* y, int64_t k);
 float or_vec_dot_q4_0_q8_0(int64_t k, const uint8_t* w, const uint8_t* xq);
 
 // Y[m][n] = sum_k X[m][k] * W[n][k] with ggml CPU semantics: X rows quantized to Q8_0, integer block dots.
+// block_q8_0 weights: ggml quantize_row_q8_0_ref (roundf of x / d, d = amax/127); vec_dot_q8_0_q8_0 and the mul_mat of
+// Q8_0 weights (activations quantized with or_quantize_row_q8_0)
+void or_quantize_row_q8_0_ref(const float* x, uint8_t* y, int64_t k);
+float or_vec_dot_q8_0_q8_0(int64_t k, const uint8_t* w, const uint8_t* xq);
+void or_mul_mat_q8_0(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nthreads);
 // W: N rows of K/32 Q4_0 blocks. nthreads <= 0: all cores (OpenMP).
 void or_mul_mat_q4_0(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nthreads);
 // The same product in fp64 over dequantized W and the fp32 X as given (no activation quantization): the
@@ -82,7 +89,7 @@ void or_paged_attn_chunked(const float* q, int nq, const int32_t* qseq, const in
                            const uint16_t* kpool, const uint16_t* vpool, int page_cells, const int32_t* pt,
                            int max_pages, float scale, int chunk, float* out);
 
-// ---- a Qwen3 dense model (the GGUF's tensors; Q4_0 matrices in GGUF block layout, ne = [K, N]) ----
+// ---- a Qwen3 dense model (the GGUF's tensors; Q4_0 or Q8_0 matrices in GGUF block layout, ne = [K, N]) ----
 typedef struct {
     const float* attn_norm;  // [E]
     const float* q_norm;     // [D]
@@ -114,6 +121,7 @@ typedef struct {
     const or_layer* mtp;
     const uint8_t* mtp_eh;
     const float *mtp_enorm, *mtp_hnorm, *mtp_head_norm;  // head_norm: shared_head_norm, else output_norm
+    int wtype;  // the matrices' block type: 2 Q4_0 (block_q4_0), 8 Q8_0 (block_q8_0)
 } or_qwen3;
 
 // The oracle's KV cache: contiguous per (sequence, layer): K and V fp16 [ctx][KVH][D]. n_layer counts the guess

@@ -46,6 +46,11 @@ def _declare(L):
         getattr(L, f).restype = None
     L.or_vec_dot_q4_0_q8_0.argtypes = [I64, P, P]
     L.or_vec_dot_q4_0_q8_0.restype = C.c_float
+    L.or_quantize_row_q8_0_ref.argtypes = [P, P, I64]
+    L.or_quantize_row_q8_0_ref.restype = None
+    L.or_vec_dot_q8_0_q8_0.argtypes = [I64, P, P]
+    L.or_vec_dot_q8_0_q8_0.restype = C.c_float
+    L.or_mul_mat_q8_0.argtypes = [P, I64, I64, P, I64, P, C.c_int]
     L.or_mul_mat_q4_0.argtypes = [P, I64, I64, P, I64, P, C.c_int]
     L.or_mul_mat_q4_0_f64.argtypes = [P, I64, I64, P, I64, P, C.c_int]
     L.or_rmsnorm.argtypes = [P, P, I64, C.c_float, P]
@@ -112,6 +117,26 @@ def dequantize_q8_0(q: np.ndarray, K: int) -> np.ndarray:
     out = np.empty((M, K), np.float32)
     lib().or_dequantize_row_q8_0(_p(q), _p(out), M * K)
     return out
+
+
+def quantize_q8_0_ref(w: np.ndarray) -> np.ndarray:
+    """[N][K] fp32 -> [N][K/32*34] uint8 (ggml quantize_row_q8_0_ref per row: the quantizer of Q8_0 model weights)."""
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    out = np.empty((N, K // 32 * 34), np.uint8)
+    lib().or_quantize_row_q8_0_ref(_p(w), _p(out), N * K)
+    return out
+
+
+def mul_mat_q8_0(Wq: np.ndarray, K: int, X: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    """Y[M][N] = X[M][K] . W[N][K]^T for Q8_0 weights, ggml CPU semantics (Q8_0 activations, vec_dot_q8_0_q8_0)."""
+    Wq = np.ascontiguousarray(Wq, np.uint8)
+    X = np.ascontiguousarray(X, np.float32)
+    N = Wq.size // (K // 32 * 34)
+    M = X.shape[0]
+    Y = np.empty((M, N), np.float32)
+    lib().or_mul_mat_q8_0(_p(Wq), N, K, _p(X), M, _p(Y), nthreads)
+    return Y
 
 
 def mul_mat_q4_0(Wq: np.ndarray, K: int, X: np.ndarray, nthreads: int = 0) -> np.ndarray:
@@ -224,7 +249,8 @@ class _Model(C.Structure):
                 ("n_expert_used", C.c_int), ("n_ff_exp", C.c_int), ("eps", C.c_float), ("rope_base", C.c_float),
                 ("tok_embd", C.c_void_p), ("output_norm", C.c_void_p), ("output", C.c_void_p),
                 ("layers", C.POINTER(_Layer)), ("mtp", C.POINTER(_Layer)), ("mtp_eh", C.c_void_p),
-                ("mtp_enorm", C.c_void_p), ("mtp_hnorm", C.c_void_p), ("mtp_head_norm", C.c_void_p)]
+                ("mtp_enorm", C.c_void_p), ("mtp_hnorm", C.c_void_p), ("mtp_head_norm", C.c_void_p),
+                ("wtype", C.c_int)]
 
 
 class _KV(C.Structure):
@@ -279,9 +305,12 @@ class Qwen3:
                 ly.wu = ptr(p + "ffn_up.weight")
                 ly.wd = ptr(p + "ffn_down.weight")
         self._layers = layers
+        wt = {"Q4_0": 2, "Q8_0": 8}[g.type_name("output.weight")]
+        self.wtype = wt
         self.m = _Model(self.L, self.E, self.H, self.KVH, self.D, self.F, self.V, self.NE, self.NEU, self.FE,
                         self.eps, self.base, ptr("token_embd.weight"), ptr("output_norm.weight"),
                         ptr("output.weight"), layers)
+        self.m.wtype = wt
         if self.n_mtp:
             p = f"blk.{self.L}.nextn."
             self.m.mtp = C.cast(C.byref(layers, self.L * C.sizeof(_Layer)), C.POINTER(_Layer))

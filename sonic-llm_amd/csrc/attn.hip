@@ -214,7 +214,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
     }
     if (a.xa) {
         // block b = lane / 16 holds dims 32 b + 2 (lane % 16) and + 1: elements e, e + 1 of block 4 h + b, stored in
-        // the operand's fragment order (q / 16 for elements 16..31), with the block's scale and correction
+        // the operand's fragment order (q / 16 for elements 16..31), with the block's scale and corrections
         float amax = fmaxf(fabsf(o0), fabsf(o1));
         for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
         const float d = amax / 127.f;
@@ -235,6 +235,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
         if ((lane & 15) == 0) {
             *(float*) (rec + XA_DX_OFF + b * 64 + 4 * (r & 15)) = (float) (_Float16) d;
             *(float*) (rec + XA_CORR_OFF + b * 64 + 4 * (r & 15)) = -(1032.0f * slo + 72.0f * shi);
+            *(float*) (rec + XA_CORR8_OFF + b * 64 + 4 * (r & 15)) = -1152.0f * (slo + shi);
         }
     }
 }

@@ -49,6 +49,7 @@ struct sn_engine {
     bool has_nextn = false;
     // qwen3moe: experts, experts a token uses, an expert's FFN width; the tile bound of a step's expert rows
     int NE = 0, NEU = 0, FE = 0, moe_tiles = 0;
+    int wt = WT_Q4_0;  // the block type of every weight matrix: WT_Q4_0 or WT_Q8_0 (GGUF Q4_0 / Q8_0)
     size_t egu_stride = 0, ed_stride = 0;
     float *hn = nullptr, *rlog = nullptr, *mw = nullptr;  // normed rows, router logits, routing weights
     int32_t *mid = nullptr, *prow = nullptr, *rsrc = nullptr, *gitems = nullptr, *gcount = nullptr;
@@ -150,27 +151,29 @@ const GgufTensor* need(const GgufFile& g, const std::string& name, int type, std
     const GgufTensor* t = g.find(name);
     if (!t) *why = "missing tensor " + name;
     else if (t->type != type) {
-        *why = "tensor " + name + " has an unsupported type (Q4_0 matrices and F32 norms / embedding are served)";
+        *why = "tensor " + name + " has an unsupported type (Q4_0 or Q8_0 matrices, all of one type, and F32 norms / "
+               "embedding are served)";
         t = nullptr;
     }
     return t;
 }
 
-// a GGUF Q4_0 matrix (ne = [K, N]) into stripes at dst (stripe stride / offset for interleaving)
+// a GGUF Q4_0 / Q8_0 matrix (ne = [K, N]) into tiles at dst (stripe stride / offset for interleaving)
 bool upload_q4(sn_engine* e, const GgufTensor* t, uint8_t* tmp, uint8_t* dst, int sstride, int soff, char* err,
                int err_len) {
     SN_HIP_TRY(hipMemcpyAsync(tmp, t->data, t->nbytes, hipMemcpyHostToDevice, e->st), false);
-    q4_repack(tmp, (int) t->ne[1], (int) t->ne[0], dst, sstride, soff, e->st);
+    q4_repack(tmp, (int) t->ne[1], (int) t->ne[0], dst, sstride, soff, e->st, e->wt);
     SN_HIP_TRY(hipStreamSynchronize(e->st), false);
     return true;
 }
 
-// a GGUF Q4_0 expert tensor (ne = [K, N, NE]) into per-expert stripes, expert x at dst + x * dst_stride
+// a GGUF Q4_0 / Q8_0 expert tensor (ne = [K, N, NE]) into per-expert tiles, expert x at dst + x * dst_stride
 bool upload_q4_experts(sn_engine* e, const GgufTensor* t, uint8_t* tmp, uint8_t* dst, int NE, int N, int K,
                        size_t dst_stride, int sstride, int soff, char* err, int err_len) {
     SN_HIP_TRY(hipMemcpyAsync(tmp, t->data, t->nbytes, hipMemcpyHostToDevice, e->st), false);
-    const size_t src_stride = (size_t) N * (K / 32) * 18;
-    for (int x = 0; x < NE; ++x) q4_repack(tmp + x * src_stride, N, K, dst + x * dst_stride, sstride, soff, e->st);
+    const size_t src_stride = (size_t) N * ggml_row_bytes(t->type, K);
+    for (int x = 0; x < NE; ++x)
+        q4_repack(tmp + x * src_stride, N, K, dst + x * dst_stride, sstride, soff, e->st, e->wt);
     SN_HIP_TRY(hipStreamSynchronize(e->st), false);
     return true;
 }
@@ -215,7 +218,7 @@ bool model_check(const GgufFile& g, std::string* why) {
         return false;
     }
     if (!g.find("output.weight")) {
-        *why = "an untied Q4_0 output.weight is required";
+        *why = "an untied Q4_0 or Q8_0 output.weight is required";
         return false;
     }
     return true;
@@ -262,6 +265,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->NQKV = e->QD + 2 * e->KD;
     const GgufTensor* emb = need(g, "token_embd.weight", GGML_F32, &why);
     if (!emb) return fail(why);
+    e->wt = g.find("output.weight")->type == GGML_Q8_0 ? WT_Q8_0 : WT_Q4_0;  // every matrix must be of this type
     e->V = (int) emb->ne[1];
     const char* pe = getenv("SN_PAGE");
     e->page_cells = pe && atoi(pe) == 32 ? 32 : 64;
@@ -286,7 +290,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     if (hipMalloc(&tmp, max_t) != hipSuccess) return fail("hipMalloc of the upload buffer failed");
     bool ok = true;
     auto q4 = [&](const std::string& n, int N, int K) -> const GgufTensor* {
-        const GgufTensor* t = need(g, n, GGML_Q4_0, &why);
+        const GgufTensor* t = need(g, n, e->wt, &why);
         if (t && (t->ne[0] != K || t->ne[1] != N)) {
             why = "tensor " + n + " has unexpected dimensions";
             t = nullptr;
@@ -307,7 +311,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->tok_embd = upload_f32(e, emb, err, err_len);
     e->out_norm = f32("output_norm.weight", E);
     if (const GgufTensor* t = ok ? q4("output.weight", e->V, E) : nullptr) {
-        e->head = e->dalloc<uint8_t>(q4t_bytes(e->V, E), err, err_len);
+        e->head = e->dalloc<uint8_t>(wt_bytes(e->wt, e->V, E), err, err_len);
         ok = e->head && upload_q4(e, t, tmp, e->head, 1, 0, err, err_len);
     }
     auto load_layer = [&](int i, DevLayer& l) {
@@ -319,13 +323,13 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
         const GgufTensor *tq = q4(p + "attn_q.weight", QD, E), *tk = q4(p + "attn_k.weight", KD, E),
                          *tv = q4(p + "attn_v.weight", KD, E), *to = q4(p + "attn_output.weight", E, QD);
         if (!ok) return;
-        l.wqkv = e->dalloc<uint8_t>(q4t_bytes(e->NQKV, E), err, err_len);
-        l.wo = e->dalloc<uint8_t>(q4t_bytes(E, QD), err, err_len);
+        l.wqkv = e->dalloc<uint8_t>(wt_bytes(e->wt, e->NQKV, E), err, err_len);
+        l.wo = e->dalloc<uint8_t>(wt_bytes(e->wt, E, QD), err, err_len);
         ok = l.wqkv && l.wo;
         // q, k, v stripes one after another (one matmul for all three)
         ok = ok && upload_q4(e, tq, tmp, l.wqkv, 1, 0, err, err_len) &&
-             upload_q4(e, tk, tmp, l.wqkv + q4t_bytes(QD, E), 1, 0, err, err_len) &&
-             upload_q4(e, tv, tmp, l.wqkv + q4t_bytes(QD + KD, E), 1, 0, err, err_len) &&
+             upload_q4(e, tk, tmp, l.wqkv + wt_bytes(e->wt, QD, E), 1, 0, err, err_len) &&
+             upload_q4(e, tv, tmp, l.wqkv + wt_bytes(e->wt, QD + KD, E), 1, 0, err, err_len) &&
              upload_q4(e, to, tmp, l.wo, 1, 0, err, err_len);
         if (!ok) return;
         if (e->NE > 0 && i < e->L) {  // experts (the guess head's block stays dense)
@@ -333,7 +337,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
             const GgufTensor* tr = need(g, p + "ffn_gate_inp.weight", GGML_F32, &why);
             if (tr && (tr->ne[0] != E || tr->ne[1] != NE)) tr = nullptr, why = "router " + p + " has unexpected dims";
             auto q4e = [&](const std::string& n, int N, int K) -> const GgufTensor* {
-                const GgufTensor* t = need(g, n, GGML_Q4_0, &why);
+                const GgufTensor* t = need(g, n, e->wt, &why);
                 if (t && (t->ne[0] != K || t->ne[1] != N || t->ne[2] != NE)) {
                     why = "tensor " + n + " has unexpected dimensions";
                     t = nullptr;
@@ -357,16 +361,16 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
         const GgufTensor *tg = q4(p + "ffn_gate.weight", F, E), *tu = q4(p + "ffn_up.weight", F, E),
                          *td = q4(p + "ffn_down.weight", E, F);
         if (!ok) return;
-        l.wgu = e->dalloc<uint8_t>(q4t_bytes(2 * F, E), err, err_len);
-        l.wd = e->dalloc<uint8_t>(q4t_bytes(E, F), err, err_len);
+        l.wgu = e->dalloc<uint8_t>(wt_bytes(e->wt, 2 * F, E), err, err_len);
+        l.wd = e->dalloc<uint8_t>(wt_bytes(e->wt, E, F), err, err_len);
         ok = l.wgu && l.wd;
         // gate and up stripes interleaved in pairs
         ok = ok && upload_q4(e, tg, tmp, l.wgu, 2, 0, err, err_len) && upload_q4(e, tu, tmp, l.wgu, 2, 1, err, err_len) &&
              upload_q4(e, td, tmp, l.wd, 1, 0, err, err_len);
     };
     if (e->NE > 0) {
-        e->egu_stride = q4t_bytes(2 * e->FE, E);
-        e->ed_stride = q4t_bytes(E, e->FE);
+        e->egu_stride = wt_bytes(e->wt, 2 * e->FE, E);
+        e->ed_stride = wt_bytes(e->wt, E, e->FE);
     }
     e->ly.resize(e->L);
     for (int i = 0; i < e->L && ok; ++i) load_layer(i, e->ly[i]);
@@ -376,7 +380,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
         load_layer(e->L, e->mtp);
         const std::string p = "blk." + std::to_string(e->L) + ".nextn.";
         if (const GgufTensor* t = ok ? q4(p + "eh_proj.weight", E, 2 * E) : nullptr) {
-            e->mtp_eh = e->dalloc<uint8_t>(q4t_bytes(E, 2 * E), err, err_len);
+            e->mtp_eh = e->dalloc<uint8_t>(wt_bytes(e->wt, E, 2 * E), err, err_len);
             ok = e->mtp_eh && upload_q4(e, t, tmp, e->mtp_eh, 1, 0, err, err_len);
         }
         if (ok) e->mtp_enorm = f32(p + "enorm.weight", E);
@@ -414,13 +418,13 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->xa = e->dalloc<uint8_t>(std::max(xa_bytes(R, KMAX), e->NE > 0 ? xa_bytes(P, std::max(E, e->FE)) : 0), err,
                                err_len);
     size_t ws = 0;
-    ws = std::max(ws, q4_workspace_bytes(R, e->NQKV, E));
-    ws = std::max(ws, q4_workspace_bytes(R, E, QD));
+    ws = std::max(ws, q4_workspace_bytes(R, e->NQKV, E, e->wt));
+    ws = std::max(ws, q4_workspace_bytes(R, E, QD, e->wt));
     if (F > 0) {
-        ws = std::max(ws, q4_workspace_bytes(R, 2 * F, E));
-        ws = std::max(ws, q4_workspace_bytes(R, E, F));
+        ws = std::max(ws, q4_workspace_bytes(R, 2 * F, E, e->wt));
+        ws = std::max(ws, q4_workspace_bytes(R, E, F, e->wt));
     }
-    ws = std::max(ws, q4_workspace_bytes(MO, e->V, E));
+    ws = std::max(ws, q4_workspace_bytes(MO, e->V, E, e->wt));
     if (e->NE > 0) {
         ws = std::max(ws, (size_t) P * 2 * e->FE * 4);  // grouped expert matmuls: one slice
         ws = std::max(ws, (size_t) P * E * 4);
@@ -436,8 +440,8 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
         if (!e->hn || !e->rlog || !e->mw || !e->mid || !e->prow || !e->rsrc || !e->gitems || !e->gcount) return fail("");
     }
     if (e->has_nextn) {
-        ws = std::max(ws, q4_workspace_bytes(R, E, 2 * E));    // eh_proj
-        ws = std::max(ws, q4_workspace_bytes(R, 2 * KD, E));   // the head's k|v (its cache fill)
+        ws = std::max(ws, q4_workspace_bytes(R, E, 2 * E, e->wt));    // eh_proj
+        ws = std::max(ws, q4_workspace_bytes(R, 2 * KD, E, e->wt));   // the head's k|v (its cache fill)
     }
     e->gemm_ws_bytes = ws;
     e->gemm_ws = e->dalloc<float>(ws, err, err_len);
@@ -653,7 +657,10 @@ int stage_copy(sn_engine* e, Stage& S) {
     return 0;
 }
 
-double gemm_bytes(int M, int N, int K) { return (double) N * (K / 32) * 18 + (double) M * K * 4 + (double) M * N * 4; }
+// algorithmic bytes of a matmul: the weights (18 or 34 bytes a block) + fp32 input rows + fp32 output rows
+double gemm_bytes(int wt, int M, int N, int K) {
+    return (double) N * (K / 32) * (wt == WT_Q8_0 ? 34 : 18) + (double) M * K * 4 + (double) M * N * 4;
+}
 
 // Device work of a step, all on the engine's stream. Matmuls leave their k-slice sums in the workspace; the next row
 // kernel adds them in slice order and applies the epilogue (RoPE for q|k|v, residual add + RMSNorm + Q8_0 for o and
@@ -665,8 +672,8 @@ struct Dev {
     int rc = 0;
 
     void gemm(const uint8_t* w, int M, int N, int K) {
-        rc |= e->launch(SNX_K_GEMM, gemm_bytes(M, N, K), [&] {
-            ks = q4_gemm_raw(w, e->xa, M, N, K, e->gemm_ws, e->gemm_ws_bytes, st);
+        rc |= e->launch(SNX_K_GEMM, gemm_bytes(e->wt, M, N, K), [&] {
+            ks = q4_gemm_raw(w, e->xa, M, N, K, e->gemm_ws, e->gemm_ws_bytes, st, e->wt);
             return ks < 0 ? -1 : 0;
         });
     }
@@ -774,7 +781,7 @@ struct Dev {
         quant(e->hn, e->rsrc, P, E, nullptr);
         rc |= e->launch(SNX_K_GEMM, used * e->egu_stride + (double) R * NU * E * 4 + (double) R * NU * 2 * FE * 4, [&] {
             return q4_gemm_grouped(l.egu, e->egu_stride, e->gitems, e->gcount, T, e->xa, P, 2 * FE, E, e->gemm_ws,
-                                   e->gemm_ws_bytes, st) < 0 ? -1 : 0;
+                                   e->gemm_ws_bytes, st, e->wt) < 0 ? -1 : 0;
         });
         rc |= e->launch(SNX_K_QUANT, (double) R * NU * FE * 14, [&] {
             swiglu_quant(e->gemm_ws, 1, P, FE, nullptr, e->xa, st);
@@ -782,7 +789,7 @@ struct Dev {
         });
         rc |= e->launch(SNX_K_GEMM, used * e->ed_stride + (double) R * NU * FE * 4 + (double) R * NU * E * 4, [&] {
             return q4_gemm_grouped(l.ed, e->ed_stride, e->gitems, e->gcount, T, e->xa, P, E, FE, e->gemm_ws,
-                                   e->gemm_ws_bytes, st) < 0 ? -1 : 0;
+                                   e->gemm_ws_bytes, st, e->wt) < 0 ? -1 : 0;
         });
         rc |= e->launch(SNX_K_OTHER, (double) R * NU * E * 4 + (double) R * E * 8, [&] {
             moe_out(x, e->gemm_ws, e->prow, e->mw, R, E, NU, st);
@@ -821,10 +828,10 @@ struct Dev {
     }
     void head_logits(int n) {
         const int E = e->E, V = e->V;
-        rc |= e->launch(SNX_K_GEMM, gemm_bytes(n, V, E), [&] {
-            if (q4_plan(V, E).ks == 1)  // one slice: the sums are the logits
-                return q4_gemm_raw(e->head, e->xa, n, V, E, e->logits, (size_t) n * V * 4, st) < 0 ? -1 : 0;
-            return q4_gemm(e->head, e->xa, n, V, E, e->logits, V, EPI_STORE, e->gemm_ws, e->gemm_ws_bytes, st);
+        rc |= e->launch(SNX_K_GEMM, gemm_bytes(e->wt, n, V, E), [&] {
+            if (q4_plan(V, E, e->wt).ks == 1)  // one slice: the sums are the logits
+                return q4_gemm_raw(e->head, e->xa, n, V, E, e->logits, (size_t) n * V * 4, st, e->wt) < 0 ? -1 : 0;
+            return q4_gemm(e->head, e->xa, n, V, E, e->logits, V, EPI_STORE, e->gemm_ws, e->gemm_ws_bytes, st, e->wt);
         });
     }
 
@@ -845,7 +852,7 @@ struct Dev {
         gemm(e->mtp_eh, R, E, 2 * E);
         resid(e->mx, R, e->mtp.attn_norm, true, false);
         // the head's k|v stripes (rows QD .. QD + 2 KD of its q|k|v matrix)
-        gemm(e->mtp.wqkv + q4t_bytes(e->QD, E), R, 2 * e->KD, E);
+        gemm(e->mtp.wqkv + wt_bytes(e->wt, e->QD, E), R, 2 * e->KD, E);
         rope(e->mtp, R, 0, d_seq, d_pos, kp(e->L), vp(e->L));
         if (nkeep > 0) rows_keep(e->mhn, d_keep, nkeep, E, e->mpend, st);
     }

@@ -43,6 +43,35 @@ __global__ void k_q4_repack(const uint8_t* __restrict__ src, int N, int K, uint8
         }
 }
 
+// GGUF Q8_0 rows (34-byte blocks) -> Q8_0 tiles (sn_common.h); stripe s goes to s * sstride + soff.
+__global__ void k_q8_repack(const uint8_t* __restrict__ src, int N, int K, uint8_t* __restrict__ dst, int sstride,
+                            int soff) {
+    const int nb = K / 32, ngroups = (nb + 3) / 4;
+    const int tile = blockIdx.x;
+    const int stripe = tile / ngroups, grp = tile % ngroups;
+    const int l = threadIdx.x, n = l & 15, g = l >> 4;
+    const int row = stripe * 16 + n;
+    uint8_t* t = dst + ((size_t) (stripe * sstride + soff) * ngroups + grp) * Q8T_BYTES;
+    uint8_t q[32];
+    uint16_t d[4];
+    for (int b = 0; b < 4; ++b) {
+        const int blk = grp * 4 + b;
+        const bool ok = row < N && blk < nb;
+        const uint8_t* s = src + ((size_t) row * nb + blk) * 34;
+        for (int j = 0; j < 4; ++j) {
+            q[8 * b + j] = ok ? s[2 + 4 * g + j] : 0;
+            q[8 * b + 4 + j] = ok ? s[2 + 16 + 4 * g + j] : 0;
+        }
+        d[b] = ok ? (uint16_t) (s[0] | (s[1] << 8)) : 0;
+    }
+    for (int j = 0; j < 32; ++j) t[32 * l + j] = q[j];
+    if (g == 0)
+        for (int b = 0; b < 4; ++b) {
+            t[Q8T_SCALE_OFF + 8 * n + 2 * b] = (uint8_t) d[b];
+            t[Q8T_SCALE_OFF + 8 * n + 2 * b + 1] = (uint8_t) (d[b] >> 8);
+        }
+}
+
 // ---------------------------------------------------------------------------------------------------------------------
 // activation quantizer: fp32 rows (optionally RMS-normed by weight nw first) -> xa operand (sn_common.h).
 // One workgroup of 256 threads per row. The norm is ggml's: y = (x * scale) * w, scale = 1/sqrt(mean(x^2) + eps).
@@ -109,7 +138,7 @@ __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, 
 // Row m, block b of a Q8_0 operand from its 32 fp32 values (this lane's 8: elements 4g..4g+3, 16+4g..16+4g+3):
 // ggml x86 quantize_row_q8_0, d = amax / 127 (stored fp16), q = round-half-even(x * 127 / amax). The 4 lanes of a
 // block are adjacent (the shuffles stay within them). Writes the lane's fragment slice (q, and q / 16 for elements
-// 16..31) and, from lane part 0, the block's scale and correction (see sn_common.h).
+// 16..31) and, from lane part 0, the block's scale and corrections (see sn_common.h).
 __device__ __forceinline__ void q8_store(const float* v, int g, uint8_t* xa, int K, int m, int b) {
     float amax = 0.0f;
     for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
@@ -134,6 +163,7 @@ __device__ __forceinline__ void q8_store(const float* v, int g, uint8_t* xa, int
     if (g == 0) {
         *(float*) (rec + XA_DX_OFF + (b & 3) * 64 + 4 * (m & 15)) = (float) (_Float16) d;
         *(float*) (rec + XA_CORR_OFF + (b & 3) * 64 + 4 * (m & 15)) = -(1032.0f * slo + 72.0f * shi);
+        *(float*) (rec + XA_CORR8_OFF + (b & 3) * 64 + 4 * (m & 15)) = -1152.0f * (slo + shi);
     }
 }
 
@@ -144,6 +174,7 @@ __device__ __forceinline__ void q8_zero(int g, uint8_t* xa, int K, int m, int b)
     if (g == 0) {
         *(float*) (rec + XA_DX_OFF + (b & 3) * 64 + 4 * (m & 15)) = 0.0f;
         *(float*) (rec + XA_CORR_OFF + (b & 3) * 64 + 4 * (m & 15)) = 0.0f;
+        *(float*) (rec + XA_CORR8_OFF + (b & 3) * 64 + 4 * (m & 15)) = 0.0f;
     }
 }
 
@@ -264,6 +295,18 @@ __device__ __forceinline__ half8 q4_unpack(uint32_t w) {
     return __builtin_bit_cast(half8, (u32x4){p0, p1, p2, p3});
 }
 
+// A Q8_0 weight lane's 8 bytes of one block (int8 q of elements 4g..4g+3 in w_lo, of 16+4g..16+4g+3 in w_hi) as the
+// MFMA operand: fp16 (1024 + u) and 16 (1024 + u), u = q + 128 (the sign bit flipped), built by two xors and four byte
+// permutes (0x64 and 0x74 are the high bytes of fp16 1024 and 16384; the latter's step is 16).
+__device__ __forceinline__ half8 q8_unpack(uint32_t w_lo, uint32_t w_hi) {
+    const uint32_t u0 = w_lo ^ 0x80808080u, u1 = w_hi ^ 0x80808080u;
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u);
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u);
+    const uint32_t p2 = __builtin_amdgcn_perm(0x74747474u, u1, 0x04010400u);
+    const uint32_t p3 = __builtin_amdgcn_perm(0x74747474u, u1, 0x04030402u);
+    return __builtin_bit_cast(half8, (u32x4){p0, p1, p2, p3});
+}
+
 #define RSRC_WORD3 0x00020000  // raw buffer resource, gfx9 data format
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short) 0, (int) bytes, RSRC_WORD3);
@@ -294,9 +337,13 @@ __device__ __forceinline__ float bload4f(__amdgpu_buffer_rsrc_t r, int vo, int s
 //
 // The kernel writes each slice's raw fp32 sums, part[slice][M][N]; whoever consumes them adds the slices in slice
 // order (k_q4_reduce here; the row kernels of the step), so the order of every sum is fixed by (N, K) alone.
-template <int MT, int S>
+template <int WT, int MT, int S>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_q4_gemm(GemmArgs a) {
     constexpr int D = 2, FPW = MT;  // ring slots, fragments each wavefront stages
+    constexpr bool Q8 = WT == WT_Q8_0;
+    constexpr int TB = Q8 ? Q8T_BYTES : Q4T_BYTES, SO = Q8 ? Q8T_SCALE_OFF : Q4T_SCALE_OFF;
+    constexpr int NW = Q8 ? 2 : 1;                               // 16-byte weight loads per lane and tile
+    constexpr int CORR = Q8 ? XA_CORR8_OFF : XA_CORR_OFF;         // the record's correction for this weight type
     __shared__ __attribute__((aligned(16))) uint8_t s_act[2][MT * 4][1024];
     __shared__ __attribute__((aligned(16))) float s_k[2][MT][2][64];  // [buffer][row tile][dx, corr][block * 16 + row]
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -313,7 +360,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     const int c0 = slice * a.gps, ng = min(a.gps, a.ngroups - c0);  // groups c0 .. c0 + ng - 1 (ng >= 1)
     const int s0 = set * (4 * S) + wave * S;
     const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(S, a.nstripes - s0)));
-    const int sbytes = a.ngroups * Q4T_BYTES;  // one stripe
+    const int sbytes = a.ngroups * TB;  // one stripe
     const __amdgpu_buffer_rsrc_t wr = buf_rsrc(wbase + (size_t) min(s0, a.nstripes - 1) * sbytes, (uint32_t) (nvalid * sbytes));
     const size_t x0 = (size_t) mt0 * a.ngroups * XA_REC;
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xa + x0, (uint32_t) (xa_bytes(a.M, a.K) - x0));
@@ -322,7 +369,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     // wave (row tile kb / 2; dx or corr) while kb < 2 MT
     const int kb = min(wave, 2 * MT - 1);
 
-    u32x4 wq[D][S];
+    u32x4 wq[D][S][NW];
     u32x2 ws[D][S];
     u32x4 ra[D][FPW];
     float rk[D];
@@ -336,11 +383,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
             const int f = wave * FPW + j;
             ra[slot][j] = bload16(xr, 16 * lane, (f / 4) * rstride + c * XA_REC + (f % 4) * 1024);
         }
-        rk[slot] = bload4f(xr, 4 * lane, (kb / 2) * rstride + c * XA_REC + XA_DX_OFF + (kb % 2) * 256);
+        rk[slot] = bload4f(xr, 4 * lane, (kb / 2) * rstride + c * XA_REC + (kb % 2 ? CORR : XA_DX_OFF));
         for (int s = 0; s < S; ++s) {
-            const int so = s * sbytes + c * Q4T_BYTES;
-            wq[slot][s] = bload16(wr, 16 * lane, so);
-            ws[slot][s] = bload8(wr, Q4T_SCALE_OFF + 8 * n_in, so);
+            const int so = s * sbytes + c * TB;
+            for (int h = 0; h < NW; ++h) wq[slot][s][h] = bload16(wr, 16 * NW * lane + 16 * h, so);
+            ws[slot][s] = bload8(wr, SO + 8 * n_in, so);
         }
     };
     auto stage = [&](int buf, int slot) {
@@ -357,7 +404,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
                 cr[mt] = *(const floatx4*) &s_k[buf][mt][1][b * 16 + 4 * g];
             }
             for (int s = 0; s < S; ++s) {
-                const half8 bw = q4_unpack(wq[slot][s][b]);
+                const half8 bw = Q8 ? q8_unpack(wq[slot][s][b / 2][2 * (b % 2)], wq[slot][s][b / 2][2 * (b % 2) + 1])
+                                    : q4_unpack(wq[slot][s][0][b]);
                 const float dw = (float) __builtin_bit_cast(half4v, ws[slot][s])[b] * m;
                 for (int mt = 0; mt < MT; ++mt) {
                     const floatx4 isum = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], bw, cr[mt], 0, 0, 0);
@@ -429,11 +477,12 @@ __global__ void k_q4_reduce(GemmArgs a) {
 // fewer than 768 workgroups, down to 4 groups and at most KS_MAX slices: on MI355X at 32 rows, short slices (a single
 // round of loads per workgroup) beat fewer, longer workgroups for the layer-sized matrices, while every slice costs
 // the consumer one more partial sum to read.
-GemmPlan q4_plan(int N, int K) {
+GemmPlan q4_plan(int N, int K, int wt) {
     GemmPlan p;
     p.nstripes = (N + 15) / 16;
     p.ngroups = (K / 32 + 3) / 4;
-    p.spw = p.nstripes >= 64 * 2 * 4 ? 2 : 1;  // stripes per wavefront: 1 while 2 would leave fewer than 64 sets
+    // stripes per wavefront: 1 while 2 would leave fewer than 64 sets, and for Q8_0 (twice the weight registers)
+    p.spw = p.nstripes >= 64 * 2 * 4 && wt != WT_Q8_0 ? 2 : 1;
     p.sets = (p.nstripes + 4 * p.spw - 1) / (4 * p.spw);
     auto slices = [&](int gps) { return (p.ngroups + gps - 1) / gps; };
     int gps = (p.ngroups + 1) / 2 * 2;
@@ -443,32 +492,47 @@ GemmPlan q4_plan(int N, int K) {
     return p;
 }
 
-size_t q4_workspace_bytes(int M, int N, int K) { return (size_t) q4_plan(N, K).ks * M * N * sizeof(float); }
+size_t q4_workspace_bytes(int M, int N, int K, int wt) { return (size_t) q4_plan(N, K, wt).ks * M * N * sizeof(float); }
+
+template <int WT>
+static void launch_gemm(int mt, int spw, dim3 grid, const GemmArgs& a, hipStream_t st) {
+    if constexpr (WT == WT_Q4_0) {
+        if (mt == 1) {
+            if (spw == 2) hipLaunchKernelGGL((k_q4_gemm<WT, 1, 2>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_q4_gemm<WT, 1, 1>), grid, dim3(256), 0, st, a);
+        } else {
+            if (spw == 2) hipLaunchKernelGGL((k_q4_gemm<WT, 2, 2>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_q4_gemm<WT, 2, 1>), grid, dim3(256), 0, st, a);
+        }
+    } else {  // Q8_0: one stripe per wavefront (q4_plan)
+        (void) spw;
+        if (mt == 1) hipLaunchKernelGGL((k_q4_gemm<WT, 1, 1>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_q4_gemm<WT, 2, 1>), grid, dim3(256), 0, st, a);
+    }
+}
 
 int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
-                hipStream_t st) {
+                hipStream_t st, int wt) {
     if (M <= 0) return 0;
-    const GemmPlan p = q4_plan(N, K);
+    if (wt != WT_Q4_0 && wt != WT_Q8_0) return -1;
+    const GemmPlan p = q4_plan(N, K, wt);
     if (part == nullptr || part_bytes < (size_t) p.ks * M * N * sizeof(float)) return -1;
     GemmArgs a{};
     a.w = w; a.xa = xa; a.part = part; a.y = nullptr;
     a.M = M; a.N = N; a.K = K; a.ldy = 0; a.epi = EPI_STORE;
     a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
     a.mtiles = (M + 15) / 16;
-    const dim3 g1(p.sets, p.ks, 1), g2(p.sets, p.ks, (a.mtiles + 1) / 2);
-    if (a.mtiles == 1) {
-        if (p.spw == 2) hipLaunchKernelGGL((k_q4_gemm<1, 2>), g1, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_q4_gemm<1, 1>), g1, dim3(256), 0, st, a);
-    } else {
-        if (p.spw == 2) hipLaunchKernelGGL((k_q4_gemm<2, 2>), g2, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_q4_gemm<2, 1>), g2, dim3(256), 0, st, a);
-    }
+    const int mt = a.mtiles == 1 ? 1 : 2;
+    const dim3 grid(p.sets, p.ks, mt == 1 ? 1 : (a.mtiles + 1) / 2);
+    if (wt == WT_Q8_0) launch_gemm<WT_Q8_0>(mt, p.spw, grid, a, st);
+    else launch_gemm<WT_Q4_0>(mt, p.spw, grid, a, st);
     return p.ks;
 }
 
 int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
-                    const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st) {
+                    const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st, int wt) {
     if (M <= 0 || max_items <= 0) return 0;
+    if (wt != WT_Q4_0 && wt != WT_Q8_0) return -1;
     if (part == nullptr || part_bytes < (size_t) M * N * sizeof(float)) return -1;
     GemmArgs a{};
     a.w = w; a.xa = xa; a.part = part;
@@ -476,14 +540,16 @@ int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, cons
     a.M = M; a.N = N; a.K = K; a.epi = EPI_STORE;
     a.nstripes = (N + 15) / 16; a.ngroups = (K / 32 + 3) / 4; a.ks = 1; a.gps = a.ngroups;
     a.mtiles = (M + 15) / 16;
-    hipLaunchKernelGGL((k_q4_gemm<1, 1>), dim3((a.nstripes + 3) / 4, 1, max_items), dim3(256), 0, st, a);
+    const dim3 grid((a.nstripes + 3) / 4, 1, max_items);
+    if (wt == WT_Q8_0) hipLaunchKernelGGL((k_q4_gemm<WT_Q8_0, 1, 1>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_q4_gemm<WT_Q4_0, 1, 1>), grid, dim3(256), 0, st, a);
     return 1;
 }
 
 int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* ws,
-            size_t ws_bytes, hipStream_t st) {
+            size_t ws_bytes, hipStream_t st, int wt) {
     if (M <= 0) return 0;
-    const int ks = q4_gemm_raw(w, xa, M, N, K, ws, ws_bytes, st);
+    const int ks = q4_gemm_raw(w, xa, M, N, K, ws, ws_bytes, st, wt);
     if (ks < 0) return -1;
     GemmArgs a{};
     a.part = ws; a.y = y;
@@ -493,9 +559,10 @@ int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, 
     return 0;
 }
 
-void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int soff, hipStream_t st) {
+void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int soff, hipStream_t st, int wt) {
     const int tiles = ((N + 15) / 16) * ((K / 32 + 3) / 4);
-    hipLaunchKernelGGL(k_q4_repack, dim3(tiles), dim3(64), 0, st, src, N, K, dst, sstride, soff);
+    if (wt == WT_Q8_0) hipLaunchKernelGGL(k_q8_repack, dim3(tiles), dim3(64), 0, st, src, N, K, dst, sstride, soff);
+    else hipLaunchKernelGGL(k_q4_repack, dim3(tiles), dim3(64), 0, st, src, N, K, dst, sstride, soff);
 }
 
 template <int IT>
@@ -561,6 +628,34 @@ __global__ void k_q4_dequant(const uint8_t* __restrict__ w, int N, int K, float*
             out[(size_t) row * K + 32 * blk + e] = w8 * dw[b];
         }
     }
+}
+
+__global__ void k_q8_dequant(const uint8_t* __restrict__ w, int N, int K, float* __restrict__ out) {
+    const int nb = K / 32, ngroups = (nb + 3) / 4;
+    const int tile = blockIdx.x, stripe = tile / ngroups, grp = tile % ngroups;
+    const int lane = threadIdx.x, n = lane & 15, g = lane >> 4, row = stripe * 16 + n;
+    const uint8_t* tp = w + (size_t) tile * Q8T_BYTES;
+    const u32x4 w0 = *(const u32x4*) (tp + 32 * lane), w1 = *(const u32x4*) (tp + 32 * lane + 16);
+    const half4v sc = *(const half4v*) (tp + Q8T_SCALE_OFF + 8 * n);
+    for (int b = 0; b < 4; ++b) {
+        const int blk = 4 * grp + b;
+        if (row >= N || blk >= nb) continue;
+        const u32x4 wv = b < 2 ? w0 : w1;
+        const half8 q = q8_unpack(wv[2 * (b % 2)], wv[2 * (b % 2) + 1]);  // 1024 + u, 16 (1024 + u); u = q + 128
+        for (int j = 0; j < 8; ++j) {
+            const int e = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
+            const float qv = j < 4 ? (float) q[j] - 1152.0f : (float) q[j] * 0.0625f - 1152.0f;  // q, exactly
+            out[(size_t) row * K + 32 * blk + e] = qv * (float) sc[b];
+        }
+    }
+}
+
+extern "C" int snk_q8_dequant(const void* d_tiles, int N, int K, float* d_w, void* stream) {
+    if (N <= 0 || K <= 0 || K % 32) return -1;
+    const int tiles = ((N + 15) / 16) * ((K / 32 + 3) / 4);
+    hipLaunchKernelGGL(k_q8_dequant, dim3(tiles), dim3(64), 0, (hipStream_t) stream, (const uint8_t*) d_tiles, N, K,
+                       d_w);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 extern "C" int snk_q4_dequant(const void* d_stripes, int N, int K, float* d_w, void* stream) {

@@ -39,6 +39,18 @@ void sn_set_err(char* err, int err_len, const char* fmt, ...);
 #define Q4T_BYTES 1152
 #define Q4T_SCALE_OFF 1024
 
+// ---- Q8_0 weights in HBM ------------------------------------------------------------------------------------------
+// A GGUF Q8_0 matrix (N rows of K/32 34-byte blocks: fp16 d, 32 int8 q; value d*q) is re-laid at upload into tiles of
+// 16 rows x 4 blocks, 2176 bytes each (= 64 x 34, the GGUF bytes):
+//   bytes [0, 2048): lane l = n + 16 g holds 32 bytes, for blocks b = 0..3 of row n: at 32 l + 8 b the int8 q of
+//                    elements 4g..4g+3, then of 16+4g..16+4g+3 (the element order of the Q4_0 tile lanes);
+//   bytes [2048, 2176): the 16 rows' fp16 scales d, 4 per row (offset 2048 + 8 n + 2 b).
+#define Q8T_BYTES 2176
+#define Q8T_SCALE_OFF 2048
+// weight types (ggml's type ids)
+enum { WT_Q4_0 = 2, WT_Q8_0 = 8 };
+__host__ __device__ static inline int wt_tile_bytes(int wt) { return wt == WT_Q8_0 ? Q8T_BYTES : Q4T_BYTES; }
+
 // ---- activation operand ("xa"): Q8_0-quantized rows as fp16 MFMA fragments -----------------------------------------
 // Rows are quantized to Q8_0 exactly as ggml's x86 CPU backend does (per 32-block: d = amax/127 stored fp16,
 // q = round-half-even(x * 127/amax)). The operand is a sequence of records, one per (16-row tile mt, 4-block group c),
@@ -46,15 +58,19 @@ void sn_set_err(char* err, int err_len, const char* fmt, ...);
 //   [bb * 1024, +1024)   the fragment of block 4c + bb: lane l = m + 16 g holds row m's elements 4g..4g+3 as q and
 //                        16+4g..16+4g+3 as q / 16 (8 fp16, all exact; the order of the weight tile lanes);
 //   [4096 + bb * 64, +64) the 16 rows' scales d as fp32 (the fp16 value, exactly);
-//   [4352 + bb * 64, +64) the 16 rows' corrections -(1032 * sum of q over elements 0..15 + 72 * sum over 16..31), an
-//                        exact integer.
-// The matmul unpacks a weight nibble w to fp16 (1024 + w) for elements 0..15 and (1024 + 16 w) for 16..31; an fp16
-// MFMA of a fragment against them, with the correction as its C input, is sum q (w - 8), ggml's integer block sum,
-// exactly: every term and every partial sum is an integer below 2^23 in magnitude.
+//   [4352 + bb * 64, +64) the 16 rows' corrections for Q4_0 weights, -(1032 * sum of q over elements 0..15 + 72 * sum
+//                        over 16..31), an exact integer;
+//   [4608 + bb * 64, +64) the 16 rows' corrections for Q8_0 weights, -1152 * sum of q over all 32 elements.
+// The Q4_0 matmul unpacks a weight nibble w to fp16 (1024 + w) for elements 0..15 and (1024 + 16 w) for 16..31; an fp16
+// MFMA of a fragment against them, with the Q4_0 correction as its C input, is sum q (w - 8), ggml's integer block sum
+// (vec_dot_q4_0_q8_0), exactly: every term and every partial sum is an integer below 2^23 in magnitude. The Q8_0
+// matmul unpacks a weight byte w (int8) to fp16 (1024 + (w + 128)) for elements 0..15 and 16 (1024 + (w + 128)) for
+// 16..31; with the Q8_0 correction the MFMA is sum q w (vec_dot_q8_0_q8_0), exactly in the same way.
 // Row tiles are rounded up to an even count and blocks to whole groups; padding blocks are zero.
-#define XA_REC 4608
+#define XA_REC 4864
 #define XA_DX_OFF 4096
 #define XA_CORR_OFF 4352
+#define XA_CORR8_OFF 4608
 
 __host__ __device__ static inline int xa_nbp(int K) { return (K / 32 + 3) / 4 * 4; }
 __host__ __device__ static inline int xa_ngroups(int K) { return (K / 32 + 3) / 4; }
@@ -65,6 +81,10 @@ __host__ __device__ static inline size_t xa_rec_off(int K, int m, int b) {
 }
 __host__ __device__ static inline size_t xa_bytes(int M, int K) { return (size_t) xa_mtp(M) * xa_ngroups(K) * XA_REC; }
 static inline size_t q4t_bytes(int N, int K) { return (size_t) ((N + 15) / 16) * ((K / 32 + 3) / 4) * Q4T_BYTES; }
+// bytes of an N x K matrix of weight type wt in the tile layout
+static inline size_t wt_bytes(int wt, int N, int K) {
+    return (size_t) ((N + 15) / 16) * ((K / 32 + 3) / 4) * wt_tile_bytes(wt);
+}
 
 // The sum, in slice order, of ks <= KM k-slices of a matmul (slice k at p + k * stride). Every load is issued before
 // any is used (the slice index is clamped, so no load sits behind a branch); the slices past ks are not added.

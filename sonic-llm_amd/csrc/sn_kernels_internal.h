@@ -25,19 +25,22 @@ struct GemmPlan {
 };
 
 // Depends on (N, K) only, never on the rows.
-GemmPlan q4_plan(int N, int K);
+GemmPlan q4_plan(int N, int K, int wt = WT_Q4_0);
 // The k-slice sums of a matmul of M rows: ks * M * N floats.
-size_t q4_workspace_bytes(int M, int N, int K);
+size_t q4_workspace_bytes(int M, int N, int K, int wt = WT_Q4_0);
 // Raw matmul: part[slice][M][N] = the slice's sums (the consumer adds the slices in order). Returns the slice count,
-// or -1 when part_bytes is too small.
+// or -1 when part_bytes is too small. wt: the weight type of w (WT_Q4_0 or WT_Q8_0 tiles).
 int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
-                hipStream_t st);
+                hipStream_t st, int wt = WT_Q4_0);
 // Grouped raw matmul of expert matrices (moe: qmm_grouped, sn_attn.inc.h:352-359): up to max_items (expert, row tile)
 // items, the device count in `count`; part[M][N] rows of each item's tile (one slice).
 int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
-                    const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st);
-// GGUF Q4_0 rows -> stripes; source stripe s lands at destination stripe s * sstride + soff.
-void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int soff, hipStream_t st);
+                    const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st,
+                    int wt = WT_Q4_0);
+// GGUF Q4_0 (wt = WT_Q4_0) or Q8_0 (WT_Q8_0) rows -> tiles; source stripe s lands at destination stripe
+// s * sstride + soff.
+void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int soff, hipStream_t st,
+               int wt = WT_Q4_0);
 // rows (optional): row m of the operand is row rows[m] of x (rows[m] < 0: a zero row). nw (optional): RMSNorm weight
 // applied first.
 // xn (optional): the normed fp32 rows, ldn apart.
@@ -53,7 +56,7 @@ int resid_quant(float* x, const float* part, int ks, int M, int K, const float* 
 // part[ks][M][2F].
 void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st);
 int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* ws,
-            size_t ws_bytes, hipStream_t st);
+            size_t ws_bytes, hipStream_t st, int wt = WT_Q4_0);
 
 // ---- paged attention ----
 // One work item = (query group, KV head, chunk of ATT_CHUNK cells). A query group is up to 16/G rows of one

@@ -16,6 +16,14 @@ extern "C" int snk_q4_repack(const void* d_q4, int N, int K, void* d_stripes, vo
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+extern "C" size_t snk_q8_tiles_bytes(int N, int K) { return wt_bytes(WT_Q8_0, N, K); }
+
+extern "C" int snk_q8_repack(const void* d_q8, int N, int K, void* d_tiles, void* stream) {
+    if (N <= 0 || K <= 0 || K % 32) return -1;
+    q4_repack((const uint8_t*) d_q8, N, K, (uint8_t*) d_tiles, 1, 0, (hipStream_t) stream, WT_Q8_0);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 extern "C" size_t snk_xa_bytes(int M, int K) { return xa_bytes(M, K); }
 
 extern "C" int snk_quant_act(const float* d_x, int M, int K, int ldx, const float* d_norm_w, float eps, void* d_xa,
@@ -33,6 +41,17 @@ extern "C" int snk_q4_gemm(const void* d_stripes, const void* d_xa, int M, int N
     if (epi == SNK_EPI_SWIGLU ? (N % 32 != 0 || ldy < N / 2) : ldy < N) return -1;
     const int rc = q4_gemm((const uint8_t*) d_stripes, (const uint8_t*) d_xa, M, N, K, d_y, ldy, epi, (float*) d_ws,
                            ws_bytes, (hipStream_t) stream);
+    return rc == 0 && hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" size_t snk_q8_workspace_bytes(int M, int N, int K) { return q4_workspace_bytes(M, N, K, WT_Q8_0); }
+
+extern "C" int snk_q8_gemm(const void* d_tiles, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi,
+                           void* d_ws, size_t ws_bytes, void* stream) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 32 || epi < 0 || epi > 2) return -1;
+    if (epi == SNK_EPI_SWIGLU ? (N % 32 != 0 || ldy < N / 2) : ldy < N) return -1;
+    const int rc = q4_gemm((const uint8_t*) d_tiles, (const uint8_t*) d_xa, M, N, K, d_y, ldy, epi, (float*) d_ws,
+                           ws_bytes, (hipStream_t) stream, WT_Q8_0);
     return rc == 0 && hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

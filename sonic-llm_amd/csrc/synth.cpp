@@ -58,6 +58,21 @@ void sn_quantize_row_q4_0(const float* x, uint8_t* y, int64_t k) {
     }
 }
 
+// ggml quantize_row_q8_0_ref: d = amax / 127 (stored fp16), id = 1/d (0 when d is 0), q = roundf(x * id)
+void sn_quantize_row_q8_0(const float* x, uint8_t* y, int64_t k) {
+    for (int64_t i = 0; i < k / 32; i++) {
+        const float* xb = x + i * 32;
+        uint8_t* yb = y + i * 34;
+        float amax = 0.0f;
+        for (int j = 0; j < 32; j++) amax = std::max(amax, fabsf(xb[j]));
+        const float d = amax / 127.f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const _Float16 dh = (_Float16) d;
+        memcpy(yb, &dh, 2);
+        for (int j = 0; j < 32; ++j) yb[2 + j] = (uint8_t) (int8_t) (int) roundf(xb[j] * id);
+    }
+}
+
 namespace {
 struct Gen {
     std::string name;
@@ -96,35 +111,40 @@ extern "C" int snx_write_model(const char* path, const snx_model_cfg* c, uint64_
         w.u32(a + ".expert_used_count", (uint32_t) c->n_expert_used);
         w.u32(a + ".expert_feed_forward_length", (uint32_t) c->n_ff_exp);
     }
+    if (c->wtype != 0 && c->wtype != GGML_Q4_0 && c->wtype != GGML_Q8_0) {
+        sn_set_err(err, err_len, "snx_write_model: wtype must be 2 (Q4_0) or 8 (Q8_0)");
+        return -1;
+    }
+    const int WQ = c->wtype == GGML_Q8_0 ? GGML_Q8_0 : GGML_Q4_0;  // the matrices' type
     const float ws = c->w_std, nstd = 0.1f;
     std::vector<Gen> g;
     g.push_back({"token_embd.weight", GGML_F32, {E, V}, 0.0f, c->emb_std});
     g.push_back({"output_norm.weight", GGML_F32, {E}, 1.0f, nstd});
-    g.push_back({"output.weight", GGML_Q4_0, {E, V}, 0.0f, ws});
+    g.push_back({"output.weight", WQ, {E, V}, 0.0f, ws});
     const int nl = c->n_layer + (c->nextn ? 1 : 0);
     for (int i = 0; i < nl; ++i) {
         const std::string p = "blk." + std::to_string(i) + ".";
         g.push_back({p + "attn_norm.weight", GGML_F32, {E}, 1.0f, nstd});
-        g.push_back({p + "attn_q.weight", GGML_Q4_0, {E, H * D}, 0.0f, ws});
-        g.push_back({p + "attn_k.weight", GGML_Q4_0, {E, KVH * D}, 0.0f, ws});
-        g.push_back({p + "attn_v.weight", GGML_Q4_0, {E, KVH * D}, 0.0f, ws});
-        g.push_back({p + "attn_output.weight", GGML_Q4_0, {H * D, E}, 0.0f, ws});
+        g.push_back({p + "attn_q.weight", WQ, {E, H * D}, 0.0f, ws});
+        g.push_back({p + "attn_k.weight", WQ, {E, KVH * D}, 0.0f, ws});
+        g.push_back({p + "attn_v.weight", WQ, {E, KVH * D}, 0.0f, ws});
+        g.push_back({p + "attn_output.weight", WQ, {H * D, E}, 0.0f, ws});
         g.push_back({p + "attn_q_norm.weight", GGML_F32, {D}, 1.0f, nstd});
         g.push_back({p + "attn_k_norm.weight", GGML_F32, {D}, 1.0f, nstd});
         g.push_back({p + "ffn_norm.weight", GGML_F32, {E}, 1.0f, nstd});
         if (moe && i < c->n_layer) {
             const int64_t NE = c->n_expert, FE = c->n_ff_exp;
             g.push_back({p + "ffn_gate_inp.weight", GGML_F32, {E, NE}, 0.0f, 1.0f / sqrtf((float) E)});
-            g.push_back({p + "ffn_gate_exps.weight", GGML_Q4_0, {E, FE, NE}, 0.0f, ws});
-            g.push_back({p + "ffn_up_exps.weight", GGML_Q4_0, {E, FE, NE}, 0.0f, ws});
-            g.push_back({p + "ffn_down_exps.weight", GGML_Q4_0, {FE, E, NE}, 0.0f, ws});
+            g.push_back({p + "ffn_gate_exps.weight", WQ, {E, FE, NE}, 0.0f, ws});
+            g.push_back({p + "ffn_up_exps.weight", WQ, {E, FE, NE}, 0.0f, ws});
+            g.push_back({p + "ffn_down_exps.weight", WQ, {FE, E, NE}, 0.0f, ws});
         } else {
-            g.push_back({p + "ffn_gate.weight", GGML_Q4_0, {E, F}, 0.0f, ws});
-            g.push_back({p + "ffn_up.weight", GGML_Q4_0, {E, F}, 0.0f, ws});
-            g.push_back({p + "ffn_down.weight", GGML_Q4_0, {F, E}, 0.0f, ws});
+            g.push_back({p + "ffn_gate.weight", WQ, {E, F}, 0.0f, ws});
+            g.push_back({p + "ffn_up.weight", WQ, {E, F}, 0.0f, ws});
+            g.push_back({p + "ffn_down.weight", WQ, {F, E}, 0.0f, ws});
         }
         if (c->nextn && i == c->n_layer) {
-            g.push_back({p + "nextn.eh_proj.weight", GGML_Q4_0, {2 * E, E}, 0.0f, ws});
+            g.push_back({p + "nextn.eh_proj.weight", WQ, {2 * E, E}, 0.0f, ws});
             g.push_back({p + "nextn.enorm.weight", GGML_F32, {E}, 1.0f, nstd});
             g.push_back({p + "nextn.hnorm.weight", GGML_F32, {E}, 1.0f, nstd});
             g.push_back({p + "nextn.shared_head_norm.weight", GGML_F32, {E}, 1.0f, nstd});
@@ -166,6 +186,7 @@ extern "C" int snx_write_model(const char* path, const snx_model_cfg* c, uint64_
                         normals(seed, ti, (uint64_t) r, t.mean, t.std, row.data(), K);
                         uint8_t* dst = buf.data() + (size_t) (r - r0) * rb;
                         if (t.type == GGML_F32) memcpy(dst, row.data(), rb);
+                        else if (t.type == GGML_Q8_0) sn_quantize_row_q8_0(row.data(), dst, K);
                         else sn_quantize_row_q4_0(row.data(), dst, K);
                     }
                 });
@@ -182,3 +203,4 @@ extern "C" int snx_write_model(const char* path, const snx_model_cfg* c, uint64_
 }
 
 extern "C" void snx_quantize_q4_0(const float* x, uint8_t* y, int64_t k) { sn_quantize_row_q4_0(x, y, k); }
+extern "C" void snx_quantize_q8_0(const float* x, uint8_t* y, int64_t k) { sn_quantize_row_q8_0(x, y, k); }

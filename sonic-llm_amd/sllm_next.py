@@ -97,6 +97,11 @@ SNK_API = [
     ("snk_q4_repack", I, [P, I, I, P, P]),
     ("snk_q4_dequant", I, [P, I, I, P, P]),
     ("snk_xa_bytes", C.c_size_t, [I, I]),
+    ("snk_q8_tiles_bytes", C.c_size_t, [I, I]),
+    ("snk_q8_repack", I, [P, I, I, P, P]),
+    ("snk_q8_dequant", I, [P, I, I, P, P]),
+    ("snk_q8_workspace_bytes", C.c_size_t, [I, I, I]),
+    ("snk_q8_gemm", I, [P, P, I, I, I, P, I, I, P, C.c_size_t, P]),
     ("snk_quant_act", I, [P, I, I, I, P, C.c_float, P, P]),
     ("snk_q4_workspace_bytes", C.c_size_t, [I, I, I]),
     ("snk_q4_gemm", I, [P, P, I, I, I, P, I, I, P, C.c_size_t, P]),
@@ -120,6 +125,7 @@ EXT_API = [
 SYNTH_API = [
     ("snx_write_model", I, [CH, P, C.c_uint64, I, CH, I]),
     ("snx_quantize_q4_0", None, [P, P, C.c_int64]),
+    ("snx_quantize_q8_0", None, [P, P, C.c_int64]),
 ]
 
 
@@ -152,13 +158,14 @@ def call(f, *args):
 class ModelCfg(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_ff", "n_vocab",
                                        "n_expert", "n_expert_used", "n_ff_exp", "nextn")] + \
-               [(n, C.c_float) for n in ("rope_base", "eps", "w_std", "emb_std")]
+               [(n, C.c_float) for n in ("rope_base", "eps", "w_std", "emb_std")] + [("wtype", C.c_int)]
 
 
 def model_cfg(n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, head_dim=128, n_expert=0, n_expert_used=0,
-              n_ff_exp=0, nextn=0, rope_base=1e6, eps=1e-6, w_std=0.02, emb_std=0.02) -> ModelCfg:
+              n_ff_exp=0, nextn=0, rope_base=1e6, eps=1e-6, w_std=0.02, emb_std=0.02, wtype=2) -> ModelCfg:
+    """wtype: the matrices' block type, 2 Q4_0 or 8 Q8_0."""
     return ModelCfg(n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_expert, n_expert_used, n_ff_exp,
-                    nextn, rope_base, eps, w_std, emb_std)
+                    nextn, rope_base, eps, w_std, emb_std, wtype)
 
 
 # The configs' models (BASELINE.json configs[2], configs[3], configs[4])

@@ -39,18 +39,19 @@ def stream():
 
 
 def xa_decode(xa: np.ndarray, M: int, K: int):
-    """The activation operand back to (q [M][K] as int, d [M][K/32] as float32): undoes the record layout (one 4608-byte
+    """The activation operand back to (q [M][K] as int, d [M][K/32] as float32): undoes the record layout (one 4864-byte
     record per 16-row tile and 4-block group: 4 fragments whose lane l = m + 16 g holds row m's elements 4g..4g+3 as q
-    and 16+4g.. as q / 16, then the rows' scales and corrections as fp32). Also checks every block's correction against
-    its integers: -(1032 * sum of q over elements 0..15 + 72 * sum over 16..31)."""
+    and 16+4g.. as q / 16, then the rows' scales and two corrections as fp32). Also checks every block's corrections
+    against its integers: -(1032 * sum of q over elements 0..15 + 72 * sum over 16..31) and -1152 * sum of q."""
     nb = K // 32
     ng = (nb + 3) // 4
     mtp = (M + 31) // 32 * 2  # row tiles, rounded up to an even count
     mt = (M + 15) // 16
-    rec = xa.view(np.uint8)[:mtp * ng * 4608].reshape(mtp, ng, 4608)[:mt]
+    rec = xa.view(np.uint8)[:mtp * ng * 4864].reshape(mtp, ng, 4864)[:mt]
     frag = rec[:, :, :4096].copy().view(np.float16).reshape(mt, ng, 4, 4, 16, 8).astype(np.float32)  # [mt][c][bb][g][m][j]
     dx = rec[:, :, 4096:4352].copy().view(np.float32).reshape(mt, ng, 4, 16)
     corr = rec[:, :, 4352:4608].copy().view(np.float32).reshape(mt, ng, 4, 16)
+    corr8 = rec[:, :, 4608:4864].copy().view(np.float32).reshape(mt, ng, 4, 16)
     q = np.zeros((mt, 16, ng * 4, 32), np.float32)  # [mt][m][block][element]
     for g in range(4):
         for j in range(8):
@@ -60,6 +61,8 @@ def xa_decode(xa: np.ndarray, M: int, K: int):
     want_corr = -(1032.0 * q[..., :16].sum(-1) + 72.0 * q[..., 16:].sum(-1))  # [mt][m][block]
     got_corr = corr.transpose(0, 3, 1, 2).reshape(mt, 16, ng * 4)
     assert np.array_equal(got_corr, want_corr), "activation operand: a block's correction does not match its integers"
+    got8 = corr8.transpose(0, 3, 1, 2).reshape(mt, 16, ng * 4)
+    assert np.array_equal(got8, -1152.0 * q.sum(-1)), "activation operand: a block's Q8_0 correction is wrong"
     d = dx.transpose(0, 3, 1, 2).reshape(mt * 16, ng * 4)[:, :nb]
     return q.reshape(mt * 16, ng * 4 * 32)[:M, :K], d[:M]
 

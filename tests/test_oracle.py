@@ -147,6 +147,71 @@ def test_mul_mat_vs_f64():
     assert np.allclose(Yf, X.astype(np.float64) @ Wd.T, rtol=1e-12, atol=1e-12)
 
 
+# ---- Q8_0 weights (block_q8_0: kernels.metal:9; ggml quantize_row_q8_0_ref, dequantize_row_q8_0, vec_dot_q8_0_q8_0) -----
+def test_quantize_q8_0_ref_invariants():
+    r = rng(21)
+    w = r.normal(0, 0.02, (6, 256)).astype(np.float32)
+    w[2, :32] = 0.0
+    q = O.quantize_q8_0_ref(w).reshape(-1, 34)
+    wb = w.reshape(-1, 32).astype(np.float64)
+    for i in range(len(q)):
+        d = float(q[i, :2].copy().view(np.float16)[0])
+        qi = q[i, 2:].view(np.int8).astype(np.int64)
+        amax = np.abs(wb[i]).max()
+        if amax == 0:
+            assert d == 0 and np.all(qi == 0)
+            continue
+        d32 = np.float32(amax) / np.float32(127)
+        assert np.float16(d32) == np.float16(d)
+        j = np.argmax(np.abs(wb[i]))
+        assert qi[j] == np.sign(wb[i][j]) * 127 and np.abs(qi).max() == 127
+        # q is the nearest integer to x / d (d in fp32 before its fp16 rounding), so d * q is within d / 2 + the fp16
+        # rounding of d times 127
+        assert np.all(np.abs(wb[i] / float(d32) - qi) <= 0.5 + 1e-5)
+    # dequantize_row_q8_0 is d * q exactly
+    deq = O.dequantize_q8_0(q.reshape(6, -1), 256).reshape(-1, 32)
+    want = q[:, 2:].view(np.int8).astype(np.float32) * q[:, :2].copy().view(np.float16).astype(np.float32)
+    assert np.array_equal(deq, want)
+
+
+def test_quantize_q8_0_ref_rounds_half_away_from_zero():
+    # d = 127 / 127 = 1 exactly, id = 1: x = k + 0.5 lands on a tie; the weights' quantizer (roundf) goes away from zero,
+    # where the activations' x86 quantizer (round-half-even) goes to the even neighbour
+    x = np.zeros((1, 32), np.float32)
+    x[0, :5] = [127.0, 2.5, 3.5, -2.5, -0.5]
+    qw = O.quantize_q8_0_ref(x).reshape(34)[2:].view(np.int8)
+    qa = O.quantize_q8_0(x).reshape(34)[2:].view(np.int8)
+    assert list(qw[:5]) == [127, 3, 4, -3, -1]
+    assert list(qa[:5]) == [127, 2, 4, -2, 0]
+
+
+def test_vec_dot_q8_0_is_integer_block_sum_bitwise():
+    r = rng(22)
+    K = 1024
+    w = O.quantize_q8_0_ref(r.normal(0, 0.02, (1, K)).astype(np.float32)).reshape(-1, 34)
+    x = O.quantize_q8_0(r.normal(0, 1, (1, K)).astype(np.float32)).reshape(-1, 34)
+    # ggml's generic loop restated in float32: sumf += float(sumi) * (dw * dx), block by block
+    sumf = np.float32(0.0)
+    for b in range(K // 32):
+        sumi = int((w[b, 2:].view(np.int8).astype(np.int64) * x[b, 2:].view(np.int8).astype(np.int64)).sum())
+        dw = np.float32(w[b, :2].copy().view(np.float16)[0])
+        dx = np.float32(x[b, :2].copy().view(np.float16)[0])
+        sumf = np.float32(sumf + np.float32(sumi) * np.float32(dw * dx))
+    got = np.float32(O.lib().or_vec_dot_q8_0_q8_0(K, O._p(w), O._p(x)))
+    assert got.view(np.uint32) == sumf.view(np.uint32)
+
+
+def test_mul_mat_q8_0_vs_f64():
+    r = rng(23)
+    N, K, M = 80, 512, 6
+    W = O.quantize_q8_0_ref(r.normal(0, 0.02, (N, K)).astype(np.float32))
+    X = r.normal(0, 1, (M, K)).astype(np.float32)
+    Y = O.mul_mat_q8_0(W, K, X)
+    Wd = O.dequantize_q8_0(W, K).astype(np.float64)
+    Xq = O.dequantize_q8_0(O.quantize_q8_0(X), K).astype(np.float64)
+    assert np.max(np.abs(Y - Xq @ Wd.T)) <= 1e-5 * np.max(np.abs(Y))
+
+
 # ---- row math -----------------------------------------------------------------------------------------------------------
 def test_rmsnorm_closed_form():
     r = rng(6)
