@@ -34,7 +34,8 @@ def log(msg):
 def model_file(cfg_kw, seed, path=None):
     import sllm_next as S
     d = os.environ.get("SN_BENCH_DIR") or "/tmp"
-    tag = ("_mtp" if cfg_kw.get("nextn") else "") + (f"_moe{cfg_kw['n_expert']}" if cfg_kw.get("n_expert") else "")
+    tag = ("_mtp" if cfg_kw.get("nextn") else "") + (f"_moe{cfg_kw['n_expert']}" if cfg_kw.get("n_expert") else "") + \
+          ("_q8" if cfg_kw.get("wtype") == 8 else "")
     path = path or os.path.join(d, f"sonic_qwen3_{cfg_kw['n_layer']}L_{cfg_kw['n_embd']}{tag}_{seed}.gguf")
     done = path + ".done"
     if not (os.path.exists(path) and os.path.exists(done)):
@@ -88,6 +89,8 @@ def main():
                          "moe: Qwen3-30B-A3B-arch batched decode (configs[4])")
     ap.add_argument("--accept", type=float, default=0.6, help="mtp: the seeded share of drafts forced to match")
     ap.add_argument("--no-graphs", action="store_true", help="launch every step eagerly (no HIP graph replay)")
+    ap.add_argument("--wtype", type=int, default=2, choices=(2, 8),
+                    help="decode / moe: the model's matrices in Q4_0 (2, the configs) or Q8_0 (8)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device once (a plain copy kernel of known size, to scale "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -116,6 +119,8 @@ def main():
         return bench_mtp(args)
     moe = args.config == "moe"
     cfg = dict(S.QWEN3_30B_A3B if moe else S.QWEN3_4B)
+    if args.wtype == 8:
+        cfg["wtype"] = 8
     path = model_file(cfg, args.seed, args.model)
     B, ctx = args.seqs, args.ctx
     total = ctx + args.warmup + args.steps + args.prof_steps + 1
@@ -171,7 +176,7 @@ def main():
     # WRITE_SIZE, scaled by a copy of known size): profiles/decode_qwen3_4b_b32_ctx2048_traffic.md
     traffic = {}
     tpath = os.path.join(ROOT, "profiles", "decode_qwen3_4b_b32_ctx2048_traffic.json")
-    if not moe and (B, ctx) == (32, 2048) and os.path.exists(tpath):
+    if not moe and args.wtype == 2 and (B, ctx) == (32, 2048) and os.path.exists(tpath):
         traffic = json.load(open(tpath))
 
     def roof(k):
@@ -187,15 +192,17 @@ def main():
         t = time.time()
         cpu = cpu_baseline(path, B, ctx, args.seed)
         log(f"[bench] cpu baseline in {time.time() - t:.1f}s: {cpu['value']:.2f} tok/s")
-    metric = ("agg decode tok/s, Qwen3-30B-A3B-arch Q4_0 MoE x32 seqs" if moe else
-              "agg decode tok/s, Qwen3-4B-arch Q4_0 x32 seqs; Q4_0 GEMV % HBM peak")
-    workload = ("Qwen3-30B-A3B-arch Q4_0 MoE batched decode step (BASELINE.json configs[4])" if moe else
-                "Qwen3-4B-arch Q4_0 batched decode step (BASELINE.json configs[2])")
+    q = "Q8_0" if args.wtype == 8 else "Q4_0"
+    metric = (f"agg decode tok/s, Qwen3-30B-A3B-arch {q} MoE x32 seqs" if moe else
+              f"agg decode tok/s, Qwen3-4B-arch {q} x32 seqs; {q} GEMV % HBM peak")
+    workload = (f"Qwen3-30B-A3B-arch {q} MoE batched decode step (BASELINE.json configs[4])" if moe else
+                f"Qwen3-4B-arch {q} batched decode step (BASELINE.json configs[2]" +
+                (")" if args.wtype == 2 else ", its matrices in Q8_0)"))
     line = {
         "metric": metric,
         "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "q4_0 x q8_0 -> f32 (fp16 MFMA); f16 KV, f32 softmax",
+        "vs_baseline": None, "dtype": f"{q.lower()} x q8_0 -> f32 (fp16 MFMA); f16 KV, f32 softmax",
         "data": "synthetic: random-init weights (seeded), random token ids, seeded N(0,1) fp16 context cells",
         "config": {"workload": workload, "seqs": B,
                    "ctx": ctx, "layers": cfg["n_layer"], "hidden": cfg["n_embd"], "heads": cfg["n_head"],
