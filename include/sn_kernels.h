@@ -71,6 +71,15 @@ int snk_qk_rope(float* d_qkv, int ldqkv, int R, int H, int KVH, const float* d_q
                 float theta_scale, const int32_t* d_seq, const int32_t* d_pos, const int32_t* d_pt, int max_pages,
                 int page_cells, void* d_kpool, void* d_vpool, void* stream);
 
+// ---- greedy argmax of logit rows (argmax / argmax_p, kernels.metal:327-442) -------------------------------------------
+// d_logits: n rows of V fp32 scores; d_out[r] = the first index of the largest score of row r; rows with d_skip[r] != 0
+// (d_skip may be NULL) never take the nban <= 8 ids of d_ban (-1 when every id is banned). d_rec (may be NULL): per row
+// 8 words: chosen id, its score, best id, best score, second id, second score (the pair over all ids, ties to the lower
+// id), log-sum-exp, 0. d_ws: snk_argmax_workspace_bytes(n, V) bytes. 0, or -1 (bad arguments, workspace too small).
+size_t snk_argmax_workspace_bytes(int n, int V);
+int snk_argmax(const float* d_logits, int V, int n, const int32_t* d_ban, int nban, const uint8_t* d_skip,
+               int32_t* d_out, float* d_rec, void* d_ws, size_t ws_bytes, void* stream);
+
 // ---- MFMA operand layout check: D = A . B for one v_mfma_f32_16x16x32_f16 (A, B as 64 lanes x 8 fp16 each, D as 64
 // lanes x 4 fp32), the raw lane contents in and out
 int snk_mfma_probe(const void* d_a, const void* d_b, float* d_d, void* stream);

@@ -239,12 +239,13 @@ void or_top2(const float* x, int64_t n, int32_t* i1, float* v1, int32_t* i2, flo
         }
     }
     double s = 0.0;
-    for (int64_t i = 0; i < n; i++) s += exp((double) x[i] - (double) m1);
+    if (m1 > -INFINITY)
+        for (int64_t i = 0; i < n; i++) s += exp((double) x[i] - (double) m1);
     *i1 = a;
     *v1 = m1;
     *i2 = b;
     *v2 = m2;
-    *lse = (float) ((double) m1 + log(s));
+    *lse = m1 > -INFINITY ? (float) ((double) m1 + log(s)) : -INFINITY;  // no finite score: -inf (kernels.metal:436)
 }
 
 // ggml_rope_cache_init with ext_factor 0, freq_scale 1, mscale 1: theta starts at p and is multiplied by theta_scale

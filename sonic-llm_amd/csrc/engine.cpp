@@ -85,6 +85,8 @@ struct sn_engine {
     int32_t *d_otok = nullptr, *h_otok = nullptr;
     float *d_rec = nullptr, *h_rec = nullptr;
     int32_t* d_ban = nullptr;
+    uint8_t* d_amx = nullptr;  // the argmax's per-chunk partials
+    size_t amx_bytes = 0;
 
     std::vector<int32_t> pt;  // [slots][max_pages], -1: no page
     std::vector<int> ref;     // holders of each page
@@ -457,8 +459,10 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->d_otok = e->dalloc<int32_t>((size_t) MO * 4, err, err_len);
     e->d_rec = e->dalloc<float>((size_t) MO * 32, err, err_len);
     e->d_ban = e->dalloc<int32_t>(8 * 4, err, err_len);
+    e->amx_bytes = argmax_workspace_bytes(MO, e->V);
+    e->d_amx = e->dalloc<uint8_t>(e->amx_bytes, err, err_len);
     if (!e->d_pt || !e->x || !e->qkv || !e->ao || !e->hb || !e->logits || !e->xa || !e->gemm_ws || !e->apart ||
-        !e->d_stage || !e->d_otok || !e->d_rec || !e->d_ban)
+        !e->d_stage || !e->d_otok || !e->d_rec || !e->d_ban || !e->d_amx)
         return fail("");
     if (e->has_nextn) {
         const int RS = std::max(R, slots);
@@ -822,8 +826,8 @@ struct Dev {
         const int nban = (int) e->eog.size();
         int32_t* out = d_otok ? d_otok : e->d_otok;
         rc |= e->launch(SNX_K_OTHER, (double) n * V * 4, [&] {
-            argmax_rows(e->logits, V, n, e->d_ban, nban, d_skip, out, e->want_probs && !d_otok ? e->d_rec : nullptr, st);
-            return 0;
+            return argmax_rows(e->logits, V, n, e->d_ban, nban, d_skip, out, e->want_probs && !d_otok ? e->d_rec : nullptr,
+                               e->d_amx, e->amx_bytes, st);
         });
     }
     void head_logits(int n) {
@@ -875,8 +879,7 @@ struct Dev {
         quant(e->mx, nullptr, n, E, e->mtp_hdnorm, e->mhg);
         head_logits(n);
         rc |= e->launch(SNX_K_OTHER, (double) n * e->V * 4, [&] {
-            argmax_rows(e->logits, e->V, n, e->d_ban, 0, nullptr, d_gout, nullptr, st);
-            return 0;
+            return argmax_rows(e->logits, e->V, n, e->d_ban, 0, nullptr, d_gout, nullptr, e->d_amx, e->amx_bytes, st);
         });
     }
 };
@@ -1255,7 +1258,9 @@ extern "C" int sn_probs(sn_engine* e, int n_out, float* dst, char* err, int err_
 }
 
 extern "C" int sn_set_eog(sn_engine* e, const int32_t* ids, int n) {
-    if (n < 0 || n > 8) return -1;
+    if (n < 0 || n > 8 || n >= e->V) return -1;
+    for (int i = 0; i < n; ++i)
+        if (ids[i] < 0 || ids[i] >= e->V) return -1;
     e->eog.assign(ids, ids + n);
     if (n > 0 && hipMemcpy(e->d_ban, ids, (size_t) n * 4, hipMemcpyHostToDevice) != hipSuccess) return -1;
     return 0;

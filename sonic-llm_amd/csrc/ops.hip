@@ -94,8 +94,11 @@ void qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, in
 }
 
 // ---- greedy argmax (argmax / argmax_p, kernels.metal:327-442) -------------------------------------------------------
-// The first index of the largest score; rows with skip[r] never take the ids in ban. rec (optional): per row 8 words:
-// chosen id, chosen score, best id, best score, second id, second score, log-sum-exp, 0 (ids ascending among ties).
+// The first index of the largest score; rows with skip[r] never take the ids in ban (a row whose every id is banned
+// gets -1). rec (optional): per row 8 words: chosen id, chosen score, best id, best score, second id, second score,
+// log-sum-exp, 0 (ids ascending among ties; the best/second pair over all ids, banned or not). NaN scores never win.
+// Two launches: every (row, chunk of AMX_CHUNK ids) workgroup reduces its chunk to a partial record, then one
+// wavefront per row merges the row's partials, so a batch of rows spreads over the whole chip.
 struct Top2 {
     float m1;
     int i1;
@@ -116,95 +119,136 @@ __device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
     }
     return o;
 }
+// the partial of a chunk: chosen (best, idx), the pair (tp), and the chunk's sum of exp(x - tp.m1) (z)
+struct AmxPart {
+    float best;
+    int idx;
+    Top2 tp;
+    float z;
+    float pad;
+};
+// merge of two partials; z of the one with the smaller max is rescaled (an empty side, max -inf, adds nothing)
+__device__ __forceinline__ AmxPart amx_merge(AmxPart a, AmxPart b, bool lse) {
+    AmxPart o;
+    const bool bb = better(b.best, b.idx, a.best, a.idx);
+    o.best = bb ? b.best : a.best;
+    o.idx = bb ? b.idx : a.idx;
+    o.tp = top2_merge(a.tp, b.tp);
+    o.z = 0.0f;
+    if (lse) {
+        const float m = o.tp.m1;
+        if (m > -INFINITY) {
+            if (a.tp.m1 > -INFINITY) o.z += a.z * expf(a.tp.m1 - m);
+            if (b.tp.m1 > -INFINITY) o.z += b.z * expf(b.tp.m1 - m);
+        }
+    }
+    o.pad = 0.0f;
+    return o;
+}
+__device__ __forceinline__ AmxPart amx_shfl(AmxPart p, int o) {
+    AmxPart q;
+    q.best = __shfl_xor(p.best, o);
+    q.idx = __shfl_xor(p.idx, o);
+    q.tp.m1 = __shfl_xor(p.tp.m1, o);
+    q.tp.i1 = __shfl_xor(p.tp.i1, o);
+    q.tp.m2 = __shfl_xor(p.tp.m2, o);
+    q.tp.i2 = __shfl_xor(p.tp.i2, o);
+    q.z = __shfl_xor(p.z, o);
+    q.pad = 0.0f;
+    return q;
+}
+__device__ __forceinline__ AmxPart amx_wave(AmxPart p, bool lse) {
+    for (int o = 32; o > 0; o >>= 1) p = amx_merge(p, amx_shfl(p, o), lse);
+    return p;
+}
 
-__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ logits, int V, const int32_t* __restrict__ ban,
-                                                 int nban, const uint8_t* __restrict__ skip, int32_t* __restrict__ out,
-                                                 float* __restrict__ rec) {
-    __shared__ float sv[16];
-    __shared__ int si[16];
-    __shared__ Top2 st2[16];
-    __shared__ float ssum[16];
-    __shared__ float s_max;
-    const int r = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+#define AMX_PER_THREAD (AMX_CHUNK / 256)
+template <bool LSE>
+__global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ logits, int V, int nch,
+                                                     const int32_t* __restrict__ ban, int nban,
+                                                     const uint8_t* __restrict__ skip, AmxPart* __restrict__ part) {
+    __shared__ AmxPart sp[4];
+    const int c = blockIdx.x, r = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
     const float* x = logits + (size_t) r * V;
     const int nb = (skip && skip[r]) ? nban : 0;
-    float best = -INFINITY;
-    int idx = 0x7fffffff;
-    Top2 tp = {-INFINITY, 0x7fffffff, -INFINITY, 0x7fffffff};
-    for (int i = t; i < V; i += 1024) {
-        const float v = x[i];
+    int bn[8];
+    for (int k = 0; k < 8; ++k) bn[k] = k < nb ? ban[k] : -1;
+    const int i0 = c * AMX_CHUNK + t;
+    float v[AMX_PER_THREAD];
+    for (int k = 0; k < AMX_PER_THREAD; ++k) {
+        const int i = i0 + 256 * k;
+        v[k] = i < V ? x[i] : -INFINITY;
+    }
+    AmxPart p = {-INFINITY, 0x7fffffff, {-INFINITY, 0x7fffffff, -INFINITY, 0x7fffffff}, 0.0f, 0.0f};
+    for (int k = 0; k < AMX_PER_THREAD; ++k) {  // ids ascending: strict > keeps the lower id of a tie
+        const int i = i0 + 256 * k;
+        if (i >= V) break;
         bool b = false;
-        for (int k = 0; k < nb; ++k) b = b || i == ban[k];
-        if (v > best && !b) {
-            best = v;
-            idx = i;
+        for (int j = 0; j < 8; ++j) b = b || i == bn[j];
+        if (!b && (p.idx == 0x7fffffff || v[k] > p.best)) {
+            p.best = v[k];
+            p.idx = i;
         }
-        if (rec) {
-            if (v > tp.m1) {
-                tp.m2 = tp.m1; tp.i2 = tp.i1; tp.m1 = v; tp.i1 = i;
-            } else if (v > tp.m2) {
-                tp.m2 = v; tp.i2 = i;
-            }
-        }
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o);
-        const int oi = __shfl_xor(idx, o);
-        if (better(ov, oi, best, idx)) {
-            best = ov;
-            idx = oi;
-        }
-        if (rec) {
-            Top2 q;
-            q.m1 = __shfl_xor(tp.m1, o); q.i1 = __shfl_xor(tp.i1, o);
-            q.m2 = __shfl_xor(tp.m2, o); q.i2 = __shfl_xor(tp.i2, o);
-            tp = top2_merge(tp, q);
+        if (v[k] > p.tp.m1) {
+            p.tp.m2 = p.tp.m1;
+            p.tp.i2 = p.tp.i1;
+            p.tp.m1 = v[k];
+            p.tp.i1 = i;
+        } else if (v[k] > p.tp.m2) {
+            p.tp.m2 = v[k];
+            p.tp.i2 = i;
         }
     }
-    if (lane == 0) {
-        sv[w] = best;
-        si[w] = idx;
-        st2[w] = tp;
-    }
+    if (LSE && p.tp.m1 > -INFINITY)
+        for (int k = 0; k < AMX_PER_THREAD; ++k)
+            if (i0 + 256 * k < V) p.z += expf(v[k] - p.tp.m1);
+    p = amx_wave(p, LSE);
+    if (lane == 0) sp[w] = p;
     __syncthreads();
     if (t == 0) {
-        for (int k = 1; k < 16; ++k) {
-            if (better(sv[k], si[k], best, idx)) {
-                best = sv[k];
-                idx = si[k];
-            }
-            if (rec) tp = top2_merge(tp, st2[k]);
-        }
-        out[r] = idx;
-        s_max = tp.m1;
-    }
-    if (!rec) return;
-    __syncthreads();
-    const float mx = s_max;
-    float s = 0.0f;
-    if (mx > -INFINITY)
-        for (int i = t; i < V; i += 1024) s += expf(x[i] - mx);
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-    if (lane == 0) ssum[w] = s;
-    __syncthreads();
-    if (t == 0) {
-        float z = 0.0f;
-        for (int k = 0; k < 16; ++k) z += ssum[k];
-        float* p = rec + (size_t) r * 8;
-        p[0] = __builtin_bit_cast(float, idx);
-        p[1] = best;
-        p[2] = __builtin_bit_cast(float, tp.i1);
-        p[3] = tp.m1;
-        p[4] = __builtin_bit_cast(float, tp.i2);
-        p[5] = tp.m2;
-        p[6] = mx > -INFINITY ? mx + logf(z) : -INFINITY;
-        p[7] = 0.0f;
+        for (int k = 1; k < 4; ++k) p = amx_merge(p, sp[k], LSE);
+        part[(size_t) r * nch + c] = p;
     }
 }
 
-void argmax_rows(const float* logits, int V, int n, const int32_t* ban, int nban, const uint8_t* skip, int32_t* out,
-                 float* rec, hipStream_t st) {
-    if (n > 0) hipLaunchKernelGGL(k_argmax, dim3(n), dim3(1024), 0, st, logits, V, ban, nban, skip, out, rec);
+template <bool LSE>
+__global__ __launch_bounds__(64) void k_argmax_fin(const AmxPart* __restrict__ part, int nch, int32_t* __restrict__ out,
+                                                   float* __restrict__ rec) {
+    const int r = blockIdx.x, lane = threadIdx.x;
+    AmxPart p = {-INFINITY, 0x7fffffff, {-INFINITY, 0x7fffffff, -INFINITY, 0x7fffffff}, 0.0f, 0.0f};
+    for (int c = lane; c < nch; c += 64) p = amx_merge(p, part[(size_t) r * nch + c], LSE);
+    p = amx_wave(p, LSE);
+    if (lane != 0) return;
+    const int idx = p.idx == 0x7fffffff ? -1 : p.idx;
+    out[r] = idx;
+    if (!LSE) return;
+    float* q = rec + (size_t) r * 8;
+    q[0] = __builtin_bit_cast(float, idx);
+    q[1] = p.best;
+    q[2] = __builtin_bit_cast(float, p.tp.i1);
+    q[3] = p.tp.m1;
+    q[4] = __builtin_bit_cast(float, p.tp.i2);
+    q[5] = p.tp.m2;
+    q[6] = p.tp.m1 > -INFINITY ? p.tp.m1 + logf(p.z) : -INFINITY;
+    q[7] = 0.0f;
+}
+
+size_t argmax_workspace_bytes(int n, int V) { return (size_t) n * argmax_chunks(V) * sizeof(AmxPart); }
+
+int argmax_rows(const float* logits, int V, int n, const int32_t* ban, int nban, const uint8_t* skip, int32_t* out,
+                float* rec, void* ws, size_t ws_bytes, hipStream_t st) {
+    if (n <= 0) return 0;
+    if (V <= 0 || nban < 0 || nban > 8 || argmax_workspace_bytes(n, V) > ws_bytes) return -1;
+    const int nch = argmax_chunks(V);
+    AmxPart* part = (AmxPart*) ws;
+    if (rec) {
+        hipLaunchKernelGGL(k_argmax_part<true>, dim3(nch, n), dim3(256), 0, st, logits, V, nch, ban, nban, skip, part);
+        hipLaunchKernelGGL(k_argmax_fin<true>, dim3(n), dim3(64), 0, st, part, nch, out, rec);
+    } else {
+        hipLaunchKernelGGL(k_argmax_part<false>, dim3(nch, n), dim3(256), 0, st, logits, V, nch, ban, nban, skip, part);
+        hipLaunchKernelGGL(k_argmax_fin<false>, dim3(n), dim3(64), 0, st, part, nch, out, rec);
+    }
+    return 0;
 }
 
 // ---- page operations of the cache (sn_copy / sn_clear / freed pages; sn_seq.inc.h:5-145) ----------------------------

@@ -113,8 +113,14 @@ void kv_stage(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L, int 
 // seeded N(0, 1) fp16 into cells [0, n) of a slot (page list on the device), every layer, K and V
 void kv_fill_normal(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L, int KVH, int page_cells,
                     const int32_t* pages, int n, uint64_t seed, hipStream_t st);
-void argmax_rows(const float* logits, int V, int n, const int32_t* ban, int nban, const uint8_t* skip, int32_t* out,
-                 float* rec, hipStream_t st);
+// greedy argmax of n rows of V scores (first index of the largest; rows with skip[r] never take the nban <= 8 ids in
+// ban), with the optional 8-word probability records; ws: argmax_workspace_bytes(n, V) bytes of partials. -1: bad
+// arguments or workspace too small (nothing launched).
+#define AMX_CHUNK 4096
+static inline int argmax_chunks(int V) { return (V + AMX_CHUNK - 1) / AMX_CHUNK; }
+size_t argmax_workspace_bytes(int n, int V);
+int argmax_rows(const float* logits, int V, int n, const int32_t* ban, int nban, const uint8_t* skip, int32_t* out,
+                float* rec, void* ws, size_t ws_bytes, hipStream_t st);
 
 // ---- the guess head (MTP) and the fused draft-verify step
 // [enorm(embed(tok)); hnorm(h)] rows into cat [R][2E]; h: src NULL: hrows row r (hrows given) or pend[seq[r]];

@@ -24,6 +24,15 @@ extern "C" int snk_q8_repack(const void* d_q8, int N, int K, void* d_tiles, void
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+extern "C" size_t snk_argmax_workspace_bytes(int n, int V) { return n > 0 && V > 0 ? argmax_workspace_bytes(n, V) : 0; }
+
+extern "C" int snk_argmax(const float* d_logits, int V, int n, const int32_t* d_ban, int nban, const uint8_t* d_skip,
+                          int32_t* d_out, float* d_rec, void* d_ws, size_t ws_bytes, void* stream) {
+    if (n < 0 || V <= 0 || nban < 0 || nban > 8 || (nban > 0 && !d_ban)) return -1;
+    const int rc = argmax_rows(d_logits, V, n, d_ban, nban, d_skip, d_out, d_rec, d_ws, ws_bytes, (hipStream_t) stream);
+    return rc == 0 && hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 extern "C" size_t snk_xa_bytes(int M, int K) { return xa_bytes(M, K); }
 
 extern "C" int snk_quant_act(const float* d_x, int M, int K, int ldx, const float* d_norm_w, float eps, void* d_xa,

@@ -111,6 +111,8 @@ SNK_API = [
     ("snk_attn_time", C.c_double, [P, P, I, P, P, P, C.c_float, P, I, I, P]),
     ("snk_attn_free", None, [P]),
     ("snk_qk_rope", I, [P, I, I, I, I, P, P, C.c_float, C.c_float, P, P, P, I, I, P, P, P]),
+    ("snk_argmax_workspace_bytes", C.c_size_t, [I, I]),
+    ("snk_argmax", I, [P, I, I, P, I, P, P, P, P, C.c_size_t, P]),
     ("snk_mfma_probe", I, [P, P, P, P]),
 ]
 EXT_API = [

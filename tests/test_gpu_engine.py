@@ -238,3 +238,39 @@ def test_graph_replay_matches_eager(tiny):
         caps, reps = ge.graph_count()
         assert reps >= 5 and caps >= 3, (caps, reps)  # replays happened, and shape changes recaptured
         assert ee.graph_count() == (0, 0)
+
+
+def test_probs_records_and_end_ban(tiny):
+    """sn_want_probs / sn_probs and sn_set_eog / sn_no_end through sn_step (argmax_p, kernels.metal:380-442): the
+    records equal the oracle's top2 and log-sum-exp of the step's own logits; a slot under no_end never takes an
+    end-of-generation id, other slots may."""
+    V = TINY["n_vocab"]
+    r = np.random.default_rng(9)
+    with S.Engine(tiny, slots=2, ctx=256, max_rows=64) as eng:
+        eng.want_probs(True)
+        prompt = r.integers(0, V, 12).astype(np.int32)
+        seq = np.array([0] * 6 + [1] * 6, np.int32)
+        pos = np.array(list(range(6)) * 2, np.int32)
+        got = eng.step(prompt, seq, pos, np.array([5, 11], np.int32), n_write=0)
+        lg = eng.logits([0, 1])
+        pr = eng.probs(2)
+        for j in range(2):
+            i1, v1, i2, v2, lse = O.top2(lg[j])
+            assert got[j] == O.argmax(lg[j])
+            assert pr[j, 0:1].view(np.int32)[0] == got[j] and pr[j, 1] == lg[j, got[j]]
+            assert pr[j, 2:3].view(np.int32)[0] == i1 and pr[j, 3] == v1
+            assert pr[j, 4:5].view(np.int32)[0] == i2 and pr[j, 5] == v2
+            assert abs(pr[j, 6] - lse) <= 2e-6 * max(1.0, abs(lse))
+        # make both rows' greedy choices end-of-generation ids; slot 1 refuses them
+        eog = np.unique(got)
+        eng.set_eog(eog)
+        eng.no_end(1, True)
+        got2 = eng.step(prompt, seq, pos, np.array([5, 11], np.int32), n_write=0)
+        lg2 = eng.logits([0, 1])
+        pr2 = eng.probs(2)
+        assert got2[0] == O.argmax(lg2[0]) == got[0]
+        assert got2[1] == O.argmax(lg2[1], list(eog)) and got2[1] not in eog
+        assert pr2[1, 0:1].view(np.int32)[0] == got2[1]
+        assert pr2[1, 2:3].view(np.int32)[0] == O.top2(lg2[1])[0]  # the pair still ranks every id
+        with pytest.raises(S.SnError):
+            eng.set_eog([V])

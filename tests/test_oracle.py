@@ -263,6 +263,14 @@ def test_argmax_ties_and_bans():
     i1, v1, i2, v2, lse = O.top2(np.array([0.5, 2.0, 2.0, 1.0], np.float32))
     assert (i1, i2) == (1, 2) and v1 == v2 == 2.0
     assert abs(lse - math.log(math.exp(0.5) + 2 * math.exp(2.0) + math.exp(1.0))) < 1e-5
+    # a row with no finite score: no pair, log-sum-exp -inf (kernels.metal:436), the first unbanned id chosen
+    i1, v1, i2, v2, lse = O.top2(np.full(7, -np.inf, np.float32))
+    assert (i1, i2) == (0x7FFFFFFF, 0x7FFFFFFF) and v1 == v2 == lse == -np.inf
+    assert O.argmax(np.full(7, -np.inf, np.float32), ban=[0, 1]) == 2
+    # the log-sum-exp against scipy's, on a wide row
+    from scipy.special import logsumexp
+    y = (r.standard_normal(151936) * 5).astype(np.float32)
+    assert abs(O.top2(y)[4] - logsumexp(y.astype(np.float64))) < 1e-5
 
 
 # ---- paged attention ----------------------------------------------------------------------------------------------------
