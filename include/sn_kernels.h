@@ -71,6 +71,28 @@ int snk_qk_rope(float* d_qkv, int ldqkv, int R, int H, int KVH, const float* d_q
                 float theta_scale, const int32_t* d_seq, const int32_t* d_pos, const int32_t* d_pt, int max_pages,
                 int page_cells, void* d_kpool, void* d_vpool, void* stream);
 
+// ---- mixture of experts (moe_ffn, sn_layers.inc.h:129-144) -------------------------------------------------------------
+// router logits d_lg [R][NE] = d_hn [R][E] (the fp32 normed rows) x d_router [NE][E] (fp32); E % 4 == 0
+int snk_moe_router(const float* d_hn, int R, int E, const float* d_router, int NE, float* d_lg, void* stream);
+// rows of the expert-major tile layout of R rows with k of NE experts each: P = 16 (min(NE, R k) + ceil(R k / 16))
+int snk_moe_tile_rows(int R, int NE, int k);
+// routing and grouping (moe_topk1 + moe_lists, kernels.metal:3419-3497): each row's k experts (softmax of its logits,
+// the k largest with ties to the lower id) d_ids [R][k] and weights d_w [R][k] (p / sum p over the k, the sum floored
+// at 6.103515625e-5); the (row, slot) pairs in expert-major 16-row tiles, expert x's pairs in (row, slot) order from
+// tile toff[x] = the tiles of the experts before it: d_prow [R][k] = the pair's tile row, d_rsrc [P] = the row a tile
+// row carries (-1: padding), d_items [2 x P / 16] = (expert, tile) of each tile, *d_count = the tiles used.
+// NE <= 256, k <= min(8, NE), R k <= 4096. 0, or -1 (bad arguments, nothing launched).
+int snk_moe_select(const float* d_lg, int R, int NE, int k, int32_t* d_ids, float* d_w, int32_t* d_prow,
+                   int32_t* d_rsrc, int32_t* d_items, int32_t* d_count, void* stream);
+// the grouped expert matmul (the block matmul's grouped mode, kernels.metal:561-563; sn_attn.inc.h:350-358): for each
+// tile i < *d_count, item (x, t) = d_items[2i], d_items[2i + 1]: rows 16t .. 16t + 15 of d_part [P][N] = the
+// activation operand's rows (d_xa, P rows of K, snk_quant_act) x expert x's matrix (N x K tiles at d_w + x * wstride;
+// Q4_0 stripes, or Q8_0 tiles with wt 8).
+// Rows p with d_rmask[p] < 0 are not written (d_rmask may be NULL). max_items: the grid's tile bound (P / 16).
+int snk_gemm_grouped(int wt, const void* d_w, size_t wstride, const int32_t* d_items, const int32_t* d_count,
+                     int max_items, const void* d_xa, int P, int N, int K, float* d_part, size_t part_bytes,
+                     const int32_t* d_rmask, void* stream);
+
 // ---- greedy argmax of logit rows (argmax / argmax_p, kernels.metal:327-442) -------------------------------------------
 // d_logits: n rows of V fp32 scores; d_out[r] = the first index of the largest score of row r; rows with d_skip[r] != 0
 // (d_skip may be NULL) never take the nban <= 8 ids of d_ban (-1 when every id is banned). d_rec (may be NULL): per row

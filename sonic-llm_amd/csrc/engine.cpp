@@ -765,8 +765,8 @@ struct Dev {
             return resid_quant(x, e->gemm_ws, ks, R, E, l.ffn_norm, e->eps, e->xa, st, true, e->hn);
         });
         rc |= e->launch(SNX_K_OTHER, (double) NE * E * 4 + (double) R * E * 4, [&] {
-            moe_route(e->hn, l.router, R, E, NE, NU, e->rlog, e->mid, e->mw, st);
-            return moe_group(e->mid, R, NU, NE, P, e->prow, e->rsrc, e->gitems, e->gcount, st);
+            moe_router(e->hn, l.router, R, E, NE, e->rlog, st);
+            return moe_select(e->rlog, R, NE, NU, P, e->mid, e->mw, e->prow, e->rsrc, e->gitems, e->gcount, st);
         });
         // the experts used (a host read only while profiling: the matmuls' algorithmic bytes)
         double used = std::min(NE, R * NU);
@@ -785,15 +785,15 @@ struct Dev {
         quant(e->hn, e->rsrc, P, E, nullptr);
         rc |= e->launch(SNX_K_GEMM, used * e->egu_stride + (double) R * NU * E * 4 + (double) R * NU * 2 * FE * 4, [&] {
             return q4_gemm_grouped(l.egu, e->egu_stride, e->gitems, e->gcount, T, e->xa, P, 2 * FE, E, e->gemm_ws,
-                                   e->gemm_ws_bytes, st, e->wt) < 0 ? -1 : 0;
+                                   e->gemm_ws_bytes, st, e->wt, e->rsrc) < 0 ? -1 : 0;
         });
         rc |= e->launch(SNX_K_QUANT, (double) R * NU * FE * 14, [&] {
-            swiglu_quant(e->gemm_ws, 1, P, FE, nullptr, e->xa, st);
+            swiglu_quant(e->gemm_ws, 1, P, FE, nullptr, e->xa, st, e->rsrc);
             return 0;
         });
         rc |= e->launch(SNX_K_GEMM, used * e->ed_stride + (double) R * NU * FE * 4 + (double) R * NU * E * 4, [&] {
             return q4_gemm_grouped(l.ed, e->ed_stride, e->gitems, e->gcount, T, e->xa, P, E, FE, e->gemm_ws,
-                                   e->gemm_ws_bytes, st, e->wt) < 0 ? -1 : 0;
+                                   e->gemm_ws_bytes, st, e->wt, e->rsrc) < 0 ? -1 : 0;
         });
         rc |= e->launch(SNX_K_OTHER, (double) R * NU * E * 4 + (double) R * E * 8, [&] {
             moe_out(x, e->gemm_ws, e->prow, e->mw, R, E, NU, st);

@@ -1,5 +1,7 @@
 // Row kernels of the step: token embedding, per-head QK-norm + NEOX RoPE + the fp16 K/V cache write, and greedy
 // argmax (with the top-2 / log-sum-exp record of sn_want_probs).
+#include <algorithm>
+
 #include "sn_kernels_internal.h"
 
 // ---- embedding: the token's fp32 table row (embed_rows / embed_into, sn_state.inc.h:250-272; the table is fp32 here)
@@ -455,87 +457,80 @@ void cut_cells(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int CL, in
 
 // ---- mixture of experts (moe_ffn, sn_layers.inc.h:129-144) -----------------------------------------------------------
 
-// Router logits [R][NE] = hn [R][E] (the normed rows) x router [NE][E] (fp32). Workgroup per expert, its router row in
-// LDS; thread (row r, segment g of 8) sums its segment's E / 8 products with float4 loads all in flight, then the 8
-// segments are added by a fixed xor tree: the order of a row's sum depends on E alone, not on the other rows.
+// Router logits [R][NE] = hn [R][E] (the normed rows) x router [NE][E] (fp32). Workgroup (4 experts, RT_ROWS rows),
+// a wavefront per expert: lane l sums elements 4l + 256j .. 4l + 256j + 3 of each of the rows, j ascending (each load
+// of the wavefront is 1 KB contiguous), then the 64 lanes are added by a fixed xor tree: the order of a row's sum
+// depends on E alone, not on the other rows.
+#define RT_ROWS 4
 __global__ __launch_bounds__(256) void k_router(const float* __restrict__ hn, const float* __restrict__ router, int R,
                                                 int E, int NE, float* __restrict__ out) {
-    extern __shared__ float wrow[];
-    const int x = blockIdx.x, t = threadIdx.x, seg = t & 7;
-    for (int i = t; i < E; i += 256) wrow[i] = router[(size_t) x * E + i];
-    __syncthreads();
-    const int SL = E / 8;  // a segment (E % 32 == 0)
-    for (int r0 = 0; r0 < R; r0 += 32) {
-        const int r = r0 + (t >> 3);
-        const float* h = hn + (size_t) min(r, R - 1) * E + seg * SL;
-        const float* w = wrow + seg * SL;
-        float s = 0.0f;
-        for (int i0 = 0; i0 < SL; i0 += 64) {
-            float4 hv[16];
-            for (int u = 0; u < 16; ++u) hv[u] = i0 + 4 * u < SL ? *(const float4*) (h + i0 + 4 * u) : (float4){};
-            for (int u = 0; u < 16; ++u)
-                if (i0 + 4 * u < SL) {
-                    const float4 wv = *(const float4*) (w + i0 + 4 * u);
-                    s += hv[u].x * wv.x + hv[u].y * wv.y + hv[u].z * wv.z + hv[u].w * wv.w;
-                }
-        }
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        s += __shfl_xor(s, 4);
-        if (seg == 0 && r < R) out[(size_t) r * NE + x] = s;
+    const int lane = threadIdx.x & 63, x = blockIdx.x * 4 + (threadIdx.x >> 6), r0 = blockIdx.y * RT_ROWS;
+    if (x >= NE) return;
+    const float* wr = router + (size_t) x * E;
+    float s[RT_ROWS];
+    for (int i = 0; i < RT_ROWS; ++i) s[i] = 0.0f;
+    for (int e0 = 4 * lane; e0 < E; e0 += 256) {
+        const float4 wv = *(const float4*) (wr + e0);
+        float4 hv[RT_ROWS];
+        for (int i = 0; i < RT_ROWS; ++i) hv[i] = *(const float4*) (hn + (size_t) min(r0 + i, R - 1) * E + e0);
+        for (int i = 0; i < RT_ROWS; ++i) s[i] += hv[i].x * wv.x + hv[i].y * wv.y + hv[i].z * wv.z + hv[i].w * wv.w;
     }
+    for (int i = 0; i < RT_ROWS; ++i)
+        for (int o = 32; o > 0; o >>= 1) s[i] += __shfl_xor(s[i], o);
+    if (lane == 0)
+        for (int i = 0; i < RT_ROWS; ++i)
+            if (r0 + i < R) out[(size_t) (r0 + i) * NE + x] = s[i];
 }
 
-// Routing of a row (moe_topk1, kernels.metal:3419-3467): softmax of its NE logits, the k largest (ties: the lower id),
-// weights p / sum(p) renormalised by their own sum floored at 6.103515625e-5. A wavefront per row.
-__global__ __launch_bounds__(64) void k_moe_topk(const float* __restrict__ lg, int NE, int k, int32_t* __restrict__ ids,
-                                                 float* __restrict__ w) {
-    const int r = blockIdx.x, lane = threadIdx.x;
-    const float* l = lg + (size_t) r * NE;
-    float p[4];
-    float m = -INFINITY;
-    for (int g = 0; g < 4; ++g) {
-        const int i = lane + 64 * g;
-        p[g] = i < NE ? l[i] : -INFINITY;
-        m = fmaxf(m, p[g]);
-    }
+// Routing of a row (moe_topk1, kernels.metal:3419-3467): softmax of its NE <= 256 logits, the k <= 8 largest (ties: the
+// lower id), weights p / sum(p) renormalised by their own sum floored at 6.103515625e-5. Workgroup per row, thread per
+// expert: the max and the sum by workgroup reductions (an order fixed by NE), then each expert's rank (the experts
+// before it in probability-descending, id-ascending order) counted against the row's probabilities in LDS; ranks below
+// k are the picks. A NaN probability ranks below every number, so the ids are always k distinct experts of [0, NE).
+__global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ lg, int NE, int k, int32_t* __restrict__ ids,
+                                                  float* __restrict__ w) {
+    __shared__ __attribute__((aligned(16))) float sp[256];
+    __shared__ float red[2][4];
+    __shared__ int spick[8];
+    __shared__ float sprob[8];
+    const int r = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const float l = t < NE ? lg[(size_t) r * NE + t] : -INFINITY;
+    float m = l;
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    float tot = 0.0f;
-    for (int g = 0; g < 4; ++g) {
-        const bool in = lane + 64 * g < NE;
-        const float e = in ? expf(p[g] - m) : 0.0f;
-        p[g] = in ? e : -INFINITY;
-        tot += e;
+    if (lane == 0) red[0][wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    const float e = t < NE ? expf(l - m) : 0.0f;
+    const float p = e == e ? e : -1.0f;
+    float s = e;
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) red[1][wave] = s;
+    sp[t] = p;
+    __syncthreads();
+    const float tot = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    if (t < NE) {
+        int rank = 0, j = 0;
+        for (; j + 4 <= NE; j += 4) {
+            const float4 v = *(const float4*) &sp[j];
+            rank += (v.x > p || (v.x == p && j < t)) + (v.y > p || (v.y == p && j + 1 < t)) +
+                    (v.z > p || (v.z == p && j + 2 < t)) + (v.w > p || (v.w == p && j + 3 < t));
+        }
+        for (; j < NE; ++j) rank += sp[j] > p || (sp[j] == p && j < t);
+        if (rank < k) {
+            spick[rank] = t;
+            sprob[rank] = p;
+        }
     }
-    for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o);
-    float pk[8];
-    int pick[8];
-    for (int j = 0; j < k; ++j) {
-        float bv = -INFINITY;
-        int bi = 1 << 30;
-        for (int g = 0; g < 4; ++g)
-            if (p[g] > bv) {
-                bv = p[g];
-                bi = lane + 64 * g;
-            }
-        float mv = bv;
-        for (int o = 32; o > 0; o >>= 1) mv = fmaxf(mv, __shfl_xor(mv, o));
-        int mi = bv == mv ? bi : 1 << 30;
-        for (int o = 32; o > 0; o >>= 1) mi = min(mi, __shfl_xor(mi, o));
-        for (int g = 0; g < 4; ++g)
-            if (lane + 64 * g == mi) p[g] = -INFINITY;
-        pk[j] = mv;
-        pick[j] = mi;
-    }
-    if (lane == 0) {
-        float sel = 0.0f;
+    __syncthreads();
+    if (t == 0) {
+        float pk[8], sel = 0.0f;
         for (int j = 0; j < k; ++j) {
-            pk[j] /= tot;
+            pk[j] = sprob[j] / tot;
             sel += pk[j];
         }
         sel = fmaxf(sel, 6.103515625e-5f);
         for (int j = 0; j < k; ++j) {
-            ids[r * k + j] = pick[j];
+            ids[r * k + j] = spick[j];
             w[r * k + j] = pk[j] / sel;
         }
     }
@@ -544,49 +539,81 @@ __global__ __launch_bounds__(64) void k_moe_topk(const float* __restrict__ lg, i
 // The (row, slot) pairs in expert-major tiles of 16 rows (moe_lists, kernels.metal:3468-3497), deterministically: expert
 // x's pairs take tiles toff[x] .. in (row, slot) order. prow[r][j] = the pair's row in that layout; rsrc[p] = the row
 // whose operand tile row p carries (-1: padding); items = (expert, tile) of every tile, count = their number. One
-// workgroup of 1024 threads: the pairs' experts in LDS, a wavefront per expert ranks its pairs with ballots.
+// workgroup of 1024 threads: wavefront w owns the w-th sixteenth of the pairs (a chunk) and counts its experts (LDS
+// atomics: counts, not order); an expert's chunk counts become its chunks' starting places (a prefix over chunks) and
+// its total gives the tile offsets (a wavefront prefix over experts); then each wavefront walks its chunk 64 pairs at
+// a time, a pair's place = its chunk's place for the expert + the earlier pairs of the 64 with that expert.
 #define MOE_MAX_PAIRS 4096
-__global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ ids, int RK, int NE, int P,
+__global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ ids, int RK, int NE, int P, int k,
                                                     int32_t* __restrict__ prow, int32_t* __restrict__ rsrc,
-                                                    int32_t* __restrict__ items, int32_t* __restrict__ count, int k) {
-    __shared__ int cnt[256], toff[257];
+                                                    int32_t* __restrict__ items, int32_t* __restrict__ count) {
     __shared__ int sid[MOE_MAX_PAIRS];
+    __shared__ int hist[16][256];  // [chunk][expert]: counts, then the chunk's next place for the expert
+    __shared__ int cnt[256], toff[257];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    for (int x = t; x < NE; x += 1024) cnt[x] = 0;
+    for (int i = t; i < 16 * 256; i += 1024) (&hist[0][0])[i] = 0;
     for (int p = t; p < P; p += 1024) rsrc[p] = -1;
     for (int q = t; q < RK; q += 1024) sid[q] = ids[q];
     __syncthreads();
-    for (int q = t; q < RK; q += 1024) atomicAdd(&cnt[sid[q]], 1);
+    const int C = (RK + 15) / 16, q0 = wave * C, q1 = min(RK, q0 + C);
+    for (int q = q0 + lane; q < q1; q += 64) atomicAdd(&hist[wave][sid[q]], 1);
     __syncthreads();
-    if (t == 0) {
-        int o = 0;
-        for (int x = 0; x < NE; ++x) {
-            toff[x] = o;
-            o += (cnt[x] + 15) / 16;
+    if (t < NE) {
+        int s = 0;
+        for (int c = 0; c < 16; ++c) {
+            const int h = hist[c][t];
+            hist[c][t] = s;
+            s += h;
         }
-        toff[NE] = o;
-        *count = o;
+        cnt[t] = s;
     }
     __syncthreads();
-    for (int x = wave; x < NE; x += 16) {
-        if (cnt[x] == 0) continue;
-        int base = 0;
-        for (int u0 = 0; u0 < RK; u0 += 64) {
-            const int u = u0 + lane;
-            const bool hit = u < RK && sid[u] == x;
-            const unsigned long long m = __ballot(hit);
-            if (hit) {
-                const int p = toff[x] * 16 + base + __popcll(m & ((1ull << lane) - 1));
-                prow[u] = p;
-                rsrc[p] = u / k;
-            }
-            base += __popcll(m);
+    if (wave == 0) {  // toff[x] = tiles of the experts before x (lane l: experts 4l .. 4l + 3)
+        int c[4], loc = 0;
+        for (int j = 0; j < 4; ++j) {
+            const int x = 4 * lane + j;
+            c[j] = x < NE ? (cnt[x] + 15) / 16 : 0;
+            loc += c[j];
         }
-        for (int i = toff[x] + lane; i < toff[x + 1]; i += 64) {
+        int inc = loc;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(inc, o);
+            if (lane >= o) inc += v;
+        }
+        int o = inc - loc;
+        for (int j = 0; j < 4; ++j) {
+            const int x = 4 * lane + j;
+            if (x < NE) toff[x] = o;
+            o += c[j];
+        }
+        if (lane == 63) {
+            toff[NE] = inc;
+            *count = inc;
+        }
+    }
+    __syncthreads();
+    for (int g0 = q0; g0 < q1; g0 += 64) {  // (wavefront-uniform trips; LDS ops of a wavefront complete in order)
+        const int q = g0 + lane, n = min(64, q1 - g0);
+        const bool in = q < q1;
+        const int x = in ? sid[q] : -1;
+        int before = 0, after = 0;
+        for (int j = 0; j < n; ++j) {
+            const int y = sid[g0 + j];
+            before += y == x && j < lane;
+            after += y == x && j > lane;
+        }
+        if (in) {
+            const int p = toff[x] * 16 + hist[wave][x] + before;
+            prow[q] = p;
+            rsrc[p] = q / k;
+            if (after == 0) hist[wave][x] += before + 1;  // the group's last pair of x moves the place on
+        }
+    }
+    for (int x = t; x < NE; x += 1024)
+        for (int i = toff[x]; i < toff[x + 1]; ++i) {
             items[2 * i] = x;
             items[2 * i + 1] = i;
         }
-    }
 }
 
 // x[r] += sum_j w[r][j] * y[prow[r][j]] in slot order (moe_out, kernels.metal:3520-3538); y = the down matmul's sums.
@@ -606,16 +633,18 @@ __global__ __launch_bounds__(256) void k_moe_out(float* __restrict__ x, const fl
     x[(size_t) r * E + i] += acc;
 }
 
-void moe_route(const float* hn, const float* router, int R, int E, int NE, int k, float* lg, int32_t* ids, float* w,
-               hipStream_t st) {
-    if (R <= 0) return;
-    hipLaunchKernelGGL(k_router, dim3(NE), dim3(256), (size_t) E * 4, st, hn, router, R, E, NE, lg);
-    hipLaunchKernelGGL(k_moe_topk, dim3(R), dim3(64), 0, st, lg, NE, k, ids, w);
+void moe_router(const float* hn, const float* router, int R, int E, int NE, float* lg, hipStream_t st) {
+    if (R > 0)
+        hipLaunchKernelGGL(k_router, dim3((NE + 3) / 4, (R + RT_ROWS - 1) / RT_ROWS), dim3(256), 0, st, hn, router, R,
+                           E, NE, lg);
 }
-int moe_group(const int32_t* ids, int R, int k, int NE, int P, int32_t* prow, int32_t* rsrc, int32_t* items,
-              int32_t* count, hipStream_t st) {
-    if (R * k > MOE_MAX_PAIRS) return -1;
-    hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(1024), 0, st, ids, R * k, NE, P, prow, rsrc, items, count, k);
+int moe_select(const float* lg, int R, int NE, int k, int P, int32_t* ids, float* w, int32_t* prow, int32_t* rsrc,
+               int32_t* items, int32_t* count, hipStream_t st) {
+    if (R <= 0) return 0;
+    if (NE < 1 || NE > 256 || k < 1 || k > 8 || k > NE || R * k > MOE_MAX_PAIRS) return -1;
+    if (P < 16 * (std::min(NE, R * k) + (R * k + 15) / 16)) return -1;  // the tiles of any grouping
+    hipLaunchKernelGGL(k_moe_topk, dim3(R), dim3(256), 0, st, lg, NE, k, ids, w);
+    hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(1024), 0, st, ids, R * k, NE, P, k, prow, rsrc, items, count);
     return 0;
 }
 void moe_out(float* x, const float* y, const int32_t* prow, const float* w, int R, int E, int k, hipStream_t st) {

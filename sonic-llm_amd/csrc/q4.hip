@@ -99,12 +99,9 @@ __global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ X, 
     __shared__ float red[4];
     const int m = blockIdx.x, nb = K / 32, t = threadIdx.x;
     const int src = rows ? rows[m] : m;
-    if (src < 0) {  // a zero row (padding of an expert's tile)
-        const int b = blockIdx.y * 64 + (t >> 2), g = t & 3;
-        if (b >= xa_nbp(K)) return;
-        q8_zero(g, xa, K, m, b);
-        return;
-    }
+    // padding of an expert's tile: not written. A row of an MFMA product depends on that row of the operand alone, so
+    // whatever the row holds reaches only output rows that nothing reads.
+    if (src < 0) return;
     const float* x = X + (size_t) src * ldx;
     float scale = 1.0f;
     if (nw) {
@@ -253,11 +250,14 @@ __global__ __launch_bounds__(1024) void k_resid_quant(float* __restrict__ X, con
 
 // SwiGLU of a stripe-interleaved gate/up matmul's k-slice sums (part[ks][M][2F]: output column 16p + n is
 // silu(column 32p + n) * column 32p + 16 + n), written as fp32 rows h (when given) and as the Q8_0 operand of the next
-// matmul. Workgroup (row m, 64 blocks), 4 lanes per block as in k_quant_act.
+// matmul. Workgroup (row m, 64 blocks), 4 lanes per block as in k_quant_act. rows (optional): rows m with rows[m] < 0
+// (padding of an expert's tile) are skipped, as in k_quant_act.
 template <int KM>
 __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ part, int ks, int M, int F,
-                                                      float* __restrict__ h, uint8_t* __restrict__ xa) {
+                                                      float* __restrict__ h, uint8_t* __restrict__ xa,
+                                                      const int32_t* __restrict__ rows) {
     const int m = blockIdx.x, t = threadIdx.x;
+    if (rows && rows[m] < 0) return;
     const int nb = F / 32, nbp = xa_nbp(F);
     const int b = blockIdx.y * 64 + (t >> 2), g = t & 3;
     if (b >= nbp) return;
@@ -440,7 +440,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
         for (int mt = 0; mt < MT; ++mt)
             for (int v = 0; v < 4; ++v) {
                 const int row = (mt0 + mt) * 16 + 4 * g + v;
-                if (row < a.M) a.part[((size_t) slice * a.M + row) * a.N + col] = acc[s][mt][v];
+                if (row < a.M && (!a.rmask || a.rmask[row] >= 0))
+                    a.part[((size_t) slice * a.M + row) * a.N + col] = acc[s][mt][v];
             }
     }
 }
@@ -530,13 +531,14 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
 }
 
 int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
-                    const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st, int wt) {
+                    const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st, int wt,
+                    const int32_t* rmask) {
     if (M <= 0 || max_items <= 0) return 0;
     if (wt != WT_Q4_0 && wt != WT_Q8_0) return -1;
     if (part == nullptr || part_bytes < (size_t) M * N * sizeof(float)) return -1;
     GemmArgs a{};
     a.w = w; a.xa = xa; a.part = part;
-    a.items = items; a.count = count; a.wstride = wstride;
+    a.items = items; a.count = count; a.wstride = wstride; a.rmask = rmask;
     a.M = M; a.N = N; a.K = K; a.epi = EPI_STORE;
     a.nstripes = (N + 15) / 16; a.ngroups = (K / 32 + 3) / 4; a.ks = 1; a.gps = a.ngroups;
     a.mtiles = (M + 15) / 16;
@@ -590,15 +592,15 @@ int resid_quant(float* x, const float* part, int ks, int M, int K, const float* 
     return 0;
 }
 
-void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st) {
+void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st, const int32_t* rows) {
     if (M <= 0) return;
     const dim3 grid(M, (xa_nbp(F) + 63) / 64);
     const int km = ks_bound(ks);
     if (km == 0) return;
-    if (km == 1) hipLaunchKernelGGL((k_swiglu_quant<1>), grid, dim3(256), 0, st, part, ks, M, F, h, xa);
-    else if (km == 2) hipLaunchKernelGGL((k_swiglu_quant<2>), grid, dim3(256), 0, st, part, ks, M, F, h, xa);
-    else if (km == 4) hipLaunchKernelGGL((k_swiglu_quant<4>), grid, dim3(256), 0, st, part, ks, M, F, h, xa);
-    else hipLaunchKernelGGL((k_swiglu_quant<8>), grid, dim3(256), 0, st, part, ks, M, F, h, xa);
+    if (km == 1) hipLaunchKernelGGL((k_swiglu_quant<1>), grid, dim3(256), 0, st, part, ks, M, F, h, xa, rows);
+    else if (km == 2) hipLaunchKernelGGL((k_swiglu_quant<2>), grid, dim3(256), 0, st, part, ks, M, F, h, xa, rows);
+    else if (km == 4) hipLaunchKernelGGL((k_swiglu_quant<4>), grid, dim3(256), 0, st, part, ks, M, F, h, xa, rows);
+    else hipLaunchKernelGGL((k_swiglu_quant<8>), grid, dim3(256), 0, st, part, ks, M, F, h, xa, rows);
 }
 
 void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const float* nw, float eps, uint8_t* xa,

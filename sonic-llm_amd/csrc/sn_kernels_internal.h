@@ -14,6 +14,7 @@ struct GemmArgs {
     const int32_t* items;
     const int32_t* count;
     size_t wstride;
+    const int32_t* rmask;  // (optional) rows p with rmask[p] < 0 are not stored
     int M, N, K, ldy, epi;
     int nstripes, ngroups, ks, gps, mtiles;
 };
@@ -36,7 +37,7 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
 // items, the device count in `count`; part[M][N] rows of each item's tile (one slice).
 int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
                     const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st,
-                    int wt = WT_Q4_0);
+                    int wt = WT_Q4_0, const int32_t* rmask = nullptr);
 // GGUF Q4_0 (wt = WT_Q4_0) or Q8_0 (WT_Q8_0) rows -> tiles; source stripe s lands at destination stripe
 // s * sstride + soff.
 void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int soff, hipStream_t st,
@@ -54,7 +55,8 @@ int resid_quant(float* x, const float* part, int ks, int M, int K, const float* 
                 hipStream_t st, bool add = true, float* xn = nullptr);
 // h (optional) and the Q8_0 operand of silu(gate) * up from a stripe-interleaved gate/up matmul's k-slice sums
 // part[ks][M][2F].
-void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st);
+void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st,
+                  const int32_t* rows = nullptr);
 int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* ws,
             size_t ws_bytes, hipStream_t st, int wt = WT_Q4_0);
 
@@ -138,12 +140,12 @@ void cut_cells(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int CL, in
                int max_pages, int n, int k, const int32_t* seq, const int32_t* pos, const int32_t* acc, hipStream_t st);
 
 // ---- mixture of experts
-// router logits lg [R][NE] of the normed rows hn, then each row's k experts ids [R][k] and weights w [R][k]
-void moe_route(const float* hn, const float* router, int R, int E, int NE, int k, float* lg, int32_t* ids, float* w,
-               hipStream_t st);
-// the pairs in expert-major 16-row tiles: prow [R][k], rsrc [P] (-1 padding), items [2 x tiles] (expert, tile), count.
-// R * k <= 4096; -1 beyond.
-int moe_group(const int32_t* ids, int R, int k, int NE, int P, int32_t* prow, int32_t* rsrc, int32_t* items,
-               int32_t* count, hipStream_t st);
+// router logits lg [R][NE] (fp32) of the normed rows hn [R][E]
+void moe_router(const float* hn, const float* router, int R, int E, int NE, float* lg, hipStream_t st);
+// each row's k experts ids [R][k] and weights w [R][k] from lg, then the pairs in expert-major 16-row tiles: prow
+// [R][k], rsrc [P] (-1 padding), items [2 x tiles] (expert, tile), count. NE <= 256, k <= 8, R * k <= 4096, P at least
+// 16 (min(NE, R k) + ceil(R k / 16)); -1 otherwise (nothing launched).
+int moe_select(const float* lg, int R, int NE, int k, int P, int32_t* ids, float* w, int32_t* prow, int32_t* rsrc,
+               int32_t* items, int32_t* count, hipStream_t st);
 // x[r] += sum_j w[r][j] y[prow[r][j]] (slot order)
 void moe_out(float* x, const float* y, const int32_t* prow, const float* w, int R, int E, int k, hipStream_t st);

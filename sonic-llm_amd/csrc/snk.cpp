@@ -24,6 +24,37 @@ extern "C" int snk_q8_repack(const void* d_q8, int N, int K, void* d_tiles, void
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+extern "C" int snk_moe_router(const float* d_hn, int R, int E, const float* d_router, int NE, float* d_lg,
+                              void* stream) {
+    if (R < 0 || E <= 0 || E % 4 || NE <= 0) return -1;
+    moe_router(d_hn, d_router, R, E, NE, d_lg, (hipStream_t) stream);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int snk_moe_tile_rows(int R, int NE, int k) {
+    if (R < 0 || NE <= 0 || k <= 0) return -1;
+    return 16 * (std::min(NE, R * k) + (R * k + 15) / 16);
+}
+
+extern "C" int snk_moe_select(const float* d_lg, int R, int NE, int k, int32_t* d_ids, float* d_w, int32_t* d_prow,
+                              int32_t* d_rsrc, int32_t* d_items, int32_t* d_count, void* stream) {
+    if (R < 0 || NE <= 0 || k <= 0) return -1;
+    const int rc = moe_select(d_lg, R, NE, k, snk_moe_tile_rows(R, NE, k), d_ids, d_w, d_prow, d_rsrc, d_items,
+                              d_count, (hipStream_t) stream);
+    return rc == 0 && hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int snk_gemm_grouped(int wt, const void* d_w, size_t wstride, const int32_t* d_items,
+                                const int32_t* d_count, int max_items, const void* d_xa, int P, int N, int K,
+                                float* d_part, size_t part_bytes, const int32_t* d_rmask, void* stream) {
+    if ((wt != WT_Q4_0 && wt != WT_Q8_0) || P <= 0 || N <= 0 || K <= 0 || K % 32 || max_items <= 0 ||
+        max_items > (P + 15) / 16)
+        return -1;
+    const int rc = q4_gemm_grouped((const uint8_t*) d_w, wstride, d_items, d_count, max_items, (const uint8_t*) d_xa, P,
+                                   N, K, d_part, part_bytes, (hipStream_t) stream, wt, d_rmask);
+    return rc >= 0 && hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 extern "C" size_t snk_argmax_workspace_bytes(int n, int V) { return n > 0 && V > 0 ? argmax_workspace_bytes(n, V) : 0; }
 
 extern "C" int snk_argmax(const float* d_logits, int V, int n, const int32_t* d_ban, int nban, const uint8_t* d_skip,

@@ -111,6 +111,10 @@ SNK_API = [
     ("snk_attn_time", C.c_double, [P, P, I, P, P, P, C.c_float, P, I, I, P]),
     ("snk_attn_free", None, [P]),
     ("snk_qk_rope", I, [P, I, I, I, I, P, P, C.c_float, C.c_float, P, P, P, I, I, P, P, P]),
+    ("snk_moe_router", I, [P, I, I, P, I, P, P]),
+    ("snk_moe_tile_rows", I, [I, I, I]),
+    ("snk_moe_select", I, [P, I, I, I, P, P, P, P, P, P, P]),
+    ("snk_gemm_grouped", I, [I, P, C.c_size_t, P, P, I, P, I, I, I, P, C.c_size_t, P, P]),
     ("snk_argmax_workspace_bytes", C.c_size_t, [I, I]),
     ("snk_argmax", I, [P, I, I, P, I, P, P, P, P, C.c_size_t, P]),
     ("snk_mfma_probe", I, [P, P, P, P]),

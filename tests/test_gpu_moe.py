@@ -80,3 +80,122 @@ def test_moe_row_invariance(moe_model):
             res.append((t, t2, lg, eng.logits(np.array([0]))))
     for a, b in zip(res[0], res[1]):
         assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+
+
+# ---- the MoE kernels through the C ABI (include/sn_kernels.h) ---------------------------------------------------------
+RTOL, ATOL = 1e-3, 2e-3  # per-op tolerance of the expert matmuls
+
+
+def dptr(t, off=0):
+    import ctypes as C
+    return C.c_void_p(t.data_ptr() + off)
+
+
+def grouping(ids, NE, k, P):
+    """The expert-major tile layout a routing must give (moe_lists, kernels.metal:3468-3497), by counting."""
+    flat = ids.reshape(-1)
+    cnt = np.bincount(flat, minlength=NE)
+    toff = np.concatenate([[0], np.cumsum((cnt + 15) // 16)])
+    prow = np.empty(flat.size, np.int32)
+    rsrc = np.full(P, -1, np.int32)
+    fill = np.zeros(NE, np.int64)
+    for u, x in enumerate(flat):
+        p = toff[x] * 16 + fill[x]
+        fill[x] += 1
+        prow[u] = p
+        rsrc[p] = u // k
+    items = np.array([(x, i) for x in range(NE) for i in range(toff[x], toff[x + 1])], np.int32).reshape(-1, 2)
+    return prow.reshape(ids.shape), rsrc, items, int(toff[NE])
+
+
+def select_gpu(lg, k):
+    L = S.lib()
+    R, NE = lg.shape
+    P = L.snk_moe_tile_rows(R, NE, k)
+    ids, w, prow = U.empty(R * k * 4), U.empty(R * k * 4), U.empty(R * k * 4)
+    rsrc, items, cnt = U.empty(P * 4), U.empty(P // 16 * 8), U.empty(4)
+    assert L.snk_moe_select(U.ptr(U.dev(lg.astype(np.float32))), R, NE, k, U.ptr(ids), U.ptr(w), U.ptr(prow),
+                            U.ptr(rsrc), U.ptr(items), U.ptr(cnt), U.stream()) == 0
+    n = int(U.host(cnt, np.int32)[0])
+    return (U.host(ids, np.int32)[:R * k].reshape(R, k), U.host(w, np.float32)[:R * k].reshape(R, k),
+            U.host(prow, np.int32)[:R * k].reshape(R, k), U.host(rsrc, np.int32)[:P],
+            U.host(items, np.int32)[:2 * n].reshape(n, 2), n, P, (rsrc, items, cnt))
+
+
+def test_moe_router_matches_f64_and_is_row_invariant():
+    L = S.lib()
+    r = np.random.default_rng(40)
+    for R, E, NE in ((32, 2048, 128), (5, 256, 16), (37, 96, 10)):
+        hn = r.standard_normal((R, E)).astype(np.float32)
+        rw = (r.standard_normal((NE, E)) * 0.05).astype(np.float32)
+        lg = U.empty(R * NE * 4)
+        assert L.snk_moe_router(U.ptr(U.dev(hn)), R, E, U.ptr(U.dev(rw)), NE, U.ptr(lg), U.stream()) == 0
+        got = U.host(lg, np.float32)[:R * NE].reshape(R, NE)
+        want = hn.astype(np.float64) @ rw.astype(np.float64).T
+        bound = 1e-5 * (np.abs(hn).astype(np.float64) @ np.abs(rw).astype(np.float64).T)
+        assert np.all(np.abs(got - want) <= bound), np.abs(got - want).max()
+        one = U.empty(NE * 4)  # the last row alone: the same bits
+        assert L.snk_moe_router(U.ptr(U.dev(hn[-1:])), 1, E, U.ptr(U.dev(rw)), NE, U.ptr(one), U.stream()) == 0
+        assert np.array_equal(U.host(one, np.float32)[:NE].view(np.uint32), got[-1].view(np.uint32))
+
+
+@pytest.mark.parametrize("R,NE,k", [(32, 128, 8), (5, 16, 4), (100, 64, 8), (3, 8, 8), (40, 6, 2)])
+def test_moe_select_matches_oracle(R, NE, k):
+    r = np.random.default_rng(R * 1000 + NE)
+    lg = (r.standard_normal((R, NE)) * 2).astype(np.float32)
+    if NE >= 8:  # ties: equal logits pick the lower id
+        lg[0, :] = 1.0
+        lg[1 % R, 3:7] = 9.0
+    ids, w, prow, rsrc, items, n, P, _ = select_gpu(lg, k)
+    for i in range(R):
+        oid, ow = O.moe_route(lg[i], k)
+        assert np.array_equal(ids[i], oid), (i, ids[i], oid)
+        np.testing.assert_allclose(w[i], ow, rtol=1e-5, atol=1e-7)
+    wp, wr, wi, wn = grouping(ids, NE, k, P)
+    assert n == wn and np.array_equal(prow, wp) and np.array_equal(rsrc, wr) and np.array_equal(items, wi)
+
+
+def test_moe_select_rejects_bad_shapes():
+    L = S.lib()
+    b = U.empty(1 << 16)
+    for R, NE, k in ((4, 300, 2), (4, 8, 9), (4, 4, 5), (600, 8, 8)):
+        assert L.snk_moe_select(U.ptr(b), R, NE, k, U.ptr(b), U.ptr(b), U.ptr(b), U.ptr(b), U.ptr(b), U.ptr(b),
+                                U.stream()) == -1
+
+
+@pytest.mark.parametrize("wt", [2, 8])
+def test_grouped_expert_matmul_matches_oracle(wt):
+    """Every real row of every tile against the oracle's matmul of its expert; padding rows are left as they were."""
+    L = S.lib()
+    r = np.random.default_rng(50 + wt)
+    NE, k, R, N, K = 6, 2, 20, 160, 384
+    lg = r.standard_normal((R, NE)).astype(np.float32)
+    lg[:, 2] += 10.0  # expert 2 in every row: two tiles
+    ids, w, prow, rsrc, items, n, P, (d_rsrc, d_items, d_cnt) = select_gpu(lg, k)
+    assert (ids == 2).sum() == R and (items[:, 0] == 2).sum() == 2
+    hn = r.standard_normal((R, K)).astype(np.float32)
+    Ws = [(r.standard_normal((N, K)) * 0.1).astype(np.float32) for _ in range(NE)]
+    if wt == 2:
+        Wq = [O.quantize_q4_0(W) for W in Ws]
+        stride, repack, mm = L.snk_q4_stripes_bytes(N, K), L.snk_q4_repack, O.mul_mat_q4_0
+    else:
+        Wq = [O.quantize_q8_0_ref(W) for W in Ws]
+        stride, repack, mm = L.snk_q8_tiles_bytes(N, K), L.snk_q8_repack, O.mul_mat_q8_0
+    wbuf = U.empty(NE * stride)
+    for x in range(NE):
+        assert repack(U.ptr(U.dev(Wq[x])), N, K, dptr(wbuf, x * stride), U.stream()) == 0
+    X = np.zeros((P, K), np.float32)
+    X[rsrc >= 0] = hn[rsrc[rsrc >= 0]]
+    xa = U.empty(L.snk_xa_bytes(P, K))
+    assert L.snk_quant_act(U.ptr(U.dev(X)), P, K, K, None, 0.0, U.ptr(xa), U.stream()) == 0
+    part = U.dev(np.full((P, N), np.nan, np.float32))
+    assert L.snk_gemm_grouped(wt, U.ptr(wbuf), stride, U.ptr(d_items), U.ptr(d_cnt), P // 16, U.ptr(xa), P, N, K,
+                              U.ptr(part), P * N * 4, U.ptr(d_rsrc), U.stream()) == 0
+    got = U.host(part, np.float32)[:P * N].reshape(P, N)
+    assert np.all(np.isnan(got[rsrc < 0]))
+    for x in range(NE):
+        rows = [p for p in range(P) if rsrc[p] >= 0 and any(items[i, 0] == x and items[i, 1] == p // 16 for i in range(n))]
+        if not rows:
+            continue
+        want = mm(Wq[x], K, hn[rsrc[rows]])
+        np.testing.assert_allclose(got[rows], want, rtol=RTOL, atol=ATOL)
