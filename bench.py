@@ -89,6 +89,8 @@ def main():
                          "moe: Qwen3-30B-A3B-arch batched decode (configs[4])")
     ap.add_argument("--accept", type=float, default=0.6, help="mtp: the seeded share of drafts forced to match")
     ap.add_argument("--no-graphs", action="store_true", help="launch every step eagerly (no HIP graph replay)")
+    ap.add_argument("--attn-mode", type=int, default=-1, choices=(-1, 0, 1),
+                    help="attention work list: -1 chosen per step, 0 per-chunk + merge, 1 whole groups")
     ap.add_argument("--wtype", type=int, default=2, choices=(2, 8),
                     help="decode / moe: the model's matrices in Q4_0 (2, the configs) or Q8_0 (8)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
@@ -128,6 +130,7 @@ def main():
     eng = S.Engine(path, slots=B, ctx=total, max_rows=B)
     if args.no_graphs:
         eng.graphs(False)
+    eng.attn_mode(args.attn_mode)
     for s in range(B):
         eng.fill_kv(s, ctx, args.seed)
     log(f"[bench] engine open + {B} x {ctx} cells in {time.time() - t:.1f}s")
@@ -233,6 +236,7 @@ def bench_mtp(args):
     total = ctx + (args.warmup + args.steps + args.prof_steps) * (k + 1) + 8
     t = time.time()
     eng = S.Engine(path, slots=B, ctx=total, max_rows=B * (k + 1))
+    eng.attn_mode(args.attn_mode)
     assert eng.guess_head() and eng.guess_on(True)
     for s in range(B):
         eng.fill_kv(s, ctx, args.seed)

@@ -36,6 +36,9 @@ int snx_prof_read(const sn_engine* e, int kind, double* ms, int* launches, doubl
 void snx_graphs(sn_engine* e, int on);
 // Steps captured as a new graph (replays 0) or replayed from the cached one (replays 1) since the engine opened.
 long snx_graph_count(const sn_engine* e, int replays);
+// The attention work list's form: -1 chosen per step (the default), 0 one item per 256-cell chunk and a merge, 1
+// whole groups (one workgroup per (group, KV head) walks the whole context: no merge). Every form gives the same bits.
+void snx_attn_mode(sn_engine* e, int mode);
 
 // Give slot `slot` the cells [0, n) (pages as a step would take them) holding seeded N(0, 1) fp16 K and V in every
 // layer: a context "already in the cache" for throughput runs (what the cells hold does not change what a step

@@ -61,6 +61,15 @@ int snk_attn_run(snk_attn* p, const float* d_q, int ldq, const void* d_kpool, co
 // average device time (microseconds) of one run (partials + merge) over `iters` runs (HIP events); synchronous
 double snk_attn_time(snk_attn* p, const float* d_q, int ldq, const void* d_kpool, const void* d_vpool,
                      const int32_t* d_pt, float scale, float* d_out, int ldo, int iters, void* stream);
+// the same with the list's form chosen by the caller: mode -1 as snk_attn_new, 0 one item per 256-cell chunk and the
+// merge, 1 whole groups (for tests and timing; both forms give the same bits for a row)
+snk_attn* snk_attn_new_mode(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH, int max_pages,
+                            int page_cells, int mode, char* err, int err_len);
+// 1 when the list is whole groups (one workgroup per (group, KV head) walks its whole context and writes the output:
+// one launch, no merge; chosen when the groups make one round of 240 .. 256 workgroups, no context is over twice the
+// mean and the contexts are long), 0 when it is one item per 256-cell chunk followed by the merge. Both give the same
+// bits for a row.
+int snk_attn_whole(const snk_attn* p);
 void snk_attn_free(snk_attn* p);
 
 // ---- per-head QK-norm + NEOX RoPE + K/V cache write (qk_rope, kernels.metal:149-197) -------------------------------

@@ -12,6 +12,8 @@
 //   O   = P . V   : A = 16 queries x 32 cells of p in fp16 hi + lo, B = 32 cells x 16 dims of fp16 V.
 // Scores of cells past a row's position are -inf and their p exactly 0, so a row's result does not depend on the
 // other rows of its group, and a verify row equals the same row run alone.
+#include <algorithm>
+
 #include "sn_kernels_internal.h"
 
 #define ATT_D 128
@@ -28,75 +30,84 @@ __device__ __forceinline__ uint32_t pick_half(uint32_t w_lo_cell, uint32_t w_hi_
     return __builtin_amdgcn_perm(w_hi_cell, w_lo_cell, odd ? 0x07060302u : 0x05040100u);
 }
 
-__global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
-    __shared__ float s_o[4][16][ATT_D + 4];
-    __shared__ float s_m[4][16], s_l[4][16];
+// ---- the steps of one wavefront's 64 cells (shared by both kernels, so a chunk's arithmetic is the same in each)
 
-    const AttnItem it = a.items[blockIdx.x];
-    const AttnGroup gr = a.groups[it.group];
-    const int kvh = blockIdx.y;
-    const int G = a.H / a.KVH;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int n = lane & 15, g = lane >> 4;
-    const int pos_last = gr.pos0 + gr.nrows - 1;
-    const int cbase = it.chunk * ATT_CHUNK + 64 * wave;  // this wavefront's first cell
-    const size_t head_stride = (size_t) a.page_cells * ATT_D;
-
-    // this lane's query (as a B column of S^T and the A row of O): n = row * G + head-in-group
-    const int qrow = n / G, qhead = kvh * G + n % G;
-    const bool qvalid = qrow < gr.nrows;
-    const int qpos = gr.pos0 + qrow;
-
-    // Q^T fragments: MFMA t covers dims 32t .. 32t+31; lane (n, g) holds dims 32t + 8g .. +7 of query n. Loaded as
-    // 16-byte pieces from a valid row (an unused column reads the group's first row) and zeroed by a select, so no load
-    // sits behind a branch.
-    half8 qh[4], ql[4];
-    {
-        const float* qp = a.q + (size_t) (gr.row0 + (qvalid ? qrow : 0)) * a.ldq + (size_t) qhead * ATT_D;
-        for (int t = 0; t < 4; ++t) {
-            const float4 x0 = *(const float4*) (qp + 32 * t + 8 * g), x1 = *(const float4*) (qp + 32 * t + 8 * g + 4);
-            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            for (int j = 0; j < 8; ++j) split_hl(qvalid ? xs[j] * a.scale : 0.0f, qh[t], ql[t], j);
-        }
+// Q^T fragments: MFMA t covers dims 32t .. 32t+31; lane (n, g) holds dims 32t + 8g .. +7 of query n. Loaded as
+// 16-byte pieces from a valid row (an unused column reads the group's first row) and zeroed by a select, so no load
+// sits behind a branch.
+__device__ __forceinline__ void attn_qfrag(const AttnArgs& a, const AttnGroup& gr, int qrow, int qhead, bool qvalid,
+                                           int g, half8 (&qh)[4], half8 (&ql)[4]) {
+    const float* qp = a.q + (size_t) (gr.row0 + (qvalid ? qrow : 0)) * a.ldq + (size_t) qhead * ATT_D;
+    for (int t = 0; t < 4; ++t) {
+        const float4 x0 = *(const float4*) (qp + 32 * t + 8 * g), x1 = *(const float4*) (qp + 32 * t + 8 * g + 4);
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        for (int j = 0; j < 8; ++j) split_hl(qvalid ? xs[j] * a.scale : 0.0f, qh[t], ql[t], j);
     }
+}
 
-    // The wavefront's 64 cells lie in one page (64-cell pages) or two (32-cell pages): their page ids are uniform, read
-    // once. Every K and V load of the wavefront is issued here, before any arithmetic, so the whole 32 KB is in flight
-    // at once (V does not depend on the scores).
-    const int32_t* ptrow = a.pt + (size_t) gr.seq * a.max_pages;
-    const int pc = a.page_cells;
-    const int p_lo = cbase <= pos_last ? ptrow[cbase / pc] : 0;
-    const int p_hi = cbase + 32 <= pos_last ? ptrow[(cbase + 32) / pc] : p_lo;
-    const uint16_t* kbase0 = a.kpool + ((size_t) p_lo * a.KVH + kvh) * head_stride;
-    const uint16_t* kbase1 = a.kpool + ((size_t) p_hi * a.KVH + kvh) * head_stride;
-    const uint16_t* vbase0 = a.vpool + ((size_t) p_lo * a.KVH + kvh) * head_stride;
-    const uint16_t* vbase1 = a.vpool + ((size_t) p_hi * a.KVH + kvh) * head_stride;
-    auto cell_off = [&](int c) { return (size_t) (c % pc) * ATT_D; };  // c - cbase < 64
-    // Cells past the group's last position are read from the same pages (memory that exists: a page holds whole
-    // cells) and then zeroed by a select (a masked cell's p is exactly 0, and 0 * V must not meet a NaN).
-    u32x4 kf[4][4], vf[2][8];
-    const u32x4 z4 = {0u, 0u, 0u, 0u};
+// The page ids of a wavefront's 64 cells from cbase: one page (64-cell pages) or two (32-cell pages). Cells past the
+// group's last position read the first page (memory that exists; the cells are zeroed later).
+__device__ __forceinline__ void attn_pages(const AttnArgs& a, const int32_t* ptrow, int cbase, int pos_last, int& p_lo,
+                                           int& p_hi) {
+    // (both entries are read unconditionally, from an index clamped to the last cell's page: no branch)
+    const int sh = a.page_cells == 64 ? 6 : 5;  // page_cells is 32 or 64
+    const int last = max(pos_last, 0) >> sh;
+    const int e_lo = ptrow[min(cbase >> sh, last)], e_hi = ptrow[min((cbase + 32) >> sh, last)];
+    p_lo = cbase <= pos_last ? e_lo : 0;
+    p_hi = cbase + 32 <= pos_last ? e_hi : p_lo;
+}
+
+// Every K and V load of the wavefront's 64 cells (32 KB), issued together as buffer loads: kf[jg][t] = cell cbase + 16 jg
+// + n, dims 32t + 8g .. +7 (the A operand of S^T); vf[st][4 jj + v] = cell cbase + 32 st + 16 jj + 4 g + v, dims 8n ..
+// 8n + 7. A cell past the group's last position gets an offset past its page's bytes, so it reads as zeros without a
+// memory access (a masked cell's p is exactly 0, and 0 * V must not meet a NaN); with live false every load does.
+#define ATT_OOB 0x40000000
+struct AttnRsrc {
+    __amdgpu_buffer_rsrc_t k0, k1, v0, v1;
+};
+__device__ __forceinline__ AttnRsrc attn_rsrc(const AttnArgs& a, int kvh, int p_lo, int p_hi, bool live) {
+    const size_t head_stride = (size_t) a.page_cells * ATT_D;
+    const uint32_t hb = live ? (uint32_t) head_stride * 2 : 0u;  // bytes of one (page, KV head) region
+    AttnRsrc r;
+    r.k0 = buf_rsrc(a.kpool + ((size_t) p_lo * a.KVH + kvh) * head_stride, hb);
+    r.k1 = buf_rsrc(a.kpool + ((size_t) p_hi * a.KVH + kvh) * head_stride, hb);
+    r.v0 = buf_rsrc(a.vpool + ((size_t) p_lo * a.KVH + kvh) * head_stride, hb);
+    r.v1 = buf_rsrc(a.vpool + ((size_t) p_hi * a.KVH + kvh) * head_stride, hb);
+    return r;
+}
+__device__ __forceinline__ void attn_issue_k(const AttnArgs& a, const AttnRsrc& r, int cbase, int pos_last, int n,
+                                             int g, u32x4 (&kf)[4][4]) {
+    const int pc = a.page_cells;  // 32 or 64
     for (int jg = 0; jg < 4; ++jg) {
         const int c = cbase + 16 * jg + n;
-        const uint16_t* kp = (c - cbase < 32 ? kbase0 : kbase1) + cell_off(c);
-        for (int t = 0; t < 4; ++t) kf[jg][t] = *(const u32x4*) (kp + 32 * t + 8 * g);
+        const int off = c <= pos_last ? (c & (pc - 1)) * (ATT_D * 2) + 16 * g : ATT_OOB;
+        for (int t = 0; t < 4; ++t) kf[jg][t] = bload16(jg < 2 ? r.k0 : r.k1, off, 64 * t);
     }
+}
+__device__ __forceinline__ void attn_issue_v(const AttnArgs& a, const AttnRsrc& r, int cbase, int pos_last, int n,
+                                             int g, u32x4 (&vf)[2][8]) {
+    const int pc = a.page_cells;
     for (int st = 0; st < 2; ++st)
         for (int jj = 0; jj < 2; ++jj)
             for (int v = 0; v < 4; ++v) {
                 const int c = cbase + 32 * st + 16 * jj + 4 * g + v;
-                vf[st][4 * jj + v] = *(const u32x4*) ((st == 0 ? vbase0 : vbase1) + cell_off(c) + 8 * n);
+                const int off = c <= pos_last ? (c & (pc - 1)) * (ATT_D * 2) + 16 * n : ATT_OOB;
+                vf[st][4 * jj + v] = bload16(st == 0 ? r.v0 : r.v1, off, 0);
             }
-    for (int jg = 0; jg < 4; ++jg)
-        if (cbase + 16 * jg + n > pos_last)
-            for (int t = 0; t < 4; ++t) kf[jg][t] = z4;
-    for (int st = 0; st < 2; ++st)
-        for (int jj = 0; jj < 2; ++jj)
-            for (int v = 0; v < 4; ++v)
-                if (cbase + 32 * st + 16 * jj + 4 * g + v > pos_last) vf[st][4 * jj + v] = z4;
+}
+__device__ __forceinline__ void attn_issue(const AttnArgs& a, int kvh, int cbase, int pos_last, int p_lo, int p_hi,
+                                           bool live, int n, int g, u32x4 (&kf)[4][4], u32x4 (&vf)[2][8]) {
+    const AttnRsrc r = attn_rsrc(a, kvh, p_lo, p_hi, live);
+    attn_issue_k(a, r, cbase, pos_last, n, g, kf);
+    attn_issue_v(a, r, cbase, pos_last, n, g, vf);
+}
 
-    // ---- scores for the wavefront's 64 cells: 4 groups of 16 cells
-    floatx4 s[4];
+// The wavefront's softmax partial over its 64 cells (the cells past the group's last position read as zeros): scores
+// S^T = K . Q^T; per query the max m and sum l of exp(s - m) (lanes n, n+16, n+32, n+48 share query n); O = P . V, MFMA
+// t covering output dims {8 c + t : c = 0..15}.
+__device__ __forceinline__ void attn_scores(const u32x4 (&kf)[4][4], const half8 (&qh)[4], const half8 (&ql)[4],
+                                            int cbase, bool qvalid, int qpos, int g, float& m, float& l,
+                                            floatx4 (&s)[4]) {
     for (int jg = 0; jg < 4; ++jg) {
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
         for (int t = 0; t < 4; ++t) {
@@ -106,9 +117,7 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
         }
         s[jg] = acc;  // lane (n, g): cells cbase + 16 jg + 4 g + v, query n
     }
-
-    // ---- the wavefront's softmax statistics per query (lanes n, n+16, n+32, n+48 share query n)
-    float m = -INFINITY;
+    m = -INFINITY;
     for (int jg = 0; jg < 4; ++jg)
         for (int v = 0; v < 4; ++v) {
             const int c = cbase + 16 * jg + 4 * g + v;
@@ -118,7 +127,7 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
         }
     m = fmaxf(m, __shfl_xor(m, 16));
     m = fmaxf(m, __shfl_xor(m, 32));
-    float l = 0.0f;
+    l = 0.0f;
     for (int jg = 0; jg < 4; ++jg)
         for (int v = 0; v < 4; ++v) {
             const float p = m == -INFINITY ? 0.0f : __expf(s[jg][v] - m);
@@ -127,9 +136,8 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
         }
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
-
-    // ---- O = P . V over two steps of 32 cells; MFMA t covers output dims {8 c + t : c = 0..15}
-    floatx4 o[8];
+}
+__device__ __forceinline__ void attn_pv(const u32x4 (&vf)[2][8], const floatx4 (&s)[4], floatx4 (&o)[8]) {
     for (int t = 0; t < 8; ++t) o[t] = (floatx4){0.f, 0.f, 0.f, 0.f};
     for (int st = 0; st < 2; ++st) {
         // P fragment: k slot 4 jj + v <-> cell cbase + 32 st + 16 jj + 4 g + v
@@ -144,47 +152,249 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
             o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, o[t], 0, 0, 0);
         }
     }
+}
 
-    // ---- the 4 wavefronts combined in wavefront order
+__device__ __forceinline__ void attn_wave(const u32x4 (&kf)[4][4], const u32x4 (&vf)[2][8], const half8 (&qh)[4],
+                                          const half8 (&ql)[4], int cbase, bool qvalid, int qpos, int g, float& m,
+                                          float& l, floatx4 (&o)[8]) {
+    floatx4 s[4];
+    attn_scores(kf, qh, ql, cbase, qvalid, qpos, g, m, l, s);
+    attn_pv(vf, s, o);
+}
+
+struct AttnShared {
+    float o[4][16][ATT_D + 4];
+    float m[4][16], l[4][16];
+};
+
+// The 4 wavefronts' partials combined in wavefront order into the chunk's partial of thread (query qq, dims d0 ..
+// d0 + 7): M = the max, L = the rescaled sum, acc = the rescaled outputs. Ends with the workgroup's LDS reads done
+// only when the caller syncs again.
+__device__ __forceinline__ void attn_combine(AttnShared& sh, int wave, int n, int g, float m, float l,
+                                             const floatx4 (&o)[8], int qq, int d0, float& M, float& L,
+                                             float (&acc)[8]) {
     if (g == 0) {
-        s_m[wave][n] = m;
-        s_l[wave][n] = l;
+        sh.m[wave][n] = m;
+        sh.l[wave][n] = l;
     }
     for (int t = 0; t < 8; ++t)
-        for (int v = 0; v < 4; ++v) s_o[wave][4 * g + v][8 * n + t] = o[t][v];
+        for (int v = 0; v < 4; ++v) sh.o[wave][4 * g + v][8 * n + t] = o[t][v];
     __syncthreads();
+    M = -INFINITY;
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, sh.m[w][qq]);
+    float e[4];
+    L = 0.0f;
+    for (int w = 0; w < 4; ++w) {
+        e[w] = sh.m[w][qq] == -INFINITY ? 0.0f : __expf(sh.m[w][qq] - M);
+        L += sh.l[w][qq] * e[w];
+    }
+    for (int d = 0; d < 8; ++d) {
+        float s = 0.0f;
+        for (int w = 0; w < 4; ++w) s += sh.o[w][qq][d0 + d] * e[w];
+        acc[d] = s;
+    }
+}
+
+// Chunk partials folded in chunk order into a row's running (M, L, o) (nd dims): the one arithmetic both the merge and
+// the whole-context kernel use, contraction off so both round alike. A chunk with no cell for the row (mc = -inf) is
+// skipped.
+template <int ND>
+__device__ __forceinline__ void attn_fold(float& M, float& L, float (&o)[ND], float mc, float lc, const float (&ov)[ND]) {
+#pragma clang fp contract(off)
+    if (mc == -INFINITY) return;
+    const float mn = fmaxf(M, mc);
+    const float e0 = M == -INFINITY ? 0.0f : __expf(M - mn), e1 = __expf(mc - mn);
+    for (int d = 0; d < ND; ++d) o[d] = o[d] * e0 + ov[d] * e1;
+    L = L * e0 + lc * e1;
+    M = mn;
+}
+
+// A row's normalised output dims (nd of them, fold done): o / L
+template <int ND>
+__device__ __forceinline__ void attn_finish(float L, float (&o)[ND]) {
+    const float il = L > 0.0f ? 1.0f / L : 0.0f;
+    for (int d = 0; d < ND; ++d) o[d] *= il;
+}
+
+// One work item = (query group, chunk); grid.y = KV head. Writes the chunk's partial (acc[128], m, l) of every query of
+// the group; k_attn_merge folds them.
+__global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
+    __shared__ AttnShared sh;
+    const AttnItem it = a.items[blockIdx.x];
+    const AttnGroup gr = a.groups[it.group];
+    const int kvh = blockIdx.y;
+    const int G = a.H / a.KVH;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int pos_last = gr.pos0 + gr.nrows - 1;
+    const int cbase = it.chunk * ATT_CHUNK + 64 * wave;  // this wavefront's first cell
+    // this lane's query (as a B column of S^T and the A row of O): n = row * G + head-in-group
+    const int qrow = n / G, qhead = kvh * G + n % G;
+    const bool qvalid = qrow < gr.nrows;
+    const int qpos = gr.pos0 + qrow;
+    half8 qh[4], ql[4];
+    attn_qfrag(a, gr, qrow, qhead, qvalid, g, qh, ql);
+    int p_lo, p_hi;
+    attn_pages(a, a.pt + (size_t) gr.seq * a.max_pages, cbase, pos_last, p_lo, p_hi);
+    u32x4 kf[4][4], vf[2][8];
+    attn_issue(a, kvh, cbase, pos_last, p_lo, p_hi, true, n, g, kf, vf);
+    float m, l;
+    floatx4 o[8];
+    attn_wave(kf, vf, qh, ql, cbase, qvalid, qpos, g, m, l, o);
     // thread -> (query qq, 8 dims)
     const int qq = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
+    float M, L, acc[8];
+    attn_combine(sh, wave, n, g, m, l, o, qq, d0, M, L, acc);
     const int row = qq / G, head = kvh * G + qq % G;
     if (row >= gr.nrows) return;
-    float M = -INFINITY;
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w][qq]);
-    float e[4], L = 0.0f;
-    for (int w = 0; w < 4; ++w) {
-        e[w] = s_m[w][qq] == -INFINITY ? 0.0f : __expf(s_m[w][qq] - M);
-        L += s_l[w][qq] * e[w];
-    }
     float* dst = a.part + (((size_t) (gr.row0 + row) * a.H + head) * a.max_chunks + it.chunk) * (ATT_D + 2);
-    for (int d = 0; d < 8; ++d) {
-        float acc = 0.0f;
-        for (int w = 0; w < 4; ++w) acc += s_o[w][qq][d0 + d] * e[w];
-        dst[d0 + d] = acc;
-    }
+    for (int d = 0; d < 8; ++d) dst[d0 + d] = acc[d];
     if ((threadIdx.x & 15) == 0) {
         dst[ATT_D] = M;
         dst[ATT_D + 1] = L;
     }
 }
 
-// per (row, head): the chunks' partials in chunk order; out = acc / l. One wavefront, 2 dims a lane; the loads of 8
-// chunks are issued together (chunk index clamped, no load behind a branch), then combined in order. With a.xa the
-// head's 128 outputs (4 Q8_0 blocks of the o-projection's input row) are also quantized there, exactly as the
-// activation quantizer does (ggml x86 quantize_row_q8_0), into the xa operand of K = H * 128.
+// The Q8_0 operand of the o-projection from a row's normalised outputs (ggml x86 quantize_row_q8_0, exactly as the
+// activation quantizer): this lane's 8 dims e0 .. e0 + 7 (e0 = 8 i, i = 0..3) of block blk, whose 4 lanes are xor
+// neighbours 1 and 2; written in the operand's fragment order (q / 16 for elements 16..31) with the block's scale and
+// corrections from the block's first lane.
+__device__ __forceinline__ void attn_xa8(uint8_t* xa, int K, int r, int blk, int e0, const float (&o)[8]) {
+    float amax = 0.0f;
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(o[j]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const float d = amax / 127.f;
+    const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+    const bool hi = e0 >= 16;
+    const float sc = hi ? 0.0625f : 1.0f;
+    float q[8], sq = 0.0f;
+    for (int j = 0; j < 8; ++j) {
+        q[j] = __builtin_rintf(o[j] * id);
+        sq += q[j];
+    }
+    uint8_t* rec = xa + xa_rec_off(K, r, blk);
+    const int gg = (e0 & 15) / 4;  // elements e0 .. e0 + 3 at lane part gg, e0 + 4 .. e0 + 7 at gg + 1
+    for (int h = 0; h < 2; ++h)
+        *(half4v*) (rec + (blk & 3) * 1024 + 16 * ((r & 15) + 16 * (gg + h)) + (hi ? 8 : 0)) =
+            (half4v){(_Float16) (q[4 * h] * sc), (_Float16) (q[4 * h + 1] * sc), (_Float16) (q[4 * h + 2] * sc),
+                     (_Float16) (q[4 * h + 3] * sc)};
+    float slo = hi ? 0.0f : sq, shi = hi ? sq : 0.0f;
+    slo += __shfl_xor(slo, 1);
+    shi += __shfl_xor(shi, 1);
+    slo += __shfl_xor(slo, 2);
+    shi += __shfl_xor(shi, 2);
+    if (e0 == 0) {
+        *(float*) (rec + XA_DX_OFF + (blk & 3) * 64 + 4 * (r & 15)) = (float) (_Float16) d;
+        *(float*) (rec + XA_CORR_OFF + (blk & 3) * 64 + 4 * (r & 15)) = -(1032.0f * slo + 72.0f * shi);
+        *(float*) (rec + XA_CORR8_OFF + (blk & 3) * 64 + 4 * (r & 15)) = -1152.0f * (slo + shi);
+    }
+}
+
+// One work item = a whole query group (every chunk of its context); grid.y = KV head. 8 wavefronts: waves 0-3 take
+// chunk c and waves 4-7 chunk c + 1 of each pair, each half combining its chunk's partial exactly as k_attn_part does;
+// the first half's threads then fold the two partials in chunk order into their running (M, L, o) (query, 8 dims) as
+// k_attn_merge would, and finally write the rows' outputs (and the o-projection's operand) themselves: no partials,
+// no merge. A pair's second chunk past the context (odd chunk counts) reads nothing and has no cell.
+struct AttnPairShared {
+    AttnShared h[2];
+    float x[257][10];  // the second half's combined partials: acc[8], M, L (row 256: the first half's dummy writes)
+};
+__global__ __launch_bounds__(512) void k_attn_whole(AttnArgs a) {
+    __shared__ AttnPairShared sh;
+    const AttnItem it = a.items[blockIdx.x];
+    const AttnGroup gr = a.groups[it.group];
+    const int kvh = blockIdx.y;
+    const int G = a.H / a.KVH;
+    const int lane = threadIdx.x & 63, w8 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int half = w8 >> 2, wave = w8 & 3, th = threadIdx.x & 255;
+    const int n = lane & 15, g = lane >> 4;
+    const int pos_last = gr.pos0 + gr.nrows - 1;
+    const int qrow = n / G, qhead = kvh * G + n % G;
+    const bool qvalid = qrow < gr.nrows;
+    const int qpos = gr.pos0 + qrow;
+    half8 qh[4], ql[4];
+    attn_qfrag(a, gr, qrow, qhead, qvalid, g, qh, ql);
+    const int32_t* ptrow = a.pt + (size_t) gr.seq * a.max_pages;
+    const int nch = it.nchunk;
+    const int qq = th >> 4, d0 = (th & 15) * 8;
+    float RM = -INFINITY, RL = 0.0f, RO[8];
+    for (int d = 0; d < 8; ++d) RO[d] = 0.0f;
+    // chunk c0 + half of each pair; the next pair's K loads go out as soon as the scores have used K, its V loads as
+    // soon as P . V has used V, so they are in flight through the softmax, the combine and the fold. Past the context
+    // (live false) the same loads read nothing, so the issue sequence has no branch.
+    u32x4 kf[4][4], vf[2][8];
+    auto rsrc_of = [&](int c0, int& cbase, int& plast) {
+        const int c = c0 + half;
+        const bool live = c < nch;
+        cbase = (live ? c : 0) * ATT_CHUNK + 64 * wave;
+        plast = live ? pos_last : -1;
+        int p_lo, p_hi;
+        attn_pages(a, ptrow, cbase, plast, p_lo, p_hi);
+        return attn_rsrc(a, kvh, p_lo, p_hi, live);
+    };
+    int cb, pl;
+    {
+        const AttnRsrc r0 = rsrc_of(0, cb, pl);
+        __builtin_amdgcn_sched_barrier(0);
+        attn_issue_k(a, r0, cb, pl, n, g, kf);  // K before V, as in the loop: the wait for K leaves V in flight
+        __builtin_amdgcn_sched_barrier(0);
+        attn_issue_v(a, r0, cb, pl, n, g, vf);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int c0 = 0; c0 < nch; c0 += 2) {  // (uniform trips: every wavefront meets every barrier)
+        const int c = c0 + half;
+        const bool live = c < nch;
+        const int cbase = c * ATT_CHUNK + 64 * wave;
+        int ncb, npl;
+        const AttnRsrc rn = rsrc_of(c0 + 2, ncb, npl);
+        float m, l;
+        floatx4 sc[4], o[8];
+        __builtin_amdgcn_sched_barrier(0);
+        attn_scores(kf, qh, ql, cbase, qvalid && live, qpos, g, m, l, sc);
+        __builtin_amdgcn_sched_barrier(0);
+        attn_issue_k(a, rn, ncb, npl, n, g, kf);
+        __builtin_amdgcn_sched_barrier(0);
+        attn_pv(vf, sc, o);
+        __builtin_amdgcn_sched_barrier(0);
+        attn_issue_v(a, rn, ncb, npl, n, g, vf);
+        __builtin_amdgcn_sched_barrier(0);
+        float M, L, acc[8];
+        attn_combine(sh.h[half], wave, n, g, m, l, o, qq, d0, M, L, acc);
+        // (no branch on the half: the second half writes its partial and also folds, into a state never used)
+        float* xw = sh.x[half ? th : 256];
+        for (int d = 0; d < 8; ++d) xw[d] = acc[d];
+        xw[8] = M;
+        xw[9] = L;
+        __syncthreads();
+        attn_fold<8>(RM, RL, RO, M, L, acc);
+        float acc1[8];
+        for (int d = 0; d < 8; ++d) acc1[d] = sh.x[th][d];
+        attn_fold<8>(RM, RL, RO, sh.x[th][8], sh.x[th][9], acc1);
+        __syncthreads();  // every read of sh done before the next pair writes it
+    }
+    const int row = qq / G, head = kvh * G + qq % G;
+    if (half != 0 || row >= gr.nrows) return;
+    const int r = gr.row0 + row;
+    attn_finish<8>(RL, RO);
+    if (a.out) {
+        float* out = a.out + (size_t) r * a.ldo + (size_t) head * ATT_D + d0;
+        *(float4*) out = (float4){RO[0], RO[1], RO[2], RO[3]};
+        *(float4*) (out + 4) = (float4){RO[4], RO[5], RO[6], RO[7]};
+    }
+    if (a.xa) attn_xa8(a.xa, a.H * ATT_D, r, head * 4 + d0 / 32, d0 & 31, RO);
+}
+
+// per (row, head) of the rows the partial kernel split (a.mrows): the chunks' partials folded in chunk order (attn_fold);
+// out = acc / l. One wavefront, 2 dims a lane; the loads of 8 chunks are issued together (chunk index clamped, no load
+// behind a branch), then folded in order. With a.xa the head's 128 outputs (4 Q8_0 blocks of the o-projection's input
+// row) are also quantized there, exactly as the activation quantizer does (ggml x86 quantize_row_q8_0), into the xa
+// operand of K = H * 128.
 __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
-    const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int r = a.mrows[blockIdx.x], h = blockIdx.y, lane = threadIdx.x;
     const int nc = a.row_pos[r] / ATT_CHUNK + 1;
     const float* p0 = a.part + ((size_t) r * a.H + h) * a.max_chunks * (ATT_D + 2);
-    float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    float M = -INFINITY, L = 0.0f, o[2] = {0.0f, 0.0f};
     for (int c0 = 0; c0 < nc; c0 += 8) {
         float2 ov[8], ml[8];
         for (int j = 0; j < 8; ++j) {
@@ -194,19 +404,13 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {  // (a fixed trip count keeps ov and ml in registers)
-            const float mc = ml[j].x, lc = ml[j].y;
-            if (c0 + j >= nc || mc == -INFINITY) continue;  // past the row's chunks, or a chunk with no cell for it
-            const float mn = fmaxf(M, mc);
-            const float e0 = M == -INFINITY ? 0.0f : __expf(M - mn), e1 = __expf(mc - mn);
-            o0 = o0 * e0 + ov[j].x * e1;
-            o1 = o1 * e0 + ov[j].y * e1;
-            L = L * e0 + lc * e1;
-            M = mn;
+            if (c0 + j >= nc) continue;  // past the row's chunks
+            const float v2[2] = {ov[j].x, ov[j].y};
+            attn_fold<2>(M, L, o, ml[j].x, ml[j].y, v2);
         }
     }
-    const float il = L > 0.0f ? 1.0f / L : 0.0f;
-    o0 *= il;
-    o1 *= il;
+    attn_finish<2>(L, o);
+    const float o0 = o[0], o1 = o[1];
     if (a.out) {
         float* out = a.out + (size_t) r * a.ldo + (size_t) h * ATT_D;
         out[2 * lane] = o0;
@@ -243,7 +447,51 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
 int paged_attention(const AttnArgs& a, hipStream_t st) {
     if (a.n_items <= 0) return 0;
     if (a.H % a.KVH != 0 || 16 % (a.H / a.KVH) != 0) return -1;
-    hipLaunchKernelGGL(k_attn_part, dim3(a.n_items, a.KVH), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(k_attn_merge, dim3(a.n_rows, a.H), dim3(64), 0, st, a);
+    if (a.whole) {
+        hipLaunchKernelGGL(k_attn_whole, dim3(a.n_items, a.KVH), dim3(512), 0, st, a);
+    } else {
+        hipLaunchKernelGGL(k_attn_part, dim3(a.n_items, a.KVH), dim3(256), 0, st, a);
+        if (a.n_mrows > 0) hipLaunchKernelGGL(k_attn_merge, dim3(a.n_mrows, a.H), dim3(64), 0, st, a);
+    }
     return 0;
+}
+
+// The work list (see sn_kernels_internal.h). Whole groups when they make one round of workgroups on the 256 CUs
+// (240 .. 256), no group's context is over twice the mean, and the contexts are long: at least 10 chunks on average,
+// or 5 with 32-cell pages. Measured on MI355X (32 sequences, K/V beyond the Infinity Cache), whole groups beat chunk
+// items plus merge by 10-20% at 12-16 chunks and at 32-cell pages, and lose 2-8% at 4 and 8 chunks of 64-cell pages
+// and whenever the groups are not one round (16 or 48 sequences). Otherwise one item per (group, 256-cell chunk) and
+// the merge folds every row's chunks.
+void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, int page_cells, AttnPlan& p, int mode) {
+    const int gmax = 16 / (H / KVH);
+    p.groups.clear();
+    p.items.clear();
+    p.mrows.clear();
+    p.max_chunk = 0;
+    int tot = 0, mx = 0;
+    for (int r = 0; r < R;) {
+        int n = 1;
+        while (r + n < R && n < gmax && seq[r + n] == seq[r] && pos[r + n] == pos[r] + n) ++n;
+        p.groups.push_back({r, n, seq[r], pos[r]});
+        const int nc = (pos[r] + n - 1) / ATT_CHUNK + 1;
+        tot += nc;
+        mx = std::max(mx, nc);
+        r += n;
+    }
+    p.max_chunk = mx;
+    const int ng = (int) p.groups.size();
+    const long wg = (long) ng * KVH;
+    const bool long_ctx = tot >= (page_cells == 32 ? 5L : 10L) * ng;
+    p.whole = mode >= 0 ? mode == 1
+                        : wg >= ATT_WHOLE_MIN_WG && wg <= ATT_WHOLE_MAX_WG && (long) mx * ng <= 2L * tot && long_ctx;
+    for (int gi = 0; gi < ng; ++gi) {
+        const AttnGroup& gr = p.groups[gi];
+        const int nc = (gr.pos0 + gr.nrows - 1) / ATT_CHUNK + 1;
+        if (p.whole) {
+            p.items.push_back({gi, 0, nc});
+        } else {
+            for (int c = 0; c < nc; ++c) p.items.push_back({gi, c, 1});
+            for (int i = 0; i < gr.nrows; ++i) p.mrows.push_back(gr.row0 + i);
+        }
+    }
 }

@@ -95,6 +95,7 @@ struct sn_engine {
     std::vector<int32_t> eog;
     std::vector<uint8_t> no_end;
     bool want_probs = false;
+    int attn_mode = -1;  // the attention work list's form (snx_attn_mode)
     int last_n_out = 0, last_pn = 0;
     std::vector<float> last_probs;
     double last_ms = 0.0;
@@ -451,9 +452,9 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     // staging: tok, seq, pos (R each), out_rows (MO), skip (MO bytes, padded), groups (R), items (R * max_chunks), pt
     // (+ with a guess head: 4 rounds of head rows, one a slot, their groups and items; row sources and keep lists)
     e->stage_bytes = (size_t) 3 * R * 4 + (size_t) MO * 4 + ((MO + 15) / 16 * 16) + (size_t) R * sizeof(AttnGroup) +
-                     (size_t) R * e->max_chunks * sizeof(AttnItem) + e->pt.size() * 4 + 256;
+                     (size_t) R * e->max_chunks * sizeof(AttnItem) + (size_t) R * 4 + e->pt.size() * 4 + 256 + 64;
     if (e->has_nextn)
-        e->stage_bytes += (size_t) 4 * slots * (sizeof(AttnGroup) + e->max_chunks * sizeof(AttnItem) + 64) +
+        e->stage_bytes += (size_t) 4 * slots * (sizeof(AttnGroup) + e->max_chunks * sizeof(AttnItem) + 4 + 64) +
                           (size_t) 16 * R * 4 + 4096;
     e->d_stage = e->dalloc<uint8_t>(e->stage_bytes, err, err_len);
     e->d_otok = e->dalloc<int32_t>((size_t) MO * 4, err, err_len);
@@ -581,39 +582,32 @@ struct Stage {
     T* dev(size_t at) const { return (T*) (e->d_stage + at); }
 };
 
-// The attention work of R rows: consecutive rows of one sequence at consecutive positions share a group (up to 16/G
-// rows: their K/V loads are shared), a group has one item per 256-cell chunk of its last row. bytes: each (sequence,
-// KV head) reads its cells once, q in and the output out, page-table entries.
+// The attention work of R rows (attn_plan: whole groups, or per-chunk items and the rows to merge). bytes: each
+// (sequence, KV head) reads its cells once, q in and the output out, page-table entries.
 struct AttnList {
-    size_t o_grp = 0, o_itm = 0;
-    int n_items = 0;
+    size_t o_grp = 0, o_itm = 0, o_mrow = 0;
+    int n_items = 0, n_mrows = 0;
+    bool whole = false;
     double bytes = 0.0;
 };
 
 AttnList attn_list(sn_engine* e, Stage& S, int R, const int32_t* seq, const int32_t* pos) {
-    const int gmax = 16 / (e->H / e->KVH);
-    std::vector<AttnGroup> groups;
-    std::vector<AttnItem> items;
-    for (int r = 0; r < R;) {
-        int n = 1;
-        while (r + n < R && n < gmax && seq[r + n] == seq[r] && pos[r + n] == pos[r] + n) ++n;
-        const int gi = (int) groups.size();
-        groups.push_back({r, n, seq[r], pos[r]});
-        const int last = pos[r] + n - 1;
-        for (int c = 0; c <= last / ATT_CHUNK; ++c) items.push_back({gi, c});
-        r += n;
-    }
+    AttnPlan p;
+    attn_plan(R, seq, pos, e->H, e->KVH, e->page_cells, p, e->attn_mode);
     AttnList al;
-    al.o_grp = S.put(groups);
-    al.o_itm = S.put(items);
-    al.n_items = (int) items.size();
+    al.o_grp = S.put(p.groups);
+    al.o_itm = S.put(p.items);
+    al.o_mrow = S.put(p.mrows);
+    al.n_items = (int) p.items.size();
+    al.n_mrows = (int) p.mrows.size();
+    al.whole = p.whole;
     al.bytes = (double) R * e->QD * 8;
     std::vector<int> seen;
-    for (const AttnGroup& g : groups) {
+    for (const AttnGroup& g : p.groups) {
         if (std::find(seen.begin(), seen.end(), g.seq) != seen.end()) continue;
         seen.push_back(g.seq);
         int last = 0;
-        for (const AttnGroup& h : groups)
+        for (const AttnGroup& h : p.groups)
             if (h.seq == g.seq) last = std::max(last, h.pos0 + h.nrows - 1);
         al.bytes += (double) (last + 1) * e->KD * 2 * 2 + 4.0 * (last / e->page_cells + 1);
     }
@@ -731,6 +725,9 @@ struct Dev {
         aa.scale = 1.0f / sqrtf((float) e->D);
         aa.n_rows = R;
         aa.row_pos = d_pos;
+        aa.whole = al.whole ? 1 : 0;
+        aa.mrows = S.dev<const int32_t>(al.o_mrow);
+        aa.n_mrows = al.n_mrows;
         rc |= e->launch(SNX_K_ATTN, al.bytes, [&] { return paged_attention(aa, st); });
     }
     uint16_t* kp(int layer) { return e->kbase + (size_t) layer * e->layer_halves; }
@@ -1196,6 +1193,12 @@ extern "C" int snx_spec_step(sn_engine* e, int n, const int32_t* seq, const int3
 extern "C" double sn_last_gpu_ms(const sn_engine* e) { return e->last_ms; }
 
 extern "C" long snx_graph_count(const sn_engine* e, int replays) { return replays ? e->graph_replays : e->graph_captures; }
+
+extern "C" void snx_graphs(sn_engine* e, int on);
+extern "C" void snx_attn_mode(sn_engine* e, int mode) {
+    e->attn_mode = mode < -1 || mode > 1 ? -1 : mode;
+    snx_graphs(e, e->graphs);  // captured graphs hold the old form's launches
+}
 
 extern "C" void snx_graphs(sn_engine* e, int on) {
     e->graphs = on != 0;

@@ -307,20 +307,6 @@ __device__ __forceinline__ half8 q8_unpack(uint32_t w_lo, uint32_t w_hi) {
     return __builtin_bit_cast(half8, (u32x4){p0, p1, p2, p3});
 }
 
-#define RSRC_WORD3 0x00020000  // raw buffer resource, gfx9 data format
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short) 0, (int) bytes, RSRC_WORD3);
-}
-__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int vo, int so) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
-}
-__device__ __forceinline__ u32x2 bload8(__amdgpu_buffer_rsrc_t r, int vo, int so) {
-    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0));
-}
-__device__ __forceinline__ float bload4f(__amdgpu_buffer_rsrc_t r, int vo, int so) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
-}
-
 // One workgroup (4 wavefronts) owns a set of 4 S consecutive 16-row stripes (wavefront w: stripes S w .. S w + S - 1 of
 // the set; S = 2, or 1 for narrow matrices), MT row tiles and a k-slice of consecutive 4-block groups, which the 4 wavefronts walk together. Per group:
 //   - the activation records of the MT row tiles (MT x 4 KB of fragments, MT x 512 B of scales and corrections) are

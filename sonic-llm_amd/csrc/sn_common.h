@@ -14,6 +14,22 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 #define SN_WAVE 64
 
+// ---- raw buffer loads: a per-lane byte offset and a wavefront-uniform one against a resource of `bytes`; a load
+// reaching past `bytes` returns zeros and touches no memory
+#define RSRC_WORD3 0x00020000  // raw buffer resource, gfx9 data format
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short) 0, (int) bytes, RSRC_WORD3);
+}
+__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
+}
+__device__ __forceinline__ u32x2 bload8(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0));
+}
+__device__ __forceinline__ float bload4f(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
+}
+
 // HIP call check for host code: on failure, format the reason into (err, err_len) and return `ret`.
 #define SN_HIP_TRY(call, ret)                                                                              \
     do {                                                                                                   \

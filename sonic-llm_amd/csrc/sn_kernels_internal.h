@@ -2,6 +2,8 @@
 #pragma once
 #include "sn_common.h"
 
+#include <vector>
+
 enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
 
 struct GemmArgs {
@@ -71,8 +73,9 @@ struct AttnGroup {
     int32_t pos0;   // position of the first row; row i is at pos0 + i and attends cells 0 .. pos0 + i
 };
 struct AttnItem {
-    int32_t group;  // index into the group list
-    int32_t chunk;  // cells chunk*ATT_CHUNK ..
+    int32_t group;   // index into the group list
+    int32_t chunk;   // cells chunk*ATT_CHUNK ..
+    int32_t nchunk;  // chunks the item covers (whole-group items: all of the group's; otherwise 1)
 };
 struct AttnArgs {
     const float* q;          // [rows][H][D] fp32 (normed, roped; the softmax scale is applied inside)
@@ -94,8 +97,28 @@ struct AttnArgs {
     float scale;
     int n_rows;
     const int32_t* row_pos;  // [rows] position of each row (merge: its chunk count)
+    int whole;               // items are whole groups: one kernel writes the outputs, no partials, no merge
+    const int32_t* mrows;    // rows the merge folds (chunk items), n_mrows of them
+    int n_mrows;
 };
 int paged_attention(const AttnArgs& a, hipStream_t st);
+// The work list of R rows: consecutive rows of one sequence at consecutive positions share a group (up to 16/G rows:
+// their K/V loads are shared). Whole groups (one item each, walked by one workgroup per KV head) when the groups give
+// one round of ATT_WHOLE_MIN_WG .. ATT_WHOLE_MAX_WG workgroups, the longest context is at most twice the mean and the
+// contexts are long; otherwise one item per (group, 256-cell chunk), every row merged. Both fold a row's chunk
+// partials in the same order with the same arithmetic, so a row's output does not depend on which list it was in.
+#define ATT_WHOLE_MIN_WG 240
+#define ATT_WHOLE_MAX_WG 256
+struct AttnPlan {
+    std::vector<AttnGroup> groups;
+    std::vector<AttnItem> items;
+    std::vector<int32_t> mrows;
+    int max_chunk = 0;  // the most chunks of any group
+    bool whole = false;
+};
+// mode: -1 as above, 0 per-chunk items, 1 whole groups
+void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, int page_cells, AttnPlan& p,
+               int mode = -1);
 
 // ---- elementwise / row kernels ----
 void embed_rows(const float* table, int E, const int32_t* tok, int R, float* x, hipStream_t st);

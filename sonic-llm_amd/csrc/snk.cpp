@@ -121,50 +121,47 @@ extern "C" double snk_q4_gemm_time(const void* const* d_stripes, int n_copies, c
 
 // ---- attention work lists
 struct snk_attn {
-    int n_rows, H, KVH, max_pages, page_cells, max_chunks, n_items;
+    int n_rows, H, KVH, max_pages, page_cells, max_chunks, n_items, n_mrows;
+    bool whole;
     AttnGroup* d_groups = nullptr;
     AttnItem* d_items = nullptr;
+    int32_t* d_mrows = nullptr;
     int32_t* d_pos = nullptr;
     float* d_part = nullptr;
 };
 
-extern "C" snk_attn* snk_attn_new(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH, int max_pages,
-                                  int page_cells, char* err, int err_len) {
-    if (n_rows <= 0 || H <= 0 || KVH <= 0 || H % KVH || 16 % (H / KVH) || (page_cells != 32 && page_cells != 64)) {
+extern "C" snk_attn* snk_attn_new_mode(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH,
+                                       int max_pages, int page_cells, int mode, char* err, int err_len) {
+    if (n_rows <= 0 || H <= 0 || KVH <= 0 || H % KVH || 16 % (H / KVH) || (page_cells != 32 && page_cells != 64) ||
+        mode < -1 || mode > 1) {
         sn_set_err(err, err_len, "snk_attn_new: bad shape");
         return nullptr;
     }
-    const int gmax = 16 / (H / KVH);
-    std::vector<AttnGroup> groups;
-    std::vector<AttnItem> items;
-    int maxpos = 0;
-    for (int r = 0; r < n_rows;) {
+    for (int r = 0; r < n_rows; ++r)
         if (pos[r] < 0 || pos[r] >= max_pages * page_cells) {
             sn_set_err(err, err_len, "snk_attn_new: a position is outside the page table");
             return nullptr;
         }
-        int n = 1;
-        while (r + n < n_rows && n < gmax && seq[r + n] == seq[r] && pos[r + n] == pos[r] + n) ++n;
-        groups.push_back({r, n, seq[r], pos[r]});
-        const int last = pos[r] + n - 1;
-        maxpos = std::max(maxpos, last);
-        for (int c = 0; c <= last / ATT_CHUNK; ++c) items.push_back({(int) groups.size() - 1, c});
-        r += n;
-    }
+    AttnPlan pl;
+    attn_plan(n_rows, seq, pos, H, KVH, page_cells, pl, mode);
     snk_attn* p = new snk_attn();
     p->n_rows = n_rows;
     p->H = H;
     p->KVH = KVH;
     p->max_pages = max_pages;
     p->page_cells = page_cells;
-    p->max_chunks = maxpos / ATT_CHUNK + 1;
-    p->n_items = (int) items.size();
-    bool ok = hipMalloc(&p->d_groups, groups.size() * sizeof(AttnGroup)) == hipSuccess &&
-              hipMalloc(&p->d_items, items.size() * sizeof(AttnItem)) == hipSuccess &&
+    p->max_chunks = pl.max_chunk;
+    p->n_items = (int) pl.items.size();
+    p->n_mrows = (int) pl.mrows.size();
+    p->whole = pl.whole;
+    bool ok = hipMalloc(&p->d_groups, pl.groups.size() * sizeof(AttnGroup)) == hipSuccess &&
+              hipMalloc(&p->d_items, pl.items.size() * sizeof(AttnItem)) == hipSuccess &&
+              hipMalloc(&p->d_mrows, std::max<size_t>(1, pl.mrows.size()) * 4) == hipSuccess &&
               hipMalloc(&p->d_pos, (size_t) n_rows * 4) == hipSuccess &&
               hipMalloc(&p->d_part, (size_t) n_rows * H * p->max_chunks * 130 * 4) == hipSuccess;
-    ok = ok && hipMemcpy(p->d_groups, groups.data(), groups.size() * sizeof(AttnGroup), hipMemcpyHostToDevice) == hipSuccess &&
-         hipMemcpy(p->d_items, items.data(), items.size() * sizeof(AttnItem), hipMemcpyHostToDevice) == hipSuccess &&
+    ok = ok && hipMemcpy(p->d_groups, pl.groups.data(), pl.groups.size() * sizeof(AttnGroup), hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(p->d_items, pl.items.data(), pl.items.size() * sizeof(AttnItem), hipMemcpyHostToDevice) == hipSuccess &&
+         (pl.mrows.empty() || hipMemcpy(p->d_mrows, pl.mrows.data(), pl.mrows.size() * 4, hipMemcpyHostToDevice) == hipSuccess) &&
          hipMemcpy(p->d_pos, pos, (size_t) n_rows * 4, hipMemcpyHostToDevice) == hipSuccess;
     if (!ok) {
         sn_set_err(err, err_len, "snk_attn_new: device allocation failed");
@@ -172,6 +169,11 @@ extern "C" snk_attn* snk_attn_new(int n_rows, const int32_t* seq, const int32_t*
         return nullptr;
     }
     return p;
+}
+
+extern "C" snk_attn* snk_attn_new(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH, int max_pages,
+                                  int page_cells, char* err, int err_len) {
+    return snk_attn_new_mode(n_rows, seq, pos, H, KVH, max_pages, page_cells, -1, err, err_len);
 }
 
 static AttnArgs attn_args(snk_attn* p, const float* d_q, int ldq, const void* d_kpool, const void* d_vpool,
@@ -196,6 +198,9 @@ static AttnArgs attn_args(snk_attn* p, const float* d_q, int ldq, const void* d_
     a.scale = scale;
     a.n_rows = p->n_rows;
     a.row_pos = p->d_pos;
+    a.whole = p->whole ? 1 : 0;
+    a.mrows = p->d_mrows;
+    a.n_mrows = p->n_mrows;
     return a;
 }
 
@@ -225,10 +230,13 @@ extern "C" double snk_attn_time(snk_attn* p, const float* d_q, int ldq, const vo
     return hipGetLastError() == hipSuccess ? 1000.0 * ms / iters : -1.0;
 }
 
+extern "C" int snk_attn_whole(const snk_attn* p) { return p && p->whole ? 1 : 0; }
+
 extern "C" void snk_attn_free(snk_attn* p) {
     if (!p) return;
     hipFree(p->d_groups);
     hipFree(p->d_items);
+    hipFree(p->d_mrows);
     hipFree(p->d_pos);
     hipFree(p->d_part);
     delete p;

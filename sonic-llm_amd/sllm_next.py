@@ -107,8 +107,10 @@ SNK_API = [
     ("snk_q4_gemm", I, [P, P, I, I, I, P, I, I, P, C.c_size_t, P]),
     ("snk_q4_gemm_time", C.c_double, [P, I, P, I, I, I, P, I, P, C.c_size_t, I, P]),
     ("snk_attn_new", P, [I, P, P, I, I, I, I, CH, I]),
+    ("snk_attn_new_mode", P, [I, P, P, I, I, I, I, I, CH, I]),
     ("snk_attn_run", I, [P, P, I, P, P, P, C.c_float, P, I, P]),
     ("snk_attn_time", C.c_double, [P, P, I, P, P, P, C.c_float, P, I, I, P]),
+    ("snk_attn_whole", I, [P]),
     ("snk_attn_free", None, [P]),
     ("snk_qk_rope", I, [P, I, I, I, I, P, P, C.c_float, C.c_float, P, P, P, I, I, P, P, P]),
     ("snk_moe_router", I, [P, I, I, P, I, P, P]),
@@ -121,6 +123,7 @@ SNK_API = [
 ]
 EXT_API = [
     ("snx_graphs", None, [P, I]),
+    ("snx_attn_mode", None, [P, I]),
     ("snx_graph_count", C.c_long, [P, I]),
     ("snx_prof", None, [P, I]),
     ("snx_prof_read", I, [P, I, C.POINTER(C.c_double), C.POINTER(I), C.POINTER(C.c_double)]),
@@ -310,6 +313,10 @@ class Engine:
     def graphs(self, on: bool):
         """snx_graphs: replay each step shape's device work as a HIP graph (the default) or launch it eagerly."""
         self.L.snx_graphs(self.e, int(on))
+
+    def attn_mode(self, mode: int):
+        """snx_attn_mode: the attention work list's form, -1 per step (default), 0 per-chunk + merge, 1 whole groups."""
+        self.L.snx_attn_mode(self.e, int(mode))
 
     def graph_count(self) -> tuple:
         """(steps captured as a new graph, steps replayed from the cached graph) since the engine opened."""

@@ -49,15 +49,19 @@ def config2_case(seed=2, S_=32, page=32, lo=256, hi=4096, n_share=8, share_cells
     return q, np.arange(S_, dtype=np.int32), (ctx - 1).astype(np.int32), kpool, vpool, pt, page
 
 
-def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None):
+def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None, whole=None, mode=-1):
+    """whole: when given, the work list's form the planner chose (whole groups, or per-chunk items and the merge) is
+    checked too; mode: the form forced (snk_attn_new_mode), -1 the planner's"""
     L = S.lib()
     err = __import__("ctypes").create_string_buffer(256)
     seq = np.ascontiguousarray(seq, np.int32)
     pos = np.ascontiguousarray(pos, np.int32)
     for s_, p_ in zip(seq, pos):  # every cell a row reads has a page (host-side check before the launch)
         assert np.all(pt[s_, :p_ // page + 1] >= 0)
-    plan = L.snk_attn_new(len(seq), seq.ctypes.data, pos.ctypes.data, H, KVH, pt.shape[1], page, err, 256)
+    plan = L.snk_attn_new_mode(len(seq), seq.ctypes.data, pos.ctypes.data, H, KVH, pt.shape[1], page, mode, err, 256)
     assert plan, err.value
+    if whole is not None:
+        assert L.snk_attn_whole(plan) == int(whole)
     if bufs is None:
         bufs = (U.dev(kpool), U.dev(vpool), U.dev(pt))
     dq = U.dev(q)
@@ -139,3 +143,23 @@ def test_page_placement_does_not_matter():
     pt2 = np.where(pt >= 0, perm[np.maximum(pt, 0)], -1).astype(np.int32)
     b = attn_gpu(q, seq, pos, kp2, vp2, pt2, page, scale)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("page,lo,hi,auto", [(32, 256, 4096, True), (64, 200, 700, False), (32, 1, 300, False),
+                                            (64, 2560, 4096, True)])
+def test_whole_group_list_equals_chunk_list_bitwise(page, lo, hi, auto):
+    """The two forms of the work list on the same 32 rows: whole groups (one workgroup walks a row's whole context and
+    writes its output, no merge) and per-chunk items with the merge. The outputs are the same bits (the chunk partials
+    are folded in the same order with the same arithmetic), they match the oracle, and the planner picks whole groups
+    for these 32 x 8 workgroups exactly when the contexts are long (auto)."""
+    q, seq, pos, kp, vp, pt, pg = config2_case(seed=11 + lo, S_=32, page=page, lo=lo, hi=hi, n_share=0)
+    scale = 1 / math.sqrt(D)
+    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    whole = attn_gpu(q, seq, pos, kp, vp, pt, pg, scale, bufs, mode=1)
+    split = attn_gpu(q, seq, pos, kp, vp, pt, pg, scale, bufs, mode=0)
+    assert np.array_equal(whole.view(np.uint32), split.view(np.uint32))
+    attn_gpu(q[:1], seq[:1], pos[:1], kp, vp, pt, pg, scale, bufs, whole=False)  # 8 workgroups: never whole
+    auto_out = attn_gpu(q, seq, pos, kp, vp, pt, pg, scale, bufs, whole=auto)
+    assert np.array_equal(auto_out.view(np.uint32), whole.view(np.uint32))
+    ref = O.paged_attn(q, seq, pos, KVH, kp, vp, pg, pt, scale)
+    assert np.all(np.abs(whole - ref) <= ATOL + RTOL * np.abs(ref))

@@ -274,3 +274,36 @@ def test_probs_records_and_end_ban(tiny):
         assert pr2[1, 2:3].view(np.int32)[0] == O.top2(lg2[1])[0]  # the pair still ranks every id
         with pytest.raises(S.SnError):
             eng.set_eog([V])
+
+
+def test_attention_list_forms_give_the_same_steps(tiny):
+    """snx_attn_mode: whole-group attention (its kernel writes the rows' outputs and the o-projection's Q8_0 operand
+    itself) and per-chunk attention with the merge give the same tokens and logits, bit for bit, over prompt and decode
+    steps that cross 256-cell chunk boundaries."""
+    r = np.random.default_rng(21)
+    V = TINY["n_vocab"]
+    lens = [300, 40, 530]
+    outs = []
+    for mode in (0, 1):
+        with S.Engine(tiny, slots=3, ctx=640, max_rows=256) as eng:
+            eng.attn_mode(mode)
+            rr = np.random.default_rng(21)
+            got = []
+            for s, n in enumerate(lens):  # prompts in 256-row steps
+                toks = rr.integers(0, V, n).astype(np.int32)
+                for a in range(0, n, 256):
+                    b = min(n, a + 256)
+                    t = eng.step(toks[a:b], np.full(b - a, s, np.int32), np.arange(a, b, dtype=np.int32),
+                                 np.array([b - a - 1], np.int32), n_write=0)
+                got.append((t.copy(), eng.logits([0]).copy()))
+            cur = rr.integers(0, V, 3).astype(np.int32)
+            pos = np.array(lens, np.int32)
+            for it in range(4):
+                t = eng.step(cur, np.arange(3, dtype=np.int32), pos, np.arange(3, dtype=np.int32))
+                got.append((t.copy(), eng.logits([0, 1, 2]).copy()))
+                cur = t.astype(np.int32)
+                pos = pos + 1
+            outs.append(got)
+    for (ta, la), (tb, lb) in zip(*outs):
+        assert np.array_equal(ta, tb)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
