@@ -89,6 +89,7 @@ def main():
                          "moe: Qwen3-30B-A3B-arch batched decode (configs[4])")
     ap.add_argument("--accept", type=float, default=0.6, help="mtp: the seeded share of drafts forced to match")
     ap.add_argument("--no-graphs", action="store_true", help="launch every step eagerly (no HIP graph replay)")
+    ap.add_argument("--no-chain", action="store_true", help="decode without sn_step's queued successor (chain = 0)")
     ap.add_argument("--attn-mode", type=int, default=-1, choices=(-1, 0, 1),
                     help="attention work list: -1 chosen per step, 0 per-chunk + merge, 1 whole groups")
     ap.add_argument("--wtype", type=int, default=2, choices=(2, 8),
@@ -139,30 +140,35 @@ def main():
     tok = np.random.default_rng(args.seed).integers(0, eng.V, B).astype(np.int32)
     pos = np.full(B, ctx, np.int32)
 
-    def step():
+    # chain (sn_step's queued successor, as a decoding caller uses it): each step has the next queued behind it on the
+    # GPU, fed its tokens there, so the host's turn-around overlaps the GPU. The last warmup step and the last timed
+    # step queue nothing, so the timed region holds exactly `steps` steps of GPU work.
+    def step(chain):
         nonlocal tok
-        tok = eng.step(tok, seq, pos, rows)
+        tok = eng.step(tok, seq, pos, rows, chain=chain)
         pos[:] += 1
 
-    for _ in range(args.warmup):
-        step()
+    use_chain = 0 if args.no_chain else 1
+    for i in range(args.warmup):
+        step(use_chain if i + 1 < args.warmup else 0)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     gpu_ms = 0.0
-    for _ in range(args.steps):
-        step()
+    for i in range(args.steps):
+        step(use_chain if i + 1 < args.steps else 0)
         gpu_ms += eng.last_gpu_ms()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     value = B * args.steps / dt
     caps, reps = eng.graph_count()
+    taken, dropped = eng.chain_count()
     log(f"[bench] {args.steps} steps: {dt * 1e3 / args.steps:.3f} ms/step wall, {gpu_ms / args.steps:.3f} ms/step GPU "
-        f"(graph captures {caps}, replays {reps})")
+        f"(graph captures {caps}, replays {reps}; queued steps taken {taken}, dropped {dropped})")
 
     # profiled pass: per-kernel-class time and algorithmic bytes
     eng.prof(True)
     for _ in range(args.prof_steps):
-        step()
+        step(0)
     prof = eng.prof_read()
     eng.prof(False)
     kernels = {}
@@ -212,7 +218,7 @@ def main():
                    "kv_heads": cfg["n_head_kv"], "ffn": cfg["n_ff"], "vocab": cfg["n_vocab"], "page_cells": 64,
                    **({"experts": cfg["n_expert"], "experts_used": cfg["n_expert_used"], "expert_ffn": cfg["n_ff_exp"]}
                       if moe else {}),
-                   "gpu_ms_per_step": round(gpu_ms / args.steps, 4)},
+                   "gpu_ms_per_step": round(gpu_ms / args.steps, 4), "chain": bool(use_chain)},
         "roofline": roof(dom) if dom else None,
         "roofline_gemm": roof("gemm") if "gemm" in kernels else None,
         "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
@@ -269,7 +275,7 @@ def bench_mtp(args):
     log(f"[bench] {args.steps} spec steps: {dt * 1e3 / args.steps:.3f} ms/step, {toks / args.steps:.2f} tokens/step")
     eng.prof(True)
     for _ in range(args.prof_steps):
-        step()
+        step(0)
     prof = eng.prof_read()
     eng.prof(False)
     eng.close()

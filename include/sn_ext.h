@@ -36,6 +36,9 @@ int snx_prof_read(const sn_engine* e, int kind, double* ms, int* launches, doubl
 void snx_graphs(sn_engine* e, int on);
 // Steps captured as a new graph (replays 0) or replayed from the cached one (replays 1) since the engine opened.
 long snx_graph_count(const sn_engine* e, int replays);
+// Steps taken from the queue (dropped 0: sn_step's chain found the queued step to be the one asked for) or queued and
+// dropped (dropped 1: another step or a cache call came first; its cells were zeroed) since the engine opened.
+long snx_chain_count(const sn_engine* e, int dropped);
 // The attention work list's form: -1 chosen per step (the default), 0 one item per 256-cell chunk and a merge, 1
 // whole groups (one workgroup per (group, KV head) walks the whole context: no merge). Every form gives the same bits.
 void snx_attn_mode(sn_engine* e, int mode);

@@ -40,6 +40,17 @@ struct DevLayer {
 
 }  // namespace
 
+// The buffers a step in flight owns: its staging copy, output tokens, probability records, logits and its start / end
+// events. Two sets alternate when a step is queued behind another (sn_step's chain); the engine's fields are the set
+// of the step the caller last received, `alt` the other one.
+#define GRAPH_CACHE 6  // step shapes whose graphs are kept
+struct StepSet {
+    uint8_t *d_stage = nullptr, *h_stage = nullptr;
+    int32_t *d_otok = nullptr, *h_otok = nullptr;
+    float *d_rec = nullptr, *h_rec = nullptr, *logits = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+};
+
 struct sn_engine {
     GgufFile gg;
     std::string arch;
@@ -101,13 +112,32 @@ struct sn_engine {
     double last_ms = 0.0;
     int guess_on = 0;
 
-    // the device work of the last step shape, captured as a HIP graph and replayed while the shape repeats: its key is
-    // every host value a launch of the step takes (row counts, work-list sizes, staging offsets), so a replay issues
-    // exactly the launches an eager step would
+    // the device work of recent step shapes, captured as HIP graphs and replayed while a shape repeats: a key is every
+    // host value a launch of the step takes (the buffer set, row counts, work-list sizes, staging offsets), so a replay
+    // issues exactly the launches an eager step would. A few shapes are kept (least recently used first out): chained
+    // steps alternate buffer sets.
     bool graphs = true;
-    std::vector<int64_t> graph_key;
-    hipGraphExec_t graph_exec = nullptr;
+    struct GraphEnt {
+        std::vector<int64_t> key;
+        hipGraphExec_t ex;
+    };
+    std::vector<GraphEnt> gcache;
     long graph_replays = 0, graph_captures = 0;
+
+    // the other buffer set, and which of the two the engine's fields are (part of every graph key)
+    StepSet alt;
+    int set_id = 0;
+    // the queued step (sn_step's chain, sn_step.inc.h:31-212): R write rows of slots ch_seq at ch_pos (one past the step
+    // before), fed that step's tokens ch_tok on the GPU; it runs in `alt` until taken or dropped
+    bool ch_on = false;
+    int ch_R = 0, ch_fast = 0;
+    bool ch_probs = false;
+    long ch_cfg = 0;
+    std::vector<int32_t> ch_seq, ch_pos, ch_tok;
+    long ch_taken = 0, ch_dropped = 0;
+    // bumped by the calls that change how a step chooses its tokens (end ids, no-end slots, probability records): a
+    // step queued before such a call is not the step asked for after it
+    long cfg_gen = 0;
 
     // per-kernel-class profiling (sn_ext.h): event pairs around each launch while on
     struct ProfRec {
@@ -282,7 +312,8 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->max_out = std::max(slots + 4, e->has_nextn ? std::min(max_rows, 5 * slots) : 0);
     e->max_chunks = (e->ctx + ATT_CHUNK - 1) / ATT_CHUNK;
     if (hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking) != hipSuccess || hipEventCreate(&e->ev0) != hipSuccess ||
-        hipEventCreate(&e->ev1) != hipSuccess)
+        hipEventCreate(&e->ev1) != hipSuccess || hipEventCreate(&e->alt.ev0) != hipSuccess ||
+        hipEventCreate(&e->alt.ev1) != hipSuccess)
         return fail("HIP stream / event creation failed (no GPU?)");
 
     // ---- weights
@@ -459,6 +490,11 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->d_stage = e->dalloc<uint8_t>(e->stage_bytes, err, err_len);
     e->d_otok = e->dalloc<int32_t>((size_t) MO * 4, err, err_len);
     e->d_rec = e->dalloc<float>((size_t) MO * 32, err, err_len);
+    e->alt.d_stage = e->dalloc<uint8_t>(e->stage_bytes, err, err_len);
+    e->alt.d_otok = e->dalloc<int32_t>((size_t) MO * 4, err, err_len);
+    e->alt.d_rec = e->dalloc<float>((size_t) MO * 32, err, err_len);
+    e->alt.logits = e->dalloc<float>((size_t) MO * e->V * 4, err, err_len);
+    if (!e->alt.d_stage || !e->alt.d_otok || !e->alt.d_rec || !e->alt.logits) return fail("");
     e->d_ban = e->dalloc<int32_t>(8 * 4, err, err_len);
     e->amx_bytes = argmax_workspace_bytes(MO, e->V);
     e->d_amx = e->dalloc<uint8_t>(e->amx_bytes, err, err_len);
@@ -481,22 +517,34 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     }
     if (hipHostMalloc((void**) &e->h_stage, e->stage_bytes, 0) != hipSuccess ||
         hipHostMalloc((void**) &e->h_otok, (size_t) MO * 4, 0) != hipSuccess ||
-        hipHostMalloc((void**) &e->h_rec, (size_t) MO * 32, 0) != hipSuccess)
+        hipHostMalloc((void**) &e->h_rec, (size_t) MO * 32, 0) != hipSuccess ||
+        hipHostMalloc((void**) &e->alt.h_stage, e->stage_bytes, 0) != hipSuccess ||
+        hipHostMalloc((void**) &e->alt.h_otok, (size_t) MO * 4, 0) != hipSuccess ||
+        hipHostMalloc((void**) &e->alt.h_rec, (size_t) MO * 32, 0) != hipSuccess)
         return fail("pinned host buffers failed");
     return e;
 }
 
+namespace {
+void swap_sets(sn_engine* e);
+int settle(sn_engine* e);
+}  // namespace
+
 extern "C" void sn_close(sn_engine* e) {
     if (!e) return;
-    if (e->st) hipStreamSynchronize(e->st);
+    if (e->st) hipStreamSynchronize(e->st);  // (a queued step ends; its cells go with the pool)
     for (void* p : e->allocs) hipFree(p);
-    if (e->h_stage) hipHostFree(e->h_stage);
-    if (e->h_otok) hipHostFree(e->h_otok);
-    if (e->h_rec) hipHostFree(e->h_rec);
-    if (e->ev0) hipEventDestroy(e->ev0);
-    if (e->ev1) hipEventDestroy(e->ev1);
+    for (int k = 0; k < 2; ++k) {  // both buffer sets
+        if (e->h_stage) hipHostFree(e->h_stage);
+        if (e->h_otok) hipHostFree(e->h_otok);
+        if (e->h_rec) hipHostFree(e->h_rec);
+        if (e->ev0) hipEventDestroy(e->ev0);
+        if (e->ev1) hipEventDestroy(e->ev1);
+        e->h_stage = nullptr, e->h_otok = nullptr, e->h_rec = nullptr, e->ev0 = nullptr, e->ev1 = nullptr;
+        swap_sets(e);
+    }
     for (auto& ev : e->prof_ev) hipEventDestroy(ev);
-    if (e->graph_exec) hipGraphExecDestroy(e->graph_exec);
+    for (auto& g : e->gcache) hipGraphExecDestroy(g.ex);
     if (e->st) hipStreamDestroy(e->st);
     delete e;
 }
@@ -640,6 +688,20 @@ int take_pages(sn_engine* e, int R, const int32_t* seq, const int32_t* pos) {
 }
 
 // the staged inputs to the device (and the page table when it changed); starts the step's GPU clock
+// exchange the engine's buffer set with the other one
+void swap_sets(sn_engine* e) {
+    std::swap(e->d_stage, e->alt.d_stage);
+    std::swap(e->h_stage, e->alt.h_stage);
+    std::swap(e->d_otok, e->alt.d_otok);
+    std::swap(e->h_otok, e->alt.h_otok);
+    std::swap(e->d_rec, e->alt.d_rec);
+    std::swap(e->h_rec, e->alt.h_rec);
+    std::swap(e->logits, e->alt.logits);
+    std::swap(e->ev0, e->alt.ev0);
+    std::swap(e->ev1, e->alt.ev1);
+    e->set_id ^= 1;
+}
+
 int stage_copy(sn_engine* e, Stage& S) {
     const bool send_pt = e->pt_dirty;
     const size_t o_pt = send_pt ? S.put(e->pt) : 0;
@@ -910,9 +972,9 @@ void note_runs(sn_engine* e, int R, const int32_t* seq, const int32_t* pos) {
 }
 
 // waits for the step; the GPU time and profiling records
-int finish(sn_engine* e, int rc, char* err, int err_len) {
-    SN_HIP_TRY(hipEventRecord(e->ev1, e->st), -1);
-    SN_HIP_TRY(hipStreamSynchronize(e->st), -1);
+int finish(sn_engine* e, int rc, char* err, int err_len, bool recorded = false) {
+    if (!recorded) SN_HIP_TRY(hipEventRecord(e->ev1, e->st), -1);
+    SN_HIP_TRY(hipEventSynchronize(e->ev1), -1);
     if (rc != 0) {
         sn_set_err(err, err_len, "a kernel launch was refused (workspace or shape)");
         return -1;
@@ -941,10 +1003,13 @@ int finish(sn_engine* e, int rc, char* err, int err_len) {
 template <class Work>
 int run_device(sn_engine* e, std::vector<int64_t>&& key, Work work) {
     if (e->graphs && !e->prof_on) {
-        if (e->graph_exec && e->graph_key == key) {
-            ++e->graph_replays;
-            return hipGraphLaunch(e->graph_exec, e->st) == hipSuccess ? 0 : -1;
-        }
+        key.insert(key.begin(), e->set_id);  // a set's graph holds that set's buffers
+        for (size_t i = 0; i < e->gcache.size(); ++i)
+            if (e->gcache[i].key == key) {
+                std::rotate(e->gcache.begin() + i, e->gcache.begin() + i + 1, e->gcache.end());  // most recent last
+                ++e->graph_replays;
+                return hipGraphLaunch(e->gcache.back().ex, e->st) == hipSuccess ? 0 : -1;
+            }
         if (hipStreamBeginCapture(e->st, hipStreamCaptureModeThreadLocal) == hipSuccess) {
             Dev d{e, e->st};
             work(d);
@@ -957,11 +1022,13 @@ int run_device(sn_engine* e, std::vector<int64_t>&& key, Work work) {
             hipGraphExec_t ex = nullptr;
             if (ok && hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) == hipSuccess) {
                 hipGraphDestroy(g);
-                if (e->graph_exec) hipGraphExecDestroy(e->graph_exec);
-                e->graph_exec = ex;
-                e->graph_key = std::move(key);
+                if (e->gcache.size() >= GRAPH_CACHE) {
+                    hipGraphExecDestroy(e->gcache.front().ex);
+                    e->gcache.erase(e->gcache.begin());
+                }
+                e->gcache.push_back({std::move(key), ex});
                 ++e->graph_captures;
-                return hipGraphLaunch(e->graph_exec, e->st) == hipSuccess ? 0 : -1;
+                return hipGraphLaunch(ex, e->st) == hipSuccess ? 0 : -1;
             }
             if (g) hipGraphDestroy(g);
         }
@@ -982,33 +1049,20 @@ bool rows_bad(const sn_engine* e, int R, const int32_t* tok, const int32_t* seq,
 
 }  // namespace
 
-extern "C" int sn_step(sn_engine* e, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos, int n_write,
-                       int n_fast, int n_out, const int32_t* out_rows, int32_t* out_tok, int chain, char* err,
-                       int err_len) {
-    (void) chain;  // a chained step is run as an ordinary step: the same tokens (sn.h:36-38)
-    if (step_shape_bad(e, R, n_write, n_fast, n_out)) {
-        sn_set_err(err, err_len, "bad step shape");
-        return -1;
-    }
-    if (rows_bad(e, R, tok, seq, pos)) {
-        sn_set_err(err, err_len, "a row is out of range (slot, position or token)");
-        return -1;
-    }
-    for (int j = 0; j < n_out; ++j)
-        if (out_rows[j] < 0 || out_rows[j] >= R) {
-            sn_set_err(err, err_len, "an output row is outside the step");
-            return -1;
-        }
-    if (take_pages(e, R, seq, pos) != 0) {
-        sn_set_err(err, err_len, "out of cache pages");
-        return -2;
-    }
-    const bool fill = e->has_nextn && e->guess_on;
+namespace {
 
-    // ---- the step's rows, attention work list and page table into one staging copy
+// One step's device work, staged into the engine's buffer set and enqueued on the stream with the tokens'
+// device-to-host copy; the set's end event recorded, nothing waited for. tok_dev: the rows' tokens are that device
+// array (a queued step is fed the step before's outputs), else tok. Returns the device work's code (0, or -1 when a
+// launch was refused), or -2 when the staging failed (nothing enqueued).
+int enqueue_step(sn_engine* e, int R, const int32_t* tok, const int32_t* tok_dev, const int32_t* seq, const int32_t* pos,
+                 int n_out, const int32_t* out_rows) {
+    const bool fill = e->has_nextn && e->guess_on;
     Stage S{e};
-    const size_t o_tok = S.put(tok, (size_t) R * 4), o_seq = S.put(seq, (size_t) R * 4), o_pos = S.put(pos, (size_t) R * 4);
-    const size_t o_out = S.put(out_rows, (size_t) n_out * 4);
+    std::vector<int32_t> tz;
+    if (!tok) tz.assign(R, 0);
+    const size_t o_tok = S.put(tok ? tok : tz.data(), (size_t) R * 4), o_seq = S.put(seq, (size_t) R * 4);
+    const size_t o_pos = S.put(pos, (size_t) R * 4), o_out = S.put(out_rows, (size_t) n_out * 4);
     std::vector<uint8_t> skip(n_out + 1, 0);
     for (int j = 0; j < n_out; ++j) skip[j] = e->no_end[seq[out_rows[j]]];
     const size_t o_skip = S.put(skip);
@@ -1021,10 +1075,9 @@ extern "C" int sn_step(sn_engine* e, int R, const int32_t* tok, const int32_t* s
         o_keep = S.put(keep);
     }
     e->prof_recs.clear();
-    if (stage_copy(e, S) != 0) {
-        sn_set_err(err, err_len, "step staging failed");
-        return -1;
-    }
+    if (stage_copy(e, S) != 0) return -2;
+    if (tok_dev && hipMemcpyAsync(e->d_stage + o_tok, tok_dev, (size_t) R * 4, hipMemcpyDeviceToDevice, e->st) != hipSuccess)
+        return -2;
     const int32_t* d_tok = S.dev<const int32_t>(o_tok);
     const int32_t* d_seq = S.dev<const int32_t>(o_seq);
     const int32_t* d_pos = S.dev<const int32_t>(o_pos);
@@ -1039,13 +1092,25 @@ extern "C" int sn_step(sn_engine* e, int R, const int32_t* tok, const int32_t* s
                         S.dev<const int32_t>(o_keep));
         if (n_out > 0 && d.rc == 0) d.outputs(e->x, n_out, S.dev<const int32_t>(o_out), S.dev<const uint8_t>(o_skip));
     });
+    int rc = drc;
     if (drc == 0 && n_out > 0) {
-        SN_HIP_TRY(hipMemcpyAsync(e->h_otok, e->d_otok, (size_t) n_out * 4, hipMemcpyDeviceToHost, e->st), -1);
-        if (e->want_probs)
-            SN_HIP_TRY(hipMemcpyAsync(e->h_rec, e->d_rec, (size_t) n_out * 32, hipMemcpyDeviceToHost, e->st), -1);
+        if (hipMemcpyAsync(e->h_otok, e->d_otok, (size_t) n_out * 4, hipMemcpyDeviceToHost, e->st) != hipSuccess ||
+            (e->want_probs &&
+             hipMemcpyAsync(e->h_rec, e->d_rec, (size_t) n_out * 32, hipMemcpyDeviceToHost, e->st) != hipSuccess))
+            rc = -1;
     }
-    if (finish(e, drc, err, err_len) != 0) return -1;
-    if (fill) note_runs(e, R, seq, pos);
+    return hipEventRecord(e->ev1, e->st) == hipSuccess ? rc : -2;  // the step's end, before anything queued behind it
+}
+
+// The step in the engine's buffer set (its end event recorded): wait for it, take its tokens and probability records
+int take_step(sn_engine* e, int rc, int R, const int32_t* seq, const int32_t* pos, int n_out, int32_t* out_tok,
+              char* err, int err_len) {
+    if (rc == -2) {
+        sn_set_err(err, err_len, "step staging failed");
+        return -1;
+    }
+    if (finish(e, rc, err, err_len, true) != 0) return -1;
+    if (e->has_nextn && e->guess_on) note_runs(e, R, seq, pos);
     if (n_out > 0) memcpy(out_tok, e->h_otok, (size_t) n_out * 4);
     e->last_n_out = n_out;
     e->last_pn = e->want_probs ? n_out : 0;
@@ -1053,8 +1118,118 @@ extern "C" int sn_step(sn_engine* e, int R, const int32_t* tok, const int32_t* s
     return 0;
 }
 
+// A write step that samples each row in order (sn_step.inc.h:137-142) can have the next one queued behind it; not
+// while the guess head fills its cells (a dropped step would have moved the slots' kept head state) or profiling.
+bool chain_shape(const sn_engine* e, int R, int n_write, int n_out, const int32_t* out_rows) {
+    if ((e->has_nextn && e->guess_on) || e->prof_on || R != n_write || n_out != R || n_out > e->slots) return false;
+    for (int j = 0; j < n_out; ++j)
+        if (out_rows[j] != j) return false;
+    return true;
+}
+
+// Queue the step after the one just enqueued (sn_step.inc.h:67-78): the same rows one position on, fed that step's
+// outputs on the GPU, staged into the other buffer set and enqueued behind it, so it runs while the caller takes this
+// step's tokens. Not when a row would pass the context or the cache is out of pages.
+void queue_next(sn_engine* e, int R, const int32_t* seq, const int32_t* pos, int n_fast) {
+    std::vector<int32_t> p1(R), rows(R);
+    for (int r = 0; r < R; ++r) {
+        p1[r] = pos[r] + 1;
+        rows[r] = r;
+        if (p1[r] >= e->ctx) return;
+    }
+    if (take_pages(e, R, seq, p1.data()) != 0) return;
+    const int32_t* fed = e->d_otok;  // this step's tokens, on the device
+    swap_sets(e);
+    const int rc = enqueue_step(e, R, nullptr, fed, seq, p1.data(), R, rows.data());
+    swap_sets(e);
+    e->ch_on = true;
+    e->ch_R = R;
+    e->ch_fast = n_fast;
+    e->ch_probs = e->want_probs;
+    e->ch_cfg = e->cfg_gen;
+    e->ch_seq.assign(seq, seq + R);
+    e->ch_pos = p1;
+    e->ch_tok.clear();  // known when this step's tokens are
+    if (rc != 0) settle(e);  // nothing usable queued: let what was enqueued end, zero its cells
+}
+
+// whether the step asked for is the queued one (sn_step.inc.h:145-169): its rows, positions and tokens, and the same
+// way of choosing tokens
+bool queued_same(const sn_engine* e, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos, int n_fast,
+                 bool shape) {
+    if (!shape || R != e->ch_R || n_fast != e->ch_fast || e->want_probs != e->ch_probs || e->cfg_gen != e->ch_cfg ||
+        (int) e->ch_tok.size() != R)
+        return false;
+    for (int r = 0; r < R; ++r)
+        if (seq[r] != e->ch_seq[r] || pos[r] != e->ch_pos[r] || tok[r] != e->ch_tok[r]) return false;
+    return true;
+}
+
+// The queued step is not the step asked for, or a cache call comes first (sn_step.inc.h:31-47): let it end and zero
+// the cells it wrote in every layer (clear_cells, sn_cache.inc.h:252-262). Its pages stay, as the reference's do.
+int settle(sn_engine* e) {
+    if (!e->ch_on) return 0;
+    e->ch_on = false;
+    ++e->ch_dropped;
+    const int pc = e->page_cells;
+    for (int r = 0; r < e->ch_R; ++r) {
+        const int p = e->seq_pages(e->ch_seq[r])[e->ch_pos[r] / pc];
+        if (p >= 0)
+            kv_page_op(e->kbase, e->vbase, e->layer_halves, e->CL, e->KVH, pc, -1, p, e->ch_pos[r] % pc,
+                       e->ch_pos[r] % pc + 1, e->st);
+    }
+    return hipStreamSynchronize(e->st) == hipSuccess ? 0 : -1;
+}
+
+}  // namespace
+
+extern "C" int sn_step(sn_engine* e, int R, const int32_t* tok, const int32_t* seq, const int32_t* pos, int n_write,
+                       int n_fast, int n_out, const int32_t* out_rows, int32_t* out_tok, int chain, char* err,
+                       int err_len) {
+    if (step_shape_bad(e, R, n_write, n_fast, n_out)) {
+        sn_set_err(err, err_len, "bad step shape");
+        return -1;
+    }
+    if (rows_bad(e, R, tok, seq, pos)) {
+        sn_set_err(err, err_len, "a row is out of range (slot, position or token)");
+        return -1;
+    }
+    for (int j = 0; j < n_out; ++j)
+        if (out_rows[j] < 0 || out_rows[j] >= R) {
+            sn_set_err(err, err_len, "an output row is outside the step");
+            return -1;
+        }
+    // (sn_step.inc.h:187-213) the step asked for may be the queued one, whether or not the caller chains on from it
+    const bool shape = chain_shape(e, R, n_write, n_out, out_rows), next = chain && shape;
+    int rc;
+    if (e->ch_on && queued_same(e, R, tok, seq, pos, n_fast, shape)) {
+        e->ch_on = false;
+        ++e->ch_taken;
+        swap_sets(e);  // its buffer set becomes the engine's
+        rc = 0;
+    } else {
+        if (settle(e) != 0) {
+            sn_set_err(err, err_len, "the queued step failed on the GPU");
+            return -1;
+        }
+        if (take_pages(e, R, seq, pos) != 0) {
+            sn_set_err(err, err_len, "out of cache pages");
+            return -2;
+        }
+        rc = enqueue_step(e, R, tok, nullptr, seq, pos, n_out, out_rows);
+    }
+    if (next && rc == 0) queue_next(e, R, seq, pos, n_fast);
+    const int trc = take_step(e, rc, R, seq, pos, n_out, out_tok, err, err_len);
+    if (e->ch_on) {
+        if (trc == 0) e->ch_tok.assign(out_tok, out_tok + R);  // the queued step was fed these
+        else settle(e);
+    }
+    return trc;
+}
+
 // k guesses of one sequence (sn_guess, sn_cache.inc.h:357-388): k head rows, each fed the guess before it on the GPU
 extern "C" int sn_guess(sn_engine* e, int seq, int32_t tok, int pos, int k, int32_t* out_tok, char* err, int err_len) {
+    if (settle(e) != 0) return -1;  // a cache call drops the queued step first (sn.h:36-38)
     if (!e->has_nextn || !e->guess_on) {
         sn_set_err(err, err_len, "sn_guess: no guess head, or guessing is off (sn_guess_on)");
         return -1;
@@ -1092,6 +1267,7 @@ extern "C" int sn_guess(sn_engine* e, int seq, int32_t tok, int pos, int k, int3
 // The fused draft-verify step (sn_ext.h): drafts, verify rows, acceptance and the cut, in one submission.
 extern "C" int snx_spec_step(sn_engine* e, int n, const int32_t* seq, const int32_t* last, const int32_t* pos, int k,
                              const uint8_t* force, int32_t* out_n, int32_t* out_tok, char* err, int err_len) {
+    if (settle(e) != 0) return -1;  // a cache call drops the queued step first (sn.h:36-38)
     if (!e->has_nextn || !e->guess_on) {
         sn_set_err(err, err_len, "snx_spec_step: no guess head, or guessing is off (sn_guess_on)");
         return -1;
@@ -1194,6 +1370,8 @@ extern "C" double sn_last_gpu_ms(const sn_engine* e) { return e->last_ms; }
 
 extern "C" long snx_graph_count(const sn_engine* e, int replays) { return replays ? e->graph_replays : e->graph_captures; }
 
+extern "C" long snx_chain_count(const sn_engine* e, int dropped) { return dropped ? e->ch_dropped : e->ch_taken; }
+
 extern "C" void snx_graphs(sn_engine* e, int on);
 extern "C" void snx_attn_mode(sn_engine* e, int mode) {
     e->attn_mode = mode < -1 || mode > 1 ? -1 : mode;
@@ -1202,12 +1380,12 @@ extern "C" void snx_attn_mode(sn_engine* e, int mode) {
 
 extern "C" void snx_graphs(sn_engine* e, int on) {
     e->graphs = on != 0;
-    if (e->graph_exec) hipGraphExecDestroy(e->graph_exec);
-    e->graph_exec = nullptr;
-    e->graph_key.clear();
+    for (auto& g : e->gcache) hipGraphExecDestroy(g.ex);
+    e->gcache.clear();
 }
 
 extern "C" void snx_prof(sn_engine* e, int on) {
+    settle(e);
     e->prof_on = on != 0;
     for (int k = 0; k < SNX_K_COUNT; ++k) {
         e->prof_ms[k] = e->prof_bytes[k] = 0.0;
@@ -1228,6 +1406,7 @@ extern "C" int snx_prof_read(const sn_engine* e, int kind, double* ms, int* laun
 }
 
 extern "C" int snx_debug_read(sn_engine* e, int which, float* dst, size_t n) {
+    if (settle(e) != 0) return -1;  // a cache call drops the queued step first (sn.h:36-38)
     const float* src = which == 0 ? e->x : which == 1 ? e->qkv : which == 2 ? e->ao : which == 3 ? e->hb : nullptr;
     const size_t cap = (size_t) e->max_rows * (which == 0 ? e->E : which == 1 ? e->NQKV : which == 2 ? e->QD : e->F);
     if (!src || n > cap) return -1;
@@ -1250,7 +1429,10 @@ extern "C" int sn_logits(sn_engine* e, int k, float* dst, char* err, int err_len
     return sn_logits_rows(e, 1, &k, dst, err, err_len);
 }
 
-extern "C" void sn_want_probs(sn_engine* e, int on) { e->want_probs = on != 0; }
+extern "C" void sn_want_probs(sn_engine* e, int on) {
+    if (e->want_probs != (on != 0)) ++e->cfg_gen;
+    e->want_probs = on != 0;
+}
 extern "C" int sn_probs(sn_engine* e, int n_out, float* dst, char* err, int err_len) {
     if (n_out < 0 || n_out > e->last_pn) {
         sn_set_err(err, err_len, "the last step has no token probabilities for these rows");
@@ -1264,18 +1446,24 @@ extern "C" int sn_set_eog(sn_engine* e, const int32_t* ids, int n) {
     if (n < 0 || n > 8 || n >= e->V) return -1;
     for (int i = 0; i < n; ++i)
         if (ids[i] < 0 || ids[i] >= e->V) return -1;
+    if (settle(e) != 0) return -1;  // the queued step reads the ban list
+    ++e->cfg_gen;
     e->eog.assign(ids, ids + n);
     if (n > 0 && hipMemcpy(e->d_ban, ids, (size_t) n * 4, hipMemcpyHostToDevice) != hipSuccess) return -1;
     return 0;
 }
 extern "C" void sn_no_end(sn_engine* e, int slot, int on) {
-    if (slot >= 0 && slot < e->slots) e->no_end[slot] = on != 0;
+    if (slot >= 0 && slot < e->slots && e->no_end[slot] != (on != 0)) {
+        e->no_end[slot] = on != 0;
+        ++e->cfg_gen;
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
 // cache calls (sn_seq.inc.h)
 
 extern "C" int sn_copy(sn_engine* e, int from, int to, int n, char* err, int err_len) {
+    if (settle(e) != 0) return -1;  // a cache call drops the queued step first (sn.h:36-38)
     if (!slot_ok(e, from, 0, n) || !slot_ok(e, to, 0, n) || from == to) {
         sn_set_err(err, err_len, "sn_copy: bad slots or cells");
         return -1;
@@ -1310,6 +1498,7 @@ extern "C" int sn_copy(sn_engine* e, int from, int to, int n, char* err, int err
 }
 
 extern "C" int sn_clear(sn_engine* e, int slot, int from, int to, char* err, int err_len) {
+    if (settle(e) != 0) return -1;  // a cache call drops the queued step first (sn.h:36-38)
     if (!slot_ok(e, slot, from, to)) {
         sn_set_err(err, err_len, "sn_clear: bad slot or cells");
         return -1;
@@ -1400,6 +1589,7 @@ static int kv_xfer(sn_engine* e, int slot, int n, void* host, int save, char* er
     return 0;
 }
 extern "C" int snx_fill_kv(sn_engine* e, int slot, int n, uint64_t seed, char* err, int err_len) {
+    if (settle(e) != 0) return -1;  // a cache call drops the queued step first (sn.h:36-38)
     if (!slot_ok(e, slot, 0, n)) {
         sn_set_err(err, err_len, "snx_fill_kv: bad slot or cells");
         return -1;
@@ -1431,9 +1621,11 @@ extern "C" int snx_fill_kv(sn_engine* e, int slot, int n, uint64_t seed, char* e
 }
 
 extern "C" int sn_kv_save(sn_engine* e, int slot, int n, void* dst, char* err, int err_len) {
+    if (settle(e) != 0) return -1;  // a cache call drops the queued step first (sn.h:36-38)
     return kv_xfer(e, slot, n, dst, 1, err, err_len);
 }
 extern "C" int sn_kv_load(sn_engine* e, int slot, int n, const void* src, char* err, int err_len) {
+    if (settle(e) != 0) return -1;  // a cache call drops the queued step first (sn.h:36-38)
     return kv_xfer(e, slot, n, (void*) src, 0, err, err_len);
 }
 
@@ -1569,6 +1761,7 @@ extern "C" float sn_embd_norm(sn_engine* e) {
 extern "C" int sn_guess_head(const sn_engine* e) { return e->has_nextn ? 1 : 0; }
 extern "C" int sn_guess_on(sn_engine* e, int on) {
     if (!e->has_nextn) return 0;
+    settle(e);
     e->guess_on = on != 0;
     return e->guess_on;
 }

@@ -124,6 +124,7 @@ SNK_API = [
 EXT_API = [
     ("snx_graphs", None, [P, I]),
     ("snx_attn_mode", None, [P, I]),
+    ("snx_chain_count", C.c_long, [P, I]),
     ("snx_graph_count", C.c_long, [P, I]),
     ("snx_prof", None, [P, I]),
     ("snx_prof_read", I, [P, I, C.POINTER(C.c_double), C.POINTER(I), C.POINTER(C.c_double)]),
@@ -317,6 +318,10 @@ class Engine:
     def attn_mode(self, mode: int):
         """snx_attn_mode: the attention work list's form, -1 per step (default), 0 per-chunk + merge, 1 whole groups."""
         self.L.snx_attn_mode(self.e, int(mode))
+
+    def chain_count(self) -> tuple:
+        """(queued steps taken, queued steps dropped) since the engine opened (sn_step's chain)."""
+        return self.L.snx_chain_count(self.e, 0), self.L.snx_chain_count(self.e, 1)
 
     def graph_count(self) -> tuple:
         """(steps captured as a new graph, steps replayed from the cached graph) since the engine opened."""

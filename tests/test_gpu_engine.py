@@ -307,3 +307,77 @@ def test_attention_list_forms_give_the_same_steps(tiny):
     for (ta, la), (tb, lb) in zip(*outs):
         assert np.array_equal(ta, tb)
         assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
+def test_chained_steps(tiny):
+    """sn_step's chain (sn.h:31-41, sn_step.inc.h:31-212): a write step that samples each row in order has the next
+    step queued behind it on the GPU, fed its tokens there. Chained decode gives the same tokens and logits, bit for
+    bit, as unchained decode and takes every queued step; a step that is not the queued one, a cache call, or a change
+    of how tokens are chosen drops it, and the cache is then exactly as if it had never run (its cell zeroed)."""
+    V = TINY["n_vocab"]
+    r = np.random.default_rng(31)
+    lens = [17, 64, 40]  # slot 1's next cell starts a new page
+    prompts = [r.integers(0, V, n).astype(np.int32) for n in lens]
+    rows = np.arange(3, dtype=np.int32)
+    seq = np.arange(3, dtype=np.int32)
+    with S.Engine(tiny, slots=3, ctx=128, max_rows=64) as a, S.Engine(tiny, slots=3, ctx=128, max_rows=64) as b:
+        for eng in (a, b):
+            for s_, pr in enumerate(prompts):
+                eng.step(pr, np.full(len(pr), s_, np.int32), np.arange(len(pr), dtype=np.int32),
+                         np.array([len(pr) - 1], np.int32), n_write=0)
+        cur = r.integers(0, V, 3).astype(np.int32)
+        pos = np.array(lens, np.int32)
+
+        def both(tok, chain=1):
+            ta = a.step(tok, seq, pos, rows, chain=chain)
+            tb = b.step(tok, seq, pos, rows)
+            assert np.array_equal(ta, tb), (ta, tb)
+            la, lb = a.logits(rows), b.logits(rows)
+            assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+            return ta
+
+        for it in range(8):  # chained decode: every step after the first is the queued one
+            cur = both(cur).astype(np.int32)
+            pos += 1
+        assert a.chain_count() == (7, 0)
+        assert b.chain_count() == (0, 0)
+
+        def cell_zero(eng, slot, p):
+            kv = eng.kv_save(slot, p + 1).reshape(-1, 2, p + 1, 256)  # [layers][K, V][cells][KV heads x 128]
+            return not kv[:, :, p, :].any()
+
+        # a step that is not the queued one (other tokens): the queued step is dropped, its cells zeroed
+        cur = both((cur + 1) % V).astype(np.int32)
+        assert a.chain_count() == (7, 1)
+        pos += 1
+        # a cache call drops the queued step (at pos), then the caches agree cell for cell
+        a.clear(2, int(pos[2]) - 1, int(pos[2]))
+        b.clear(2, int(pos[2]) - 1, int(pos[2]))
+        assert a.chain_count() == (7, 2)
+        for s_ in range(3):
+            assert cell_zero(a, s_, int(pos[s_]))
+            n = int(pos[s_]) - (1 if s_ == 2 else 0)
+            assert np.array_equal(a.kv_save(s_, n), b.kv_save(s_, n)), s_
+        pos[2] -= 1
+        cur[2] = 5
+        cur = both(cur).astype(np.int32)  # (not the queued one: nothing queued)
+        pos += 1
+        cur = both(cur).astype(np.int32)  # the queued one
+        pos += 1
+        assert a.chain_count() == (8, 2)
+        a.want_probs(True)  # a change of how tokens are chosen: the queued step is not the one asked for
+        b.want_probs(True)
+        cur = both(cur).astype(np.int32)
+        assert a.chain_count() == (8, 3)
+        assert np.array_equal(a.probs(3), b.probs(3))
+        pos += 1
+        cur = both(cur, chain=0).astype(np.int32)  # taken, nothing queued after it
+        assert a.chain_count() == (9, 3)
+        pos += 1
+        both(cur, chain=0)
+        assert a.chain_count() == (9, 3)
+    # a row at the context's last cell queues nothing
+    with S.Engine(tiny, slots=1, ctx=64, max_rows=64) as a:
+        a.step(prompts[0][:10], np.zeros(10, np.int32), np.arange(10, dtype=np.int32), np.array([9], np.int32), n_write=0)
+        a.step(np.array([3], np.int32), np.zeros(1, np.int32), np.array([63], np.int32), np.zeros(1, np.int32), chain=1)
+        assert a.chain_count() == (0, 0)
