@@ -32,6 +32,19 @@ size_t snk_q8_workspace_bytes(int M, int N, int K);
 int snk_q8_gemm(const void* d_tiles, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi, void* d_ws,
                 size_t ws_bytes, void* stream);
 
+// Q6_K weights (block_q6_K: ql[128], qh[64], int8 scales[16], fp16 d per 256 weights; the reference reads them for the
+// token table and the LM head, sn_load.inc.h:341-359, kernels.metal:1010-1120), with ggml's CPU numerics
+// (vec_dot_q6_K_q8_K: Q8_K activations, integer sums per 16-weight group times its scale): bytes of the tile layout,
+// GGUF rows -> tiles (K % 256 == 0), the tiles dequantized back with the matmul's own unpack ((d * scale) * (q - 32),
+// for the bit-exactness check against dequantize_row_q6_K), the Q8_K activation records (quantize_row_q8_K_ref; RMS-
+// normed by d_norm_w first when not NULL), and the matmul y[m][n] (ldy apart, no workspace). 0, or -1 (bad shape).
+size_t snk_q6k_tiles_bytes(int N, int K);
+int snk_q6k_repack(const void* d_q6k, int N, int K, void* d_tiles, void* stream);
+int snk_q6k_dequant(const void* d_tiles, int N, int K, float* d_w, void* stream);
+size_t snk_xk_bytes(int M, int K);
+int snk_quant_q8k(const float* d_x, int M, int K, int ldx, const float* d_norm_w, float eps, void* d_xk, void* stream);
+int snk_q6k_gemm(const void* d_tiles, const void* d_xk, int M, int N, int K, float* d_y, int ldy, void* stream);
+
 // activation operand: M fp32 rows (ldx apart) quantized to Q8_0 (ggml x86 quantize_row_q8_0), RMS-normed by d_norm_w
 // first when it is not NULL (the rmsnorm of kernels.metal:121-140 fused in front)
 size_t snk_xa_bytes(int M, int K);

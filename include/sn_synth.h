@@ -16,10 +16,13 @@ typedef struct {
     float w_std;    // std of the matrices before quantization (configs: 0.02)
     float emb_std;  // std of the fp32 embedding table
     int wtype;      // the matrices' block type: 2 (0 too) Q4_0, 8 Q8_0
+    int embd_type;  // token_embd's type: 0 F32, 2 Q4_0, 8 Q8_0, 14 Q6_K (seeded valid blocks; n_embd % 256 == 0)
+    int tied;       // 1: no output.weight, the LM head is token_embd (which must then be quantized)
 } snx_model_cfg;
 
 // Write the model to `path` (GGUF v3; matrices quantized with ggml's quantize_row_q4_0_ref or quantize_row_q8_0_ref;
-// norms 1 + N(0, 0.1)). nthreads <= 0: all cores. The bytes depend only on (cfg, seed). 0, or -1 with the reason in err.
+// norms 1 + N(0, 0.1); a Q6_K token table as seeded blocks: q uniform in 0..63, scales uniform in -15..15, d chosen
+// for emb_std). nthreads <= 0: all cores. The bytes depend only on (cfg, seed). 0, or -1 with the reason in err.
 int snx_write_model(const char* path, const snx_model_cfg* cfg, uint64_t seed, int nthreads, char* err, int err_len);
 
 // ggml quantize_row_q4_0_ref of k values (k % 32 == 0): 18-byte blocks into y.

@@ -3,7 +3,7 @@
 Follows the GGUF layout the reference's own golden fixture records
 (engine/sllm-core/tests/fixtures/gguf_py_qwen3-0.6b-Q4_0.json: kv table, tensor table with ne = [K, N, ...], offsets
 from an aligned data section). Tensors come back as numpy views of a memory map: F32 as float32 [..., ne1, ne0],
-Q4_0 / Q8_0 as uint8 rows [..., ne1, row_bytes].
+Q4_0 / Q8_0 / Q6_K as uint8 rows [..., ne1, row_bytes].
 """
 from __future__ import annotations
 
@@ -11,7 +11,7 @@ import struct
 
 import numpy as np
 
-TYPES = {0: ("F32", 4, 1), 1: ("F16", 2, 1), 2: ("Q4_0", 18, 32), 8: ("Q8_0", 34, 32)}
+TYPES = {0: ("F32", 4, 1), 1: ("F16", 2, 1), 2: ("Q4_0", 18, 32), 8: ("Q8_0", 34, 32), 14: ("Q6_K", 210, 256)}
 _SCALAR = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<B", 10: "<Q", 11: "<q", 12: "<d"}
 
 

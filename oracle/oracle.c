@@ -139,6 +139,141 @@ float or_vec_dot_q8_0_q8_0(int64_t k, const uint8_t* w, const uint8_t* xq) {
 }
 
 // ggml CPU mul_mat of Q8_0 weights: the activation rows quantized to Q8_0 (x86 quantize_row_q8_0), then
+// ---- Q6_K / Q8_K ----
+// dequantize_row_q6_K: per 128-element half, l = 0..31 gives elements l, l+32, l+64, l+96 from ql[l], ql[l+32], qh[l]
+void or_dequantize_row_q6_K(const uint8_t* x, float* y, int64_t k) {
+    const int64_t nb = k / 256;
+    for (int64_t i = 0; i < nb; ++i) {
+        const uint8_t* b = x + i * 210;
+        const float d = h2f(b + 208);
+        const uint8_t* ql = b;
+        const uint8_t* qh = b + 128;
+        const int8_t* sc = (const int8_t*) (b + 192);
+        for (int n = 0; n < 256; n += 128) {
+            for (int l = 0; l < 32; ++l) {
+                const int is = l / 16;
+                const int q1 = (int) ((ql[l + 0] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                const int q2 = (int) ((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                const int q3 = (int) ((ql[l + 0] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                const int q4 = (int) ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                y[l + 0] = d * sc[is + 0] * q1;
+                y[l + 32] = d * sc[is + 2] * q2;
+                y[l + 64] = d * sc[is + 4] * q3;
+                y[l + 96] = d * sc[is + 6] * q4;
+            }
+            y += 128;
+            ql += 64;
+            qh += 32;
+            sc += 8;
+        }
+    }
+}
+
+// ggml's nearest_int: round half to even through the fp32 magic constant 1.5 * 2^23
+static int nearest_int(float fval) {
+    const float val = fval + 12582912.f;
+    int i;
+    memcpy(&i, &val, sizeof i);
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+void or_quantize_row_q8_K(const float* x, uint8_t* y, int64_t k) {
+    const int64_t nb = k / 256;
+    for (int64_t i = 0; i < nb; ++i) {
+        uint8_t* b = y + i * 292;
+        int8_t* qs = (int8_t*) (b + 4);
+        int16_t bs[16];
+        float max = 0.0f, amax = 0.0f;
+        for (int j = 0; j < 256; ++j) {
+            const float ax = fabsf(x[j]);
+            if (ax > amax) {
+                amax = ax;
+                max = x[j];
+            }
+        }
+        if (!amax) {
+            const float z = 0.0f;
+            memcpy(b, &z, 4);
+            memset(qs, 0, 256);
+            memset(b + 260, 0, 32);
+            x += 256;
+            continue;
+        }
+        const float iscale = -127.f / max;
+        for (int j = 0; j < 256; ++j) {
+            const int v = nearest_int(iscale * x[j]);
+            qs[j] = (int8_t) (v < 127 ? v : 127);
+        }
+        for (int j = 0; j < 16; ++j) {
+            int sum = 0;
+            for (int ii = 0; ii < 16; ++ii) sum += qs[j * 16 + ii];
+            bs[j] = (int16_t) sum;
+        }
+        memcpy(b + 260, bs, 32);
+        const float d = 1 / iscale;
+        memcpy(b, &d, 4);
+        x += 256;
+    }
+}
+
+float or_vec_dot_q6_K_q8_K(int64_t k, const uint8_t* w, const uint8_t* xq) {
+    const int64_t nb = k / 256;
+    int8_t aux8[256];
+    int16_t aux16[8];
+    int32_t aux32[8];
+    float sums[8] = {0};
+    for (int64_t i = 0; i < nb; ++i) {
+        const uint8_t* bw = w + i * 210;
+        const uint8_t* bx = xq + i * 292;
+        const uint8_t* q4 = bw;
+        const uint8_t* qh = bw + 128;
+        const int8_t* sc = (const int8_t*) (bw + 192);
+        const int8_t* q8 = (const int8_t*) (bx + 4);
+        memset(aux32, 0, sizeof aux32);
+        int8_t* a = aux8;
+        for (int j = 0; j < 256; j += 128) {
+            for (int l = 0; l < 32; ++l) {
+                a[l + 0] = (int8_t) ((q4[l + 0] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                a[l + 32] = (int8_t) ((q4[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                a[l + 64] = (int8_t) ((q4[l + 0] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                a[l + 96] = (int8_t) ((q4[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            }
+            a += 128;
+            q4 += 64;
+            qh += 32;
+        }
+        a = aux8;
+        for (int j = 0; j < 16; ++j) {
+            const int scale = sc[j];
+            for (int l = 0; l < 8; ++l) aux16[l] = (int16_t) (q8[l] * a[l]);
+            for (int l = 0; l < 8; ++l) aux32[l] += scale * aux16[l];
+            q8 += 8;
+            a += 8;
+            for (int l = 0; l < 8; ++l) aux16[l] = (int16_t) (q8[l] * a[l]);
+            for (int l = 0; l < 8; ++l) aux32[l] += scale * aux16[l];
+            q8 += 8;
+            a += 8;
+        }
+        float d8;
+        memcpy(&d8, bx, 4);
+        const float d = h2f(bw + 208) * d8;
+        for (int l = 0; l < 8; ++l) sums[l] += d * aux32[l];
+    }
+    float sumf = 0.0f;
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+void or_mul_mat_q6_K(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nthreads) {
+    const int64_t nb = K / 256;
+    uint8_t* xq = (uint8_t*) malloc((size_t) M * nb * 292);
+    for (int64_t m = 0; m < M; ++m) or_quantize_row_q8_K(X + m * K, xq + m * nb * 292, K);
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t m = 0; m < M; ++m) Y[m * N + n] = or_vec_dot_q6_K_q8_K(K, W + n * nb * 210, xq + m * nb * 292);
+    free(xq);
+}
+
 // vec_dot_q8_0_q8_0 per (row, output)
 void or_mul_mat_q8_0(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nthreads) {
     const int64_t nb = K / QK;
@@ -427,6 +562,13 @@ static void mm(const or_qwen3* m, const uint8_t* W, int64_t N, int64_t K, const 
     if (m->wtype == 8) or_mul_mat_q8_0(W, N, K, X, M, Y, nt);
     else or_mul_mat_q4_0(W, N, K, X, M, Y, nt);
 }
+// the LM head (its own block type: Q6_K when tied to a Q6_K token table)
+static void mm_head(const or_qwen3* m, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nt) {
+    const int t = m->head_type ? m->head_type : m->wtype;
+    if (t == 14) or_mul_mat_q6_K(m->output, N, K, X, M, Y, nt);
+    else if (t == 8) or_mul_mat_q8_0(m->output, N, K, X, M, Y, nt);
+    else or_mul_mat_q4_0(m->output, N, K, X, M, Y, nt);
+}
 // bytes of one block of the model's matrices
 static size_t wblock(const or_qwen3* m) { return m->wtype == 8 ? 34 : 18; }
 
@@ -535,7 +677,7 @@ void or_qwen3_step(const or_qwen3* m, or_kv* kv, int R, const int32_t* tok, cons
     float* ho = (float*) malloc((size_t) (n_out > 0 ? n_out : 1) * E * 4);
     for (int j = 0; j < n_out; ++j) or_rmsnorm(x + (size_t) out_rows[j] * E, m->output_norm, E, m->eps, ho + (size_t) j * E);
     if (hidden) memcpy(hidden, ho, (size_t) n_out * E * 4);
-    if (n_out > 0) mm(m, m->output, V, E, ho, n_out, logits, nthreads);
+    if (n_out > 0) mm_head(m, V, E, ho, n_out, logits, nthreads);
     for (int j = 0; j < n_out; ++j) out_tok[j] = or_argmax(logits + (size_t) j * V, V, NULL, 0);
     free(ho);
     free(x);
@@ -583,7 +725,7 @@ void or_mtp_guess(const or_qwen3* m, or_kv* kv, int seq, int32_t tok, int pos, i
         mtp_in(m, 1, &t, h, x, nthreads);
         block(m, m->mtp, kv, m->n_layer, 1, &seq, &p, x, cs, 0, nthreads);
         or_rmsnorm(x, m->mtp_head_norm, E, m->eps, h);  // the head's output state: the next row's hprev
-        mm(m, m->output, V, E, h, 1, lg, nthreads);
+        mm_head(m, V, E, h, 1, lg, nthreads);
         t = or_argmax(lg, V, NULL, 0);
         out_tok[j] = t;
         if (logits) memcpy(logits + (size_t) j * V, lg, (size_t) V * 4);

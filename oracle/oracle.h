@@ -16,13 +16,19 @@
 //     iterative theta (kernels.metal:149-197), SwiGLU silu(g)*u (kernels.metal:564-568), greedy argmax with the lowest id on
 //     ties (kernels.metal:327-356), paged GQA decode attention (kernels.metal:1122-1192), the Qwen3 layer order
 //     (sn_attn.inc.h:216-231) and the output stage (sn_encode.inc.h:248-317).
+//   * Q6_K (the token table / tied LM head of real Qwen3 GGUFs; the reference reads them, sn_load.inc.h:341-359,
+//     kernels.metal:1010-1120): ggml `dequantize_row_q6_K`, the Q8_K activations of a Q6_K mul_mat
+//     (`quantize_row_q8_K_ref`) and the generic `ggml_vec_dot_q6_K_q8_K` (integer sums of scale * (q6 - 32) * q8 per
+//     16-element group in 8 lanes, fp32 sums[l] += d6 * d8 * aux32[l]).
 //   * MoE routing softmax -> top-k (ties: lower id) -> renormalise with the sum floored at 6.1035e-5 (kernels.metal:3419-3467).
 //   * Draft acceptance: rows checked in order, kept while draft == target argmax (next_engine/take.rs:339-357).
 //
 // How each function is pinned (tests/test_oracle.py, tests/test_golden.py): dequant by the closed form on every nibble
 // and fp16 specials; fp16 conversion against numpy; mul_mat against an fp64 product of the dequantized operands and
 // against the integer block sum; RMSNorm, RoPE, argmax/top-2, MoE routing and acceptance against closed forms or brute
-// force; paged attention against an fp64 dense softmax over page-gathered cells, chunked == monolithic, page-placement
+// force; Q6_K dequant by an independent packer of explicit values, Q8_K by its invariants, vec_dot_q6_K_q8_K by the
+// explicit integer block sum and the fp64 product of the dequantized operands; paged attention against an fp64 dense
+// softmax over page-gathered cells, chunked == monolithic, page-placement
 // and shared-prefix invariance; the model writer's GGUF layout against the reference's own GGUF fixture.
 // Parity unpinned against ggml itself (no ggml vector exists offline): the exact bytes of quantize_row_q4_0_ref and of
 // x86 quantize_row_q8_0 (their rounding rules are restated from ggml's published source and checked by invariants
@@ -89,6 +95,22 @@ void or_paged_attn_chunked(const float* q, int nq, const int32_t* qseq, const in
                            const uint16_t* kpool, const uint16_t* vpool, int page_cells, const int32_t* pt,
                            int max_pages, float scale, int chunk, float* out);
 
+// ---- Q6_K weights / Q8_K activations (ggml k-quants, QK_K = 256 elements a block) ----
+// block_q6_K: 210 bytes = ql[128] (low 4 bits), qh[64] (high 2 bits), int8 scales[16], fp16 d. Element e of a block:
+// half h = e / 128, quarter c = (e % 128) / 32, l = e % 32: the low nibble (c < 2) or high nibble (c >= 2) of
+// ql[64h + 32 (c & 1) + l], high bits (qh[32h + l] >> 2c) & 3; value d * scales[e / 16] * (q - 32)
+// (ggml dequantize_row_q6_K: (d * scale) * (q - 32), fp32 left to right).
+// block_q8_K: fp32 d, int8 qs[256], int16 bsums[16] (292 bytes). quantize_row_q8_K_ref: max = the element of largest
+// |x| (the first on ties), iscale = -127 / max, q = min(127, nearest_int(iscale * x)) (round half to even),
+// d = 1 / iscale, bsums = the sums of 16 consecutive q; an all-zero block gets d = 0, q = 0.
+void or_dequantize_row_q6_K(const uint8_t* x, float* y, int64_t k);
+void or_quantize_row_q8_K(const float* x, uint8_t* y, int64_t k);
+// ggml_vec_dot_q6_K_q8_K (generic form): per block the integer sums scale * (q6 - 32) * q8 in 8 lanes (aux32), then
+// sums[l] += (d6 * d8) * aux32[l]; the result is the sum of the 8 lanes
+float or_vec_dot_q6_K_q8_K(int64_t k, const uint8_t* w, const uint8_t* xq);
+// Y[M][N] = X[M][K] . W[N][K]^T with Q6_K weights (ggml CPU mul_mat: Q8_K activations, vec_dot_q6_K_q8_K); K % 256 == 0
+void or_mul_mat_q6_K(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nthreads);
+
 // ---- a Qwen3 dense model (the GGUF's tensors; Q4_0 or Q8_0 matrices in GGUF block layout, ne = [K, N]) ----
 typedef struct {
     const float* attn_norm;  // [E]
@@ -121,7 +143,8 @@ typedef struct {
     const or_layer* mtp;
     const uint8_t* mtp_eh;
     const float *mtp_enorm, *mtp_hnorm, *mtp_head_norm;  // head_norm: shared_head_norm, else output_norm
-    int wtype;  // the matrices' block type: 2 Q4_0 (block_q4_0), 8 Q8_0 (block_q8_0)
+    int wtype;      // the matrices' block type: 2 Q4_0 (block_q4_0), 8 Q8_0 (block_q8_0)
+    int head_type;  // the output matrix's: 2 Q4_0, 8 Q8_0, 14 Q6_K (token_embd's when the head is tied); 0: wtype
 } or_qwen3;
 
 // The oracle's KV cache: contiguous per (sequence, layer): K and V fp16 [ctx][KVH][D]. n_layer counts the guess

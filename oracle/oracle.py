@@ -51,6 +51,12 @@ def _declare(L):
     L.or_vec_dot_q8_0_q8_0.argtypes = [I64, P, P]
     L.or_vec_dot_q8_0_q8_0.restype = C.c_float
     L.or_mul_mat_q8_0.argtypes = [P, I64, I64, P, I64, P, C.c_int]
+    for f in ("or_dequantize_row_q6_K", "or_quantize_row_q8_K"):
+        getattr(L, f).argtypes = [P, P, I64]
+        getattr(L, f).restype = None
+    L.or_vec_dot_q6_K_q8_K.argtypes = [I64, P, P]
+    L.or_vec_dot_q6_K_q8_K.restype = C.c_float
+    L.or_mul_mat_q6_K.argtypes = [P, I64, I64, P, I64, P, C.c_int]
     L.or_mul_mat_q4_0.argtypes = [P, I64, I64, P, I64, P, C.c_int]
     L.or_mul_mat_q4_0_f64.argtypes = [P, I64, I64, P, I64, P, C.c_int]
     L.or_rmsnorm.argtypes = [P, P, I64, C.c_float, P]
@@ -117,6 +123,40 @@ def dequantize_q8_0(q: np.ndarray, K: int) -> np.ndarray:
     out = np.empty((M, K), np.float32)
     lib().or_dequantize_row_q8_0(_p(q), _p(out), M * K)
     return out
+
+
+def dequantize_q6_K(q: np.ndarray, K: int) -> np.ndarray:
+    """[N][K/256*210] uint8 block_q6_K rows -> [N][K] fp32 (ggml dequantize_row_q6_K)."""
+    q = np.ascontiguousarray(q, np.uint8)
+    N = q.size // (K // 256 * 210)
+    out = np.empty((N, K), np.float32)
+    lib().or_dequantize_row_q6_K(_p(q), _p(out), N * K)
+    return out
+
+
+def quantize_q8_K(x: np.ndarray) -> np.ndarray:
+    """[M][K] fp32 -> [M][K/256*292] uint8 block_q8_K rows (ggml quantize_row_q8_K_ref)."""
+    x = np.ascontiguousarray(x, np.float32)
+    M, K = x.shape
+    out = np.empty((M, K // 256 * 292), np.uint8)
+    lib().or_quantize_row_q8_K(_p(x), _p(out), M * K)
+    return out
+
+
+def vec_dot_q6_K_q8_K(w_row: np.ndarray, xq_row: np.ndarray, K: int) -> float:
+    return float(lib().or_vec_dot_q6_K_q8_K(K, _p(np.ascontiguousarray(w_row, np.uint8)),
+                                            _p(np.ascontiguousarray(xq_row, np.uint8))))
+
+
+def mul_mat_q6_K(Wq: np.ndarray, K: int, X: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    """Y[M][N] = X[M][K] . W[N][K]^T for Q6_K weights, ggml CPU semantics (Q8_K activations, vec_dot_q6_K_q8_K)."""
+    Wq = np.ascontiguousarray(Wq, np.uint8)
+    X = np.ascontiguousarray(X, np.float32)
+    N = Wq.size // (K // 256 * 210)
+    M = X.shape[0]
+    Y = np.empty((M, N), np.float32)
+    lib().or_mul_mat_q6_K(_p(Wq), N, K, _p(X), M, _p(Y), nthreads)
+    return Y
 
 
 def quantize_q8_0_ref(w: np.ndarray) -> np.ndarray:
@@ -250,7 +290,7 @@ class _Model(C.Structure):
                 ("tok_embd", C.c_void_p), ("output_norm", C.c_void_p), ("output", C.c_void_p),
                 ("layers", C.POINTER(_Layer)), ("mtp", C.POINTER(_Layer)), ("mtp_eh", C.c_void_p),
                 ("mtp_enorm", C.c_void_p), ("mtp_hnorm", C.c_void_p), ("mtp_head_norm", C.c_void_p),
-                ("wtype", C.c_int)]
+                ("wtype", C.c_int), ("head_type", C.c_int)]
 
 
 class _KV(C.Structure):
@@ -280,6 +320,10 @@ class Qwen3:
         emb = g.tensor("token_embd.weight")
         self.V = emb.shape[0]
         self._keep = []
+        # a quantized token table (Q4_0, Q8_0, Q6_K: ggml's dequantize_row_*) is used as its fp32 rows
+        et = g.type_name("token_embd.weight")
+        self._emb = emb if et == "F32" else {"Q4_0": dequantize_q4_0, "Q8_0": dequantize_q8_0,
+                                             "Q6_K": dequantize_q6_K}[et](emb, self.E)
 
         def ptr(name):
             t = g.tensor(name)
@@ -305,12 +349,17 @@ class Qwen3:
                 ly.wu = ptr(p + "ffn_up.weight")
                 ly.wd = ptr(p + "ffn_down.weight")
         self._layers = layers
-        wt = {"Q4_0": 2, "Q8_0": 8}[g.type_name("output.weight")]
+        types = {"Q4_0": 2, "Q8_0": 8, "Q6_K": 14}
+        wt = types[g.type_name("blk.0.attn_q.weight")]
+        head = "output.weight" if "output.weight" in g.tinfo else "token_embd.weight"  # no output: tied
         self.wtype = wt
+        self.head_type = types[g.type_name(head)]
+        emb32 = np.ascontiguousarray(self._emb, np.float32)
+        self._keep.append(emb32)
         self.m = _Model(self.L, self.E, self.H, self.KVH, self.D, self.F, self.V, self.NE, self.NEU, self.FE,
-                        self.eps, self.base, ptr("token_embd.weight"), ptr("output_norm.weight"),
-                        ptr("output.weight"), layers)
+                        self.eps, self.base, emb32.ctypes.data, ptr("output_norm.weight"), ptr(head), layers)
         self.m.wtype = wt
+        self.m.head_type = self.head_type
         if self.n_mtp:
             p = f"blk.{self.L}.nextn."
             self.m.mtp = C.cast(C.byref(layers, self.L * C.sizeof(_Layer)), C.POINTER(_Layer))

@@ -13,6 +13,7 @@ size_t ggml_row_bytes(int type, int64_t ne0) {
         case GGML_F16: return (size_t) ne0 * 2;
         case GGML_Q4_0: return (size_t) (ne0 / 32) * 18;
         case GGML_Q8_0: return (size_t) (ne0 / 32) * 34;
+        case GGML_Q6_K: return (size_t) (ne0 / 256) * 210;
         default: return 0;
     }
 }

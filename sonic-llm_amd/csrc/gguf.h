@@ -9,7 +9,7 @@
 #include <string>
 #include <vector>
 
-enum GgmlType { GGML_F32 = 0, GGML_F16 = 1, GGML_Q4_0 = 2, GGML_Q8_0 = 8 };
+enum GgmlType { GGML_F32 = 0, GGML_F16 = 1, GGML_Q4_0 = 2, GGML_Q8_0 = 8, GGML_Q6_K = 14 };
 
 struct GgufValue {
     int type = -1;  // gguf value type of the scalar (or of the array's items)

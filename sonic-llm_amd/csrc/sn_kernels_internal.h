@@ -62,6 +62,16 @@ void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa
 int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* ws,
             size_t ws_bytes, hipStream_t st, int wt = WT_Q4_0);
 
+// ---- Q6_K weights (csrc/q6k.hip) ----
+// GGUF Q6_K rows [N][K / 256 x 210 bytes] -> tiles (K % 256 == 0); the tiles back to fp32 [N][K] (bit-exact check)
+void q6k_repack(const uint8_t* src, int N, int K, uint8_t* dst, hipStream_t st);
+void q6k_dequant(const uint8_t* tiles, int N, int K, float* out, hipStream_t st);
+// rows of X (source rows[m] when given; ldx floats apart), RMS-normed by nw when given, into Q8_K records (xk_bytes)
+void quant_q8k(const float* x, const int32_t* rows, int M, int K, int ldx, const float* nw, float eps, uint8_t* xk,
+               hipStream_t st);
+// y[m][n] (ldy apart) = the rows of xk . the tiles' rows (ggml vec_dot_q6_K_q8_K); 0, or -1 (K % 256)
+int q6k_gemm(const uint8_t* tiles, const uint8_t* xk, int M, int N, int K, float* y, int ldy, hipStream_t st);
+
 // ---- paged attention ----
 // One work item = (query group, KV head, chunk of ATT_CHUNK cells). A query group is up to 16/G rows of one
 // sequence (G = H/KVH query heads per KV head); its rows' positions rise by one (draft rows, prompt rows).

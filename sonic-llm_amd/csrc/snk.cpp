@@ -66,6 +66,36 @@ extern "C" int snk_argmax(const float* d_logits, int V, int n, const int32_t* d_
 
 extern "C" size_t snk_xa_bytes(int M, int K) { return xa_bytes(M, K); }
 
+extern "C" size_t snk_q6k_tiles_bytes(int N, int K) { return N > 0 && K > 0 && K % 256 == 0 ? q6t_bytes(N, K) : 0; }
+
+extern "C" int snk_q6k_repack(const void* d_q6k, int N, int K, void* d_tiles, void* stream) {
+    if (N <= 0 || K <= 0 || K % 256) return -1;
+    q6k_repack((const uint8_t*) d_q6k, N, K, (uint8_t*) d_tiles, (hipStream_t) stream);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int snk_q6k_dequant(const void* d_tiles, int N, int K, float* d_w, void* stream) {
+    if (N <= 0 || K <= 0 || K % 256) return -1;
+    q6k_dequant((const uint8_t*) d_tiles, N, K, d_w, (hipStream_t) stream);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" size_t snk_xk_bytes(int M, int K) { return M > 0 && K > 0 && K % 256 == 0 ? xk_bytes(M, K) : 0; }
+
+extern "C" int snk_quant_q8k(const float* d_x, int M, int K, int ldx, const float* d_norm_w, float eps, void* d_xk,
+                             void* stream) {
+    if (M <= 0 || K <= 0 || K % 256 || ldx < K) return -1;
+    quant_q8k(d_x, nullptr, M, K, ldx, d_norm_w, eps, (uint8_t*) d_xk, (hipStream_t) stream);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int snk_q6k_gemm(const void* d_tiles, const void* d_xk, int M, int N, int K, float* d_y, int ldy,
+                            void* stream) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 256 || ldy < N) return -1;
+    const int rc = q6k_gemm((const uint8_t*) d_tiles, (const uint8_t*) d_xk, M, N, K, d_y, ldy, (hipStream_t) stream);
+    return rc == 0 && hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 extern "C" int snk_quant_act(const float* d_x, int M, int K, int ldx, const float* d_norm_w, float eps, void* d_xa,
                              void* stream) {
     if (M <= 0 || K <= 0 || K % 32 || ldx < K || ldx % 4) return -1;

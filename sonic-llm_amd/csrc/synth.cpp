@@ -73,6 +73,23 @@ void sn_quantize_row_q8_0(const float* x, uint8_t* y, int64_t k) {
     }
 }
 
+// A Q6_K row of seeded valid blocks (block_q6_K: ql[128], qh[64], int8 scales[16], fp16 d): q uniform in 0..63,
+// scales uniform in -15..15, d = std / 165 (the values' std is then about `std`)
+static void q6k_row(uint64_t seed, uint64_t tensor, uint64_t row, float std, uint8_t* dst, int64_t K) {
+    uint64_t s = seed ^ (tensor * 0xD1B54A32D192ED03ull) ^ (row * 0x9E3779B97F4A7C15ull) ^ 0x6A09E667F3BCC909ull;
+    splitmix64(&s);
+    for (int64_t b = 0; b < K / 256; ++b) {
+        uint8_t* blk = dst + b * 210;
+        for (int i = 0; i < 192; i += 8) {  // ql and qh: every bit pattern is a valid quant
+            const uint64_t v = splitmix64(&s);
+            memcpy(blk + i, &v, 8);
+        }
+        for (int i = 0; i < 16; ++i) blk[192 + i] = (uint8_t) (int8_t) ((int) (splitmix64(&s) % 31) - 15);
+        const _Float16 d = (_Float16) (std / 165.0f);
+        memcpy(blk + 208, &d, 2);
+    }
+}
+
 namespace {
 struct Gen {
     std::string name;
@@ -111,6 +128,13 @@ extern "C" int snx_write_model(const char* path, const snx_model_cfg* c, uint64_
         w.u32(a + ".expert_used_count", (uint32_t) c->n_expert_used);
         w.u32(a + ".expert_feed_forward_length", (uint32_t) c->n_ff_exp);
     }
+    const int ET = c->embd_type;
+    if ((ET != GGML_F32 && ET != GGML_Q4_0 && ET != GGML_Q8_0 && ET != GGML_Q6_K) || (ET == GGML_Q6_K && E % 256) ||
+        (c->tied && ET == GGML_F32)) {
+        sn_set_err(err, err_len, "snx_write_model: embd_type must be 0, 2, 8 or 14 (Q6_K: n_embd %% 256 == 0), and "
+                                 "quantized when the head is tied");
+        return -1;
+    }
     if (c->wtype != 0 && c->wtype != GGML_Q4_0 && c->wtype != GGML_Q8_0) {
         sn_set_err(err, err_len, "snx_write_model: wtype must be 2 (Q4_0) or 8 (Q8_0)");
         return -1;
@@ -118,9 +142,9 @@ extern "C" int snx_write_model(const char* path, const snx_model_cfg* c, uint64_
     const int WQ = c->wtype == GGML_Q8_0 ? GGML_Q8_0 : GGML_Q4_0;  // the matrices' type
     const float ws = c->w_std, nstd = 0.1f;
     std::vector<Gen> g;
-    g.push_back({"token_embd.weight", GGML_F32, {E, V}, 0.0f, c->emb_std});
+    g.push_back({"token_embd.weight", ET, {E, V}, 0.0f, c->emb_std});
     g.push_back({"output_norm.weight", GGML_F32, {E}, 1.0f, nstd});
-    g.push_back({"output.weight", WQ, {E, V}, 0.0f, ws});
+    if (!c->tied) g.push_back({"output.weight", WQ, {E, V}, 0.0f, ws});
     const int nl = c->n_layer + (c->nextn ? 1 : 0);
     for (int i = 0; i < nl; ++i) {
         const std::string p = "blk." + std::to_string(i) + ".";
@@ -186,6 +210,7 @@ extern "C" int snx_write_model(const char* path, const snx_model_cfg* c, uint64_
                         normals(seed, ti, (uint64_t) r, t.mean, t.std, row.data(), K);
                         uint8_t* dst = buf.data() + (size_t) (r - r0) * rb;
                         if (t.type == GGML_F32) memcpy(dst, row.data(), rb);
+                        else if (t.type == GGML_Q6_K) q6k_row(seed, ti, (uint64_t) r, t.std, dst, K);
                         else if (t.type == GGML_Q8_0) sn_quantize_row_q8_0(row.data(), dst, K);
                         else sn_quantize_row_q4_0(row.data(), dst, K);
                     }

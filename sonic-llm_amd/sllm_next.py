@@ -97,6 +97,12 @@ SNK_API = [
     ("snk_q4_repack", I, [P, I, I, P, P]),
     ("snk_q4_dequant", I, [P, I, I, P, P]),
     ("snk_xa_bytes", C.c_size_t, [I, I]),
+    ("snk_q6k_tiles_bytes", C.c_size_t, [I, I]),
+    ("snk_q6k_repack", I, [P, I, I, P, P]),
+    ("snk_q6k_dequant", I, [P, I, I, P, P]),
+    ("snk_xk_bytes", C.c_size_t, [I, I]),
+    ("snk_quant_q8k", I, [P, I, I, I, P, C.c_float, P, P]),
+    ("snk_q6k_gemm", I, [P, P, I, I, I, P, I, P]),
     ("snk_q8_tiles_bytes", C.c_size_t, [I, I]),
     ("snk_q8_repack", I, [P, I, I, P, P]),
     ("snk_q8_dequant", I, [P, I, I, P, P]),
@@ -168,14 +174,17 @@ def call(f, *args):
 class ModelCfg(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_ff", "n_vocab",
                                        "n_expert", "n_expert_used", "n_ff_exp", "nextn")] + \
-               [(n, C.c_float) for n in ("rope_base", "eps", "w_std", "emb_std")] + [("wtype", C.c_int)]
+               [(n, C.c_float) for n in ("rope_base", "eps", "w_std", "emb_std")] + \
+               [(n, C.c_int) for n in ("wtype", "embd_type", "tied")]
 
 
 def model_cfg(n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, head_dim=128, n_expert=0, n_expert_used=0,
-              n_ff_exp=0, nextn=0, rope_base=1e6, eps=1e-6, w_std=0.02, emb_std=0.02, wtype=2) -> ModelCfg:
-    """wtype: the matrices' block type, 2 Q4_0 or 8 Q8_0."""
+              n_ff_exp=0, nextn=0, rope_base=1e6, eps=1e-6, w_std=0.02, emb_std=0.02, wtype=2, embd_type=0,
+              tied=0) -> ModelCfg:
+    """wtype: the matrices' block type, 2 Q4_0 or 8 Q8_0; embd_type: token_embd's, 0 F32, 2 Q4_0, 8 Q8_0, 14 Q6_K;
+    tied: no output.weight (the LM head is token_embd)."""
     return ModelCfg(n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_expert, n_expert_used, n_ff_exp,
-                    nextn, rope_base, eps, w_std, emb_std, wtype)
+                    nextn, rope_base, eps, w_std, emb_std, wtype, embd_type, tied)
 
 
 # The configs' models (BASELINE.json configs[2], configs[3], configs[4])

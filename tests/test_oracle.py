@@ -373,3 +373,90 @@ def test_accept_rule_brute_force():
                 while want < k and d[want] == t[want]:
                     want += 1
                 assert a == want
+
+
+# ---- Q6_K / Q8_K (ggml k-quants) ------------------------------------------------------------------------------------
+def pack_q6_K(q: np.ndarray, sc: np.ndarray, d: np.ndarray) -> np.ndarray:
+    """block_q6_K bytes from explicit values: q [nb][256] in 0..63 (value q - 32), sc [nb][16] int8, d [nb] fp16. Element
+    e: half h = e // 128, quarter c = (e % 128) // 32, l = e % 32; low 4 bits in ql[64h + 32(c & 1) + l] (low nibble
+    for c < 2, high for c >= 2), high 2 bits at bit 2c of qh[32h + l]."""
+    nb = q.shape[0]
+    out = np.zeros((nb, 210), np.uint8)
+    for b in range(nb):
+        ql = np.zeros(128, np.int64)
+        qh = np.zeros(64, np.int64)
+        for e in range(256):
+            h, c, l = e // 128, (e % 128) // 32, e % 32
+            v = int(q[b, e])
+            i = 64 * h + 32 * (c & 1) + l
+            ql[i] |= (v & 15) << (4 if c >= 2 else 0)
+            qh[32 * h + l] |= (v >> 4) << (2 * c)
+        out[b, :128] = ql
+        out[b, 128:192] = qh
+        out[b, 192:208] = sc[b].astype(np.int8).view(np.uint8)
+        out[b, 208:210] = np.array([d[b]], np.float16).view(np.uint8)
+    return out
+
+
+def test_q6_K_dequant_closed_form():
+    r = rng(60)
+    nb = 3
+    q = r.integers(0, 64, (nb, 256))
+    q[0] = np.arange(256) % 64  # every value in every position class
+    sc = r.integers(-128, 128, (nb, 16))
+    sc[1, :2] = (-128, 127)
+    d = np.array([0.0123, -3.5e-5, 6.1e-5], np.float16)  # normal, small negative, near the subnormal edge
+    blocks = pack_q6_K(q, sc, d)
+    got = O.dequantize_q6_K(blocks.reshape(-1), 256 * nb).reshape(nb, 256)
+    want = (d.astype(np.float32)[:, None] * sc.astype(np.float32)[:, np.arange(256) // 16]) * (q - 32).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+
+
+def test_quantize_q8_K_invariants():
+    r = rng(61)
+    x = (r.standard_normal((4, 512)) * 3).astype(np.float32)
+    x[1, 7] = -9.0  # a negative extreme
+    x[2, 300], x[2, 301] = 5.0, -5.0  # equal |x|: the first is the extreme
+    x[3, 256:] = 0.0  # an all-zero block
+    xq = O.quantize_q8_K(x).reshape(4, 2, 292)
+    for m in range(4):
+        for b in range(2):
+            blk = xq[m, b]
+            d = blk[:4].copy().view(np.float32)[0]
+            qs = blk[4:260].copy().view(np.int8).astype(np.int64)
+            bs = blk[260:292].copy().view(np.int16).astype(np.int64)
+            xs = x[m, 256 * b:256 * (b + 1)]
+            if not np.any(xs):
+                assert d == 0 and not qs.any() and not bs.any()
+                continue
+            j = int(np.argmax(np.abs(xs)))  # numpy: the first of equal maxima
+            assert qs[j] == -127  # iscale = -127 / max sends the extreme to -127
+            assert np.all(qs >= -127) and np.all(qs <= 127)
+            assert np.array_equal(bs, qs.reshape(16, 16).sum(1))
+            assert abs(d * -127 - xs[j]) <= 1e-6 * abs(xs[j])
+            assert np.all(np.abs(d * qs - xs) <= abs(d) * 0.5 + 1e-6 * abs(xs[j]))
+
+
+def test_vec_dot_q6_K_is_the_integer_block_sum():
+    r = rng(62)
+    nb, K = 4, 1024
+    q = r.integers(0, 64, (nb, 256))
+    sc = r.integers(-128, 128, (nb, 16))
+    d = (r.random(nb) * 1e-3 + 1e-4).astype(np.float16)
+    w = pack_q6_K(q, sc, d).reshape(-1)
+    x = r.standard_normal((1, K)).astype(np.float32)
+    xq = O.quantize_q8_K(x).reshape(nb, 292)
+    got = O.vec_dot_q6_K_q8_K(w, xq.reshape(-1), K)
+    want = 0.0
+    for b in range(nb):
+        q8 = xq[b, 4:260].copy().view(np.int8).astype(np.int64)
+        isum = int(np.sum(sc[b][np.arange(256) // 16] * (q[b] - 32) * q8))
+        want += float(np.float32(np.float32(d[b]) * xq[b, :4].copy().view(np.float32)[0])) * isum
+    assert abs(got - want) <= 1e-5 * max(1.0, abs(want))
+    # and the f64 product of the dequantized operands (the same numbers)
+    wd = O.dequantize_q6_K(w, K).astype(np.float64)
+    xd = np.concatenate([xq[b, :4].copy().view(np.float32)[0] * xq[b, 4:260].copy().view(np.int8).astype(np.float64)
+                         for b in range(nb)])
+    assert abs(got - float(wd[0] @ xd)) <= 1e-5 * max(1.0, abs(want))
+    Y = O.mul_mat_q6_K(w.reshape(1, -1), K, x)
+    assert Y.shape == (1, 1) and Y[0, 0] == np.float32(got)
