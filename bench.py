@@ -35,7 +35,7 @@ def model_file(cfg_kw, seed, path=None):
     import sllm_next as S
     d = os.environ.get("SN_BENCH_DIR") or "/tmp"
     tag = ("_mtp" if cfg_kw.get("nextn") else "") + (f"_moe{cfg_kw['n_expert']}" if cfg_kw.get("n_expert") else "") + \
-          ("_q8" if cfg_kw.get("wtype") == 8 else "")
+          ("_q8" if cfg_kw.get("wtype") == 8 else "") + ("_q6kt" if cfg_kw.get("tied") else "")
     path = path or os.path.join(d, f"sonic_qwen3_{cfg_kw['n_layer']}L_{cfg_kw['n_embd']}{tag}_{seed}.gguf")
     done = path + ".done"
     if not (os.path.exists(path) and os.path.exists(done)):
@@ -94,6 +94,9 @@ def main():
                     help="attention work list: -1 chosen per step, 0 per-chunk + merge, 1 whole groups")
     ap.add_argument("--wtype", type=int, default=2, choices=(2, 8),
                     help="decode / moe: the model's matrices in Q4_0 (2, the configs) or Q8_0 (8)")
+    ap.add_argument("--table", default="f32", choices=("f32", "q6k-tied"),
+                    help="decode: an F32 token table and an untied head of the matrices' type (the configs), or a "
+                         "Q6_K token table tied to the LM head (the layout of Qwen3's published GGUFs)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device once (a plain copy kernel of known size, to scale "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -124,6 +127,9 @@ def main():
     cfg = dict(S.QWEN3_30B_A3B if moe else S.QWEN3_4B)
     if args.wtype == 8:
         cfg["wtype"] = 8
+    tied = args.table == "q6k-tied"
+    if tied:
+        cfg.update(embd_type=14, tied=1)
     path = model_file(cfg, args.seed, args.model)
     B, ctx = args.seqs, args.ctx
     total = ctx + args.warmup + args.steps + args.prof_steps + 1
@@ -185,7 +191,7 @@ def main():
     # WRITE_SIZE, scaled by a copy of known size): profiles/decode_qwen3_4b_b32_ctx2048_traffic.md
     traffic = {}
     tpath = os.path.join(ROOT, "profiles", "decode_qwen3_4b_b32_ctx2048_traffic.json")
-    if not moe and args.wtype == 2 and (B, ctx) == (32, 2048) and os.path.exists(tpath):
+    if not moe and args.wtype == 2 and not tied and (B, ctx) == (32, 2048) and os.path.exists(tpath):
         traffic = json.load(open(tpath))
 
     def roof(k):
@@ -206,7 +212,8 @@ def main():
               f"agg decode tok/s, Qwen3-4B-arch {q} x32 seqs; {q} GEMV % HBM peak")
     workload = (f"Qwen3-30B-A3B-arch {q} MoE batched decode step (BASELINE.json configs[4])" if moe else
                 f"Qwen3-4B-arch {q} batched decode step (BASELINE.json configs[2]" +
-                (")" if args.wtype == 2 else ", its matrices in Q8_0)"))
+                (")" if args.wtype == 2 else ", its matrices in Q8_0)")) + \
+               ("; Q6_K token table tied to the LM head" if tied else "")
     line = {
         "metric": metric,
         "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -218,7 +225,8 @@ def main():
                    "kv_heads": cfg["n_head_kv"], "ffn": cfg["n_ff"], "vocab": cfg["n_vocab"], "page_cells": 64,
                    **({"experts": cfg["n_expert"], "experts_used": cfg["n_expert_used"], "expert_ffn": cfg["n_ff_exp"]}
                       if moe else {}),
-                   "gpu_ms_per_step": round(gpu_ms / args.steps, 4), "chain": bool(use_chain)},
+                   "gpu_ms_per_step": round(gpu_ms / args.steps, 4), "chain": bool(use_chain),
+                   "token_table": "Q6_K, tied LM head" if tied else f"F32, untied {q} LM head"},
         "roofline": roof(dom) if dom else None,
         "roofline_gemm": roof("gemm") if "gemm" in kernels else None,
         "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},

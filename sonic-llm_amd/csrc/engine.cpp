@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/sn.h"
@@ -60,7 +61,8 @@ struct sn_engine {
     bool has_nextn = false;
     // qwen3moe: experts, experts a token uses, an expert's FFN width; the tile bound of a step's expert rows
     int NE = 0, NEU = 0, FE = 0, moe_tiles = 0;
-    int wt = WT_Q4_0;  // the block type of every weight matrix: WT_Q4_0 or WT_Q8_0 (GGUF Q4_0 / Q8_0)
+    int wt = WT_Q4_0;  // the block type of every layer matrix: WT_Q4_0 or WT_Q8_0 (GGUF Q4_0 / Q8_0)
+    int head_t = WT_Q4_0;  // the LM head's: output.weight's, or token_embd's when tied (GGUF Q4_0, Q8_0 or Q6_K)
     size_t egu_stride = 0, ed_stride = 0;
     float *hn = nullptr, *rlog = nullptr, *mw = nullptr;  // normed rows, router logits, routing weights
     int32_t *mid = nullptr, *prow = nullptr, *rsrc = nullptr, *gitems = nullptr, *gcount = nullptr;
@@ -191,11 +193,13 @@ const GgufTensor* need(const GgufFile& g, const std::string& name, int type, std
     return t;
 }
 
-// a GGUF Q4_0 / Q8_0 matrix (ne = [K, N]) into tiles at dst (stripe stride / offset for interleaving)
+// a GGUF Q4_0 / Q8_0 matrix (ne = [K, N]) into tiles at dst (stripe stride / offset for interleaving); Q6_K (the
+// head) into its own tiles
 bool upload_q4(sn_engine* e, const GgufTensor* t, uint8_t* tmp, uint8_t* dst, int sstride, int soff, char* err,
                int err_len) {
     SN_HIP_TRY(hipMemcpyAsync(tmp, t->data, t->nbytes, hipMemcpyHostToDevice, e->st), false);
-    q4_repack(tmp, (int) t->ne[1], (int) t->ne[0], dst, sstride, soff, e->st, e->wt);
+    if (t->type == GGML_Q6_K) q6k_repack(tmp, (int) t->ne[1], (int) t->ne[0], dst, e->st);
+    else q4_repack(tmp, (int) t->ne[1], (int) t->ne[0], dst, sstride, soff, e->st, t->type == GGML_Q8_0 ? WT_Q8_0 : WT_Q4_0);
     SN_HIP_TRY(hipStreamSynchronize(e->st), false);
     return true;
 }
@@ -209,6 +213,77 @@ bool upload_q4_experts(sn_engine* e, const GgufTensor* t, uint8_t* tmp, uint8_t*
         q4_repack(tmp + x * src_stride, N, K, dst + x * dst_stride, sstride, soff, e->st, e->wt);
     SN_HIP_TRY(hipStreamSynchronize(e->st), false);
     return true;
+}
+
+// rows [r0, r0 + nr) of a token table as fp32: ggml's dequantize_row_q4_0 (x0 * d), _q8_0 (q * d) and _q6_K
+// ((d * scale) * (q - 32)), element for element
+void table_rows(const GgufTensor* t, int64_t r0, int64_t nr, float* out) {
+    const int64_t K = t->ne[0];
+    const size_t rb = ggml_row_bytes(t->type, K);
+    auto h2f = [](const uint8_t* p) {
+        _Float16 h;
+        memcpy(&h, p, 2);
+        return (float) h;
+    };
+    for (int64_t r = 0; r < nr; ++r) {
+        const uint8_t* row = t->data + (size_t) (r0 + r) * rb;
+        float* y = out + (size_t) r * K;
+        if (t->type == GGML_F32) {
+            memcpy(y, row, (size_t) K * 4);
+        } else if (t->type == GGML_Q4_0) {
+            for (int64_t b = 0; b < K / 32; ++b) {
+                const uint8_t* blk = row + b * 18;
+                const float d = h2f(blk);
+                for (int j = 0; j < 16; ++j) {
+                    y[32 * b + j] = (float) ((blk[2 + j] & 0x0F) - 8) * d;
+                    y[32 * b + j + 16] = (float) ((blk[2 + j] >> 4) - 8) * d;
+                }
+            }
+        } else if (t->type == GGML_Q8_0) {
+            for (int64_t b = 0; b < K / 32; ++b) {
+                const uint8_t* blk = row + b * 34;
+                const float d = h2f(blk);
+                for (int j = 0; j < 32; ++j) y[32 * b + j] = (float) (int8_t) blk[2 + j] * d;
+            }
+        } else {  // Q6_K
+            for (int64_t b = 0; b < K / 256; ++b) {
+                const uint8_t* blk = row + b * 210;
+                const float d = h2f(blk + 208);
+                const int8_t* sc = (const int8_t*) (blk + 192);
+                for (int e = 0; e < 256; ++e) {
+                    const int h = e >> 7, c = (e & 127) >> 5, l = e & 31;
+                    const uint8_t lb = blk[64 * h + 32 * (c & 1) + l];
+                    const int q = ((c < 2 ? lb & 15 : lb >> 4) | (((blk[128 + 32 * h + l] >> (2 * c)) & 3) << 4)) - 32;
+                    y[256 * b + e] = (d * (float) sc[e >> 4]) * (float) q;
+                }
+            }
+        }
+    }
+}
+
+// the token table on the device as fp32 rows (a quantized table dequantized once here: the gathers read fp32)
+float* upload_table(sn_engine* e, const GgufTensor* t, char* err, int err_len) {
+    const int64_t K = t->ne[0], V = t->ne[1];
+    float* d = e->dalloc<float>((size_t) V * K * 4, err, err_len);
+    if (!d) return nullptr;
+    const int64_t chunk = std::max<int64_t>(1, (64 << 20) / (K * 4));
+    std::vector<float> buf((size_t) std::min(chunk, V) * K);
+    const unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    for (int64_t r0 = 0; r0 < V; r0 += chunk) {
+        const int64_t nr = std::min(chunk, V - r0);
+        std::vector<std::thread> th;
+        for (unsigned k = 0; k < nt; ++k)
+            th.emplace_back([&, k] {
+                const int64_t a = nr * k / nt, b = nr * (k + 1) / nt;
+                table_rows(t, r0 + a, b - a, buf.data() + (size_t) a * K);
+            });
+        for (auto& x : th) x.join();
+        if (hipMemcpy(d + (size_t) r0 * K, buf.data(), (size_t) nr * K * 4, hipMemcpyHostToDevice) != hipSuccess) {
+            sn_set_err(err, err_len, "upload of %s failed", t->name.c_str());
+            return nullptr;
+        }
+    }
+    return d;
 }
 
 float* upload_f32(sn_engine* e, const GgufTensor* t, char* err, int err_len) {
@@ -250,8 +325,26 @@ bool model_check(const GgufFile& g, std::string* why) {
         *why = "embedding length must be a multiple of 32";
         return false;
     }
-    if (!g.find("output.weight")) {
-        *why = "an untied Q4_0 or Q8_0 output.weight is required";
+    // the token table: F32, Q4_0, Q8_0 or Q6_K; the head: output.weight, or the table when tied (sn_load.inc.h:341-352)
+    const GgufTensor* te = g.find("token_embd.weight");
+    const GgufTensor* to = g.find("output.weight");
+    const GgufTensor* tq = g.find("blk.0.attn_q.weight");
+    auto qtype = [](int t) { return t == GGML_Q4_0 || t == GGML_Q8_0 || t == GGML_Q6_K; };
+    if (!te || !(te->type == GGML_F32 || qtype(te->type))) {
+        *why = "token_embd must be F32, Q4_0, Q8_0 or Q6_K";
+        return false;
+    }
+    const GgufTensor* head = to ? to : te;
+    if (!qtype(head->type)) {
+        *why = to ? "output.weight must be Q4_0, Q8_0 or Q6_K" : "a tied LM head needs a Q4_0, Q8_0 or Q6_K token table";
+        return false;
+    }
+    if ((te->type == GGML_Q6_K || head->type == GGML_Q6_K) && E % 256) {
+        *why = "a Q6_K token table or head needs an embedding length that is a multiple of 256";
+        return false;
+    }
+    if (!tq || (tq->type != GGML_Q4_0 && tq->type != GGML_Q8_0)) {
+        *why = "the layer matrices must be Q4_0 or Q8_0";
         return false;
     }
     return true;
@@ -296,9 +389,10 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->QD = e->H * e->D;
     e->KD = e->KVH * e->D;
     e->NQKV = e->QD + 2 * e->KD;
-    const GgufTensor* emb = need(g, "token_embd.weight", GGML_F32, &why);
-    if (!emb) return fail(why);
-    e->wt = g.find("output.weight")->type == GGML_Q8_0 ? WT_Q8_0 : WT_Q4_0;  // every matrix must be of this type
+    const GgufTensor* emb = g.find("token_embd.weight");
+    const GgufTensor* head_t = g.find("output.weight") ? g.find("output.weight") : emb;  // no output: tied
+    e->wt = g.find("blk.0.attn_q.weight")->type == GGML_Q8_0 ? WT_Q8_0 : WT_Q4_0;  // every layer matrix is this type
+    e->head_t = head_t->type;
     e->V = (int) emb->ne[1];
     const char* pe = getenv("SN_PAGE");
     e->page_cells = pe && atoi(pe) == 32 ? 32 : 64;
@@ -342,11 +436,17 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
         ok = ok && d;
         return d;
     };
-    e->tok_embd = upload_f32(e, emb, err, err_len);
+    if (emb->ne[0] != E || head_t->ne[0] != E || head_t->ne[1] != e->V) {
+        hipFree(tmp);
+        return fail("token_embd / output.weight have unexpected dimensions");
+    }
+    e->tok_embd = upload_table(e, emb, err, err_len);
+    ok = ok && e->tok_embd;
     e->out_norm = f32("output_norm.weight", E);
-    if (const GgufTensor* t = ok ? q4("output.weight", e->V, E) : nullptr) {
-        e->head = e->dalloc<uint8_t>(wt_bytes(e->wt, e->V, E), err, err_len);
-        ok = e->head && upload_q4(e, t, tmp, e->head, 1, 0, err, err_len);
+    if (ok) {
+        e->head = e->dalloc<uint8_t>(e->head_t == GGML_Q6_K ? q6t_bytes(e->V, E) : wt_bytes(e->head_t, e->V, E), err,
+                                     err_len);
+        ok = e->head && upload_q4(e, head_t, tmp, e->head, 1, 0, err, err_len);
     }
     auto load_layer = [&](int i, DevLayer& l) {
         const std::string p = "blk." + std::to_string(i) + ".";
@@ -449,8 +549,10 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     if (RK > 4096) return fail("a MoE model's steps take at most 4096 / experts-used rows (max_rows)");
     e->moe_tiles = e->NE > 0 ? std::min(e->NE, RK) + (RK + 15) / 16 : 0;
     const int P = e->moe_tiles * 16;
-    e->xa = e->dalloc<uint8_t>(std::max(xa_bytes(R, KMAX), e->NE > 0 ? xa_bytes(P, std::max(E, e->FE)) : 0), err,
-                               err_len);
+    // xa also holds the Q6_K head's Q8_K records
+    e->xa = e->dalloc<uint8_t>(std::max({xa_bytes(R, KMAX), e->NE > 0 ? xa_bytes(P, std::max(E, e->FE)) : 0,
+                                         e->head_t == GGML_Q6_K ? xk_bytes(MO, E) : 0}),
+                               err, err_len);
     size_t ws = 0;
     ws = std::max(ws, q4_workspace_bytes(R, e->NQKV, E, e->wt));
     ws = std::max(ws, q4_workspace_bytes(R, E, QD, e->wt));
@@ -458,7 +560,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
         ws = std::max(ws, q4_workspace_bytes(R, 2 * F, E, e->wt));
         ws = std::max(ws, q4_workspace_bytes(R, E, F, e->wt));
     }
-    ws = std::max(ws, q4_workspace_bytes(MO, e->V, E, e->wt));
+    if (e->head_t != GGML_Q6_K) ws = std::max(ws, q4_workspace_bytes(MO, e->V, E, e->head_t));
     if (e->NE > 0) {
         ws = std::max(ws, (size_t) P * 2 * e->FE * 4);  // grouped expert matmuls: one slice
         ws = std::max(ws, (size_t) P * E * 4);
@@ -878,9 +980,8 @@ struct Dev {
     // drafts, greedy argmax into d_otok (and the probability records when on)
     void outputs(const float* x, int n, const int32_t* d_rows, const uint8_t* d_skip, const uint8_t* d_force = nullptr,
                  const int32_t* d_ftok = nullptr, int32_t* d_otok = nullptr, const float* hdnorm = nullptr) {
-        const int E = e->E, V = e->V;
-        quant(x, d_rows, n, E, hdnorm ? hdnorm : e->out_norm);
-        head_logits(n);
+        const int V = e->V;
+        head_logits(n, x, d_rows, hdnorm ? hdnorm : e->out_norm);
         if (d_force) force_rows(e->logits, V, n, d_force, d_ftok, st);
         const int nban = (int) e->eog.size();
         int32_t* out = d_otok ? d_otok : e->d_otok;
@@ -889,12 +990,30 @@ struct Dev {
                                e->d_amx, e->amx_bytes, st);
         });
     }
-    void head_logits(int n) {
-        const int E = e->E, V = e->V;
-        rc |= e->launch(SNX_K_GEMM, gemm_bytes(e->wt, n, V, E), [&] {
-            if (q4_plan(V, E, e->wt).ks == 1)  // one slice: the sums are the logits
-                return q4_gemm_raw(e->head, e->xa, n, V, E, e->logits, (size_t) n * V * 4, st, e->wt) < 0 ? -1 : 0;
-            return q4_gemm(e->head, e->xa, n, V, E, e->logits, V, EPI_STORE, e->gemm_ws, e->gemm_ws_bytes, st, e->wt);
+    // the LM head over rows `rows` (n of them; null: the first n) of x after the norm nw (null: x is normed): a Q4_0 /
+    // Q8_0 head from Q8_0 activations, a Q6_K head from Q8_K records (ggml's CPU operand for each type)
+    void head_logits(int n, const float* x, const int32_t* rows, const float* nw) {
+        const int E = e->E, V = e->V, ht = e->head_t;
+        if (ht == GGML_Q6_K) {
+            rc |= e->launch(SNX_K_QUANT, (double) n * E * 8, [&] {
+                quant_q8k(x, rows, n, E, E, nw, e->eps, e->xa, st);
+                return 0;
+            });
+            rc |= e->launch(SNX_K_GEMM, (double) V * (E / 256) * 210 + (double) n * E * 4 + (double) n * V * 4, [&] {
+                return q6k_gemm(e->head, e->xa, n, V, E, e->logits, V, st);
+            });
+            return;
+        }
+        quant(x, rows, n, E, nw);
+        head_logits_q(n);
+    }
+    // a Q4_0 / Q8_0 head over the xa operand's n rows
+    void head_logits_q(int n) {
+        const int E = e->E, V = e->V, ht = e->head_t;
+        rc |= e->launch(SNX_K_GEMM, gemm_bytes(ht, n, V, E), [&] {
+            if (q4_plan(V, E, ht).ks == 1)  // one slice: the sums are the logits
+                return q4_gemm_raw(e->head, e->xa, n, V, E, e->logits, (size_t) n * V * 4, st, ht) < 0 ? -1 : 0;
+            return q4_gemm(e->head, e->xa, n, V, E, e->logits, V, EPI_STORE, e->gemm_ws, e->gemm_ws_bytes, st, ht);
         });
     }
 
@@ -935,8 +1054,9 @@ struct Dev {
         gemm(e->mtp_eh, n, E, 2 * E);
         resid(e->mx, n, e->mtp.attn_norm, true, false);
         if (block(e->mtp, e->L, e->mx, n, S, al, d_seq, d_pos)) resid(e->mx, n, nullptr, false);
-        quant(e->mx, nullptr, n, E, e->mtp_hdnorm, e->mhg);
-        head_logits(n);
+        quant(e->mx, nullptr, n, E, e->mtp_hdnorm, e->mhg);  // mhg: the head's output state (the next row's input)
+        if (e->head_t == GGML_Q6_K) head_logits(n, e->mhg, nullptr, nullptr);
+        else head_logits_q(n);
         rc |= e->launch(SNX_K_OTHER, (double) n * e->V * 4, [&] {
             return argmax_rows(e->logits, e->V, n, e->d_ban, 0, nullptr, d_gout, nullptr, e->d_amx, e->amx_bytes, st);
         });

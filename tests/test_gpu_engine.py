@@ -51,11 +51,26 @@ def check_tokens(got, ref_tok, ref_logits, stats):
 
 
 def test_prefill_and_decode_match_oracle(tiny):
-    ref = O.Qwen3(GGUF(tiny), n_seq=4, ctx=256)
+    prefill_and_decode(tiny)
+
+
+@pytest.mark.parametrize("embd_type,tied,wtype", [(14, 1, 2), (14, 0, 8), (8, 1, 8), (2, 1, 2), (8, 0, 2)])
+def test_token_tables_and_tied_heads(tmp_path, embd_type, tied, wtype):
+    """Quantized token tables (Q4_0, Q8_0, Q6_K: dequantized at load, ggml's dequantize_row_* element for element) and
+    the LM head tied to them (sn_load.inc.h:341-352): Q6_K heads take Q8_K activations, as ggml's CPU path does."""
+    path = str(tmp_path / "t.gguf")
+    S.write_model(path, S.model_cfg(**TINY, embd_type=embd_type, tied=tied, wtype=wtype), seed=12)
+    g = GGUF(path)
+    assert ("output.weight" in g.tinfo) == (not tied)
+    prefill_and_decode(path)
+
+
+def prefill_and_decode(path):
+    ref = O.Qwen3(GGUF(path), n_seq=4, ctx=256)
     r = np.random.default_rng(0)
     lens = [40, 23]
     toks = [r.integers(0, TINY["n_vocab"], n).astype(np.int32) for n in lens]
-    with S.Engine(tiny, slots=4, ctx=256, max_rows=64) as eng:
+    with S.Engine(path, slots=4, ctx=256, max_rows=64) as eng:
         # one step of prompt rows for both sequences, outputs at their last rows
         tok = np.concatenate(toks)
         seq = np.concatenate([np.full(n, s, np.int32) for s, n in enumerate(lens)])

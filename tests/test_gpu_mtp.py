@@ -101,7 +101,23 @@ def test_guessing_leaves_the_model_alone(model):
         assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
 
 
+@pytest.fixture(scope="module")
+def model_q6k_tied(tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("model") / "mtp_q6k.gguf")
+    S.write_model(path, S.model_cfg(**TINY, embd_type=14, tied=1), seed=22)
+    return path
+
+
 def test_guesses_match_oracle(model):
+    guesses_match_oracle(model)
+
+
+def test_guesses_match_oracle_q6k_tied_head(model_q6k_tied):
+    """the guess head through a Q6_K token table tied to the LM head (its Q8_K operand from the head norm's rows)"""
+    guesses_match_oracle(model_q6k_tied)
+
+
+def guesses_match_oracle(model):
     n_seq = 6
     ps = prompts(n_seq, 2)
     ref = Ref(model, n_seq, 64)
@@ -170,7 +186,9 @@ def test_fused_step_equals_unfused(model):
         assert np.array_equal(a, b)
 
 
-def test_fused_step_matches_oracle(model):
+@pytest.mark.parametrize("which", ["model", "model_q6k_tied"])
+def test_fused_step_matches_oracle(request, which):
+    model = request.getfixturevalue(which)
     n_seq, steps = 4, 5
     ps = prompts(n_seq, 4)
     ref = Ref(model, n_seq, 64)
