@@ -67,20 +67,20 @@ void sn_set_err(char* err, int err_len, const char* fmt, ...);
 enum { WT_Q4_0 = 2, WT_Q8_0 = 8 };
 __host__ __device__ static inline int wt_tile_bytes(int wt) { return wt == WT_Q8_0 ? Q8T_BYTES : Q4T_BYTES; }
 
-// ---- Q6_K weights in HBM (csrc/q6k.hip): tiles of 16 rows x one 256-element block, 3360 bytes (= 16 x 210) --------
-#define Q6T_BYTES 3360
-#define Q6T_SCALE_OFF 3072
-#define Q6T_D_OFF 3328
-static inline size_t q6t_bytes(int N, int K) { return (size_t) ((N + 15) / 16) * (K / 256) * Q6T_BYTES; }
+// ---- Q6_K weights in HBM (csrc/q6k.hip): tiles of 32 rows x one 256-element block, 6720 bytes (= 32 x 210) --------
+#define Q6T_ROWS 32
+#define Q6T_BYTES 6720
+#define Q6T_SCALE_OFF 6144
+#define Q6T_D_OFF 6656
+static inline size_t q6t_bytes(int N, int K) { return (size_t) ((N + 31) / 32) * (K / 256) * Q6T_BYTES; }
 
-// ---- Q8_K activation records ("xk", the Q6_K matmul's operand): one 9280-byte record per (16-row tile, 256-block):
-//   [G * 512, +512)     group G's fragment: lane l = m + 16 g holds row m's q of elements 16 G + 4 g .. + 3 (fp16);
-//   [8192 + G * 64, +64) the 16 rows' corrections -1056 * (sum of q over group G) (fp32, exact);
-//   [9216, +64)          the 16 rows' d (fp32, 1 / iscale of quantize_row_q8_K_ref).
+// ---- Q8_K activation records ("xk", the Q6_K matmul's operand): one 8320-byte record per (32-row tile, 256-block):
+//   [G * 512, +512)  group G's fragment: lane l = m + 32 h holds row m's int8 q of elements 16 G + 8 h .. + 7;
+//   [8192, +128)     the 32 rows' d (fp32, 1 / iscale of quantize_row_q8_K_ref).
 // Row tiles are rounded up to an even count.
-#define XK_REC 9280
-#define XK_CORR_OFF 8192
-#define XK_D_OFF 9216
+#define XK_REC 8320
+#define XK_D_OFF 8192
+__host__ __device__ static inline int xk_tiles(int M) { return (M + 63) / 64 * 2; }
 
 // ---- activation operand ("xa"): Q8_0-quantized rows as fp16 MFMA fragments -----------------------------------------
 // Rows are quantized to Q8_0 exactly as ggml's x86 CPU backend does (per 32-block: d = amax/127 stored fp16,
@@ -112,9 +112,9 @@ __host__ __device__ static inline size_t xa_rec_off(int K, int m, int b) {
 }
 __host__ __device__ static inline size_t xa_bytes(int M, int K) { return (size_t) xa_mtp(M) * xa_ngroups(K) * XA_REC; }
 __host__ __device__ static inline size_t xk_rec_off(int K, int m, int b) {
-    return ((size_t) (m >> 4) * (K / 256) + b) * XK_REC;
+    return ((size_t) (m >> 5) * (K / 256) + b) * XK_REC;
 }
-__host__ __device__ static inline size_t xk_bytes(int M, int K) { return (size_t) xa_mtp(M) * (K / 256) * XK_REC; }
+__host__ __device__ static inline size_t xk_bytes(int M, int K) { return (size_t) xk_tiles(M) * (K / 256) * XK_REC; }
 static inline size_t q4t_bytes(int N, int K) { return (size_t) ((N + 15) / 16) * ((K / 32 + 3) / 4) * Q4T_BYTES; }
 // bytes of an N x K matrix of weight type wt in the tile layout
 static inline size_t wt_bytes(int wt, int N, int K) {

@@ -57,16 +57,15 @@ def gemm_q6k(t, xk, M, N, K):
 
 
 def xk_decode(xk, M, K):
-    """the records back to (q [M][K] int, d [M][K/256], corr [M][K/16]): undoes the fragment order (lane m + 16 g holds
-    row m's elements 16 G + 4 g .. + 3 of group G)"""
+    """the records back to (q [M][K] int, d [M][K/256]): undoes the fragment order (lane m + 32 h of group G's fragment
+    holds row m's int8 q of elements 16 G + 8 h .. + 7)"""
     nb = K // 256
-    mt = (M + 15) // 16
-    rec = U.host(xk, np.uint8)[:mt * nb * 9280].reshape(mt, nb, 9280)
-    frag = rec[:, :, :8192].copy().view(np.float16).reshape(mt, nb, 16, 4, 16, 4).astype(np.float32)  # [mt][b][G][g][m][j]
-    q = frag.transpose(0, 4, 1, 2, 3, 5).reshape(mt * 16, K)[:M].astype(np.int64)
-    corr = rec[:, :, 8192:9216].copy().view(np.float32).reshape(mt, nb, 16, 16).transpose(0, 3, 1, 2).reshape(mt * 16, nb * 16)[:M]
-    d = rec[:, :, 9216:9280].copy().view(np.float32).reshape(mt, nb, 16).transpose(0, 2, 1).reshape(mt * 16, nb)[:M]
-    return q, d, corr
+    mt = (M + 31) // 32
+    rec = U.host(xk, np.uint8)[:mt * nb * 8320].reshape(mt, nb, 8320)
+    frag = rec[:, :, :8192].copy().view(np.int8).reshape(mt, nb, 16, 2, 32, 8)  # [mt][b][G][h][m][j]
+    q = frag.transpose(0, 4, 1, 2, 3, 5).reshape(mt * 32, K)[:M].astype(np.int64)
+    d = rec[:, :, 8192:8320].copy().view(np.float32).reshape(mt, nb, 32).transpose(0, 2, 1).reshape(mt * 32, nb)[:M]
+    return q, d
 
 
 def test_q6k_dequant_bit_exact():
@@ -92,24 +91,23 @@ def test_q8k_activations_bit_exact():
     X[3, 300], X[3, 301] = 4.0, -4.0  # equal |x|: the first is the extreme
     X[4, 256:512] = 0.0  # an all-zero block
     X[5, :] = 0.0
-    q, d, corr = xk_decode(xk_gpu(X), M, K)
+    q, d = xk_decode(xk_gpu(X), M, K)
     want = O.quantize_q8_K(X).reshape(M, K // 256, 292)
     wq = want[:, :, 4:260].copy().view(np.int8).reshape(M, K).astype(np.int64)
     wd = want[:, :, :4].copy().view(np.float32).reshape(M, K // 256)
-    wbs = want[:, :, 260:292].copy().view(np.int16).reshape(M, K // 16).astype(np.float32)
     assert np.array_equal(q, wq)
     assert np.array_equal(d.view(np.uint32), wd.view(np.uint32))
-    assert np.array_equal(corr, -1056.0 * wbs)
     # with the output norm fused: the quantizer of the normed rows (the norm to fp32 rounding)
     nw = (1 + 0.1 * r.standard_normal(K)).astype(np.float32)
-    qn, dn, _ = xk_decode(xk_gpu(X, nw), M, K)
+    qn, dn = xk_decode(xk_gpu(X, nw), M, K)
     Xn = O.rmsnorm(X, nw, 1e-6)
     wn = O.quantize_q8_K(Xn).reshape(M, K // 256, 292)
     diff = np.abs(qn - wn[:, :, 4:260].copy().view(np.int8).reshape(M, K).astype(np.int64))
     assert diff.max() <= 1 and (diff > 0).mean() < 1e-3  # one-step flips where the norm's last bit differs
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (8, 4096, 2560), (32, 5000, 1024), (17, 2049, 768), (33, 300, 512)])
+@pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (8, 4096, 2560), (32, 5000, 1024), (17, 2049, 768), (33, 300, 512),
+                                   (64, 1000, 512), (100, 777, 256)])
 def test_q6k_matmul_vs_oracle(M, N, K):
     r = np.random.default_rng(M * 7 + N)
     Wq = random_q6k(r, N, K)
