@@ -84,9 +84,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--model", default=None, help="GGUF path (generated when missing)")
     ap.add_argument("--seed", type=int, default=42)
-    ap.add_argument("--config", default="decode", choices=("decode", "mtp", "moe"),
+    ap.add_argument("--config", default="decode", choices=("decode", "mtp", "moe", "matmul", "attn"),
                     help="decode: the headline (configs[2]); mtp: the fused draft-verify step (configs[3]); "
-                         "moe: Qwen3-30B-A3B-arch batched decode (configs[4])")
+                         "moe: Qwen3-30B-A3B-arch batched decode (configs[4]); matmul: one 8 x 4096 x 4096 Q4_0 "
+                         "matmul (configs[0]); attn: one layer of paged decode attention (configs[1])")
     ap.add_argument("--accept", type=float, default=0.6, help="mtp: the seeded share of drafts forced to match")
     ap.add_argument("--no-graphs", action="store_true", help="launch every step eagerly (no HIP graph replay)")
     ap.add_argument("--no-chain", action="store_true", help="decode without sn_step's queued successor (chain = 0)")
@@ -123,6 +124,10 @@ def main():
 
     if args.config == "mtp":
         return bench_mtp(args)
+    if args.config == "matmul":
+        return bench_matmul(args)
+    if args.config == "attn":
+        return bench_attn(args)
     moe = args.config == "moe"
     cfg = dict(S.QWEN3_30B_A3B if moe else S.QWEN3_4B)
     if args.wtype == 8:
@@ -283,7 +288,7 @@ def bench_mtp(args):
     log(f"[bench] {args.steps} spec steps: {dt * 1e3 / args.steps:.3f} ms/step, {toks / args.steps:.2f} tokens/step")
     eng.prof(True)
     for _ in range(args.prof_steps):
-        step(0)
+        step()
     prof = eng.prof_read()
     eng.prof(False)
     eng.close()
@@ -291,9 +296,12 @@ def bench_mtp(args):
     for name, p in prof.items():
         if p["launches"]:
             gbs = p["bytes"] / (p["ms"] * 1e-3) / 1e9
-            kernels[name] = {"ms_per_step": round(p["ms"] / args.prof_steps, 4),
-                             "launches_per_step": p["launches"] / args.prof_steps,
+            kernels[name] = {"ms_per_step": round(p["ms"] / max(args.prof_steps, 1), 4),
+                             "launches_per_step": p["launches"] / max(args.prof_steps, 1),
+                             "bytes_per_launch": round(p["bytes"] / p["launches"]),
+                             "us_per_launch": round(1e3 * p["ms"] / p["launches"], 2),
                              "GBps": round(gbs, 1), "frac": round(gbs * 1e9 / HBM_PEAK, 4)}
+    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"]) if kernels else None
     line = {
         "metric": "MTP draft+verify tok/s, Qwen3-4B-arch Q4_0 + 1 Q4_0 guess-head block, 8 seqs x 4096, k=3",
         "value": round(toks / dt, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -304,8 +312,279 @@ def bench_mtp(args):
         "config": {"workload": "fused MTP draft+verify step (BASELINE.json configs[3])", "seqs": B, "ctx": ctx,
                    "drafts": k, "verify_rows": B * (k + 1), "tokens_per_step": round(toks / args.steps, 3),
                    "gpu_ms_per_step": round(gpu_ms / args.steps, 4)},
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": kernels[dom]["GBps"], "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": kernels[dom]["frac"], "traffic": None,
+                     "bytes_per_launch": kernels[dom]["bytes_per_launch"],
+                     "us_per_launch": kernels[dom]["us_per_launch"]} if dom else None,
         "kernels": kernels,
+        "cpu_baseline": None,
     }
+    print(json.dumps(line), flush=True)
+
+
+def graph_us(fn, n, reps=10):
+    """Device time (microseconds) of one of n calls fn(i, stream) captured into a HIP graph (torch.cuda.graph: the
+    launches replay back to back with no host launch cost), timed with HIP events over `reps` replays."""
+    import ctypes as C
+
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for i in range(n):
+            fn(i, st)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps / n
+
+
+def cpu_threads():
+    return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count())
+
+
+class Dev:
+    """Device buffers through torch (allocation and streams only): the kernel ABI takes plain pointers."""
+
+    @staticmethod
+    def copy(a):
+        import numpy as np
+        import torch
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1).copy()).to("cuda")
+
+    @staticmethod
+    def empty(nbytes):
+        import torch
+        return torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device="cuda")
+
+    @staticmethod
+    def host(t, dtype):
+        import torch
+        torch.cuda.synchronize()
+        return t.cpu().numpy().view(dtype)
+
+    @staticmethod
+    def ptr(t):
+        import ctypes as C
+        return C.c_void_p(t.data_ptr())
+
+    @staticmethod
+    def stream():
+        import ctypes as C
+
+        import torch
+        return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def bench_matmul(args):
+    """configs[0] (C1): one Q4_0 matmul Y[8][4096] = X[8][4096] . W[4096][4096]^T. W ~ N(0, 0.02) (seed 1) quantized
+    by ggml's reference Q4_0 rule, X ~ N(0, 1). One call is the op as a drop-in runs it: X quantized to the Q8_0 operand,
+    the matmul's k-slices, their reduction into Y. 40 copies of W (377 MB, beyond the 256 MB Infinity Cache) are used
+    in turn; the calls replay from a HIP graph. value = algorithmic bytes (W + X + Y) per call / time per call."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    import sllm_next as S
+
+    U = Dev
+    L = S.lib()
+    N = K = 4096
+    M = 8
+    r = np.random.default_rng(1)
+    Wq = S.quantize_q4_0((r.standard_normal((N, K)) * 0.02).astype(np.float32))
+    X = r.standard_normal((M, K)).astype(np.float32)
+    copies = 40
+    st0 = U.stream()
+    dW = U.copy(Wq)
+    tiles = [U.empty(L.snk_q4_stripes_bytes(N, K)) for _ in range(copies)]
+    for t in tiles:
+        assert L.snk_q4_repack(U.ptr(dW), N, K, U.ptr(t), st0) == 0
+    dX = U.copy(X)
+    xa = U.empty(L.snk_xa_bytes(M, K))
+    wsb = L.snk_q4_workspace_bytes(M, N, K)
+    ws = U.empty(wsb)
+    y = U.empty(M * N * 4)
+    torch.cuda.synchronize()
+
+    def op(i, st):
+        L.snk_quant_act(U.ptr(dX), M, K, K, None, C.c_float(0.0), U.ptr(xa), st)
+        L.snk_q4_gemm(U.ptr(tiles[i % copies]), U.ptr(xa), M, N, K, U.ptr(y), N, 0, U.ptr(ws), C.c_size_t(wsb), st)
+
+    for _ in range(args.warmup):
+        op(0, st0)
+    torch.cuda.synchronize()
+    n = max(copies, args.steps)
+    us = graph_us(op, n)
+    # the matmul kernel alone (its k-slice sums, launches timed with HIP events on the stream they run on)
+    ptrs = (C.c_void_p * copies)(*[t.data_ptr() for t in tiles])
+    us_gemm = L.snk_q4_gemm_time(C.cast(ptrs, C.c_void_p), copies, U.ptr(xa), M, N, K, U.ptr(y), N, U.ptr(ws), C.c_size_t(wsb), 200, st0)
+    alg = N * K // 32 * 18 + M * K * 4 + M * N * 4
+    got = U.host(y, np.float32)[:M * N].reshape(M, N)
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        O.build() if not os.path.exists(O.LIB_PATH) else None
+        nt = cpu_threads()
+        t = time.perf_counter()
+        reps = 0
+        while True:
+            want = O.mul_mat_q4_0(Wq, K, X, nthreads=nt)
+            reps += 1
+            if time.perf_counter() - t > 10.0:
+                break
+        dt = (time.perf_counter() - t) / reps
+        err = float(np.abs(got - want).max())
+        log(f"[bench] max |GPU - oracle| {err:.3g} (max |y| {float(np.abs(want).max()):.3g})")
+        cpu = {"value": round(alg / dt / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+               "sample": f"the same 8 x 4096 x 4096 matmul through oracle/oracle.c (ggml-semantics CPU restatement: "
+                         f"Q8_0 activations, integer block dots), {reps} calls in {dt * reps:.1f} s on {nt} threads"}
+    gbs, gbs_k = alg / (us * 1e-6) / 1e9, alg / (us_gemm * 1e-6) / 1e9
+    log(f"[bench] C1 matmul: {us:.2f} us per call (quantize + matmul + reduce), matmul kernel {us_gemm:.2f} us")
+    line = {
+        "metric": "Q4_0 matmul GB/s (algorithmic W + X + Y bytes), 8 x 4096 x 4096",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": n, "warmup": args.warmup,
+        "ms_per_step": round(us * 1e-3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_0 x q8_0 -> f32 (fp16 MFMA)",
+        "data": "synthetic: W ~ N(0, 0.02) seed 1 quantized to Q4_0 (ggml reference rule), X ~ N(0, 1)",
+        "config": {"workload": "single Q4_0 matmul (BASELINE.json configs[0])", "M": M, "N": N, "K": K,
+                   "weight_copies": copies, "algorithmic_bytes": alg, "us_per_call": round(us, 3),
+                   "us_matmul_kernel": round(us_gemm, 3)},
+        "roofline": {"kernel": "k_q4_gemm", "bound": "hbm", "achieved": round(gbs_k, 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(gbs_k * 1e9 / HBM_PEAK, 4), "traffic": None,
+                     "bytes_per_launch": alg, "us_per_launch": round(us_gemm, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def config2_case(seed=2, n_seq=32, page=32, lo=256, hi=4096, n_share=8, share_cells=1024):
+    """configs[1] (C2): contexts ~ U[lo, hi] (the n_share sharers' from [share_cells, hi], so each holds the whole
+    shared prefix), the page table a seeded permutation of one pool, sequences 0 .. n_share - 1 sharing the pages of
+    their first share_cells cells. Returns (ctx, page table [n_seq][max_pages] (-1: none), pool pages)."""
+    import numpy as np
+    r = np.random.default_rng(seed)
+    ctx = r.integers(lo, hi + 1, n_seq)
+    ctx[:n_share] = r.integers(share_cells, hi + 1, n_share)
+    maxp = (hi + page - 1) // page
+    sp = share_cells // page
+    npages = [(c + page - 1) // page for c in ctx]
+    need = sum(npages) - (n_share - 1) * sp if n_share else sum(npages)
+    perm = r.permutation(need).astype(np.int32)
+    pt = np.full((n_seq, maxp), -1, np.int32)
+    nxt = 0
+    shared = perm[:sp] if n_share else None
+    if n_share:
+        nxt = sp
+    for s in range(n_seq):
+        for c in range(npages[s]):
+            if s < n_share and c < sp:
+                pt[s, c] = shared[c]
+            else:
+                pt[s, c] = perm[nxt]
+                nxt += 1
+    return ctx, pt, need
+
+
+def bench_attn(args):
+    """configs[1] (C2): paged GQA decode attention, one layer: 32 sequences, 32 query heads, 8 KV heads, head_dim 128,
+    contexts ~ U[256, 4096] (seed 2), fp16 K/V ~ N(0, 1) in 32-cell pages of one pool (a seeded permutation), 8
+    sequences sharing the pages of their first 1024 cells; q ~ N(0, 1), scale 1/sqrt(128). One row per sequence at
+    its last position. 3 pool copies (beyond the Infinity Cache) are used in turn; launches replay from a HIP graph.
+    value = unique algorithmic bytes (every cell once, shared pages once; q, output, page-table entries) / time."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    import sllm_next as S
+
+    U = Dev
+    L = S.lib()
+    H, KVH, D, page = 32, 8, 128, 32
+    n_seq, n_share, share = 32, 8, 1024
+    ctx, pt, need = config2_case(page=page, n_seq=n_seq, n_share=n_share, share_cells=share)
+    seq = np.arange(n_seq, dtype=np.int32)
+    pos = (ctx - 1).astype(np.int32)
+    r = np.random.default_rng(3)
+    q = r.standard_normal((n_seq, H, D), dtype=np.float32)
+    copies = 3
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2)
+    pools = [(torch.randn(need * KVH * page * D, generator=gen, device="cuda").half(),
+              torch.randn(need * KVH * page * D, generator=gen, device="cuda").half()) for _ in range(copies)]
+    dpt, dq = U.copy(pt), U.copy(q)
+    out = U.empty(n_seq * H * D * 4)
+    err = C.create_string_buffer(256)
+    plan = L.snk_attn_new_mode(n_seq, seq.ctypes.data, pos.ctypes.data, H, KVH, pt.shape[1], page, args.attn_mode, err,
+                               256)
+    assert plan, err.value
+    whole = bool(L.snk_attn_whole(plan))
+    scale = C.c_float(1.0 / np.sqrt(D))
+
+    def run(i, st):
+        kp, vp = pools[i % copies]
+        L.snk_attn_run(plan, U.ptr(dq), H * D, U.ptr(kp), U.ptr(vp), U.ptr(dpt), scale, U.ptr(out), H * D, st)
+
+    st0 = U.stream()
+    for _ in range(args.warmup):
+        run(0, st0)
+    torch.cuda.synchronize()
+    n = max(36, args.steps)
+    us = graph_us(run, n)
+    cells = int(ctx.sum()) - int(np.minimum(ctx[1:n_share], share).sum())
+    pages = int(sum((c + page - 1) // page for c in ctx))
+    alg = cells * KVH * D * 2 * 2 + 2 * n_seq * H * D * 4 + 4 * pages
+    alg_per_seq = int(ctx.sum()) * KVH * D * 2 * 2 + 2 * n_seq * H * D * 4 + 4 * pages
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        O.build() if not os.path.exists(O.LIB_PATH) else None
+        kp, vp = pools[0]
+        kh = kp.cpu().numpy().view(np.uint16).reshape(need, KVH, page, D)
+        vh = vp.cpu().numpy().view(np.uint16).reshape(need, KVH, page, D)
+        run(0, st0)
+        got = U.host(out, np.float32)[:n_seq * H * D].reshape(n_seq, H, D)
+        nt = cpu_threads()
+        t = time.perf_counter()
+        reps = 0
+        while True:
+            want = O.paged_attn(q, seq, pos, KVH, kh, vh, page, pt, 1.0 / np.sqrt(D), nthreads=nt)
+            reps += 1
+            if time.perf_counter() - t > 10.0:
+                break
+        dt = (time.perf_counter() - t) / reps
+        log(f"[bench] max |GPU - oracle| {float(np.abs(got - want).max()):.3g}")
+        cpu = {"value": round(alg / dt / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+               "sample": f"the same 32-row attention through oracle/oracle.c (fp32 softmax over fp16 cells), "
+                         f"{reps} calls in {dt * reps:.1f} s on {nt} threads"}
+    gbs = alg / (us * 1e-6) / 1e9
+    kern = "k_attn_whole" if whole else "k_attn_part + k_attn_merge"
+    log(f"[bench] C2 attention: {us:.2f} us per launch ({kern}), {alg / 1e6:.1f} MB unique, "
+        f"{alg_per_seq / 1e6:.1f} MB counting shared pages per sequence")
+    line = {
+        "metric": "paged GQA decode attention GB/s (unique algorithmic bytes), 32 seqs, ctx U[256,4096], 32-cell pages",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": n, "warmup": args.warmup,
+        "ms_per_step": round(us * 1e-3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 K/V, f32 q / softmax / output (fp16 MFMA with split operands)",
+        "data": "synthetic: contexts U[256, 4096] seed 2 (sharers' from [1024, 4096]), K/V ~ N(0, 1) fp16, q ~ N(0, 1)",
+        "config": {"workload": "paged GQA decode attention, one layer (BASELINE.json configs[1])", "seqs": n_seq,
+                   "heads": H, "kv_heads": KVH, "page_cells": page, "shared_prefix_seqs": n_share,
+                   "shared_prefix_cells": share, "mean_ctx": round(float(ctx.mean()), 1), "form": kern,
+                   "unique_bytes": alg, "bytes_counting_shared_per_seq": alg_per_seq,
+                   "GBps_counting_shared_per_seq": round(alg_per_seq / (us * 1e-6) / 1e9, 1)},
+        "roofline": {"kernel": kern, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(gbs * 1e9 / HBM_PEAK, 4), "traffic": None,
+                     "bytes_per_launch": alg, "us_per_launch": round(us, 3)},
+        "cpu_baseline": cpu,
+    }
+    L.snk_attn_free(plan)
     print(json.dumps(line), flush=True)
 
 

@@ -79,7 +79,7 @@ double snk_attn_time(snk_attn* p, const float* d_q, int ldq, const void* d_kpool
 snk_attn* snk_attn_new_mode(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH, int max_pages,
                             int page_cells, int mode, char* err, int err_len);
 // 1 when the list is whole groups (one workgroup per (group, KV head) walks its whole context and writes the output:
-// one launch, no merge; chosen when the groups make one round of 240 .. 256 workgroups, no context is over twice the
+// one launch, no merge; chosen when the groups make one round of 240 .. 256 workgroups, no context is over 9/8 of the
 // mean and the contexts are long), 0 when it is one item per 256-cell chunk followed by the merge. Both give the same
 // bits for a row.
 int snk_attn_whole(const snk_attn* p);

@@ -457,11 +457,12 @@ int paged_attention(const AttnArgs& a, hipStream_t st) {
 }
 
 // The work list (see sn_kernels_internal.h). Whole groups when they make one round of workgroups on the 256 CUs
-// (240 .. 256), no group's context is over twice the mean, and the contexts are long: at least 10 chunks on average,
+// (240 .. 256), no group's context is over 9/8 of the mean, and the contexts are long: at least 10 chunks on average,
 // or 5 with 32-cell pages. Measured on MI355X (32 sequences, K/V beyond the Infinity Cache), whole groups beat chunk
-// items plus merge by 10-20% at 12-16 chunks and at 32-cell pages, and lose 2-8% at 4 and 8 chunks of 64-cell pages
-// and whenever the groups are not one round (16 or 48 sequences). Otherwise one item per (group, 256-cell chunk) and
-// the merge folds every row's chunks.
+// items plus merge by 10-20% at 12-16 chunks and at 32-cell pages when the contexts are alike, and lose 2-8% at 4 and
+// 8 chunks of 64-cell pages and whenever the groups are not one round (16 or 48 sequences). A whole-group launch lasts
+// as long as its longest context: at contexts U[256, 4096] (longest 1.7x the mean) it took 81.5 us against 66.0 for
+// chunk items. Otherwise one item per (group, 256-cell chunk) and the merge folds every row's chunks.
 void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, int page_cells, AttnPlan& p, int mode) {
     const int gmax = 16 / (H / KVH);
     p.groups.clear();
@@ -483,7 +484,7 @@ void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, in
     const long wg = (long) ng * KVH;
     const bool long_ctx = tot >= (page_cells == 32 ? 5L : 10L) * ng;
     p.whole = mode >= 0 ? mode == 1
-                        : wg >= ATT_WHOLE_MIN_WG && wg <= ATT_WHOLE_MAX_WG && (long) mx * ng <= 2L * tot && long_ctx;
+                        : wg >= ATT_WHOLE_MIN_WG && wg <= ATT_WHOLE_MAX_WG && 8L * mx * ng <= 9L * tot && long_ctx;
     for (int gi = 0; gi < ng; ++gi) {
         const AttnGroup& gr = p.groups[gi];
         const int nc = (gr.pos0 + gr.nrows - 1) / ATT_CHUNK + 1;

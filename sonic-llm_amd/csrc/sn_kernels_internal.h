@@ -114,7 +114,7 @@ struct AttnArgs {
 int paged_attention(const AttnArgs& a, hipStream_t st);
 // The work list of R rows: consecutive rows of one sequence at consecutive positions share a group (up to 16/G rows:
 // their K/V loads are shared). Whole groups (one item each, walked by one workgroup per KV head) when the groups give
-// one round of ATT_WHOLE_MIN_WG .. ATT_WHOLE_MAX_WG workgroups, the longest context is at most twice the mean and the
+// one round of ATT_WHOLE_MIN_WG .. ATT_WHOLE_MAX_WG workgroups, the longest context is at most 9/8 of the mean and the
 // contexts are long; otherwise one item per (group, 256-cell chunk), every row merged. Both fold a row's chunk
 // partials in the same order with the same arithmetic, so a row's output does not depend on which list it was in.
 #define ATT_WHOLE_MIN_WG 240

@@ -145,13 +145,13 @@ def test_page_placement_does_not_matter():
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("page,lo,hi,auto", [(32, 256, 4096, True), (64, 200, 700, False), (32, 1, 300, False),
-                                            (64, 2560, 4096, True)])
+@pytest.mark.parametrize("page,lo,hi,auto", [(32, 256, 4096, False), (64, 200, 700, False), (32, 1, 300, False),
+                                            (64, 2560, 4096, False), (32, 3000, 3100, True), (64, 2560, 2600, True)])
 def test_whole_group_list_equals_chunk_list_bitwise(page, lo, hi, auto):
     """The two forms of the work list on the same 32 rows: whole groups (one workgroup walks a row's whole context and
     writes its output, no merge) and per-chunk items with the merge. The outputs are the same bits (the chunk partials
     are folded in the same order with the same arithmetic), they match the oracle, and the planner picks whole groups
-    for these 32 x 8 workgroups exactly when the contexts are long (auto)."""
+    for these 32 x 8 workgroups exactly when the contexts are long and alike (auto)."""
     q, seq, pos, kp, vp, pt, pg = config2_case(seed=11 + lo, S_=32, page=page, lo=lo, hi=hi, n_share=0)
     scale = 1 / math.sqrt(D)
     bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
