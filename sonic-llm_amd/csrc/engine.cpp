@@ -377,6 +377,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->H = (int) g.num(a + ".attention.head_count", 0);
     e->KVH = (int) g.num(a + ".attention.head_count_kv", 0);
     e->F = (int) g.num(a + ".feed_forward_length", 0);
+    if (e->has_nextn && e->E > 4096) return fail("the guess head takes an embedding length of at most 4096");
     if (a == "qwen3moe") {
         e->NE = (int) g.num(a + ".expert_count", 0);
         e->NEU = (int) g.num(a + ".expert_used_count", 0);

@@ -338,31 +338,55 @@ __device__ __forceinline__ float row_sumsq256(const float* x, int n, float* red)
 
 // The head's input rows [enorm(embed(tok)); hnorm(h)] (sn_cache.inc.h:357-363, sn_state.inc.h:294-305), h the row's
 // hidden state before it: src NULL: hrows row r when hrows is given, else the slot's kept state pend[seq]; with src:
-// src[r] >= 0 row src[r] of hrows, -1 pend[seq[r]], -2 none (zeros: a sequence's first cell).
+// src[r] >= 0 row src[r] of hrows, -1 pend[seq[r]], -2 none (zeros: a sequence's first cell). Both rows (E <=
+// 256 MTP_CAT_J) are loaded before either sum of squares is reduced: one latency period, not two; each sum keeps the
+// per-thread order and reduction of row_sumsq256.
+#define MTP_CAT_J 16
 __global__ __launch_bounds__(256) void k_mtp_cat(const float* __restrict__ table, int E, const int32_t* __restrict__ tok,
                                                  const float* __restrict__ hrows, const float* __restrict__ pend,
                                                  const int32_t* __restrict__ src, const int32_t* __restrict__ seq,
                                                  const float* __restrict__ enorm, const float* __restrict__ hnorm,
                                                  float eps, float* __restrict__ cat) {
-    __shared__ float red[4];
-    const int r = blockIdx.x;
+    __shared__ float red[2][4];
+    const int r = blockIdx.x, t = threadIdx.x;
     const float* em = table + (size_t) tok[r] * E;
     const int s = src ? src[r] : (hrows ? r : -1);
     const float* h = s >= 0 ? hrows + (size_t) s * E : s == -1 ? pend + (size_t) seq[r] * E : nullptr;
     float* y = cat + (size_t) r * 2 * E;
-    const float se = 1.0f / sqrtf(row_sumsq256(em, E, red) / (float) E + eps);
-    for (int i = threadIdx.x; i < E; i += 256) y[i] = (em[i] * se) * enorm[i];
-    if (!h) {
-        for (int i = threadIdx.x; i < E; i += 256) y[E + i] = 0.0f;
-        return;
+    float ve[MTP_CAT_J], vh[MTP_CAT_J];
+    for (int j = 0; j < MTP_CAT_J; ++j) {
+        const int i = t + 256 * j;
+        ve[j] = i < E ? em[i] : 0.0f;
+        vh[j] = h && i < E ? h[i] : 0.0f;
     }
-    const float sh = 1.0f / sqrtf(row_sumsq256(h, E, red) / (float) E + eps);
-    for (int i = threadIdx.x; i < E; i += 256) y[E + i] = (h[i] * sh) * hnorm[i];
+    float se = 0.0f, sh = 0.0f;
+    for (int j = 0; j < MTP_CAT_J; ++j)
+        if (t + 256 * j < E) {
+            se += ve[j] * ve[j];
+            sh += vh[j] * vh[j];
+        }
+    for (int o = 32; o > 0; o >>= 1) {
+        se += __shfl_xor(se, o);
+        sh += __shfl_xor(sh, o);
+    }
+    if ((t & 63) == 0) {
+        red[0][t >> 6] = se;
+        red[1][t >> 6] = sh;
+    }
+    __syncthreads();
+    const float ie = 1.0f / sqrtf(((red[0][0] + red[0][1]) + (red[0][2] + red[0][3])) / (float) E + eps);
+    const float ih = 1.0f / sqrtf(((red[1][0] + red[1][1]) + (red[1][2] + red[1][3])) / (float) E + eps);
+    for (int j = 0; j < MTP_CAT_J; ++j) {
+        const int i = t + 256 * j;
+        if (i >= E) break;
+        y[i] = (ve[j] * ie) * enorm[i];
+        y[E + i] = h ? (vh[j] * ih) * hnorm[i] : 0.0f;
+    }
 }
 
 void mtp_cat(const float* table, int E, const int32_t* tok, const float* hrows, const float* pend, const int32_t* src,
              const int32_t* seq, const float* enorm, const float* hnorm, float eps, float* cat, int R, hipStream_t st) {
-    if (R > 0)
+    if (R > 0 && E <= 256 * MTP_CAT_J)
         hipLaunchKernelGGL(k_mtp_cat, dim3(R), dim3(256), 0, st, table, E, tok, hrows, pend, src, seq, enorm, hnorm, eps,
                            cat);
 }
