@@ -509,8 +509,12 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
     a.M = M; a.N = N; a.K = K; a.ldy = 0; a.epi = EPI_STORE;
     a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
     a.mtiles = (M + 15) / 16;
-    const int mt = a.mtiles == 1 ? 1 : 2;
-    const dim3 grid(p.sets, p.ks, mt == 1 ? 1 : (a.mtiles + 1) / 2);
+    // row tiles of 16 per workgroup (grid z: one per tile) for matrices narrower than 512 stripes: twice the
+    // workgroups and loads in flight (q|k|v, o, down: 8.4 against 9.1 us at 32 rows; the second tile's weight reads
+    // mostly hit the Infinity Cache); pairs of tiles for the wide ones (gate|up, the LM head), where single tiles were
+    // slower. Either way a row's sums are the same (same slices, same order).
+    const int mt = a.mtiles == 1 || p.nstripes < 64 * 2 * 4 ? 1 : 2;
+    const dim3 grid(p.sets, p.ks, mt == 1 ? a.mtiles : (a.mtiles + 1) / 2);
     if (wt == WT_Q8_0) launch_gemm<WT_Q8_0>(mt, p.spw, grid, a, st);
     else launch_gemm<WT_Q4_0>(mt, p.spw, grid, a, st);
     return p.ks;
