@@ -457,19 +457,21 @@ __global__ void k_q4_reduce(GemmArgs a) {
 // ---------------------------------------------------------------------------------------------------------------------
 // host side
 
-// The launch shape depends on (N, K) only, never on the rows (row invariance): 4 spw stripes per workgroup (spw = 1 for
-// matrices too narrow to give 64 sets of 8),
-// and the groups of K in slices across workgroups. A slice holds an even number of groups (the kernel walks groups in
+// The launch shape depends on (N, K) only, never on the rows (row invariance): 4 spw stripes per workgroup (spw = 2
+// only for LM-head-wide matrices) and the groups of K in slices across workgroups. A slice holds an even number of groups (the kernel walks groups in
 // pairs, one per ring slot; an odd count would add a masked pass), halved from the whole of K while the launch has
 // fewer than 768 workgroups, down to 4 groups and at most KS_MAX slices: on MI355X at 32 rows, short slices (a single
 // round of loads per workgroup) beat fewer, longer workgroups for the layer-sized matrices, while every slice costs
 // the consumer one more partial sum to read.
+#define Q4_WIDE (8 * 768)  // stripes of an LM-head-wide matrix
 GemmPlan q4_plan(int N, int K, int wt) {
     GemmPlan p;
     p.nstripes = (N + 15) / 16;
     p.ngroups = (K / 32 + 3) / 4;
-    // stripes per wavefront: 1 while 2 would leave fewer than 64 sets, and for Q8_0 (twice the weight registers)
-    p.spw = p.nstripes >= 64 * 2 * 4 && wt != WT_Q8_0 ? 2 : 1;
+    // stripes per wavefront: 2 only for LM-head-wide matrices (at least 768 sets of 8 stripes: enough workgroups with
+    // no k-split; 67 against 77 us for the Q4_0 head at 32 rows), and never for Q8_0 (twice the weight registers);
+    // 1 otherwise (gate|up: the same 14.3 us with 3 slices instead of 5, so its consumer reads fewer partials)
+    p.spw = p.nstripes >= Q4_WIDE && wt != WT_Q8_0 ? 2 : 1;
     p.sets = (p.nstripes + 4 * p.spw - 1) / (4 * p.spw);
     auto slices = [&](int gps) { return (p.ngroups + gps - 1) / gps; };
     int gps = (p.ngroups + 1) / 2 * 2;
@@ -509,11 +511,12 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
     a.M = M; a.N = N; a.K = K; a.ldy = 0; a.epi = EPI_STORE;
     a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
     a.mtiles = (M + 15) / 16;
-    // row tiles of 16 per workgroup (grid z: one per tile) for matrices narrower than 512 stripes: twice the
-    // workgroups and loads in flight (q|k|v, o, down: 8.4 against 9.1 us at 32 rows; the second tile's weight reads
-    // mostly hit the Infinity Cache); pairs of tiles for the wide ones (gate|up, the LM head), where single tiles were
-    // slower. Either way a row's sums are the same (same slices, same order).
-    const int mt = a.mtiles == 1 || p.nstripes < 64 * 2 * 4 ? 1 : 2;
+    // row tiles of 16 per workgroup (grid z: one per tile) for matrices narrower than 512 stripes: twice the workgroups
+    // and loads in flight (q|k|v, o, down: 8.4 against 9.1 us at 32 rows; the two workgroups of a tile pair run on the
+    // same XCD, so the second reads the weights from its L2); pairs of tiles for the wider ones (the Q8_0 gate|up and
+    // the LM heads were slower with single tiles, the Q4_0 gate|up the same). Either way a row's sums are the same
+    // (same slices, same order).
+    const int mt = a.mtiles == 1 || p.nstripes < 512 ? 1 : 2;
     const dim3 grid(p.sets, p.ks, mt == 1 ? a.mtiles : (a.mtiles + 1) / 2);
     if (wt == WT_Q8_0) launch_gemm<WT_Q8_0>(mt, p.spw, grid, a, st);
     else launch_gemm<WT_Q4_0>(mt, p.spw, grid, a, st);
