@@ -832,6 +832,7 @@ struct Dev {
     sn_engine* e;
     hipStream_t st;
     int ks = 0;  // k-slices of the last matmul
+    bool moe_pending = false;  // x awaits a MoE layer's weighted expert rows (added by the next resid)
     int rc = 0;
 
     void gemm(const uint8_t* w, int M, int N, int K) {
@@ -849,6 +850,15 @@ struct Dev {
     // x (R rows of E) += the last matmul's sums (add false: x = the sums); then the Q8_0 operand of norm(x) when asked
     void resid(float* x, int R, const float* nw, bool quantize, bool add = true) {
         const int E = e->E;
+        if (moe_pending) {  // x += the MoE output (the grouped down matmul's rows, weighted), then the operand
+            moe_pending = false;
+            rc |= e->launch(SNX_K_QUANT, (double) R * e->NEU * E * 4 + (double) R * E * 8 +
+                                             (quantize ? (double) R * E * 2 : 0.0), [&] {
+                return moe_resid_quant(x, e->gemm_ws, e->prow, e->mw, e->NEU, R, E, nw, e->eps,
+                                       quantize ? e->xa : nullptr, st);
+            });
+            return;
+        }
         rc |= e->launch(SNX_K_QUANT, (double) R * E * (8 + 4 * ks) + (quantize ? (double) R * E * 2 : 0.0), [&] {
             return resid_quant(x, e->gemm_ws, ks, R, E, nw, e->eps, quantize ? e->xa : nullptr, st, add);
         });
@@ -899,7 +909,8 @@ struct Dev {
     uint16_t* vp(int layer) { return e->vbase + (size_t) layer * e->layer_halves; }
 
     // one block over R rows whose Q8_0 operand of attn_norm(x) is in xa. Returns whether x still awaits its down
-    // projection's sums (left in the workspace): a dense FFN; a MoE layer adds its experts itself.
+    // projection's sums (left in the workspace: a dense FFN's k-slices, a MoE layer's expert rows); the next resid adds
+    // them.
     bool block(const DevLayer& l, int layer, float* x, int R, const Stage& S, const AttnList& al, const int32_t* d_seq,
                const int32_t* d_pos) {
         const int E = e->E, F = e->F;
@@ -909,7 +920,7 @@ struct Dev {
         gemm(l.wo, R, E, e->QD);
         if (l.egu) {
             moe(l, x, R);
-            return false;
+            return true;
         }
         resid(x, R, l.ffn_norm, true);
         gemm(l.wgu, R, 2 * F, E);
@@ -957,10 +968,7 @@ struct Dev {
             return q4_gemm_grouped(l.ed, e->ed_stride, e->gitems, e->gcount, T, e->xa, P, E, FE, e->gemm_ws,
                                    e->gemm_ws_bytes, st, e->wt, e->rsrc) < 0 ? -1 : 0;
         });
-        rc |= e->launch(SNX_K_OTHER, (double) R * NU * E * 4 + (double) R * E * 8, [&] {
-            moe_out(x, e->gemm_ws, e->prow, e->mw, R, E, NU, st);
-            return 0;
-        });
+        moe_pending = true;  // x += the weighted expert rows: the next resid, fused with its norm and operand
     }
 
     // the model's layers over R rows (qwen_layers, sn_attn.inc.h:216-231); leaves x = the final residual rows

@@ -640,23 +640,6 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ 
         }
 }
 
-// x[r] += sum_j w[r][j] * y[prow[r][j]] in slot order (moe_out, kernels.metal:3520-3538); y = the down matmul's sums.
-// Workgroup (row, 256 elements).
-__global__ __launch_bounds__(256) void k_moe_out(float* __restrict__ x, const float* __restrict__ y,
-                                                 const int32_t* __restrict__ prow, const float* __restrict__ w, int E,
-                                                 int k) {
-    const int r = blockIdx.x, i = blockIdx.y * 256 + threadIdx.x;
-    if (i >= E) return;
-    float yv[8], wv[8];
-    for (int j = 0; j < k; ++j) {
-        wv[j] = w[r * k + j];
-        yv[j] = y[(size_t) prow[r * k + j] * E + i];
-    }
-    float acc = 0.0f;
-    for (int j = 0; j < k; ++j) acc += wv[j] * yv[j];
-    x[(size_t) r * E + i] += acc;
-}
-
 void moe_router(const float* hn, const float* router, int R, int E, int NE, float* lg, hipStream_t st) {
     if (R > 0)
         hipLaunchKernelGGL(k_router, dim3((NE + 3) / 4, (R + RT_ROWS - 1) / RT_ROWS), dim3(256), 0, st, hn, router, R,
@@ -665,12 +648,9 @@ void moe_router(const float* hn, const float* router, int R, int E, int NE, floa
 int moe_select(const float* lg, int R, int NE, int k, int P, int32_t* ids, float* w, int32_t* prow, int32_t* rsrc,
                int32_t* items, int32_t* count, hipStream_t st) {
     if (R <= 0) return 0;
-    if (NE < 1 || NE > 256 || k < 1 || k > 8 || k > NE || R * k > MOE_MAX_PAIRS) return -1;
+    if (NE < 1 || NE > 256 || k < 1 || k > MOE_MAX_K || k > NE || R * k > MOE_MAX_PAIRS) return -1;
     if (P < 16 * (std::min(NE, R * k) + (R * k + 15) / 16)) return -1;  // the tiles of any grouping
     hipLaunchKernelGGL(k_moe_topk, dim3(R), dim3(256), 0, st, lg, NE, k, ids, w);
     hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(1024), 0, st, ids, R * k, NE, P, k, prow, rsrc, items, count);
     return 0;
-}
-void moe_out(float* x, const float* y, const int32_t* prow, const float* w, int R, int E, int k, hipStream_t st) {
-    if (R > 0) hipLaunchKernelGGL(k_moe_out, dim3(R, (E + 255) / 256), dim3(256), 0, st, x, y, prow, w, E, k);
 }

@@ -188,14 +188,38 @@ __device__ __forceinline__ float block_reduce_sum(float v, float* red) {
     return s;
 }
 
+// The MoE output of row m at elements e .. e + 3: the weighted sum over its k slots of the expert rows y[prow[j]],
+// accumulated from zero in slot order (moe_out, kernels.metal:3520-3538; sn_layers.inc.h:129-144)
+__device__ __forceinline__ float4 pairs_sum4(const float* y, const int32_t* prow, const float* w, int k, int K, int e) {
+    float4 v[MOE_MAX_K];
+    float wv[MOE_MAX_K];
+    for (int j = 0; j < MOE_MAX_K; ++j)
+        if (j < k) {
+            wv[j] = w[j];
+            v[j] = ld4(y + (size_t) prow[j] * K + e);
+        }
+    float4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < MOE_MAX_K; ++j)
+        if (j < k) {
+            acc.x += wv[j] * v[j].x;
+            acc.y += wv[j] * v[j].y;
+            acc.z += wv[j] * v[j].z;
+            acc.w += wv[j] * v[j].w;
+        }
+    return acc;
+}
+
 // Residual rows: x[m] += the k-slice sums of a matmul (part[ks][M][K], slices added in order; add 0: x[m] = the
-// sums), written back; then, when xa is given, the RMSNorm (weight nw) and Q8_0 operand of the new row. One workgroup
-// per row (the norm needs the whole row before any value is quantized), 4 lanes per 32-block: lane t covers blocks
-// t / 4 + (blockDim / 4) i, i < IT. Every load (residual, slices, norm weight) is issued before the row's reduction.
-template <int IT, int KM>
+// sums), or with PAIRS the MoE output (pairs_sum4 over part = the grouped down matmul's rows), written back; then,
+// when xa is given, the RMSNorm (weight nw) and Q8_0 operand of the new row. One workgroup per row (the norm needs the
+// whole row before any value is quantized), 4 lanes per 32-block: lane t covers blocks t / 4 + (blockDim / 4) i,
+// i < IT. Every load (residual, slices, norm weight) is issued before the row's reduction.
+template <int IT, int KM, bool PAIRS = false>
 __global__ __launch_bounds__(1024) void k_resid_quant(float* __restrict__ X, const float* __restrict__ part, int ks,
                                                       int M, int K, const float* __restrict__ nw, float eps,
-                                                      uint8_t* __restrict__ xa, int add, float* __restrict__ xn) {
+                                                      uint8_t* __restrict__ xa, int add, float* __restrict__ xn,
+                                                      const int32_t* __restrict__ prow = nullptr,
+                                                      const float* __restrict__ pw = nullptr) {
     __shared__ float red[16];
     const int m = blockIdx.x, t = threadIdx.x, g = t & 3, bstep = blockDim.x >> 2;
     const int nb = K / 32, nbp = xa_nbp(K);
@@ -212,8 +236,10 @@ __global__ __launch_bounds__(1024) void k_resid_quant(float* __restrict__ X, con
             for (int j = 0; j < 8; ++j) w[it][j] = w8[j];
         }
         float4 lo = add ? ld4(x + e0) : (float4){0.f, 0.f, 0.f, 0.f}, hi = add ? ld4(x + e1) : (float4){0.f, 0.f, 0.f, 0.f};
-        const float4 slo = slices_sum4<KM>(part + (size_t) m * K + e0, (size_t) M * K, ks);
-        const float4 shi = slices_sum4<KM>(part + (size_t) m * K + e1, (size_t) M * K, ks);
+        const float4 slo = PAIRS ? pairs_sum4(part, prow + (size_t) m * ks, pw + (size_t) m * ks, ks, K, e0)
+                                 : slices_sum4<KM>(part + (size_t) m * K + e0, (size_t) M * K, ks);
+        const float4 shi = PAIRS ? pairs_sum4(part, prow + (size_t) m * ks, pw + (size_t) m * ks, ks, K, e1)
+                                 : slices_sum4<KM>(part + (size_t) m * K + e1, (size_t) M * K, ks);
         lo = add4(lo, slo);
         hi = add4(hi, shi);
         *(float4*) (x + e0) = lo;
@@ -582,6 +608,20 @@ int resid_quant(float* x, const float* part, int ks, int M, int K, const float* 
     if (it == 1) launch_resid<1>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
     else if (it == 2) launch_resid<2>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
     else launch_resid<4>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
+    return 0;
+}
+
+int moe_resid_quant(float* x, const float* y, const int32_t* prow, const float* w, int k, int M, int K, const float* nw,
+                    float eps, uint8_t* xa, hipStream_t st) {
+    if (M <= 0) return 0;
+    const int lanes = 4 * xa_nbp(K), nt = std::min(1024, (lanes + 63) / 64 * 64), it = (lanes + nt - 1) / nt;
+    if (K % 32 || it > 4 || k < 1 || k > MOE_MAX_K) return -1;
+#define MQ(IT_) hipLaunchKernelGGL((k_resid_quant<IT_, 1, true>), dim3(M), dim3(nt), 0, st, x, y, k, M, K, nw, eps, xa, 1, \
+                                   (float*) nullptr, prow, w)
+    if (it == 1) MQ(1);
+    else if (it == 2) MQ(2);
+    else MQ(4);
+#undef MQ
     return 0;
 }
 

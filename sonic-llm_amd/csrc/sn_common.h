@@ -124,6 +124,7 @@ static inline size_t wt_bytes(int wt, int N, int K) {
 // The sum, in slice order, of ks <= KM k-slices of a matmul (slice k at p + k * stride). Every load is issued before
 // any is used (the slice index is clamped, so no load sits behind a branch); the slices past ks are not added.
 #define KS_MAX 8
+#define MOE_MAX_K 8  // experts used per row
 template <int KM>
 __device__ __forceinline__ float4 slices_sum4(const float* p, size_t stride, int ks) {
     float4 v[KM];

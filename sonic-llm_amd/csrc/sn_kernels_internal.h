@@ -181,4 +181,8 @@ void moe_router(const float* hn, const float* router, int R, int E, int NE, floa
 int moe_select(const float* lg, int R, int NE, int k, int P, int32_t* ids, float* w, int32_t* prow, int32_t* rsrc,
                int32_t* items, int32_t* count, hipStream_t st);
 // x[r] += sum_j w[r][j] y[prow[r][j]] (slot order)
-void moe_out(float* x, const float* y, const int32_t* prow, const float* w, int R, int E, int k, hipStream_t st);
+// x[r] += the MoE output of row r (sum over its k slots, in slot order, of w[r][j] * y[prow[r][j]]: y the grouped down
+// matmul's rows) and then, when xa is given, the RMSNorm (nw) + Q8_0 operand of the new rows, in one launch (one
+// workgroup a row, the arithmetic of resid_quant); 0, or -1 (bad shape)
+int moe_resid_quant(float* x, const float* y, const int32_t* prow, const float* w, int k, int M, int K, const float* nw,
+                    float eps, uint8_t* xa, hipStream_t st);
