@@ -352,6 +352,9 @@ __device__ __forceinline__ half8 q8_unpack(uint32_t w_lo, uint32_t w_hi) {
 template <int WT, int MT, int S>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_q4_gemm(GemmArgs a) {
     constexpr int D = 2, FPW = MT;  // ring slots, fragments each wavefront stages
+    // the loop below stages group i + 1 from register slot j ^ 1 into LDS buffer j ^ 1 and sums group i from buffer j:
+    // the register ring and the LDS double buffer are one and the same pair of slots
+    static_assert(D == 2, "the ring is indexed j ^ 1 over the two LDS buffers s_act / s_k");
     constexpr bool Q8 = WT == WT_Q8_0;
     constexpr int TB = Q8 ? Q8T_BYTES : Q4T_BYTES, SO = Q8 ? Q8T_SCALE_OFF : Q4T_SCALE_OFF;
     constexpr int NW = Q8 ? 2 : 1;                               // 16-byte weight loads per lane and tile
