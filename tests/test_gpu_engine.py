@@ -98,6 +98,38 @@ def prefill_and_decode(path):
         assert stats["same"] == stats["rows"]
 
 
+def test_large_prompt_step_matches_oracle(tiny):
+    """One step of 500 prompt rows of one sequence (32 row tiles, 125 attention query groups over up to 2 chunks) and a
+    second sequence's 37, then decode steps of both: logits and tokens against the oracle as above."""
+    ref = O.Qwen3(GGUF(tiny), n_seq=2, ctx=1024)
+    r = np.random.default_rng(41)
+    lens = [500, 37]
+    toks = [r.integers(0, TINY["n_vocab"], n).astype(np.int32) for n in lens]
+    tok = np.concatenate(toks)
+    seq = np.concatenate([np.full(n, s, np.int32) for s, n in enumerate(lens)])
+    pos = np.concatenate([np.arange(n, dtype=np.int32) for n in lens])
+    outs = np.array([lens[0] - 1, sum(lens) - 1], np.int32)
+    stats = {"rows": 0, "checked": 0, "same": 0}
+    with S.Engine(tiny, slots=2, ctx=1024, max_rows=544) as eng:
+        got = eng.step(tok, seq, pos, outs, n_write=0)
+        rt, rl, _ = ref.step(tok, seq, pos, outs)
+        gl = eng.logits([0, 1])
+        print("500-row prompt max |logit diff|", np.abs(gl - rl).max())
+        assert np.abs(gl - rl).max() <= MODEL_ATOL
+        check_tokens(got, rt, rl, stats)
+        cur = rt.copy()
+        p = np.array(lens, np.int32)
+        for _ in range(3):
+            got = eng.step(cur, np.array([0, 1], np.int32), p, np.array([0, 1], np.int32))
+            rt, rl, _ = ref.step(cur, np.array([0, 1], np.int32), p, np.array([0, 1], np.int32))
+            assert np.abs(eng.logits([0, 1]) - rl).max() <= MODEL_ATOL
+            check_tokens(got, rt, rl, stats)
+            cur = rt.copy()
+            p += 1
+    print("end to end:", stats)  # tokens are compared where the oracle's top-2 gap clears the bound (check_tokens)
+    assert stats["checked"] >= 4
+
+
 def test_stagewise_parity(tmp_path):
     """One layer, 40 prompt rows of one sequence: each stage against the oracle given the engine's previous stage."""
     import ctypes as C
