@@ -247,6 +247,26 @@ def test_error_paths(tiny):
         assert eng.pages_free() == 0
         eng.clear(1, 0, 65)
         assert eng.pages_free() == 2
+    # empty, ragged and out-of-range inputs are refused before anything runs (sn_step.inc.h:97-99); the engine then
+    # steps normally
+    V = TINY["n_vocab"]
+    with S.Engine(tiny, slots=2, ctx=256, max_rows=16) as eng:
+        one = lambda t, s_, p_, o, **kw: eng.step(np.array(t, np.int32), np.array(s_, np.int32), np.array(p_, np.int32),
+                                                  np.array(o, np.int32), **kw)
+        for args, kw in [(([], [], [], []), {}),                      # no rows
+                         (([1], [0], [0], [0]), {"n_write": 2}),      # more write rows than rows
+                         (([1, 2], [0, 0], [0, 1], [2]), {}),         # an output row outside the step
+                         (([V], [0], [0], [0]), {}),                  # a token outside the vocabulary
+                         (([1], [0], [-1], [0]), {}),                 # a negative position
+                         (([1], [0], [256], [0]), {})]:               # a position past the context
+            with pytest.raises(S.SnError) as ei:
+                one(*args, **kw)
+            assert ei.value.rc == -1, args
+        assert eng.pages_free() == eng.pages_total()
+        assert one([3, 4, 5], [0, 0, 0], [0, 1, 2], [], n_write=0).size == 0  # no outputs: the cells are written
+        assert eng.seq_pages(0)[0] == 1
+        t = one([6], [0], [3], [0])
+        assert t.size == 1 and 0 <= t[0] < V
 
 
 def test_graph_replay_matches_eager(tiny):
