@@ -14,11 +14,12 @@ extern "C" {
 // kernel classes of a step
 enum {
     SNX_K_GEMM = 0,   // Q4_0 x Q8_0 matmuls (q/k/v, o, gate/up, down, LM head) incl. their k-slice reductions
-    SNX_K_ATTN = 1,   // paged attention: partials and merge
+    SNX_K_ATTN = 1,   // paged attention: the chunk partials (per-chunk items), or whole groups (outputs written)
     SNX_K_QUANT = 2,  // Q8_0 activation quantizers (with the RMSNorm fused in front)
     SNX_K_ROPE = 3,   // QK-norm + RoPE + K/V cache write
     SNX_K_OTHER = 4,  // embedding, argmax, copies
-    SNX_K_COUNT = 5
+    SNX_K_MERGE = 5,  // the attention merge: chunk partials folded into the outputs and the o-projection operand
+    SNX_K_COUNT = 6
 };
 
 // Profiling on (resets the counters) or off. While on, every launch of a step is bracketed by HIP events on the

@@ -444,16 +444,21 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
     }
 }
 
-int paged_attention(const AttnArgs& a, hipStream_t st) {
+int attention_items(const AttnArgs& a, hipStream_t st) {
     if (a.n_items <= 0) return 0;
     if (a.H % a.KVH != 0 || 16 % (a.H / a.KVH) != 0) return -1;
-    if (a.whole) {
-        hipLaunchKernelGGL(k_attn_whole, dim3(a.n_items, a.KVH), dim3(512), 0, st, a);
-    } else {
-        hipLaunchKernelGGL(k_attn_part, dim3(a.n_items, a.KVH), dim3(256), 0, st, a);
-        if (a.n_mrows > 0) hipLaunchKernelGGL(k_attn_merge, dim3(a.n_mrows, a.H), dim3(64), 0, st, a);
-    }
+    if (a.whole) hipLaunchKernelGGL(k_attn_whole, dim3(a.n_items, a.KVH), dim3(512), 0, st, a);
+    else hipLaunchKernelGGL(k_attn_part, dim3(a.n_items, a.KVH), dim3(256), 0, st, a);
     return 0;
+}
+int attention_merge(const AttnArgs& a, hipStream_t st) {
+    if (a.n_items <= 0 || a.whole || a.n_mrows <= 0) return 0;
+    hipLaunchKernelGGL(k_attn_merge, dim3(a.n_mrows, a.H), dim3(64), 0, st, a);
+    return 0;
+}
+int paged_attention(const AttnArgs& a, hipStream_t st) {
+    const int rc = attention_items(a, st);
+    return rc ? rc : attention_merge(a, st);
 }
 
 // The work list (see sn_kernels_internal.h). Whole groups when they make one round of workgroups on the 256 CUs

@@ -734,12 +734,13 @@ struct Stage {
 };
 
 // The attention work of R rows (attn_plan: whole groups, or per-chunk items and the rows to merge). bytes: each
-// (sequence, KV head) reads its cells once, q in and the output out, page-table entries.
+// (sequence, KV head) reads its cells once, q in, page-table entries, and the outputs out (whole groups) or the
+// chunk partials out; merge_bytes: the partials in, the outputs and the o-projection operand out (chunk items).
 struct AttnList {
     size_t o_grp = 0, o_itm = 0, o_mrow = 0;
     int n_items = 0, n_mrows = 0;
     bool whole = false;
-    double bytes = 0.0;
+    double bytes = 0.0, merge_bytes = 0.0;
 };
 
 AttnList attn_list(sn_engine* e, Stage& S, int R, const int32_t* seq, const int32_t* pos) {
@@ -752,7 +753,13 @@ AttnList attn_list(sn_engine* e, Stage& S, int R, const int32_t* seq, const int3
     al.n_items = (int) p.items.size();
     al.n_mrows = (int) p.mrows.size();
     al.whole = p.whole;
-    al.bytes = (double) R * e->QD * 8;
+    // chunk partials: (acc[128], m, l) per (row, head, chunk of the row)
+    double part = 0.0;
+    for (const AttnGroup& g : p.groups)
+        for (int i = 0; i < g.nrows; ++i) part += (double) ((g.pos0 + i) / ATT_CHUNK + 1) * e->H * (e->D + 2) * 4;
+    const double out = (double) R * e->QD * 4, operand = (double) R * e->QD / 32 * 76;  // 76 B a row block (xa)
+    al.bytes = (double) R * e->QD * 4 + (p.whole ? out + operand : part);
+    al.merge_bytes = p.whole ? 0.0 : part + out + operand;
     std::vector<int> seen;
     for (const AttnGroup& g : p.groups) {
         if (std::find(seen.begin(), seen.end(), g.seq) != seen.end()) continue;
@@ -903,7 +910,9 @@ struct Dev {
         aa.whole = al.whole ? 1 : 0;
         aa.mrows = S.dev<const int32_t>(al.o_mrow);
         aa.n_mrows = al.n_mrows;
-        rc |= e->launch(SNX_K_ATTN, al.bytes, [&] { return paged_attention(aa, st); });
+        rc |= e->launch(SNX_K_ATTN, al.bytes, [&] { return attention_items(aa, st); });
+        if (!al.whole && al.n_mrows > 0)
+            rc |= e->launch(SNX_K_MERGE, al.merge_bytes, [&] { return attention_merge(aa, st); });
     }
     uint16_t* kp(int layer) { return e->kbase + (size_t) layer * e->layer_halves; }
     uint16_t* vp(int layer) { return e->vbase + (size_t) layer * e->layer_halves; }

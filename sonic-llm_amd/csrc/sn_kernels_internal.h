@@ -111,7 +111,9 @@ struct AttnArgs {
     const int32_t* mrows;    // rows the merge folds (chunk items), n_mrows of them
     int n_mrows;
 };
-int paged_attention(const AttnArgs& a, hipStream_t st);
+int paged_attention(const AttnArgs& a, hipStream_t st);  // attention_items, then attention_merge
+int attention_items(const AttnArgs& a, hipStream_t st);  // the partials (chunk items) or whole groups
+int attention_merge(const AttnArgs& a, hipStream_t st);  // chunk items: the merge (nothing for whole groups)
 // The work list of R rows: consecutive rows of one sequence at consecutive positions share a group (up to 16/G rows:
 // their K/V loads are shared). Whole groups (one item each, walked by one workgroup per KV head) when the groups give
 // one round of ATT_WHOLE_MIN_WG .. ATT_WHOLE_MAX_WG workgroups, the longest context is at most 9/8 of the mean and the

@@ -339,7 +339,7 @@ class Engine:
     def prof(self, on: bool):
         self.L.snx_prof(self.e, int(on))
 
-    KINDS = ("gemm", "attn", "quant", "rope", "other")
+    KINDS = ("gemm", "attn", "quant", "rope", "other", "merge")
 
     def prof_read(self) -> dict:
         out = {}
