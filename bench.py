@@ -344,6 +344,15 @@ def graph_us(fn, n, reps=10):
     return e0.elapsed_time(e1) * 1e3 / reps / n
 
 
+def profile_traffic(name, key):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 counter runs (profiles/), or None"""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    v = json.load(open(path)).get(key)
+    return round(v) if v is not None else None
+
+
 def cpu_threads():
     return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count())
 
@@ -457,7 +466,8 @@ def bench_matmul(args):
                    "weight_copies": copies, "algorithmic_bytes": alg, "us_per_call": round(us, 3),
                    "us_matmul_kernel": round(us_gemm, 3)},
         "roofline": {"kernel": "k_q4_gemm", "bound": "hbm", "achieved": round(gbs_k, 1), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(gbs_k * 1e9 / HBM_PEAK, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs_k * 1e9 / HBM_PEAK, 4),
+                     "traffic": profile_traffic("matmul_q4_0_b8_4096x4096_traffic.json", "k_q4_gemm"),
                      "bytes_per_launch": alg, "us_per_launch": round(us_gemm, 3)},
         "cpu_baseline": cpu,
     }
@@ -580,7 +590,8 @@ def bench_attn(args):
                    "unique_bytes": alg, "bytes_counting_shared_per_seq": alg_per_seq,
                    "GBps_counting_shared_per_seq": round(alg_per_seq / (us * 1e-6) / 1e9, 1)},
         "roofline": {"kernel": kern, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(gbs * 1e9 / HBM_PEAK, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs * 1e9 / HBM_PEAK, 4),
+                     "traffic": profile_traffic("attn_config2_b32_ctx256_4096_page32_traffic.json", kern),
                      "bytes_per_launch": alg, "us_per_launch": round(us, 3)},
         "cpu_baseline": cpu,
     }
