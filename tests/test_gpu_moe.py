@@ -122,6 +122,37 @@ def select_gpu(lg, k):
             U.host(items, np.int32)[:2 * n].reshape(n, 2), n, P, (rsrc, items, cnt))
 
 
+def test_moe_graphs_and_chained_steps_are_bitwise_eager(moe_model):
+    """MoE decode through HIP-graph replay and through sn_step's queued successor (chain) against eager, unchained
+    steps of a second engine: the same tokens and logits bit for bit (the expert grouping and the weighted sum folded
+    into the next layer's residual kernel run inside captured and queued steps alike)."""
+    n, steps = 4, 6
+    r = np.random.default_rng(17)
+    prompts = [r.integers(0, TINY_MOE["n_vocab"], int(r.integers(5, 20))).astype(np.int32) for _ in range(n)]
+    runs = []
+    for graphs, chain in ((True, 1), (False, 0)):
+        with S.Engine(moe_model, slots=n, ctx=128, max_rows=96) as eng:
+            eng.graphs(graphs)
+            tok = np.concatenate(prompts)
+            seq = np.concatenate([np.full(len(p), s, np.int32) for s, p in enumerate(prompts)])
+            pos = np.concatenate([np.arange(len(p), dtype=np.int32) for p in prompts])
+            last = eng.step(tok, seq, pos, np.cumsum([len(p) for p in prompts]).astype(np.int32) - 1, n_write=0)
+            p = np.array([len(x) for x in prompts], np.int32)
+            trace = []
+            for i in range(steps):
+                last = eng.step(last, np.arange(n, dtype=np.int32), p, np.arange(n, dtype=np.int32),
+                                chain=chain if i + 1 < steps else 0)
+                trace.append((last.copy(), eng.logits(np.arange(n)).copy()))
+                p += 1
+            if chain:
+                taken, _ = eng.chain_count()
+                assert taken == steps - 1
+            runs.append(trace)
+    for (ta, la), (tb, lb) in zip(*runs):
+        assert np.array_equal(ta, tb)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
 def test_moe_router_matches_f64_and_is_row_invariant():
     L = S.lib()
     r = np.random.default_rng(40)
