@@ -98,6 +98,17 @@ def prefill_and_decode(path):
         assert stats["same"] == stats["rows"]
 
 
+def test_32_cell_pages_match_oracle(tiny, monkeypatch):
+    """SN_PAGE=32 (config 2's page size, sn.h:13 keeps 64 by default): the same prefill and decode against the oracle,
+    with a 40-row prompt taking two pages."""
+    monkeypatch.setenv("SN_PAGE", "32")
+    with S.Engine(tiny, slots=2, ctx=256, max_rows=64) as eng:
+        eng.step(np.arange(40, dtype=np.int32), np.zeros(40, np.int32), np.arange(40, dtype=np.int32),
+                 np.array([39], np.int32), n_write=0)
+        assert eng.seq_pages(0)[0] == 2
+    prefill_and_decode(tiny)
+
+
 def test_large_prompt_step_matches_oracle(tiny):
     """One step of 500 prompt rows of one sequence (32 row tiles, 125 attention query groups over up to 2 chunks) and a
     second sequence's 37, then decode steps of both: logits and tokens against the oracle as above."""

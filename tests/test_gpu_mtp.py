@@ -108,8 +108,20 @@ def model_q6k_tied(tmp_path_factory):
     return path
 
 
+@pytest.fixture(scope="module")
+def model_q8(tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("model") / "mtp_q8.gguf")
+    S.write_model(path, S.model_cfg(**TINY, wtype=8), seed=23)
+    return path
+
+
 def test_guesses_match_oracle(model):
     guesses_match_oracle(model)
+
+
+def test_guesses_match_oracle_q8_0(model_q8):
+    """the guess head with Q8_0 matrices (its block, eh_proj and the LM head)"""
+    guesses_match_oracle(model_q8)
 
 
 def test_guesses_match_oracle_q6k_tied_head(model_q6k_tied):
