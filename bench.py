@@ -25,6 +25,7 @@ for p in (ROOT, os.path.join(ROOT, "sonic-llm_amd")):
         sys.path.insert(0, p)
 
 HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
+MFMA_F16_PEAK = 2.5e15  # MI355X dense fp16 MFMA, flop/s
 
 
 def log(msg):
@@ -84,10 +85,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--model", default=None, help="GGUF path (generated when missing)")
     ap.add_argument("--seed", type=int, default=42)
-    ap.add_argument("--config", default="decode", choices=("decode", "mtp", "moe", "matmul", "attn"),
+    ap.add_argument("--config", default="decode", choices=("decode", "mtp", "moe", "matmul", "attn", "prefill"),
                     help="decode: the headline (configs[2]); mtp: the fused draft-verify step (configs[3]); "
                          "moe: Qwen3-30B-A3B-arch batched decode (configs[4]); matmul: one 8 x 4096 x 4096 Q4_0 "
-                         "matmul (configs[0]); attn: one layer of paged decode attention (configs[1])")
+                         "matmul (configs[0]); attn: one layer of paged decode attention (configs[1]); prefill: "
+                         "2048-token prompts in 512-row steps")
     ap.add_argument("--accept", type=float, default=0.6, help="mtp: the seeded share of drafts forced to match")
     ap.add_argument("--no-graphs", action="store_true", help="launch every step eagerly (no HIP graph replay)")
     ap.add_argument("--no-chain", action="store_true", help="decode without sn_step's queued successor (chain = 0)")
@@ -128,6 +130,8 @@ def main():
         return bench_matmul(args)
     if args.config == "attn":
         return bench_attn(args)
+    if args.config == "prefill":
+        return bench_prefill(args)
     moe = args.config == "moe"
     cfg = dict(S.QWEN3_30B_A3B if moe else S.QWEN3_4B)
     if args.wtype == 8:
@@ -318,6 +322,95 @@ def bench_mtp(args):
                      "us_per_launch": kernels[dom]["us_per_launch"]} if dom else None,
         "kernels": kernels,
         "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_prefill(args):
+    """Prompt rows (the next row after the decode step): 8 sequences of 2048 prompt tokens on the Qwen3-4B-arch model,
+    fed 512 rows a step (4 steps a sequence; every row writes its cell, the last row's token is sampled), as a serving
+    loop prefills. value = prompt tokens per second over the timed sequences (after one warmup sequence)."""
+    import numpy as np
+    import torch
+
+    import sllm_next as S
+
+    cfg = dict(S.QWEN3_4B)
+    path = model_file(cfg, args.seed, args.model)
+    n_seq, ctx, rows = 8, 2048, 512
+    eng = S.Engine(path, slots=n_seq + 1, ctx=ctx + 1, max_rows=rows)
+    rng = np.random.default_rng(args.seed)
+
+    def prefill(s):
+        toks = rng.integers(0, eng.V, ctx).astype(np.int32)
+        for c0 in range(0, ctx, rows):
+            eng.step(toks[c0:c0 + rows], np.full(rows, s, np.int32), np.arange(c0, c0 + rows, dtype=np.int32),
+                     np.array([rows - 1], np.int32), n_write=0)
+
+    prefill(n_seq)  # warmup on the spare slot
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(n_seq):
+        prefill(s)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    toks = n_seq * ctx
+    # profiled pass: one more sequence's steps on the spare slot (cleared first)
+    eng.clear(n_seq, 0, ctx)
+    eng.prof(True)
+    prefill(n_seq)
+    prof = eng.prof_read()
+    eng.prof(False)
+    eng.close()
+    steps = ctx // rows
+    kernels = {}
+    for name, p in prof.items():
+        if p["launches"]:
+            gbs = p["bytes"] / (p["ms"] * 1e-3) / 1e9
+            kernels[name] = {"ms_per_step": round(p["ms"] / steps, 4), "launches_per_step": p["launches"] / steps,
+                             "bytes_per_launch": round(p["bytes"] / p["launches"]),
+                             "us_per_launch": round(1e3 * p["ms"] / p["launches"], 2),
+                             "GBps": round(gbs, 1), "frac": round(gbs * 1e9 / HBM_PEAK, 4)}
+    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"]) if kernels else None
+    # at 512 rows the matmuls are MFMA work: 2 M N K flop per matrix (q|k|v, o, gate|up, down per layer; the LM head
+    # for the step's one output row), against MI355X's dense fp16 peak (the operands are fp16)
+    E, F, H, KVH = cfg["n_embd"], cfg["n_ff"], cfg["n_head"], cfg["n_head_kv"]
+    layer = (H + 2 * KVH) * 128 * E + E * H * 128 + 2 * F * E + E * F
+    flop = 2.0 * rows * layer * cfg["n_layer"] + 2.0 * E * cfg["n_vocab"]
+    g = kernels.get("gemm")
+    roof_mfma = {"kernel": "k_q4_gemm", "bound": "mfma", "achieved": round(flop / (g["ms_per_step"] * 1e-3) / 1e12, 1),
+                 "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
+                 "frac": round(flop / (g["ms_per_step"] * 1e-3) / MFMA_F16_PEAK, 4), "traffic": None,
+                 "flop_per_launch": round(flop / g["launches_per_step"]),
+                 "us_per_launch": g["us_per_launch"]} if g else None
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        from oracle.gguf import GGUF
+        O.build() if not os.path.exists(O.LIB_PATH) else None
+        ref = O.Qwen3(GGUF(path), n_seq=1, ctx=ctx)
+        n = 64
+        tok = rng.integers(0, ref.V, n).astype(np.int32)
+        t = time.perf_counter()
+        ref.step(tok, np.zeros(n, np.int32), np.arange(n, dtype=np.int32), np.array([n - 1], np.int32))
+        cdt = time.perf_counter() - t
+        nt = cpu_threads()
+        cpu = {"value": round(n / cdt, 2), "unit": "tok/s", "cores": nt, "kind": "port",
+               "sample": f"one 64-row prompt step (positions 0..63, all layers, the last row's LM head) through "
+                         f"oracle/oracle.c, {cdt:.1f} s on {nt} threads"}
+    log(f"[bench] prefill: {n_seq} x {ctx} prompt tokens in {dt:.3f} s ({dt * 1e3 / (n_seq * steps):.2f} ms per "
+        f"{rows}-row step)")
+    line = {
+        "metric": "prefill tok/s, Qwen3-4B-arch Q4_0, 512-row prompt steps",
+        "value": round(toks / dt, 1), "unit": "tok/s", "n_gpus": 1, "steps": n_seq * steps, "warmup": steps,
+        "ms_per_step": round(dt * 1e3 / (n_seq * steps), 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "q4_0 x q8_0 -> f32 (fp16 MFMA); f16 KV, f32 softmax",
+        "data": "synthetic: random-init weights (seeded), random prompt token ids",
+        "config": {"workload": "prompt rows of the batched step (sn_step prompt rows, 512 a step)", "seqs": n_seq,
+                   "prompt": ctx, "rows_per_step": rows, "layers": cfg["n_layer"], "hidden": cfg["n_embd"]},
+        "roofline": roof_mfma if dom == "gemm" else None,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
