@@ -115,7 +115,7 @@ def test_config1_q4_matmul_4096x4096_b8():
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (3, 160, 96), (16, 512, 512), (17, 6144, 2560), (32, 2560, 9728),
-                                   (33, 1024, 4096), (64, 304, 1024)])
+                                   (33, 1024, 4096), (64, 304, 1024), (300, 1000, 512), (512, 2560, 1024)])
 def test_matmul_shapes(M, N, K):
     r = np.random.default_rng(M * 7 + N)
     Wq = O.quantize_q4_0(r.normal(0, 0.02, (N, K)).astype(np.float32))
@@ -159,11 +159,12 @@ def test_row_invariance_bitwise():
     r = np.random.default_rng(4)
     N, K = 1536, 2560
     Wq = O.quantize_q4_0(r.normal(0, 0.02, (N, K)).astype(np.float32))
-    X = r.normal(0, 1, (40, K)).astype(np.float32)
+    # 300 rows: every matrix takes its row tiles in pairs (prompt rows); the 1..40-row subsets single tiles here
+    X = r.normal(0, 1, (300, K)).astype(np.float32)
     L = S.lib()
     wbuf = U.empty(L.snk_q4_stripes_bytes(N, K))
     assert L.snk_q4_repack(U.ptr(U.dev(Wq)), N, K, U.ptr(wbuf), U.stream()) == 0
     full, _ = gemm_gpu(None, N, K, X, wbuf=wbuf)
-    for rows in ([0], [5, 6, 7], list(range(17)), list(range(8, 40))):
+    for rows in ([0], [5, 6, 7], list(range(17)), list(range(8, 40)), list(range(43, 300))):
         part, _ = gemm_gpu(None, N, K, X[rows], wbuf=wbuf)
         assert np.array_equal(part.view(np.uint32), full[rows].view(np.uint32))

@@ -71,7 +71,7 @@ def test_q8_dequant_bit_exact():
 
 
 @pytest.mark.parametrize("M,N,K", [(8, 4096, 4096), (1, 1000, 256), (3, 160, 96), (17, 6144, 2560), (32, 2560, 9728),
-                                   (33, 1024, 4096)])
+                                   (33, 1024, 4096), (300, 1000, 512)])
 def test_q8_matmul_vs_oracle(M, N, K):
     r = np.random.default_rng(M * 7 + N)
     Wq = O.quantize_q8_0_ref(r.normal(0, 0.02, (N, K)).astype(np.float32))
@@ -94,6 +94,10 @@ def test_q8_epilogues_and_row_invariance():
     for i in (0, 16, 32):  # each row alone equals its row in the 33-row matmul, bit for bit
         Yi, _ = gemm_q8(Wq, N, K, X[i:i + 1], wbuf=wbuf)
         assert np.array_equal(Yi[0].view(np.uint32), Y[i].view(np.uint32))
+    # 280 rows (row tiles in pairs, from other offsets) hold the same 33 rows' results
+    Xl = np.concatenate([r.normal(0, 1, (200, K)).astype(np.float32), X, X[:47]])
+    Yl, _ = gemm_q8(Wq, N, K, Xl, wbuf=wbuf)
+    assert np.array_equal(Yl[200:233].view(np.uint32), Y.view(np.uint32))
     y0 = r.normal(0, 1, (33, N)).astype(np.float32)
     Ya, _ = gemm_q8(Wq, N, K, X, epi=1, y0=y0, wbuf=wbuf)
     assert np.allclose(Ya, y0 + Y, rtol=1e-6, atol=1e-6)
