@@ -380,7 +380,8 @@ def bench_prefill(args):
     g = kernels.get("gemm")
     roof_mfma = {"kernel": "k_q4_gemm", "bound": "mfma", "achieved": round(flop / (g["ms_per_step"] * 1e-3) / 1e12, 1),
                  "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
-                 "frac": round(flop / (g["ms_per_step"] * 1e-3) / MFMA_F16_PEAK, 4), "traffic": None,
+                 "frac": round(flop / (g["ms_per_step"] * 1e-3) / MFMA_F16_PEAK, 4),
+                 "traffic": profile_traffic("prefill_qwen3_4b_2048_rows512_traffic.json", "k_q4_gemm"),
                  "flop_per_launch": round(flop / g["launches_per_step"]),
                  "us_per_launch": g["us_per_launch"]} if g else None
     cpu = None
