@@ -43,6 +43,13 @@ long snx_chain_count(const sn_engine* e, int dropped);
 // The attention work list's form: -1 chosen per step (the default), 0 one item per 256-cell chunk and a merge, 1
 // whole groups (one workgroup per (group, KV head) walks the whole context: no merge). Every form gives the same bits.
 void snx_attn_mode(sn_engine* e, int mode);
+// The graph key sn_step forms for a step of R rows (slots seq, positions pos; every row sampled in order) on an engine
+// of H query heads, KVH KV heads and page_cells-cell pages with attention form `mode` (as snx_attn_mode), computed on
+// the host alone (no device): two steps replay one captured graph exactly when their keys are equal. Writes at most
+// cap values to key and the attention form chosen to *whole (when given); returns the key's length, or -1 for bad
+// arguments. (Host code only; for checks of the replay rule.)
+int snx_step_key(int H, int KVH, int page_cells, int mode, int R, const int32_t* seq, const int32_t* pos,
+                 int64_t* key, int cap, int* whole);
 
 // Give slot `slot` the cells [0, n) (pages as a step would take them) holding seeded N(0, 1) fp16 K and V in every
 // layer: a context "already in the cache" for throughput runs (what the cells hold does not change what a step

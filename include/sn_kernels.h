@@ -52,6 +52,10 @@ int snk_quant_act(const float* d_x, int M, int K, int ldx, const float* d_norm_w
 // the matmul; epi: store, add into d_y, or SwiGLU over interleaved gate/up stripe pairs (N = 2F, output F columns).
 // d_ws: k-slice partial sums of snk_q4_workspace_bytes(M, N, K) bytes (may be 0). 0, or -1 (workspace too small).
 size_t snk_q4_workspace_bytes(int M, int N, int K);
+// the launch plan of an N x K matrix of weight type wt (2 Q4_0, 8 Q8_0), which depends on (N, K, wt) alone: 16-row
+// stripes per wavefront (*spw: 2 for Q4_0 matrices of LM-head width, at least 6144 stripes; else 1) and k-slices
+// (*ks). 0, or -1 (bad shape or type).
+int snk_q4_plan(int N, int K, int wt, int* spw, int* ks);
 int snk_q4_gemm(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi, void* d_ws,
                 size_t ws_bytes, void* stream);
 // average device time (microseconds) of one raw matmul launch (the k-slice sums into d_ws, as a decode step runs it:

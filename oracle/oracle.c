@@ -125,10 +125,16 @@ void or_quantize_row_q8_0_ref(const float* x, uint8_t* y, int64_t k) {
 }
 
 // ggml_vec_dot_q8_0_q8_0 (generic form): per block the integer sum of qw * qx, then sumf += sumi * (dw * dx)
+// Test hook (or_set_sum_order): the Q4_0 / Q8_0 dots add their blocks' fp32 terms last block first. The same
+// arithmetic in another summation order: how far two correct implementations drift apart over a model's layers.
+static int g_sum_reverse = 0;
+void or_set_sum_order(int reverse) { g_sum_reverse = reverse != 0; }
+
 float or_vec_dot_q8_0_q8_0(int64_t k, const uint8_t* w, const uint8_t* xq) {
     const int64_t nb = k / QK;
     float sumf = 0.0f;
-    for (int64_t ib = 0; ib < nb; ++ib) {
+    for (int64_t jb = 0; jb < nb; ++jb) {
+        const int64_t ib = g_sum_reverse ? nb - 1 - jb : jb;
         const uint8_t* bw = w + ib * 34;
         const uint8_t* bx = xq + ib * 34;
         int sumi = 0;
@@ -289,7 +295,8 @@ void or_mul_mat_q8_0(const uint8_t* W, int64_t N, int64_t K, const float* X, int
 float or_vec_dot_q4_0_q8_0(int64_t k, const uint8_t* w, const uint8_t* xq) {
     const int64_t nb = k / QK;
     float sumf = 0.0f;
-    for (int64_t ib = 0; ib < nb; ++ib) {
+    for (int64_t jb = 0; jb < nb; ++jb) {
+        const int64_t ib = g_sum_reverse ? nb - 1 - jb : jb;
         const uint8_t* bw = w + ib * 18;
         const uint8_t* bx = xq + ib * 34;
         int sumi0 = 0, sumi1 = 0;
@@ -551,6 +558,28 @@ void or_moe_route(const float* logits, int n_expert, int k, int32_t* ids, float*
     free(p);
 }
 
+// Test hook (or_moe_trace): each routing's margin, the smallest router logit chosen minus the largest one not chosen
+// (a near tie there is where two implementations may pick different experts), in call order: layer by layer, row by row.
+static float* g_moe_margin = NULL;
+static int g_moe_cap = 0, g_moe_n = 0;
+void or_moe_trace(float* margins, int cap) {
+    g_moe_margin = margins;
+    g_moe_cap = margins ? cap : 0;
+    g_moe_n = 0;
+}
+int or_moe_trace_count(void) { return g_moe_n; }
+static void moe_note_margin(const float* lg, int n_expert, const int32_t* ids, int k) {
+    if (!g_moe_margin || g_moe_n >= g_moe_cap) return;
+    float lo = INFINITY, hi = -INFINITY;
+    for (int j = 0; j < k; ++j) lo = fminf(lo, lg[ids[j]]);
+    for (int i = 0; i < n_expert; ++i) {
+        int chosen = 0;
+        for (int j = 0; j < k; ++j) chosen |= ids[j] == i;
+        if (!chosen) hi = fmaxf(hi, lg[i]);
+    }
+    g_moe_margin[g_moe_n++] = lo - hi;
+}
+
 int or_accept(const int32_t* draft, const int32_t* target, int k) {
     int a = 0;
     while (a < k && draft[a] == target[a]) ++a;
@@ -633,10 +662,14 @@ static void block(const or_qwen3* m, const or_layer* L, or_kv* kv, int kl, int R
             float w[64];
             for (int e = 0; e < NE; ++e) {
                 float s = 0.0f;
-                for (int i = 0; i < E; ++i) s += L->router[(size_t) e * E + i] * h[(size_t) r * E + i];
+                for (int ii = 0; ii < E; ++ii) {
+                    const int i = g_sum_reverse ? E - 1 - ii : ii;
+                    s += L->router[(size_t) e * E + i] * h[(size_t) r * E + i];
+                }
                 lg[e] = s;
             }
             or_moe_route(lg, NE, K, ids, w);
+            moe_note_margin(lg, NE, ids, K);
             float* acc = (float*) calloc((size_t) E, 4);
             for (int j = 0; j < K; ++j) {
                 mm(m, L->eg + ids[j] * gsz, FE, E, h + (size_t) r * E, 1, g, nthreads);

@@ -60,6 +60,11 @@ float or_vec_dot_q4_0_q8_0(int64_t k, const uint8_t* w, const uint8_t* xq);
 void or_quantize_row_q8_0_ref(const float* x, uint8_t* y, int64_t k);
 float or_vec_dot_q8_0_q8_0(int64_t k, const uint8_t* w, const uint8_t* xq);
 void or_mul_mat_q8_0(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nthreads);
+// Test hook: reverse 1 makes or_vec_dot_q4_0_q8_0 and or_vec_dot_q8_0_q8_0 (and so every Q4_0 / Q8_0 mul_mat and model
+// step; also the fp32 MoE router's dots) add their terms last first; 0 (the default) is ggml's order. Two implementations of the same
+// arithmetic that differ only in summation order: the distance between them over a whole model is the end-to-end
+// bound any other implementation (the GPU's) can be held to.
+void or_set_sum_order(int reverse);
 // W: N rows of K/32 Q4_0 blocks. nthreads <= 0: all cores (OpenMP).
 void or_mul_mat_q4_0(const uint8_t* W, int64_t N, int64_t K, const float* X, int64_t M, float* Y, int nthreads);
 // The same product in fp64 over dequantized W and the fp32 X as given (no activation quantization): the
@@ -178,6 +183,12 @@ void or_mtp_guess(const or_qwen3* m, or_kv* kv, int seq, int32_t tok, int pos, i
 // MoE FFN routing of one row: softmax over n_expert router logits, the k largest (ties: lower id), weights
 // renormalised by their sum floored at 6.103515625e-5 (kernels.metal:3419-3467).
 void or_moe_route(const float* logits, int n_expert, int k, int32_t* ids, float* w);
+
+// Test hook: while margins is set, every MoE routing of or_qwen3_step records its margin, the smallest router logit
+// chosen minus the largest one not chosen, into margins (at most cap, in call order: layer by layer, row by row);
+// or_moe_trace_count() is the number recorded. NULL turns it off.
+void or_moe_trace(float* margins, int cap);
+int or_moe_trace_count(void);
 
 // Greedy acceptance of one sequence's verify rows: target[i] is row i's argmax (row 0: the last accepted token's
 // row, row i: draft i's row), draft[i] (i < k) the i-th draft. Returns the accepted count a in 0..k; the tokens the

@@ -58,6 +58,11 @@ def _declare(L):
     L.or_vec_dot_q6_K_q8_K.restype = C.c_float
     L.or_mul_mat_q6_K.argtypes = [P, I64, I64, P, I64, P, C.c_int]
     L.or_mul_mat_q4_0.argtypes = [P, I64, I64, P, I64, P, C.c_int]
+    L.or_set_sum_order.argtypes = [C.c_int]
+    L.or_set_sum_order.restype = None
+    L.or_moe_trace.argtypes = [P, C.c_int]
+    L.or_moe_trace.restype = None
+    L.or_moe_trace_count.restype = C.c_int
     L.or_mul_mat_q4_0_f64.argtypes = [P, I64, I64, P, I64, P, C.c_int]
     L.or_rmsnorm.argtypes = [P, P, I64, C.c_float, P]
     L.or_silu.argtypes = [C.c_float]
@@ -89,6 +94,30 @@ def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
     """RNE fp16 bits (uint16) of fp32 values, via the oracle's F16C conversion."""
     x = np.ascontiguousarray(x, np.float32)
     return np.array([lib().or_f32_to_f16(float(v)) for v in x.ravel()], np.uint16).reshape(x.shape)
+
+
+def set_sum_order(reverse: bool) -> None:
+    """Test hook: the Q4_0 / Q8_0 dots add their blocks' fp32 terms last block first (True) or in ggml's order."""
+    lib().or_set_sum_order(int(reverse))
+
+
+class MoeTrace:
+    """Test hook: while open, every MoE routing of a model step records its margin (the smallest router logit chosen
+    minus the largest not chosen), layer by layer, row by row; .margins() after the steps."""
+
+    def __init__(self, cap=1 << 20):
+        self.buf = np.zeros(cap, np.float32)
+
+    def __enter__(self):
+        lib().or_moe_trace(_p(self.buf), self.buf.size)
+        return self
+
+    def __exit__(self, *a):
+        self.n = lib().or_moe_trace_count()
+        lib().or_moe_trace(None, 0)
+
+    def margins(self):
+        return self.buf[:self.n].copy()
 
 
 # ---- Q4_0 / Q8_0 ----

@@ -741,6 +741,12 @@ struct AttnList {
     int n_items = 0, n_mrows = 0;
     bool whole = false;
     double bytes = 0.0, merge_bytes = 0.0;
+    // every value of the list the attention launches take, for a graph key: the form (whole groups launch another
+    // kernel and no merge), the item and merge-row counts (grid sizes) and the staging offsets of the three arrays
+    void key(std::vector<int64_t>& k) const {
+        k.insert(k.end(), {(int64_t) whole, (int64_t) n_items, (int64_t) n_mrows, (int64_t) o_grp, (int64_t) o_itm,
+                           (int64_t) o_mrow});
+    }
 };
 
 AttnList attn_list(sn_engine* e, Stage& S, int R, const int32_t* seq, const int32_t* pos) {
@@ -1189,46 +1195,67 @@ bool rows_bad(const sn_engine* e, int R, const int32_t* tok, const int32_t* seq,
 
 namespace {
 
+// The host half of a step: its inputs placed in the staging buffer (tokens, slots, positions, output rows, no-end
+// flags, the attention work list, the guess head's row sources) and the key of its device work, which holds every host
+// value the step's launches take, so that a cached graph is replayed only for a step that would launch exactly the
+// same kernels with the same arguments.
+struct StepStage {
+    size_t o_tok = 0, o_seq = 0, o_pos = 0, o_out = 0, o_skip = 0, o_src = 0, o_keep = 0;
+    int nkeep = 0;  // (slot, row) pairs whose head state is kept
+    bool fill = false;
+    AttnList al;
+    std::vector<int64_t> key;
+};
+
+void stage_step(sn_engine* e, Stage& S, StepStage& ss, int R, const int32_t* tok, const int32_t* seq,
+                const int32_t* pos, int n_out, const int32_t* out_rows) {
+    ss.fill = e->has_nextn && e->guess_on;
+    std::vector<int32_t> tz;
+    if (!tok) tz.assign(R, 0);
+    ss.o_tok = S.put(tok ? tok : tz.data(), (size_t) R * 4);
+    ss.o_seq = S.put(seq, (size_t) R * 4);
+    ss.o_pos = S.put(pos, (size_t) R * 4);
+    ss.o_out = S.put(out_rows, (size_t) n_out * 4);
+    std::vector<uint8_t> skip(n_out + 1, 0);
+    for (int j = 0; j < n_out; ++j) skip[j] = e->no_end[seq[out_rows[j]]];
+    ss.o_skip = S.put(skip);
+    ss.al = attn_list(e, S, R, seq, pos);
+    if (ss.fill) {
+        std::vector<int32_t> src, keep;
+        head_sources(e, R, seq, pos, src, keep);
+        ss.o_src = S.put(src);
+        ss.o_keep = S.put(keep);
+        ss.nkeep = (int) keep.size() / 2;
+    }
+    ss.key = {1, R, n_out, ss.fill, e->want_probs, (int64_t) e->eog.size(), ss.nkeep, (int64_t) ss.o_tok,
+              (int64_t) ss.o_seq, (int64_t) ss.o_pos, (int64_t) ss.o_out, (int64_t) ss.o_skip, (int64_t) ss.o_src,
+              (int64_t) ss.o_keep};
+    ss.al.key(ss.key);
+}
+
 // One step's device work, staged into the engine's buffer set and enqueued on the stream with the tokens'
 // device-to-host copy; the set's end event recorded, nothing waited for. tok_dev: the rows' tokens are that device
 // array (a queued step is fed the step before's outputs), else tok. Returns the device work's code (0, or -1 when a
 // launch was refused), or -2 when the staging failed (nothing enqueued).
 int enqueue_step(sn_engine* e, int R, const int32_t* tok, const int32_t* tok_dev, const int32_t* seq, const int32_t* pos,
                  int n_out, const int32_t* out_rows) {
-    const bool fill = e->has_nextn && e->guess_on;
     Stage S{e};
-    std::vector<int32_t> tz;
-    if (!tok) tz.assign(R, 0);
-    const size_t o_tok = S.put(tok ? tok : tz.data(), (size_t) R * 4), o_seq = S.put(seq, (size_t) R * 4);
-    const size_t o_pos = S.put(pos, (size_t) R * 4), o_out = S.put(out_rows, (size_t) n_out * 4);
-    std::vector<uint8_t> skip(n_out + 1, 0);
-    for (int j = 0; j < n_out; ++j) skip[j] = e->no_end[seq[out_rows[j]]];
-    const size_t o_skip = S.put(skip);
-    const AttnList al = attn_list(e, S, R, seq, pos);
-    std::vector<int32_t> src, keep;
-    size_t o_src = 0, o_keep = 0;
-    if (fill) {
-        head_sources(e, R, seq, pos, src, keep);
-        o_src = S.put(src);
-        o_keep = S.put(keep);
-    }
+    StepStage ss;
+    stage_step(e, S, ss, R, tok, seq, pos, n_out, out_rows);
     e->prof_recs.clear();
     if (stage_copy(e, S) != 0) return -2;
-    if (tok_dev && hipMemcpyAsync(e->d_stage + o_tok, tok_dev, (size_t) R * 4, hipMemcpyDeviceToDevice, e->st) != hipSuccess)
+    if (tok_dev && hipMemcpyAsync(e->d_stage + ss.o_tok, tok_dev, (size_t) R * 4, hipMemcpyDeviceToDevice, e->st) != hipSuccess)
         return -2;
-    const int32_t* d_tok = S.dev<const int32_t>(o_tok);
-    const int32_t* d_seq = S.dev<const int32_t>(o_seq);
-    const int32_t* d_pos = S.dev<const int32_t>(o_pos);
-
-    std::vector<int64_t> key = {1, R, n_out, fill, e->want_probs, (int64_t) e->eog.size(), (int64_t) keep.size(),
-                                (int64_t) o_tok, (int64_t) o_seq, (int64_t) o_pos, (int64_t) o_out, (int64_t) o_skip,
-                                (int64_t) al.o_grp, (int64_t) al.o_itm, al.n_items, (int64_t) o_src, (int64_t) o_keep};
-    const int drc = run_device(e, std::move(key), [&](Dev& d) {
+    const int32_t* d_tok = S.dev<const int32_t>(ss.o_tok);
+    const int32_t* d_seq = S.dev<const int32_t>(ss.o_seq);
+    const int32_t* d_pos = S.dev<const int32_t>(ss.o_pos);
+    const AttnList& al = ss.al;
+    const int drc = run_device(e, std::move(ss.key), [&](Dev& d) {
         d.model(R, d_tok, d_seq, d_pos, S, al);
-        if (fill && d.rc == 0)
-            d.head_fill(R, d_tok, d_seq, d_pos, S.dev<const int32_t>(o_src), (int) keep.size() / 2,
-                        S.dev<const int32_t>(o_keep));
-        if (n_out > 0 && d.rc == 0) d.outputs(e->x, n_out, S.dev<const int32_t>(o_out), S.dev<const uint8_t>(o_skip));
+        if (ss.fill && d.rc == 0)
+            d.head_fill(R, d_tok, d_seq, d_pos, S.dev<const int32_t>(ss.o_src), ss.nkeep, S.dev<const int32_t>(ss.o_keep));
+        if (n_out > 0 && d.rc == 0)
+            d.outputs(e->x, n_out, S.dev<const int32_t>(ss.o_out), S.dev<const uint8_t>(ss.o_skip));
     });
     int rc = drc;
     if (drc == 0 && n_out > 0) {
@@ -1520,6 +1547,37 @@ extern "C" void snx_graphs(sn_engine* e, int on) {
     e->graphs = on != 0;
     for (auto& g : e->gcache) hipGraphExecDestroy(g.ex);
     e->gcache.clear();
+}
+
+extern "C" int snx_step_key(int H, int KVH, int page_cells, int mode, int R, const int32_t* seq, const int32_t* pos,
+                            int64_t* key, int cap, int* whole) {
+    if (H <= 0 || KVH <= 0 || H % KVH || 16 % (H / KVH) || (page_cells != 32 && page_cells != 64) || R <= 0 ||
+        mode < -1 || mode > 1)
+        return -1;
+    int slots = 0, cells = 0;
+    for (int r = 0; r < R; ++r) {
+        if (seq[r] < 0 || pos[r] < 0) return -1;
+        slots = std::max(slots, seq[r] + 1);
+        cells = std::max(cells, pos[r] + 1);
+    }
+    sn_engine e;  // the fields the host half of a step reads; nothing on the device
+    e.H = H, e.KVH = KVH, e.D = 128, e.QD = H * 128, e.KD = KVH * 128;
+    e.page_cells = page_cells, e.attn_mode = mode, e.slots = slots, e.max_rows = R;
+    e.max_chunks = (cells + ATT_CHUNK - 1) / ATT_CHUNK;
+    e.no_end.assign(slots, 0);
+    e.stage_bytes = (size_t) R * (64 + sizeof(AttnGroup) + (size_t) e.max_chunks * sizeof(AttnItem)) + 4096;
+    std::vector<uint8_t> host(e.stage_bytes);
+    e.h_stage = host.data();
+    std::vector<int32_t> tok(R, 0), rows(R);
+    for (int r = 0; r < R; ++r) rows[r] = r;
+    Stage S{&e};
+    StepStage ss;
+    stage_step(&e, S, ss, R, tok.data(), seq, pos, R, rows.data());
+    e.h_stage = nullptr;
+    if (S.over) return -1;
+    if (whole) *whole = ss.al.whole ? 1 : 0;
+    for (int i = 0; i < (int) ss.key.size() && i < cap; ++i) key[i] = ss.key[i];
+    return (int) ss.key.size();
 }
 
 extern "C" void snx_prof(sn_engine* e, int on) {

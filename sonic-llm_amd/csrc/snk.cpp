@@ -105,6 +105,14 @@ extern "C" int snk_quant_act(const float* d_x, int M, int K, int ldx, const floa
 
 extern "C" size_t snk_q4_workspace_bytes(int M, int N, int K) { return q4_workspace_bytes(M, N, K); }
 
+extern "C" int snk_q4_plan(int N, int K, int wt, int* spw, int* ks) {
+    if (N <= 0 || K <= 0 || K % 32 || (wt != WT_Q4_0 && wt != WT_Q8_0)) return -1;
+    const GemmPlan p = q4_plan(N, K, wt);
+    if (spw) *spw = p.spw;
+    if (ks) *ks = p.ks;
+    return 0;
+}
+
 extern "C" int snk_q4_gemm(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi,
                            void* d_ws, size_t ws_bytes, void* stream) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 32 || epi < 0 || epi > 2) return -1;

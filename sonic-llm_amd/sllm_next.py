@@ -110,6 +110,7 @@ SNK_API = [
     ("snk_q8_gemm", I, [P, P, I, I, I, P, I, I, P, C.c_size_t, P]),
     ("snk_quant_act", I, [P, I, I, I, P, C.c_float, P, P]),
     ("snk_q4_workspace_bytes", C.c_size_t, [I, I, I]),
+    ("snk_q4_plan", I, [I, I, I, C.POINTER(I), C.POINTER(I)]),
     ("snk_q4_gemm", I, [P, P, I, I, I, P, I, I, P, C.c_size_t, P]),
     ("snk_q4_gemm_time", C.c_double, [P, I, P, I, I, I, P, I, P, C.c_size_t, I, P]),
     ("snk_attn_new", P, [I, P, P, I, I, I, I, CH, I]),
@@ -130,6 +131,7 @@ SNK_API = [
 EXT_API = [
     ("snx_graphs", None, [P, I]),
     ("snx_attn_mode", None, [P, I]),
+    ("snx_step_key", I, [I, I, I, I, I, P, P, P, I, P]),
     ("snx_chain_count", C.c_long, [P, I]),
     ("snx_graph_count", C.c_long, [P, I]),
     ("snx_prof", None, [P, I]),
@@ -193,6 +195,14 @@ QWEN3_30B_A3B = dict(n_layer=48, n_embd=2048, n_head=32, n_head_kv=4, n_ff=6144,
                      n_expert_used=8, n_ff_exp=768)
 
 
+def q4_plan(N: int, K: int, wt: int = 2) -> tuple:
+    """snk_q4_plan (host only): (stripes per wavefront, k-slices) of an N x K matrix's matmul launches."""
+    spw, ks = C.c_int(), C.c_int()
+    if lib().snk_q4_plan(N, K, wt, C.byref(spw), C.byref(ks)) != 0:
+        raise SnError(-1, "snk_q4_plan: bad shape or type")
+    return spw.value, ks.value
+
+
 def write_model(path: str, cfg: ModelCfg, seed: int, nthreads: int = 0) -> None:
     call(lib().snx_write_model, path.encode(), C.byref(cfg), seed, nthreads)
 
@@ -202,6 +212,19 @@ def quantize_q4_0(x: np.ndarray) -> np.ndarray:
     out = np.empty(x.size // 32 * 18, np.uint8)
     lib().snx_quantize_q4_0(_p(x), _p(out), x.size)
     return out.reshape(x.shape[:-1] + (x.shape[-1] // 32 * 18,))
+
+
+def step_key(H: int, KVH: int, page_cells: int, mode: int, seq, pos):
+    """snx_step_key (host only): the graph key sn_step forms for a step of rows (seq, pos), every row sampled, and
+    whether its attention runs as whole groups. Two steps replay one captured graph exactly when their keys are equal."""
+    seq = np.ascontiguousarray(seq, np.int32)
+    pos = np.ascontiguousarray(pos, np.int32)
+    key = np.zeros(64, np.int64)
+    whole = C.c_int(-1)
+    n = lib().snx_step_key(H, KVH, page_cells, mode, seq.size, _p(seq), _p(pos), _p(key), key.size, C.byref(whole))
+    if n < 0:
+        raise SnError(n, "snx_step_key: bad arguments")
+    return tuple(int(v) for v in key[:n]), bool(whole.value)
 
 
 # ---- sn.h ----

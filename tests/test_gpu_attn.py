@@ -24,7 +24,7 @@ def setup_module(module):
     U.torch().cuda.init()
 
 
-def config2_case(seed=2, S_=32, page=32, lo=256, hi=4096, n_share=8, share_cells=1024):
+def config2_case(seed=2, S_=32, page=32, lo=256, hi=4096, n_share=8, share_cells=1024, kvh=KVH):
     """BASELINE.json configs[1]: 32 sequences, ctx ~ U[256, 4096], 32-token pages from a seeded permutation of one pool;
     sequences 0..7 share their first 1024 cells (their own ctx drawn from [1024, 4096] so each holds the prefix)."""
     r = np.random.default_rng(seed)
@@ -43,22 +43,23 @@ def config2_case(seed=2, S_=32, page=32, lo=256, hi=4096, n_share=8, share_cells
             else:
                 pt[s, c] = perm[k]
                 k += 1
-    kpool = r.standard_normal((need, KVH, page, D), dtype=np.float32).astype(np.float16).view(np.uint16)
-    vpool = r.standard_normal((need, KVH, page, D), dtype=np.float32).astype(np.float16).view(np.uint16)
+    kpool = r.standard_normal((need, kvh, page, D), dtype=np.float32).astype(np.float16).view(np.uint16)
+    vpool = r.standard_normal((need, kvh, page, D), dtype=np.float32).astype(np.float16).view(np.uint16)
     q = r.standard_normal((S_, H, D), dtype=np.float32)
     return q, np.arange(S_, dtype=np.int32), (ctx - 1).astype(np.int32), kpool, vpool, pt, page
 
 
 def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None, whole=None, mode=-1):
     """whole: when given, the work list's form the planner chose (whole groups, or per-chunk items and the merge) is
-    checked too; mode: the form forced (snk_attn_new_mode), -1 the planner's"""
+    checked too; mode: the form forced (snk_attn_new_mode), -1 the planner's. The KV head count is the pools'."""
     L = S.lib()
+    kvh = kpool.shape[1]
     err = __import__("ctypes").create_string_buffer(256)
     seq = np.ascontiguousarray(seq, np.int32)
     pos = np.ascontiguousarray(pos, np.int32)
     for s_, p_ in zip(seq, pos):  # every cell a row reads has a page (host-side check before the launch)
         assert np.all(pt[s_, :p_ // page + 1] >= 0)
-    plan = L.snk_attn_new_mode(len(seq), seq.ctypes.data, pos.ctypes.data, H, KVH, pt.shape[1], page, mode, err, 256)
+    plan = L.snk_attn_new_mode(len(seq), seq.ctypes.data, pos.ctypes.data, H, kvh, pt.shape[1], page, mode, err, 256)
     assert plan, err.value
     if whole is not None:
         assert L.snk_attn_whole(plan) == int(whole)
@@ -163,3 +164,37 @@ def test_whole_group_list_equals_chunk_list_bitwise(page, lo, hi, auto):
     assert np.array_equal(auto_out.view(np.uint32), whole.view(np.uint32))
     ref = O.paged_attn(q, seq, pos, KVH, kp, vp, pg, pt, scale)
     assert np.all(np.abs(whole - ref) <= ATOL + RTOL * np.abs(ref))
+
+
+@pytest.mark.parametrize("kvh", [4, 2, 16])
+def test_gqa_group_sizes(kvh):
+    """Other query-group sizes G = H / KVH: 8 (configs[4], Qwen3-30B-A3B: 32 query heads on 4 KV heads, so a query
+    group holds 2 rows of a sequence), 16 (one row a group) and 2 (up to 8 rows). Decode rows of 32 sequences with
+    C5-like contexts (about 2048 cells, 4 sharers of a 1024-cell prefix), then 4 verify rows of 8 sequences each
+    (split into groups of 16 / G rows): against the fp32 and fp64 oracle, verify rows bit for bit equal to the same
+    rows alone, and both work-list forms bit for bit equal (the kernels index rows and heads by G; attn_part, any G,
+    kernels.metal:1135-1200; fa2_128_g8, kernels.metal:2674-2770)."""
+    q, seq, pos, kp, vp, pt, page = config2_case(seed=31 + kvh, S_=32, page=64, lo=1500, hi=2600, n_share=4,
+                                                 kvh=kvh)
+    scale = 1 / math.sqrt(D)
+    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    got = attn_gpu(q, seq, pos, kp, vp, pt, page, scale, bufs)
+    ref = O.paged_attn(q, seq, pos, kvh, kp, vp, page, pt, scale)
+    err = np.abs(got - ref)
+    print(f"G={H // kvh} decode: max abs err {err.max():.3g}")
+    assert np.all(err <= ATOL + RTOL * np.abs(ref))
+    ref64 = O.paged_attn(q, seq, pos, kvh, kp, vp, page, pt, scale, f64=True)
+    assert np.max(np.abs(got - ref64)) < 1e-4
+    for mode in (0, 1):
+        forced = attn_gpu(q, seq, pos, kp, vp, pt, page, scale, bufs, mode=mode)
+        assert np.array_equal(forced.view(np.uint32), got.view(np.uint32)), mode
+    # verify rows: 4 consecutive positions of each of 8 sequences
+    vseq = np.repeat(seq[:8], 4).astype(np.int32)
+    vpos = (np.repeat(pos[:8] - 3, 4) + np.tile(np.arange(4), 8)).astype(np.int32)
+    qv = np.random.default_rng(kvh).standard_normal((32, H, D), dtype=np.float32)
+    grouped = attn_gpu(qv, vseq, vpos, kp, vp, pt, page, scale, bufs)
+    ref = O.paged_attn(qv, vseq, vpos, kvh, kp, vp, page, pt, scale)
+    assert np.all(np.abs(grouped - ref) <= ATOL + RTOL * np.abs(ref))
+    for i in (0, 1, 2, 3, 13, 31):
+        one = attn_gpu(qv[i:i + 1].copy(), vseq[i:i + 1].copy(), vpos[i:i + 1].copy(), kp, vp, pt, page, scale, bufs)
+        assert np.array_equal(one[0].view(np.uint32), grouped[i].view(np.uint32)), i

@@ -1,0 +1,264 @@
+"""The benchmark configurations' own shapes, end to end through sn.h on the GPU against the oracle.
+
+  * the Qwen3-4B-architecture decode step, all 36 layers, 32 sequences at position 2048 over seeded
+    cached cells (the reference's b32 scenario, qbench.m:132-168);
+  * the fused draft-verify step (k = 3, 8 sequences at 4096 cells, seeded ~60% forced acceptance) on a
+    Qwen3-4B-width model with 2 layers and a guess head (draft.rs:135-178, take.rs:339-357);
+  * the Qwen3-30B-A3B-architecture MoE decode step (128 experts, top-8, 4 KV heads: G = 8), 32 sequences
+    at 2048 cells, 2 layers (sn_layers.inc.h:129-144).
+
+The oracle's KV cache is given the engine's own cells (sn_kv_save), so both start from the same bytes. The GPU and the
+oracle sum in different fp32 orders, so now and then an fp16 cell or a Q8_0 activation rounds the other way, and over
+layers that moves the logits by the activations' Q8_0 noise (a perturbation that flips no rounding changes nothing:
+every matmul input is re-quantized). The bar is therefore set by the oracle itself: the same oracle step summed in
+another order (Drift). North_star asks for identical tokens wherever the top-2 gap exceeds 1e-4; no implementation
+whose summation order differs from ggml's can hold that where the gap is inside the drift, and each test prints how
+many rows clear 1e-4 and how many of those agree, for the GPU and for the reversed oracle.
+"""
+import numpy as np
+import pytest
+
+import sllm_next as S
+from oracle import oracle as O
+from oracle.gguf import GGUF
+from tests import gpu_util as U
+
+pytestmark = pytest.mark.gpu
+
+
+def setup_module(module):
+    U.torch().cuda.init()
+
+
+def load_cells(eng, ref, slots, n):
+    """The engine's cells [0, n) of each slot (every cache layer) into the oracle's cache."""
+    L = ref.L + ref.n_mtp
+    for s in slots:
+        a = eng.kv_save(int(s), n).reshape(L, 2, n, ref.KVH, ref.D)
+        ref.k[s, :, :n] = a[:, 0]
+        ref.v[s, :, :n] = a[:, 1]
+
+
+class Drift:
+    """The GPU's output rows against the oracle's, measured against the oracle's own drift: the same oracle step run
+    with its Q4_0 / Q8_0 dots and MoE router dots summed last term first (or_set_sum_order). Both orders are exact
+    restatements of one arithmetic, so their distance is what any implementation with another fp32 summation order
+    (the GPU's) shows.
+
+      * logits: the GPU's mean |difference| within SLACK x the reversed oracle's mean, its max within SLACK x its max;
+      * tokens: identical on every row whose top-2 gap exceeds twice the larger of the two drifts (no summation order
+        moves a logit that far), and, as a check of the GPU's argmax, on every row whose gap exceeds twice that row's
+        own largest GPU difference;
+      * MoE rows whose top-k routing is a near tie in some layer (the oracle's smallest chosen router logit within TIE
+        of the largest unchosen one) may take another expert in either implementation, which moves their logits by
+        far more than the drift (the reversed oracle does it too): they are left out of the logit bars, and every row
+        of the GPU outside SLACK x the drift must be one of them;
+      * reported: rows whose top-2 gap exceeds 1e-4 (north_star's bar) and how many of those agree, for the GPU and
+        for the reversed oracle."""
+
+    SLACK = 2.0
+    TIE = 1e-2
+
+    def __init__(self):
+        self.gpu, self.rev, self.tie_rows = [], [], []
+        self.rows = self.over_1e4 = self.same_gpu = self.same_rev = self.checked = 0
+
+    def add(self, got_tok, got_logits, ref_tok, ref_logits, rev_tok, rev_logits, margins=None):
+        dg, dr = np.abs(got_logits - ref_logits), np.abs(rev_logits - ref_logits)
+        tie = np.zeros(len(got_tok), bool) if margins is None else margins < self.TIE
+        self.gpu.append(dg[~tie])
+        self.rev.append(dr[~tie])
+        for j in np.nonzero(tie)[0]:
+            self.tie_rows.append((float(margins[j]), float(dg[j].max()), float(dr[j].max())))
+        lim = 2 * max(dg[~tie].max(initial=0.0), dr[~tie].max(initial=0.0))
+        for j in range(len(got_tok)):
+            _, v1, _, v2, _ = O.top2(ref_logits[j])
+            gap = v1 - v2
+            self.rows += 1
+            if gap > 1e-4:
+                self.over_1e4 += 1
+                self.same_gpu += int(got_tok[j] == ref_tok[j])
+                self.same_rev += int(rev_tok[j] == ref_tok[j])
+            if (gap > lim and not tie[j]) or gap > 2 * dg[j].max():
+                self.checked += 1
+                assert got_tok[j] == ref_tok[j], (j, got_tok[j], ref_tok[j], gap)
+
+    def report(self, name):
+        dg, dr = np.concatenate(self.gpu), np.concatenate(self.rev)
+        print(f"{name}: |logit diff| GPU vs oracle max {dg.max():.3g} mean {dg.mean():.3g}; reversed-order oracle vs "
+              f"oracle max {dr.max():.3g} mean {dr.mean():.3g}; rows {self.rows}, top-2 gap > 1e-4: {self.over_1e4}, of "
+              f"those the same token: GPU {self.same_gpu}, reversed oracle {self.same_rev}; rows whose gap clears the "
+              f"drift (must agree): {self.checked}")
+        if self.tie_rows:
+            t = np.array(self.tie_rows)
+            print(f"  routing near ties (margin < {self.TIE}): {len(t)} rows, margins {np.round(t[:, 0], 5).tolist()}, "
+                  f"their max |logit diff| GPU {np.round(t[:, 1], 3).tolist()}, reversed oracle "
+                  f"{np.round(t[:, 2], 3).tolist()}")
+        assert dg.mean() <= self.SLACK * dr.mean() + 1e-6
+        assert dg.max() <= self.SLACK * dr.max() + 1e-5
+
+
+def oracle_both(step, moe_rows=0, moe_layers=0):
+    """the oracle step run in reversed summation order, then in ggml's order (the state it leaves is ggml order's);
+    with moe_rows, also the ggml-order run's smallest routing margin of each row over its moe_layers layers"""
+    O.set_sum_order(True)
+    try:
+        rev = step()
+    finally:
+        O.set_sum_order(False)
+    if not moe_rows:
+        return step(), rev
+    with O.MoeTrace() as tr:
+        fwd = step()
+    return fwd, rev, tr.margins().reshape(moe_layers, moe_rows).min(0)
+
+
+def test_config3_decode_step_matches_oracle(tmp_path):
+    path = str(tmp_path / "qwen3_4b.gguf")
+    S.write_model(path, S.model_cfg(**S.QWEN3_4B), seed=42)
+    n_seq, ctx = 32, 2048
+    seq = np.arange(n_seq, dtype=np.int32)
+    ref = O.Qwen3(GGUF(path), n_seq=n_seq, ctx=ctx + 2)
+    r = np.random.default_rng(3)
+    drift = Drift()
+    with S.Engine(path, slots=n_seq, ctx=ctx + 64, max_rows=n_seq) as eng:
+        for s in seq:
+            eng.fill_kv(int(s), ctx, seed=42)
+        load_cells(eng, ref, seq, ctx)
+        tok = r.integers(0, ref.V, n_seq).astype(np.int32)
+        for p in (ctx, ctx + 1):  # two decode steps, the second fed the oracle's tokens
+            pos = np.full(n_seq, p, np.int32)
+            got = eng.step(tok, seq, pos, seq)
+            gl = eng.logits(seq)
+            (want, rl, _), (rt, rv, _) = oracle_both(lambda: ref.step(tok, seq, pos, seq))
+            drift.add(got, gl, want, rl, rt, rv)
+            tok = want.astype(np.int32)
+    drift.report("configs[2] decode step (36 layers)")
+
+
+K = 3
+
+
+class MtpRef:
+    """The oracle with the guess head's per-step cell fill and each slot's kept state (mtp_fill, sn_state.inc.h:283-313)
+    and the fused step's drafts, verify rows, acceptance and cut (draft.rs:135-178, take.rs:339-357)."""
+
+    def __init__(self, path, n_seq, ctx):
+        self.m = O.Qwen3(GGUF(path), n_seq=n_seq, ctx=ctx)
+        self.pend = np.zeros((n_seq, self.m.E), np.float32)
+
+    def step(self, tok, seq, pos, out_rows):
+        R = len(tok)
+        hn = np.zeros((R, self.m.E), np.float32)
+        out, lg, _ = self.m.step(tok, seq, pos, out_rows, hn_all=hn)
+        hprev = np.zeros_like(hn)
+        for r in range(R):
+            if r > 0 and seq[r] == seq[r - 1] and pos[r] == pos[r - 1] + 1:
+                hprev[r] = hn[r - 1]
+            elif pos[r] > 0:
+                hprev[r] = self.pend[seq[r]]
+        self.m.mtp_fill(tok, seq, pos, hprev)
+        for r in range(R):
+            if r + 1 == R or not (seq[r + 1] == seq[r] and pos[r + 1] == pos[r] + 1):
+                self.pend[seq[r]] = hn[r]
+        return out, lg, hn
+
+    def spec(self, s, last, pos, force):
+        """one sequence's fused step: (drafts, their logits, verify targets, verify logits, accepted count)"""
+        d, dl = self.m.mtp_guess(s, last, pos, K, self.pend[s])
+        tok = np.array([last] + list(d), np.int32)
+        _, vl, hn = self.step(tok, np.full(K + 1, s, np.int32), np.arange(pos, pos + K + 1, dtype=np.int32),
+                              np.arange(K + 1, dtype=np.int32))
+        for i in range(K):
+            if force[i]:
+                vl[i, d[i]] = 3.0e38
+        tg = np.array([O.argmax(vl[i]) for i in range(K + 1)], np.int32)
+        a = int(O.accept(d, tg[:K]))
+        self.m.k[s, :, pos + a + 1:pos + K + 1] = 0
+        self.m.v[s, :, pos + a + 1:pos + K + 1] = 0
+        self.pend[s] = hn[a]
+        return d, dl, tg, vl, a
+
+
+def clear_of(lg, tok, bound):
+    i1, v1, i2, v2, _ = O.top2(lg)
+    return i1 == tok and v1 - v2 > 2 * bound
+
+
+def test_config4_spec_step_matches_oracle(tmp_path):
+    cfg = dict(S.QWEN3_4B, n_layer=2, nextn=1)
+    path = str(tmp_path / "qwen3_4b_mtp.gguf")
+    S.write_model(path, S.model_cfg(**cfg), seed=43)
+    n_seq, ctx, steps = 8, 4096, 3
+    seq = np.arange(n_seq, dtype=np.int32)
+    ref = MtpRef(path, n_seq, ctx + 1 + (K + 1) * steps)
+    rng = np.random.default_rng(5)
+    drift = Drift()
+    stats = {"decisions": 0, "accepted": 0, "followed": 0}
+    with S.Engine(path, slots=n_seq, ctx=ctx + 64, max_rows=n_seq * (K + 1)) as eng:
+        for s in seq:
+            eng.fill_kv(int(s), ctx, seed=43)
+        load_cells(eng, ref.m, seq, ctx)
+        eng.guess_on(True)
+        # a decode step at position 4096 (the head fills its cell of each row, the slots keep their states)
+        tok = rng.integers(0, ref.m.V, n_seq).astype(np.int32)
+        pos = np.full(n_seq, ctx, np.int32)
+        got = eng.step(tok, seq, pos, seq)
+        pend0 = ref.pend.copy()
+
+        def decode():  # (each run starts from the same kept head states)
+            ref.pend[:] = pend0
+            return ref.step(tok, seq, pos, seq)
+
+        (want, rl, _), (rt, rv, _) = oracle_both(decode)
+        drift.add(got, eng.logits(seq), want, rl, rt, rv)
+        # a draft or verify decision is clear when its top-2 gap exceeds twice the largest drift seen on that step
+        bound = max(np.abs(drift.gpu[0]).max(), np.abs(drift.rev[0]).max())
+        last, pos = want.astype(np.int32), pos + 1
+        alive = [True] * n_seq
+        for _ in range(steps):
+            force = (rng.random((n_seq, K)) < 0.6).astype(np.uint8)
+            n, t = eng.spec_step(seq, last, pos, K, force=force)
+            for s in range(n_seq):
+                d, dl, tg, vl, a = ref.spec(s, last[s], pos[s], force[s])
+                if alive[s]:
+                    same = n[s] == a + 1 and list(t[s, :a + 1]) == list(d[:a]) + [tg[a]]
+                    sure = all(clear_of(dl[j], d[j], bound) for j in range(min(a + 1, K)))
+                    sure = sure and all((i < K and force[s, i]) or clear_of(vl[i], tg[i], bound)
+                                        for i in range(a + 1))
+                    assert same or not sure, (s, n[s], t[s], a, d, tg)
+                    stats["decisions"] += 1
+                    stats["accepted"] += a if same else 0
+                    stats["followed"] += int(same)
+                    alive[s] = same
+                last[s] = tg[a]
+                pos[s] += a + 1
+    drift.report("configs[3] decode step before the draft-verify steps (2 layers + guess head)")
+    print(f"configs[3] fused steps against the oracle (decision bound {bound:.3g}): {stats}")
+    assert stats["followed"] >= 0.75 * stats["decisions"] and stats["accepted"] >= 6
+
+
+def test_config5_moe_step_matches_oracle(tmp_path):
+    cfg = dict(S.QWEN3_30B_A3B, n_layer=2)
+    path = str(tmp_path / "qwen3_30b_a3b.gguf")
+    S.write_model(path, S.model_cfg(**cfg), seed=44)
+    n_seq, ctx = 32, 2048
+    seq = np.arange(n_seq, dtype=np.int32)
+    ref = O.Qwen3(GGUF(path), n_seq=n_seq, ctx=ctx + 2)
+    assert (ref.H, ref.KVH, ref.NE, ref.NEU) == (32, 4, 128, 8)
+    r = np.random.default_rng(4)
+    drift = Drift()
+    with S.Engine(path, slots=n_seq, ctx=ctx + 64, max_rows=n_seq) as eng:
+        for s in seq:
+            eng.fill_kv(int(s), ctx, seed=44)
+        load_cells(eng, ref, seq, ctx)
+        tok = r.integers(0, ref.V, n_seq).astype(np.int32)
+        for p in (ctx, ctx + 1):
+            pos = np.full(n_seq, p, np.int32)
+            got = eng.step(tok, seq, pos, seq)
+            gl = eng.logits(seq)
+            (want, rl, _), (rt, rv, _), margins = oracle_both(lambda: ref.step(tok, seq, pos, seq), n_seq, ref.L)
+            drift.add(got, gl, want, rl, rt, rv, margins)
+            tok = want.astype(np.int32)
+    drift.report("configs[4] MoE decode step (2 layers)")
+    assert len(drift.tie_rows) <= drift.rows // 2

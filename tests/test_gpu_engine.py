@@ -318,6 +318,33 @@ def test_graph_replay_matches_eager(tiny):
         assert ee.graph_count() == (0, 0)
 
 
+def test_graph_key_separates_attention_forms(tmp_path):
+    """Regression: a step whose attention the planner runs as whole groups must not replay the graph of a step with
+    per-chunk items of the same row and item counts. 32 decode rows on an H = 32, KVH = 8 model: at position 100 every
+    row is one chunk (32 items and a merge); at position 3000 the contexts are long and alike, so the auto plan takes
+    whole groups (32 x 8 = 256 workgroups, 32 items, no merge). Both shapes are captured and replayed, in alternation,
+    and every step equals an eager engine's bit for bit."""
+    path = str(tmp_path / "g8.gguf")
+    S.write_model(path, S.model_cfg(n_layer=1, n_embd=256, n_head=32, n_head_kv=8, n_ff=512, n_vocab=1000), seed=21)
+    seq = np.arange(32, dtype=np.int32)
+    assert S.step_key(32, 8, 64, -1, seq, np.full(32, 100, np.int32))[1] is False
+    assert S.step_key(32, 8, 64, -1, seq, np.full(32, 3000, np.int32))[1] is True
+    r = np.random.default_rng(6)
+    with S.Engine(path, slots=32, ctx=3072, max_rows=32) as ge, S.Engine(path, slots=32, ctx=3072, max_rows=32) as ee:
+        ee.graphs(False)
+        for eng in (ge, ee):
+            for s in range(32):
+                eng.fill_kv(s, 3004, seed=77)
+        for it, p in enumerate((100, 3000, 101, 3001, 102)):
+            tok = r.integers(0, 1000, 32).astype(np.int32)
+            pos = np.full(32, p, np.int32)
+            tg, te = ge.step(tok, seq, pos, seq), ee.step(tok, seq, pos, seq)
+            lg, le = ge.logits(seq), ee.logits(seq)
+            assert np.array_equal(tg, te), (it, p)
+            assert np.array_equal(lg.view(np.uint32), le.view(np.uint32)), (it, p)
+        assert ge.graph_count() == (2, 3), ge.graph_count()  # two shapes captured, each replayed
+
+
 def test_probs_records_and_end_ban(tiny):
     """sn_want_probs / sn_probs and sn_set_eog / sn_no_end through sn_step (argmax_p, kernels.metal:380-442): the
     records equal the oracle's top2 and log-sum-exp of the step's own logits; a slot under no_end never takes an

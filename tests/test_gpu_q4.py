@@ -168,3 +168,37 @@ def test_row_invariance_bitwise():
     for rows in ([0], [5, 6, 7], list(range(17)), list(range(8, 40)), list(range(43, 300))):
         part, _ = gemm_gpu(None, N, K, X[rows], wbuf=wbuf)
         assert np.array_equal(part.view(np.uint32), full[rows].view(np.uint32))
+
+
+@pytest.fixture(scope="module")
+def lm_head():
+    """The Qwen3-4B LM head's shape (configs[2..4]: V = 151,936 rows of K = 2560), seeded N(0, 0.02) weights quantized
+    with ggml's reference quantizer, and 300 activation rows with the full-width product of all of them."""
+    r = np.random.default_rng(8)
+    N, K = 151936, 2560
+    Wq = O.quantize_q4_0(r.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+    X = r.normal(0, 1, (300, K)).astype(np.float32)
+    L = S.lib()
+    wbuf = U.empty(L.snk_q4_stripes_bytes(N, K))
+    assert L.snk_q4_repack(U.ptr(U.dev(Wq)), N, K, U.ptr(wbuf), U.stream()) == 0
+    full, _ = gemm_gpu(None, N, K, X, wbuf=wbuf)
+    return Wq, X, wbuf, full
+
+
+@pytest.mark.parametrize("M", [1, 8, 32, 300])
+def test_lm_head_width_matmul(lm_head, M):
+    """The LM head's launches (two stripes a wavefront, no k-split: the kernel instances every decode, draft and MoE
+    step's output stage runs, sn_encode.inc.h:304-317) against the oracle at 1, 8 (drafts), 32 (decode) and 300 rows,
+    and each row bit for bit equal to the same row of the 300-row product."""
+    Wq, X, wbuf, full = lm_head
+    N, K = 151936, 2560
+    assert S.q4_plan(N, K) == (2, 1)
+    Y, _ = gemm_gpu(None, N, K, X[:M], wbuf=wbuf)
+    ref = O.mul_mat_q4_0(Wq, K, X[:M])
+    err = np.abs(Y - ref)
+    print(f"LM head M={M}: max abs err {err.max():.3g}")
+    assert np.all(err <= ATOL + RTOL * np.abs(ref))
+    assert np.array_equal(Y.view(np.uint32), full[:M].view(np.uint32))
+    if M > 1:  # rows from the middle of the batch, alone
+        part, _ = gemm_gpu(None, N, K, X[M // 2:M], wbuf=wbuf)
+        assert np.array_equal(part.view(np.uint32), full[M // 2:M].view(np.uint32))
