@@ -58,6 +58,15 @@ size_t snk_q4_workspace_bytes(int M, int N, int K);
 int snk_q4_plan(int N, int K, int wt, int* spw, int* ks);
 int snk_q4_gemm(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi, void* d_ws,
                 size_t ws_bytes, void* stream);
+// snk_q4_gemm without a workspace and without allocating: the k-slice partial sums go to a fixed device array of
+// 32 MiB that the library holds on each GPU it runs on (until the process ends), so the call makes no hipMalloc,
+// hipFree or other allocating call. The same kernels as snk_q4_gemm, so the same bits. A shape whose partials
+// (snk_q4_workspace_bytes(M, N, K)) exceed 32 MiB is refused with the reason in err. Calls that overlap on one GPU
+// (other streams or threads) share the array and race. 0, or -1 (err).
+// No counterpart in the reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving
+// loops, harnesses that forbid hipMalloc).
+int snk_q4_gemm_noalloc(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi,
+                        void* stream, char* err, int err_len);
 // average device time (microseconds) of one raw matmul launch (the k-slice sums into d_ws, as a decode step runs it:
 // the step's row kernels add the slices) over `iters` launches timed with HIP events on `stream`, the weights taken
 // from n_copies stripe copies in turn (copies beyond the 256 MB Infinity Cache keep the reads in HBM). d_y and ldy are

@@ -11,8 +11,11 @@
 // One fma per output then adds isum * (dw * dx) (the product of two fp16 values is exact in fp32) to the fp32
 // accumulator. The order of the sums of an output is fixed by (N, K) alone, never by the number of rows, so a row's
 // result is the same in any step (sn.h:1-3).
-#include <type_traits>
+#include <stdarg.h>
+
 #include <algorithm>
+#include <mutex>
+#include <type_traits>
 
 #include "sn_kernels_internal.h"
 
@@ -608,6 +611,66 @@ int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, 
     a.M = M; a.N = N; a.K = K; a.ldy = ldy; a.epi = epi; a.ks = ks;
     const int tot = M * (epi == EPI_SWIGLU ? N / 2 : N);
     hipLaunchKernelGGL(k_q4_reduce, dim3((tot + 255) / 256), dim3(256), 0, st, a);
+    return 0;
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// the matmul without allocation (snk_q4_gemm_noalloc): the k-slice partials in a fixed device array
+
+// Each GPU the library runs on holds its own copy of this array, from the code object's load until the process ends.
+// Host code never passes `scratch` itself (in host code the name is a stand-in, not a device address): it looks up the
+// current device's copy once with hipGetSymbolAddress and passes that address.
+#define Q4_SCRATCH_BYTES (32u << 20)
+static __device__ __align__(256) uint8_t scratch[Q4_SCRATCH_BYTES];
+
+// the current device's copy of `scratch`, looked up on the first call on that device (with it current) and kept
+static float* q4_scratch(char* err, int err_len) {
+    static std::mutex mu;
+    static void* addr[64];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        sn_set_err(err, err_len, "snk_q4_gemm_noalloc: no current HIP device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            sn_set_err(err, err_len, "snk_q4_gemm_noalloc: hipGetSymbolAddress of the scratch array failed on device %d: "
+                       "%s", dev, hipGetErrorString(e));
+            return nullptr;
+        }
+        addr[dev] = p;
+    }
+    return (float*) addr[dev];
+}
+
+// snk_q4_gemm with the partials in the device's scratch array: the same kernels, the same slices in the same order, so
+// the same bits. Nothing in the array has to start at zero: every partial the reduction reads is written first by the
+// same call's matmul. Calls that overlap on one GPU (other streams, other threads) share the array and race.
+extern "C" int snk_q4_gemm_noalloc(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y, int ldy,
+                                   int epi, void* stream, char* err, int err_len) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 32 || epi < 0 || epi > 2 ||
+        (epi == EPI_SWIGLU ? (N % 32 != 0 || ldy < N / 2) : ldy < N)) {
+        sn_set_err(err, err_len, "snk_q4_gemm_noalloc: bad shape (M %d, N %d, K %d, ldy %d, epi %d)", M, N, K, ldy, epi);
+        return -1;
+    }
+    const size_t need = q4_workspace_bytes(M, N, K);
+    if (need > Q4_SCRATCH_BYTES) {
+        sn_set_err(err, err_len, "snk_q4_gemm_noalloc: %d x %d x %d needs %zu bytes of k-slice partials; the scratch "
+                   "array holds %u", M, N, K, need, Q4_SCRATCH_BYTES);
+        return -1;
+    }
+    float* ws = q4_scratch(err, err_len);
+    if (!ws) return -1;
+    const int rc = q4_gemm((const uint8_t*) d_stripes, (const uint8_t*) d_xa, M, N, K, d_y, ldy, epi, ws,
+                           Q4_SCRATCH_BYTES, (hipStream_t) stream);
+    const hipError_t e = hipGetLastError();
+    if (rc != 0 || e != hipSuccess) {
+        sn_set_err(err, err_len, "snk_q4_gemm_noalloc: launch failed: %s", hipGetErrorString(e));
+        return -1;
+    }
     return 0;
 }
 
