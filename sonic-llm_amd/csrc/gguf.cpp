@@ -26,7 +26,7 @@ struct Rd {
     template <class T>
     T get() {
         T v{};
-        if (p + sizeof(T) > end) {
+        if (sizeof(T) > (size_t) (end - p)) {
             ok = false;
             return v;
         }
@@ -36,7 +36,7 @@ struct Rd {
     }
     std::string s() {
         const uint64_t n = get<uint64_t>();
-        if (!ok || p + n > end) {
+        if (!ok || n > (uint64_t) (end - p)) {
             ok = false;
             return {};
         }
@@ -114,7 +114,7 @@ bool GgufFile::open(const char* path, std::string* why) {
                 for (uint64_t j = 0; j < v.n_items && r.ok; ++j) r.s();
             } else {
                 const size_t sz = scalar_size(it);
-                if (!sz || r.p + sz * v.n_items > r.end) r.ok = false;
+                if (!sz || v.n_items > (uint64_t) (r.end - r.p) / sz) r.ok = false;
                 else r.p += sz * v.n_items;
             }
         } else {
@@ -122,7 +122,15 @@ bool GgufFile::open(const char* path, std::string* why) {
         }
         kv[key] = v;
     }
-    if (kv.count("general.alignment")) alignment = (size_t) kv["general.alignment"].num;
+    if (kv.count("general.alignment")) {
+        // a power of two, at most 1 MiB (the data section starts at the next multiple of it)
+        const double a = kv["general.alignment"].num;
+        alignment = a >= 1 && a <= (1 << 20) ? (size_t) a : 0;
+        if (!alignment || (alignment & (alignment - 1))) {
+            *why = "general.alignment must be a power of two up to 1 MiB";
+            return false;
+        }
+    }
     for (uint64_t i = 0; i < n_t && r.ok; ++i) {
         GgufTensor t;
         t.name = r.s();
@@ -131,7 +139,11 @@ bool GgufFile::open(const char* path, std::string* why) {
             r.ok = false;
             break;
         }
-        for (int d = 0; d < t.n_dims; ++d) t.ne[d] = (int64_t) r.get<uint64_t>();
+        for (int d = 0; d < t.n_dims; ++d) {
+            const uint64_t ne = r.get<uint64_t>();
+            if (ne < 1 || ne > (1ull << 40)) r.ok = false;  // (each factor of the size products below stays small)
+            t.ne[d] = (int64_t) ne;
+        }
         t.type = (int) r.get<uint32_t>();
         t.offset = r.get<uint64_t>();
         tensors.push_back(t);
@@ -142,12 +154,27 @@ bool GgufFile::open(const char* path, std::string* why) {
     }
     const size_t hdr = (size_t) (r.p - map);
     data_offset = (hdr + alignment - 1) / alignment * alignment;
+    if (data_offset > size) {
+        *why = "truncated GGUF file (no data section)";
+        return false;
+    }
+    const size_t room = size - data_offset;  // bytes of the data section
     for (size_t i = 0; i < tensors.size(); ++i) {
         GgufTensor& t = tensors[i];
         const size_t rb = ggml_row_bytes(t.type, t.ne[0]);
-        t.nbytes = rb * (size_t) (t.ne[1] * t.ne[2] * t.ne[3]);
-        if (!rb || data_offset + t.offset + t.nbytes > size) {
-            *why = "tensor " + t.name + ": unsupported type or out of the file";
+        const int bk = t.type == GGML_Q6_K ? 256 : (t.type == GGML_Q4_0 || t.type == GGML_Q8_0) ? 32 : 1;
+        // rows: each dimension at most 2^40 (checked above), so every partial product is checked against the room
+        // before the next multiply
+        size_t rows = 1;
+        bool fits = rb != 0 && t.ne[0] % bk == 0;
+        for (int d = 1; d < 4 && fits; ++d) {
+            if ((size_t) t.ne[d] > room / rows) fits = false;
+            else rows *= (size_t) t.ne[d];
+        }
+        fits = fits && rows <= room / rb;
+        t.nbytes = fits ? rb * rows : 0;
+        if (!fits || t.offset > room || t.nbytes > room - t.offset) {
+            *why = "tensor " + t.name + ": unsupported type or shape, or out of the file";
             return false;
         }
         t.data = map + data_offset + t.offset;
@@ -217,7 +244,11 @@ bool GgufWriter::begin(FILE* f, size_t* data_start) {
     long pos = ftell(f);
     const size_t start = ((size_t) pos + alignment - 1) / alignment * alignment;
     static const uint8_t zeros[64] = {0};
-    ok = ok && w(zeros, start - (size_t) pos);
+    for (size_t left = start - (size_t) pos; ok && left > 0;) {  // (alignments above 64 bytes: in pieces)
+        const size_t n = left < sizeof zeros ? left : sizeof zeros;
+        ok = w(zeros, n);
+        left -= n;
+    }
     *data_start = start;
     return ok;
 }
