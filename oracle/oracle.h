@@ -30,6 +30,11 @@
 // explicit integer block sum and the fp64 product of the dequantized operands; paged attention against an fp64 dense
 // softmax over page-gathered cells, chunked == monolithic, page-placement
 // and shared-prefix invariance; the model writer's GGUF layout against the reference's own GGUF fixture.
+// The composed functions (tests/test_oracle_model.py): or_qwen3_step (dense Q4_0 / Q8_0 and MoE layers, the output
+// stage), or_mtp_fill and or_mtp_guess equal, bit for bit (logits, tokens, normed rows, cache cells), tests/ref64.py, a
+// numpy restatement written from the reference's layer program, MoE FFN, output stage and guess-head rows with ggml's
+// per-operation fp32 arithmetic; and two invariants: one expert copied to every expert gives the dense FFN, a guess
+// head whose eh_proj ignores the hidden-state half guesses independently of it.
 // Parity unpinned against ggml itself (no ggml vector exists offline): the exact bytes of quantize_row_q4_0_ref and of
 // x86 quantize_row_q8_0 (their rounding rules are restated from ggml's published source and checked by invariants
 // only), and ggml's fp32 summation order inside mul_mat (checked to tolerance only).
