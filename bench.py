@@ -47,31 +47,50 @@ def model_file(cfg_kw, seed, path=None):
     return path
 
 
-def cpu_baseline(path, seqs, ctx, seed):
-    """The oracle's step for the same rows on the host cores: one step of `seqs` rows at position ctx (its KV cells are
-    zeros: the cost of a step does not depend on what they hold)."""
+def cpu_spec_baseline(path, n, ctx, k, seed, layers, accept):
+    """The oracle's fused draft-verify step (oracle/oracle.c) for n sequences at position ctx on the host cores: each
+    sequence's k guesses (or_mtp_guess), one model step over the n (k + 1) verify rows, the guess head's cells of those
+    rows (or_mtp_fill), greedy acceptance with the benchmark's forced share of drafts. Median of at least 10 warm runs
+    of a one-layer and a two-layer cut (each with the guess head and the output stage), scaled to `layers`."""
     import numpy as np
 
     from oracle import oracle as O
     from oracle.gguf import GGUF
 
     O.build() if not os.path.exists(O.LIB_PATH) else None
-    ref = O.Qwen3(GGUF(path), n_seq=seqs, ctx=ctx + 1)
-    r = np.random.default_rng(seed)
-    tok = r.integers(0, ref.V, seqs).astype(np.int32)
-    seq = np.arange(seqs, dtype=np.int32)
-    pos = np.full(seqs, ctx, np.int32)
-    ref.k[:, :, :ctx] = 0  # touch the cells the step reads before timing
-    ref.v[:, :, :ctx] = 0
-    t = time.perf_counter()
-    ref.step(tok, seq, pos, seq)
-    dt = time.perf_counter() - t
-    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count())
-    return {"value": seqs / dt, "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"one decode step of the full workload ({seqs} rows at position {ctx}, all layers and the LM "
-                      f"head) through oracle/oracle.c (ggml-semantics CPU restatement: Q8_0 activations, integer block "
-                      f"dots, fp32 attention over fp16 cells; ggml b11669 itself is not available offline), "
-                      f"{dt:.1f} s on {cores} threads"}
+    g = GGUF(path)
+    rng = np.random.default_rng(seed)
+    ts = {}
+    for nl in (1, 2):
+        ref = O.Qwen3(LayerCut(g, nl), n_seq=n, ctx=ctx + k + 2)
+        ref.k[:, :, :ctx] = 0
+        ref.v[:, :, :ctx] = 0
+        last = rng.integers(0, ref.V, n).astype(np.int32)
+        hprev = np.zeros((n, ref.E), np.float32)
+        nt = cpu_threads()
+
+        def spec():
+            drafts = [ref.mtp_guess(s, int(last[s]), ctx, k, hprev[s], nthreads=nt)[0] for s in range(n)]
+            tok = np.concatenate([[last[s]] + list(drafts[s]) for s in range(n)]).astype(np.int32)
+            seq = np.repeat(np.arange(n, dtype=np.int32), k + 1)
+            pos = np.tile(np.arange(ctx, ctx + k + 1, dtype=np.int32), n)
+            hn = np.zeros((n * (k + 1), ref.E), np.float32)
+            _, lg, _ = ref.step(tok, seq, pos, np.arange(n * (k + 1), dtype=np.int32), hn_all=hn, nthreads=nt)
+            ref.mtp_fill(tok, seq, pos, np.concatenate([hprev[:1], hn[:-1]]), nthreads=nt)
+            force = rng.random((n, k)) < accept
+            for s in range(n):
+                tg = [O.argmax(lg[s * (k + 1) + i]) if not (i < k and force[s, i]) else drafts[s][i] for i in range(k + 1)]
+                O.accept(drafts[s], np.array(tg[:k], np.int32))
+
+        ts[nl] = median_time(spec)
+        del ref
+    t = ts[1][0] + (layers - 1) * max(ts[2][0] - ts[1][0], 0.0)
+    sample = (f"{n} sequences' draft-verify step at position {ctx} (k = {k} guesses each, one step over the "
+              f"{n * (k + 1)} verify rows, the guess head's cells, acceptance) through oracle/oracle.c "
+              f"(ggml-semantics CPU restatement; generic scalar loops): median of {ts[1][1]} / {ts[2][1]} warm runs of "
+              f"a 1- and a 2-layer cut of the model with its guess head and output stage ({ts[1][0]:.3f} / "
+              f"{ts[2][0]:.3f} s), scaled to {layers} layers: {t:.2f} s a step")
+    return t, sample
 
 
 def main():
@@ -85,8 +104,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--model", default=None, help="GGUF path (generated when missing)")
     ap.add_argument("--seed", type=int, default=42)
-    ap.add_argument("--config", default="decode", choices=("decode", "mtp", "moe", "matmul", "attn", "prefill"),
-                    help="decode: the headline (configs[2]); mtp: the fused draft-verify step (configs[3]); "
+    ap.add_argument("--config", default="all", choices=("all", "decode", "mtp", "moe", "matmul", "attn", "prefill"),
+                    help="all (default): the headline (configs[2]) with configs[0], [1], [3], [4] inside its line; "
+                         "decode: the headline alone; mtp: the fused draft-verify step (configs[3]); "
                          "moe: Qwen3-30B-A3B-arch batched decode (configs[4]); matmul: one 8 x 4096 x 4096 Q4_0 "
                          "matmul (configs[0]); attn: one layer of paged decode attention (configs[1]); prefill: "
                          "2048-token prompts in 512-row steps")
@@ -119,20 +139,36 @@ def main():
               f"across GPUs with no per-step exchange; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
 
+    subs = {"mtp": bench_mtp, "matmul": bench_matmul, "attn": bench_attn, "prefill": bench_prefill}
+    if args.config in subs:
+        print(json.dumps(subs[args.config](args)), flush=True)
+        return
+    if args.config in ("decode", "moe"):
+        print(json.dumps(bench_decode(args, moe=args.config == "moe")), flush=True)
+        return
+    # all: the headline with the other configurations' lines inside it
+    line = bench_decode(args, moe=False)
+    line["configs"] = {}
+    for name, fn in (("c1_matmul", bench_matmul), ("c2_attn", bench_attn), ("c4_mtp", bench_mtp),
+                     ("c5_moe", lambda a: bench_decode(a, moe=True))):
+        t = time.time()
+        try:
+            line["configs"][name] = fn(args)
+        except Exception as e:  # (the headline stands; the failure is reported in its place)
+            import traceback
+            traceback.print_exc()
+            line["configs"][name] = {"error": repr(e)}
+        log(f"[bench] {name} in {time.time() - t:.1f}s")
+    print(json.dumps(line), flush=True)
+
+
+def bench_decode(args, moe):
+    """configs[2] (the headline) or configs[4] (moe): batched decode steps of 32 sequences at 2048 cells."""
     import numpy as np
     import torch
 
     import sllm_next as S
 
-    if args.config == "mtp":
-        return bench_mtp(args)
-    if args.config == "matmul":
-        return bench_matmul(args)
-    if args.config == "attn":
-        return bench_attn(args)
-    if args.config == "prefill":
-        return bench_prefill(args)
-    moe = args.config == "moe"
     cfg = dict(S.QWEN3_30B_A3B if moe else S.QWEN3_4B)
     if args.wtype == 8:
         cfg["wtype"] = 8
@@ -199,8 +235,9 @@ def main():
     # HBM bytes per launch of each class from the committed rocprofv3 counter runs of this workload (FETCH_SIZE and
     # WRITE_SIZE, scaled by a copy of known size): profiles/decode_qwen3_4b_b32_ctx2048_traffic.md
     traffic = {}
-    tpath = os.path.join(ROOT, "profiles", "decode_qwen3_4b_b32_ctx2048_traffic.json")
-    if not moe and args.wtype == 2 and not tied and (B, ctx) == (32, 2048) and os.path.exists(tpath):
+    tname = "moe_qwen3_30b_a3b_b32_ctx2048_traffic" if moe else "decode_qwen3_4b_b32_ctx2048_traffic"
+    tpath = os.path.join(ROOT, "profiles", tname + ".json")
+    if args.wtype == 2 and not tied and (B, ctx) == (32, 2048) and os.path.exists(tpath):
         traffic = json.load(open(tpath))
 
     def roof(k):
@@ -208,13 +245,14 @@ def main():
         return {"kernel": k, "bound": "hbm", "achieved": round(c["GBps"], 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                 "frac": round(c["frac"], 4), "traffic": round(traffic[k]) if k in traffic else None,
                 "bytes_per_launch": round(c["bytes_per_launch"]), "us_per_launch": round(c["us_per_launch"], 2),
-                **({"traffic_source": "profiles/decode_qwen3_4b_b32_ctx2048_traffic.md"} if k in traffic else {})}
+                **({"traffic_source": f"profiles/{tname}.md"} if k in traffic else {})}
 
     eng.close()
     cpu = None
-    if not args.no_cpu and not moe:
+    if not args.no_cpu:
         t = time.time()
-        cpu = cpu_baseline(path, B, ctx, args.seed)
+        sec, sample = cpu_step_baseline(path, B, ctx, args.seed, cfg["n_layer"])
+        cpu = {"value": round(B / sec, 3), "unit": "tok/s", **cpu_info(), "kind": "port", "sample": sample}
         log(f"[bench] cpu baseline in {time.time() - t:.1f}s: {cpu['value']:.2f} tok/s")
     q = "Q8_0" if args.wtype == 8 else "Q4_0"
     metric = (f"agg decode tok/s, Qwen3-30B-A3B-arch {q} MoE x32 seqs" if moe else
@@ -241,7 +279,7 @@ def main():
         "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+    return line
 
 
 def bench_mtp(args):
@@ -296,6 +334,14 @@ def bench_mtp(args):
     prof = eng.prof_read()
     eng.prof(False)
     eng.close()
+    cpu = None
+    if not args.no_cpu:
+        t = time.time()
+        sec, sample = cpu_spec_baseline(path, B, ctx, k, args.seed, cfg["n_layer"], args.accept)
+        per_step = toks / args.steps
+        cpu = {"value": round(per_step / sec, 3), "unit": "tok/s", **cpu_info(), "kind": "port",
+               "sample": sample + f"; tokens kept a step as on the GPU ({per_step:.2f})"}
+        log(f"[bench] cpu baseline in {time.time() - t:.1f}s: {cpu['value']:.2f} tok/s")
     kernels = {}
     for name, p in prof.items():
         if p["launches"]:
@@ -317,13 +363,15 @@ def bench_mtp(args):
                    "drafts": k, "verify_rows": B * (k + 1), "tokens_per_step": round(toks / args.steps, 3),
                    "gpu_ms_per_step": round(gpu_ms / args.steps, 4)},
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": kernels[dom]["GBps"], "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": kernels[dom]["frac"], "traffic": None,
+                     "unit": "GB/s", "frac": kernels[dom]["frac"],
+                     "traffic": profile_traffic("mtp_qwen3_4b_b8_ctx4096_k3_traffic.json", dom),
                      "bytes_per_launch": kernels[dom]["bytes_per_launch"],
                      "us_per_launch": kernels[dom]["us_per_launch"]} if dom else None,
+        "verify_gemm_mfma": profile_traffic("mtp_qwen3_4b_b8_ctx4096_k3_traffic.json", "verify_gemm_mfma_busy"),
         "kernels": kernels,
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+    return line
 
 
 def bench_prefill(args):
@@ -413,7 +461,7 @@ def bench_prefill(args):
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+    return line
 
 
 def graph_us(fn, n, reps=10):
@@ -449,6 +497,101 @@ def profile_traffic(name, key):
 
 def cpu_threads():
     return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count())
+
+
+def cpu_info():
+    """the host the CPU baseline ran on: threads used, logical CPUs, CPU model"""
+    model = ""
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cores": cpu_threads(), "nproc": os.cpu_count(), "cpu_model": model}
+
+
+def median_time(fn, min_runs=10, min_s=0.0):
+    """median wall time of fn() over at least min_runs runs (and at least min_s seconds) after one warm-up run"""
+    import statistics
+    fn()
+    ts = []
+    t_all = time.perf_counter()
+    while len(ts) < min_runs or time.perf_counter() - t_all < min_s:
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return statistics.median(ts), len(ts)
+
+
+class LayerCut:
+    """A GGUF model read as its first n layers (and its guess-head block, renumbered after them): the oracle's CPU
+    baseline times a cut of one and of two layers and scales by the layer count (every layer of these models costs
+    the same)."""
+
+    def __init__(self, g, n):
+        a = g.kv["general.architecture"]
+        self.g, self.n = g, n
+        self.n_mtp = int(g.kv.get(f"{a}.nextn_predict_layers", 0))
+        self.L = int(g.kv[f"{a}.block_count"]) - self.n_mtp
+        self.kv = dict(g.kv)
+        self.kv[f"{a}.block_count"] = n + self.n_mtp
+        self.tinfo = {self._rename(k): v for k, v in g.tinfo.items() if self._keep(k)}
+
+    def _keep(self, name):
+        if not name.startswith("blk."):
+            return True
+        i = int(name.split(".")[1])
+        return i < self.n or i == self.L
+
+    def _rename(self, name):  # the guess head's block L -> n
+        if name.startswith(f"blk.{self.L}."):
+            return f"blk.{self.n}." + name[len(f"blk.{self.L}."):]
+        return name
+
+    def _orig(self, name):
+        if self.n_mtp and name.startswith(f"blk.{self.n}."):
+            return f"blk.{self.L}." + name[len(f"blk.{self.n}."):]
+        return name
+
+    def tensor(self, name):
+        return self.g.tensor(self._orig(name))
+
+    def type_name(self, name):
+        return self.g.type_name(self._orig(name))
+
+
+def cpu_step_baseline(path, n_rows, ctx, seed, layers):
+    """The oracle's step (oracle/oracle.c, ggml-semantics CPU restatement) of n_rows decode rows at position ctx on the
+    host cores: the median of at least 10 warm runs of a one-layer and of a two-layer cut of the model (each with the
+    output stage), scaled to `layers`: per step = t1 + (layers - 1) (t2 - t1). Returns (seconds per step, sample)."""
+    import numpy as np
+
+    from oracle import oracle as O
+    from oracle.gguf import GGUF
+
+    O.build() if not os.path.exists(O.LIB_PATH) else None
+    g = GGUF(path)
+    r = np.random.default_rng(seed)
+    ts = {}
+    for n in (1, 2):
+        ref = O.Qwen3(LayerCut(g, n), n_seq=n_rows, ctx=ctx + 1)
+        ref.k[:, :, :ctx] = 0  # (touch the cells the step reads)
+        ref.v[:, :, :ctx] = 0
+        tok = r.integers(0, ref.V, n_rows).astype(np.int32)
+        seq = np.arange(n_rows, dtype=np.int32)
+        pos = np.full(n_rows, ctx, np.int32)
+        ts[n] = median_time(lambda: ref.step(tok, seq, pos, seq, nthreads=cpu_threads()))
+        del ref
+    per_layer = max(ts[2][0] - ts[1][0], 0.0)
+    t = ts[1][0] + (layers - 1) * per_layer
+    sample = (f"{n_rows} decode rows at position {ctx} through oracle/oracle.c (ggml-semantics CPU restatement: Q8_0 "
+              f"activations, integer block dots, fp32 attention over fp16 cells; ggml b11669 is not available offline, "
+              f"and these generic scalar loops are slower than ggml's AVX2 / AVX-512 kernels): median of "
+              f"{ts[1][1]} / {ts[2][1]} warm runs of a 1- and a 2-layer cut of the model with its output stage "
+              f"({ts[1][0]:.3f} / {ts[2][0]:.3f} s), scaled to {layers} layers: {t:.2f} s a step")
+    return t, sample
 
 
 class Dev:
@@ -535,19 +678,14 @@ def bench_matmul(args):
         from oracle import oracle as O
         O.build() if not os.path.exists(O.LIB_PATH) else None
         nt = cpu_threads()
-        t = time.perf_counter()
-        reps = 0
-        while True:
-            want = O.mul_mat_q4_0(Wq, K, X, nthreads=nt)
-            reps += 1
-            if time.perf_counter() - t > 10.0:
-                break
-        dt = (time.perf_counter() - t) / reps
+        want = O.mul_mat_q4_0(Wq, K, X, nthreads=nt)
+        dt, reps = median_time(lambda: O.mul_mat_q4_0(Wq, K, X, nthreads=nt), min_s=2.0)
         err = float(np.abs(got - want).max())
         log(f"[bench] max |GPU - oracle| {err:.3g} (max |y| {float(np.abs(want).max()):.3g})")
-        cpu = {"value": round(alg / dt / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+        cpu = {"value": round(alg / dt / 1e9, 3), "unit": "GB/s", **cpu_info(), "kind": "port",
                "sample": f"the same 8 x 4096 x 4096 matmul through oracle/oracle.c (ggml-semantics CPU restatement: "
-                         f"Q8_0 activations, integer block dots), {reps} calls in {dt * reps:.1f} s on {nt} threads"}
+                         f"Q8_0 activations, integer block dots; generic scalar loops, slower than ggml's AVX2 / "
+                         f"AVX-512 kernels): median of {reps} warm calls, {dt * 1e3:.2f} ms each"}
     gbs, gbs_k = alg / (us * 1e-6) / 1e9, alg / (us_gemm * 1e-6) / 1e9
     log(f"[bench] C1 matmul: {us:.2f} us per call (quantize + matmul + reduce), matmul kernel {us_gemm:.2f} us")
     line = {
@@ -565,7 +703,7 @@ def bench_matmul(args):
                      "bytes_per_launch": alg, "us_per_launch": round(us_gemm, 3)},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+    return line
 
 
 def config2_case(seed=2, n_seq=32, page=32, lo=256, hi=4096, n_share=8, share_cells=1024):
@@ -656,18 +794,16 @@ def bench_attn(args):
         run(0, st0)
         got = U.host(out, np.float32)[:n_seq * H * D].reshape(n_seq, H, D)
         nt = cpu_threads()
-        t = time.perf_counter()
-        reps = 0
-        while True:
-            want = O.paged_attn(q, seq, pos, KVH, kh, vh, page, pt, 1.0 / np.sqrt(D), nthreads=nt)
-            reps += 1
-            if time.perf_counter() - t > 10.0:
-                break
-        dt = (time.perf_counter() - t) / reps
+
+        def attn_cpu():
+            return O.paged_attn(q, seq, pos, KVH, kh, vh, page, pt, 1.0 / np.sqrt(D), nthreads=nt)
+
+        want = attn_cpu()
+        dt, reps = median_time(attn_cpu)
         log(f"[bench] max |GPU - oracle| {float(np.abs(got - want).max()):.3g}")
-        cpu = {"value": round(alg / dt / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
-               "sample": f"the same 32-row attention through oracle/oracle.c (fp32 softmax over fp16 cells), "
-                         f"{reps} calls in {dt * reps:.1f} s on {nt} threads"}
+        cpu = {"value": round(alg / dt / 1e9, 3), "unit": "GB/s", **cpu_info(), "kind": "port",
+               "sample": f"the same 32-row attention through oracle/oracle.c (fp32 softmax over fp16 cells): median "
+                         f"of {reps} warm calls, {dt * 1e3:.1f} ms each"}
     gbs = alg / (us * 1e-6) / 1e9
     kern = "k_attn_whole" if whole else "k_attn_part + k_attn_merge"
     log(f"[bench] C2 attention: {us:.2f} us per launch ({kern}), {alg / 1e6:.1f} MB unique, "
@@ -690,7 +826,7 @@ def bench_attn(args):
         "cpu_baseline": cpu,
     }
     L.snk_attn_free(plan)
-    print(json.dumps(line), flush=True)
+    return line
 
 
 if __name__ == "__main__":
