@@ -74,6 +74,16 @@ int snk_q4_gemm_noalloc(const void* d_stripes, const void* d_xa, int M, int N, i
 double snk_q4_gemm_time(const void* const* d_stripes, int n_copies, const void* d_xa, int M, int N, int K, float* d_y,
                         int ldy, void* d_ws, size_t ws_bytes, int iters, void* stream);
 
+// Launch-plan tuning of the matmul (raw k-slice sums of Q4_0 stripes): an explicit plan of mt row tiles a workgroup
+// (1, 2), spw stripes a wavefront (1, 2) and G groups a slice with every load of the slice issued at once (G 0: the
+// default plan). snk_q4_gemm_plan_time: average device time (microseconds) of one launch over `iters` launches on
+// `stream`, weights from n_copies stripe copies in turn; -1 for a plan that is not instantiated or too small a
+// workspace. snk_q4_gemm_plan_sums: the plan's slices added in order into d_y [M][N], for checking a plan; 0 or -1.
+double snk_q4_gemm_plan_time(const void* const* d_stripes, int n_copies, const void* d_xa, int M, int N, int K,
+                             void* d_ws, size_t ws_bytes, int mt, int spw, int G, int iters, void* stream);
+int snk_q4_gemm_plan_sums(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y, void* d_ws,
+                          size_t ws_bytes, int mt, int spw, int G, void* stream);
+
 // ---- paged GQA attention (decode and verify rows) -------------------------------------------------------------------
 // Replaces attn_part + attn_merge (kernels.metal:1122-1192) and fa2 (kernels.metal:2674-2770). q: [rows][H][128] fp32
 // (ldq floats apart); K/V pool fp16, page p of KV head h at pool + ((p * KVH + h) * page_cells) * 128; d_pt:

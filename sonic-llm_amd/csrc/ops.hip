@@ -91,7 +91,8 @@ void qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, in
     if (km == 1) QKR(1);
     else if (km == 2) QKR(2);
     else if (km == 4) QKR(4);
-    else QKR(8);
+    else if (km == 8) QKR(8);
+    else QKR(16);
 #undef QKR
 }
 

@@ -489,6 +489,109 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     }
 }
 
+// The streaming form: the slice's activation records (gps groups, up to GMAX) are loaded once per workgroup by the 4
+// wavefronts together and staged into LDS behind the kernel's only barrier; each wavefront then streams its own S
+// stripes' weights through a ring of D register slots (group i + D's loads issued as soon as group i is summed), with
+// no further synchronisation. The activation fragment, scales and corrections read from LDS for a block serve S x MT
+// MFMAs. Same arithmetic and order as k_q4_gemm.
+template <int WT, int MT, int S, int D, int GMAX>
+__global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
+    constexpr bool Q8 = WT == WT_Q8_0;
+    constexpr int TB = Q8 ? Q8T_BYTES : Q4T_BYTES, SO = Q8 ? Q8T_SCALE_OFF : Q4T_SCALE_OFF;
+    constexpr int NW = Q8 ? 2 : 1;
+    constexpr int CORR = Q8 ? XA_CORR8_OFF : XA_CORR_OFF;
+    constexpr int NF = GMAX * MT * 4, FPW = NF / 4;
+    constexpr int NK = GMAX * MT * 2, KPW = (NK + 3) / 4;
+    __shared__ __attribute__((aligned(16))) uint8_t s_act[NF][1024];
+    __shared__ __attribute__((aligned(16))) float s_k[GMAX][MT][2][64];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_in = lane & 15, g = lane >> 4;
+    const int set = blockIdx.x, slice = blockIdx.y;
+    const int mt0 = __builtin_amdgcn_readfirstlane((int) blockIdx.z * MT);
+    const int c0 = slice * a.gps, ng = __builtin_amdgcn_readfirstlane(min(a.gps, a.ngroups - c0));
+    const int s0 = set * (4 * S) + wave * S;
+    const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(S, a.nstripes - s0)));
+    const int sbytes = a.ngroups * TB;
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(a.w + (size_t) min(s0, a.nstripes - 1) * sbytes, (uint32_t) (nvalid * sbytes));
+    const size_t x0 = (size_t) mt0 * a.ngroups * XA_REC;
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xa + x0, (uint32_t) (xa_bytes(a.M, a.K) - x0));
+    const int rstride = a.ngroups * XA_REC;
+
+    // the slice's activation (fragments past the slice repeat its last group: loads stay in bounds, never summed)
+    u32x4 ra[FPW];
+    float rk[KPW];
+    for (int j = 0; j < FPW; ++j) {
+        const int f = wave + 4 * j, c = c0 + min(f / (4 * MT), ng - 1);
+        ra[j] = bload16(xr, 16 * lane, ((f / 4) % MT) * rstride + c * XA_REC + (f % 4) * 1024);
+    }
+    for (int j = 0; j < KPW; ++j) {
+        const int k = min(wave + 4 * j, NK - 1), c = c0 + min(k / (2 * MT), ng - 1);
+        rk[j] = bload4f(xr, 4 * lane, ((k / 2) % MT) * rstride + c * XA_REC + (k % 2 ? CORR : XA_DX_OFF));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 wq[D][S][NW];
+    u32x2 ws[D][S];
+    auto wload = [&](int slot, int i) {  // group i's weights (i past the slice: its last group again)
+        const int c = c0 + min(i, ng - 1);
+        for (int t = 0; t < S; ++t) {
+            const int so = t * sbytes + c * TB;
+            for (int h = 0; h < NW; ++h) wq[slot][t][h] = bload16(wr, 16 * NW * lane + 16 * h, so);
+            ws[slot][t] = bload8(wr, SO + 8 * n_in, so);
+        }
+    };
+    for (int j = 0; j < D; ++j) {
+        wload(j, j);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int j = 0; j < FPW; ++j) *(u32x4*) &s_act[wave + 4 * j][16 * lane] = ra[j];
+    for (int j = 0; j < KPW; ++j) {
+        const int k = wave + 4 * j;
+        if (k < NK) s_k[k / (2 * MT)][(k / 2) % MT][k % 2][lane] = rk[j];
+    }
+    __syncthreads();
+
+    floatx4 acc[S][MT];
+    for (int t = 0; t < S; ++t)
+        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    const int trips = (ng + D - 1) / D;
+    for (int tr = 0; tr < trips; ++tr)
+        for (int j = 0; j < D; ++j) {
+            const int i = tr * D + j;
+            const float m = i < ng ? 1.0f : 0.0f;
+            const int li = min(i, ng - 1);  // (its LDS group)
+            __builtin_amdgcn_sched_barrier(0);
+            for (int b = 0; b < 4; ++b) {
+                half8 A[MT];
+                floatx4 dx[MT], cr[MT];
+                for (int mt = 0; mt < MT; ++mt) {
+                    A[mt] = *(const half8*) &s_act[(li * MT + mt) * 4 + b][16 * lane];
+                    dx[mt] = *(const floatx4*) &s_k[li][mt][0][b * 16 + 4 * g];
+                    cr[mt] = *(const floatx4*) &s_k[li][mt][1][b * 16 + 4 * g];
+                }
+                for (int t = 0; t < S; ++t) {
+                    const half8 bw = Q8 ? q8_unpack(wq[j][t][b / 2][2 * (b % 2)], wq[j][t][b / 2][2 * (b % 2) + 1])
+                                        : q4_unpack(wq[j][t][0][b]);
+                    const float dw = (float) __builtin_bit_cast(half4v, ws[j][t])[b] * m;
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const floatx4 isum = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], bw, cr[mt], 0, 0, 0);
+                        for (int v = 0; v < 4; ++v) acc[t][mt][v] = __builtin_fmaf(isum[v], dw * dx[mt][v], acc[t][mt][v]);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            wload(j, i + D);
+        }
+    for (int t = 0; t < S; ++t) {
+        const int stripe = s0 + t, col = stripe * 16 + n_in;
+        if (stripe >= a.nstripes || col >= a.N) continue;
+        for (int mt = 0; mt < MT; ++mt)
+            for (int v = 0; v < 4; ++v) {
+                const int row = (mt0 + mt) * 16 + 4 * g + v;
+                if (row < a.M) a.part[((size_t) slice * a.M + row) * a.N + col] = acc[t][mt][v];
+            }
+    }
+}
+
 // k-slice partial sums added in slice order, then the epilogue
 __global__ void k_q4_reduce(GemmArgs a) {
     const int outN = a.epi == EPI_SWIGLU ? a.N / 2 : a.N;
@@ -526,16 +629,32 @@ GemmPlan q4_plan(int N, int K, int wt) {
     GemmPlan p;
     p.nstripes = (N + 15) / 16;
     p.ngroups = (K / 32 + 3) / 4;
-    // stripes per wavefront: 2 only for LM-head-wide matrices (at least 768 sets of 8 stripes: enough workgroups with
-    // no k-split; 67 against 77 us for the Q4_0 head at 32 rows), and never for Q8_0 (twice the weight registers);
-    // 1 otherwise (gate|up: the same 14.3 us with 3 slices instead of 5, so its consumer reads fewer partials)
-    p.spw = p.nstripes >= Q4_WIDE && wt != WT_Q8_0 ? 2 : 1;
-    p.sets = (p.nstripes + 4 * p.spw - 1) / (4 * p.spw);
     auto slices = [&](int gps) { return (p.ngroups + gps - 1) / gps; };
-    int gps = (p.ngroups + 1) / 2 * 2;
-    while (gps > 4 && p.sets * slices(gps) < 768 && slices(gps - 2) <= KS_MAX) gps -= 2;
-    p.gps = gps;
-    p.ks = slices(gps);
+    if (p.nstripes >= Q4_WIDE) {
+        // LM-head-wide: the ring kernel, 2 stripes a wavefront (never for Q8_0: twice the weight registers), enough
+        // workgroups with no k-split (67 against 77 us for the Q4_0 head at 32 rows)
+        p.stream = false;
+        p.spw = wt != WT_Q8_0 ? 2 : 1;
+        p.sets = (p.nstripes + 4 * p.spw - 1) / (4 * p.spw);
+        int gps = (p.ngroups + 1) / 2 * 2;
+        while (gps > 4 && p.sets * slices(gps) < 768 && slices(gps - 2) <= KS_MAX) gps -= 2;
+        p.gps = gps;
+        p.ks = slices(gps);
+        p.sspw = p.smt = 1;
+        return p;
+    }
+    // Layer matrices: slices of 4 groups, or 8 for the wide (gate|up) and the deep (down) ones. Measured at 32 rows on
+    // MI355X (streaming kernel, launches back to back): q|k|v 6.2 us (2 stripes a wavefront), o 5.5, gate|up 12.9 (2
+    // stripes, both row tiles in one workgroup), down 8.4 (10 slices); the ring kernel with its earlier slices took
+    // 7.5, 6.4, 15.0 and 10.8.
+    p.stream = true;
+    p.gps = std::min(p.nstripes >= 1024 || p.ngroups >= 64 ? 8 : 4, (p.ngroups + 1) / 2 * 2);
+    p.ks = slices(p.gps);
+    p.sspw = wt != WT_Q8_0 && p.nstripes >= 384 ? 2 : 1;
+    p.smt = p.nstripes >= 1024 ? 2 : 1;
+    // the ring kernel (prompt rows) with the same slices: one stripe a wavefront
+    p.spw = 1;
+    p.sets = (p.nstripes + 3) / 4;
     return p;
 }
 
@@ -558,6 +677,25 @@ static void launch_gemm(int mt, int spw, dim3 grid, const GemmArgs& a, hipStream
     }
 }
 
+// k_q4_gemm_s launches: ring depth D, gps groups a slice (LDS sized for up to 4 or 8), (MT, S); false when the
+// combination is not instantiated. Q8_0 tiles take one stripe a wavefront (their weight registers are twice as many).
+template <int WT>
+static bool launch_gemm_s(int mt, int spw, int D, int gps, dim3 grid, const GemmArgs& a, hipStream_t st) {
+#define GSX(MT_, S_, D_, GM_)                                                                                \
+    if (mt == MT_ && spw == S_ && D == D_ && gps <= GM_) {                                                   \
+        hipLaunchKernelGGL((k_q4_gemm_s<WT, MT_, S_, D_, GM_>), grid, dim3(256), 0, st, a);                  \
+        return true;                                                                                         \
+    }
+    GSX(1, 1, 2, 4) GSX(1, 1, 2, 8) GSX(2, 1, 2, 4) GSX(2, 1, 2, 8)
+    if constexpr (WT == WT_Q4_0) {
+        GSX(1, 1, 4, 4) GSX(1, 1, 4, 8) GSX(2, 1, 4, 4)
+        GSX(1, 2, 2, 4) GSX(1, 2, 2, 8) GSX(1, 2, 4, 8) GSX(2, 2, 2, 4) GSX(2, 2, 2, 8) GSX(2, 2, 4, 4)
+        GSX(1, 4, 2, 4) GSX(1, 4, 2, 8) GSX(2, 4, 2, 4)
+    }
+#undef GSX
+    return false;
+}
+
 int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
                 hipStream_t st, int wt) {
     if (M <= 0) return 0;
@@ -569,6 +707,13 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
     a.M = M; a.N = N; a.K = K; a.ldy = 0; a.epi = EPI_STORE;
     a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
     a.mtiles = (M + 15) / 16;
+    if (p.stream && a.M < Q4_PAIR_ROWS) {  // the streaming kernel (ring depth 2)
+        const int mt = std::min(p.smt, a.mtiles);
+        const dim3 grid((p.nstripes + 4 * p.sspw - 1) / (4 * p.sspw), p.ks, (a.mtiles + mt - 1) / mt);
+        const bool ok = wt == WT_Q8_0 ? launch_gemm_s<WT_Q8_0>(mt, p.sspw, 2, p.gps, grid, a, st)
+                                      : launch_gemm_s<WT_Q4_0>(mt, p.sspw, 2, p.gps, grid, a, st);
+        return ok ? p.ks : -1;
+    }
     // row tiles of 16 per workgroup (grid z: one per tile) for matrices narrower than 512 stripes: twice the workgroups
     // and loads in flight (q|k|v, o, down: 8.4 against 9.1 us at 32 rows; the two workgroups of a tile pair run on the
     // same XCD, so the second reads the weights from its L2); pairs of tiles for the wider ones (the Q8_0 gate|up and
@@ -581,6 +726,27 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
     if (wt == WT_Q8_0) launch_gemm<WT_Q8_0>(mt, p.spw, grid, a, st);
     else launch_gemm<WT_Q4_0>(mt, p.spw, grid, a, st);
     return p.ks;
+}
+
+// An explicit launch plan (for tuning): the streaming kernel with mt row tiles a workgroup (1, 2), spw stripes a
+// wavefront (1, 2, 4), ring depth D and gps groups a slice, encoded G = -(100 D + gps); G 0: the default plan. The
+// k-slice sums go to part. Returns the slice count, or -1 (a plan not instantiated, or part too small).
+int q4_gemm_raw_plan(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
+                     hipStream_t st, int wt, int mt, int spw, int G) {
+    if (G == 0) return q4_gemm_raw(w, xa, M, N, K, part, part_bytes, st, wt);
+    if (G > 0) return -1;
+    const int gps = (-G) % 100, D = (-G) / 100;
+    GemmArgs a{};
+    a.w = w; a.xa = xa; a.part = part;
+    a.M = M; a.N = N; a.K = K; a.epi = EPI_STORE;
+    a.nstripes = (N + 15) / 16; a.ngroups = (K / 32 + 3) / 4; a.gps = gps; a.ks = (a.ngroups + gps - 1) / gps;
+    a.mtiles = (M + 15) / 16;
+    if (gps <= 0 || a.ks > KS_MAX || part == nullptr || part_bytes < (size_t) a.ks * M * N * sizeof(float)) return -1;
+    const int sets = (a.nstripes + 4 * spw - 1) / (4 * spw);
+    const dim3 grid(sets, a.ks, (a.mtiles + mt - 1) / mt);
+    const bool ok = wt == WT_Q8_0 ? launch_gemm_s<WT_Q8_0>(mt, spw, D, gps, grid, a, st)
+                                  : launch_gemm_s<WT_Q4_0>(mt, spw, D, gps, grid, a, st);
+    return ok ? a.ks : -1;
 }
 
 int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
@@ -599,6 +765,13 @@ int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, cons
     if (wt == WT_Q8_0) hipLaunchKernelGGL((k_q4_gemm<WT_Q8_0, 1, 1>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((k_q4_gemm<WT_Q4_0, 1, 1>), grid, dim3(256), 0, st, a);
     return 1;
+}
+
+void q4_reduce_slices(const float* part, int ks, int M, int N, float* y, hipStream_t st) {
+    GemmArgs a{};
+    a.part = const_cast<float*>(part); a.y = y;
+    a.M = M; a.N = N; a.ldy = N; a.epi = EPI_STORE; a.ks = ks;
+    hipLaunchKernelGGL(k_q4_reduce, dim3((M * N + 255) / 256), dim3(256), 0, st, a);
 }
 
 int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* ws,
@@ -687,7 +860,8 @@ static void launch_resid(int km, int nt, float* x, const float* part, int ks, in
     if (km == 1) RQ(1);
     else if (km == 2) RQ(2);
     else if (km == 4) RQ(4);
-    else RQ(8);
+    else if (km == 8) RQ(8);
+    else RQ(16);
 #undef RQ
 }
 
@@ -730,7 +904,8 @@ void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa
         if (km == 1) hipLaunchKernelGGL((k_swiglu_quant<1, S>), grid, dim3(256), 0, st, part, ks, M, F, h, xa, rows);
         else if (km == 2) hipLaunchKernelGGL((k_swiglu_quant<2, S>), grid, dim3(256), 0, st, part, ks, M, F, h, xa, rows);
         else if (km == 4) hipLaunchKernelGGL((k_swiglu_quant<4, S>), grid, dim3(256), 0, st, part, ks, M, F, h, xa, rows);
-        else hipLaunchKernelGGL((k_swiglu_quant<8, S>), grid, dim3(256), 0, st, part, ks, M, F, h, xa, rows);
+        else if (km == 8) hipLaunchKernelGGL((k_swiglu_quant<8, S>), grid, dim3(256), 0, st, part, ks, M, F, h, xa, rows);
+        else hipLaunchKernelGGL((k_swiglu_quant<16, S>), grid, dim3(256), 0, st, part, ks, M, F, h, xa, rows);
     };
     if (M >= SWQ_STAGE_ROWS) go(std::true_type{});
     else go(std::false_type{});

@@ -123,7 +123,7 @@ static inline size_t wt_bytes(int wt, int N, int K) {
 
 // The sum, in slice order, of ks <= KM k-slices of a matmul (slice k at p + k * stride). Every load is issued before
 // any is used (the slice index is clamped, so no load sits behind a branch); the slices past ks are not added.
-#define KS_MAX 8
+#define KS_MAX 16
 #define MOE_MAX_K 8  // experts used per row
 template <int KM>
 __device__ __forceinline__ float4 slices_sum4(const float* p, size_t stride, int ks) {
@@ -144,4 +144,6 @@ __device__ __forceinline__ float slices_sum1(const float* p, size_t stride, int 
     return s;
 }
 // the smallest slice bound of the kernels' instances that holds ks (0: ks out of range)
-static inline int ks_bound(int ks) { return ks < 1 ? 0 : ks == 1 ? 1 : ks <= 2 ? 2 : ks <= 4 ? 4 : ks <= KS_MAX ? 8 : 0; }
+static inline int ks_bound(int ks) {
+    return ks < 1 ? 0 : ks == 1 ? 1 : ks <= 2 ? 2 : ks <= 4 ? 4 : ks <= 8 ? 8 : ks <= KS_MAX ? 16 : 0;
+}

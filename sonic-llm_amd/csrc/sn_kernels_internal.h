@@ -22,13 +22,23 @@ struct GemmArgs {
 };
 
 // Launch shape of one matrix: a workgroup owns 4 spw stripes (a "set": spw per wavefront) and gps consecutive 4-block
-// groups (a slice).
+// groups (a slice). Layer-sized matrices at decode row counts run the streaming kernel (sspw stripes a wavefront,
+// smt row tiles a workgroup); LM-head-wide matrices and prompt-sized row counts the ring kernel (spw, sets). The
+// slices are the same for both, so a row's sums do not depend on the kernel.
 struct GemmPlan {
     int nstripes, ngroups, spw, sets, ks, gps;
+    bool stream;    // the streaming kernel serves this matrix below Q4_PAIR_ROWS rows
+    int sspw, smt;  // its stripes a wavefront and row tiles a workgroup
 };
 
 // Depends on (N, K) only, never on the rows.
 GemmPlan q4_plan(int N, int K, int wt = WT_Q4_0);
+// the raw matmul with an explicit plan (tuning): mt row tiles a workgroup, spw stripes a wavefront, G groups a slice
+// loaded at once (G 0: the default plan); the slice count, or -1
+// part[ks][M][N] added in slice order into y [M][N]
+void q4_reduce_slices(const float* part, int ks, int M, int N, float* y, hipStream_t st);
+int q4_gemm_raw_plan(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
+                     hipStream_t st, int wt, int mt, int spw, int G);
 // The k-slice sums of a matmul of M rows: ks * M * N floats.
 size_t q4_workspace_bytes(int M, int N, int K, int wt = WT_Q4_0);
 // Raw matmul: part[slice][M][N] = the slice's sums (the consumer adds the slices in order). Returns the slice count,

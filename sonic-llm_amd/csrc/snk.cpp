@@ -157,6 +157,39 @@ extern "C" double snk_q4_gemm_time(const void* const* d_stripes, int n_copies, c
     return hipGetLastError() == hipSuccess ? 1000.0 * ms / iters : -1.0;
 }
 
+extern "C" double snk_q4_gemm_plan_time(const void* const* d_stripes, int n_copies, const void* d_xa, int M, int N,
+                                        int K, void* d_ws, size_t ws_bytes, int mt, int spw, int G, int iters,
+                                        void* stream) {
+    hipStream_t st = (hipStream_t) stream;
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return -1.0;
+    for (int c = 0; c < n_copies; ++c)
+        if (q4_gemm_raw_plan((const uint8_t*) d_stripes[c], (const uint8_t*) d_xa, M, N, K, (float*) d_ws, ws_bytes,
+                             st, WT_Q4_0, mt, spw, G) < 0)
+            return -1.0;
+    hipEventRecord(a, st);
+    for (int i = 0; i < iters; ++i)
+        q4_gemm_raw_plan((const uint8_t*) d_stripes[i % n_copies], (const uint8_t*) d_xa, M, N, K, (float*) d_ws,
+                         ws_bytes, st, WT_Q4_0, mt, spw, G);
+    hipEventRecord(b, st);
+    hipEventSynchronize(b);
+    float ms = 0.0f;
+    hipEventElapsedTime(&ms, a, b);
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    return hipGetLastError() == hipSuccess ? 1000.0 * ms / iters : -1.0;
+}
+
+extern "C" int snk_q4_gemm_plan_sums(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y,
+                                     void* d_ws, size_t ws_bytes, int mt, int spw, int G, void* stream) {
+    // the plan's slices added in order into y [M][N] (for checking a plan against the default one)
+    const int ks = q4_gemm_raw_plan((const uint8_t*) d_stripes, (const uint8_t*) d_xa, M, N, K, (float*) d_ws,
+                                    ws_bytes, (hipStream_t) stream, WT_Q4_0, mt, spw, G);
+    if (ks < 0) return -1;
+    q4_reduce_slices((const float*) d_ws, ks, M, N, d_y, (hipStream_t) stream);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // ---- attention work lists
 struct snk_attn {
     int n_rows, H, KVH, max_pages, page_cells, max_chunks, n_items, n_mrows;
