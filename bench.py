@@ -327,7 +327,9 @@ def bench_mtp(args):
         gpu_ms += eng.last_gpu_ms()
     dt = time.perf_counter() - t0
     toks = kept
-    log(f"[bench] {args.steps} spec steps: {dt * 1e3 / args.steps:.3f} ms/step, {toks / args.steps:.2f} tokens/step")
+    caps, reps = eng.graph_count()
+    log(f"[bench] {args.steps} spec steps: {dt * 1e3 / args.steps:.3f} ms/step, {toks / args.steps:.2f} tokens/step "
+        f"(graph captures {caps}, replays {reps})")
     eng.prof(True)
     for _ in range(args.prof_steps):
         step()

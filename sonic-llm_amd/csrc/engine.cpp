@@ -1500,26 +1500,35 @@ extern "C" int snx_spec_step(sn_engine* e, int n, const int32_t* seq, const int3
     int32_t* d_outt = S.dev<int32_t>(o_outt);
     int32_t* d_keep = S.dev<int32_t>(o_keep);
     int32_t* d_acc = S.dev<int32_t>(o_acc);
-    Dev d{e, st};
-    // drafts: k rounds of n head rows (one a sequence), each round fed the guesses before it
-    for (int j = 0; j < k && d.rc == 0; ++j)
-        d.head_rows(n, j ? e->d_gtok + (j - 1) * e->slots : S.dev<const int32_t>(o_last), S.dev<const int32_t>(o_hseq),
-                    S.dev<const int32_t>(o_hpos) + (size_t) j * n, j == 0, S, hal[j], e->d_gtok + j * e->slots);
-    // verify rows [last, d1 .. dk] of every sequence through the model; the head's cells of those rows
-    spec_rows(n, k, e->slots, e->d_gtok, d_vtok, d_ftok, st);
-    d.model(R, d_vtok, d_vseq, d_vpos, S, al);
-    if (d.rc == 0) d.head_fill(R, d_vtok, d_vseq, d_vpos, S.dev<const int32_t>(o_src), 0, nullptr);
-    if (d.rc == 0)
-        d.outputs(e->x, R, S.dev<const int32_t>(o_rows), S.dev<const uint8_t>(o_skip),
-                  force ? S.dev<const uint8_t>(o_force) : nullptr, d_ftok);
-    // acceptance, the refused rows' cells cut in every layer, the head's state at the last kept row
-    accept_rows(n, k, e->slots, e->d_gtok, e->d_otok, d_vseq, d_outn, d_outt, d_keep, d_acc, st);
-    cut_cells(e->kbase, e->vbase, e->layer_halves, e->CL, e->KVH, e->page_cells, e->d_pt, e->max_pages, n, k, d_vseq,
-              d_vpos, d_acc, st);
-    rows_keep(e->mhn, d_keep, n, e->E, e->mpend, st);
+    // the key of the device work: the step's shape, how tokens are chosen, every staging offset, every attention list
+    std::vector<int64_t> key = {2, n, k, R, force != nullptr, e->want_probs, (int64_t) e->eog.size()};
+    for (size_t o : {o_vtok, o_vseq, o_vpos, o_rows, o_skip, o_force, o_last, o_hseq, o_hpos, o_src, o_ftok, o_outn,
+                     o_outt, o_keep, o_acc})
+        key.push_back((int64_t) o);
+    for (const AttnList& h : hal) h.key(key);
+    al.key(key);
+    const int drc = run_device(e, std::move(key), [&](Dev& d) {
+        // drafts: k rounds of n head rows (one a sequence), each round fed the guesses before it
+        for (int j = 0; j < k && d.rc == 0; ++j)
+            d.head_rows(n, j ? e->d_gtok + (j - 1) * e->slots : S.dev<const int32_t>(o_last),
+                        S.dev<const int32_t>(o_hseq), S.dev<const int32_t>(o_hpos) + (size_t) j * n, j == 0, S, hal[j],
+                        e->d_gtok + j * e->slots);
+        // verify rows [last, d1 .. dk] of every sequence through the model; the head's cells of those rows
+        spec_rows(n, k, e->slots, e->d_gtok, d_vtok, d_ftok, d.st);
+        d.model(R, d_vtok, d_vseq, d_vpos, S, al);
+        if (d.rc == 0) d.head_fill(R, d_vtok, d_vseq, d_vpos, S.dev<const int32_t>(o_src), 0, nullptr);
+        if (d.rc == 0)
+            d.outputs(e->x, R, S.dev<const int32_t>(o_rows), S.dev<const uint8_t>(o_skip),
+                      force ? S.dev<const uint8_t>(o_force) : nullptr, d_ftok);
+        // acceptance, the refused rows' cells cut in every layer, the head's state at the last kept row
+        accept_rows(n, k, e->slots, e->d_gtok, e->d_otok, d_vseq, d_outn, d_outt, d_keep, d_acc, d.st);
+        cut_cells(e->kbase, e->vbase, e->layer_halves, e->CL, e->KVH, e->page_cells, e->d_pt, e->max_pages, n, k,
+                  d_vseq, d_vpos, d_acc, d.st);
+        rows_keep(e->mhn, d_keep, n, e->E, e->mpend, d.st);
+    });
     SN_HIP_TRY(hipMemcpyAsync(e->h_otok, d_outt, (size_t) R * 4, hipMemcpyDeviceToHost, st), -1);
     SN_HIP_TRY(hipMemcpyAsync(e->h_rec, d_outn, (size_t) n * 4, hipMemcpyDeviceToHost, st), -1);
-    if (finish(e, d.rc, err, err_len) != 0) return -1;
+    if (finish(e, drc, err, err_len) != 0) return -1;
     memcpy(out_tok, e->h_otok, (size_t) R * 4);
     memcpy(out_n, e->h_rec, (size_t) n * 4);
     for (int s = 0; s < n; ++s) {  // the run each sequence keeps (sn_clear's cut of the head state)

@@ -198,6 +198,41 @@ def test_fused_step_equals_unfused(model):
         assert np.array_equal(a, b)
 
 
+def test_fused_step_graph_replay_equals_eager(model):
+    """The fused step's device work is captured as a HIP graph per shape (sequences, drafts, attention work-list
+    sizes, staging offsets) and replayed while the shape repeats: replays, and recaptures when a sequence's rows cross
+    a 256-cell chunk, give the tokens, accepted lengths and cache cells of eager launches, bit for bit."""
+    ps = prompts(4, 7)
+    res = []
+    for graphs in (True, False):
+        with S.Engine(model, slots=4, ctx=640, max_rows=64) as eng:
+            eng.graphs(graphs)
+            eng.guess_on(True)
+            last, _ = prefill(eng, None, ps)
+            pos = np.array([len(p) for p in ps], np.int32)
+            seqs = np.arange(4, dtype=np.int32)
+            for s in range(4):  # contexts just short of the 256-cell chunk boundary
+                eng.fill_kv(s, 250 + 2 * s, seed=3)
+            pos = np.array([250 + 2 * s for s in range(4)], np.int32)
+            rf = np.random.default_rng(4)
+            trace = []
+            for _ in range(8):
+                force = (rf.random((4, K)) < 0.6).astype(np.uint8)
+                n, t = eng.spec_step(seqs, last, pos, K, force=force)
+                trace.append((n.copy(), t.copy()))
+                last = t[np.arange(4), n - 1].astype(np.int32)
+                pos = pos + n
+            kv = [eng.kv_save(s, int(pos[s])) for s in range(4)]
+            res.append((trace, kv, eng.graph_count()))
+    (ta, kva, ga), (tb, kvb, gb) = res
+    for (na, xa), (nb, xb) in zip(ta, tb):
+        assert np.array_equal(na, nb) and np.array_equal(xa, xb), (na, nb, xa, xb)
+    for a, b in zip(kva, kvb):
+        assert np.array_equal(a, b)
+    assert ga[1] >= 2 and ga[0] >= 2, ga  # replays, and recaptures at the chunk crossings
+    assert gb == (0, 0)
+
+
 @pytest.mark.parametrize("which", ["model", "model_q6k_tied"])
 def test_fused_step_matches_oracle(request, which):
     model = request.getfixturevalue(which)
