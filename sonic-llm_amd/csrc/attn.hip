@@ -163,22 +163,29 @@ __device__ __forceinline__ void attn_wave(const u32x4 (&kf)[4][4], const u32x4 (
 }
 
 struct AttnShared {
-    float o[4][16][ATT_D + 4];
+    __attribute__((aligned(16))) float o[4][16][ATT_D + 4];  // (rows of 528 bytes: 16-byte pieces stay aligned)
     float m[4][16], l[4][16];
 };
 
 // The 4 wavefronts' partials combined in wavefront order into the chunk's partial of thread (query qq, dims d0 ..
-// d0 + 7): M = the max, L = the rescaled sum, acc = the rescaled outputs. Ends with the workgroup's LDS reads done
-// only when the caller syncs again.
-__device__ __forceinline__ void attn_combine(AttnShared& sh, int wave, int n, int g, float m, float l,
+// d0 + 7): M = the max, L = the rescaled sum, acc = the rescaled outputs. Only the group's nq = rows x G queries are
+// exchanged (lane part g holds queries 4g .. 4g + 3; a decode row's G = 4 queries are lane part 0's): each lane writes
+// its 8 dims of a query as two 16-byte pieces, each thread reads its query's 8 dims of each wavefront the same way.
+// The threads of queries past nq read LDS nobody wrote this round and compute values nobody stores. Ends with the
+// workgroup's LDS reads done only when the caller syncs again.
+__device__ __forceinline__ void attn_combine(AttnShared& sh, int wave, int n, int g, int nq, float m, float l,
                                              const floatx4 (&o)[8], int qq, int d0, float& M, float& L,
                                              float (&acc)[8]) {
     if (g == 0) {
         sh.m[wave][n] = m;
         sh.l[wave][n] = l;
     }
-    for (int t = 0; t < 8; ++t)
-        for (int v = 0; v < 4; ++v) sh.o[wave][4 * g + v][8 * n + t] = o[t][v];
+    if (4 * g < nq)
+        for (int v = 0; v < 4; ++v) {
+            float* row = &sh.o[wave][4 * g + v][8 * n];
+            *(float4*) row = (float4){o[0][v], o[1][v], o[2][v], o[3][v]};
+            *(float4*) (row + 4) = (float4){o[4][v], o[5][v], o[6][v], o[7][v]};
+        }
     __syncthreads();
     M = -INFINITY;
     for (int w = 0; w < 4; ++w) M = fmaxf(M, sh.m[w][qq]);
@@ -188,9 +195,15 @@ __device__ __forceinline__ void attn_combine(AttnShared& sh, int wave, int n, in
         e[w] = sh.m[w][qq] == -INFINITY ? 0.0f : __expf(sh.m[w][qq] - M);
         L += sh.l[w][qq] * e[w];
     }
+    float ow[4][8];
+    for (int w = 0; w < 4; ++w) {
+        const float4 a = *(const float4*) &sh.o[w][qq][d0], b = *(const float4*) &sh.o[w][qq][d0 + 4];
+        ow[w][0] = a.x, ow[w][1] = a.y, ow[w][2] = a.z, ow[w][3] = a.w;
+        ow[w][4] = b.x, ow[w][5] = b.y, ow[w][6] = b.z, ow[w][7] = b.w;
+    }
     for (int d = 0; d < 8; ++d) {
         float s = 0.0f;
-        for (int w = 0; w < 4; ++w) s += sh.o[w][qq][d0 + d] * e[w];
+        for (int w = 0; w < 4; ++w) s += ow[w][d] * e[w];
         acc[d] = s;
     }
 }
@@ -244,15 +257,15 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
     // thread -> (query qq, 8 dims)
     const int qq = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
     float M, L, acc[8];
-    attn_combine(sh, wave, n, g, m, l, o, qq, d0, M, L, acc);
+    attn_combine(sh, wave, n, g, gr.nrows * G, m, l, o, qq, d0, M, L, acc);
     const int row = qq / G, head = kvh * G + qq % G;
     if (row >= gr.nrows) return;
     float* dst = a.part + (((size_t) (gr.row0 + row) * a.H + head) * a.max_chunks + it.chunk) * (ATT_D + 2);
-    for (int d = 0; d < 8; ++d) dst[d0 + d] = acc[d];
-    if ((threadIdx.x & 15) == 0) {
-        dst[ATT_D] = M;
-        dst[ATT_D + 1] = L;
-    }
+    *(float2*) (dst + d0) = (float2){acc[0], acc[1]};  // (a partial is 130 floats: 8-byte aligned)
+    *(float2*) (dst + d0 + 2) = (float2){acc[2], acc[3]};
+    *(float2*) (dst + d0 + 4) = (float2){acc[4], acc[5]};
+    *(float2*) (dst + d0 + 6) = (float2){acc[6], acc[7]};
+    if ((threadIdx.x & 15) == 0) *(float2*) (dst + ATT_D) = (float2){M, L};
 }
 
 // The Q8_0 operand of the o-projection from a row's normalised outputs (ggml x86 quantize_row_q8_0, exactly as the
@@ -360,7 +373,7 @@ __global__ __launch_bounds__(512) void k_attn_whole(AttnArgs a) {
         attn_issue_v(a, rn, ncb, npl, n, g, vf);
         __builtin_amdgcn_sched_barrier(0);
         float M, L, acc[8];
-        attn_combine(sh.h[half], wave, n, g, m, l, o, qq, d0, M, L, acc);
+        attn_combine(sh.h[half], wave, n, g, gr.nrows * G, m, l, o, qq, d0, M, L, acc);
         // (no branch on the half: the second half writes its partial and also folds, into a state never used)
         float* xw = sh.x[half ? th : 256];
         for (int d = 0; d < 8; ++d) xw[d] = acc[d];
