@@ -944,9 +944,10 @@ struct Dev {
         return true;
     }
 
-    // MoE FFN (moe_ffn, sn_layers.inc.h:129-144): x += o's sums, ffn norm (the rows kept as hn); router, top-k and
-    // renormalised weights; the (row, expert) pairs in expert-major 16-row tiles; their Q8_0 operand gathered from hn;
-    // grouped gate/up (SwiGLU + Q8_0) and down matmuls over the used experts; the weighted sum in slot order into x
+    // MoE FFN (moe_ffn, sn_layers.inc.h:129-144): x += o's sums, ffn norm (the rows kept as hn, their Q8_0 operand in
+    // row order); router, top-k and renormalised weights; the (row, expert) pairs in expert-major 16-row tiles;
+    // grouped gate/up (its operand rows gathered from hn's, SwiGLU + Q8_0) and down matmuls over the used experts; the
+    // weighted sum in slot order into x
     void moe(const DevLayer& l, float* x, int R) {
         const int E = e->E, NE = e->NE, NU = e->NEU, FE = e->FE, T = e->moe_tiles, P = T * 16;
         rc |= e->launch(SNX_K_QUANT, (double) R * E * (8 + 4 * ks) + (double) R * E * 6, [&] {
@@ -970,10 +971,10 @@ struct Dev {
                     if (!seen[it[2 * i]]) seen[it[2 * i]] = true, used += 1;
             }
         }
-        quant(e->hn, e->rsrc, P, E, nullptr);
+        // (the expert tiles' rows gathered from hn's Q8_0 operand, which the resid above wrote in row order)
         rc |= e->launch(SNX_K_GEMM, used * e->egu_stride + (double) R * NU * E * 4 + (double) R * NU * 2 * FE * 4, [&] {
             return q4_gemm_grouped(l.egu, e->egu_stride, e->gitems, e->gcount, T, e->xa, P, 2 * FE, E, e->gemm_ws,
-                                   e->gemm_ws_bytes, st, e->wt, e->rsrc) < 0 ? -1 : 0;
+                                   e->gemm_ws_bytes, st, e->wt, e->rsrc, e->rsrc, R) < 0 ? -1 : 0;
         });
         rc |= e->launch(SNX_K_QUANT, (double) R * NU * FE * 14, [&] {
             swiglu_quant(e->gemm_ws, 1, P, FE, nullptr, e->xa, st, e->rsrc);

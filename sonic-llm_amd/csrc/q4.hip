@@ -405,9 +405,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(S, a.nstripes - s0)));
     const int sbytes = a.ngroups * TB;  // one stripe
     const __amdgpu_buffer_rsrc_t wr = buf_rsrc(wbase + (size_t) min(s0, a.nstripes - 1) * sbytes, (uint32_t) (nvalid * sbytes));
-    const size_t x0 = (size_t) mt0 * a.ngroups * XA_REC;
-    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xa + x0, (uint32_t) (xa_bytes(a.M, a.K) - x0));
     const int rstride = a.ngroups * XA_REC;  // between row tiles' records
+    // the activation: the operand's records from row tile mt0 on; or, gathering (a.gsrc, one row tile), each lane's row
+    // m = lane % 16 of the tile taken from row gsrc[16 mt0 + m] of a row-ordered operand of a.gM rows (a padding row,
+    // gsrc < 0, reads as zeros: its offset is past the buffer). The per-lane offset of a row's piece of a record:
+    // fragments 16 (row % 16 + 16 g), scales and corrections 4 (16 b + row % 16), b = lane / 16.
+    size_t x0 = (size_t) mt0 * a.ngroups * XA_REC;
+    uint32_t xbytes = (uint32_t) (xa_bytes(a.M, a.K) - x0);
+    int vf_off = 16 * lane, vk_off = 4 * lane;
+    if (a.gsrc) {
+        const int sr = a.gsrc[16 * mt0 + (lane & 15)];
+        x0 = 0;
+        xbytes = (uint32_t) xa_bytes(a.gM, a.K);
+        vf_off = sr < 0 ? (int) XA_GATHER_OOB : (sr >> 4) * rstride + 16 * ((sr & 15) + 16 * g);
+        vk_off = sr < 0 ? (int) XA_GATHER_OOB : (sr >> 4) * rstride + 4 * (16 * g + (sr & 15));
+    }
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xa + x0, xbytes);
     // what this wavefront stages: fragments f = wave * FPW + j (row tile f / 4, block f % 4); constant block kb =
     // wave (row tile kb / 2; dx or corr) while kb < 2 MT
     const int kb = min(wave, 2 * MT - 1);
@@ -424,9 +437,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
         const int c = c0 + min(i, ng - 1);
         for (int j = 0; j < FPW; ++j) {
             const int f = wave * FPW + j;
-            ra[slot][j] = bload16(xr, 16 * lane, (f / 4) * rstride + c * XA_REC + (f % 4) * 1024);
+            ra[slot][j] = bload16(xr, vf_off, (f / 4) * rstride + c * XA_REC + (f % 4) * 1024);
         }
-        rk[slot] = bload4f(xr, 4 * lane, (kb / 2) * rstride + c * XA_REC + (kb % 2 ? CORR : XA_DX_OFF));
+        rk[slot] = bload4f(xr, vk_off, (kb / 2) * rstride + c * XA_REC + (kb % 2 ? CORR : XA_DX_OFF));
         for (int s = 0; s < S; ++s) {
             const int so = s * sbytes + c * TB;
             for (int h = 0; h < NW; ++h) wq[slot][s][h] = bload16(wr, 16 * NW * lane + 16 * h, so);
@@ -751,13 +764,15 @@ int q4_gemm_raw_plan(const uint8_t* w, const uint8_t* xa, int M, int N, int K, f
 
 int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
                     const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st, int wt,
-                    const int32_t* rmask) {
+                    const int32_t* rmask, const int32_t* gsrc, int gM) {
     if (M <= 0 || max_items <= 0) return 0;
     if (wt != WT_Q4_0 && wt != WT_Q8_0) return -1;
     if (part == nullptr || part_bytes < (size_t) M * N * sizeof(float)) return -1;
+    if (gsrc && gM <= 0) return -1;
     GemmArgs a{};
     a.w = w; a.xa = xa; a.part = part;
     a.items = items; a.count = count; a.wstride = wstride; a.rmask = rmask;
+    a.gsrc = gsrc; a.gM = gM;
     a.M = M; a.N = N; a.K = K; a.epi = EPI_STORE;
     a.nstripes = (N + 15) / 16; a.ngroups = (K / 32 + 3) / 4; a.ks = 1; a.gps = a.ngroups;
     a.mtiles = (M + 15) / 16;

@@ -17,6 +17,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // ---- raw buffer loads: a per-lane byte offset and a wavefront-uniform one against a resource of `bytes`; a load
 // reaching past `bytes` returns zeros and touches no memory
 #define RSRC_WORD3 0x00020000  // raw buffer resource, gfx9 data format
+#define XA_GATHER_OOB 0x40000000u  // a per-lane offset past any buffer this code makes: the load reads zeros
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short) 0, (int) bytes, RSRC_WORD3);
 }

@@ -17,6 +17,10 @@ struct GemmArgs {
     const int32_t* count;
     size_t wstride;
     const int32_t* rmask;  // (optional) rows p with rmask[p] < 0 are not stored
+    // (optional, grouped) the activation gathered: tile row p is row gsrc[p] (< 0: zeros) of a row-ordered operand of
+    // gM rows, instead of row p of a tile-ordered one
+    const int32_t* gsrc;
+    int gM;
     int M, N, K, ldy, epi;
     int nstripes, ngroups, ks, gps, mtiles;
 };
@@ -47,9 +51,11 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
                 hipStream_t st, int wt = WT_Q4_0);
 // Grouped raw matmul of expert matrices (moe: qmm_grouped, sn_attn.inc.h:352-359): up to max_items (expert, row tile)
 // items, the device count in `count`; part[M][N] rows of each item's tile (one slice).
+// gsrc (optional): the operand's tile row p is row gsrc[p] of the row-ordered operand xa of gM rows (gathered while
+// loading; gsrc[p] < 0 reads zeros), as if the rows had been quantized into expert-tile order.
 int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
                     const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st,
-                    int wt = WT_Q4_0, const int32_t* rmask = nullptr);
+                    int wt = WT_Q4_0, const int32_t* rmask = nullptr, const int32_t* gsrc = nullptr, int gM = 0);
 // GGUF Q4_0 (wt = WT_Q4_0) or Q8_0 (WT_Q8_0) rows -> tiles; source stripe s lands at destination stripe
 // s * sstride + soff.
 void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int soff, hipStream_t st,
