@@ -25,6 +25,9 @@ for p in (ROOT, os.path.join(ROOT, "sonic-llm_amd")):
         sys.path.insert(0, p)
 
 HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
+# the matrices of the Qwen3-4B-arch decode step at its 32 rows: (M, N, K); q|k|v and gate|up fused
+DECODE_SHAPES = {"qkv": (32, 6144, 2560), "o": (32, 2560, 4096), "gateup": (32, 19456, 2560), "down": (32, 2560, 9728),
+                 "head": (32, 151936, 2560)}
 MFMA_F16_PEAK = 2.5e15  # MI355X dense fp16 MFMA, flop/s
 
 
@@ -111,6 +114,8 @@ def main():
                          "matmul (configs[0]); attn: one layer of paged decode attention (configs[1]); prefill: "
                          "2048-token prompts in 512-row steps")
     ap.add_argument("--accept", type=float, default=0.6, help="mtp: the seeded share of drafts forced to match")
+    ap.add_argument("--mm-shape", default="c1", choices=("c1",) + tuple(DECODE_SHAPES),
+                    help="matmul: configs[0] (c1, the default) or one of the 32-row decode step's matrices")
     ap.add_argument("--no-graphs", action="store_true", help="launch every step eagerly (no HIP graph replay)")
     ap.add_argument("--no-chain", action="store_true", help="decode without sn_step's queued successor (chain = 0)")
     ap.add_argument("--attn-mode", type=int, default=-1, choices=(-1, 0, 1),
@@ -148,6 +153,14 @@ def main():
         return
     # all: the headline with the other configurations' lines inside it
     line = bench_decode(args, moe=False)
+    t = time.time()
+    try:
+        line["gemm_shapes"] = {name: matmul_shape(*mnk, seed=3) for name, mnk in DECODE_SHAPES.items()}
+    except Exception as e:
+        import traceback
+        traceback.print_exc()
+        line["gemm_shapes"] = {"error": repr(e)}
+    log(f"[bench] gemm shapes in {time.time() - t:.1f}s")
     line["configs"] = {}
     for name, fn in (("c1_matmul", bench_matmul), ("c2_attn", bench_attn), ("c4_mtp", bench_mtp),
                      ("c5_moe", lambda a: bench_decode(a, moe=True))):
@@ -629,6 +642,57 @@ class Dev:
         return C.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
+def matmul_shape(M, N, K, seed, copies=None, Wq=None):
+    """One Q4_0 matmul shape: the matmul kernel's average launch time (its k-slice sums, launches back to back on one
+    stream, weight copies in turn beyond the 256 MB Infinity Cache) beside a plain streaming read of the same weight
+    bytes from the same copies (snk_read_time): the floor a launch of that size meets on this box."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    import sllm_next as S
+
+    U = Dev
+    L = S.lib()
+    r = np.random.default_rng(seed)
+    if Wq is None:  # (a seeded block of up to 8192 rows, repeated: a launch costs the same whatever W holds)
+        nb = min(N, 8192)
+        Wq = S.quantize_q4_0((r.standard_normal((nb, K)) * 0.02).astype(np.float32))
+        Wq = np.ascontiguousarray(np.tile(Wq, ((N + nb - 1) // nb, 1))[:N])
+    sb = L.snk_q4_stripes_bytes(N, K)
+    copies = copies or max(2, int(np.ceil(600e6 / sb)))
+    st0 = U.stream()
+    dW = U.copy(Wq)
+    tiles = [U.empty(sb) for _ in range(copies)]
+    for t in tiles:
+        assert L.snk_q4_repack(U.ptr(dW), N, K, U.ptr(t), st0) == 0
+    X = r.standard_normal((M, K)).astype(np.float32)
+    dX = U.copy(X)
+    xa = U.empty(L.snk_xa_bytes(M, K))
+    assert L.snk_quant_act(U.ptr(dX), M, K, K, None, C.c_float(0.0), U.ptr(xa), st0) == 0
+    wsb = L.snk_q4_workspace_bytes(M, N, K)
+    ws = U.empty(wsb)
+    y = U.empty(M * N * 4)
+    sink = U.empty(1024)
+    torch.cuda.synchronize()
+    ptrs = (C.c_void_p * copies)(*[t.data_ptr() for t in tiles])
+    us = L.snk_q4_gemm_time(C.cast(ptrs, C.c_void_p), copies, U.ptr(xa), M, N, K, U.ptr(y), N, U.ptr(ws),
+                            C.c_size_t(wsb), 200, st0)
+    us_read = L.snk_read_time(C.cast(ptrs, C.c_void_p), copies, C.c_size_t(sb // 16 * 16), C.c_void_p(sink.data_ptr()),
+                              200, st0)
+    alg = N * K // 32 * 18 + M * K * 4 + M * N * 4
+    out = {"M": M, "N": N, "K": K, "weight_copies": copies, "algorithmic_bytes": alg, "us_per_launch": round(us, 3),
+           "GBps": round(alg / (us * 1e-6) / 1e9, 1), "frac": round(alg / (us * 1e-6) / HBM_PEAK, 4),
+           "read_floor_us": round(us_read, 3), "read_floor_GBps": round(sb / (us_read * 1e-6) / 1e9, 1),
+           "floor_frac": round(us_read / us, 4)}
+    log(f"[bench] matmul {M}x{N}x{K}: {us:.2f} us ({out['GBps']} GB/s); a plain read of its {sb / 1e6:.1f} MB of "
+        f"weights {us_read:.2f} us ({out['read_floor_GBps']} GB/s)")
+    del tiles
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_matmul(args):
     """configs[0] (C1): one Q4_0 matmul Y[8][4096] = X[8][4096] . W[4096][4096]^T. W ~ N(0, 0.02) (seed 1) quantized
     by ggml's reference Q4_0 rule, X ~ N(0, 1). One call is the op as a drop-in runs it: X quantized to the Q8_0 operand,
@@ -641,6 +705,16 @@ def bench_matmul(args):
 
     import sllm_next as S
 
+    if args.mm_shape != "c1":  # one of the decode step's matrices: the kernel beside its read floor, no CPU line
+        M, N, K = DECODE_SHAPES[args.mm_shape]
+        sh = matmul_shape(M, N, K, seed=3)
+        return {"metric": f"Q4_0 matmul GB/s (algorithmic W + X + Y bytes), {M} x {N} x {K}", "value": sh["GBps"],
+                "unit": "GB/s", "n_gpus": 1, "steps": 200, "warmup": sh["weight_copies"],
+                "ms_per_step": round(sh["us_per_launch"] * 1e-3, 5), "higher_is_better": True, "scaling": "weak",
+                "vs_baseline": None, "dtype": "q4_0 x q8_0 -> f32 (fp16 MFMA)",
+                "data": "synthetic: W ~ N(0, 0.02) seed 3 quantized to Q4_0, X ~ N(0, 1)",
+                "config": {"workload": f"the {args.mm_shape} matrix of the 32-row decode step (BASELINE.json "
+                                       f"configs[2])", **sh}}
     U = Dev
     L = S.lib()
     N = K = 4096
@@ -689,7 +763,11 @@ def bench_matmul(args):
                          f"Q8_0 activations, integer block dots; generic scalar loops, slower than ggml's AVX2 / "
                          f"AVX-512 kernels): median of {reps} warm calls, {dt * 1e3:.2f} ms each"}
     gbs, gbs_k = alg / (us * 1e-6) / 1e9, alg / (us_gemm * 1e-6) / 1e9
-    log(f"[bench] C1 matmul: {us:.2f} us per call (quantize + matmul + reduce), matmul kernel {us_gemm:.2f} us")
+    sink = U.empty(1024)
+    us_read = L.snk_read_time(C.cast(ptrs, C.c_void_p), copies, C.c_size_t(L.snk_q4_stripes_bytes(N, K)),
+                              C.c_void_p(sink.data_ptr()), 200, st0)
+    log(f"[bench] C1 matmul: {us:.2f} us per call (quantize + matmul + reduce), matmul kernel {us_gemm:.2f} us; a "
+        f"plain read of the weights {us_read:.2f} us")
     line = {
         "metric": "Q4_0 matmul GB/s (algorithmic W + X + Y bytes), 8 x 4096 x 4096",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": n, "warmup": args.warmup,
@@ -698,7 +776,8 @@ def bench_matmul(args):
         "data": "synthetic: W ~ N(0, 0.02) seed 1 quantized to Q4_0 (ggml reference rule), X ~ N(0, 1)",
         "config": {"workload": "single Q4_0 matmul (BASELINE.json configs[0])", "M": M, "N": N, "K": K,
                    "weight_copies": copies, "algorithmic_bytes": alg, "us_per_call": round(us, 3),
-                   "us_matmul_kernel": round(us_gemm, 3)},
+                   "us_matmul_kernel": round(us_gemm, 3), "read_floor_us": round(us_read, 3),
+                   "floor_frac": round(us_read / us_gemm, 4)},
         "roofline": {"kernel": "k_q4_gemm", "bound": "hbm", "achieved": round(gbs_k, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(gbs_k * 1e9 / HBM_PEAK, 4),
                      "traffic": profile_traffic("matmul_q4_0_b8_4096x4096_traffic.json", "k_q4_gemm"),

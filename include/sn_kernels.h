@@ -74,6 +74,12 @@ int snk_q4_gemm_noalloc(const void* d_stripes, const void* d_xa, int M, int N, i
 double snk_q4_gemm_time(const void* const* d_stripes, int n_copies, const void* d_xa, int M, int N, int K, float* d_y,
                         int ldy, void* d_ws, size_t ws_bytes, int iters, void* stream);
 
+// Average device time (microseconds) of one plain streaming read of `bytes` (a multiple of 16) over `iters` launches
+// back to back on `stream`, from n_copies buffers in turn (d_sink: 1 KB of device memory the kernel could write): the
+// floor for launches that move that many bytes, measured beside them. No counterpart in the reference (a calibration
+// of this box); -1 for bad arguments.
+double snk_read_time(const void* const* d_bufs, int n_copies, size_t bytes, float* d_sink, int iters, void* stream);
+
 // Launch-plan tuning of the matmul (raw k-slice sums of Q4_0 stripes): an explicit plan of mt row tiles a workgroup
 // (1, 2), spw stripes a wavefront (1, 2) and G groups a slice with every load of the slice issued at once (G 0: the
 // default plan). snk_q4_gemm_plan_time: average device time (microseconds) of one launch over `iters` launches on

@@ -56,6 +56,9 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
 int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
                     const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st,
                     int wt = WT_Q4_0, const int32_t* rmask = nullptr, const int32_t* gsrc = nullptr, int gM = 0);
+// one plain streaming read of `bytes` (a multiple of 16) from buf (a calibration launch; sink: 1 KB, never written
+// in practice)
+void read_floor(const void* buf, size_t bytes, float* sink, hipStream_t st);
 // GGUF Q4_0 (wt = WT_Q4_0) or Q8_0 (WT_Q8_0) rows -> tiles; source stripe s lands at destination stripe
 // s * sstride + soff.
 void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int soff, hipStream_t st,

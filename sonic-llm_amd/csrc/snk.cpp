@@ -157,6 +157,24 @@ extern "C" double snk_q4_gemm_time(const void* const* d_stripes, int n_copies, c
     return hipGetLastError() == hipSuccess ? 1000.0 * ms / iters : -1.0;
 }
 
+extern "C" double snk_read_time(const void* const* d_bufs, int n_copies, size_t bytes, float* d_sink, int iters,
+                                void* stream) {
+    if (n_copies <= 0 || bytes < 16 || bytes % 16 || iters <= 0 || !d_sink) return -1.0;
+    hipStream_t st = (hipStream_t) stream;
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return -1.0;
+    for (int c = 0; c < n_copies; ++c) read_floor(d_bufs[c], bytes, d_sink, st);
+    hipEventRecord(a, st);
+    for (int i = 0; i < iters; ++i) read_floor(d_bufs[i % n_copies], bytes, d_sink, st);
+    hipEventRecord(b, st);
+    hipEventSynchronize(b);
+    float ms = 0.0f;
+    hipEventElapsedTime(&ms, a, b);
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    return hipGetLastError() == hipSuccess ? 1000.0 * ms / iters : -1.0;
+}
+
 extern "C" double snk_q4_gemm_plan_time(const void* const* d_stripes, int n_copies, const void* d_xa, int M, int N,
                                         int K, void* d_ws, size_t ws_bytes, int mt, int spw, int G, int iters,
                                         void* stream) {

@@ -115,6 +115,7 @@ SNK_API = [
     ("snk_q4_gemm_noalloc", I, [P, P, I, I, I, P, I, I, P, CH, I]),
     ("snk_q4_gemm_time", C.c_double, [P, I, P, I, I, I, P, I, P, C.c_size_t, I, P]),
     ("snk_q4_gemm_plan_time", C.c_double, [P, I, P, I, I, I, P, C.c_size_t, I, I, I, I, P]),
+    ("snk_read_time", C.c_double, [P, I, C.c_size_t, P, I, P]),
     ("snk_q4_gemm_plan_sums", I, [P, P, I, I, I, P, P, C.c_size_t, I, I, I, P]),
     ("snk_attn_new", P, [I, P, P, I, I, I, I, CH, I]),
     ("snk_attn_new_mode", P, [I, P, P, I, I, I, I, I, CH, I]),
