@@ -310,6 +310,8 @@ def bench_mtp(args):
     total = ctx + (args.warmup + args.steps + args.prof_steps) * (k + 1) + 8
     t = time.time()
     eng = S.Engine(path, slots=B, ctx=total, max_rows=B * (k + 1))
+    if args.no_graphs:
+        eng.graphs(False)
     eng.attn_mode(args.attn_mode)
     assert eng.guess_head() and eng.guess_on(True)
     for s in range(B):
@@ -382,7 +384,8 @@ def bench_mtp(args):
                      "traffic": profile_traffic("mtp_qwen3_4b_b8_ctx4096_k3_traffic.json", dom),
                      "bytes_per_launch": kernels[dom]["bytes_per_launch"],
                      "us_per_launch": kernels[dom]["us_per_launch"]} if dom else None,
-        "verify_gemm_mfma": profile_traffic("mtp_qwen3_4b_b8_ctx4096_k3_traffic.json", "verify_gemm_mfma_busy"),
+        "verify_gemm_mfma": profile_value("mtp_qwen3_4b_b8_ctx4096_k3_traffic.json",
+                                          ("verify_gemm_mfma_busy", "verify_gemm_tflops")),
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
@@ -508,6 +511,15 @@ def profile_traffic(name, key):
         return None
     v = json.load(open(path)).get(key)
     return round(v) if v is not None else None
+
+
+def profile_value(name, keys):
+    """values measured by the committed rocprofv3 counter runs (profiles/), with their source, or None"""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    d = json.load(open(path))
+    return {**{k: d.get(k) for k in keys}, "source": "profiles/" + name.replace(".json", ".md")}
 
 
 def cpu_threads():
