@@ -857,8 +857,10 @@ def bench_attn(args):
     dpt, dq = U.copy(pt), U.copy(q)
     out = U.empty(n_seq * H * D * 4)
     err = C.create_string_buffer(256)
-    plan = L.snk_attn_new_mode(n_seq, seq.ctypes.data, pos.ctypes.data, H, KVH, pt.shape[1], page, args.attn_mode, err,
-                               256)
+    # the planner sees the page table: the sharers' common 1024-cell prefix is read once per (chunk, KV head)
+    ptc = np.ascontiguousarray(pt, np.int32)
+    plan = L.snk_attn_new_pt(n_seq, seq.ctypes.data, pos.ctypes.data, H, KVH, pt.shape[1], page, args.attn_mode,
+                             ptc.ctypes.data, err, 256)
     assert plan, err.value
     whole = bool(L.snk_attn_whole(plan))
     scale = C.c_float(1.0 / np.sqrt(D))

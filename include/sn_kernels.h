@@ -107,6 +107,12 @@ double snk_attn_time(snk_attn* p, const float* d_q, int ldq, const void* d_kpool
 // merge, 1 whole groups (for tests and timing; both forms give the same bits for a row)
 snk_attn* snk_attn_new_mode(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH, int max_pages,
                             int page_cells, int mode, char* err, int err_len);
+// the same with the host copy of the page table (pt [slots][max_pages], the rows' slots index it): a decode row's
+// 256-cell chunk that lies wholly below its position on the very pages of other decode rows' same chunk (a shared
+// prefix: sn_copy's pages) is read once for up to 4 such rows (16 / (H / KVH) at most), the engine's plan for every
+// step (attn_part's per-chunk items, kernels.metal:1122-1192, with sharers batched). Gives the same bits for a row.
+snk_attn* snk_attn_new_pt(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH, int max_pages,
+                          int page_cells, int mode, const int32_t* pt, char* err, int err_len);
 // 1 when the list is whole groups (one workgroup per (group, KV head) walks its whole context and writes the output:
 // one launch, no merge; chosen when the groups make one round of 240 .. 256 workgroups, no context is over 9/8 of the
 // mean and the contexts are long), 0 when it is one item per 256-cell chunk followed by the merge. Both give the same

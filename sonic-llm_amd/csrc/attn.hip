@@ -13,6 +13,7 @@
 // Scores of cells past a row's position are -inf and their p exactly 0, so a row's result does not depend on the
 // other rows of its group, and a verify row equals the same row run alone.
 #include <algorithm>
+#include <map>
 
 #include "sn_kernels_internal.h"
 
@@ -32,17 +33,23 @@ __device__ __forceinline__ uint32_t pick_half(uint32_t w_lo_cell, uint32_t w_hi_
 
 // ---- the steps of one wavefront's 64 cells (shared by both kernels, so a chunk's arithmetic is the same in each)
 
-// Q^T fragments: MFMA t covers dims 32t .. 32t+31; lane (n, g) holds dims 32t + 8g .. +7 of query n. Loaded as
-// 16-byte pieces from a valid row (an unused column reads the group's first row) and zeroed by a select, so no load
-// sits behind a branch.
-__device__ __forceinline__ void attn_qfrag(const AttnArgs& a, const AttnGroup& gr, int qrow, int qhead, bool qvalid,
-                                           int g, half8 (&qh)[4], half8 (&ql)[4]) {
-    const float* qp = a.q + (size_t) (gr.row0 + (qvalid ? qrow : 0)) * a.ldq + (size_t) qhead * ATT_D;
+// Q^T fragments of step row `row` (an unused column passes a valid row and qvalid false)
+__device__ __forceinline__ void attn_qfrag_row(const AttnArgs& a, int row, int qhead, bool qvalid, int g,
+                                               half8 (&qh)[4], half8 (&ql)[4]) {
+    const float* qp = a.q + (size_t) row * a.ldq + (size_t) qhead * ATT_D;
     for (int t = 0; t < 4; ++t) {
         const float4 x0 = *(const float4*) (qp + 32 * t + 8 * g), x1 = *(const float4*) (qp + 32 * t + 8 * g + 4);
         const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         for (int j = 0; j < 8; ++j) split_hl(qvalid ? xs[j] * a.scale : 0.0f, qh[t], ql[t], j);
     }
+}
+
+// Q^T fragments: MFMA t covers dims 32t .. 32t+31; lane (n, g) holds dims 32t + 8g .. +7 of query n. Loaded as
+// 16-byte pieces from a valid row (an unused column reads the group's first row) and zeroed by a select, so no load
+// sits behind a branch.
+__device__ __forceinline__ void attn_qfrag(const AttnArgs& a, const AttnGroup& gr, int qrow, int qhead, bool qvalid,
+                                           int g, half8 (&qh)[4], half8 (&ql)[4]) {
+    attn_qfrag_row(a, gr.row0 + (qvalid ? qrow : 0), qhead, qvalid, g, qh, ql);
 }
 
 // The page ids of a wavefront's 64 cells from cbase: one page (64-cell pages) or two (32-cell pages). Cells past the
@@ -229,8 +236,15 @@ __device__ __forceinline__ void attn_finish(float L, float (&o)[ND]) {
     for (int d = 0; d < ND; ++d) o[d] *= il;
 }
 
-// One work item = (query group, chunk); grid.y = KV head. Writes the chunk's partial (acc[128], m, l) of every query of
-// the group; k_attn_merge folds them.
+// the group of a shared item's member m (0: the item's own group; -1: none), by selects (m may differ per lane)
+__device__ __forceinline__ int attn_member(const AttnItem& it, int m) {
+    static_assert(ATT_SHARE_MAX == 4, "three shared members after the item's own group");
+    return m == 0 ? it.group : m == 1 ? it.share[0] : m == 2 ? it.share[1] : m == 3 ? it.share[2] : -1;
+}
+
+// One work item = (query group, chunk), or a shared chunk of up to ATT_SHARE_MAX one-row groups; grid.y = KV head.
+// Writes the chunk's partial (acc[128], m, l) of every query of the item's rows; k_attn_merge folds them. A query's
+// partial depends on its own column only, so it is the same whichever item computes it.
 __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
     __shared__ AttnShared sh;
     const AttnItem it = a.items[blockIdx.x];
@@ -239,14 +253,33 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
     const int G = a.H / a.KVH;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
+    const bool shared = it.share[0] >= 0;  // (uniform)
+    int nshare = 1;
+    if (shared)
+        while (nshare < ATT_SHARE_MAX && nshare * G < 16 && attn_member(it, nshare) >= 0) ++nshare;
+    // the pages and the cells' bound come from the item's own group (a shared chunk lies wholly below every member's
+    // position, on the same pages)
     const int pos_last = gr.pos0 + gr.nrows - 1;
     const int cbase = it.chunk * ATT_CHUNK + 64 * wave;  // this wavefront's first cell
-    // this lane's query (as a B column of S^T and the A row of O): n = row * G + head-in-group
-    const int qrow = n / G, qhead = kvh * G + n % G;
-    const bool qvalid = qrow < gr.nrows;
-    const int qpos = gr.pos0 + qrow;
+    // this lane's query (as a B column of S^T and the A row of O): n = row * G + head-in-group, the row being a row of
+    // the item's group, or (shared) the one row of member n / G
+    const int qhead = kvh * G + n % G;
+    int qstep, qpos;  // the query's step row and position
+    bool qvalid;
+    if (shared) {
+        const int mq = n / G;
+        const AttnGroup& gm = a.groups[attn_member(it, min(mq, nshare - 1))];
+        qstep = gm.row0;
+        qpos = gm.pos0;
+        qvalid = mq < nshare;
+    } else {
+        const int qrow = n / G;
+        qvalid = qrow < gr.nrows;
+        qstep = gr.row0 + (qvalid ? qrow : 0);
+        qpos = gr.pos0 + qrow;
+    }
     half8 qh[4], ql[4];
-    attn_qfrag(a, gr, qrow, qhead, qvalid, g, qh, ql);
+    attn_qfrag_row(a, qstep, qhead, qvalid, g, qh, ql);
     int p_lo, p_hi;
     attn_pages(a, a.pt + (size_t) gr.seq * a.max_pages, cbase, pos_last, p_lo, p_hi);
     u32x4 kf[4][4], vf[2][8];
@@ -257,10 +290,11 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
     // thread -> (query qq, 8 dims)
     const int qq = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
     float M, L, acc[8];
-    attn_combine(sh, wave, n, g, gr.nrows * G, m, l, o, qq, d0, M, L, acc);
+    attn_combine(sh, wave, n, g, (shared ? nshare : gr.nrows) * G, m, l, o, qq, d0, M, L, acc);
     const int row = qq / G, head = kvh * G + qq % G;
-    if (row >= gr.nrows) return;
-    float* dst = a.part + (((size_t) (gr.row0 + row) * a.H + head) * a.max_chunks + it.chunk) * (ATT_D + 2);
+    if (row >= (shared ? nshare : gr.nrows)) return;
+    const int orow = shared ? a.groups[attn_member(it, row)].row0 : gr.row0 + row;
+    float* dst = a.part + (((size_t) orow * a.H + head) * a.max_chunks + it.chunk) * (ATT_D + 2);
     *(float2*) (dst + d0) = (float2){acc[0], acc[1]};  // (a partial is 130 floats: 8-byte aligned)
     *(float2*) (dst + d0 + 2) = (float2){acc[2], acc[3]};
     *(float2*) (dst + d0 + 4) = (float2){acc[4], acc[5]};
@@ -481,7 +515,8 @@ int paged_attention(const AttnArgs& a, hipStream_t st) {
 // 8 chunks of 64-cell pages and whenever the groups are not one round (16 or 48 sequences). A whole-group launch lasts
 // as long as its longest context: at contexts U[256, 4096] (longest 1.7x the mean) it took 81.5 us against 66.0 for
 // chunk items. Otherwise one item per (group, 256-cell chunk) and the merge folds every row's chunks.
-void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, int page_cells, AttnPlan& p, int mode) {
+void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, int page_cells, AttnPlan& p, int mode,
+               const int32_t* pt, int max_pages) {
     const int gmax = 16 / (H / KVH);
     p.groups.clear();
     p.items.clear();
@@ -503,13 +538,56 @@ void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, in
     const bool long_ctx = tot >= (page_cells == 32 ? 5L : 10L) * ng;
     p.whole = mode >= 0 ? mode == 1
                         : wg >= ATT_WHOLE_MIN_WG && wg <= ATT_WHOLE_MAX_WG && 8L * mx * ng <= 9L * tot && long_ctx;
+    const AttnItem none = {0, 0, 0, {-1, -1, -1}};
+    // shared chunks: a one-row group's chunk that lies wholly below its position, keyed by the chunk's pages
+    std::vector<std::vector<int>> taken(ng);  // per group, its chunks that went into shared items
+    if (!p.whole && pt && max_pages > 0) {
+        const int members = std::min(ATT_SHARE_MAX, 16 / (H / KVH));
+        const int ppc = ATT_CHUNK / page_cells;  // pages a chunk
+        std::map<std::vector<int32_t>, std::vector<int>> by_pages;  // pages + chunk -> groups
+        for (int gi = 0; gi < ng; ++gi) {
+            const AttnGroup& gr = p.groups[gi];
+            if (gr.nrows != 1) continue;
+            for (int c = 0; (c + 1) * ATT_CHUNK - 1 <= gr.pos0; ++c) {
+                std::vector<int32_t> k(ppc + 1);
+                bool ok = true;
+                for (int j = 0; j < ppc; ++j) {
+                    k[j] = pt[(size_t) gr.seq * max_pages + c * ppc + j];
+                    ok = ok && k[j] >= 0;
+                }
+                k[ppc] = c;
+                if (ok) by_pages[k].push_back(gi);
+            }
+        }
+        for (auto& kv : by_pages) {
+            const std::vector<int>& gs = kv.second;
+            const int c = kv.first.back();
+            for (size_t i = 0; i + 1 < gs.size(); i += members) {  // (a last lone group keeps its own item)
+                const int cnt = (int) std::min<size_t>(members, gs.size() - i);
+                AttnItem it = none;
+                it.group = gs[i];
+                it.chunk = c;
+                it.nchunk = 1;
+                for (int j = 1; j < cnt; ++j) it.share[j - 1] = gs[i + j];
+                p.items.push_back(it);
+                for (int j = 0; j < cnt; ++j) taken[gs[i + j]].push_back(c);
+            }
+        }
+    }
     for (int gi = 0; gi < ng; ++gi) {
         const AttnGroup& gr = p.groups[gi];
         const int nc = (gr.pos0 + gr.nrows - 1) / ATT_CHUNK + 1;
         if (p.whole) {
-            p.items.push_back({gi, 0, nc});
+            AttnItem it = none;
+            it.group = gi, it.nchunk = nc;
+            p.items.push_back(it);
         } else {
-            for (int c = 0; c < nc; ++c) p.items.push_back({gi, c, 1});
+            for (int c = 0; c < nc; ++c) {
+                if (std::find(taken[gi].begin(), taken[gi].end(), c) != taken[gi].end()) continue;
+                AttnItem it = none;
+                it.group = gi, it.chunk = c, it.nchunk = 1;
+                p.items.push_back(it);
+            }
             for (int i = 0; i < gr.nrows; ++i) p.mrows.push_back(gr.row0 + i);
         }
     }

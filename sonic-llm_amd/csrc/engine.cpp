@@ -751,7 +751,8 @@ struct AttnList {
 
 AttnList attn_list(sn_engine* e, Stage& S, int R, const int32_t* seq, const int32_t* pos) {
     AttnPlan p;
-    attn_plan(R, seq, pos, e->H, e->KVH, e->page_cells, p, e->attn_mode);
+    attn_plan(R, seq, pos, e->H, e->KVH, e->page_cells, p, e->attn_mode, e->pt.empty() ? nullptr : e->pt.data(),
+              e->max_pages);
     AttnList al;
     al.o_grp = S.put(p.groups);
     al.o_itm = S.put(p.items);

@@ -101,10 +101,15 @@ struct AttnGroup {
     int32_t seq;    // the sequence (page-table row)
     int32_t pos0;   // position of the first row; row i is at pos0 + i and attends cells 0 .. pos0 + i
 };
+#define ATT_SHARE_MAX 4  // groups a shared-chunk item serves
 struct AttnItem {
     int32_t group;   // index into the group list
     int32_t chunk;   // cells chunk*ATT_CHUNK ..
     int32_t nchunk;  // chunks the item covers (whole-group items: all of the group's; otherwise 1)
+    // a shared-chunk item (chunk items only): more groups of one row each whose chunk `chunk` lies wholly below their
+    // positions on the very pages of `group`'s: their queries take the MFMA columns after `group`'s (-1: none), so the
+    // chunk's K/V cells are read once for all of them
+    int32_t share[ATT_SHARE_MAX - 1];
 };
 struct AttnArgs {
     const float* q;          // [rows][H][D] fp32 (normed, roped; the softmax scale is applied inside)
@@ -147,9 +152,11 @@ struct AttnPlan {
     int max_chunk = 0;  // the most chunks of any group
     bool whole = false;
 };
-// mode: -1 as above, 0 per-chunk items, 1 whole groups
+// mode: -1 as above, 0 per-chunk items, 1 whole groups. pt (optional, host [slots][max_pages]): the page table, from
+// which chunk items of one-row groups whose chunk is wholly below their positions on the same pages become shared
+// items (a chunk's partial is computed alike in either kind, so a row's output does not depend on the sharing).
 void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, int page_cells, AttnPlan& p,
-               int mode = -1);
+               int mode = -1, const int32_t* pt = nullptr, int max_pages = 0);
 
 // ---- elementwise / row kernels ----
 void embed_rows(const float* table, int E, const int32_t* tok, int R, float* x, hipStream_t st);

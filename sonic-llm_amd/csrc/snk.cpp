@@ -219,8 +219,17 @@ struct snk_attn {
     float* d_part = nullptr;
 };
 
+extern "C" snk_attn* snk_attn_new_pt(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH,
+                                     int max_pages, int page_cells, int mode, const int32_t* pt, char* err,
+                                     int err_len);
 extern "C" snk_attn* snk_attn_new_mode(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH,
                                        int max_pages, int page_cells, int mode, char* err, int err_len) {
+    return snk_attn_new_pt(n_rows, seq, pos, H, KVH, max_pages, page_cells, mode, nullptr, err, err_len);
+}
+
+extern "C" snk_attn* snk_attn_new_pt(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH,
+                                     int max_pages, int page_cells, int mode, const int32_t* pt, char* err,
+                                     int err_len) {
     if (n_rows <= 0 || H <= 0 || KVH <= 0 || H % KVH || 16 % (H / KVH) || (page_cells != 32 && page_cells != 64) ||
         mode < -1 || mode > 1) {
         sn_set_err(err, err_len, "snk_attn_new: bad shape");
@@ -232,7 +241,7 @@ extern "C" snk_attn* snk_attn_new_mode(int n_rows, const int32_t* seq, const int
             return nullptr;
         }
     AttnPlan pl;
-    attn_plan(n_rows, seq, pos, H, KVH, page_cells, pl, mode);
+    attn_plan(n_rows, seq, pos, H, KVH, page_cells, pl, mode, pt, max_pages);
     snk_attn* p = new snk_attn();
     p->n_rows = n_rows;
     p->H = H;

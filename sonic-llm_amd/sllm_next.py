@@ -119,6 +119,7 @@ SNK_API = [
     ("snk_q4_gemm_plan_sums", I, [P, P, I, I, I, P, P, C.c_size_t, I, I, I, P]),
     ("snk_attn_new", P, [I, P, P, I, I, I, I, CH, I]),
     ("snk_attn_new_mode", P, [I, P, P, I, I, I, I, I, CH, I]),
+    ("snk_attn_new_pt", P, [I, P, P, I, I, I, I, I, P, CH, I]),
     ("snk_attn_run", I, [P, P, I, P, P, P, C.c_float, P, I, P]),
     ("snk_attn_time", C.c_double, [P, P, I, P, P, P, C.c_float, P, I, I, P]),
     ("snk_attn_whole", I, [P]),

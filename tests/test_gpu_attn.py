@@ -49,9 +49,10 @@ def config2_case(seed=2, S_=32, page=32, lo=256, hi=4096, n_share=8, share_cells
     return q, np.arange(S_, dtype=np.int32), (ctx - 1).astype(np.int32), kpool, vpool, pt, page
 
 
-def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None, whole=None, mode=-1):
+def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None, whole=None, mode=-1, share=False):
     """whole: when given, the work list's form the planner chose (whole groups, or per-chunk items and the merge) is
-    checked too; mode: the form forced (snk_attn_new_mode), -1 the planner's. The KV head count is the pools'."""
+    checked too; mode: the form forced (snk_attn_new_mode), -1 the planner's; share: the planner sees the page table
+    (snk_attn_new_pt) and reads shared chunks once for their rows. The KV head count is the pools'."""
     L = S.lib()
     kvh = kpool.shape[1]
     err = __import__("ctypes").create_string_buffer(256)
@@ -59,7 +60,13 @@ def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None, whole=None, 
     pos = np.ascontiguousarray(pos, np.int32)
     for s_, p_ in zip(seq, pos):  # every cell a row reads has a page (host-side check before the launch)
         assert np.all(pt[s_, :p_ // page + 1] >= 0)
-    plan = L.snk_attn_new_mode(len(seq), seq.ctypes.data, pos.ctypes.data, H, kvh, pt.shape[1], page, mode, err, 256)
+    if share:
+        ptc = np.ascontiguousarray(pt, np.int32)
+        plan = L.snk_attn_new_pt(len(seq), seq.ctypes.data, pos.ctypes.data, H, kvh, pt.shape[1], page, mode,
+                                 ptc.ctypes.data, err, 256)
+    else:
+        plan = L.snk_attn_new_mode(len(seq), seq.ctypes.data, pos.ctypes.data, H, kvh, pt.shape[1], page, mode, err,
+                                   256)
     assert plan, err.value
     if whole is not None:
         assert L.snk_attn_whole(plan) == int(whole)
@@ -84,6 +91,23 @@ def test_config2_paged_attention():
     assert np.all(err <= ATOL + RTOL * np.abs(ref))
     ref64 = O.paged_attn(q, seq, pos, KVH, kp, vp, page, pt, scale, f64=True)
     assert np.max(np.abs(got - ref64)) < 1e-4
+
+
+@pytest.mark.parametrize("kvh,n_share", [(8, 8), (8, 6), (4, 5)])
+def test_shared_prefix_read_once(kvh, n_share):
+    """Rows of sequences whose first 1024 cells are the same pages (config 2's sharers): the planner given the page
+    table serves each shared 256-cell chunk of up to 16 / G rows with one work item, so its K/V is read once for them.
+    Each row's output equals the unshared plan's bit for bit (a query's chunk partial depends on its own column only),
+    with groups of sharers split into items of up to 4 (G = 4) or 2 (G = 8) rows and a lone last sharer on its own
+    item; and it matches the oracle."""
+    q, seq, pos, kp, vp, pt, page = config2_case(n_share=n_share, kvh=kvh)
+    scale = 1 / math.sqrt(D)
+    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    a = attn_gpu(q, seq, pos, kp, vp, pt, page, scale, bufs=bufs, mode=0)
+    b = attn_gpu(q, seq, pos, kp, vp, pt, page, scale, bufs=bufs, mode=0, share=True)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    ref = O.paged_attn(q, seq, pos, kvh, kp, vp, page, pt, scale)
+    assert np.all(np.abs(b - ref) <= ATOL + RTOL * np.abs(ref))
 
 
 @pytest.mark.parametrize("page", [32, 64])
