@@ -733,9 +733,10 @@ struct Stage {
     T* dev(size_t at) const { return (T*) (e->d_stage + at); }
 };
 
-// The attention work of R rows (attn_plan: whole groups, or per-chunk items and the rows to merge). bytes: each
-// (sequence, KV head) reads its cells once, q in, page-table entries, and the outputs out (whole groups) or the
-// chunk partials out; merge_bytes: the partials in, the outputs and the o-projection operand out (chunk items).
+// The attention work of R rows (attn_plan: whole groups, or per-chunk items and the rows to merge). bytes (the
+// algorithmic bytes of the attention launch): each (sequence, KV head) reads its cells once, q in, page-table entries,
+// and with whole groups the outputs and the o-projection operand out (the chunk partials, an intermediate, are not
+// counted); merge_bytes: the partials in, the outputs and the operand out (chunk items).
 struct AttnList {
     size_t o_grp = 0, o_itm = 0, o_mrow = 0;
     int n_items = 0, n_mrows = 0;
@@ -765,7 +766,7 @@ AttnList attn_list(sn_engine* e, Stage& S, int R, const int32_t* seq, const int3
     for (const AttnGroup& g : p.groups)
         for (int i = 0; i < g.nrows; ++i) part += (double) ((g.pos0 + i) / ATT_CHUNK + 1) * e->H * (e->D + 2) * 4;
     const double out = (double) R * e->QD * 4, operand = (double) R * e->QD / 32 * 76;  // 76 B a row block (xa)
-    al.bytes = (double) R * e->QD * 4 + (p.whole ? out + operand : part);
+    al.bytes = (double) R * e->QD * 4 + (p.whole ? out + operand : 0.0);
     al.merge_bytes = p.whole ? 0.0 : part + out + operand;
     std::vector<int> seen;
     for (const AttnGroup& g : p.groups) {
