@@ -790,9 +790,10 @@ def bench_matmul(args):
                    "weight_copies": copies, "algorithmic_bytes": alg, "us_per_call": round(us, 3),
                    "us_matmul_kernel": round(us_gemm, 3), "read_floor_us": round(us_read, 3),
                    "floor_frac": round(us_read / us_gemm, 4)},
-        "roofline": {"kernel": "k_q4_gemm", "bound": "hbm", "achieved": round(gbs_k, 1), "peak": HBM_PEAK / 1e9,
+        "roofline": {"kernel": "k_q4_gemm_s", "bound": "hbm", "achieved": round(gbs_k, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(gbs_k * 1e9 / HBM_PEAK, 4),
                      "traffic": profile_traffic("matmul_q4_0_b8_4096x4096_traffic.json", "k_q4_gemm"),
+                     "traffic_source": "profiles/matmul_q4_0_b8_4096x4096_traffic.md",
                      "bytes_per_launch": alg, "us_per_launch": round(us_gemm, 3)},
         "cpu_baseline": cpu,
     }
@@ -917,6 +918,7 @@ def bench_attn(args):
         "roofline": {"kernel": kern, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(gbs * 1e9 / HBM_PEAK, 4),
                      "traffic": profile_traffic("attn_config2_b32_ctx256_4096_page32_traffic.json", kern),
+                     "traffic_source": "profiles/attn_config2_b32_ctx256_4096_page32_traffic.md",
                      "bytes_per_launch": alg, "us_per_launch": round(us, 3)},
         "cpu_baseline": cpu,
     }
