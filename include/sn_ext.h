@@ -41,7 +41,9 @@ long snx_graph_count(const sn_engine* e, int replays);
 // dropped (dropped 1: another step or a cache call came first; its cells were zeroed) since the engine opened.
 long snx_chain_count(const sn_engine* e, int dropped);
 // The attention work list's form: -1 chosen per step (the default), 0 one item per 256-cell chunk and a merge, 1
-// whole groups (one workgroup per (group, KV head) walks the whole context: no merge). Every form gives the same bits.
+// whole groups (one workgroup per (group, KV head) walks the whole context: no merge), 2 run items for every
+// sequence with two or more consecutive full query groups (prompt rows; -1 takes them when they make at least 128
+// workgroups), the other rows as -1. Every form gives the same bits.
 void snx_attn_mode(sn_engine* e, int mode);
 // The graph key sn_step forms for a step of R rows (slots seq, positions pos; every row sampled in order) on an engine
 // of H query heads, KVH KV heads and page_cells-cell pages with attention form `mode` (as snx_attn_mode), computed on

@@ -104,7 +104,9 @@ int snk_attn_run(snk_attn* p, const float* d_q, int ldq, const void* d_kpool, co
 double snk_attn_time(snk_attn* p, const float* d_q, int ldq, const void* d_kpool, const void* d_vpool,
                      const int32_t* d_pt, float scale, float* d_out, int ldo, int iters, void* stream);
 // the same with the list's form chosen by the caller: mode -1 as snk_attn_new, 0 one item per 256-cell chunk and the
-// merge, 1 whole groups (for tests and timing; both forms give the same bits for a row)
+// merge, 1 whole groups, 2 run items wherever a sequence has two or more consecutive full query groups (prompt rows;
+// -1 takes them when they make at least 128 workgroups), the other rows as -1 (for tests and timing; every form gives
+// the same bits for a row)
 snk_attn* snk_attn_new_mode(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH, int max_pages,
                             int page_cells, int mode, char* err, int err_len);
 // the same with the host copy of the page table (pt [slots][max_pages], the rows' slots index it): a decode row's
@@ -118,6 +120,10 @@ snk_attn* snk_attn_new_pt(int n_rows, const int32_t* seq, const int32_t* pos, in
 // mean and the contexts are long), 0 when it is one item per 256-cell chunk followed by the merge. Both give the same
 // bits for a row.
 int snk_attn_whole(const snk_attn* p);
+// the list's run items: up to 4 consecutive query groups of one sequence (16 prompt rows at G = 4) walked over their
+// context by one workgroup per (item, KV head), which writes their outputs (no partials, no merge); the K/V cells of
+// a chunk are read once for all of them (the prompt rows of attn_pre, kernels.metal:1201-1306, sn_attn.inc.h:195-206)
+int snk_attn_runs(const snk_attn* p);
 void snk_attn_free(snk_attn* p);
 
 // ---- per-head QK-norm + NEOX RoPE + K/V cache write (qk_rope, kernels.metal:149-197) -------------------------------

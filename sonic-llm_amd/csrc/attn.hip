@@ -14,6 +14,7 @@
 // other rows of its group, and a verify row equals the same row run alone.
 #include <algorithm>
 #include <map>
+#include <type_traits>
 
 #include "sn_kernels_internal.h"
 
@@ -432,6 +433,147 @@ __global__ __launch_bounds__(512) void k_attn_whole(AttnArgs a) {
     if (a.xa) attn_xa8(a.xa, a.H * ATT_D, r, head * 4 + d0 / 32, d0 & 31, RO);
 }
 
+// One work item = a run of nmem consecutive query groups of one sequence (prompt rows), every chunk of the last
+// group's context; grid.y = KV head. The whole-group kernel's walk (waves 0-3 on chunk c, 4-7 on chunk c + 1 of each
+// pair, each half combining its chunk's partial as k_attn_part does, the first half folding the two in chunk order),
+// with the pair's K/V cells held in registers for every group of the run in turn: each group's queries (staged in LDS
+// as hi + lo, as attn_qfrag_row splits them) take the MFMA columns, its rows' masks are its own, and its running
+// (M, L, o) lives in LDS between pairs. A cell past a group's rows but within the run's has a real value where that
+// group's own item would read zeros; its score is -inf and its p exactly 0 either way, so every group's output is the
+// one its own whole-group or chunk items give, bit for bit. Outputs and the o-projection's operand are written here.
+struct AttnRunShared {
+    AttnShared h[2];
+    float x[257][10];                 // the second half's combined partials (row 256: the first half's dummy writes)
+    float st[ATT_RUN_MAX][10][256];   // each group's running o[8], M, L per first-half thread
+    __attribute__((aligned(16))) _Float16 q[ATT_RUN_MAX][2][16][ATT_D + 8];  // each group's queries: hi, lo
+};
+__global__ __launch_bounds__(512) void k_attn_run(AttnArgs a) {
+    __shared__ AttnRunShared sh;
+    const AttnItem it = a.runs[blockIdx.x];
+    const int kvh = blockIdx.y;
+    const int G = a.H / a.KVH;
+    const int lane = threadIdx.x & 63, w8 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int half = w8 >> 2, wave = w8 & 3, th = threadIdx.x & 255;
+    const int n = lane & 15, g = lane >> 4;
+    const int nm = it.nmem;
+    const AttnGroup glast = a.groups[it.group + nm - 1];
+    const int pos_last = glast.pos0 + glast.nrows - 1;  // the run's last cell
+    const int32_t* ptrow = a.pt + (size_t) glast.seq * a.max_pages;
+    const int nch = it.nchunk;
+    const int qq = th >> 4, d0 = (th & 15) * 8;
+    {  // the groups' queries: thread t takes dims 4 (t % 32) .. + 3 of query column t / 32 of each group
+        const int qn = threadIdx.x >> 5, dd = 4 * (threadIdx.x & 31);
+        for (int m = 0; m < nm; ++m) {
+            const AttnGroup gm = a.groups[it.group + m];
+            const int row = qn / G;
+            const bool ok = row < gm.nrows;
+            const float4 v = *(const float4*) (a.q + (size_t) (gm.row0 + (ok ? row : 0)) * a.ldq +
+                                               (size_t) (kvh * G + qn % G) * ATT_D + dd);
+            const float xs[4] = {v.x, v.y, v.z, v.w};
+            for (int j = 0; j < 4; ++j) {
+                const float x = ok ? xs[j] * a.scale : 0.0f;
+                const _Float16 h = (_Float16) x;
+                sh.q[m][0][qn][dd + j] = h;
+                sh.q[m][1][qn][dd + j] = (_Float16) (x - (float) h);
+            }
+        }
+        if (half == 0)
+            for (int m = 0; m < ATT_RUN_MAX; ++m) {
+                for (int d = 0; d < 8; ++d) sh.st[m][d][th] = 0.0f;
+                sh.st[m][8][th] = -INFINITY;
+                sh.st[m][9][th] = 0.0f;
+            }
+    }
+    __syncthreads();
+    u32x4 kf[4][4], vf[2][8];
+    auto rsrc_of = [&](int c0, int& cbase, int& plast) {
+        const int c = c0 + half;
+        const bool live = c < nch;
+        cbase = (live ? c : 0) * ATT_CHUNK + 64 * wave;
+        plast = live ? pos_last : -1;
+        int p_lo, p_hi;
+        attn_pages(a, ptrow, cbase, plast, p_lo, p_hi);
+        return attn_rsrc(a, kvh, p_lo, p_hi, live);
+    };
+    int cb, pl;
+    {
+        const AttnRsrc r0 = rsrc_of(0, cb, pl);
+        __builtin_amdgcn_sched_barrier(0);
+        attn_issue_k(a, r0, cb, pl, n, g, kf);
+        __builtin_amdgcn_sched_barrier(0);
+        attn_issue_v(a, r0, cb, pl, n, g, vf);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int c0 = 0; c0 < nch; c0 += 2) {  // (uniform trips: every wavefront meets every barrier)
+        const int c = c0 + half;
+        const bool live = c < nch;
+        const int cbase = c * ATT_CHUNK + 64 * wave;
+        int ncb, npl;
+        const AttnRsrc rn = rsrc_of(c0 + 2, ncb, npl);
+        // group m of the run on this pair; the last one issues the next pair's loads (K once its scores have used K,
+        // V once P . V has used V), so they are in flight through its softmax, combine and fold
+        auto member = [&](int m, auto last) {
+            const AttnGroup gm = a.groups[it.group + m];
+            half8 qh[4], ql[4];
+            for (int t = 0; t < 4; ++t) {
+                qh[t] = *(const half8*) &sh.q[m][0][n][32 * t + 8 * g];
+                ql[t] = *(const half8*) &sh.q[m][1][n][32 * t + 8 * g];
+            }
+            const int qrow = n / G;
+            const bool qvalid = qrow < gm.nrows;
+            float ml, ll;
+            floatx4 sc[4], o[8];
+            __builtin_amdgcn_sched_barrier(0);
+            attn_scores(kf, qh, ql, cbase, qvalid && live, gm.pos0 + qrow, g, ml, ll, sc);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (decltype(last)::value) attn_issue_k(a, rn, ncb, npl, n, g, kf);
+            __builtin_amdgcn_sched_barrier(0);
+            attn_pv(vf, sc, o);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (decltype(last)::value) attn_issue_v(a, rn, ncb, npl, n, g, vf);
+            __builtin_amdgcn_sched_barrier(0);
+            float M, L, acc[8];
+            attn_combine(sh.h[half], wave, n, g, gm.nrows * G, ml, ll, o, qq, d0, M, L, acc);
+            float* xw = sh.x[half ? th : 256];
+            for (int d = 0; d < 8; ++d) xw[d] = acc[d];
+            xw[8] = M;
+            xw[9] = L;
+            __syncthreads();
+            // (the second half folds a copy it never stores)
+            float RM = sh.st[m][8][th], RL = sh.st[m][9][th], RO[8];
+            for (int d = 0; d < 8; ++d) RO[d] = sh.st[m][d][th];
+            attn_fold<8>(RM, RL, RO, M, L, acc);
+            float acc1[8];
+            for (int d = 0; d < 8; ++d) acc1[d] = sh.x[th][d];
+            attn_fold<8>(RM, RL, RO, sh.x[th][8], sh.x[th][9], acc1);
+            if (half == 0) {
+                for (int d = 0; d < 8; ++d) sh.st[m][d][th] = RO[d];
+                sh.st[m][8][th] = RM;
+                sh.st[m][9][th] = RL;
+            }
+            __syncthreads();  // every read of sh.h and sh.x done before the next group writes them
+        };
+        for (int m = 0; m + 1 < nm; ++m) member(m, std::false_type{});
+        member(nm - 1, std::true_type{});
+    }
+    if (half != 0) return;
+    const int row = qq / G, head = kvh * G + qq % G;
+    for (int m = 0; m < nm; ++m) {
+        const AttnGroup gm = a.groups[it.group + m];
+        if (row >= gm.nrows) continue;  // (a block's 4 lanes share the row: attn_xa8's shuffles stay within them)
+        float RL = sh.st[m][9][th], RO[8];
+        for (int d = 0; d < 8; ++d) RO[d] = sh.st[m][d][th];
+        attn_finish<8>(RL, RO);
+        const int r = gm.row0 + row;
+        if (a.out) {
+            float* out = a.out + (size_t) r * a.ldo + (size_t) head * ATT_D + d0;
+            *(float4*) out = (float4){RO[0], RO[1], RO[2], RO[3]};
+            *(float4*) (out + 4) = (float4){RO[4], RO[5], RO[6], RO[7]};
+        }
+        if (a.xa) attn_xa8(a.xa, a.H * ATT_D, r, head * 4 + d0 / 32, d0 & 31, RO);
+    }
+}
+
 // per (row, head) of the rows the partial kernel split (a.mrows): the chunks' partials folded in chunk order (attn_fold);
 // out = acc / l. One wavefront, 2 dims a lane; the loads of 8 chunks are issued together (chunk index clamped, no load
 // behind a branch), then folded in order. With a.xa the head's 128 outputs (4 Q8_0 blocks of the o-projection's input
@@ -491,6 +633,12 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
     }
 }
 
+int attention_runs(const AttnArgs& a, hipStream_t st) {
+    if (a.n_runs <= 0) return 0;
+    if (a.H % a.KVH != 0 || 16 % (a.H / a.KVH) != 0) return -1;
+    hipLaunchKernelGGL(k_attn_run, dim3(a.n_runs, a.KVH), dim3(512), 0, st, a);
+    return 0;
+}
 int attention_items(const AttnArgs& a, hipStream_t st) {
     if (a.n_items <= 0) return 0;
     if (a.H % a.KVH != 0 || 16 % (a.H / a.KVH) != 0) return -1;
@@ -504,7 +652,8 @@ int attention_merge(const AttnArgs& a, hipStream_t st) {
     return 0;
 }
 int paged_attention(const AttnArgs& a, hipStream_t st) {
-    const int rc = attention_items(a, st);
+    int rc = attention_runs(a, st);
+    if (!rc) rc = attention_items(a, st);
     return rc ? rc : attention_merge(a, st);
 }
 
@@ -514,31 +663,65 @@ int paged_attention(const AttnArgs& a, hipStream_t st) {
 // items plus merge by 10-20% at 12-16 chunks and at 32-cell pages when the contexts are alike, and lose 2-8% at 4 and
 // 8 chunks of 64-cell pages and whenever the groups are not one round (16 or 48 sequences). A whole-group launch lasts
 // as long as its longest context: at contexts U[256, 4096] (longest 1.7x the mean) it took 81.5 us against 66.0 for
-// chunk items. Otherwise one item per (group, 256-cell chunk) and the merge folds every row's chunks.
+// chunk items. Otherwise one item per (group, 256-cell chunk) and the merge folds every row's chunks. Prompt rows: run
+// items first (see sn_kernels_internal.h), the rule above then over the groups outside them.
 void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, int page_cells, AttnPlan& p, int mode,
                const int32_t* pt, int max_pages) {
     const int gmax = 16 / (H / KVH);
     p.groups.clear();
     p.items.clear();
+    p.runs.clear();
     p.mrows.clear();
     p.max_chunk = 0;
-    int tot = 0, mx = 0;
     for (int r = 0; r < R;) {
         int n = 1;
         while (r + n < R && n < gmax && seq[r + n] == seq[r] && pos[r + n] == pos[r] + n) ++n;
         p.groups.push_back({r, n, seq[r], pos[r]});
-        const int nc = (pos[r] + n - 1) / ATT_CHUNK + 1;
-        tot += nc;
-        mx = std::max(mx, nc);
+        p.max_chunk = std::max(p.max_chunk, (pos[r] + n - 1) / ATT_CHUNK + 1);
         r += n;
     }
-    p.max_chunk = mx;
     const int ng = (int) p.groups.size();
-    const long wg = (long) ng * KVH;
-    const bool long_ctx = tot >= (page_cells == 32 ? 5L : 10L) * ng;
-    p.whole = mode >= 0 ? mode == 1
-                        : wg >= ATT_WHOLE_MIN_WG && wg <= ATT_WHOLE_MAX_WG && 8L * mx * ng <= 9L * tot && long_ctx;
-    const AttnItem none = {0, 0, 0, {-1, -1, -1}};
+    const AttnItem none = {0, 0, 0, {-1, -1, -1}, 1};
+    // run items: a sequence's consecutive groups at consecutive positions, every one but the last full
+    std::vector<char> in_run(ng, 0);
+    if (mode == -1 || mode == 2) {
+        std::vector<AttnItem> runs;
+        for (int gi = 0; gi < ng;) {
+            int n = 1;
+            while (gi + n < ng && p.groups[gi + n].seq == p.groups[gi].seq && p.groups[gi + n - 1].nrows == gmax &&
+                   p.groups[gi + n].pos0 == p.groups[gi + n - 1].pos0 + gmax)
+                ++n;
+            if (n >= 2)
+                for (int j = 0; j < n; j += ATT_RUN_MAX) {
+                    AttnItem it = none;
+                    it.group = gi + j;
+                    it.nmem = std::min(ATT_RUN_MAX, n - j);
+                    const AttnGroup& gl = p.groups[gi + j + it.nmem - 1];
+                    it.nchunk = (gl.pos0 + gl.nrows - 1) / ATT_CHUNK + 1;
+                    runs.push_back(it);
+                }
+            gi += n;
+        }
+        if (!runs.empty() && (mode == 2 || (long) runs.size() * KVH >= ATT_RUN_MIN_WG)) {
+            p.runs = runs;
+            for (const AttnItem& it : runs)
+                for (int j = 0; j < it.nmem; ++j) in_run[it.group + j] = 1;
+        }
+    }
+    // the other groups: whole groups or chunk items
+    int tot = 0, mx = 0, nrest = 0;
+    for (int gi = 0; gi < ng; ++gi) {
+        if (in_run[gi]) continue;
+        const AttnGroup& gr = p.groups[gi];
+        const int nc = (gr.pos0 + gr.nrows - 1) / ATT_CHUNK + 1;
+        tot += nc;
+        mx = std::max(mx, nc);
+        ++nrest;
+    }
+    const long wg = (long) nrest * KVH;
+    const bool long_ctx = tot >= (page_cells == 32 ? 5L : 10L) * nrest;
+    p.whole = mode == 0 || mode == 1 ? mode == 1
+              : nrest > 0 && wg >= ATT_WHOLE_MIN_WG && wg <= ATT_WHOLE_MAX_WG && 8L * mx * nrest <= 9L * tot && long_ctx;
     // shared chunks: a one-row group's chunk that lies wholly below its position, keyed by the chunk's pages
     std::vector<std::vector<int>> taken(ng);  // per group, its chunks that went into shared items
     if (!p.whole && pt && max_pages > 0) {
@@ -547,7 +730,7 @@ void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, in
         std::map<std::vector<int32_t>, std::vector<int>> by_pages;  // pages + chunk -> groups
         for (int gi = 0; gi < ng; ++gi) {
             const AttnGroup& gr = p.groups[gi];
-            if (gr.nrows != 1) continue;
+            if (gr.nrows != 1 || in_run[gi]) continue;
             for (int c = 0; (c + 1) * ATT_CHUNK - 1 <= gr.pos0; ++c) {
                 std::vector<int32_t> k(ppc + 1);
                 bool ok = true;
@@ -575,6 +758,7 @@ void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, in
         }
     }
     for (int gi = 0; gi < ng; ++gi) {
+        if (in_run[gi]) continue;
         const AttnGroup& gr = p.groups[gi];
         const int nc = (gr.pos0 + gr.nrows - 1) / ATT_CHUNK + 1;
         if (p.whole) {

@@ -733,20 +733,21 @@ struct Stage {
     T* dev(size_t at) const { return (T*) (e->d_stage + at); }
 };
 
-// The attention work of R rows (attn_plan: whole groups, or per-chunk items and the rows to merge). bytes (the
-// algorithmic bytes of the attention launch): each (sequence, KV head) reads its cells once, q in, page-table entries,
-// and with whole groups the outputs and the o-projection operand out (the chunk partials, an intermediate, are not
-// counted); merge_bytes: the partials in, the outputs and the operand out (chunk items).
+// The attention work of R rows (attn_plan: run items for prompt rows, then whole groups or per-chunk items and the
+// rows to merge). bytes (the algorithmic bytes of the attention launches): each (sequence, KV head) reads its cells
+// once, q in, page-table entries, and for the rows of run items and whole groups the outputs and the o-projection
+// operand out (the chunk partials, an intermediate, are not counted); merge_bytes: the partials in, the outputs and
+// the operand out (the rows of chunk items).
 struct AttnList {
-    size_t o_grp = 0, o_itm = 0, o_mrow = 0;
-    int n_items = 0, n_mrows = 0;
+    size_t o_grp = 0, o_itm = 0, o_mrow = 0, o_run = 0;
+    int n_items = 0, n_mrows = 0, n_runs = 0;
     bool whole = false;
     double bytes = 0.0, merge_bytes = 0.0;
     // every value of the list the attention launches take, for a graph key: the form (whole groups launch another
-    // kernel and no merge), the item and merge-row counts (grid sizes) and the staging offsets of the three arrays
+    // kernel and no merge), the item, merge-row and run-item counts (grid sizes) and the staging offsets of the arrays
     void key(std::vector<int64_t>& k) const {
         k.insert(k.end(), {(int64_t) whole, (int64_t) n_items, (int64_t) n_mrows, (int64_t) o_grp, (int64_t) o_itm,
-                           (int64_t) o_mrow});
+                           (int64_t) o_mrow, (int64_t) n_runs, (int64_t) o_run});
     }
 };
 
@@ -758,16 +759,21 @@ AttnList attn_list(sn_engine* e, Stage& S, int R, const int32_t* seq, const int3
     al.o_grp = S.put(p.groups);
     al.o_itm = S.put(p.items);
     al.o_mrow = S.put(p.mrows);
+    al.o_run = S.put(p.runs);
     al.n_items = (int) p.items.size();
     al.n_mrows = (int) p.mrows.size();
+    al.n_runs = (int) p.runs.size();
     al.whole = p.whole;
-    // chunk partials: (acc[128], m, l) per (row, head, chunk of the row)
+    // chunk partials: (acc[128], m, l) per (row, head, chunk of the row), for the rows the merge folds
     double part = 0.0;
     for (const AttnGroup& g : p.groups)
-        for (int i = 0; i < g.nrows; ++i) part += (double) ((g.pos0 + i) / ATT_CHUNK + 1) * e->H * (e->D + 2) * 4;
-    const double out = (double) R * e->QD * 4, operand = (double) R * e->QD / 32 * 76;  // 76 B a row block (xa)
-    al.bytes = (double) R * e->QD * 4 + (p.whole ? out + operand : 0.0);
-    al.merge_bytes = p.whole ? 0.0 : part + out + operand;
+        for (int i = 0; i < g.nrows; ++i)
+            if (std::find(p.mrows.begin(), p.mrows.end(), g.row0 + i) != p.mrows.end())
+                part += (double) ((g.pos0 + i) / ATT_CHUNK + 1) * e->H * (e->D + 2) * 4;
+    const double row_out = (double) e->QD * 4 + (double) e->QD / 32 * 76;  // a row's output and operand (76 B a block)
+    const double merged = (double) p.mrows.size();
+    al.bytes = (double) R * e->QD * 4 + (R - merged) * row_out;
+    al.merge_bytes = merged > 0 ? part + merged * row_out : 0.0;
     std::vector<int> seen;
     for (const AttnGroup& g : p.groups) {
         if (std::find(seen.begin(), seen.end(), g.seq) != seen.end()) continue;
@@ -905,6 +911,8 @@ struct Dev {
         aa.groups = S.dev<const AttnGroup>(al.o_grp);
         aa.items = S.dev<const AttnItem>(al.o_itm);
         aa.n_items = al.n_items;
+        aa.runs = S.dev<const AttnItem>(al.o_run);
+        aa.n_runs = al.n_runs;
         aa.part = e->apart;
         aa.max_chunks = e->max_chunks;
         aa.out = e->ao;
@@ -918,7 +926,10 @@ struct Dev {
         aa.whole = al.whole ? 1 : 0;
         aa.mrows = S.dev<const int32_t>(al.o_mrow);
         aa.n_mrows = al.n_mrows;
-        rc |= e->launch(SNX_K_ATTN, al.bytes, [&] { return attention_items(aa, st); });
+        if (al.n_runs > 0)  // (the class's bytes go with its first launch of the step)
+            rc |= e->launch(SNX_K_ATTN, al.bytes, [&] { return attention_runs(aa, st); });
+        if (al.n_items > 0)
+            rc |= e->launch(SNX_K_ATTN, al.n_runs > 0 ? 0.0 : al.bytes, [&] { return attention_items(aa, st); });
         if (!al.whole && al.n_mrows > 0)
             rc |= e->launch(SNX_K_MERGE, al.merge_bytes, [&] { return attention_merge(aa, st); });
     }
@@ -1551,7 +1562,7 @@ extern "C" long snx_chain_count(const sn_engine* e, int dropped) { return droppe
 
 extern "C" void snx_graphs(sn_engine* e, int on);
 extern "C" void snx_attn_mode(sn_engine* e, int mode) {
-    e->attn_mode = mode < -1 || mode > 1 ? -1 : mode;
+    e->attn_mode = mode < -1 || mode > 2 ? -1 : mode;
     snx_graphs(e, e->graphs);  // captured graphs hold the old form's launches
 }
 
@@ -1564,7 +1575,7 @@ extern "C" void snx_graphs(sn_engine* e, int on) {
 extern "C" int snx_step_key(int H, int KVH, int page_cells, int mode, int R, const int32_t* seq, const int32_t* pos,
                             int64_t* key, int cap, int* whole) {
     if (H <= 0 || KVH <= 0 || H % KVH || 16 % (H / KVH) || (page_cells != 32 && page_cells != 64) || R <= 0 ||
-        mode < -1 || mode > 1)
+        mode < -1 || mode > 2)
         return -1;
     int slots = 0, cells = 0;
     for (int r = 0; r < R; ++r) {

@@ -110,7 +110,12 @@ struct AttnItem {
     // positions on the very pages of `group`'s: their queries take the MFMA columns after `group`'s (-1: none), so the
     // chunk's K/V cells are read once for all of them
     int32_t share[ATT_SHARE_MAX - 1];
+    // a run item (k_attn_run): groups group .. group + nmem - 1, consecutive groups of one sequence at consecutive
+    // positions (prompt rows), walked together over the last one's nchunk chunks; 1 for every other item
+    int32_t nmem;
 };
+#define ATT_RUN_MAX 4       // groups a run item holds (their queries staged in LDS, K/V cells read once for all)
+#define ATT_RUN_MIN_WG 128  // run items are used when they make at least this many workgroups (items x KV heads)
 struct AttnArgs {
     const float* q;          // [rows][H][D] fp32 (normed, roped; the softmax scale is applied inside)
     int ldq;                 // floats between rows of q
@@ -122,6 +127,8 @@ struct AttnArgs {
     const AttnGroup* groups;
     const AttnItem* items;
     int n_items;
+    const AttnItem* runs;    // run items (k_attn_run: outputs written directly, no partials), n_runs of them
+    int n_runs;
     float* part;             // partials [rows][H][max_chunks][130]: acc[128], m, l
     int max_chunks;
     float* out;              // [rows][ldo] fp32 (merge output), or NULL
@@ -135,7 +142,8 @@ struct AttnArgs {
     const int32_t* mrows;    // rows the merge folds (chunk items), n_mrows of them
     int n_mrows;
 };
-int paged_attention(const AttnArgs& a, hipStream_t st);  // attention_items, then attention_merge
+int paged_attention(const AttnArgs& a, hipStream_t st);  // attention_runs, attention_items, then attention_merge
+int attention_runs(const AttnArgs& a, hipStream_t st);   // the run items (nothing without)
 int attention_items(const AttnArgs& a, hipStream_t st);  // the partials (chunk items) or whole groups
 int attention_merge(const AttnArgs& a, hipStream_t st);  // chunk items: the merge (nothing for whole groups)
 // The work list of R rows: consecutive rows of one sequence at consecutive positions share a group (up to 16/G rows:
@@ -143,16 +151,22 @@ int attention_merge(const AttnArgs& a, hipStream_t st);  // chunk items: the mer
 // one round of ATT_WHOLE_MIN_WG .. ATT_WHOLE_MAX_WG workgroups, the longest context is at most 9/8 of the mean and the
 // contexts are long; otherwise one item per (group, 256-cell chunk), every row merged. Both fold a row's chunk
 // partials in the same order with the same arithmetic, so a row's output does not depend on which list it was in.
+// Prompt rows: a sequence's consecutive full groups at consecutive positions become run items of up to ATT_RUN_MAX
+// groups (one workgroup per (run item, KV head) walks the last group's context once for all of them, folding each
+// group's chunk partials in chunk order as the whole-group kernel does) when the run items make at least
+// ATT_RUN_MIN_WG workgroups; the other groups follow the rule above.
 #define ATT_WHOLE_MIN_WG 240
 #define ATT_WHOLE_MAX_WG 256
 struct AttnPlan {
     std::vector<AttnGroup> groups;
     std::vector<AttnItem> items;
+    std::vector<AttnItem> runs;
     std::vector<int32_t> mrows;
     int max_chunk = 0;  // the most chunks of any group
     bool whole = false;
 };
-// mode: -1 as above, 0 per-chunk items, 1 whole groups. pt (optional, host [slots][max_pages]): the page table, from
+// mode: -1 as above, 0 per-chunk items, 1 whole groups (0 and 1: no run items), 2 run items wherever a sequence has
+// two or more such groups, the other groups as -1. pt (optional, host [slots][max_pages]): the page table, from
 // which chunk items of one-row groups whose chunk is wholly below their positions on the same pages become shared
 // items (a chunk's partial is computed alike in either kind, so a row's output does not depend on the sharing).
 void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, int page_cells, AttnPlan& p,

@@ -210,10 +210,11 @@ extern "C" int snk_q4_gemm_plan_sums(const void* d_stripes, const void* d_xa, in
 
 // ---- attention work lists
 struct snk_attn {
-    int n_rows, H, KVH, max_pages, page_cells, max_chunks, n_items, n_mrows;
+    int n_rows, H, KVH, max_pages, page_cells, max_chunks, n_items, n_mrows, n_runs;
     bool whole;
     AttnGroup* d_groups = nullptr;
     AttnItem* d_items = nullptr;
+    AttnItem* d_runs = nullptr;
     int32_t* d_mrows = nullptr;
     int32_t* d_pos = nullptr;
     float* d_part = nullptr;
@@ -231,7 +232,7 @@ extern "C" snk_attn* snk_attn_new_pt(int n_rows, const int32_t* seq, const int32
                                      int max_pages, int page_cells, int mode, const int32_t* pt, char* err,
                                      int err_len) {
     if (n_rows <= 0 || H <= 0 || KVH <= 0 || H % KVH || 16 % (H / KVH) || (page_cells != 32 && page_cells != 64) ||
-        mode < -1 || mode > 1) {
+        mode < -1 || mode > 2) {
         sn_set_err(err, err_len, "snk_attn_new: bad shape");
         return nullptr;
     }
@@ -251,14 +252,17 @@ extern "C" snk_attn* snk_attn_new_pt(int n_rows, const int32_t* seq, const int32
     p->max_chunks = pl.max_chunk;
     p->n_items = (int) pl.items.size();
     p->n_mrows = (int) pl.mrows.size();
+    p->n_runs = (int) pl.runs.size();
     p->whole = pl.whole;
     bool ok = hipMalloc(&p->d_groups, pl.groups.size() * sizeof(AttnGroup)) == hipSuccess &&
-              hipMalloc(&p->d_items, pl.items.size() * sizeof(AttnItem)) == hipSuccess &&
+              hipMalloc(&p->d_items, std::max<size_t>(1, pl.items.size()) * sizeof(AttnItem)) == hipSuccess &&
+              hipMalloc(&p->d_runs, std::max<size_t>(1, pl.runs.size()) * sizeof(AttnItem)) == hipSuccess &&
               hipMalloc(&p->d_mrows, std::max<size_t>(1, pl.mrows.size()) * 4) == hipSuccess &&
               hipMalloc(&p->d_pos, (size_t) n_rows * 4) == hipSuccess &&
               hipMalloc(&p->d_part, (size_t) n_rows * H * p->max_chunks * 130 * 4) == hipSuccess;
     ok = ok && hipMemcpy(p->d_groups, pl.groups.data(), pl.groups.size() * sizeof(AttnGroup), hipMemcpyHostToDevice) == hipSuccess &&
-         hipMemcpy(p->d_items, pl.items.data(), pl.items.size() * sizeof(AttnItem), hipMemcpyHostToDevice) == hipSuccess &&
+         (pl.items.empty() || hipMemcpy(p->d_items, pl.items.data(), pl.items.size() * sizeof(AttnItem), hipMemcpyHostToDevice) == hipSuccess) &&
+         (pl.runs.empty() || hipMemcpy(p->d_runs, pl.runs.data(), pl.runs.size() * sizeof(AttnItem), hipMemcpyHostToDevice) == hipSuccess) &&
          (pl.mrows.empty() || hipMemcpy(p->d_mrows, pl.mrows.data(), pl.mrows.size() * 4, hipMemcpyHostToDevice) == hipSuccess) &&
          hipMemcpy(p->d_pos, pos, (size_t) n_rows * 4, hipMemcpyHostToDevice) == hipSuccess;
     if (!ok) {
@@ -287,6 +291,8 @@ static AttnArgs attn_args(snk_attn* p, const float* d_q, int ldq, const void* d_
     a.groups = p->d_groups;
     a.items = p->d_items;
     a.n_items = p->n_items;
+    a.runs = p->d_runs;
+    a.n_runs = p->n_runs;
     a.part = p->d_part;
     a.max_chunks = p->max_chunks;
     a.out = d_out;
@@ -330,10 +336,13 @@ extern "C" double snk_attn_time(snk_attn* p, const float* d_q, int ldq, const vo
 
 extern "C" int snk_attn_whole(const snk_attn* p) { return p && p->whole ? 1 : 0; }
 
+extern "C" int snk_attn_runs(const snk_attn* p) { return p ? p->n_runs : 0; }
+
 extern "C" void snk_attn_free(snk_attn* p) {
     if (!p) return;
     hipFree(p->d_groups);
     hipFree(p->d_items);
+    hipFree(p->d_runs);
     hipFree(p->d_mrows);
     hipFree(p->d_pos);
     hipFree(p->d_part);

@@ -123,6 +123,7 @@ SNK_API = [
     ("snk_attn_run", I, [P, P, I, P, P, P, C.c_float, P, I, P]),
     ("snk_attn_time", C.c_double, [P, P, I, P, P, P, C.c_float, P, I, I, P]),
     ("snk_attn_whole", I, [P]),
+    ("snk_attn_runs", I, [P]),
     ("snk_attn_free", None, [P]),
     ("snk_qk_rope", I, [P, I, I, I, I, P, P, C.c_float, C.c_float, P, P, P, I, I, P, P, P]),
     ("snk_moe_router", I, [P, I, I, P, I, P, P]),
@@ -353,7 +354,8 @@ class Engine:
         self.L.snx_graphs(self.e, int(on))
 
     def attn_mode(self, mode: int):
-        """snx_attn_mode: the attention work list's form, -1 per step (default), 0 per-chunk + merge, 1 whole groups."""
+        """snx_attn_mode: the attention work list's form, -1 per step (default), 0 per-chunk + merge, 1 whole groups,
+        2 run items for prompt rows wherever possible."""
         self.L.snx_attn_mode(self.e, int(mode))
 
     def chain_count(self) -> tuple:

@@ -49,10 +49,11 @@ def config2_case(seed=2, S_=32, page=32, lo=256, hi=4096, n_share=8, share_cells
     return q, np.arange(S_, dtype=np.int32), (ctx - 1).astype(np.int32), kpool, vpool, pt, page
 
 
-def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None, whole=None, mode=-1, share=False):
+def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None, whole=None, mode=-1, share=False, runs=None):
     """whole: when given, the work list's form the planner chose (whole groups, or per-chunk items and the merge) is
     checked too; mode: the form forced (snk_attn_new_mode), -1 the planner's; share: the planner sees the page table
-    (snk_attn_new_pt) and reads shared chunks once for their rows. The KV head count is the pools'."""
+    (snk_attn_new_pt) and reads shared chunks once for their rows; runs: when given, the number of run items the list
+    holds. The KV head count is the pools'."""
     L = S.lib()
     kvh = kpool.shape[1]
     err = __import__("ctypes").create_string_buffer(256)
@@ -70,6 +71,8 @@ def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None, whole=None, 
     assert plan, err.value
     if whole is not None:
         assert L.snk_attn_whole(plan) == int(whole)
+    if runs is not None:
+        assert L.snk_attn_runs(plan) == runs, (L.snk_attn_runs(plan), runs)
     if bufs is None:
         bufs = (U.dev(kpool), U.dev(vpool), U.dev(pt))
     dq = U.dev(q)
@@ -222,3 +225,58 @@ def test_gqa_group_sizes(kvh):
     for i in (0, 1, 2, 3, 13, 31):
         one = attn_gpu(qv[i:i + 1].copy(), vseq[i:i + 1].copy(), vpos[i:i + 1].copy(), kp, vp, pt, page, scale, bufs)
         assert np.array_equal(one[0].view(np.uint32), grouped[i].view(np.uint32)), i
+
+
+@pytest.mark.parametrize("kvh,page", [(8, 32), (8, 64), (4, 64)])
+def test_prompt_runs_equal_chunk_items_bitwise(kvh, page):
+    """Prompt rows as run items: up to 4 consecutive query groups of one sequence (16 rows at G = 4, 8 at G = 8) walked
+    over their context by one workgroup per (item, KV head), K/V cells read once for all of them, outputs written
+    directly (the prompt attention of attn_pre, kernels.metal:1201-1306). Rows of four sequences: 64 prompt rows
+    across the 256-cell chunk edge, 41 rows (a run whose last group is short and a lone row after it), a decode row
+    and 6 rows from position 0. Run items (mode 2), per-chunk items with the merge (mode 0) and whole groups (mode 1)
+    give the same bits for every row; the planner's own choice (-1: too few workgroups for run items) too; and the
+    rows match the fp32 oracle."""
+    q, seq, pos, kp, vp, pt, pg = config2_case(seed=40 + kvh + page, S_=4, page=page, lo=1100, hi=1500, n_share=0,
+                                               kvh=kvh)
+    G = H // kvh
+    spans = [(0, 230, 64), (1, 1000, 41), (2, int(pos[2]), 1), (3, 0, 6)]
+    rseq = np.concatenate([np.full(n, s_, np.int32) for s_, _, n in spans])
+    rpos = np.concatenate([np.arange(p0, p0 + n, dtype=np.int32) for _, p0, n in spans])
+    r = np.random.default_rng(kvh * page)
+    qr = r.standard_normal((len(rseq), H, D), dtype=np.float32)
+    scale = 1 / math.sqrt(D)
+    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    # run items of up to 4 groups: 64 rows in groups of 16 / G rows; 41 rows in 10 (G = 4) or 20 (G = 8) full groups
+    # and a short last one, which joins the run; the 6 rows from position 0 in 2 (G = 4) or 3 groups; the decode row
+    # stays a group of its own
+    gmax = 16 // G
+    n_runs = sum(-(-(-(-n // gmax)) // 4) for n in (64, 41, 6))
+    runs = attn_gpu(qr, rseq, rpos, kp, vp, pt, pg, scale, bufs, mode=2, runs=n_runs)
+    chunks = attn_gpu(qr, rseq, rpos, kp, vp, pt, pg, scale, bufs, mode=0, runs=0)
+    whole = attn_gpu(qr, rseq, rpos, kp, vp, pt, pg, scale, bufs, mode=1, runs=0)
+    auto = attn_gpu(qr, rseq, rpos, kp, vp, pt, pg, scale, bufs, runs=0)
+    assert np.array_equal(runs.view(np.uint32), chunks.view(np.uint32))
+    assert np.array_equal(runs.view(np.uint32), whole.view(np.uint32))
+    assert np.array_equal(runs.view(np.uint32), auto.view(np.uint32))
+    ref = O.paged_attn(qr, rseq, rpos, kvh, kp, vp, pg, pt, scale)
+    err = np.abs(runs - ref)
+    print(f"G={G} page {pg}: {len(rseq)} rows, max abs err {err.max():.3g}")
+    assert np.all(err <= ATOL + RTOL * np.abs(ref))
+
+
+def test_prompt_runs_chosen_for_prompt_steps():
+    """The planner takes run items by itself when they make at least 128 workgroups: one sequence's 512 prompt rows
+    at positions 1536 .. 2047 (128 groups of 4 rows: 32 run items x 8 KV heads), bit for bit the chunk items' output
+    and the oracle's within tolerance."""
+    q, seq, pos, kp, vp, pt, pg = config2_case(seed=50, S_=1, page=64, lo=2048, hi=2048, n_share=0)
+    rseq = np.zeros(512, np.int32)
+    rpos = np.arange(1536, 2048, dtype=np.int32)
+    qr = np.random.default_rng(51).standard_normal((512, H, D), dtype=np.float32)
+    scale = 1 / math.sqrt(D)
+    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    auto = attn_gpu(qr, rseq, rpos, kp, vp, pt, pg, scale, bufs, runs=32)
+    chunks = attn_gpu(qr, rseq, rpos, kp, vp, pt, pg, scale, bufs, mode=0, runs=0)
+    assert np.array_equal(auto.view(np.uint32), chunks.view(np.uint32))
+    sel = np.r_[0:8, 250:262, 504:512]  # rows at the first, middle and last chunk edges (the oracle is slow)
+    ref = O.paged_attn(qr[sel], rseq[sel], rpos[sel], KVH, kp, vp, pg, pt, scale)
+    assert np.all(np.abs(auto[sel] - ref) <= ATOL + RTOL * np.abs(ref))

@@ -383,13 +383,13 @@ def test_probs_records_and_end_ban(tiny):
 
 def test_attention_list_forms_give_the_same_steps(tiny):
     """snx_attn_mode: whole-group attention (its kernel writes the rows' outputs and the o-projection's Q8_0 operand
-    itself) and per-chunk attention with the merge give the same tokens and logits, bit for bit, over prompt and decode
-    steps that cross 256-cell chunk boundaries."""
-    r = np.random.default_rng(21)
+    itself), per-chunk attention with the merge and run items for the prompt rows (mode 2: up to 4 consecutive query
+    groups a workgroup, writing their outputs and operand) give the same tokens and logits, bit for bit, over prompt
+    and decode steps that cross 256-cell chunk boundaries."""
     V = TINY["n_vocab"]
     lens = [300, 40, 530]
     outs = []
-    for mode in (0, 1):
+    for mode in (0, 1, 2):
         with S.Engine(tiny, slots=3, ctx=640, max_rows=256) as eng:
             eng.attn_mode(mode)
             rr = np.random.default_rng(21)
@@ -409,9 +409,10 @@ def test_attention_list_forms_give_the_same_steps(tiny):
                 cur = t.astype(np.int32)
                 pos = pos + 1
             outs.append(got)
-    for (ta, la), (tb, lb) in zip(*outs):
-        assert np.array_equal(ta, tb)
-        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    for other in outs[1:]:
+        for (ta, la), (tb, lb) in zip(outs[0], other):
+            assert np.array_equal(ta, tb)
+            assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
 
 
 def test_chained_steps(tiny):

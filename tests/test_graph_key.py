@@ -7,8 +7,9 @@ import pytest
 
 import sllm_next as S
 
-# The attention plan's fields in the key: form, items, merge rows, and the offsets of groups, items and merge rows
-ATTN_FIELDS = 6
+# The attention plan's fields in the key: form, items, merge rows, the offsets of groups, items and merge rows, run
+# items and their offset
+ATTN_FIELDS = 8
 
 
 def rows(n, pos):
@@ -31,6 +32,7 @@ def test_chunk_and_whole_forms_have_different_keys(page_cells, long_pos):
     # the groups and items agree, which alone left the two forms on one graph
     assert a_chunk[1] == a_whole[1] == 32 and a_chunk[3:5] == a_whole[3:5]
     assert (a_chunk[0], a_chunk[2]) == (0, 32) and (a_whole[0], a_whole[2]) == (1, 0)
+    assert a_chunk[6] == a_whole[6] == 0  # no run items (decode rows)
     # ... and the keys differ
     assert k_chunk != k_whole
 
@@ -61,3 +63,17 @@ def test_bad_arguments_are_refused():
         S.step_key(32, 7, 64, -1, *rows(4, 10))  # G not a divisor of 16
     with pytest.raises(S.SnError):
         S.step_key(32, 8, 48, -1, *rows(4, 10))  # page size
+
+
+def test_prompt_run_items_change_the_key():
+    """512 prompt rows of one sequence: the planner's run items (128 groups of 4 rows in 32 items, 256 workgroups)
+    against the same rows forced to per-chunk items (mode 0): the run-item count is in the key."""
+    seq = np.zeros(512, np.int32)
+    pos = np.arange(1536, 2048, dtype=np.int32)
+    k_run, _ = S.step_key(32, 8, 64, -1, seq, pos)
+    k_chunk, _ = S.step_key(32, 8, 64, 0, seq, pos)
+    assert k_run[-ATTN_FIELDS:][6] == 32 and k_chunk[-ATTN_FIELDS:][6] == 0
+    assert k_run != k_chunk
+    # 64 prompt rows make 4 run items, 32 workgroups: too few, the planner keeps chunk items; mode 2 takes them
+    assert S.step_key(32, 8, 64, -1, seq[:64], pos[:64])[0][-ATTN_FIELDS:][6] == 0
+    assert S.step_key(32, 8, 64, 2, seq[:64], pos[:64])[0][-ATTN_FIELDS:][6] == 4
