@@ -112,10 +112,12 @@ __device__ __forceinline__ void attn_issue(const AttnArgs& a, int kvh, int cbase
 
 // The wavefront's softmax partial over its 64 cells (the cells past the group's last position read as zeros): scores
 // S^T = K . Q^T; per query the max m and sum l of exp(s - m) (lanes n, n+16, n+32, n+48 share query n); O = P . V, MFMA
-// t covering output dims {8 c + t : c = 0..15}.
+// t covering output dims {8 c + t : c = 0..15}. full (wavefront-uniform): every one of the 64 cells lies at or below
+// every valid query's position, so no score is masked and the masking is skipped (the same values; a column without
+// a query then holds finite garbage that no one reads).
 __device__ __forceinline__ void attn_scores(const u32x4 (&kf)[4][4], const half8 (&qh)[4], const half8 (&ql)[4],
                                             int cbase, bool qvalid, int qpos, int g, float& m, float& l,
-                                            floatx4 (&s)[4]) {
+                                            floatx4 (&s)[4], bool full) {
     for (int jg = 0; jg < 4; ++jg) {
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
         for (int t = 0; t < 4; ++t) {
@@ -126,22 +128,36 @@ __device__ __forceinline__ void attn_scores(const u32x4 (&kf)[4][4], const half8
         s[jg] = acc;  // lane (n, g): cells cbase + 16 jg + 4 g + v, query n
     }
     m = -INFINITY;
-    for (int jg = 0; jg < 4; ++jg)
-        for (int v = 0; v < 4; ++v) {
-            const int c = cbase + 16 * jg + 4 * g + v;
-            const bool ok = qvalid && c <= qpos;
-            s[jg][v] = ok ? s[jg][v] : -INFINITY;
-            m = fmaxf(m, s[jg][v]);
-        }
+    if (full) {
+        for (int jg = 0; jg < 4; ++jg)
+            for (int v = 0; v < 4; ++v) m = fmaxf(m, s[jg][v]);
+    } else {
+        for (int jg = 0; jg < 4; ++jg)
+            for (int v = 0; v < 4; ++v) {
+                const int c = cbase + 16 * jg + 4 * g + v;
+                const bool ok = qvalid && c <= qpos;
+                s[jg][v] = ok ? s[jg][v] : -INFINITY;
+                m = fmaxf(m, s[jg][v]);
+            }
+    }
     m = fmaxf(m, __shfl_xor(m, 16));
     m = fmaxf(m, __shfl_xor(m, 32));
     l = 0.0f;
-    for (int jg = 0; jg < 4; ++jg)
-        for (int v = 0; v < 4; ++v) {
-            const float p = m == -INFINITY ? 0.0f : __expf(s[jg][v] - m);
-            s[jg][v] = p;
-            l += p;
-        }
+    if (full) {  // (m is finite)
+        for (int jg = 0; jg < 4; ++jg)
+            for (int v = 0; v < 4; ++v) {
+                const float p = __expf(s[jg][v] - m);
+                s[jg][v] = p;
+                l += p;
+            }
+    } else {
+        for (int jg = 0; jg < 4; ++jg)
+            for (int v = 0; v < 4; ++v) {
+                const float p = m == -INFINITY ? 0.0f : __expf(s[jg][v] - m);
+                s[jg][v] = p;
+                l += p;
+            }
+    }
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
 }
@@ -164,9 +180,9 @@ __device__ __forceinline__ void attn_pv(const u32x4 (&vf)[2][8], const floatx4 (
 
 __device__ __forceinline__ void attn_wave(const u32x4 (&kf)[4][4], const u32x4 (&vf)[2][8], const half8 (&qh)[4],
                                           const half8 (&ql)[4], int cbase, bool qvalid, int qpos, int g, float& m,
-                                          float& l, floatx4 (&o)[8]) {
+                                          float& l, floatx4 (&o)[8], bool full) {
     floatx4 s[4];
-    attn_scores(kf, qh, ql, cbase, qvalid, qpos, g, m, l, s);
+    attn_scores(kf, qh, ql, cbase, qvalid, qpos, g, m, l, s, full);
     attn_pv(vf, s, o);
 }
 
@@ -285,9 +301,11 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
     attn_pages(a, a.pt + (size_t) gr.seq * a.max_pages, cbase, pos_last, p_lo, p_hi);
     u32x4 kf[4][4], vf[2][8];
     attn_issue(a, kvh, cbase, pos_last, p_lo, p_hi, true, n, g, kf, vf);
+    // (a shared chunk lies wholly below every member's position; otherwise the group's first row is its lowest)
+    const bool full = shared || cbase + 63 <= gr.pos0;
     float m, l;
     floatx4 o[8];
-    attn_wave(kf, vf, qh, ql, cbase, qvalid, qpos, g, m, l, o);
+    attn_wave(kf, vf, qh, ql, cbase, qvalid, qpos, g, m, l, o, full);
     // thread -> (query qq, 8 dims)
     const int qq = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
     float M, L, acc[8];
@@ -399,7 +417,7 @@ __global__ __launch_bounds__(512) void k_attn_whole(AttnArgs a) {
         float m, l;
         floatx4 sc[4], o[8];
         __builtin_amdgcn_sched_barrier(0);
-        attn_scores(kf, qh, ql, cbase, qvalid && live, qpos, g, m, l, sc);
+        attn_scores(kf, qh, ql, cbase, qvalid && live, qpos, g, m, l, sc, live && cbase + 63 <= gr.pos0);
         __builtin_amdgcn_sched_barrier(0);
         attn_issue_k(a, rn, ncb, npl, n, g, kf);
         __builtin_amdgcn_sched_barrier(0);
@@ -419,7 +437,8 @@ __global__ __launch_bounds__(512) void k_attn_whole(AttnArgs a) {
         float acc1[8];
         for (int d = 0; d < 8; ++d) acc1[d] = sh.x[th][d];
         attn_fold<8>(RM, RL, RO, sh.x[th][8], sh.x[th][9], acc1);
-        __syncthreads();  // every read of sh done before the next pair writes it
+        // (no barrier here: the next pair writes sh.h after every thread's combine reads, which precede the barrier
+        // above, and sh.x after its combine's barrier, which every thread reaches only once its fold has read sh.x)
     }
     const int row = qq / G, head = kvh * G + qq % G;
     if (half != 0 || row >= gr.nrows) return;
@@ -524,7 +543,7 @@ __global__ __launch_bounds__(512) void k_attn_run(AttnArgs a) {
             float ml, ll;
             floatx4 sc[4], o[8];
             __builtin_amdgcn_sched_barrier(0);
-            attn_scores(kf, qh, ql, cbase, qvalid && live, gm.pos0 + qrow, g, ml, ll, sc);
+            attn_scores(kf, qh, ql, cbase, qvalid && live, gm.pos0 + qrow, g, ml, ll, sc, live && cbase + 63 <= gm.pos0);
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (decltype(last)::value) attn_issue_k(a, rn, ncb, npl, n, g, kf);
             __builtin_amdgcn_sched_barrier(0);
@@ -546,12 +565,14 @@ __global__ __launch_bounds__(512) void k_attn_run(AttnArgs a) {
             float acc1[8];
             for (int d = 0; d < 8; ++d) acc1[d] = sh.x[th][d];
             attn_fold<8>(RM, RL, RO, sh.x[th][8], sh.x[th][9], acc1);
-            if (half == 0) {
+            if (half == 0) {  // (a thread's own slots: no barrier needed for them)
                 for (int d = 0; d < 8; ++d) sh.st[m][d][th] = RO[d];
                 sh.st[m][8][th] = RM;
                 sh.st[m][9][th] = RL;
             }
-            __syncthreads();  // every read of sh.h and sh.x done before the next group writes them
+            // (no barrier here: the next group writes sh.h after every thread's combine reads, which precede the
+            // barrier above, and sh.x after its combine's barrier, which every thread reaches only once its fold has
+            // read sh.x)
         };
         for (int m = 0; m + 1 < nm; ++m) member(m, std::false_type{});
         member(nm - 1, std::true_type{});

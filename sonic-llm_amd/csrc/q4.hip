@@ -377,8 +377,12 @@ __device__ __forceinline__ half8 q8_unpack(uint32_t w_lo, uint32_t w_hi) {
 //
 // The kernel writes each slice's raw fp32 sums, part[slice][M][N]; whoever consumes them adds the slices in slice
 // order (k_q4_reduce here; the row kernels of the step), so the order of every sum is fixed by (N, K) alone.
-template <int WT, int MT, int S>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_q4_gemm(GemmArgs a) {
+// FK (prompt rows, grid.y = 1): the workgroup walks every slice in turn, each summed into a fresh accumulator exactly
+// as its own launch would (the same groups, an odd slice's extra group added with scale 0 as its own ring pads it),
+// and adds the slices in slice order as the consumers do ((p0 + p1) + p2 ...), so part[0] holds, bit for bit, what
+// the consumers would have made of the split launch's slices: they read it as one slice.
+template <int WT, int MT, int S, bool FK>
+__device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
     constexpr int D = 2, FPW = MT;  // ring slots, fragments each wavefront stages
     // the loop below stages group i + 1 from register slot j ^ 1 into LDS buffer j ^ 1 and sums group i from buffer j:
     // the register ring and the LDS double buffer are one and the same pair of slots
@@ -400,7 +404,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
         mt0 = a.items[2 * blockIdx.z + 1];
     }
     mt0 = __builtin_amdgcn_readfirstlane(mt0);
-    const int c0 = slice * a.gps, ng = min(a.gps, a.ngroups - c0);  // groups c0 .. c0 + ng - 1 (ng >= 1)
+    // groups c0 .. c0 + ng - 1 (ng >= 1). FK: every group (the slices hold an even number of groups, so the walk is
+    // the groups in order, the last slice padded to an even count as its own launch pads it)
+    const int c0 = FK ? 0 : slice * a.gps, ng = FK ? a.ngroups : min(a.gps, a.ngroups - c0);
     const int s0 = set * (4 * S) + wave * S;
     const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(S, a.nstripes - s0)));
     const int sbytes = a.ngroups * TB;  // one stripe
@@ -429,9 +435,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     u32x2 ws[D][S];
     u32x4 ra[D][FPW];
     float rk[D];
-    floatx4 acc[S][MT];
+    floatx4 acc[S][MT], tot[S][MT];
     for (int s = 0; s < S; ++s)
-        for (int mt = 0; mt < MT; ++mt) acc[s][mt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < MT; ++mt) acc[s][mt] = tot[s][mt] = (floatx4){0.f, 0.f, 0.f, 0.f};
 
     auto load = [&](int slot, int i) {
         const int c = c0 + min(i, ng - 1);
@@ -477,6 +483,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     }
     stage(0, 0);
     const int trips = (ng + D - 1) / D;
+    int in_slice = 0;  // FK: groups of the current slice summed so far
+    bool first = true;
     for (int t = 0; t < trips; ++t)
         for (int j = 0; j < D; ++j) {
             const int i = t * D + j;
@@ -485,9 +493,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
             stage(j ^ 1, j ^ 1);  // group i + 1 (its registers: slot (i + 1) % D)
             __builtin_amdgcn_sched_barrier(0);
             compute(j, j, i < ng ? 1.0f : 0.0f);
+            if constexpr (FK) {
+                if (++in_slice == a.gps || i == D * trips - 1) {  // the slice's last group: add the slice on
+                    in_slice = 0;
+                    for (int s = 0; s < S; ++s)
+                        for (int mt = 0; mt < MT; ++mt) {
+                            if (first) tot[s][mt] = acc[s][mt];
+                            else
+                                for (int v = 0; v < 4; ++v) tot[s][mt][v] = tot[s][mt][v] + acc[s][mt][v];
+                            acc[s][mt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+                        }
+                    first = false;
+                }
+            }
             __builtin_amdgcn_sched_barrier(0);
             load(j, i + D);
         }
+    if constexpr (FK)
+        for (int s = 0; s < S; ++s)
+            for (int mt = 0; mt < MT; ++mt) acc[s][mt] = tot[s][mt];
 
     // lane (n, g) holds rows 4g + v of each row tile, column n of each of its stripes
     for (int s = 0; s < S; ++s) {
@@ -500,6 +524,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
                     a.part[((size_t) slice * a.M + row) * a.N + col] = acc[s][mt][v];
             }
     }
+}
+
+template <int WT, int MT, int S, bool FK = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_q4_gemm(GemmArgs a) {
+    q4_gemm_ring<WT, MT, S, FK>(a);
+}
+// the FK walk with two stripes a wavefront (prompt rows of the wide matrices): its accumulators and slice sums need
+// more than the 168 registers of 3 wavefronts a SIMD
+template <int WT, int MT, int S>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_q4_gemm_fk2(GemmArgs a) {
+    q4_gemm_ring<WT, MT, S, true>(a);
 }
 
 // The streaming form: the slice's activation records (gps groups, up to GMAX) are loaded once per workgroup by the 4
@@ -673,20 +708,21 @@ GemmPlan q4_plan(int N, int K, int wt) {
 
 size_t q4_workspace_bytes(int M, int N, int K, int wt) { return (size_t) q4_plan(N, K, wt).ks * M * N * sizeof(float); }
 
-template <int WT>
+// (FK: one stripe a wavefront only, the plan of every split layer matrix)
+template <int WT, bool FK = false>
 static void launch_gemm(int mt, int spw, dim3 grid, const GemmArgs& a, hipStream_t st) {
-    if constexpr (WT == WT_Q4_0) {
+    if constexpr (WT == WT_Q4_0 && !FK) {
         if (mt == 1) {
-            if (spw == 2) hipLaunchKernelGGL((k_q4_gemm<WT, 1, 2>), grid, dim3(256), 0, st, a);
-            else hipLaunchKernelGGL((k_q4_gemm<WT, 1, 1>), grid, dim3(256), 0, st, a);
+            if (spw == 2) hipLaunchKernelGGL((k_q4_gemm<WT, 1, 2, FK>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_q4_gemm<WT, 1, 1, FK>), grid, dim3(256), 0, st, a);
         } else {
-            if (spw == 2) hipLaunchKernelGGL((k_q4_gemm<WT, 2, 2>), grid, dim3(256), 0, st, a);
-            else hipLaunchKernelGGL((k_q4_gemm<WT, 2, 1>), grid, dim3(256), 0, st, a);
+            if (spw == 2) hipLaunchKernelGGL((k_q4_gemm<WT, 2, 2, FK>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_q4_gemm<WT, 2, 1, FK>), grid, dim3(256), 0, st, a);
         }
-    } else {  // Q8_0: one stripe per wavefront (q4_plan)
+    } else {  // Q8_0: one stripe per wavefront (q4_plan); FK likewise
         (void) spw;
-        if (mt == 1) hipLaunchKernelGGL((k_q4_gemm<WT, 1, 1>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_q4_gemm<WT, 2, 1>), grid, dim3(256), 0, st, a);
+        if (mt == 1) hipLaunchKernelGGL((k_q4_gemm<WT, 1, 1, FK>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_q4_gemm<WT, 2, 1, FK>), grid, dim3(256), 0, st, a);
     }
 }
 
@@ -735,6 +771,23 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
     // 16.6 all single; 4 tiles, at 2 wavefronts a SIMD for their registers, 17.5). Either way a row's sums are the same
     // (same slices, same order).
     const int mt = a.mtiles == 1 || (p.nstripes < 512 && a.M < Q4_PAIR_ROWS) ? 1 : 2;
+    // prompt rows: one workgroup walks every slice of its tiles and leaves their sum in part[0] (the same bits the
+    // consumers make of the slices), so no slice is written or read back (at 512 rows the split launches wrote 16-120
+    // MB of slices a matrix)
+    if (a.M >= Q4_PAIR_ROWS && p.ks > 1 && p.spw == 1 && p.gps % 2 == 0) {
+        // Qwen3-4B at 512 rows a step (launches of one sequence's prompt): 2 stripes a wavefront for the wide q|k|v
+        // and gate|up (33 and 92 us against 42 and 119 with one; 4 stripes: 42 and 92), one for o and down (54 us
+        // against 60 with two); 40.7k -> 43.3k prompt tok/s on one box. The split launches and their slices: 34.7k.
+        if (wt == WT_Q4_0 && p.nstripes >= 384) {
+            const dim3 grid((p.nstripes + 7) / 8, 1, (a.mtiles + 1) / 2);
+            hipLaunchKernelGGL((k_q4_gemm_fk2<WT_Q4_0, 2, 2>), grid, dim3(256), 0, st, a);
+        } else {
+            const dim3 grid(p.sets, 1, (a.mtiles + 1) / 2);
+            if (wt == WT_Q8_0) launch_gemm<WT_Q8_0, true>(2, 1, grid, a, st);
+            else launch_gemm<WT_Q4_0, true>(2, 1, grid, a, st);
+        }
+        return 1;
+    }
     const dim3 grid(p.sets, p.ks, mt == 1 ? a.mtiles : (a.mtiles + 1) / 2);
     if (wt == WT_Q8_0) launch_gemm<WT_Q8_0>(mt, p.spw, grid, a, st);
     else launch_gemm<WT_Q4_0>(mt, p.spw, grid, a, st);

@@ -170,6 +170,25 @@ def test_row_invariance_bitwise():
         assert np.array_equal(part.view(np.uint32), full[rows].view(np.uint32))
 
 
+@pytest.mark.parametrize("N,K", [(6144, 2560), (19456, 2560), (2560, 9728)])
+def test_row_invariance_prompt_shapes(N, K):
+    """The Qwen3-4B layer matrices (q|k|v, gate|up, down) at 300 prompt rows, where one workgroup walks every k-slice
+    of its tiles and adds them in slice order itself, against decode-sized subsets of the same rows, which the split
+    launches and the consumer's slice sum serve: every row bit for bit the same (sn.h:1-3)."""
+    r = np.random.default_rng(N + K)
+    Wq = O.quantize_q4_0(r.normal(0, 0.02, (N, K)).astype(np.float32))
+    X = r.normal(0, 1, (300, K)).astype(np.float32)
+    L = S.lib()
+    wbuf = U.empty(L.snk_q4_stripes_bytes(N, K))
+    assert L.snk_q4_repack(U.ptr(U.dev(Wq)), N, K, U.ptr(wbuf), U.stream()) == 0
+    full, _ = gemm_gpu(None, N, K, X, wbuf=wbuf)
+    for rows in ([0], list(range(100, 132)), list(range(290, 300))):
+        part, _ = gemm_gpu(None, N, K, X[rows], wbuf=wbuf)
+        assert np.array_equal(part.view(np.uint32), full[rows].view(np.uint32)), rows
+    ref = O.mul_mat_q4_0(Wq, K, X[:4])
+    assert np.all(np.abs(full[:4] - ref) <= ATOL + RTOL * np.abs(ref))
+
+
 @pytest.fixture(scope="module")
 def lm_head():
     """The Qwen3-4B LM head's shape (configs[2..4]: V = 151,936 rows of K = 2560), seeded N(0, 0.02) weights quantized
