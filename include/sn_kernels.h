@@ -65,6 +65,13 @@ int snk_q4_gemm(const void* d_stripes, const void* d_xa, int M, int N, int K, fl
 // (other streams or threads) share the array and race. 0, or -1 (err).
 // No counterpart in the reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving
 // loops, harnesses that forbid hipMalloc).
+// Prompt rows (M >= 256) of a stripe-interleaved gate|up matrix (N = 2F, F a multiple of 128, the wide split plans)
+// with its SwiGLU as the epilogue: silu(gate) * up as fp32 rows d_h [M][F] and as the Q8_0 operand d_xo (K = F, not
+// d_xa), the same bits as snk_q4_gemm's SwiGLU epilogue and snk_quant_act of its rows (the prompt step's fused
+// up-projection epilogue, qmm_epi flag 4, kernels.metal:566-568, with the next block matmul's input written directly
+// as its flag 32 does). 0, 1 when the shape does not take it (nothing launched), or -1
+int snk_q4_gemm_swiglu(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_h, void* d_xo,
+                       void* stream);
 int snk_q4_gemm_noalloc(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi,
                         void* stream, char* err, int err_len);
 // average device time (microseconds) of one raw matmul launch (the k-slice sums into d_ws, as a decode step runs it:

@@ -91,6 +91,7 @@ struct sn_engine {
     float *x = nullptr, *qkv = nullptr, *ao = nullptr, *hb = nullptr, *logits = nullptr, *gemm_ws = nullptr;
     size_t gemm_ws_bytes = 0;
     uint8_t* xa = nullptr;
+    uint8_t* xa2 = nullptr;  // the down projection's operand when prompt rows' gate|up writes it (q4_gemm_swiglu)
     float* apart = nullptr;
     int max_chunks = 0;
     uint8_t *d_stage = nullptr, *h_stage = nullptr;
@@ -554,6 +555,8 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->xa = e->dalloc<uint8_t>(std::max({xa_bytes(R, KMAX), e->NE > 0 ? xa_bytes(P, std::max(E, e->FE)) : 0,
                                          e->head_t == GGML_Q6_K ? xk_bytes(MO, E) : 0}),
                                err, err_len);
+    if (e->NE == 0 && F > 0 && q4_gemm_swiglu_fits(R, 2 * F, E, e->wt))
+        e->xa2 = e->dalloc<uint8_t>(xa_bytes(R, F), err, err_len);
     size_t ws = 0;
     ws = std::max(ws, q4_workspace_bytes(R, e->NQKV, E, e->wt));
     ws = std::max(ws, q4_workspace_bytes(R, E, QD, e->wt));
@@ -856,11 +859,21 @@ struct Dev {
     bool moe_pending = false;  // x awaits a MoE layer's weighted expert rows (added by the next resid)
     int rc = 0;
 
-    void gemm(const uint8_t* w, int M, int N, int K) {
+    void gemm(const uint8_t* w, int M, int N, int K, const uint8_t* xa = nullptr) {
         rc |= e->launch(SNX_K_GEMM, gemm_bytes(e->wt, M, N, K), [&] {
-            ks = q4_gemm_raw(w, e->xa, M, N, K, e->gemm_ws, e->gemm_ws_bytes, st, e->wt);
+            ks = q4_gemm_raw(w, xa ? xa : e->xa, M, N, K, e->gemm_ws, e->gemm_ws_bytes, st, e->wt);
             return ks < 0 ? -1 : 0;
         });
+    }
+    // prompt rows: gate|up with its SwiGLU + Q8_0 as the epilogue (the rows h and the down projection's operand in
+    // xa2); false when the shape does not take it
+    bool gemm_swiglu(const uint8_t* w, int M) {
+        const int F = e->F, E = e->E;
+        if (!e->xa2 || !q4_gemm_swiglu_fits(M, 2 * F, E, e->wt)) return false;
+        rc |= e->launch(SNX_K_GEMM, gemm_bytes(e->wt, M, 2 * F, E) - (double) M * F * 4 + (double) M * F * 6, [&] {
+            return q4_gemm_swiglu(w, e->xa, M, 2 * F, E, e->hb, e->xa2, st, e->wt) == 1 ? 0 : -1;
+        });
+        return true;
     }
     void quant(const float* x, const int32_t* rows, int M, int K, const float* nw, float* xn = nullptr) {
         rc |= e->launch(SNX_K_QUANT, (double) M * K * 8, [&] {
@@ -951,6 +964,10 @@ struct Dev {
             return true;
         }
         resid(x, R, l.ffn_norm, true);
+        if (gemm_swiglu(l.wgu, R)) {
+            gemm(l.wd, R, E, F, e->xa2);
+            return true;
+        }
         gemm(l.wgu, R, 2 * F, E);
         swiglu(R);
         gemm(l.wd, R, E, F);

@@ -381,7 +381,7 @@ __device__ __forceinline__ half8 q8_unpack(uint32_t w_lo, uint32_t w_hi) {
 // as its own launch would (the same groups, an odd slice's extra group added with scale 0 as its own ring pads it),
 // and adds the slices in slice order as the consumers do ((p0 + p1) + p2 ...), so part[0] holds, bit for bit, what
 // the consumers would have made of the split launch's slices: they read it as one slice.
-template <int WT, int MT, int S, bool FK>
+template <int WT, int MT, int S, bool FK, bool SW = false>
 __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
     constexpr int D = 2, FPW = MT;  // ring slots, fragments each wavefront stages
     // the loop below stages group i + 1 from register slot j ^ 1 into LDS buffer j ^ 1 and sums group i from buffer j:
@@ -513,6 +513,30 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
         for (int s = 0; s < S; ++s)
             for (int mt = 0; mt < MT; ++mt) acc[s][mt] = tot[s][mt];
 
+    if constexpr (SW) {
+        // SwiGLU of the tiles, as k_swiglu_quant makes it of the slices (the same sums: silu(gate) * up, Q8_0 blocks of
+        // 32 F columns): wavefront w's stripes are gate and up of F columns 64 set + 16 w .. + 15; the workgroup's 2 x 16
+        // rows x 64 columns go through LDS to threads (row, block of 32, lane part) for the quantizer
+        static_assert(FK && S == 2 && MT == 2, "the SwiGLU epilogue takes the FK walk with gate and up a wavefront");
+        __shared__ float s_h[32][64 + 4];
+        for (int mt = 0; mt < MT; ++mt)
+            for (int v = 0; v < 4; ++v) s_h[16 * mt + 4 * g + v][16 * wave + n_in] = silu(acc[0][mt][v]) * acc[1][mt][v];
+        __syncthreads();
+        const int t = threadIdx.x, r = t >> 3, blk = (t >> 2) & 1, gq = t & 3;
+        const int row = mt0 * 16 + r, F = a.N / 2, b = 2 * set + blk;
+        float v8[8];
+        for (int j = 0; j < 4; ++j) {
+            v8[j] = s_h[r][32 * blk + 4 * gq + j];
+            v8[4 + j] = s_h[r][32 * blk + 16 + 4 * gq + j];
+        }
+        if (row >= a.M || 32 * b >= F) return;  // (a block's 4 lane parts share the row and block: q8_store's shuffles)
+        float* o = a.h + (size_t) row * F + 32 * b;
+        *(float4*) (o + 4 * gq) = (float4){v8[0], v8[1], v8[2], v8[3]};
+        *(float4*) (o + 16 + 4 * gq) = (float4){v8[4], v8[5], v8[6], v8[7]};
+        q8_store(v8, gq, a.xo, F, row, b);
+        return;
+    }
+
     // lane (n, g) holds rows 4g + v of each row tile, column n of each of its stripes
     for (int s = 0; s < S; ++s) {
         const int stripe = s0 + s, col = stripe * 16 + n_in;
@@ -531,10 +555,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     q4_gemm_ring<WT, MT, S, FK>(a);
 }
 // the FK walk with two stripes a wavefront (prompt rows of the wide matrices): its accumulators and slice sums need
-// more than the 168 registers of 3 wavefronts a SIMD
-template <int WT, int MT, int S>
+// more than the 168 registers of 3 wavefronts a SIMD. SW: the gate|up matrix's SwiGLU + Q8_0 as its epilogue
+template <int WT, int MT, int S, bool SW = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_q4_gemm_fk2(GemmArgs a) {
-    q4_gemm_ring<WT, MT, S, true>(a);
+    q4_gemm_ring<WT, MT, S, true, SW>(a);
 }
 
 // The streaming form: the slice's activation records (gps groups, up to GMAX) are loaded once per workgroup by the 4
@@ -832,6 +856,26 @@ int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, cons
     const dim3 grid((a.nstripes + 3) / 4, 1, max_items);
     if (wt == WT_Q8_0) hipLaunchKernelGGL((k_q4_gemm<WT_Q8_0, 1, 1>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((k_q4_gemm<WT_Q4_0, 1, 1>), grid, dim3(256), 0, st, a);
+    return 1;
+}
+
+bool q4_gemm_swiglu_fits(int M, int N, int K, int wt) {
+    if (wt != WT_Q4_0 || M < Q4_PAIR_ROWS || N % 256 != 0) return false;
+    const GemmPlan p = q4_plan(N, K, wt);
+    return p.ks > 1 && p.spw == 1 && p.gps % 2 == 0 && p.nstripes >= 384;  // (the FK walk's shapes)
+}
+
+int q4_gemm_swiglu(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* h, uint8_t* xo, hipStream_t st,
+                   int wt) {
+    if (!q4_gemm_swiglu_fits(M, N, K, wt) || xo == xa || h == nullptr || xo == nullptr) return 0;
+    const GemmPlan p = q4_plan(N, K, wt);
+    GemmArgs a{};
+    a.w = w; a.xa = xa; a.h = h; a.xo = xo;
+    a.M = M; a.N = N; a.K = K; a.epi = EPI_STORE;
+    a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
+    a.mtiles = (M + 15) / 16;
+    const dim3 grid((p.nstripes + 7) / 8, 1, (a.mtiles + 1) / 2);
+    hipLaunchKernelGGL((k_q4_gemm_fk2<WT_Q4_0, 2, 2, true>), grid, dim3(256), 0, st, a);
     return 1;
 }
 

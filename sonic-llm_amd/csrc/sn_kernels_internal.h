@@ -21,6 +21,9 @@ struct GemmArgs {
     // gM rows, instead of row p of a tile-ordered one
     const int32_t* gsrc;
     int gM;
+    // (prompt gate|up, q4_gemm_swiglu) SwiGLU of the sums as fp32 rows h [M][N / 2] and as the Q8_0 operand xo
+    float* h;
+    uint8_t* xo;
     int M, N, K, ldy, epi;
     int nstripes, ngroups, ks, gps, mtiles;
 };
@@ -40,6 +43,13 @@ GemmPlan q4_plan(int N, int K, int wt = WT_Q4_0);
 // the raw matmul with an explicit plan (tuning): mt row tiles a workgroup, spw stripes a wavefront, G groups a slice
 // loaded at once (G 0: the default plan); the slice count, or -1
 // part[ks][M][N] added in slice order into y [M][N]
+// The prompt rows' gate|up matmul with its SwiGLU: from Q4_PAIR_ROWS rows, a Q4_0 stripe-interleaved matrix of
+// N = 2F (F a multiple of 128) walked whole (k_q4_gemm_w2, FK) with silu(gate) * up written as fp32 rows h [M][F] and
+// as the Q8_0 operand xo (K = F), the same bits as the matmul's slices through k_swiglu_quant. xo must not be xa.
+// Returns 1, or 0 when the shape does not qualify (nothing launched: use the matmul and swiglu_quant).
+int q4_gemm_swiglu(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* h, uint8_t* xo, hipStream_t st,
+                   int wt);
+bool q4_gemm_swiglu_fits(int M, int N, int K, int wt);  // whether q4_gemm_swiglu takes this shape
 void q4_reduce_slices(const float* part, int ks, int M, int N, float* y, hipStream_t st);
 int q4_gemm_raw_plan(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
                      hipStream_t st, int wt, int mt, int spw, int G);

@@ -122,6 +122,15 @@ extern "C" int snk_q4_gemm(const void* d_stripes, const void* d_xa, int M, int N
     return rc == 0 && hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+extern "C" int snk_q4_gemm_swiglu(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_h,
+                                  void* d_xo, void* stream) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 32 || !d_h || !d_xo || d_xo == d_xa) return -1;
+    if (!q4_gemm_swiglu_fits(M, N, K, WT_Q4_0)) return 1;
+    const int rc = q4_gemm_swiglu((const uint8_t*) d_stripes, (const uint8_t*) d_xa, M, N, K, d_h, (uint8_t*) d_xo,
+                                  (hipStream_t) stream, WT_Q4_0);
+    return rc == 1 && hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 extern "C" size_t snk_q8_workspace_bytes(int M, int N, int K) { return q4_workspace_bytes(M, N, K, WT_Q8_0); }
 
 extern "C" int snk_q8_gemm(const void* d_tiles, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi,

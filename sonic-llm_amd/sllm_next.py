@@ -112,6 +112,7 @@ SNK_API = [
     ("snk_q4_workspace_bytes", C.c_size_t, [I, I, I]),
     ("snk_q4_plan", I, [I, I, I, C.POINTER(I), C.POINTER(I)]),
     ("snk_q4_gemm", I, [P, P, I, I, I, P, I, I, P, C.c_size_t, P]),
+    ("snk_q4_gemm_swiglu", I, [P, P, I, I, I, P, P, P]),
     ("snk_q4_gemm_noalloc", I, [P, P, I, I, I, P, I, I, P, CH, I]),
     ("snk_q4_gemm_time", C.c_double, [P, I, P, I, I, I, P, I, P, C.c_size_t, I, P]),
     ("snk_q4_gemm_plan_time", C.c_double, [P, I, P, I, I, I, P, C.c_size_t, I, I, I, I, P]),

@@ -189,6 +189,33 @@ def test_row_invariance_prompt_shapes(N, K):
     assert np.all(np.abs(full[:4] - ref) <= ATOL + RTOL * np.abs(ref))
 
 
+def test_prompt_gate_up_swiglu_epilogue():
+    """Prompt rows of an interleaved gate|up matrix with the SwiGLU + Q8_0 as the matmul's epilogue
+    (snk_q4_gemm_swiglu): the fp32 rows and the down projection's operand are bit for bit the matmul with its SwiGLU
+    output (snk_q4_gemm, epilogue 2) and the activation quantizer over those rows (snk_quant_act); below 256 rows the
+    call declines (1) and launches nothing."""
+    r = np.random.default_rng(12)
+    F, K, M = 3072, 2560, 300
+    N = 2 * F
+    Wq = O.quantize_q4_0(r.normal(0, 0.02, (N, K)).astype(np.float32))
+    X = r.normal(0, 1, (M, K)).astype(np.float32)
+    L = S.lib()
+    st = U.stream()
+    wbuf = U.empty(L.snk_q4_stripes_bytes(N, K))
+    assert L.snk_q4_repack(U.ptr(U.dev(Wq)), N, K, U.ptr(wbuf), st) == 0
+    Y, xa = gemm_gpu(None, N, K, X, epi=2, wbuf=wbuf)  # silu(gate) * up through the split-free launch and reduction
+    dxa = U.dev(xa)
+    h = U.dev(np.zeros((M, F), np.float32))
+    xo = U.dev(np.zeros(L.snk_xa_bytes(M, F), np.uint8))
+    assert L.snk_q4_gemm_swiglu(U.ptr(wbuf), U.ptr(dxa), M, N, K, U.ptr(h), U.ptr(xo), st) == 0
+    gh = U.host(h, np.float32)[:M * F].reshape(M, F)
+    assert np.array_equal(gh.view(np.uint32), Y.view(np.uint32))
+    ref_xo = U.dev(np.zeros(L.snk_xa_bytes(M, F), np.uint8))
+    assert L.snk_quant_act(U.ptr(U.dev(Y)), M, F, F, None, 0.0, U.ptr(ref_xo), st) == 0
+    assert np.array_equal(U.host(xo, np.uint8), U.host(ref_xo, np.uint8))
+    assert L.snk_q4_gemm_swiglu(U.ptr(wbuf), U.ptr(dxa), 200, N, K, U.ptr(h), U.ptr(xo), st) == 1
+
+
 @pytest.fixture(scope="module")
 def lm_head():
     """The Qwen3-4B LM head's shape (configs[2..4]: V = 151,936 rows of K = 2560), seeded N(0, 0.02) weights quantized
