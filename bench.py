@@ -108,7 +108,8 @@ def main():
     ap.add_argument("--model", default=None, help="GGUF path (generated when missing)")
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--config", default="all", choices=("all", "decode", "mtp", "moe", "matmul", "attn", "prefill"),
-                    help="all (default): the headline (configs[2]) with configs[0], [1], [3], [4] inside its line; "
+                    help="all (default): the headline (configs[2]) with configs[0], [1], [3], [4] and the prompt "
+                         "rows inside its line; "
                          "decode: the headline alone; mtp: the fused draft-verify step (configs[3]); "
                          "moe: Qwen3-30B-A3B-arch batched decode (configs[4]); matmul: one 8 x 4096 x 4096 Q4_0 "
                          "matmul (configs[0]); attn: one layer of paged decode attention (configs[1]); prefill: "
@@ -118,8 +119,9 @@ def main():
                     help="matmul: configs[0] (c1, the default) or one of the 32-row decode step's matrices")
     ap.add_argument("--no-graphs", action="store_true", help="launch every step eagerly (no HIP graph replay)")
     ap.add_argument("--no-chain", action="store_true", help="decode without sn_step's queued successor (chain = 0)")
-    ap.add_argument("--attn-mode", type=int, default=-1, choices=(-1, 0, 1),
-                    help="attention work list: -1 chosen per step, 0 per-chunk + merge, 1 whole groups")
+    ap.add_argument("--attn-mode", type=int, default=-1, choices=(-1, 0, 1, 2),
+                    help="attention work list: -1 chosen per step, 0 per-chunk + merge, 1 whole groups, 2 run items "
+                         "for prompt rows wherever possible")
     ap.add_argument("--wtype", type=int, default=2, choices=(2, 8),
                     help="decode / moe: the model's matrices in Q4_0 (2, the configs) or Q8_0 (8)")
     ap.add_argument("--table", default="f32", choices=("f32", "q6k-tied"),
@@ -163,7 +165,7 @@ def main():
     log(f"[bench] gemm shapes in {time.time() - t:.1f}s")
     line["configs"] = {}
     for name, fn in (("c1_matmul", bench_matmul), ("c2_attn", bench_attn), ("c4_mtp", bench_mtp),
-                     ("c5_moe", lambda a: bench_decode(a, moe=True))):
+                     ("c5_moe", lambda a: bench_decode(a, moe=True)), ("f1_prefill", bench_prefill)):
         t = time.time()
         try:
             line["configs"][name] = fn(args)
@@ -444,12 +446,14 @@ def bench_prefill(args):
     layer = (H + 2 * KVH) * 128 * E + E * H * 128 + 2 * F * E + E * F
     flop = 2.0 * rows * layer * cfg["n_layer"] + 2.0 * E * cfg["n_vocab"]
     g = kernels.get("gemm")
-    roof_mfma = {"kernel": "k_q4_gemm", "bound": "mfma", "achieved": round(flop / (g["ms_per_step"] * 1e-3) / 1e12, 1),
+    roof_mfma = {"kernel": "k_q4_gemm / k_q4_gemm_fk2 (the full-K walk)", "bound": "mfma", "achieved": round(flop / (g["ms_per_step"] * 1e-3) / 1e12, 1),
                  "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
                  "frac": round(flop / (g["ms_per_step"] * 1e-3) / MFMA_F16_PEAK, 4),
                  "traffic": profile_traffic("prefill_qwen3_4b_2048_rows512_traffic.json", "k_q4_gemm"),
                  "flop_per_launch": round(flop / g["launches_per_step"]),
-                 "us_per_launch": g["us_per_launch"]} if g else None
+                 "us_per_launch": g["us_per_launch"],
+                 "mfma_busy": profile_value("prefill_qwen3_4b_2048_rows512_traffic.json",
+                                            ("gemm_mfma_busy", "gemm_valu_per_mfma"))} if g else None
     cpu = None
     if not args.no_cpu:
         from oracle import oracle as O
