@@ -415,6 +415,32 @@ def test_attention_list_forms_give_the_same_steps(tiny):
             assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
 
 
+def test_prompt_chunking_does_not_change_the_next_row(tmp_path):
+    """A prompt fed in one step or in several gives the same cells and so the same next row, bit for bit (qbench.m's
+    read_chunks, qbench.m:124-130): 600 prompt rows in one step (the full-K matmul walk and run items at 600 rows),
+    in 200-row steps (the split launches and chunk items), and in 64 + 536, then the same decode row. The model's
+    matrices all split K (n_embd 1024: 2 slices) and its gate|up is wide enough (n_ff 3072: 384 stripes) for the prompt
+    SwiGLU epilogue."""
+    path = str(tmp_path / "w.gguf")
+    S.write_model(path, S.model_cfg(n_layer=2, n_embd=1024, n_head=8, n_head_kv=2, n_ff=3072, n_vocab=1000), seed=13)
+    assert S.q4_plan(2 * 3072, 1024)[1] > 1 and S.q4_plan(1024, 3072)[1] > 1  # (k-slices: the full-K walk applies)
+    r = np.random.default_rng(14)
+    toks = r.integers(0, 1000, 600).astype(np.int32)
+    nxt = np.array([int(r.integers(0, 1000))], np.int32)
+    outs = []
+    for cuts in ([0, 600], [0, 200, 400, 600], [0, 64, 600]):
+        with S.Engine(path, slots=1, ctx=1024, max_rows=600) as eng:
+            for a, b in zip(cuts[:-1], cuts[1:]):
+                eng.step(toks[a:b], np.zeros(b - a, np.int32), np.arange(a, b, dtype=np.int32),
+                         np.array([b - a - 1], np.int32), n_write=0)
+            last = eng.logits([0]).copy()
+            eng.step(nxt, np.zeros(1, np.int32), np.array([600], np.int32), np.array([0], np.int32))
+            outs.append((last, eng.logits([0]).copy()))
+    for other in outs[1:]:
+        assert np.array_equal(outs[0][0].view(np.uint32), other[0].view(np.uint32))
+        assert np.array_equal(outs[0][1].view(np.uint32), other[1].view(np.uint32))
+
+
 def test_chained_steps(tiny):
     """sn_step's chain (sn.h:31-41, sn_step.inc.h:31-212): a write step that samples each row in order has the next
     step queued behind it on the GPU, fed its tokens there. Chained decode gives the same tokens and logits, bit for
