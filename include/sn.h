@@ -84,7 +84,7 @@ int sn_small_rows(const sn_engine* e);               // sn.h:138 — 0 (one matm
 int sn_chat_exact(const sn_engine* e);               // sn.h:142 — 1 (rows are always exact)
 int sn_mark(sn_engine* e, int slot);                 // sn.h:146 — 0
 int sn_state_take(sn_engine* e, int seq);            // sn.h:147 — -1
-int sn_cut_best(const sn_engine* e, int slot, int n);  // sn.h:151 — n
+int sn_cut_best(const sn_engine* e, int slot, int n);  // sn.h:151 — n when sn_cut_ok takes it, 0 for a bad slot or n <= 0
 
 // sn.h:155-158 — the page pool.
 int sn_pages_total(const sn_engine* e);

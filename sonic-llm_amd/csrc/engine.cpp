@@ -1891,10 +1891,11 @@ extern "C" size_t sn_mem_used(const sn_engine* e) {
     return (size_t) (e->n_pages - (int) e->freel.size()) * sn_page_bytes(e);
 }
 extern "C" int sn_cut_ok(const sn_engine* e, int slot, int n) { return slot_ok(e, slot, 0, n) ? 1 : 0; }
+// the most cells of the slot's first n it can be cut back to (sn_cache.inc.h:448-452): n when sn_cut_ok takes it (no
+// recurrent state here), 0 for a bad slot or n <= 0
 extern "C" int sn_cut_best(const sn_engine* e, int slot, int n) {
-    (void) e;
-    (void) slot;
-    return n;
+    if (!e || slot < 0 || slot >= e->slots || n <= 0) return 0;
+    return sn_cut_ok(e, slot, n) ? n : 0;
 }
 extern "C" int sn_recurrent(const sn_engine* e) {
     (void) e;

@@ -240,6 +240,10 @@ def test_row_invariance_copy_and_cut(tiny):
 
 def test_error_paths(tiny):
     with S.Engine(tiny, slots=2, ctx=256, max_rows=16, pages=3) as eng:
+        # sn_cut_best (sn_cache.inc.h:448-452): a bad slot or n <= 0 gives 0, otherwise sn_cut_ok's n
+        L = S.lib()
+        assert (L.sn_cut_best(eng.e, -1, 5), L.sn_cut_best(eng.e, 2, 5), L.sn_cut_best(eng.e, 0, 0)) == (0, 0, 0)
+        assert L.sn_cut_best(eng.e, 1, 10) == 10 and L.sn_cut_ok(eng.e, 1, 10) == 1
         with pytest.raises(S.SnError) as ei:
             eng.step(np.array([1], np.int32), np.array([5], np.int32), np.array([0], np.int32), np.array([0], np.int32))
         assert ei.value.rc == -1
