@@ -295,12 +295,12 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
         qstep = gr.row0 + (qvalid ? qrow : 0);
         qpos = gr.pos0 + qrow;
     }
-    half8 qh[4], ql[4];
-    attn_qfrag_row(a, qstep, qhead, qvalid, g, qh, ql);
     int p_lo, p_hi;
     attn_pages(a, a.pt + (size_t) gr.seq * a.max_pages, cbase, pos_last, p_lo, p_hi);
     u32x4 kf[4][4], vf[2][8];
     attn_issue(a, kvh, cbase, pos_last, p_lo, p_hi, true, n, g, kf, vf);
+    half8 qh[4], ql[4];
+    attn_qfrag_row(a, qstep, qhead, qvalid, g, qh, ql);
     // (a shared chunk lies wholly below every member's position; otherwise the group's first row is its lowest)
     const bool full = shared || cbase + 63 <= gr.pos0;
     float m, l;
@@ -379,8 +379,6 @@ __global__ __launch_bounds__(512) void k_attn_whole(AttnArgs a) {
     const int qrow = n / G, qhead = kvh * G + n % G;
     const bool qvalid = qrow < gr.nrows;
     const int qpos = gr.pos0 + qrow;
-    half8 qh[4], ql[4];
-    attn_qfrag(a, gr, qrow, qhead, qvalid, g, qh, ql);
     const int32_t* ptrow = a.pt + (size_t) gr.seq * a.max_pages;
     const int nch = it.nchunk;
     const int qq = th >> 4, d0 = (th & 15) * 8;
@@ -408,6 +406,8 @@ __global__ __launch_bounds__(512) void k_attn_whole(AttnArgs a) {
         attn_issue_v(a, r0, cb, pl, n, g, vf);
         __builtin_amdgcn_sched_barrier(0);
     }
+    half8 qh[4], ql[4];  // (loaded and split while the first pair's cells are in flight)
+    attn_qfrag(a, gr, qrow, qhead, qvalid, g, qh, ql);
     for (int c0 = 0; c0 < nch; c0 += 2) {  // (uniform trips: every wavefront meets every barrier)
         const int c = c0 + half;
         const bool live = c < nch;
