@@ -1021,7 +1021,7 @@ struct Dev {
     void model(int R, const int32_t* d_tok, const int32_t* d_seq, const int32_t* d_pos, const Stage& S,
                const AttnList& al) {
         const int E = e->E;
-        rc |= e->launch(SNX_K_OTHER, (double) R * E * 8, [&] { embed_rows(e->tok_embd, E, d_tok, R, e->x, st); return 0; });
+        rc |= e->launch(SNX_K_OTHER, (double) R * E * 8, [&] { embed_rows(e->tok_embd, e->V, E, d_tok, R, e->x, st); return 0; });
         bool pending = false;  // x awaits the previous layer's down projection sums
         for (int i = 0; i < e->L && rc == 0; ++i) {
             if (pending) resid(e->x, R, e->ly[i].attn_norm, true);  // x += them, then the attn_norm operand
@@ -1081,8 +1081,8 @@ struct Dev {
         const int E = e->E;
         quant(e->x, nullptr, R, E, e->out_norm, e->mhn);
         rc |= e->launch(SNX_K_OTHER, (double) R * E * 16, [&] {
-            mtp_cat(e->tok_embd, E, d_tok, e->mhn, e->mpend, d_src, d_seq, e->mtp_enorm, e->mtp_hnorm, e->eps, e->mcat, R,
-                    st);
+            mtp_cat(e->tok_embd, e->V, E, d_tok, e->mhn, e->mpend, d_src, d_seq, e->mtp_enorm, e->mtp_hnorm, e->eps,
+                    e->mcat, R, st);
             return 0;
         });
         quant(e->mcat, nullptr, R, 2 * E, nullptr);
@@ -1101,7 +1101,7 @@ struct Dev {
                    const AttnList& al, int32_t* d_gout) {
         const int E = e->E;
         rc |= e->launch(SNX_K_OTHER, (double) n * E * 16, [&] {
-            mtp_cat(e->tok_embd, E, d_tok, first ? nullptr : e->mhg, e->mpend, nullptr, d_seq, e->mtp_enorm,
+            mtp_cat(e->tok_embd, e->V, E, d_tok, first ? nullptr : e->mhg, e->mpend, nullptr, d_seq, e->mtp_enorm,
                     e->mtp_hnorm, e->eps, e->mcat, n, st);
             return 0;
         });

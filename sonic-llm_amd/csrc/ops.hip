@@ -5,14 +5,19 @@
 #include "sn_kernels_internal.h"
 
 // ---- embedding: the token's fp32 table row (embed_rows / embed_into, sn_state.inc.h:250-272; the table is fp32 here)
-__global__ void k_embed(const float* __restrict__ table, int E, const int32_t* __restrict__ tok, float* __restrict__ x) {
-    const int r = blockIdx.x;
-    const float* src = table + (size_t) tok[r] * E;
-    for (int i = threadIdx.x; i < E; i += blockDim.x) x[(size_t) r * E + i] = src[i];
+// Token ids come from the host (checked there) or from an argmax on the GPU (a queued step's tokens, the guess head's
+// drafts), which gives -1 for a row without a finite score (all NaN): an id outside [0, V) makes a zero row, read from
+// nowhere, so such a row is garbage but never an access out of the table.
+__global__ void k_embed(const float* __restrict__ table, int V, int E, const int32_t* __restrict__ tok,
+                        float* __restrict__ x) {
+    const int r = blockIdx.x, id = tok[r];
+    const bool ok = id >= 0 && id < V;
+    const float* src = table + (size_t) (ok ? id : 0) * E;
+    for (int i = threadIdx.x; i < E; i += blockDim.x) x[(size_t) r * E + i] = ok ? src[i] : 0.0f;
 }
 
-void embed_rows(const float* table, int E, const int32_t* tok, int R, float* x, hipStream_t st) {
-    if (R > 0) hipLaunchKernelGGL(k_embed, dim3(R), dim3(256), 0, st, table, E, tok, x);
+void embed_rows(const float* table, int V, int E, const int32_t* tok, int R, float* x, hipStream_t st) {
+    if (R > 0) hipLaunchKernelGGL(k_embed, dim3(R), dim3(256), 0, st, table, V, E, tok, x);
 }
 
 // ---- QK-norm + RoPE + K/V into the cache (qk_rope, kernels.metal:149-197) -------------------------------------------
@@ -343,21 +348,24 @@ __device__ __forceinline__ float row_sumsq256(const float* x, int n, float* red)
 // 256 MTP_CAT_J) are loaded before either sum of squares is reduced: one latency period, not two; each sum keeps the
 // per-thread order and reduction of row_sumsq256.
 #define MTP_CAT_J 16
-__global__ __launch_bounds__(256) void k_mtp_cat(const float* __restrict__ table, int E, const int32_t* __restrict__ tok,
+__global__ __launch_bounds__(256) void k_mtp_cat(const float* __restrict__ table, int V, int E,
+                                                 const int32_t* __restrict__ tok,
                                                  const float* __restrict__ hrows, const float* __restrict__ pend,
                                                  const int32_t* __restrict__ src, const int32_t* __restrict__ seq,
                                                  const float* __restrict__ enorm, const float* __restrict__ hnorm,
                                                  float eps, float* __restrict__ cat) {
     __shared__ float red[2][4];
     const int r = blockIdx.x, t = threadIdx.x;
-    const float* em = table + (size_t) tok[r] * E;
+    const int id = tok[r];
+    const bool tok_ok = id >= 0 && id < V;  // (an id outside [0, V): a zero embedding, as in k_embed)
+    const float* em = table + (size_t) (tok_ok ? id : 0) * E;
     const int s = src ? src[r] : (hrows ? r : -1);
     const float* h = s >= 0 ? hrows + (size_t) s * E : s == -1 ? pend + (size_t) seq[r] * E : nullptr;
     float* y = cat + (size_t) r * 2 * E;
     float ve[MTP_CAT_J], vh[MTP_CAT_J];
     for (int j = 0; j < MTP_CAT_J; ++j) {
         const int i = t + 256 * j;
-        ve[j] = i < E ? em[i] : 0.0f;
+        ve[j] = tok_ok && i < E ? em[i] : 0.0f;
         vh[j] = h && i < E ? h[i] : 0.0f;
     }
     float se = 0.0f, sh = 0.0f;
@@ -385,11 +393,12 @@ __global__ __launch_bounds__(256) void k_mtp_cat(const float* __restrict__ table
     }
 }
 
-void mtp_cat(const float* table, int E, const int32_t* tok, const float* hrows, const float* pend, const int32_t* src,
-             const int32_t* seq, const float* enorm, const float* hnorm, float eps, float* cat, int R, hipStream_t st) {
+void mtp_cat(const float* table, int V, int E, const int32_t* tok, const float* hrows, const float* pend,
+             const int32_t* src, const int32_t* seq, const float* enorm, const float* hnorm, float eps, float* cat,
+             int R, hipStream_t st) {
     if (R > 0 && E <= 256 * MTP_CAT_J)
-        hipLaunchKernelGGL(k_mtp_cat, dim3(R), dim3(256), 0, st, table, E, tok, hrows, pend, src, seq, enorm, hnorm, eps,
-                           cat);
+        hipLaunchKernelGGL(k_mtp_cat, dim3(R), dim3(256), 0, st, table, V, E, tok, hrows, pend, src, seq, enorm, hnorm,
+                           eps, cat);
 }
 
 // keep[j] = (slot, row): dst row `slot` = src row `row` (mtp_keep: a slot's last hidden state of the step)
@@ -419,7 +428,7 @@ __global__ void k_spec_rows(int n, int k, int slots, const int32_t* __restrict__
 __global__ void k_force(float* __restrict__ logits, int V, int R, const uint8_t* __restrict__ force,
                         const int32_t* __restrict__ ftok) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r < R && force[r]) logits[(size_t) r * V + ftok[r]] = 3.0e38f;
+    if (r < R && force[r] && ftok[r] >= 0 && ftok[r] < V) logits[(size_t) r * V + ftok[r]] = 3.0e38f;
 }
 
 // Greedy acceptance (next_engine/take.rs:339-357) per sequence: a = the leading drafts equal to their row's argmax;

@@ -183,7 +183,8 @@ void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, in
                int mode = -1, const int32_t* pt = nullptr, int max_pages = 0);
 
 // ---- elementwise / row kernels ----
-void embed_rows(const float* table, int E, const int32_t* tok, int R, float* x, hipStream_t st);
+// (a token id outside [0, V) gives a zero row)
+void embed_rows(const float* table, int V, int E, const int32_t* tok, int R, float* x, hipStream_t st);
 // q|k|v rows: from qkv (part NULL) or from the q|k|v matmul's k-slice sums part[ks][R][(H + 2 KVH) 128], which are
 // then also written to qkv (k and v as summed, q after QK-norm and RoPE); k and v go to the rows' cache cells.
 void qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, int H, int KVH, const float* qw,
@@ -212,8 +213,9 @@ int argmax_rows(const float* logits, int V, int n, const int32_t* ban, int nban,
 // ---- the guess head (MTP) and the fused draft-verify step
 // [enorm(embed(tok)); hnorm(h)] rows into cat [R][2E]; h: src NULL: hrows row r (hrows given) or pend[seq[r]];
 // src[r] >= 0: hrows row src[r], -1: pend[seq[r]], -2: zeros
-void mtp_cat(const float* table, int E, const int32_t* tok, const float* hrows, const float* pend, const int32_t* src,
-             const int32_t* seq, const float* enorm, const float* hnorm, float eps, float* cat, int R, hipStream_t st);
+void mtp_cat(const float* table, int V, int E, const int32_t* tok, const float* hrows, const float* pend,
+             const int32_t* src, const int32_t* seq, const float* enorm, const float* hnorm, float eps, float* cat,
+             int R, hipStream_t st);
 // keep [n][2] = (slot, row): dst[slot] = src[row] (E floats); slot < 0 skips
 void rows_keep(const float* src, const int32_t* keep, int n, int E, float* dst, hipStream_t st);
 // verify rows of n sequences x (k + 1) from the drafts gtok [k][slots]: vtok rows i > 0, ftok (row i < k: draft i)
