@@ -89,7 +89,7 @@ __device__ __forceinline__ void attn_issue_k(const AttnArgs& a, const AttnRsrc& 
     for (int jg = 0; jg < 4; ++jg) {
         const int c = cbase + 16 * jg + n;
         const int off = c <= pos_last ? (c & (pc - 1)) * (ATT_D * 2) + 16 * g : ATT_OOB;
-        for (int t = 0; t < 4; ++t) kf[jg][t] = bload16(jg < 2 ? r.k0 : r.k1, off, 64 * t);
+        for (int t = 0; t < 4; ++t) kf[jg][t] = bload16nt(jg < 2 ? r.k0 : r.k1, off, 64 * t);
     }
 }
 __device__ __forceinline__ void attn_issue_v(const AttnArgs& a, const AttnRsrc& r, int cbase, int pos_last, int n,
@@ -100,7 +100,7 @@ __device__ __forceinline__ void attn_issue_v(const AttnArgs& a, const AttnRsrc& 
             for (int v = 0; v < 4; ++v) {
                 const int c = cbase + 32 * st + 16 * jj + 4 * g + v;
                 const int off = c <= pos_last ? (c & (pc - 1)) * (ATT_D * 2) + 16 * n : ATT_OOB;
-                vf[st][4 * jj + v] = bload16(st == 0 ? r.v0 : r.v1, off, 0);
+                vf[st][4 * jj + v] = bload16nt(st == 0 ? r.v0 : r.v1, off, 0);
             }
 }
 __device__ __forceinline__ void attn_issue(const AttnArgs& a, int kvh, int cbase, int pos_last, int p_lo, int p_hi,
