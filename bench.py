@@ -107,13 +107,15 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--model", default=None, help="GGUF path (generated when missing)")
     ap.add_argument("--seed", type=int, default=42)
-    ap.add_argument("--config", default="all", choices=("all", "decode", "mtp", "moe", "matmul", "attn", "prefill"),
+    ap.add_argument("--config", default="all",
+                    choices=("all", "decode", "mtp", "moe", "matmul", "attn", "prefill", "fewrows"),
                     help="all (default): the headline (configs[2]) with configs[0], [1], [3], [4] and the prompt "
                          "rows inside its line; "
                          "decode: the headline alone; mtp: the fused draft-verify step (configs[3]); "
                          "moe: Qwen3-30B-A3B-arch batched decode (configs[4]); matmul: one 8 x 4096 x 4096 Q4_0 "
                          "matmul (configs[0]); attn: one layer of paged decode attention (configs[1]); prefill: "
-                         "2048-token prompts in 512-row steps")
+                         "2048-token prompts in 512-row steps; fewrows: the MFMA matmul against the per-column "
+                         "integer-dot GEMV at 1-8 rows on the decode step's matrices and configs[0]")
     ap.add_argument("--accept", type=float, default=0.6, help="mtp: the seeded share of drafts forced to match")
     ap.add_argument("--mm-shape", default="c1", choices=("c1",) + tuple(DECODE_SHAPES),
                     help="matmul: configs[0] (c1, the default) or one of the 32-row decode step's matrices")
@@ -146,7 +148,8 @@ def main():
               f"across GPUs with no per-step exchange; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
 
-    subs = {"mtp": bench_mtp, "matmul": bench_matmul, "attn": bench_attn, "prefill": bench_prefill}
+    subs = {"mtp": bench_mtp, "matmul": bench_matmul, "attn": bench_attn, "prefill": bench_prefill,
+            "fewrows": bench_fewrows}
     if args.config in subs:
         print(json.dumps(subs[args.config](args)), flush=True)
         return
@@ -707,6 +710,62 @@ def matmul_shape(M, N, K, seed, copies=None, Wq=None):
     del tiles
     torch.cuda.empty_cache()
     return out
+
+
+def bench_fewrows(args):
+    """The matmul at few rows (1, 2, 4, 8): the default MFMA launch against the per-column integer-dot GEMV (the
+    north star's mat-vec design; snk_q4_gemm_plan_time with mt 0, at most 4 rows), both with the default plan's
+    slices and the same bits, average launch time with weight copies in turn beyond the Infinity Cache. The line's
+    value is the geometric mean of GEMV / MFMA time over the shapes and row counts the GEMV takes (below 1: the GEMV
+    is faster)."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    import sllm_next as S
+
+    U = Dev
+    L = S.lib()
+    st = U.stream()
+    r = np.random.default_rng(1)
+    shapes = dict(c1=(4096, 4096), **{k: v[1:] for k, v in DECODE_SHAPES.items()})
+    res, ratios = {}, []
+    for name, (N, K) in shapes.items():
+        nb = min(N, 8192)
+        Wq = S.quantize_q4_0((r.standard_normal((nb, K)) * 0.02).astype(np.float32))
+        Wq = np.ascontiguousarray(np.tile(Wq, ((N + nb - 1) // nb, 1))[:N])
+        sb = L.snk_q4_stripes_bytes(N, K)
+        copies = max(2, int(np.ceil(600e6 / sb)))
+        dW = U.copy(Wq)
+        tiles = [U.empty(sb) for _ in range(copies)]
+        for t in tiles:
+            assert L.snk_q4_repack(U.ptr(dW), N, K, U.ptr(t), st) == 0
+        ptrs = C.cast((C.c_void_p * copies)(*[t.data_ptr() for t in tiles]), C.c_void_p)
+        res[name] = {"N": N, "K": K}
+        for M in (1, 2, 4, 8):
+            X = r.standard_normal((M, K)).astype(np.float32)
+            xa = U.empty(L.snk_xa_bytes(M, K))
+            assert L.snk_quant_act(U.ptr(U.copy(X)), M, K, K, None, C.c_float(0.0), U.ptr(xa), st) == 0
+            wsb = L.snk_q4_workspace_bytes(M, N, K)
+            ws = U.empty(wsb)
+            torch.cuda.synchronize()
+            t_m = L.snk_q4_gemm_plan_time(ptrs, copies, U.ptr(xa), M, N, K, U.ptr(ws), C.c_size_t(wsb), 1, 1, 0, 100, st)
+            row = {"mfma_us": round(t_m, 2)}
+            if M <= 4:
+                t_v = L.snk_q4_gemm_plan_time(ptrs, copies, U.ptr(xa), M, N, K, U.ptr(ws), C.c_size_t(wsb), 0, 0, 0,
+                                              100, st)
+                row["gemv_us"] = round(t_v, 2)
+                ratios.append(t_v / t_m)
+            res[name][f"M{M}"] = row
+            log(f"[bench] fewrows {name} M={M}: {row}")
+        del tiles
+        torch.cuda.empty_cache()
+    gm = float(np.exp(np.mean(np.log(ratios))))
+    return {"metric": "few-row Q4_0 matmul: per-column integer-dot GEMV time / MFMA time (geometric mean)",
+            "value": round(gm, 4), "unit": "ratio", "n_gpus": 1, "higher_is_better": False, "vs_baseline": None,
+            "dtype": "q4_0 x q8_0 -> f32 (both kernels: the same bits)", "data": "synthetic: seeded weights, rows",
+            "config": {"workload": "decode step matrices and configs[0] at 1-8 rows", "shapes": res}}
 
 
 def bench_matmul(args):

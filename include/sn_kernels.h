@@ -89,7 +89,8 @@ double snk_read_time(const void* const* d_bufs, int n_copies, size_t bytes, floa
 
 // Launch-plan tuning of the matmul (raw k-slice sums of Q4_0 stripes): an explicit plan of mt row tiles a workgroup
 // (1, 2), spw stripes a wavefront (1, 2) and G groups a slice with every load of the slice issued at once (G 0: the
-// default plan). snk_q4_gemm_plan_time: average device time (microseconds) of one launch over `iters` launches on
+// default plan; mt 0, spw 0, G 0: the per-column integer-dot GEMV of M <= 4 rows, with the default plan's slices and
+// the same bits). snk_q4_gemm_plan_time: average device time (microseconds) of one launch over `iters` launches on
 // `stream`, weights from n_copies stripe copies in turn; -1 for a plan that is not instantiated or too small a
 // workspace. snk_q4_gemm_plan_sums: the plan's slices added in order into d_y [M][N], for checking a plan; 0 or -1.
 double snk_q4_gemm_plan_time(const void* const* d_stripes, int n_copies, const void* d_xa, int M, int N, int K,

@@ -681,6 +681,120 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     }
 }
 
+// The few-row matmul (M <= 4 rows: the reference's mat-vec rows, mv_q4, kernels.metal:1324-1411). One lane per output
+// column: a wavefront takes 4 stripes (64 columns), a workgroup 16, and the plan's k-slices go across workgroups as
+// the MFMA kernels split them. The slice's activation rows are staged once into LDS as int8 (from the operand's fp16
+// fragments: q, and q / 16 for elements 16..31) with each block's sum of q. A lane loads its column's 64 bytes of a
+// tile (its row's 16 bytes at each of the 4 lane positions of the tile: 4 bytes of each of the 4 blocks), unpacks the
+// nibbles with a mask and a shift and sums a block with 8 v_dot4 per row: isum = sum q w - 8 sum q = sum q (w - 8),
+// the integer the MFMA kernels form; then acc = fma(isum, dw * dx, acc) block by block in the slice's order, a slice
+// with an odd group count padded with a zero-scale group as the MFMA kernels' rings pad it. So every sum is the MFMA
+// kernels' fp32 bits, and part[slice][M][N] is what their consumers expect. D groups of weights in flight a wavefront.
+#define GEMV_GMAX 32  // groups of a slice the staging holds
+#define GEMV_ROWS 0   // steps of at most this many rows take the GEMV by default (the MFMA kernels otherwise)
+template <int MR, int D>
+__global__ __launch_bounds__(256) void k_q4_gemv(GemmArgs a) {
+    constexpr int TB = Q4T_BYTES, SO = Q4T_SCALE_OFF;
+    constexpr int NIT = MR * GEMV_GMAX * 16 / 256;  // staging items (row, block, lane part) a thread
+    constexpr int NDX = (MR * GEMV_GMAX * 4 + 255) / 256;  // block scales a thread stages
+    __shared__ __attribute__((aligned(16))) uint32_t s_q[MR][GEMV_GMAX * 4][8];  // int8 q of (row, block)
+    __shared__ float s_dx[MR][GEMV_GMAX * 4];
+    __shared__ int32_t s_sx[MR][GEMV_GMAX * 4];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, sl = lane >> 4;
+    const int set = blockIdx.x, slice = blockIdx.y;
+    const int c0 = slice * a.gps, ng = __builtin_amdgcn_readfirstlane(min(a.gps, a.ngroups - c0));
+    const int ngp = (ng + 1) & ~1;  // the groups summed: the slice's, an odd count padded with a zero-scale group
+    const int nb = 4 * ng;          // blocks of the slice
+    const int s0 = set * 16 + wave * 4;
+    const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(4, a.nstripes - s0)));
+    const int sbytes = a.ngroups * TB;
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(a.w + (size_t) min(s0, a.nstripes - 1) * sbytes, (uint32_t) (nvalid * sbytes));
+    const int vst = sl * sbytes;  // this lane's stripe
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xa, (uint32_t) xa_bytes(a.M, a.K));
+    // the staging loads first (item (m, block, part g): the 8 fp16 of row m's fragment piece g), then the weights
+    u32x4 rq[NIT];
+    float rdx[NDX];
+    for (int j = 0; j < NIT; ++j) {
+        const int it = min((int) threadIdx.x + 256 * j, MR * nb * 4 - 1), g = it & 3, b = (it >> 2) % nb, m = (it >> 2) / nb;
+        rq[j] = bload16(xr, 16 * (m + 16 * g), (c0 + b / 4) * XA_REC + (b % 4) * 1024);
+    }
+    for (int j = 0; j < NDX; ++j) {
+        const int it = min((int) threadIdx.x + 256 * j, MR * nb - 1), b = it % nb, m = it / nb;
+        rdx[j] = bload4f(xr, 4 * m, (c0 + b / 4) * XA_REC + XA_DX_OFF + (b % 4) * 64);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 wq[D][4];
+    u32x2 ws[D];
+    auto load = [&](int slot, int i) {  // group i of the slice (past it: its last group again)
+        const int so = (c0 + min(i, ng - 1)) * TB;
+        for (int g = 0; g < 4; ++g) wq[slot][g] = bload16(wr, vst + 16 * (n + 16 * g), so);
+        ws[slot] = bload8(wr, vst + SO + 8 * n, so);
+    };
+    for (int j = 0; j < D; ++j) {
+        load(j, j);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int j = 0; j < NIT; ++j) {
+        const int it = (int) threadIdx.x + 256 * j;  // (the item count is a multiple of 4: the 4 parts of a block
+        const bool ok = it < MR * nb * 4;              // are adjacent lanes, all in or all out)
+        const int g = it & 3, b = (it >> 2) % nb, m = (it >> 2) / nb;
+        const half8 h = __builtin_bit_cast(half8, rq[j]);
+        int q[8];
+        for (int e = 0; e < 4; ++e) q[e] = (int) (float) h[e];
+        for (int e = 4; e < 8; ++e) q[e] = (int) ((float) h[e] * 16.0f);
+        int sx = q[0] + q[1] + q[2] + q[3] + q[4] + q[5] + q[6] + q[7];
+        sx += __shfl_xor(sx, 1);
+        sx += __shfl_xor(sx, 2);
+        if (ok) {
+            s_q[m][b][g] = (q[0] & 255) | (q[1] & 255) << 8 | (q[2] & 255) << 16 | (uint32_t) (q[3] & 255) << 24;
+            s_q[m][b][4 + g] = (q[4] & 255) | (q[5] & 255) << 8 | (q[6] & 255) << 16 | (uint32_t) (q[7] & 255) << 24;
+            if (g == 0) s_sx[m][b] = sx;
+        }
+    }
+    for (int j = 0; j < NDX; ++j) {
+        const int it = (int) threadIdx.x + 256 * j;
+        if (it < MR * nb) s_dx[it / nb][it % nb] = rdx[j];
+    }
+    __syncthreads();
+
+    const int M = min(a.M, MR);
+    float acc[MR];
+    for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
+    const int trips = (ngp + D - 1) / D;
+    for (int tr = 0; tr < trips; ++tr)
+        for (int j = 0; j < D; ++j) {
+            const int i = tr * D + j;
+            const float msc = i < ng ? 1.0f : 0.0f;  // (the padding group adds with scale 0)
+            const bool live = i < ngp;               // (groups past the padded count: computed, not added)
+            const int lb = 4 * min(i, ng - 1);       // (its blocks in LDS)
+            __builtin_amdgcn_sched_barrier(0);
+            for (int b = 0; b < 4; ++b) {
+                uint32_t wl[4], wh[4];
+                for (int g = 0; g < 4; ++g) {
+                    wl[g] = wq[j][g][b] & 0x0F0F0F0Fu;
+                    wh[g] = (wq[j][g][b] >> 4) & 0x0F0F0F0Fu;
+                }
+                const float dw = (float) __builtin_bit_cast(half4v, ws[j])[b] * msc;
+                for (int m = 0; m < MR; ++m) {
+                    const u32x4 q0 = *(const u32x4*) &s_q[m][lb + b][0], q1 = *(const u32x4*) &s_q[m][lb + b][4];
+                    int isum = 0;
+                    for (int g = 0; g < 4; ++g) isum = __builtin_amdgcn_sdot4((int) q0[g], (int) wl[g], isum, false);
+                    for (int g = 0; g < 4; ++g) isum = __builtin_amdgcn_sdot4((int) q1[g], (int) wh[g], isum, false);
+                    isum -= 8 * s_sx[m][lb + b];
+                    const float v = __builtin_fmaf((float) isum, dw * s_dx[m][lb + b], acc[m]);
+                    acc[m] = live ? v : acc[m];
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load(j, i + D);
+        }
+    const int stripe = s0 + sl, col = stripe * 16 + n;
+    if (sl < nvalid && col < a.N)
+        for (int m = 0; m < MR; ++m)
+            if (m < M) a.part[((size_t) slice * a.M + m) * a.N + col] = acc[m];
+}
+
 // k-slice partial sums added in slice order, then the epilogue
 __global__ void k_q4_reduce(GemmArgs a) {
     const int outN = a.epi == EPI_SWIGLU ? a.N / 2 : a.N;
@@ -786,6 +900,16 @@ static bool launch_gemm_s(int mt, int spw, int D, int gps, dim3 grid, const Gemm
     return false;
 }
 
+// The per-column GEMV (k_q4_gemv) of M <= 4 rows with the plan's slices; false when it does not take the shape.
+static bool launch_gemv(const GemmPlan& p, const GemmArgs& a, hipStream_t st) {
+    if (a.M < 1 || a.M > 4 || p.gps > GEMV_GMAX) return false;
+    const dim3 grid((p.nstripes + 15) / 16, p.ks);
+    if (a.M == 1) hipLaunchKernelGGL((k_q4_gemv<1, 4>), grid, dim3(256), 0, st, a);
+    else if (a.M == 2) hipLaunchKernelGGL((k_q4_gemv<2, 4>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_q4_gemv<4, 4>), grid, dim3(256), 0, st, a);
+    return true;
+}
+
 int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
                 hipStream_t st, int wt) {
     if (M <= 0) return 0;
@@ -797,6 +921,7 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
     a.M = M; a.N = N; a.K = K; a.ldy = 0; a.epi = EPI_STORE;
     a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
     a.mtiles = (M + 15) / 16;
+    if (wt == WT_Q4_0 && M <= GEMV_ROWS && launch_gemv(p, a, st)) return p.ks;  // few rows: the per-column GEMV
     if (p.stream && a.M < Q4_PAIR_ROWS) {  // the streaming kernel (ring depth 2)
         const int mt = std::min(p.smt, a.mtiles);
         const dim3 grid((p.nstripes + 4 * p.sspw - 1) / (4 * p.sspw), p.ks, (a.mtiles + mt - 1) / mt);
@@ -843,6 +968,15 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
 // k-slice sums go to part. Returns the slice count, or -1 (a plan not instantiated, or part too small).
 int q4_gemm_raw_plan(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
                      hipStream_t st, int wt, int mt, int spw, int G) {
+    if (mt == 0) {  // the per-column GEMV with the default plan's slices (Q4_0, M <= 4)
+        const GemmPlan p = q4_plan(N, K, wt);
+        if (wt != WT_Q4_0 || G != 0 || part == nullptr || part_bytes < (size_t) p.ks * M * N * sizeof(float)) return -1;
+        GemmArgs a{};
+        a.w = w; a.xa = xa; a.part = part;
+        a.M = M; a.N = N; a.K = K; a.epi = EPI_STORE;
+        a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps; a.mtiles = (M + 15) / 16;
+        return launch_gemv(p, a, st) ? p.ks : -1;
+    }
     if (G == 0) return q4_gemm_raw(w, xa, M, N, K, part, part_bytes, st, wt);
     if (G > 0) return -1;
     const int gps = (-G) % 100, D = (-G) / 100;

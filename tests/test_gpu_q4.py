@@ -248,3 +248,33 @@ def test_lm_head_width_matmul(lm_head, M):
     if M > 1:  # rows from the middle of the batch, alone
         part, _ = gemm_gpu(None, N, K, X[M // 2:M], wbuf=wbuf)
         assert np.array_equal(part.view(np.uint32), full[M // 2:M].view(np.uint32))
+
+
+@pytest.mark.parametrize("N,K", [(6144, 2560), (19456, 2560), (2560, 9728), (200, 640), (98304, 2560)])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_gemv_equals_mfma_bitwise(M, N, K):
+    """The per-column integer-dot GEMV for few rows (snk_q4_gemm_plan_* with mt 0: 8 v_dot4 a block and row, then the
+    MFMA kernels' fma(isum, dw * dx, acc) in the same order) against the default MFMA launch of the same plan: the
+    same slice sums, bit for bit. Shapes: q|k|v (4-group slices), gate|up and down (8-group slices, a short last one),
+    200 x 640 (a partial stripe set, a one-group last slice padded with a zero-scale group) and a wide matrix with the
+    LM head's plan (one 20-group slice)."""
+    L = S.lib()
+    st = U.stream()
+    r = np.random.default_rng(100 + M + N)
+    nb = min(N, 4096)
+    Wq = O.quantize_q4_0(r.normal(0, 0.02, (nb, K)).astype(np.float32))
+    Wq = np.ascontiguousarray(np.tile(Wq, ((N + nb - 1) // nb, 1))[:N])
+    wbuf = U.empty(L.snk_q4_stripes_bytes(N, K))
+    assert L.snk_q4_repack(U.ptr(U.dev(Wq)), N, K, U.ptr(wbuf), st) == 0
+    X = r.normal(0, 1, (M, K)).astype(np.float32)
+    X[0, :32] = 0.0  # an all-zero block
+    xa = U.empty(L.snk_xa_bytes(M, K))
+    assert L.snk_quant_act(U.ptr(U.dev(X)), M, K, K, None, 0.0, U.ptr(xa), st) == 0
+    wsb = L.snk_q4_workspace_bytes(M, N, K)
+    out = []
+    for mt in (1, 0):
+        y, ws = U.empty(M * N * 4), U.empty(wsb)
+        assert L.snk_q4_gemm_plan_sums(U.ptr(wbuf), U.ptr(xa), M, N, K, U.ptr(y), U.ptr(ws), wsb, mt, mt, 0, st) == 0
+        out.append(U.host(y, np.float32)[:M * N].reshape(M, N))
+    assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
+    assert np.count_nonzero(out[1]) > M * N // 2
