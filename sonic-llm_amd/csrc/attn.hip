@@ -83,15 +83,17 @@ __device__ __forceinline__ AttnRsrc attn_rsrc(const AttnArgs& a, int kvh, int p_
     r.v1 = buf_rsrc(a.vpool + ((size_t) p_hi * a.KVH + kvh) * head_stride, hb);
     return r;
 }
+template <int CPOL = 2>  // the loads' cache policy: nt (cells read once a step), 0 for run items (cells read again)
 __device__ __forceinline__ void attn_issue_k(const AttnArgs& a, const AttnRsrc& r, int cbase, int pos_last, int n,
                                              int g, u32x4 (&kf)[4][4]) {
     const int pc = a.page_cells;  // 32 or 64
     for (int jg = 0; jg < 4; ++jg) {
         const int c = cbase + 16 * jg + n;
         const int off = c <= pos_last ? (c & (pc - 1)) * (ATT_D * 2) + 16 * g : ATT_OOB;
-        for (int t = 0; t < 4; ++t) kf[jg][t] = bload16nt(jg < 2 ? r.k0 : r.k1, off, 64 * t);
+        for (int t = 0; t < 4; ++t) kf[jg][t] = bload16nt<CPOL>(jg < 2 ? r.k0 : r.k1, off, 64 * t);
     }
 }
+template <int CPOL = 2>
 __device__ __forceinline__ void attn_issue_v(const AttnArgs& a, const AttnRsrc& r, int cbase, int pos_last, int n,
                                              int g, u32x4 (&vf)[2][8]) {
     const int pc = a.page_cells;
@@ -100,7 +102,7 @@ __device__ __forceinline__ void attn_issue_v(const AttnArgs& a, const AttnRsrc& 
             for (int v = 0; v < 4; ++v) {
                 const int c = cbase + 32 * st + 16 * jj + 4 * g + v;
                 const int off = c <= pos_last ? (c & (pc - 1)) * (ATT_D * 2) + 16 * n : ATT_OOB;
-                vf[st][4 * jj + v] = bload16nt(st == 0 ? r.v0 : r.v1, off, 0);
+                vf[st][4 * jj + v] = bload16nt<CPOL>(st == 0 ? r.v0 : r.v1, off, 0);
             }
 }
 __device__ __forceinline__ void attn_issue(const AttnArgs& a, int kvh, int cbase, int pos_last, int p_lo, int p_hi,
@@ -518,9 +520,9 @@ __global__ __launch_bounds__(512) void k_attn_run(AttnArgs a) {
     {
         const AttnRsrc r0 = rsrc_of(0, cb, pl);
         __builtin_amdgcn_sched_barrier(0);
-        attn_issue_k(a, r0, cb, pl, n, g, kf);
+        attn_issue_k<0>(a, r0, cb, pl, n, g, kf);
         __builtin_amdgcn_sched_barrier(0);
-        attn_issue_v(a, r0, cb, pl, n, g, vf);
+        attn_issue_v<0>(a, r0, cb, pl, n, g, vf);
         __builtin_amdgcn_sched_barrier(0);
     }
     for (int c0 = 0; c0 < nch; c0 += 2) {  // (uniform trips: every wavefront meets every barrier)
@@ -545,11 +547,11 @@ __global__ __launch_bounds__(512) void k_attn_run(AttnArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             attn_scores(kf, qh, ql, cbase, qvalid && live, gm.pos0 + qrow, g, ml, ll, sc, live && cbase + 63 <= gm.pos0);
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (decltype(last)::value) attn_issue_k(a, rn, ncb, npl, n, g, kf);
+            if constexpr (decltype(last)::value) attn_issue_k<0>(a, rn, ncb, npl, n, g, kf);
             __builtin_amdgcn_sched_barrier(0);
             attn_pv(vf, sc, o);
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (decltype(last)::value) attn_issue_v(a, rn, ncb, npl, n, g, vf);
+            if constexpr (decltype(last)::value) attn_issue_v<0>(a, rn, ncb, npl, n, g, vf);
             __builtin_amdgcn_sched_barrier(0);
             float M, L, acc[8];
             attn_combine(sh.h[half], wave, n, g, gm.nrows * G, ml, ll, o, qq, d0, M, L, acc);

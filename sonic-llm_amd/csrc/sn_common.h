@@ -27,9 +27,11 @@ __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int vo, int s
 // A 16-byte load with the non-temporal hint (cache-policy bit nt = 2): the attention's K/V cells, read once a step.
 // Measured on MI355X: configs[1] 63.3 -> 61.4 us, the decode step's attention 54.3 -> 52.8 us a layer; nt | sc0 the
 // same, sc0 alone slower (63.4 us); the nt hint on the matmuls' weight tiles made them slower (gate|up 2203 -> 2095
-// GB/s), so they load with the default policy.
+// GB/s), so they load with the default policy, and so do the prompt rows' run items, whose items of one sequence read
+// the same cells in turn (their prompt steps: 52.6 against 47.4 us a launch with the hint).
+template <int CPOL = 2>
 __device__ __forceinline__ u32x4 bload16nt(__amdgpu_buffer_rsrc_t r, int vo, int so) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 2));
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, CPOL));
 }
 __device__ __forceinline__ u32x2 bload8(__amdgpu_buffer_rsrc_t r, int vo, int so) {
     return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0));
