@@ -21,12 +21,68 @@ void embed_rows(const float* table, int V, int E, const int32_t* tok, int R, flo
 }
 
 // ---- QK-norm + RoPE + K/V into the cache (qk_rope, kernels.metal:149-197) -------------------------------------------
-// Workgroup (row, y): wavefront w takes head 4 y + w of the row's q heads, k heads and v heads in that order; lane i
-// the dims (i, i + 64), which are a rotation pair for q and k.
-// Per q/k head: RMSNorm over 128 dims with weight w, then y_i = x_i cos - x_{i+64} sin, y_{i+64} = x_i sin +
-// x_{i+64} cos with theta_i = p * s^i formed by i successive fp32 multiplies from p (ggml_rope_cache_init's loop),
-// s = base^(-2/128) computed on the host. q stays in place (fp32); k and v go to the row's cell in fp16 (with part
-// given, k and v as the matmul made them are also written into the row).
+// Lane i of a wavefront takes the dims (i, i + 64) of a head, which are a rotation pair for q and k. The rotation's
+// cos / sin of theta_i = p * s^i (i successive fp32 multiplies from p, ggml_rope_cache_init's loop; s = base^(-2/128)
+// computed on the host) are the same for every head of a row. Per q/k head: RMSNorm over 128 dims with weight w, then
+// y_i = x_i cos - x_{i+64} sin, y_{i+64} = x_i sin + x_{i+64} cos. q stays in place (fp32); k and v go to the row's
+// cell in fp16 (with part given, k and v as the matmul made them are also written into the row). Two launch shapes do
+// the same operations in the same order with contraction off, so a row gets the same bits from either: k_qk_rope, a
+// wavefront a head (the most wavefronts, for decode-sized steps), and k_qk_rope_rows (through rope_cs, qk_load and
+// qk_head), a workgroup a row with the angles formed once and shared through LDS (for prompt-sized steps).
+__device__ __forceinline__ void rope_cs(int p, int lane, float theta_scale, float& c, float& s) {
+#pragma clang fp contract(off)
+    float theta = (float) p;
+    for (int i = 0; i < lane; ++i) theta *= theta_scale;
+    c = cosf(theta);
+    s = sinf(theta);
+}
+// a head's two dims: the q|k|v matmul's k-slice sums (added in slice order) or the row's values
+template <int KM>
+__device__ __forceinline__ void qk_load(const float* __restrict__ qkv, int ldqkv, const float* __restrict__ part, int ks,
+                                        int R, int N, int r, int h, int lane, float& a0, float& a1) {
+    if (part) {
+        a0 = slices_sum1<KM>(part + (size_t) r * N + h * 128 + lane, (size_t) R * N, ks);
+        a1 = slices_sum1<KM>(part + (size_t) r * N + h * 128 + lane + 64, (size_t) R * N, ks);
+    } else {
+        const float* x = qkv + (size_t) r * ldqkv + (size_t) h * 128;
+        a0 = x[lane];
+        a1 = x[lane + 64];
+    }
+}
+// head h (q heads, k heads, v heads in that order) of the row at x, cell off of page; (w0, w1) the lane's norm weights
+__device__ __forceinline__ void qk_head(float* __restrict__ x, int lane, int h, int H, int KVH, bool raw_kv, float a0,
+                                        float a1, float c, float s, float w0, float w1, float eps,
+                                        uint16_t* __restrict__ kpool, uint16_t* __restrict__ vpool, int page,
+                                        int page_cells, int off) {
+#pragma clang fp contract(off)
+    const bool isq = h < H, isv = h >= H + KVH;
+    if (raw_kv && !isq) {  // k and v as the matmul made them (q is overwritten below)
+        x[lane] = a0;
+        x[lane + 64] = a1;
+    }
+    if (isv) {
+        uint16_t* vc = vpool + (((size_t) page * KVH + (h - H - KVH)) * page_cells + off) * 128;
+        vc[lane] = __builtin_bit_cast(uint16_t, (_Float16) a0);
+        vc[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16) a1);
+        return;
+    }
+    float ss = a0 * a0 + a1 * a1;
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    const float sc = 1.0f / sqrtf(ss / 128.f + eps);
+    a0 = (a0 * sc) * w0;
+    a1 = (a1 * sc) * w1;
+    const float y0 = a0 * c - a1 * s, y1 = a0 * s + a1 * c;
+    if (isq) {
+        x[lane] = y0;
+        x[lane + 64] = y1;
+    } else {
+        uint16_t* kc = kpool + (((size_t) page * KVH + (h - H)) * page_cells + off) * 128;
+        kc[lane] = __builtin_bit_cast(uint16_t, (_Float16) y0);
+        kc[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16) y1);
+    }
+}
+
+// Workgroup (row, y): wavefront w takes head 4 y + w
 template <int KM>
 __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ldqkv, const float* __restrict__ part,
                                                  int ks, int R, int H, int KVH, const float* __restrict__ qw,
@@ -34,6 +90,7 @@ __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ld
                                                  const int32_t* __restrict__ seq, const int32_t* __restrict__ pos,
                                                  const int32_t* __restrict__ pt, int max_pages, int page_cells,
                                                  uint16_t* __restrict__ kpool, uint16_t* __restrict__ vpool) {
+#pragma clang fp contract(off)
     const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h = 4 * blockIdx.y + wave;
     if (h >= H + 2 * KVH) return;
@@ -82,17 +139,63 @@ __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ld
     }
 }
 
+// Workgroup = one row of QKR_WAVES wavefronts: wavefront w takes heads w, w + QKR_WAVES, ... in rounds of
+// QKR_WAVES x QKR_HPW heads, each round's loads issued before anything waits on them; wavefront 0 forms the angles
+#define QKR_WAVES 16
+#define QKR_HPW 4
+#define QKR_ROWS_MIN 128  // steps of at least this many rows take k_qk_rope_rows
+template <int KM>
+__global__ __launch_bounds__(64 * QKR_WAVES) void k_qk_rope_rows(
+    float* __restrict__ qkv, int ldqkv, const float* __restrict__ part, int ks, int R, int H, int KVH,
+    const float* __restrict__ qw, const float* __restrict__ kw, float eps, float theta_scale,
+    const int32_t* __restrict__ seq, const int32_t* __restrict__ pos, const int32_t* __restrict__ pt, int max_pages,
+    int page_cells, uint16_t* __restrict__ kpool, uint16_t* __restrict__ vpool) {
+    __shared__ float s_cs[2][64];
+    const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int NH = H + 2 * KVH;
+    const float qw0 = qw[lane], qw1 = qw[lane + 64], kw0 = kw[lane], kw1 = kw[lane + 64];
+    const int p = pos[r];
+    const int page = pt[(size_t) seq[r] * max_pages + p / page_cells];
+    float c = 0.0f, s = 0.0f;
+    for (int h0 = 0; h0 < NH; h0 += QKR_WAVES * QKR_HPW) {  // the same trips in every wavefront
+        float a0[QKR_HPW], a1[QKR_HPW];
+        for (int j = 0; j < QKR_HPW; ++j)  // (past the last head: a re-read of it, unused)
+            qk_load<KM>(qkv, ldqkv, part, ks, R, NH * 128, r, min(h0 + wave + QKR_WAVES * j, NH - 1), lane, a0[j],
+                        a1[j]);
+        if (h0 == 0) {
+            if (wave == 0) rope_cs(p, lane, theta_scale, s_cs[0][lane], s_cs[1][lane]);
+            __syncthreads();
+            c = s_cs[0][lane];
+            s = s_cs[1][lane];
+        }
+        for (int j = 0; j < QKR_HPW; ++j) {
+            const int h = h0 + wave + QKR_WAVES * j;
+            if (h >= NH) break;
+            const bool isq = h < H;
+            qk_head(qkv + (size_t) r * ldqkv + (size_t) h * 128, lane, h, H, KVH, part != nullptr, a0[j], a1[j], c,
+                    s, isq ? qw0 : kw0, isq ? qw1 : kw1, eps, kpool, vpool, page, page_cells, p % page_cells);
+        }
+    }
+}
+
 void qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, int H, int KVH, const float* qw,
                      const float* kw, float eps, float theta_scale, const int32_t* seq, const int32_t* pos,
                      const int32_t* pt, int max_pages, int page_cells, uint16_t* kpool, uint16_t* vpool,
                      hipStream_t st) {
     if (R <= 0) return;
-    const dim3 grid(R, (H + 2 * KVH + 3) / 4);
     const int km = part ? ks_bound(ks) : 1;
     if (km == 0) return;
-#define QKR(KM_)                                                                                                 \
-    hipLaunchKernelGGL((k_qk_rope<KM_>), grid, dim3(256), 0, st, qkv, ldqkv, part, ks, R, H, KVH, qw, kw, eps, \
-                       theta_scale, seq, pos, pt, max_pages, page_cells, kpool, vpool)
+    const bool rows = R >= QKR_ROWS_MIN;
+    const dim3 grid = rows ? dim3(R) : dim3(R, (H + 2 * KVH + 3) / 4);
+#define QKR(KM_)                                                                                                   \
+    do {                                                                                                           \
+        if (rows)                                                                                                  \
+            hipLaunchKernelGGL((k_qk_rope_rows<KM_>), grid, dim3(64 * QKR_WAVES), 0, st, qkv, ldqkv, part, ks, R, \
+                               H, KVH, qw, kw, eps, theta_scale, seq, pos, pt, max_pages, page_cells, kpool, vpool); \
+        else                                                                                                       \
+            hipLaunchKernelGGL((k_qk_rope<KM_>), grid, dim3(256), 0, st, qkv, ldqkv, part, ks, R, H, KVH, qw, kw, \
+                               eps, theta_scale, seq, pos, pt, max_pages, page_cells, kpool, vpool);             \
+    } while (0)
     if (km == 1) QKR(1);
     else if (km == 2) QKR(2);
     else if (km == 4) QKR(4);
