@@ -422,7 +422,8 @@ def test_attention_list_forms_give_the_same_steps(tiny):
 def test_prompt_chunking_does_not_change_the_next_row(tmp_path):
     """A prompt fed in one step or in several gives the same cells and so the same next row, bit for bit (qbench.m's
     read_chunks, qbench.m:124-130): 600 prompt rows in one step (the full-K matmul walk and run items at 600 rows),
-    in 200-row steps (the split launches and chunk items), and in 64 + 536, then the same decode row. The model's
+    in 200-row steps (the split launches and chunk items; the workgroup-per-row QK-RoPE adding the k-slice sums), and
+    in 64 + 536 (the 64 rows through the wavefront-per-head QK-RoPE), then the same decode row. The model's
     matrices all split K (n_embd 1024: 2 slices) and its gate|up is wide enough (n_ff 3072: 384 stripes) for the prompt
     SwiGLU epilogue."""
     path = str(tmp_path / "w.gguf")
