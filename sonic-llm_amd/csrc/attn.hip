@@ -602,20 +602,21 @@ __global__ __launch_bounds__(512) void k_attn_run(AttnArgs a) {
 // behind a branch), then folded in order. With a.xa the head's 128 outputs (4 Q8_0 blocks of the o-projection's input
 // row) are also quantized there, exactly as the activation quantizer does (ggml x86 quantize_row_q8_0), into the xa
 // operand of K = H * 128.
+#define MERGE_BATCH 16  // chunk partials a lane loads before folding them
 __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
     const int r = a.mrows[blockIdx.x], h = blockIdx.y, lane = threadIdx.x;
     const int nc = a.row_pos[r] / ATT_CHUNK + 1;
     const float* p0 = a.part + ((size_t) r * a.H + h) * a.max_chunks * (ATT_D + 2);
     float M = -INFINITY, L = 0.0f, o[2] = {0.0f, 0.0f};
-    for (int c0 = 0; c0 < nc; c0 += 8) {
-        float2 ov[8], ml[8];
-        for (int j = 0; j < 8; ++j) {
+    for (int c0 = 0; c0 < nc; c0 += MERGE_BATCH) {  // (contexts up to 4096 cells: one round of loads)
+        float2 ov[MERGE_BATCH], ml[MERGE_BATCH];
+        for (int j = 0; j < MERGE_BATCH; ++j) {
             const float* pc = p0 + (size_t) (c0 + j < nc ? c0 + j : nc - 1) * (ATT_D + 2);
             ov[j] = *(const float2*) (pc + 2 * lane);
             ml[j] = *(const float2*) (pc + ATT_D);
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {  // (a fixed trip count keeps ov and ml in registers)
+        for (int j = 0; j < MERGE_BATCH; ++j) {  // (a fixed trip count keeps ov and ml in registers)
             if (c0 + j >= nc) continue;  // past the row's chunks
             const float v2[2] = {ov[j].x, ov[j].y};
             attn_fold<2>(M, L, o, ml[j].x, ml[j].y, v2);
