@@ -37,17 +37,7 @@ def log(msg):
 
 def model_file(cfg_kw, seed, path=None):
     import sllm_next as S
-    d = os.environ.get("SN_BENCH_DIR") or "/tmp"
-    tag = ("_mtp" if cfg_kw.get("nextn") else "") + (f"_moe{cfg_kw['n_expert']}" if cfg_kw.get("n_expert") else "") + \
-          ("_q8" if cfg_kw.get("wtype") == 8 else "") + ("_q6kt" if cfg_kw.get("tied") else "")
-    path = path or os.path.join(d, f"sonic_qwen3_{cfg_kw['n_layer']}L_{cfg_kw['n_embd']}{tag}_{seed}.gguf")
-    done = path + ".done"
-    if not (os.path.exists(path) and os.path.exists(done)):
-        t = time.time()
-        S.write_model(path, S.model_cfg(**cfg_kw), seed, nthreads=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
-        open(done, "w").write("ok")
-        log(f"[bench] wrote {path} ({os.path.getsize(path) / 1e9:.2f} GB) in {time.time() - t:.1f}s")
-    return path
+    return S.cached_model(cfg_kw, seed, path, log=lambda m: log("[bench] " + m))
 
 
 def cpu_spec_baseline(path, n, ctx, k, seed, layers, accept):

@@ -49,7 +49,9 @@ void snx_attn_mode(sn_engine* e, int mode);
 // of H query heads, KVH KV heads and page_cells-cell pages with attention form `mode` (as snx_attn_mode), computed on
 // the host alone (no device): two steps replay one captured graph exactly when their keys are equal. Writes at most
 // cap values to key and the attention form chosen to *whole (when given); returns the key's length, or -1 for bad
-// arguments. (Host code only; for checks of the replay rule.)
+// arguments. (Host code only; for checks of the replay rule.) The probe has no page table, so it plans the step as
+// an engine whose slots share no pages: for an engine with pages shared by sn_copy, the shared-prefix attention items
+// its step forms (and so its key) are not covered.
 int snx_step_key(int H, int KVH, int page_cells, int mode, int R, const int32_t* seq, const int32_t* pos,
                  int64_t* key, int cap, int* whole);
 

@@ -58,13 +58,6 @@ size_t snk_q4_workspace_bytes(int M, int N, int K);
 int snk_q4_plan(int N, int K, int wt, int* spw, int* ks);
 int snk_q4_gemm(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi, void* d_ws,
                 size_t ws_bytes, void* stream);
-// snk_q4_gemm without a workspace and without allocating: the k-slice partial sums go to a fixed device array of
-// 32 MiB that the library holds on each GPU it runs on (until the process ends), so the call makes no hipMalloc,
-// hipFree or other allocating call. The same kernels as snk_q4_gemm, so the same bits. A shape whose partials
-// (snk_q4_workspace_bytes(M, N, K)) exceed 32 MiB is refused with the reason in err. Calls that overlap on one GPU
-// (other streams or threads) share the array and race. 0, or -1 (err).
-// No counterpart in the reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving
-// loops, harnesses that forbid hipMalloc).
 // Prompt rows (M >= 256) of a stripe-interleaved gate|up matrix (N = 2F, F a multiple of 128, the wide split plans)
 // with its SwiGLU as the epilogue: silu(gate) * up as fp32 rows d_h [M][F] and as the Q8_0 operand d_xo (K = F, not
 // d_xa), the same bits as snk_q4_gemm's SwiGLU epilogue and snk_quant_act of its rows (the prompt step's fused
@@ -72,6 +65,14 @@ int snk_q4_gemm(const void* d_stripes, const void* d_xa, int M, int N, int K, fl
 // as its flag 32 does). 0, 1 when the shape does not take it (nothing launched), or -1
 int snk_q4_gemm_swiglu(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_h, void* d_xo,
                        void* stream);
+// snk_q4_gemm without a workspace and without allocating: the k-slice partial sums go to a fixed device array of
+// 32 MiB that the library holds on each GPU it runs on (until the process ends), so the call makes no hipMalloc,
+// hipFree or other allocating call. The same kernels as snk_q4_gemm, so the same bits. A shape whose partials
+// (snk_q4_workspace_bytes(M, N, K)) exceed 32 MiB is refused with the reason in err. Calls that overlap on one GPU
+// (other streams or threads) share the array and race. 0, or -1 (err; an error state that HIP held before the call is
+// left as it was and not reported as this call's).
+// No counterpart in the reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving
+// loops, harnesses that forbid hipMalloc).
 int snk_q4_gemm_noalloc(const void* d_stripes, const void* d_xa, int M, int N, int K, float* d_y, int ldy, int epi,
                         void* stream, char* err, int err_len);
 // average device time (microseconds) of one raw matmul launch (the k-slice sums into d_ws, as a decode step runs it:

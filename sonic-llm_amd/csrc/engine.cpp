@@ -348,6 +348,18 @@ bool model_check(const GgufFile& g, std::string* why) {
         *why = "the layer matrices must be Q4_0 or Q8_0";
         return false;
     }
+    // the row kernels after a layer matrix add its k-slices: every plan must stay within KS_MAX of them
+    const int F = (int) g.num(a + ".feed_forward_length", 0), QD = H * D, NQKV = (H + 2 * KVH) * D;
+    const int shapes[][2] = {{NQKV, E}, {E, QD}, {2 * F, E}, {E, F}, {E, 2 * E}};
+    for (const auto& sh : shapes) {
+        if (sh[0] <= 0 || sh[1] <= 0 || sh[1] % 32) continue;  // (absent: a MoE model's dense FFN width)
+        const int ks = q4_plan(sh[0], sh[1], tq->type).ks;
+        if (ks < 1 || ks > KS_MAX) {
+            *why = "matrix " + std::to_string(sh[0]) + " x " + std::to_string(sh[1]) + " would take " + std::to_string(ks) +
+                   " k-slices; the row kernels add at most " + std::to_string(KS_MAX);
+            return false;
+        }
+    }
     return true;
 }
 
@@ -900,16 +912,14 @@ struct Dev {
     void swiglu(int R) {
         const int F = e->F;
         rc |= e->launch(SNX_K_QUANT, (double) R * 2 * F * 4 * ks + (double) R * F * 6, [&] {
-            swiglu_quant(e->gemm_ws, ks, R, F, e->hb, e->xa, st);
-            return 0;
+            return swiglu_quant(e->gemm_ws, ks, R, F, e->hb, e->xa, st);
         });
     }
     void rope(const DevLayer& l, int R, int H, const int32_t* d_seq, const int32_t* d_pos, uint16_t* kp, uint16_t* vp) {
         const int N = (H + 2 * e->KVH) * e->D;
         rc |= e->launch(SNX_K_ROPE, (double) R * (N * 4.0 * (ks + 1) + H * e->D * 4 + 2 * e->KD * 2), [&] {
-            qk_norm_rope_kv(e->qkv, e->NQKV, e->gemm_ws, ks, R, H, e->KVH, l.q_norm, l.k_norm, e->eps, e->theta_scale,
-                            d_seq, d_pos, e->d_pt, e->max_pages, e->page_cells, kp, vp, st);
-            return 0;
+            return qk_norm_rope_kv(e->qkv, e->NQKV, e->gemm_ws, ks, R, H, e->KVH, l.q_norm, l.k_norm, e->eps,
+                                   e->theta_scale, d_seq, d_pos, e->d_pt, e->max_pages, e->page_cells, kp, vp, st);
         });
     }
     void attention(const Stage& S, const AttnList& al, int R, const int32_t* d_pos, uint16_t* kp, uint16_t* vp) {
@@ -1007,8 +1017,7 @@ struct Dev {
                                    e->gemm_ws_bytes, st, e->wt, e->rsrc, e->rsrc, R) < 0 ? -1 : 0;
         });
         rc |= e->launch(SNX_K_QUANT, (double) R * NU * FE * 14, [&] {
-            swiglu_quant(e->gemm_ws, 1, P, FE, nullptr, e->xa, st, e->rsrc);
-            return 0;
+            return swiglu_quant(e->gemm_ws, 1, P, FE, nullptr, e->xa, st, e->rsrc);
         });
         rc |= e->launch(SNX_K_GEMM, used * e->ed_stride + (double) R * NU * FE * 4 + (double) R * NU * E * 4, [&] {
             return q4_gemm_grouped(l.ed, e->ed_stride, e->gitems, e->gcount, T, e->xa, P, E, FE, e->gemm_ws,

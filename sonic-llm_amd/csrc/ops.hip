@@ -178,13 +178,13 @@ __global__ __launch_bounds__(64 * QKR_WAVES) void k_qk_rope_rows(
     }
 }
 
-void qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, int H, int KVH, const float* qw,
-                     const float* kw, float eps, float theta_scale, const int32_t* seq, const int32_t* pos,
-                     const int32_t* pt, int max_pages, int page_cells, uint16_t* kpool, uint16_t* vpool,
-                     hipStream_t st) {
-    if (R <= 0) return;
+int qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, int H, int KVH, const float* qw,
+                    const float* kw, float eps, float theta_scale, const int32_t* seq, const int32_t* pos,
+                    const int32_t* pt, int max_pages, int page_cells, uint16_t* kpool, uint16_t* vpool,
+                    hipStream_t st) {
+    if (R <= 0) return 0;
     const int km = part ? ks_bound(ks) : 1;
-    if (km == 0) return;
+    if (km == 0) return -1;  // more k-slices than the kernels add (q4_plan keeps every plan within KS_MAX)
     const bool rows = R >= QKR_ROWS_MIN;
     const dim3 grid = rows ? dim3(R) : dim3(R, (H + 2 * KVH + 3) / 4);
 #define QKR(KM_)                                                                                                   \
@@ -202,6 +202,7 @@ void qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, in
     else if (km == 8) QKR(8);
     else QKR(16);
 #undef QKR
+    return 0;
 }
 
 // ---- greedy argmax (argmax / argmax_p, kernels.metal:327-442) -------------------------------------------------------

@@ -852,6 +852,11 @@ GemmPlan q4_plan(int N, int K, int wt) {
     // 7.5, 6.4, 15.0 and 10.8.
     p.stream = true;
     p.gps = std::min(p.nstripes >= 1024 || p.ngroups >= 64 ? 8 : 4, (p.ngroups + 1) / 2 * 2);
+    // the slices' consumers (the row kernels) add at most KS_MAX of them: deeper matrices take longer slices (Qwen3-14B's
+    // down projection, K = 17408: 10 groups, 14 slices; Qwen3-32B's, K = 25600: 14 groups, 15 slices). The streaming
+    // kernel stages at most 8 groups of a slice in LDS; longer slices go to the ring kernel, whose LDS holds two groups.
+    while (slices(p.gps) > KS_MAX) p.gps += 2;
+    if (p.gps > 8) p.stream = false;
     p.ks = slices(p.gps);
     p.sspw = wt != WT_Q8_0 && p.nstripes >= 384 ? 2 : 1;
     p.smt = p.nstripes >= 1024 ? 2 : 1;
@@ -1107,11 +1112,18 @@ extern "C" int snk_q4_gemm_noalloc(const void* d_stripes, const void* d_xa, int 
     }
     float* ws = q4_scratch(err, err_len);
     if (!ws) return -1;
+    // the error state is read, not cleared: a state HIP held before the call stays the caller's, and only a change of
+    // it during the launches is this call's failure
+    const hipError_t before = hipPeekAtLastError();
     const int rc = q4_gemm((const uint8_t*) d_stripes, (const uint8_t*) d_xa, M, N, K, d_y, ldy, epi, ws,
                            Q4_SCRATCH_BYTES, (hipStream_t) stream);
-    const hipError_t e = hipGetLastError();
-    if (rc != 0 || e != hipSuccess) {
-        sn_set_err(err, err_len, "snk_q4_gemm_noalloc: launch failed: %s", hipGetErrorString(e));
+    const hipError_t after = hipPeekAtLastError();
+    if (rc != 0) {
+        sn_set_err(err, err_len, "snk_q4_gemm_noalloc: no launch plan for %d x %d x %d", M, N, K);
+        return -1;
+    }
+    if (after != hipSuccess && after != before) {
+        sn_set_err(err, err_len, "snk_q4_gemm_noalloc: launch failed: %s", hipGetErrorString(after));
         return -1;
     }
     return 0;
@@ -1164,11 +1176,11 @@ int moe_resid_quant(float* x, const float* y, const int32_t* prow, const float* 
 }
 
 #define SWQ_STAGE_ROWS 256  // rows from which k_swiglu_quant stages its sums through LDS
-void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st, const int32_t* rows) {
-    if (M <= 0) return;
+int swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st, const int32_t* rows) {
+    if (M <= 0) return 0;
     const dim3 grid(M, (xa_nbp(F) + 63) / 64);
     const int km = ks_bound(ks);
-    if (km == 0) return;
+    if (km == 0 || F % 32) return -1;
     auto go = [&](auto stage) {
         constexpr bool S = decltype(stage)::value;
         if (km == 1) hipLaunchKernelGGL((k_swiglu_quant<1, S>), grid, dim3(256), 0, st, part, ks, M, F, h, xa, rows);
@@ -1179,6 +1191,7 @@ void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa
     };
     if (M >= SWQ_STAGE_ROWS) go(std::true_type{});
     else go(std::false_type{});
+    return 0;
 }
 
 void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const float* nw, float eps, uint8_t* xa,

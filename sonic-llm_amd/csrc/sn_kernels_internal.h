@@ -85,8 +85,8 @@ void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const
 int resid_quant(float* x, const float* part, int ks, int M, int K, const float* nw, float eps, uint8_t* xa,
                 hipStream_t st, bool add = true, float* xn = nullptr);
 // h (optional) and the Q8_0 operand of silu(gate) * up from a stripe-interleaved gate/up matmul's k-slice sums
-// part[ks][M][2F].
-void swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st,
+// part[ks][M][2F]. 0, or -1 (more than KS_MAX slices, F not a multiple of 32: nothing launched).
+int swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st,
                   const int32_t* rows = nullptr);
 int q4_gemm(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* y, int ldy, int epi, float* ws,
             size_t ws_bytes, hipStream_t st, int wt = WT_Q4_0);
@@ -187,10 +187,10 @@ void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, in
 void embed_rows(const float* table, int V, int E, const int32_t* tok, int R, float* x, hipStream_t st);
 // q|k|v rows: from qkv (part NULL) or from the q|k|v matmul's k-slice sums part[ks][R][(H + 2 KVH) 128], which are
 // then also written to qkv (k and v as summed, q after QK-norm and RoPE); k and v go to the rows' cache cells.
-void qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, int H, int KVH, const float* qw,
-                     const float* kw, float eps, float theta_scale, const int32_t* seq, const int32_t* pos,
-                     const int32_t* pt, int max_pages, int page_cells, uint16_t* kpool, uint16_t* vpool,
-                     hipStream_t st);
+int qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, int H, int KVH, const float* qw,
+                    const float* kw, float eps, float theta_scale, const int32_t* seq, const int32_t* pos,
+                    const int32_t* pt, int max_pages, int page_cells, uint16_t* kpool, uint16_t* vpool,
+                    hipStream_t st);  // 0, or -1 (more than KS_MAX slices: nothing launched)
 // cells [a, b) of page `dst` in every layer: copied from page `src` (src >= 0) or zeroed (src < 0)
 void kv_page_op(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L, int KVH, int page_cells, int src, int dst,
                 int a, int b, hipStream_t st);

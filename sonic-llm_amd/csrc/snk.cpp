@@ -362,7 +362,7 @@ extern "C" int snk_qk_rope(float* d_qkv, int ldqkv, int R, int H, int KVH, const
                            float eps, float theta_scale, const int32_t* d_seq, const int32_t* d_pos, const int32_t* d_pt,
                            int max_pages, int page_cells, void* d_kpool, void* d_vpool, void* stream) {
     if (R <= 0 || H <= 0 || KVH <= 0 || ldqkv < (H + 2 * KVH) * 128 || (page_cells != 32 && page_cells != 64)) return -1;
-    qk_norm_rope_kv(d_qkv, ldqkv, nullptr, 1, R, H, KVH, d_qw, d_kw, eps, theta_scale, d_seq, d_pos, d_pt, max_pages, page_cells,
-                    (uint16_t*) d_kpool, (uint16_t*) d_vpool, (hipStream_t) stream);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    const int rc = qk_norm_rope_kv(d_qkv, ldqkv, nullptr, 1, R, H, KVH, d_qw, d_kw, eps, theta_scale, d_seq, d_pos, d_pt,
+                                   max_pages, page_cells, (uint16_t*) d_kpool, (uint16_t*) d_vpool, (hipStream_t) stream);
+    return rc == 0 && hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -210,6 +210,25 @@ def q4_plan(N: int, K: int, wt: int = 2) -> tuple:
     return spw.value, ks.value
 
 
+def cached_model(cfg_kw: dict, seed: int, path: str | None = None, log=None) -> str:
+    """A random-init model file of configuration cfg_kw (model_cfg's keywords) and seed, written once into
+    $SN_BENCH_DIR (default /tmp) under a name made of the two and reused while its ".done" marker exists (the
+    benchmark and the config-shaped tests share the files)."""
+    d = os.environ.get("SN_BENCH_DIR") or "/tmp"
+    tag = ("_mtp" if cfg_kw.get("nextn") else "") + (f"_moe{cfg_kw['n_expert']}" if cfg_kw.get("n_expert") else "") + \
+          ("_q8" if cfg_kw.get("wtype") == 8 else "") + ("_q6kt" if cfg_kw.get("tied") else "")
+    path = path or os.path.join(d, f"sonic_qwen3_{cfg_kw['n_layer']}L_{cfg_kw['n_embd']}{tag}_{seed}.gguf")
+    done = path + ".done"
+    if not (os.path.exists(path) and os.path.exists(done)):
+        import time
+        t = time.time()
+        write_model(path, model_cfg(**cfg_kw), seed, nthreads=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
+        open(done, "w").write("ok")
+        if log:
+            log(f"wrote {path} ({os.path.getsize(path) / 1e9:.2f} GB) in {time.time() - t:.1f}s")
+    return path
+
+
 def write_model(path: str, cfg: ModelCfg, seed: int, nthreads: int = 0) -> None:
     call(lib().snx_write_model, path.encode(), C.byref(cfg), seed, nthreads)
 

@@ -2,18 +2,24 @@
 
   * the Qwen3-4B-architecture decode step, all 36 layers, 32 sequences at position 2048 over seeded
     cached cells (the reference's b32 scenario, qbench.m:132-168);
-  * the fused draft-verify step (k = 3, 8 sequences at 4096 cells, seeded ~60% forced acceptance) on a
-    Qwen3-4B-width model with 2 layers and a guess head (draft.rs:135-178, take.rs:339-357);
+  * the fused draft-verify step (k = 3, 8 sequences at 4096 cells, seeded ~60% forced acceptance) on the
+    Qwen3-4B architecture, all 36 layers, with a guess head (draft.rs:135-178, take.rs:339-357; draft_test.m:45-67);
   * the Qwen3-30B-A3B-architecture MoE decode step (128 experts, top-8, 4 KV heads: G = 8), 32 sequences
-    at 2048 cells, 2 layers (sn_layers.inc.h:129-144).
+    at 2048 cells, all 48 layers (sn_layers.inc.h:129-144).
 
 The oracle's KV cache is given the engine's own cells (sn_kv_save), so both start from the same bytes. The GPU and the
 oracle sum in different fp32 orders, so now and then an fp16 cell or a Q8_0 activation rounds the other way, and over
 layers that moves the logits by the activations' Q8_0 noise (a perturbation that flips no rounding changes nothing:
 every matmul input is re-quantized). The bar is therefore set by the oracle itself: the same oracle step summed in
 another order (Drift). North_star asks for identical tokens wherever the top-2 gap exceeds 1e-4; no implementation
-whose summation order differs from ggml's can hold that where the gap is inside the drift, and each test prints how
-many rows clear 1e-4 and how many of those agree, for the GPU and for the reversed oracle.
+whose summation order differs from ggml's can hold that where the gap is inside the drift (the reversed oracle does
+not hold it against ggml's order either). What the tests hold instead, with the counts in each assertion's message:
+
+  * on rows whose top-2 gap exceeds 1e-4, the GPU's tokens disagree with the oracle's on at most SLACK times as many
+    rows as the reversed oracle's do, plus TOKEN_SLACK rows (small counts: one row is 1.6% of configs[2]'s 64);
+  * in configs[3], the fused steps' decisions (accepted count and tokens of a sequence) diverge from the oracle's at
+    most SLACK times as often as the reversed oracle's decisions do, plus TOKEN_SLACK; a diverged sequence is brought
+    back onto the oracle's path (its cells cut and the oracle's kept rows stepped in), so every step is compared.
 """
 import numpy as np
 import pytest
@@ -57,6 +63,7 @@ class Drift:
         for the reversed oracle."""
 
     SLACK = 2.0
+    TOKEN_SLACK = 4
     TIE = 1e-2
 
     def __init__(self):
@@ -94,8 +101,12 @@ class Drift:
             print(f"  routing near ties (margin < {self.TIE}): {len(t)} rows, margins {np.round(t[:, 0], 5).tolist()}, "
                   f"their max |logit diff| GPU {np.round(t[:, 1], 3).tolist()}, reversed oracle "
                   f"{np.round(t[:, 2], 3).tolist()}")
-        assert dg.mean() <= self.SLACK * dr.mean() + 1e-6
-        assert dg.max() <= self.SLACK * dr.max() + 1e-5
+        assert dg.mean() <= self.SLACK * dr.mean() + 1e-6, (dg.mean(), dr.mean())
+        assert dg.max() <= self.SLACK * dr.max() + 1e-5, (dg.max(), dr.max())
+        off_gpu, off_rev = self.over_1e4 - self.same_gpu, self.over_1e4 - self.same_rev
+        assert off_gpu <= self.SLACK * off_rev + self.TOKEN_SLACK, (
+            f"{name}: of {self.over_1e4} rows with a top-2 gap > 1e-4, the GPU's token differs from the oracle's on "
+            f"{off_gpu}, the reversed oracle's on {off_rev} (bar: {self.SLACK} x {off_rev} + {self.TOKEN_SLACK})")
 
 
 def oracle_both(step, moe_rows=0, moe_layers=0):
@@ -113,9 +124,8 @@ def oracle_both(step, moe_rows=0, moe_layers=0):
     return fwd, rev, tr.margins().reshape(moe_layers, moe_rows).min(0)
 
 
-def test_config3_decode_step_matches_oracle(tmp_path):
-    path = str(tmp_path / "qwen3_4b.gguf")
-    S.write_model(path, S.model_cfg(**S.QWEN3_4B), seed=42)
+def test_config3_decode_step_matches_oracle():
+    path = S.cached_model(S.QWEN3_4B, 42)  # (the benchmark's file)
     n_seq, ctx = 32, 2048
     seq = np.arange(n_seq, dtype=np.int32)
     ref = O.Qwen3(GGUF(path), n_seq=n_seq, ctx=ctx + 2)
@@ -185,69 +195,97 @@ def clear_of(lg, tok, bound):
     return i1 == tok and v1 - v2 > 2 * bound
 
 
-def test_config4_spec_step_matches_oracle(tmp_path):
-    cfg = dict(S.QWEN3_4B, n_layer=2, nextn=1)
-    path = str(tmp_path / "qwen3_4b_mtp.gguf")
-    S.write_model(path, S.model_cfg(**cfg), seed=43)
-    n_seq, ctx, steps = 8, 4096, 3
+def test_config4_spec_step_matches_oracle():
+    path = S.cached_model(dict(S.QWEN3_4B, nextn=1), 42)  # (the benchmark's file)
+    n_seq, ctx, steps = 8, 4096, 4
     seq = np.arange(n_seq, dtype=np.int32)
-    ref = MtpRef(path, n_seq, ctx + 1 + (K + 1) * steps)
+    cap = ctx + 1 + (K + 1) * steps
+    ref, rev = MtpRef(path, n_seq, cap), MtpRef(path, n_seq, cap)  # ggml's summation order; the reversed one
+    assert ref.m.L == 36
     rng = np.random.default_rng(5)
     drift = Drift()
-    stats = {"decisions": 0, "accepted": 0, "followed": 0}
+    stats = {"decisions": 0, "diverged_gpu": 0, "diverged_rev": 0, "accepted": 0, "clear": 0}
     with S.Engine(path, slots=n_seq, ctx=ctx + 64, max_rows=n_seq * (K + 1)) as eng:
         for s in seq:
             eng.fill_kv(int(s), ctx, seed=43)
         load_cells(eng, ref.m, seq, ctx)
+        load_cells(eng, rev.m, seq, ctx)
         eng.guess_on(True)
         # a decode step at position 4096 (the head fills its cell of each row, the slots keep their states)
         tok = rng.integers(0, ref.m.V, n_seq).astype(np.int32)
         pos = np.full(n_seq, ctx, np.int32)
         got = eng.step(tok, seq, pos, seq)
-        pend0 = ref.pend.copy()
-
-        def decode():  # (each run starts from the same kept head states)
-            ref.pend[:] = pend0
-            return ref.step(tok, seq, pos, seq)
-
-        (want, rl, _), (rt, rv, _) = oracle_both(decode)
+        want, rl, _ = ref.step(tok, seq, pos, seq)
+        O.set_sum_order(True)
+        try:
+            rt, rv, _ = rev.step(tok, seq, pos, seq)
+        finally:
+            O.set_sum_order(False)
         drift.add(got, eng.logits(seq), want, rl, rt, rv)
+        # the reversed oracle continues from the forward one's state (the same cells and kept states)
+        rev.m.k[...] = ref.m.k
+        rev.m.v[...] = ref.m.v
+        rev.pend[...] = ref.pend
         # a draft or verify decision is clear when its top-2 gap exceeds twice the largest drift seen on that step
         bound = max(np.abs(drift.gpu[0]).max(), np.abs(drift.rev[0]).max())
         last, pos = want.astype(np.int32), pos + 1
-        alive = [True] * n_seq
         for _ in range(steps):
             force = (rng.random((n_seq, K)) < 0.6).astype(np.uint8)
             n, t = eng.spec_step(seq, last, pos, K, force=force)
             for s in range(n_seq):
-                d, dl, tg, vl, a = ref.spec(s, last[s], pos[s], force[s])
-                if alive[s]:
-                    same = n[s] == a + 1 and list(t[s, :a + 1]) == list(d[:a]) + [tg[a]]
-                    sure = all(clear_of(dl[j], d[j], bound) for j in range(min(a + 1, K)))
-                    sure = sure and all((i < K and force[s, i]) or clear_of(vl[i], tg[i], bound)
-                                        for i in range(a + 1))
-                    assert same or not sure, (s, n[s], t[s], a, d, tg)
-                    stats["decisions"] += 1
-                    stats["accepted"] += a if same else 0
-                    stats["followed"] += int(same)
-                    alive[s] = same
+                p0 = int(pos[s])
+                d, dl, tg, vl, a = ref.spec(s, last[s], p0, force[s])
+                O.set_sum_order(True)
+                try:
+                    rd, _, rtg, _, ra = rev.spec(s, last[s], p0, force[s])
+                finally:
+                    O.set_sum_order(False)
+                kept = list(d[:a]) + [tg[a]]
+                same = n[s] == a + 1 and list(t[s, :a + 1]) == kept
+                rsame = ra == a and list(rd[:ra]) + [rtg[ra]] == kept
+                sure = all(clear_of(dl[j], d[j], bound) for j in range(min(a + 1, K)))
+                sure = sure and all((i < K and force[s, i]) or clear_of(vl[i], tg[i], bound) for i in range(a + 1))
+                assert same or not sure, (s, n[s], t[s], a, d, tg)
+                stats["decisions"] += 1
+                stats["clear"] += int(sure)
+                stats["accepted"] += a
+                stats["diverged_gpu"] += int(not same)
+                stats["diverged_rev"] += int(not rsame)
+                if not rsame:  # the reversed oracle back onto the forward one's path
+                    rev.m.k[s] = ref.m.k[s]
+                    rev.m.v[s] = ref.m.v[s]
+                    rev.pend[s] = ref.pend[s]
+                if not same:  # the engine back onto the oracle's path: its cells cut, the kept rows stepped in
+                    eng.clear(s, p0, p0 + K + 1)
+                    rows = np.array([last[s]] + list(d[:a]), np.int32)
+                    eng.step(rows, np.full(a + 1, s, np.int32), np.arange(p0, p0 + a + 1, dtype=np.int32),
+                             np.array([a], np.int32), n_write=0)
                 last[s] = tg[a]
                 pos[s] += a + 1
-    drift.report("configs[3] decode step before the draft-verify steps (2 layers + guess head)")
+    drift.report("configs[3] decode step before the draft-verify steps (36 layers + guess head)")
     print(f"configs[3] fused steps against the oracle (decision bound {bound:.3g}): {stats}")
-    assert stats["followed"] >= 0.75 * stats["decisions"] and stats["accepted"] >= 6
+    assert stats["accepted"] >= stats["decisions"], stats  # (~60% of 3 drafts forced: about 1.8 a decision)
+    assert stats["diverged_gpu"] <= Drift.SLACK * stats["diverged_rev"] + Drift.TOKEN_SLACK, (
+        f"fused-step decisions diverging from the oracle's: GPU {stats['diverged_gpu']}, reversed oracle "
+        f"{stats['diverged_rev']} of {stats['decisions']} (bar: {Drift.SLACK} x {stats['diverged_rev']} + "
+        f"{Drift.TOKEN_SLACK})")
 
 
-def test_config5_moe_step_matches_oracle(tmp_path):
-    cfg = dict(S.QWEN3_30B_A3B, n_layer=2)
-    path = str(tmp_path / "qwen3_30b_a3b.gguf")
-    S.write_model(path, S.model_cfg(**cfg), seed=44)
+@pytest.mark.parametrize("layers", [2, 48])
+def test_config5_moe_step_matches_oracle(layers):
+    """configs[4]'s MoE decode step. At 2 layers the rows whose routing is a near tie are left out of the logit bars
+    (Drift); at all 48 layers nearly every row meets a near tie in some layer, so the bars hold over all rows: the
+    GPU's logit drift, routing flips included, within SLACK x the reversed oracle's (which flips routings too), and the
+    token-agreement bar."""
+    cfg = dict(S.QWEN3_30B_A3B, n_layer=layers)
+    path = S.cached_model(cfg, 42)  # (at 48 layers, the benchmark's file)
     n_seq, ctx = 32, 2048
     seq = np.arange(n_seq, dtype=np.int32)
     ref = O.Qwen3(GGUF(path), n_seq=n_seq, ctx=ctx + 2)
-    assert (ref.H, ref.KVH, ref.NE, ref.NEU) == (32, 4, 128, 8)
+    assert (ref.L, ref.H, ref.KVH, ref.NE, ref.NEU) == (layers, 32, 4, 128, 8)
     r = np.random.default_rng(4)
     drift = Drift()
+    near = []
     with S.Engine(path, slots=n_seq, ctx=ctx + 64, max_rows=n_seq) as eng:
         for s in seq:
             eng.fill_kv(int(s), ctx, seed=44)
@@ -258,7 +296,10 @@ def test_config5_moe_step_matches_oracle(tmp_path):
             got = eng.step(tok, seq, pos, seq)
             gl = eng.logits(seq)
             (want, rl, _), (rt, rv, _), margins = oracle_both(lambda: ref.step(tok, seq, pos, seq), n_seq, ref.L)
-            drift.add(got, gl, want, rl, rt, rv, margins)
+            near.append(int((margins < Drift.TIE).sum()))
+            drift.add(got, gl, want, rl, rt, rv, margins if layers <= 2 else None)
             tok = want.astype(np.int32)
-    drift.report("configs[4] MoE decode step (2 layers)")
+    print(f"configs[4] at {layers} layers: rows with a routing margin below {Drift.TIE} in some layer: {near} of "
+          f"{n_seq} a step")
+    drift.report(f"configs[4] MoE decode step ({layers} layers)")
     assert len(drift.tie_rows) <= drift.rows // 2

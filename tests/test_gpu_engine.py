@@ -65,6 +65,17 @@ def test_token_tables_and_tied_heads(tmp_path, embd_type, tied, wtype):
     prefill_and_decode(path)
 
 
+@pytest.mark.parametrize("n_ff", [17408, 25600])
+def test_deep_down_projection_matches_oracle(tmp_path, n_ff):
+    """FFN widths of Qwen3-14B (17408) and Qwen3-32B (25600): the down projection's plan takes slices of 10 and 14
+    groups (the ring kernel at decode row counts) so that the row kernels add at most 16 k-slices; prefill and decode
+    against the oracle (its reversed-order drift on these models: 0.011)."""
+    path = str(tmp_path / "deep.gguf")
+    S.write_model(path, S.model_cfg(**dict(TINY, n_ff=n_ff)), seed=14)
+    assert S.q4_plan(TINY["n_embd"], n_ff)[1] <= 16
+    prefill_and_decode(path)
+
+
 def prefill_and_decode(path):
     ref = O.Qwen3(GGUF(path), n_seq=4, ctx=256)
     r = np.random.default_rng(0)

@@ -67,3 +67,33 @@ def test_noalloc_refuses_shapes_beyond_the_array():
     # refused on the host before any launch (the pointers are never touched)
     rc = L.snk_q4_gemm_noalloc(None, None, M, N, K, None, N, 0, U.stream(), buf, 512)
     assert rc == -1 and b"scratch array holds" in buf.value, buf.value
+
+
+def test_noalloc_under_graph_capture():
+    """A warm call (the device array's address looked up), then one call captured into a HIP graph and replayed
+    several times, with eager work of the program between the replays: every replay bit for bit the eager result."""
+    T = U.torch()
+    L = S.lib()
+    r = np.random.default_rng(77)
+    M, N, K = 32, 2560, 4096
+    Wq, X, wbuf, xa = operands(r, M, N, K)
+    y_eager, y_graph = U.empty(M * N * 4), U.empty(M * N * 4)
+    S.call(L.snk_q4_gemm_noalloc, U.ptr(wbuf), U.ptr(xa), M, N, K, U.ptr(y_eager), N, 0, U.stream())
+    want = U.host(y_eager, np.float32)[:M * N].copy()
+    g = T.cuda.CUDAGraph()
+    side = T.cuda.Stream()
+    side.wait_stream(T.cuda.current_stream())
+    with T.cuda.stream(side):
+        S.call(L.snk_q4_gemm_noalloc, U.ptr(wbuf), U.ptr(xa), M, N, K, U.ptr(y_graph), N, 0, U.stream())  # (warm)
+        with T.cuda.graph(g, stream=side):
+            S.call(L.snk_q4_gemm_noalloc, U.ptr(wbuf), U.ptr(xa), M, N, K, U.ptr(y_graph), N, 0,
+                   C.c_void_p(side.cuda_stream))
+    T.cuda.current_stream().wait_stream(side)
+    for rep in range(4):
+        y_graph.fill_(0xFF)  # eager work between the replays (a fill kernel, outside the graph)
+        g.replay()
+        got = U.host(y_graph, np.float32)[:M * N]
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), rep
+        # the eager call again on another output, between replays
+        S.call(L.snk_q4_gemm_noalloc, U.ptr(wbuf), U.ptr(xa), M, N, K, U.ptr(y_eager), N, 0, U.stream())
+        assert np.array_equal(U.host(y_eager, np.float32)[:M * N].view(np.uint32), want.view(np.uint32)), rep
