@@ -45,6 +45,14 @@ long snx_chain_count(const sn_engine* e, int dropped);
 // sequence with two or more consecutive full query groups (prompt rows; -1 takes them when they make at least 128
 // workgroups), the other rows as -1. Every form gives the same bits.
 void snx_attn_mode(sn_engine* e, int mode);
+// The matmul epilogues fused into decode-sized steps' q|k|v (QK-norm, RoPE, cache write) and gate|up (SwiGLU + Q8_0)
+// launches, done by each set's last workgroup through its XCD's L2: on when sn_open's probe found the device dealing
+// workgroups to its XCDs in turn by linear id (and SN_NO_FUSE is unset). on 0 switches them off (the split path: the
+// same bits), 1 back on where the probe allows. Returns whether they are on. Drops captured graphs.
+int snx_fuse(sn_engine* e, int on);
+// Whether a fused launch ran a workgroup on another XCD than the probe predicted (then its epilogue may have read
+// stale sums): 0 never, 1 it did, -1 error. Waits for the engine's work.
+int snx_xcd_faults(sn_engine* e);
 // The graph key sn_step forms for a step of R rows (slots seq, positions pos; every row sampled in order) on an engine
 // of H query heads, KVH KV heads and page_cells-cell pages with attention form `mode` (as snx_attn_mode), computed on
 // the host alone (no device): two steps replay one captured graph exactly when their keys are equal. Writes at most

@@ -91,7 +91,15 @@ struct sn_engine {
     float *x = nullptr, *qkv = nullptr, *ao = nullptr, *hb = nullptr, *logits = nullptr, *gemm_ws = nullptr;
     size_t gemm_ws_bytes = 0;
     uint8_t* xa = nullptr;
-    uint8_t* xa2 = nullptr;  // the down projection's operand when prompt rows' gate|up writes it (q4_gemm_swiglu)
+    uint8_t* xa2 = nullptr;  // the down projection's operand when gate|up writes it (q4_gemm_swiglu, q4_gemm_fused)
+    // the streaming matmul's fused epilogues (q4_gemm_fused): on when the open-time probe found the device dealing
+    // workgroups to its XCDs in turn (snx_fuse switches them off and on); the arrival counters and the XCD check word
+    bool fuse = false, fuse_ok = false;
+    int nxcd = 1;
+    uint64_t* d_fcnt = nullptr;
+    float2* rope_cs = nullptr;  // a step's rotation table (rope_table) [max_rows][64]
+    int32_t* d_xerr = nullptr;
+    int fcnt_len = 0;
     float* apart = nullptr;
     int max_chunks = 0;
     uint8_t *d_stage = nullptr, *h_stage = nullptr;
@@ -567,8 +575,19 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->xa = e->dalloc<uint8_t>(std::max({xa_bytes(R, KMAX), e->NE > 0 ? xa_bytes(P, std::max(E, e->FE)) : 0,
                                          e->head_t == GGML_Q6_K ? xk_bytes(MO, E) : 0}),
                                err, err_len);
-    if (e->NE == 0 && F > 0 && q4_gemm_swiglu_fits(R, 2 * F, E, e->wt))
-        e->xa2 = e->dalloc<uint8_t>(xa_bytes(R, F), err, err_len);
+    if (e->NE == 0 && F > 0) e->xa2 = e->dalloc<uint8_t>(xa_bytes(R, F), err, err_len);
+    // the fused epilogues' arrival counters (sets x row-tile groups of any decode-sized launch; zero between launches:
+    // each set's last workgroup resets its own) and the XCD check word
+    e->fcnt_len = 1 << 16;
+    e->d_fcnt = e->dalloc<uint64_t>((size_t) e->fcnt_len * 8, err, err_len);
+    e->d_xerr = e->dalloc<int32_t>(4, err, err_len);
+    if (!e->d_fcnt || !e->d_xerr || hipMemset(e->d_fcnt, 0, (size_t) e->fcnt_len * 8) != hipSuccess ||
+        hipMemset(e->d_xerr, 0, 4) != hipSuccess)
+        return fail("fused-epilogue counters");
+    e->rope_cs = e->dalloc<float2>((size_t) std::max(R, slots) * 64 * sizeof(float2), err, err_len);
+    if (!e->rope_cs) return fail("");
+    e->fuse_ok = xcd_round_robin(e->st, &e->nxcd);
+    e->fuse = e->fuse_ok && !getenv("SN_NO_FUSE");
     size_t ws = 0;
     ws = std::max(ws, q4_workspace_bytes(R, e->NQKV, E, e->wt));
     ws = std::max(ws, q4_workspace_bytes(R, E, QD, e->wt));
@@ -867,6 +886,8 @@ double gemm_bytes(int wt, int M, int N, int K) {
 struct Dev {
     sn_engine* e;
     hipStream_t st;
+    const int32_t* cs_pos = nullptr;  // the positions whose rotation table e->rope_cs holds in this step
+    int cs_R = 0;
     int ks = 0;  // k-slices of the last matmul
     bool moe_pending = false;  // x awaits a MoE layer's weighted expert rows (added by the next resid)
     int rc = 0;
@@ -886,6 +907,47 @@ struct Dev {
             return q4_gemm_swiglu(w, e->xa, M, 2 * F, E, e->hb, e->xa2, st, e->wt) == 1 ? 0 : -1;
         });
         return true;
+    }
+    // decode-sized rows: a matmul whose last workgroup of each set runs the set's epilogue (the split path's row
+    // kernel, same bits); false when the engine or the shape has no fused launch (nothing launched)
+    bool gemm_fused(const uint8_t* w, int M, int N, int K, int fe, GemmArgs& ea, double extra_bytes) {
+        if (!e->fuse || !q4_gemm_fused_fits(M, N, K, e->wt, fe, e->nxcd, e->fcnt_len)) return false;
+        ea.cnt = e->d_fcnt, ea.xerr = e->d_xerr, ea.nxcd = e->nxcd;
+        int r = 0;
+        rc |= e->launch(SNX_K_GEMM, gemm_bytes(e->wt, M, N, K) + extra_bytes, [&] {
+            r = q4_gemm_fused(w, e->xa, M, N, K, e->gemm_ws, e->gemm_ws_bytes, st, e->wt, fe, ea, e->fcnt_len);
+            return r < 0 ? -1 : 0;
+        });
+        return r == 1;
+    }
+    // the rotation table of R rows at positions d_pos (formed by one small launch when the step has not formed it)
+    const float2* cs_for(int R, const int32_t* d_pos) {
+        if (cs_pos != d_pos || cs_R < R) {
+            rc |= e->launch(SNX_K_OTHER, (double) R * 64 * 8, [&] {
+                rope_table(d_pos, R, e->theta_scale, e->rope_cs, st);
+                return 0;
+            });
+            cs_pos = d_pos, cs_R = R;
+        }
+        return e->rope_cs;
+    }
+    // q|k|v with QK-norm + RoPE + the cache write fused (H query heads; 0 for the guess head's k|v)
+    bool gemm_rope(const uint8_t* w, const DevLayer& l, int R, int N, int H, const int32_t* d_seq,
+                   const int32_t* d_pos, uint16_t* kp, uint16_t* vp) {
+        GemmArgs ea{};
+        ea.qkv = e->qkv, ea.ldqkv = e->NQKV, ea.qw = l.q_norm, ea.kw = l.k_norm, ea.eps = e->eps;
+        ea.theta_scale = e->theta_scale, ea.seq = d_seq, ea.pos = d_pos, ea.pt = e->d_pt, ea.max_pages = e->max_pages;
+        ea.page_cells = e->page_cells, ea.kpool = kp, ea.vpool = vp, ea.H = H, ea.KVH = e->KVH;
+        if (!e->fuse || !q4_gemm_fused_fits(R, N, e->E, e->wt, FE_ROPE, e->nxcd, e->fcnt_len)) return false;
+        ea.rope_cs = cs_for(R, d_pos);
+        return gemm_fused(w, R, N, e->E, FE_ROPE, ea, (double) R * (H * e->D * 4 + 2 * e->KD * 2));
+    }
+    // gate|up with SwiGLU + Q8_0 fused: the down projection's operand in xa2, the rows in hb
+    bool gemm_swiglu_dec(const uint8_t* w, int R) {
+        if (!e->xa2) return false;
+        GemmArgs ea{};
+        ea.h = e->hb, ea.xo = e->xa2;
+        return gemm_fused(w, R, 2 * e->F, e->E, FE_SWIGLU, ea, (double) R * e->F * 6);
     }
     void quant(const float* x, const int32_t* rows, int M, int K, const float* nw, float* xn = nullptr) {
         rc |= e->launch(SNX_K_QUANT, (double) M * K * 8, [&] {
@@ -919,7 +981,8 @@ struct Dev {
         const int N = (H + 2 * e->KVH) * e->D;
         rc |= e->launch(SNX_K_ROPE, (double) R * (N * 4.0 * (ks + 1) + H * e->D * 4 + 2 * e->KD * 2), [&] {
             return qk_norm_rope_kv(e->qkv, e->NQKV, e->gemm_ws, ks, R, H, e->KVH, l.q_norm, l.k_norm, e->eps,
-                                   e->theta_scale, d_seq, d_pos, e->d_pt, e->max_pages, e->page_cells, kp, vp, st);
+                                   e->theta_scale, d_seq, d_pos, e->d_pt, e->max_pages, e->page_cells, kp, vp, st,
+                                   cs_pos == d_pos && cs_R >= R ? e->rope_cs : nullptr);
         });
     }
     void attention(const Stage& S, const AttnList& al, int R, const int32_t* d_pos, uint16_t* kp, uint16_t* vp) {
@@ -965,8 +1028,10 @@ struct Dev {
     bool block(const DevLayer& l, int layer, float* x, int R, const Stage& S, const AttnList& al, const int32_t* d_seq,
                const int32_t* d_pos) {
         const int E = e->E, F = e->F;
-        gemm(l.wqkv, R, e->NQKV, E);
-        rope(l, R, e->H, d_seq, d_pos, kp(layer), vp(layer));
+        if (!gemm_rope(l.wqkv, l, R, e->NQKV, e->H, d_seq, d_pos, kp(layer), vp(layer))) {
+            gemm(l.wqkv, R, e->NQKV, E);
+            rope(l, R, e->H, d_seq, d_pos, kp(layer), vp(layer));
+        }
         attention(S, al, R, d_pos, kp(layer), vp(layer));
         gemm(l.wo, R, E, e->QD);
         if (l.egu) {
@@ -974,7 +1039,7 @@ struct Dev {
             return true;
         }
         resid(x, R, l.ffn_norm, true);
-        if (gemm_swiglu(l.wgu, R)) {
+        if (gemm_swiglu(l.wgu, R) || gemm_swiglu_dec(l.wgu, R)) {
             gemm(l.wd, R, E, F, e->xa2);
             return true;
         }
@@ -1098,8 +1163,11 @@ struct Dev {
         gemm(e->mtp_eh, R, E, 2 * E);
         resid(e->mx, R, e->mtp.attn_norm, true, false);
         // the head's k|v stripes (rows QD .. QD + 2 KD of its q|k|v matrix)
-        gemm(e->mtp.wqkv + wt_bytes(e->wt, e->QD, E), R, 2 * e->KD, E);
-        rope(e->mtp, R, 0, d_seq, d_pos, kp(e->L), vp(e->L));
+        const uint8_t* wkv = e->mtp.wqkv + wt_bytes(e->wt, e->QD, E);
+        if (!gemm_rope(wkv, e->mtp, R, 2 * e->KD, 0, d_seq, d_pos, kp(e->L), vp(e->L))) {
+            gemm(wkv, R, 2 * e->KD, E);
+            rope(e->mtp, R, 0, d_seq, d_pos, kp(e->L), vp(e->L));
+        }
         if (nkeep > 0) rows_keep(e->mhn, d_keep, nkeep, E, e->mpend, st);
     }
 
@@ -1590,6 +1658,20 @@ extern "C" void snx_graphs(sn_engine* e, int on);
 extern "C" void snx_attn_mode(sn_engine* e, int mode) {
     e->attn_mode = mode < -1 || mode > 2 ? -1 : mode;
     snx_graphs(e, e->graphs);  // captured graphs hold the old form's launches
+}
+
+extern "C" int snx_fuse(sn_engine* e, int on) {
+    e->fuse = on != 0 && e->fuse_ok;
+    snx_graphs(e, e->graphs);  // captured graphs hold the other path's launches
+    return e->fuse ? 1 : 0;
+}
+
+extern "C" int snx_xcd_faults(sn_engine* e) {
+    if (settle(e) != 0) return -1;
+    int32_t v = 0;
+    if (hipStreamSynchronize(e->st) != hipSuccess || hipMemcpy(&v, e->d_xerr, 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    return v;
 }
 
 extern "C" void snx_graphs(sn_engine* e, int on) {

@@ -3,6 +3,7 @@
 #include <algorithm>
 
 #include "sn_kernels_internal.h"
+#include "sn_rows.h"
 
 // ---- embedding: the token's fp32 table row (embed_rows / embed_into, sn_state.inc.h:250-272; the table is fp32 here)
 // Token ids come from the host (checked there) or from an argmax on the GPU (a queued step's tokens, the guess head's
@@ -28,14 +29,8 @@ void embed_rows(const float* table, int V, int E, const int32_t* tok, int R, flo
 // cell in fp16 (with part given, k and v as the matmul made them are also written into the row). Two launch shapes do
 // the same operations in the same order with contraction off, so a row gets the same bits from either: k_qk_rope, a
 // wavefront a head (the most wavefronts, for decode-sized steps), and k_qk_rope_rows (through rope_cs, qk_load and
-// qk_head), a workgroup a row with the angles formed once and shared through LDS (for prompt-sized steps).
-__device__ __forceinline__ void rope_cs(int p, int lane, float theta_scale, float& c, float& s) {
-#pragma clang fp contract(off)
-    float theta = (float) p;
-    for (int i = 0; i < lane; ++i) theta *= theta_scale;
-    c = cosf(theta);
-    s = sinf(theta);
-}
+// qk_head of sn_rows.h), a workgroup a row with the angles formed once and shared through LDS (for prompt-sized steps).
+// The q|k|v matmul's fused epilogue (q4.hip) goes through rope_cs and qk_head too.
 // a head's two dims: the q|k|v matmul's k-slice sums (added in slice order) or the row's values
 template <int KM>
 __device__ __forceinline__ void qk_load(const float* __restrict__ qkv, int ldqkv, const float* __restrict__ part, int ks,
@@ -49,39 +44,6 @@ __device__ __forceinline__ void qk_load(const float* __restrict__ qkv, int ldqkv
         a1 = x[lane + 64];
     }
 }
-// head h (q heads, k heads, v heads in that order) of the row at x, cell off of page; (w0, w1) the lane's norm weights
-__device__ __forceinline__ void qk_head(float* __restrict__ x, int lane, int h, int H, int KVH, bool raw_kv, float a0,
-                                        float a1, float c, float s, float w0, float w1, float eps,
-                                        uint16_t* __restrict__ kpool, uint16_t* __restrict__ vpool, int page,
-                                        int page_cells, int off) {
-#pragma clang fp contract(off)
-    const bool isq = h < H, isv = h >= H + KVH;
-    if (raw_kv && !isq) {  // k and v as the matmul made them (q is overwritten below)
-        x[lane] = a0;
-        x[lane + 64] = a1;
-    }
-    if (isv) {
-        uint16_t* vc = vpool + (((size_t) page * KVH + (h - H - KVH)) * page_cells + off) * 128;
-        vc[lane] = __builtin_bit_cast(uint16_t, (_Float16) a0);
-        vc[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16) a1);
-        return;
-    }
-    float ss = a0 * a0 + a1 * a1;
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-    const float sc = 1.0f / sqrtf(ss / 128.f + eps);
-    a0 = (a0 * sc) * w0;
-    a1 = (a1 * sc) * w1;
-    const float y0 = a0 * c - a1 * s, y1 = a0 * s + a1 * c;
-    if (isq) {
-        x[lane] = y0;
-        x[lane + 64] = y1;
-    } else {
-        uint16_t* kc = kpool + (((size_t) page * KVH + (h - H)) * page_cells + off) * 128;
-        kc[lane] = __builtin_bit_cast(uint16_t, (_Float16) y0);
-        kc[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16) y1);
-    }
-}
-
 // Workgroup (row, y): wavefront w takes head 4 y + w
 template <int KM>
 __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ldqkv, const float* __restrict__ part,
@@ -89,7 +51,8 @@ __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ld
                                                  const float* __restrict__ kw, float eps, float theta_scale,
                                                  const int32_t* __restrict__ seq, const int32_t* __restrict__ pos,
                                                  const int32_t* __restrict__ pt, int max_pages, int page_cells,
-                                                 uint16_t* __restrict__ kpool, uint16_t* __restrict__ vpool) {
+                                                 uint16_t* __restrict__ kpool, uint16_t* __restrict__ vpool,
+                                                 const float2* __restrict__ cs) {
 #pragma clang fp contract(off)
     const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h = 4 * blockIdx.y + wave;
@@ -120,9 +83,13 @@ __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ld
         vc[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16) x1);
         return;
     }
-    float theta = (float) p;
-    for (int i = 0; i < lane; ++i) theta *= theta_scale;
-    const float c = cosf(theta), s = sinf(theta);
+    float c, s;
+    if (cs) {  // the step's table (rope_table: the same function of (p, lane))
+        const float2 t = cs[(size_t) r * 64 + lane];
+        c = t.x, s = t.y;
+    } else {
+        rope_cs(p, lane, theta_scale, c, s);
+    }
     float ss = x0 * x0 + x1 * x1;
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
     const float sc = 1.0f / sqrtf(ss / 128.f + eps);
@@ -178,10 +145,22 @@ __global__ __launch_bounds__(64 * QKR_WAVES) void k_qk_rope_rows(
     }
 }
 
+// the rotation's (cos, sin) of rows 0 .. R - 1 at positions pos, lanes 0 .. 63 (rope_cs), into cs [R][64]
+__global__ __launch_bounds__(64) void k_rope_table(const int32_t* __restrict__ pos, float theta_scale,
+                                                   float2* __restrict__ cs) {
+    float c, s;
+    rope_cs(pos[blockIdx.x], threadIdx.x, theta_scale, c, s);
+    cs[(size_t) blockIdx.x * 64 + threadIdx.x] = make_float2(c, s);
+}
+
+void rope_table(const int32_t* pos, int R, float theta_scale, float2* cs, hipStream_t st) {
+    if (R > 0) hipLaunchKernelGGL(k_rope_table, dim3(R), dim3(64), 0, st, pos, theta_scale, cs);
+}
+
 int qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, int H, int KVH, const float* qw,
                     const float* kw, float eps, float theta_scale, const int32_t* seq, const int32_t* pos,
                     const int32_t* pt, int max_pages, int page_cells, uint16_t* kpool, uint16_t* vpool,
-                    hipStream_t st) {
+                    hipStream_t st, const float2* cs) {
     if (R <= 0) return 0;
     const int km = part ? ks_bound(ks) : 1;
     if (km == 0) return -1;  // more k-slices than the kernels add (q4_plan keeps every plan within KS_MAX)
@@ -194,7 +173,7 @@ int qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, int
                                H, KVH, qw, kw, eps, theta_scale, seq, pos, pt, max_pages, page_cells, kpool, vpool); \
         else                                                                                                       \
             hipLaunchKernelGGL((k_qk_rope<KM_>), grid, dim3(256), 0, st, qkv, ldqkv, part, ks, R, H, KVH, qw, kw, \
-                               eps, theta_scale, seq, pos, pt, max_pages, page_cells, kpool, vpool);             \
+                               eps, theta_scale, seq, pos, pt, max_pages, page_cells, kpool, vpool, cs);         \
     } while (0)
     if (km == 1) QKR(1);
     else if (km == 2) QKR(2);

@@ -16,8 +16,10 @@
 #include <algorithm>
 #include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "sn_kernels_internal.h"
+#include "sn_rows.h"
 
 // ---------------------------------------------------------------------------------------------------------------------
 // weight upload: GGUF rows -> stripes (sn_common.h)
@@ -578,12 +580,107 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     q4_gemm_ring<WT, MT, S, true, SW>(a);
 }
 
+// A k-slice sum of the workspace, read by the set's last workgroup (sc0: past the CU's L1, from the XCD's L2, where
+// the set's other workgroups' stores are)
+__device__ __forceinline__ float4 part_load4(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 1));
+}
+__device__ __forceinline__ float part_load1(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 1));
+}
+
+// The fused epilogue of set `set`, row tiles mt0 .. mt0 + MT - 1, run by the set's last workgroup once every slice's
+// sums are in the workspace: the slices of each value added in slice order ((p0 + p1) + p2 ...), as slices_sum4 and
+// slices_sum1 add them for the row kernels, then the row kernel's own arithmetic.
+//   FE_SWIGLU: the set's 4 S stripes are S Q8_0 blocks of F = N / 2 SwiGLU columns (the gate|up matrix interleaved
+//              stripe by stripe): k_swiglu_quant's silu(gate) * up and q8_store, 4 lanes a block (thread: row, block,
+//              lane part), into a.h (fp32 rows, when given) and the operand a.xo;
+//   FE_ROPE:   the set's 8 stripes are head `set` (128 columns): wavefront w takes rows w, w + 4, ..., lane i the dims
+//              (i, i + 64), and qk_head norms, rotates and writes q to a.qkv, k and v to the row's cell (and k, v as
+//              summed to a.qkv), as k_qk_rope does.
+template <int FE, int MT, int S>
+__device__ __forceinline__ void q4_epilogue(const GemmArgs& a, int set, int mt0) {
+    const int ks = (int) gridDim.y;
+    const __amdgpu_buffer_rsrc_t pr = buf_rsrc(a.part, (uint32_t) ((size_t) ks * a.M * a.N * sizeof(float)));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int KM = 1 << (FE & 7);  // the slices' bound: every slice's values loaded at once (the index clamped,
+                                       // so no load sits behind a branch; the slices past ks are not added)
+    if constexpr (FE >= FE_SWIGLU && FE < FE_ROPE) {
+        const int F = a.N / 2;
+        for (int it = threadIdx.x; it < 16 * MT * S * 4; it += 256) {
+            const int r = it / (4 * S), blk = (it >> 2) % S, g = it & 3;
+            const int row = mt0 * 16 + r, b = set * S + blk;
+            if (row >= a.M || 32 * b >= F) continue;  // (a block's 4 lane parts together: q8_store's shuffles)
+            float4 pv[4][KM];
+            for (int q = 0; q < 4; ++q)  // gate, up of pair 2b; gate, up of pair 2b + 1
+                for (int k = 0; k < KM; ++k)
+                    pv[q][k] = part_load4(pr, (row * a.N + 64 * b + 16 * q + 4 * g) * 4 + min(k, ks - 1) * a.M * a.N * 4);
+            float4 v4[4];
+            for (int q = 0; q < 4; ++q) {
+                float4 acc = pv[q][0];
+                for (int k = 1; k < KM; ++k)
+                    if (k < ks) acc = (float4){acc.x + pv[q][k].x, acc.y + pv[q][k].y, acc.z + pv[q][k].z, acc.w + pv[q][k].w};
+                v4[q] = acc;
+            }
+            const float4 g0 = v4[0], u0 = v4[1], g1 = v4[2], u1 = v4[3];
+            float v[8] = {silu(g0.x) * u0.x, silu(g0.y) * u0.y, silu(g0.z) * u0.z, silu(g0.w) * u0.w,
+                          silu(g1.x) * u1.x, silu(g1.y) * u1.y, silu(g1.z) * u1.z, silu(g1.w) * u1.w};
+            if (a.h) {
+                float* o = a.h + (size_t) row * F + 32 * b;
+                *(float4*) (o + 4 * g) = (float4){v[0], v[1], v[2], v[3]};
+                *(float4*) (o + 16 + 4 * g) = (float4){v[4], v[5], v[6], v[7]};
+            }
+            q8_store(v, g, a.xo, F, row, b);
+        }
+    } else if constexpr (FE >= FE_ROPE) {  // (2 rows a wavefront at once)
+        constexpr int RC = 2;
+        static_assert(S == 2, "a head is the 8 stripes of a set");
+        const int h = set, H = a.H, KVH = a.KVH;
+        const bool isq = h < H, isv = h >= H + KVH;
+        const float* w = isq ? a.qw : a.kw;
+        const float w0 = isv ? 0.0f : w[lane], w1 = isv ? 0.0f : w[lane + 64];
+        for (int r0 = wave * RC; r0 < 16 * MT; r0 += 4 * RC) {
+            if (mt0 * 16 + r0 >= a.M) break;
+            float x0[RC][KM], x1[RC][KM];
+            for (int j = 0; j < RC; ++j) {
+                const int row = min(mt0 * 16 + r0 + j, a.M - 1);  // (past M: the last row again, not written)
+                const int off = (row * a.N + h * 128 + lane) * 4;
+                for (int k = 0; k < KM; ++k) {
+                    const int o = off + min(k, ks - 1) * a.M * a.N * 4;
+                    x0[j][k] = part_load1(pr, o);
+                    x1[j][k] = part_load1(pr, o + 256);
+                }
+            }
+            for (int j = 0; j < RC; ++j) {
+                const int row = mt0 * 16 + r0 + j;
+                if (row >= a.M) break;
+                float v0 = x0[j][0], v1 = x1[j][0];
+                for (int k = 1; k < KM; ++k)
+                    if (k < ks) v0 += x0[j][k], v1 += x1[j][k];
+                const int p = a.pos[row];
+                const int page = a.pt[(size_t) a.seq[row] * a.max_pages + p / a.page_cells];
+                float c = 0.0f, sn = 0.0f;
+                if (!isv) {
+                    if (a.rope_cs) {
+                        const float2 t = a.rope_cs[(size_t) row * 64 + lane];
+                        c = t.x, sn = t.y;
+                    } else {
+                        rope_cs(p, lane, a.theta_scale, c, sn);
+                    }
+                }
+                qk_head(a.qkv + (size_t) row * a.ldqkv + (size_t) h * 128, lane, h, H, KVH, true, v0, v1, c, sn, w0,
+                        w1, a.eps, a.kpool, a.vpool, page, a.page_cells, p % a.page_cells);
+            }
+        }
+    }
+}
+
 // The streaming form: the slice's activation records (gps groups, up to GMAX) are loaded once per workgroup by the 4
 // wavefronts together and staged into LDS behind the kernel's only barrier; each wavefront then streams its own S
 // stripes' weights through a ring of D register slots (group i + D's loads issued as soon as group i is summed), with
 // no further synchronisation. The activation fragment, scales and corrections read from LDS for a block serve S x MT
-// MFMAs. Same arithmetic and order as k_q4_gemm.
-template <int WT, int MT, int S, int D, int GMAX>
+// MFMAs. Same arithmetic and order as k_q4_gemm. FE: the fused epilogue run by each set's last workgroup (GemmArgs).
+template <int WT, int MT, int S, int D, int GMAX, int FE = FE_NONE>
 __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     constexpr bool Q8 = WT == WT_Q8_0;
     constexpr int TB = Q8 ? Q8T_BYTES : Q4T_BYTES, SO = Q8 ? Q8T_SCALE_OFF : Q4T_SCALE_OFF;
@@ -596,6 +693,9 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n_in = lane & 15, g = lane >> 4;
     const int set = blockIdx.x, slice = blockIdx.y;
+    if constexpr (FE != FE_NONE) {
+        if (set * 4 * S >= a.nstripes) return;  // a padding set (the grid's sets: a multiple of nxcd)
+    }
     const int mt0 = __builtin_amdgcn_readfirstlane((int) blockIdx.z * MT);
     const int c0 = slice * a.gps, ng = __builtin_amdgcn_readfirstlane(min(a.gps, a.ngroups - c0));
     const int s0 = set * (4 * S) + wave * S;
@@ -678,6 +778,32 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
                 const int row = (mt0 + mt) * 16 + 4 * g + v;
                 if (row < a.M) a.part[((size_t) slice * a.M + row) * a.N + col] = acc[t][mt][v];
             }
+    }
+    if constexpr (FE != FE_NONE) {
+        // this workgroup's sums have reached the L2 (vmcnt counts stores); then it counts itself, and the count's
+        // completer (it resets the counter for the next launch) finishes the set
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        __shared__ int s_last;
+        if (threadIdx.x == 0) {
+            unsigned xcc;
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+            const int f = 8 + 5 * (int) (xcc & 7);  // this XCD's field of the count
+            uint64_t* c = a.cnt + set + (int) gridDim.x * (int) blockIdx.z;
+            const uint64_t add = 1ull + (1ull << f);
+            const uint64_t n = __hip_atomic_fetch_add(c, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+            s_last = (int) (n & 255) == (int) gridDim.y;
+            if (s_last) {
+                if ((int) ((n >> f) & 31) != (int) gridDim.y)  // some workgroup of the set ran on another XCD
+                    __hip_atomic_fetch_or(a.xerr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                // back to zero by an atomic of the same kind, performed where the counts were (a plain store of an
+                // atomic compiles to a write-through store, which need not meet the L2's copy)
+                __hip_atomic_fetch_add(c, (uint64_t) 0 - n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __syncthreads();
+        if (!s_last) return;
+        q4_epilogue<FE, MT, S>(a, set, mt0);
     }
 }
 
@@ -966,6 +1092,129 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
     if (wt == WT_Q8_0) launch_gemm<WT_Q8_0>(mt, p.spw, grid, a, st);
     else launch_gemm<WT_Q4_0>(mt, p.spw, grid, a, st);
     return p.ks;
+}
+
+// the streaming kernel with a fused epilogue: false when (FE, MT, S, gps) is not instantiated
+template <int WT, int FE>
+static bool launch_gemm_fe(int mt, int spw, int gps, dim3 grid, const GemmArgs& a, hipStream_t st) {
+#define GSF(MT_, S_, GM_)                                                                                    \
+    if (mt == MT_ && spw == S_ && gps <= GM_) {                                                              \
+        hipLaunchKernelGGL((k_q4_gemm_s<WT, MT_, S_, 2, GM_, FE>), grid, dim3(256), 0, st, a);               \
+        return true;                                                                                         \
+    }
+    if constexpr (WT == WT_Q4_0 && FE >= FE_ROPE) {  // (q|k|v: one row tile a workgroup below 1024 stripes)
+        GSF(1, 2, 4) GSF(1, 2, 8)
+    } else if constexpr (WT == WT_Q4_0) {
+        GSF(1, 2, 4) GSF(1, 2, 8) GSF(2, 2, 4) GSF(2, 2, 8)
+    } else if constexpr (FE < FE_ROPE) {  // (Q8_0 tiles: one stripe a wavefront; a set is one Q8_0 block of F)
+        GSF(1, 1, 4) GSF(1, 1, 8) GSF(2, 1, 4) GSF(2, 1, 8)
+    }
+#undef GSF
+    return false;
+}
+
+// the fused launch's shape: stripes a wavefront, row tiles a workgroup, the grid (its sets padded to a multiple of
+// nxcd); false when the plan, the weight type or the epilogue's unit does not allow one
+static bool fused_shape(int M, int N, int K, int wt, int fe, int nxcd, int cnt_len, GemmPlan& p, int& spw, int& mt,
+                        dim3& grid) {
+    if (M <= 0 || M >= Q4_PAIR_ROWS || nxcd < 1 || (wt != WT_Q4_0 && wt != WT_Q8_0)) return false;
+    p = q4_plan(N, K, wt);
+    if (!p.stream || p.gps > 8) return false;
+    // a set must hold whole epilogue units: one head (8 stripes: two a wavefront, Q4_0 tiles), or S Q8_0 blocks of
+    // SwiGLU columns (64 S interleaved columns)
+    if (fe == FE_ROPE) {
+        if (wt != WT_Q4_0 || N % 128) return false;
+        spw = 2;
+    } else if (fe == FE_SWIGLU) {
+        spw = wt == WT_Q4_0 ? 2 : 1;  // (the instances: Q8_0 tiles one stripe a wavefront)
+        if (N % (64 * spw) || p.ks > 8) return false;  // (more slices: their loads would not fit the registers)
+    } else {
+        return false;
+    }
+    const int mtiles = (M + 15) / 16;
+    mt = std::min(p.smt, mtiles);
+    if (fe == FE_ROPE && mt != 1) return false;  // (the instances)
+    const int sets = (p.nstripes + 4 * spw - 1) / (4 * spw);
+    grid = dim3((sets + nxcd - 1) / nxcd * nxcd, p.ks, (mtiles + mt - 1) / mt);
+    return (long) grid.x * grid.z <= cnt_len;
+}
+
+bool q4_gemm_fused_fits(int M, int N, int K, int wt, int fe, int nxcd, int cnt_len) {
+    GemmPlan p;
+    int spw, mt;
+    dim3 grid;
+    return fused_shape(M, N, K, wt, fe, nxcd, cnt_len, p, spw, mt, grid);
+}
+
+int q4_gemm_fused(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
+                  hipStream_t st, int wt, int fe, const GemmArgs& ea, int cnt_len) {
+    if (M <= 0) return 0;
+    if (!ea.cnt || !ea.xerr || (fe == FE_SWIGLU && (!ea.xo || ea.xo == xa))) return -1;
+    GemmPlan p;
+    int spw, mt;
+    dim3 grid;
+    if (!fused_shape(M, N, K, wt, fe, ea.nxcd, cnt_len, p, spw, mt, grid)) return 0;
+    if (part == nullptr || part_bytes < (size_t) p.ks * M * N * sizeof(float)) return -1;
+    GemmArgs a = ea;
+    a.w = w; a.xa = xa; a.part = part; a.y = nullptr;
+    a.M = M; a.N = N; a.K = K; a.ldy = 0; a.epi = EPI_STORE;
+    a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
+    a.mtiles = (M + 15) / 16;
+    a.items = nullptr; a.count = nullptr; a.rmask = nullptr; a.gsrc = nullptr;
+    // the epilogue's slice bound (as the row kernels' KM): instance FE + log2 KM
+    const int lk = p.ks <= 1 ? 0 : p.ks <= 2 ? 1 : p.ks <= 4 ? 2 : p.ks <= 8 ? 3 : 4;
+    bool ok = false;
+    auto go = [&](auto fe_c) {
+        constexpr int F0 = decltype(fe_c)::value;
+        if (wt == WT_Q8_0) {
+            if constexpr (F0 == FE_SWIGLU) {
+                if (lk == 0) ok = launch_gemm_fe<WT_Q8_0, F0>(mt, spw, p.gps, grid, a, st);
+                else if (lk == 1) ok = launch_gemm_fe<WT_Q8_0, F0 + 1>(mt, spw, p.gps, grid, a, st);
+                else if (lk == 2) ok = launch_gemm_fe<WT_Q8_0, F0 + 2>(mt, spw, p.gps, grid, a, st);
+                else if (lk == 3) ok = launch_gemm_fe<WT_Q8_0, F0 + 3>(mt, spw, p.gps, grid, a, st);
+                else ok = launch_gemm_fe<WT_Q8_0, F0 + 4>(mt, spw, p.gps, grid, a, st);
+            }
+            return;
+        }
+        if (lk == 0) ok = launch_gemm_fe<WT_Q4_0, F0>(mt, spw, p.gps, grid, a, st);
+        else if (lk == 1) ok = launch_gemm_fe<WT_Q4_0, F0 + 1>(mt, spw, p.gps, grid, a, st);
+        else if (lk == 2) ok = launch_gemm_fe<WT_Q4_0, F0 + 2>(mt, spw, p.gps, grid, a, st);
+        else if (lk == 3) ok = launch_gemm_fe<WT_Q4_0, F0 + 3>(mt, spw, p.gps, grid, a, st);
+        else ok = launch_gemm_fe<WT_Q4_0, F0 + 4>(mt, spw, p.gps, grid, a, st);
+    };
+    if (fe == FE_SWIGLU) go(std::integral_constant<int, FE_SWIGLU>{});
+    else go(std::integral_constant<int, FE_ROPE>{});
+    return ok ? 1 : -1;
+}
+
+// One workgroup of the probe records the XCD it runs on
+__global__ __launch_bounds__(64) void k_xcd_probe(int32_t* out) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    if (threadIdx.x == 0) out[blockIdx.x] = (int32_t) (xcc & 15);
+}
+
+bool xcd_round_robin(hipStream_t st, int* nxcd) {
+    const int n = 8192;
+    int32_t* d = nullptr;
+    *nxcd = 1;
+    if (hipMalloc(&d, n * sizeof(int32_t)) != hipSuccess) return false;
+    std::vector<int32_t> h(n, -1);
+    hipLaunchKernelGGL(k_xcd_probe, dim3(n), dim3(64), 0, st, d);
+    const bool ran = hipStreamSynchronize(st) == hipSuccess &&
+                     hipMemcpy(h.data(), d, n * sizeof(int32_t), hipMemcpyDeviceToHost) == hipSuccess;
+    hipFree(d);
+    if (!ran) return false;
+    unsigned seen = 0;
+    for (int i = 0; i < n; ++i) {
+        if (h[i] < 0 || h[i] > 15) return false;
+        seen |= 1u << h[i];
+    }
+    *nxcd = __builtin_popcount(seen);
+    if (*nxcd > 8) return false;  // (the count's XCD fields: 8 of 5 bits)
+    for (int i = 0; i < n; ++i)
+        if (h[i] != h[i % *nxcd]) return false;
+    return true;
 }
 
 // An explicit launch plan (for tuning): the streaming kernel with mt row tiles a workgroup (1, 2), spw stripes a

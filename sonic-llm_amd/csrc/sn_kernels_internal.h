@@ -26,7 +26,32 @@ struct GemmArgs {
     uint8_t* xo;
     int M, N, K, ldy, epi;
     int nstripes, ngroups, ks, gps, mtiles;
+    // The streaming kernel's fused epilogues (decode rows, q4_gemm_fused): a workgroup that has stored its slice's sums
+    // counts itself in cnt[set + gridDim.x * z] (zero between launches), and the set's last one adds the set's slices in
+    // slice order and applies the epilogue itself. The hardware deals a launch's workgroups to the device's nxcd XCDs
+    // in turn by linear id (from where the queue's last launch left off), and the grid's sets are padded to a multiple
+    // of nxcd, so every workgroup of a set runs on one XCD and the sums reach the last one through that XCD's L2. Each
+    // workgroup also adds 1 to its XCD's 5-bit field of the 64-bit count: a last workgroup that finds the count's
+    // workgroups on more than one XCD sets *xerr (its epilogue may have read stale sums).
+    uint64_t* cnt;
+    int32_t* xerr;
+    int nxcd;
+    // FE_ROPE: the rows' q|k|v heads normed, rotated, and k, v written to their cells (qk_norm_rope_kv's arguments)
+    float* qkv;
+    int ldqkv;
+    const float *qw, *kw;
+    float eps, theta_scale;
+    const int32_t *seq, *pos, *pt;
+    int max_pages, page_cells;
+    uint16_t *kpool, *vpool;
+    int H, KVH;
+    const float2* rope_cs;  // the rows' rotation table (rope_table), or null (each head forms its angles)
 };
+// the streaming kernel's fused epilogues: none (the k-slice sums for the row kernels), the SwiGLU + Q8_0 of a
+// stripe-interleaved gate|up matrix (k_swiglu_quant's arithmetic), the q|k|v heads' QK-norm + RoPE + cache write
+// (k_qk_rope's arithmetic)
+// (the kernel's instances: FE + log2 KM, KM the slice bound of the epilogue's loads)
+enum { FE_NONE = 0, FE_SWIGLU = 8, FE_ROPE = 16 };
 
 // Launch shape of one matrix: a workgroup owns 4 spw stripes (a "set": spw per wavefront) and gps consecutive 4-block
 // groups (a slice). Layer-sized matrices at decode row counts run the streaming kernel (sspw stripes a wavefront,
@@ -59,6 +84,19 @@ size_t q4_workspace_bytes(int M, int N, int K, int wt = WT_Q4_0);
 // or -1 when part_bytes is too small. wt: the weight type of w (WT_Q4_0 or WT_Q8_0 tiles).
 int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
                 hipStream_t st, int wt = WT_Q4_0);
+// The raw matmul of decode-sized rows with a fused epilogue fe (FE_SWIGLU: a.h, a.xo; FE_ROPE: the rope fields of a)
+// through the streaming kernel: the same sums in the same order as q4_gemm_raw followed by swiglu_quant (xo must not be
+// xa) or qk_norm_rope_kv, so the same bits. `a` carries the epilogue's fields and the counters (a.cnt, cnt_len of
+// them), a.xerr and a.nxcd. Returns 1 when launched, 0 when the shape or weight type has no fused launch
+// (nothing launched: use the split path), -1 on bad arguments.
+int q4_gemm_fused(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
+                  hipStream_t st, int wt, int fe, const GemmArgs& a, int cnt_len);
+// whether q4_gemm_fused launches this shape (host only)
+bool q4_gemm_fused_fits(int M, int N, int K, int wt, int fe, int nxcd, int cnt_len);
+// Whether the current device deals a launch's workgroups to its XCDs in turn by linear id: a probe launch on `st`
+// (synchronous) of 8192 workgroups, each recording its XCD id; true when workgroups i and i mod nxcd ran on the same
+// XCD for every i, with nxcd the number of XCD ids seen (at most 8). The condition of the fused epilogues.
+bool xcd_round_robin(hipStream_t st, int* nxcd);
 // Grouped raw matmul of expert matrices (moe: qmm_grouped, sn_attn.inc.h:352-359): up to max_items (expert, row tile)
 // items, the device count in `count`; part[M][N] rows of each item's tile (one slice).
 // gsrc (optional): the operand's tile row p is row gsrc[p] of the row-ordered operand xa of gM rows (gathered while
@@ -187,10 +225,15 @@ void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, in
 void embed_rows(const float* table, int V, int E, const int32_t* tok, int R, float* x, hipStream_t st);
 // q|k|v rows: from qkv (part NULL) or from the q|k|v matmul's k-slice sums part[ks][R][(H + 2 KVH) 128], which are
 // then also written to qkv (k and v as summed, q after QK-norm and RoPE); k and v go to the rows' cache cells.
+// cs (optional): the rows' rotation table (rope_table of the same positions), else each head forms its angles.
+// 0, or -1 (more than KS_MAX slices: nothing launched).
 int qk_norm_rope_kv(float* qkv, int ldqkv, const float* part, int ks, int R, int H, int KVH, const float* qw,
                     const float* kw, float eps, float theta_scale, const int32_t* seq, const int32_t* pos,
                     const int32_t* pt, int max_pages, int page_cells, uint16_t* kpool, uint16_t* vpool,
-                    hipStream_t st);  // 0, or -1 (more than KS_MAX slices: nothing launched)
+                    hipStream_t st, const float2* cs = nullptr);
+// the rotation's (cos, sin) of R rows at positions pos (device), 64 lanes each, into cs [R][64]: the values each head's
+// QK-RoPE would form itself (rope_cs), formed once for all of a step's heads and layers
+void rope_table(const int32_t* pos, int R, float theta_scale, float2* cs, hipStream_t st);
 // cells [a, b) of page `dst` in every layer: copied from page `src` (src >= 0) or zeroed (src < 0)
 void kv_page_op(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L, int KVH, int page_cells, int src, int dst,
                 int a, int b, hipStream_t st);

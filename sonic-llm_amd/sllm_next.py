@@ -138,6 +138,8 @@ SNK_API = [
 EXT_API = [
     ("snx_graphs", None, [P, I]),
     ("snx_attn_mode", None, [P, I]),
+    ("snx_fuse", I, [P, I]),
+    ("snx_xcd_faults", I, [P]),
     ("snx_step_key", I, [I, I, I, I, I, P, P, P, I, P]),
     ("snx_chain_count", C.c_long, [P, I]),
     ("snx_graph_count", C.c_long, [P, I]),
@@ -377,6 +379,15 @@ class Engine:
         """snx_attn_mode: the attention work list's form, -1 per step (default), 0 per-chunk + merge, 1 whole groups,
         2 run items for prompt rows wherever possible."""
         self.L.snx_attn_mode(self.e, int(mode))
+
+    def fuse(self, on: bool) -> bool:
+        """snx_fuse: the matmul epilogues fused into decode-sized steps (q|k|v + RoPE, gate|up + SwiGLU), on (where
+        sn_open's XCD probe allows) or off (the split path, the same bits); returns whether they are on."""
+        return bool(self.L.snx_fuse(self.e, int(on)))
+
+    def xcd_faults(self) -> int:
+        """snx_xcd_faults: 1 when a fused launch ran a workgroup on another XCD than predicted, else 0."""
+        return self.L.snx_xcd_faults(self.e)
 
     def chain_count(self) -> tuple:
         """(queued steps taken, queued steps dropped) since the engine opened (sn_step's chain)."""
