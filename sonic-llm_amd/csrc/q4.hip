@@ -706,16 +706,17 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xa + x0, (uint32_t) (xa_bytes(a.M, a.K) - x0));
     const int rstride = a.ngroups * XA_REC;
 
-    // the slice's activation (fragments past the slice repeat its last group: loads stay in bounds, never summed)
-    u32x4 ra[FPW];
-    float rk[KPW];
-    for (int j = 0; j < FPW; ++j) {
-        const int f = wave + 4 * j, c = c0 + min(f / (4 * MT), ng - 1);
-        ra[j] = bload16(xr, 16 * lane, ((f / 4) % MT) * rstride + c * XA_REC + (f % 4) * 1024);
+    // the slice's activation straight into LDS (buffer loads to LDS: lane l's 16 bytes land at 16 l of the fragment,
+    // no registers; fragments past the slice repeat its last group: loads stay in bounds, never summed)
+    for (int f = wave; f < NF; f += 4) {
+        const int c = c0 + min(f / (4 * MT), ng - 1);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr) &s_act[f][0], 16, 16 * lane,
+                                                 ((f / 4) % MT) * rstride + c * XA_REC + (f % 4) * 1024, 0, 0);
     }
-    for (int j = 0; j < KPW; ++j) {
-        const int k = min(wave + 4 * j, NK - 1), c = c0 + min(k / (2 * MT), ng - 1);
-        rk[j] = bload4f(xr, 4 * lane, ((k / 2) % MT) * rstride + c * XA_REC + (k % 2 ? CORR : XA_DX_OFF));
+    for (int k = wave; k < NK; k += 4) {
+        const int c = c0 + min(k / (2 * MT), ng - 1);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr) &s_k[k / (2 * MT)][(k / 2) % MT][k % 2][0], 4, 4 * lane,
+                                                 ((k / 2) % MT) * rstride + c * XA_REC + (k % 2 ? CORR : XA_DX_OFF), 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     u32x4 wq[D][S][NW];
@@ -732,11 +733,10 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
         wload(j, j);
         __builtin_amdgcn_sched_barrier(0);
     }
-    for (int j = 0; j < FPW; ++j) *(u32x4*) &s_act[wave + 4 * j][16 * lane] = ra[j];
-    for (int j = 0; j < KPW; ++j) {
-        const int k = wave + 4 * j;
-        if (k < NK) s_k[k / (2 * MT)][(k / 2) % MT][k % 2][lane] = rk[j];
-    }
+    // the LDS loads were issued first: waiting until no more than the weights' loads are outstanding waits for them
+    constexpr int NWL = D * S * (NW + 1);
+    static_assert(NWL < 64, "vmcnt holds 6 bits");
+    __builtin_amdgcn_s_waitcnt((NWL & 15) | ((NWL >> 4) << 14) | (7 << 4) | (15 << 8));
     __syncthreads();
 
     floatx4 acc[S][MT];
@@ -749,35 +749,65 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
             const float m = i < ng ? 1.0f : 0.0f;
             const int li = min(i, ng - 1);  // (its LDS group)
             __builtin_amdgcn_sched_barrier(0);
-            for (int b = 0; b < 4; ++b) {
-                half8 A[MT];
-                floatx4 dx[MT], cr[MT];
-                for (int mt = 0; mt < MT; ++mt) {
-                    A[mt] = *(const half8*) &s_act[(li * MT + mt) * 4 + b][16 * lane];
-                    dx[mt] = *(const floatx4*) &s_k[li][mt][0][b * 16 + 4 * g];
-                    cr[mt] = *(const floatx4*) &s_k[li][mt][1][b * 16 + 4 * g];
-                }
-                for (int t = 0; t < S; ++t) {
-                    const half8 bw = Q8 ? q8_unpack(wq[j][t][b / 2][2 * (b % 2)], wq[j][t][b / 2][2 * (b % 2) + 1])
-                                        : q4_unpack(wq[j][t][0][b]);
-                    const float dw = (float) __builtin_bit_cast(half4v, ws[j][t])[b] * m;
+            // block b's MFMAs are issued before block b - 1's scale FMAs (the same FMAs in the same order per output,
+            // so the same sums), so a block's matrix-core latency is spent on the previous block's VALU work
+            floatx4 is[2][S][MT], dxs[2][MT];
+            float dws[2][S];
+            for (int b = 0; b < 5; ++b) {
+                if (b < 4) {
+                    half8 A[MT];
+                    floatx4 cr[MT];
                     for (int mt = 0; mt < MT; ++mt) {
-                        const floatx4 isum = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], bw, cr[mt], 0, 0, 0);
-                        for (int v = 0; v < 4; ++v) acc[t][mt][v] = __builtin_fmaf(isum[v], dw * dx[mt][v], acc[t][mt][v]);
+                        A[mt] = *(const half8*) &s_act[(li * MT + mt) * 4 + b][16 * lane];
+                        dxs[b & 1][mt] = *(const floatx4*) &s_k[li][mt][0][b * 16 + 4 * g];
+                        cr[mt] = *(const floatx4*) &s_k[li][mt][1][b * 16 + 4 * g];
+                    }
+                    for (int t = 0; t < S; ++t) {
+                        const half8 bw = Q8 ? q8_unpack(wq[j][t][b / 2][2 * (b % 2)], wq[j][t][b / 2][2 * (b % 2) + 1])
+                                            : q4_unpack(wq[j][t][0][b]);
+                        dws[b & 1][t] = (float) __builtin_bit_cast(half4v, ws[j][t])[b] * m;
+                        for (int mt = 0; mt < MT; ++mt)
+                            is[b & 1][t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], bw, cr[mt], 0, 0, 0);
                     }
                 }
+                if (b > 0) {
+                    const int pb = (b - 1) & 1;
+                    for (int t = 0; t < S; ++t)
+                        for (int mt = 0; mt < MT; ++mt)
+                            for (int v = 0; v < 4; ++v)
+                                acc[t][mt][v] = __builtin_fmaf(is[pb][t][mt][v], dws[pb][t] * dxs[pb][mt][v], acc[t][mt][v]);
+                }
             }
+            // the group's sums are complete here (left to the compiler, they sank below the next loads)
+            for (int t = 0; t < S; ++t)
+                for (int mt = 0; mt < MT; ++mt) asm volatile("" : "+v"(acc[t][mt]));
             __builtin_amdgcn_sched_barrier(0);
             wload(j, i + D);
         }
-    for (int t = 0; t < S; ++t) {
-        const int stripe = s0 + t, col = stripe * 16 + n_in;
-        if (stripe >= a.nstripes || col >= a.N) continue;
+    // the sums out through LDS (the activation's space, once every wavefront is done with it): each wavefront's
+    // [16 MT rows][16 S columns] tile is written back as 16-byte pieces of rows, part[slice][row][col]
+    __syncthreads();
+    constexpr int TW = 16 * S + 4;  // (a tile row's floats, padded)
+    static_assert(4 * 16 * MT * TW * 4 <= NF * 1024, "the tiles fit the activation's LDS");
+    float* tile = (float*) &s_act[0][0] + wave * 16 * MT * TW;
+    for (int t = 0; t < S; ++t)
         for (int mt = 0; mt < MT; ++mt)
-            for (int v = 0; v < 4; ++v) {
-                const int row = (mt0 + mt) * 16 + 4 * g + v;
-                if (row < a.M) a.part[((size_t) slice * a.M + row) * a.N + col] = acc[t][mt][v];
-            }
+            for (int v = 0; v < 4; ++v) tile[(mt * 16 + 4 * g + v) * TW + 16 * t + n_in] = acc[t][mt][v];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the tile is written (it is this wavefront's own)
+    __builtin_amdgcn_wave_barrier();
+    for (int e = lane; e < 16 * MT * 4 * S; e += 64) {
+        const int r = e / (4 * S), c4 = (e % (4 * S)) * 4;
+        const int row = mt0 * 16 + r, col = s0 * 16 + c4;
+        if (row >= a.M || col >= a.N) continue;  // (a stripe past the matrix is not stored)
+        const float4 v = *(const float4*) &tile[r * TW + c4];
+        float* dst = &a.part[((size_t) slice * a.M + row) * a.N + col];
+        if (a.N % 4 == 0) {
+            *(float4*) dst = v;
+        } else {  // (a ragged N: rows are not 16-byte aligned, and the last piece may cross the row's end)
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+            for (int q = 0; q < 4; ++q)
+                if (col + q < a.N) dst[q] = vv[q];
+        }
     }
     if constexpr (FE != FE_NONE) {
         // this workgroup's sums have reached the L2 (vmcnt counts stores); then it counts itself, and the count's
@@ -1025,7 +1055,6 @@ static bool launch_gemm_s(int mt, int spw, int D, int gps, dim3 grid, const Gemm
     if constexpr (WT == WT_Q4_0) {
         GSX(1, 1, 4, 4) GSX(1, 1, 4, 8) GSX(2, 1, 4, 4)
         GSX(1, 2, 2, 4) GSX(1, 2, 2, 8) GSX(1, 2, 4, 8) GSX(2, 2, 2, 4) GSX(2, 2, 2, 8) GSX(2, 2, 4, 4)
-        GSX(1, 4, 2, 4) GSX(1, 4, 2, 8) GSX(2, 4, 2, 4)
     }
 #undef GSX
     return false;
@@ -1102,9 +1131,7 @@ static bool launch_gemm_fe(int mt, int spw, int gps, dim3 grid, const GemmArgs& 
         hipLaunchKernelGGL((k_q4_gemm_s<WT, MT_, S_, 2, GM_, FE>), grid, dim3(256), 0, st, a);               \
         return true;                                                                                         \
     }
-    if constexpr (WT == WT_Q4_0 && FE >= FE_ROPE) {  // (q|k|v: one row tile a workgroup below 1024 stripes)
-        GSF(1, 2, 4) GSF(1, 2, 8)
-    } else if constexpr (WT == WT_Q4_0) {
+    if constexpr (WT == WT_Q4_0) {
         GSF(1, 2, 4) GSF(1, 2, 8) GSF(2, 2, 4) GSF(2, 2, 8)
     } else if constexpr (FE < FE_ROPE) {  // (Q8_0 tiles: one stripe a wavefront; a set is one Q8_0 block of F)
         GSF(1, 1, 4) GSF(1, 1, 8) GSF(2, 1, 4) GSF(2, 1, 8)
@@ -1133,7 +1160,6 @@ static bool fused_shape(int M, int N, int K, int wt, int fe, int nxcd, int cnt_l
     }
     const int mtiles = (M + 15) / 16;
     mt = std::min(p.smt, mtiles);
-    if (fe == FE_ROPE && mt != 1) return false;  // (the instances)
     const int sets = (p.nstripes + 4 * spw - 1) / (4 * spw);
     grid = dim3((sets + nxcd - 1) / nxcd * nxcd, p.ks, (mtiles + mt - 1) / mt);
     return (long) grid.x * grid.z <= cnt_len;
@@ -1167,12 +1193,11 @@ int q4_gemm_fused(const uint8_t* w, const uint8_t* xa, int M, int N, int K, floa
     auto go = [&](auto fe_c) {
         constexpr int F0 = decltype(fe_c)::value;
         if (wt == WT_Q8_0) {
-            if constexpr (F0 == FE_SWIGLU) {
+            if constexpr (F0 == FE_SWIGLU) {  // (SwiGLU: at most 8 slices, fused_shape)
                 if (lk == 0) ok = launch_gemm_fe<WT_Q8_0, F0>(mt, spw, p.gps, grid, a, st);
                 else if (lk == 1) ok = launch_gemm_fe<WT_Q8_0, F0 + 1>(mt, spw, p.gps, grid, a, st);
                 else if (lk == 2) ok = launch_gemm_fe<WT_Q8_0, F0 + 2>(mt, spw, p.gps, grid, a, st);
                 else if (lk == 3) ok = launch_gemm_fe<WT_Q8_0, F0 + 3>(mt, spw, p.gps, grid, a, st);
-                else ok = launch_gemm_fe<WT_Q8_0, F0 + 4>(mt, spw, p.gps, grid, a, st);
             }
             return;
         }
@@ -1180,7 +1205,7 @@ int q4_gemm_fused(const uint8_t* w, const uint8_t* xa, int M, int N, int K, floa
         else if (lk == 1) ok = launch_gemm_fe<WT_Q4_0, F0 + 1>(mt, spw, p.gps, grid, a, st);
         else if (lk == 2) ok = launch_gemm_fe<WT_Q4_0, F0 + 2>(mt, spw, p.gps, grid, a, st);
         else if (lk == 3) ok = launch_gemm_fe<WT_Q4_0, F0 + 3>(mt, spw, p.gps, grid, a, st);
-        else ok = launch_gemm_fe<WT_Q4_0, F0 + 4>(mt, spw, p.gps, grid, a, st);
+        else if constexpr (F0 == FE_ROPE) ok = launch_gemm_fe<WT_Q4_0, F0 + 4>(mt, spw, p.gps, grid, a, st);
     };
     if (fe == FE_SWIGLU) go(std::integral_constant<int, FE_SWIGLU>{});
     else go(std::integral_constant<int, FE_ROPE>{});

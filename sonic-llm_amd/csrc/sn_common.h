@@ -21,6 +21,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short) 0, (int) bytes, RSRC_WORD3);
 }
+typedef __attribute__((address_space(3))) void* lds_ptr;  // an LDS address (buffer loads straight into LDS)
 __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int vo, int so) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
 }
