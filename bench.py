@@ -7,11 +7,12 @@ quantized to Q4_0 with ggml's reference quantizer; fp32 embedding and norms; unt
 hold), one new token per sequence per step, greedy argmax fed back as the next token. A step is one sn_step call of 32
 rows: inputs resident on the GPU, one host round trip (the 32 tokens back).
 
-Output: one JSON line. `value` = 32 * steps / wall time of the timed steps. `roofline` is the kernel class that takes
-the most GPU time in a separate profiled pass of the same steps (HIP events around every launch on the engine's
-stream), its algorithmic bytes / time against 8 TB/s; `roofline_gemm` is the Q4_0 matmul's (the metric's "Q4_0 GEMV %
-HBM peak"). `cpu_baseline` times the oracle (oracle/, a C restatement of ggml's CPU semantics) on the host cores for
-one step of the same workload.
+Output: one JSON line. `value` = 32 * steps / wall time of the timed steps. `roofline` is the Q4_0 matmul class (the
+metric's "Q4_0 GEMV % HBM peak"): its algorithmic bytes / time against 8 TB/s in a separate profiled pass of the same
+steps (HIP events around every launch on the engine's stream); `roofline_dominant` is the class with the most GPU time
+a step (paged attention). `cpu_baseline` times the oracle (oracle/, a C restatement of ggml's CPU semantics) on the
+host cores for one step of the same workload. The default run ends the line with a short summary of configs[0], [1],
+[3], [4] and the prompt rows (`configs`); every configuration's full line goes to stderr.
 """
 import argparse
 import json
@@ -146,11 +147,17 @@ def main():
     if args.config in ("decode", "moe"):
         print(json.dumps(bench_decode(args, moe=args.config == "moe")), flush=True)
         return
-    # all: the headline with the other configurations' lines inside it
+    # all: the headline with a short summary of the other configurations at the end of its line (each
+    # configuration's full line, and the headline's own, go to stderr)
     line = bench_decode(args, moe=False)
+    log("[bench] headline full line " + json.dumps(line))
+    line["kernels"] = {k: {"ms_per_step": v["ms_per_step"], "frac": v["frac"]} for k, v in line["kernels"].items()}
     t = time.time()
     try:
-        line["gemm_shapes"] = {name: matmul_shape(*mnk, seed=3) for name, mnk in DECODE_SHAPES.items()}
+        shapes = {name: matmul_shape(*mnk, seed=3) for name, mnk in DECODE_SHAPES.items()}
+        log("[bench] gemm_shapes " + json.dumps(shapes))
+        line["gemm_shapes"] = {n: {"us": v["us_per_launch"], "read_floor_us": v["read_floor_us"], "frac": v["frac"]}
+                               for n, v in shapes.items()}
     except Exception as e:
         import traceback
         traceback.print_exc()
@@ -161,13 +168,30 @@ def main():
                      ("c5_moe", lambda a: bench_decode(a, moe=True)), ("f1_prefill", bench_prefill)):
         t = time.time()
         try:
-            line["configs"][name] = fn(args)
+            full = fn(args)
+            log(f"[bench] {name} full line " + json.dumps(full))
+            line["configs"][name] = summary(full)
         except Exception as e:  # (the headline stands; the failure is reported in its place)
             import traceback
             traceback.print_exc()
             line["configs"][name] = {"error": repr(e)}
         log(f"[bench] {name} in {time.time() - t:.1f}s")
     print(json.dumps(line), flush=True)
+
+
+def summary(full):
+    """A configuration's line cut to its figures: value, time, the roofline fraction and the CPU baseline"""
+    r = full.get("roofline") or {}
+    cpu = full.get("cpu_baseline") or {}
+    out = {"metric": full.get("metric"), "value": full.get("value"), "unit": full.get("unit"),
+           "ms_per_step": full.get("ms_per_step"), "roofline": {k: r.get(k) for k in ("kernel", "bound", "frac", "unit",
+                                                                                    "achieved", "traffic")}}
+    if "us_per_launch" in full:
+        out["us_per_launch"] = full["us_per_launch"]
+    if cpu:
+        out["cpu_baseline"] = {"value": cpu.get("value"), "unit": cpu.get("unit"), "cores": cpu.get("cores"),
+                               "kind": cpu.get("kind")}
+    return out
 
 
 def bench_decode(args, moe):
@@ -282,8 +306,10 @@ def bench_decode(args, moe):
                       if moe else {}),
                    "gpu_ms_per_step": round(gpu_ms / args.steps, 4), "chain": bool(use_chain),
                    "token_table": "Q6_K, tied LM head" if tied else f"F32, untied {q} LM head"},
-        "roofline": roof(dom) if dom else None,
-        "roofline_gemm": roof("gemm") if "gemm" in kernels else None,
+        # the metric names the Q4_0 GEMV's fraction of HBM peak: that class is the line's roofline; the class with the
+        # most time a step (paged attention) is roofline_dominant
+        "roofline": roof("gemm") if "gemm" in kernels else None,
+        "roofline_dominant": roof(dom) if dom else None,
         "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
         "cpu_baseline": cpu,
     }

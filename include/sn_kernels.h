@@ -156,6 +156,14 @@ int snk_moe_tile_rows(int R, int NE, int k);
 // NE <= 256, k <= min(8, NE), R k <= 4096. 0, or -1 (bad arguments, nothing launched).
 int snk_moe_select(const float* d_lg, int R, int NE, int k, int32_t* d_ids, float* d_w, int32_t* d_prow,
                    int32_t* d_rsrc, int32_t* d_items, int32_t* d_count, void* stream);
+// The routing in one launch (router logits, top-k with renormalised weights, the expert-major tiles), the same results
+// as snk_moe_router followed by snk_moe_select: each block of 4 rows is routed by the last of its workgroups to finish,
+// whose logits it reads through its XCD's L2, and the last block groups every pair. Allocates and frees its counters
+// and probes the XCD dealing (synchronous; for tests). *xerr (optional): 1 when a row block's workgroups ran on more
+// than one XCD. 0, or -1.
+int snk_moe_route(const float* d_hn, int R, int E, const float* d_router, int NE, int k, float* d_lg, int32_t* d_ids,
+                  float* d_w, int32_t* d_prow, int32_t* d_rsrc, int32_t* d_items, int32_t* d_count, int* xerr,
+                  void* stream);
 // the grouped expert matmul (the block matmul's grouped mode, kernels.metal:561-563; sn_attn.inc.h:350-358): for each
 // tile i < *d_count, item (x, t) = d_items[2i], d_items[2i + 1]: rows 16t .. 16t + 15 of d_part [P][N] = the
 // activation operand's rows (d_xa, P rows of K, snk_quant_act) x expert x's matrix (N x K tiles at d_w + x * wstride;

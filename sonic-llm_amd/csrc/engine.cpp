@@ -97,6 +97,7 @@ struct sn_engine {
     bool fuse = false, fuse_ok = false;
     int nxcd = 1;
     uint64_t* d_fcnt = nullptr;
+    int32_t* d_gcnt = nullptr;  // the one-launch MoE routing's system-scope counter
     float2* rope_cs = nullptr;  // a step's rotation table (rope_table) [max_rows][64]
     int32_t* d_xerr = nullptr;
     int fcnt_len = 0;
@@ -581,8 +582,9 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     e->fcnt_len = 1 << 16;
     e->d_fcnt = e->dalloc<uint64_t>((size_t) e->fcnt_len * 8, err, err_len);
     e->d_xerr = e->dalloc<int32_t>(4, err, err_len);
-    if (!e->d_fcnt || !e->d_xerr || hipMemset(e->d_fcnt, 0, (size_t) e->fcnt_len * 8) != hipSuccess ||
-        hipMemset(e->d_xerr, 0, 4) != hipSuccess)
+    e->d_gcnt = e->dalloc<int32_t>(4, err, err_len);
+    if (!e->d_fcnt || !e->d_xerr || !e->d_gcnt || hipMemset(e->d_fcnt, 0, (size_t) e->fcnt_len * 8) != hipSuccess ||
+        hipMemset(e->d_xerr, 0, 4) != hipSuccess || hipMemset(e->d_gcnt, 0, 4) != hipSuccess)
         return fail("fused-epilogue counters");
     e->rope_cs = e->dalloc<float2>((size_t) std::max(R, slots) * 64 * sizeof(float2), err, err_len);
     if (!e->rope_cs) return fail("");
@@ -1059,6 +1061,9 @@ struct Dev {
             return resid_quant(x, e->gemm_ws, ks, R, E, l.ffn_norm, e->eps, e->xa, st, true, e->hn);
         });
         rc |= e->launch(SNX_K_OTHER, (double) NE * E * 4 + (double) R * E * 4, [&] {
+            if (e->fuse)  // (one launch: the same results)
+                return moe_route(e->hn, l.router, R, E, NE, NU, P, e->rlog, e->mid, e->mw, e->prow, e->rsrc, e->gitems,
+                                 e->gcount, e->d_fcnt, e->fcnt_len, e->d_gcnt, e->d_xerr, e->nxcd, st);
             moe_router(e->hn, l.router, R, E, NE, e->rlog, st);
             return moe_select(e->rlog, R, NE, NU, P, e->mid, e->mw, e->prow, e->rsrc, e->gitems, e->gcount, st);
         });

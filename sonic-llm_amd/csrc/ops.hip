@@ -579,10 +579,9 @@ void cut_cells(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int CL, in
 // of the wavefront is 1 KB contiguous), then the 64 lanes are added by a fixed xor tree: the order of a row's sum
 // depends on E alone, not on the other rows.
 #define RT_ROWS 4
-__global__ __launch_bounds__(256) void k_router(const float* __restrict__ hn, const float* __restrict__ router, int R,
-                                                int E, int NE, float* __restrict__ out) {
-    const int lane = threadIdx.x & 63, x = blockIdx.x * 4 + (threadIdx.x >> 6), r0 = blockIdx.y * RT_ROWS;
-    if (x >= NE) return;
+// expert x's logits of rows r0 .. r0 + RT_ROWS - 1 (one wavefront; lane 0 writes them)
+__device__ __forceinline__ void router_dot(const float* __restrict__ hn, const float* __restrict__ router, int R, int E,
+                                           int NE, float* __restrict__ out, int x, int r0, int lane) {
     const float* wr = router + (size_t) x * E;
     float s[RT_ROWS];
     for (int i = 0; i < RT_ROWS; ++i) s[i] = 0.0f;
@@ -598,20 +597,33 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ hn, co
         for (int i = 0; i < RT_ROWS; ++i)
             if (r0 + i < R) out[(size_t) (r0 + i) * NE + x] = s[i];
 }
+__global__ __launch_bounds__(256) void k_router(const float* __restrict__ hn, const float* __restrict__ router, int R,
+                                                int E, int NE, float* __restrict__ out) {
+    const int lane = threadIdx.x & 63, x = blockIdx.x * 4 + (threadIdx.x >> 6), r0 = blockIdx.y * RT_ROWS;
+    if (x >= NE) return;
+    router_dot(hn, router, R, E, NE, out, x, r0, lane);
+}
 
 // Routing of a row (moe_topk1, kernels.metal:3419-3467): softmax of its NE <= 256 logits, the k <= 8 largest (ties: the
 // lower id), weights p / sum(p) renormalised by their own sum floored at 6.103515625e-5. Workgroup per row, thread per
 // expert: the max and the sum by workgroup reductions (an order fixed by NE), then each expert's rank (the experts
 // before it in probability-descending, id-ascending order) counted against the row's probabilities in LDS; ranks below
 // k are the picks. A NaN probability ranks below every number, so the ids are always k distinct experts of [0, NE).
-__global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ lg, int NE, int k, int32_t* __restrict__ ids,
-                                                  float* __restrict__ w) {
-    __shared__ __attribute__((aligned(16))) float sp[256];
-    __shared__ float red[2][4];
-    __shared__ int spick[8];
-    __shared__ float sprob[8];
-    const int r = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const float l = t < NE ? lg[(size_t) r * NE + t] : -INFINITY;
+struct TopkShared {
+    __attribute__((aligned(16))) float sp[256];
+    float red[2][4];
+    int spick[8];
+    float sprob[8];
+};
+// row r's routing by the 256 threads t = 0..255 of a part of the workgroup (its own TopkShared); l: this thread's logit
+// (expert t; -inf past NE). Every part of the workgroup passes the same barriers.
+__device__ __forceinline__ void moe_topk_row(TopkShared& sh, float l, int r, int t, int NE, int k,
+                                             int32_t* __restrict__ ids, float* __restrict__ w) {
+    float* sp = sh.sp;
+    float (*red)[4] = sh.red;
+    int* spick = sh.spick;
+    float* sprob = sh.sprob;
+    const int lane = t & 63, wave = t >> 6;
     float m = l;
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     if (lane == 0) red[0][wave] = m;
@@ -652,6 +664,12 @@ __global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ lg, 
         }
     }
 }
+__global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ lg, int NE, int k, int32_t* __restrict__ ids,
+                                                  float* __restrict__ w) {
+    __shared__ TopkShared sh;
+    const int r = blockIdx.x, t = threadIdx.x;
+    moe_topk_row(sh, t < NE ? lg[(size_t) r * NE + t] : -INFINITY, r, t, NE, k, ids, w);
+}
 
 // The (row, slot) pairs in expert-major tiles of 16 rows (moe_lists, kernels.metal:3468-3497), deterministically: expert
 // x's pairs take tiles toff[x] .. in (row, slot) order. prow[r][j] = the pair's row in that layout; rsrc[p] = the row
@@ -661,16 +679,25 @@ __global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ lg, 
 // its total gives the tile offsets (a wavefront prefix over experts); then each wavefront walks its chunk 64 pairs at
 // a time, a pair's place = its chunk's place for the expert + the earlier pairs of the 64 with that expert.
 #define MOE_MAX_PAIRS 4096
-__global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ ids, int RK, int NE, int P, int k,
-                                                    int32_t* __restrict__ prow, int32_t* __restrict__ rsrc,
-                                                    int32_t* __restrict__ items, int32_t* __restrict__ count) {
-    __shared__ int sid[MOE_MAX_PAIRS];
-    __shared__ int hist[16][256];  // [chunk][expert]: counts, then the chunk's next place for the expert
-    __shared__ int cnt[256], toff[257];
+struct GroupShared {
+    int sid[MOE_MAX_PAIRS];
+    int hist[16][256];  // [chunk][expert]: counts, then the chunk's next place for the expert
+    int cnt[256], toff[257];
+};
+// by a workgroup of 1024 threads; SYS: the ids were written on other XCDs in this launch (system-coherent loads)
+template <bool SYS>
+__device__ __forceinline__ void moe_group(GroupShared& sh, const int32_t* __restrict__ ids, int RK, int NE, int P,
+                                          int k, int32_t* __restrict__ prow, int32_t* __restrict__ rsrc,
+                                          int32_t* __restrict__ items, int32_t* __restrict__ count) {
+    int* sid = sh.sid;
+    int (*hist)[256] = sh.hist;
+    int* cnt = sh.cnt;
+    int* toff = sh.toff;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     for (int i = t; i < 16 * 256; i += 1024) (&hist[0][0])[i] = 0;
     for (int p = t; p < P; p += 1024) rsrc[p] = -1;
-    for (int q = t; q < RK; q += 1024) sid[q] = ids[q];
+    for (int q = t; q < RK; q += 1024)
+        sid[q] = SYS ? __hip_atomic_load(ids + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) : ids[q];
     __syncthreads();
     const int C = (RK + 15) / 16, q0 = wave * C, q1 = min(RK, q0 + C);
     for (int q = q0 + lane; q < q1; q += 64) atomicAdd(&hist[wave][sid[q]], 1);
@@ -732,12 +759,97 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ 
             items[2 * i + 1] = i;
         }
 }
+__global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ ids, int RK, int NE, int P, int k,
+                                                    int32_t* __restrict__ prow, int32_t* __restrict__ rsrc,
+                                                    int32_t* __restrict__ items, int32_t* __restrict__ count) {
+    __shared__ GroupShared sh;
+    moe_group<false>(sh, ids, RK, NE, P, k, prow, rsrc, items, count);
+}
+
+// The whole routing in one launch (router, top-k and grouping; the same arithmetic as k_router, k_moe_topk and
+// k_moe_group): workgroup (row block b of RT_ROWS rows, expert block x of 16 experts), 16 wavefronts, each an expert's
+// logits of the block's rows (router_dot). The row block's workgroups are dealt to one XCD (grid x: the row blocks,
+// padded to a multiple of nxcd), so the last of them to count itself (an L2 atomic; 5-bit per-XCD fields flag a block
+// spread over XCDs in *xerr) reads their logits from that L2 and routes the block's rows, 256 threads a row
+// (moe_topk_row). It stores the rows' expert ids system-coherently and counts itself in a system-scope counter; the
+// last row block to do so reads every id the same way and groups the pairs (moe_group). Counters return to zero.
+__global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ hn, const float* __restrict__ router, int R,
+                                                    int E, int NE, int k, int P, float* __restrict__ lg,
+                                                    int32_t* __restrict__ ids, float* __restrict__ w,
+                                                    int32_t* __restrict__ prow, int32_t* __restrict__ rsrc,
+                                                    int32_t* __restrict__ items, int32_t* __restrict__ count,
+                                                    uint64_t* __restrict__ cnt, int32_t* __restrict__ gcnt,
+                                                    int32_t* __restrict__ xerr) {
+    __shared__ TopkShared tsh[RT_ROWS];
+    __shared__ GroupShared gsh;
+    __shared__ int s_last;
+    const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int nrb = (R + RT_ROWS - 1) / RT_ROWS, nxb = (int) gridDim.y;
+    if (b >= nrb) return;  // a padding row block
+    const int x = blockIdx.y * 16 + wave, r0 = b * RT_ROWS;
+    if (x < NE) router_dot(hn, router, R, E, NE, lg, x, r0, lane);
+    __builtin_amdgcn_s_waitcnt(0);  // the logits have reached the L2
+    __syncthreads();
+    if (t == 0) {
+        unsigned xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        const int f = 8 + 5 * (int) (xcc & 7);
+        const uint64_t add = 1ull + (1ull << f);
+        const uint64_t n = __hip_atomic_fetch_add(cnt + b, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+        s_last = (int) (n & 255) == nxb;
+        if (s_last) {
+            if ((int) ((n >> f) & 31) != nxb) __hip_atomic_fetch_or(xerr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_fetch_add(cnt + b, (uint64_t) 0 - n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // the row block's rows, a quarter of the workgroup each (a row past R: the last row again, not written), into LDS
+    __shared__ int32_t s_ids[RT_ROWS][8];
+    __shared__ float s_w[RT_ROWS][8];
+    {
+        const int q = t >> 8, tq = t & 255, r = min(r0 + q, R - 1);
+        const float l = tq < NE ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                      buf_rsrc(lg, (uint32_t) ((size_t) R * NE * 4)), (r * NE + tq) * 4, 0, 1))
+                                : -INFINITY;  // (sc0: past the CU's L1, from the L2 the logits are in)
+        moe_topk_row(tsh[q], l, 0, tq, NE, k, &s_ids[q][0], &s_w[q][0]);
+    }
+    __syncthreads();
+    // the rows' ids stored system-coherently (the last row block reads them from another XCD), their weights plainly
+    if (t < RT_ROWS * k && r0 + t / k < R) {
+        __hip_atomic_store(ids + r0 * k + t, s_ids[t / k][t % k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        w[r0 * k + t] = s_w[t / k][t % k];
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t == 0) {
+        const int n = __hip_atomic_fetch_add(gcnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        s_last = n == nrb - 1;
+        if (s_last) __hip_atomic_store(gcnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    moe_group<true>(gsh, ids, R * k, NE, P, k, prow, rsrc, items, count);
+}
 
 void moe_router(const float* hn, const float* router, int R, int E, int NE, float* lg, hipStream_t st) {
     if (R > 0)
         hipLaunchKernelGGL(k_router, dim3((NE + 3) / 4, (R + RT_ROWS - 1) / RT_ROWS), dim3(256), 0, st, hn, router, R,
                            E, NE, lg);
 }
+int moe_route(const float* hn, const float* router, int R, int E, int NE, int k, int P, float* lg, int32_t* ids,
+              float* w, int32_t* prow, int32_t* rsrc, int32_t* items, int32_t* count, uint64_t* cnt, int cnt_len,
+              int32_t* gcnt, int32_t* xerr, int nxcd, hipStream_t st) {
+    if (R <= 0) return 0;
+    if (NE < 1 || NE > 256 || k < 1 || k > MOE_MAX_K || k > NE || R * k > MOE_MAX_PAIRS || E % 4 || nxcd < 1) return -1;
+    if (P < 16 * (std::min(NE, R * k) + (R * k + 15) / 16)) return -1;
+    const int nrb = (R + RT_ROWS - 1) / RT_ROWS, gx = (nrb + nxcd - 1) / nxcd * nxcd;
+    if (gx > cnt_len || (NE + 15) / 16 > 255) return -1;
+    hipLaunchKernelGGL(k_moe_route, dim3(gx, (NE + 15) / 16), dim3(1024), 0, st, hn, router, R, E, NE, k, P, lg, ids, w,
+                       prow, rsrc, items, count, cnt, gcnt, xerr);
+    return 0;
+}
+
 int moe_select(const float* lg, int R, int NE, int k, int P, int32_t* ids, float* w, int32_t* prow, int32_t* rsrc,
                int32_t* items, int32_t* count, hipStream_t st) {
     if (R <= 0) return 0;

@@ -1533,23 +1533,24 @@ extern "C" int snk_q4_dequant(const void* d_stripes, int N, int K, float* d_w, v
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// A plain streaming read of `n4` 16-byte words (every word loaded once, grid-stride, the sum kept live by a store that
-// only a sum of exactly 1234.5 makes): the time this box takes to read a buffer of that size in one launch, the floor
-// against which a matmul of the same weight bytes is measured.
+// A plain streaming read of `n4` 16-byte words: every lane loads RF words 4 KB apart, all issued before any is used,
+// one workgroup per 256 x RF words, so every load of the launch is in flight at once (16 KB a workgroup; the sum is kept
+// live by a store that only a sum of exactly 1234.5 makes). The time this box takes to read a buffer of that size in
+// one launch: the floor against which a matmul of the same weight bytes is measured.
+#define RF 4
 __global__ __launch_bounds__(256) void k_read_floor(const float4* __restrict__ src, size_t n4, float* __restrict__ sink) {
+    float4 v[RF];
+    const size_t base = (size_t) blockIdx.x * 256 * RF + threadIdx.x;
+    for (int r = 0; r < RF; ++r) v[r] = src[min(base + 256 * r, n4 - 1)];
     float s = 0.0f;
-    for (size_t i = (size_t) blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t) gridDim.x * 256) {
-        const float4 v = src[i];
-        s += (v.x + v.y) + (v.z + v.w);
-    }
+    for (int r = 0; r < RF; ++r) s += (v[r].x + v[r].y) + (v[r].z + v[r].w);
     if (s == 1234.5f) sink[threadIdx.x] = s;
 }
 
 void read_floor(const void* buf, size_t bytes, float* sink, hipStream_t st) {
     const size_t n4 = bytes / 16;
-    // about 8 words a thread, at least one round and at most 8 rounds of 256 workgroups
-    const int grid = (int) std::min<size_t>(2048, std::max<size_t>(256, n4 / (256 * 8)));
-    hipLaunchKernelGGL(k_read_floor, dim3(grid), dim3(256), 0, st, (const float4*) buf, n4, sink);
+    const size_t grid = (n4 + 256 * RF - 1) / (256 * RF);
+    hipLaunchKernelGGL(k_read_floor, dim3((unsigned) grid), dim3(256), 0, st, (const float4*) buf, n4, sink);
 }
 
 __global__ void k_mfma_probe(const half8* a, const half8* b, floatx4* d) {

@@ -277,6 +277,13 @@ void moe_router(const float* hn, const float* router, int R, int E, int NE, floa
 // 16 (min(NE, R k) + ceil(R k / 16)); -1 otherwise (nothing launched).
 int moe_select(const float* lg, int R, int NE, int k, int P, int32_t* ids, float* w, int32_t* prow, int32_t* rsrc,
                int32_t* items, int32_t* count, hipStream_t st);
+// moe_router + moe_select in one launch, the same results: the row blocks' logits, then each block's routing by the
+// block's last workgroup (an XCD-local handoff: the launch's workgroups are dealt to nxcd XCDs in turn), then the
+// grouping by the last block (a system-coherent handoff). cnt: cnt_len 64-bit counters, gcnt one, both zero between
+// launches; *xerr set when a row block's workgroups ran on more than one XCD. -1 otherwise (nothing launched).
+int moe_route(const float* hn, const float* router, int R, int E, int NE, int k, int P, float* lg, int32_t* ids,
+              float* w, int32_t* prow, int32_t* rsrc, int32_t* items, int32_t* count, uint64_t* cnt, int cnt_len,
+              int32_t* gcnt, int32_t* xerr, int nxcd, hipStream_t st);
 // x[r] += sum_j w[r][j] y[prow[r][j]] (slot order)
 // x[r] += the MoE output of row r (sum over its k slots, in slot order, of w[r][j] * y[prow[r][j]]: y the grouped down
 // matmul's rows) and then, when xa is given, the RMSNorm (nw) + Q8_0 operand of the new rows, in one launch (one

@@ -44,6 +44,34 @@ extern "C" int snk_moe_select(const float* d_lg, int R, int NE, int k, int32_t* 
     return rc == 0 && hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// moe_route through a throwaway set of counters: the one-launch routing (same results as snk_moe_router +
+// snk_moe_select); *xerr (optional) receives the XCD check
+extern "C" int snk_moe_route(const float* d_hn, int R, int E, const float* d_router, int NE, int k, float* d_lg,
+                             int32_t* d_ids, float* d_w, int32_t* d_prow, int32_t* d_rsrc, int32_t* d_items,
+                             int32_t* d_count, int* xerr, void* stream) {
+    hipStream_t st = (hipStream_t) stream;
+    int nxcd = 1;
+    if (!xcd_round_robin(st, &nxcd)) return -1;
+    const int cnt_len = 1024;
+    uint64_t* cnt = nullptr;
+    int32_t* gx = nullptr;  // [0] the global counter, [1] the XCD check
+    if (hipMalloc(&cnt, cnt_len * 8) != hipSuccess) return -1;
+    if (hipMalloc(&gx, 8) != hipSuccess) {
+        hipFree(cnt);
+        return -1;
+    }
+    int rc = hipMemsetAsync(cnt, 0, cnt_len * 8, st) == hipSuccess && hipMemsetAsync(gx, 0, 8, st) == hipSuccess ? 0 : -1;
+    if (rc == 0)
+        rc = moe_route(d_hn, d_router, R, E, NE, k, snk_moe_tile_rows(R, NE, k), d_lg, d_ids, d_w, d_prow, d_rsrc,
+                       d_items, d_count, cnt, cnt_len, gx, gx + 1, nxcd, st);
+    int32_t h[2] = {0, 0};
+    if (hipStreamSynchronize(st) != hipSuccess || hipMemcpy(h, gx, 8, hipMemcpyDeviceToHost) != hipSuccess) rc = -1;
+    if (xerr) *xerr = h[1];
+    hipFree(cnt);
+    hipFree(gx);
+    return rc == 0 && hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 extern "C" int snk_gemm_grouped(int wt, const void* d_w, size_t wstride, const int32_t* d_items,
                                 const int32_t* d_count, int max_items, const void* d_xa, int P, int N, int K,
                                 float* d_part, size_t part_bytes, const int32_t* d_rmask, void* stream) {

@@ -130,6 +130,7 @@ SNK_API = [
     ("snk_moe_router", I, [P, I, I, P, I, P, P]),
     ("snk_moe_tile_rows", I, [I, I, I]),
     ("snk_moe_select", I, [P, I, I, I, P, P, P, P, P, P, P]),
+    ("snk_moe_route", I, [P, I, I, P, I, I, P, P, P, P, P, P, P, P, P]),
     ("snk_gemm_grouped", I, [I, P, C.c_size_t, P, P, I, P, I, I, I, P, C.c_size_t, P, P]),
     ("snk_argmax_workspace_bytes", C.c_size_t, [I, I]),
     ("snk_argmax", I, [P, I, I, P, I, P, P, P, P, C.c_size_t, P]),

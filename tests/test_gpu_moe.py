@@ -4,6 +4,8 @@ weights, Q4_0 expert matmuls with ggml's Q8_0 activations, the weighted sum in s
 oracle's top-2 gap exceeds the model's logit bound. A row's expert grouping depends on the other rows of the step (which
 rows share an expert, where its tile falls); its logits must not: row invariance is checked bit for bit.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -184,6 +186,41 @@ def test_moe_select_matches_oracle(R, NE, k):
         np.testing.assert_allclose(w[i], ow, rtol=1e-5, atol=1e-7)
     wp, wr, wi, wn = grouping(ids, NE, k, P)
     assert n == wn and np.array_equal(prow, wp) and np.array_equal(rsrc, wr) and np.array_equal(items, wi)
+
+
+@pytest.mark.parametrize("R,E,NE,k", [(32, 2048, 128, 8), (5, 256, 16, 4), (100, 96, 64, 8), (3, 64, 8, 8),
+                                      (40, 32, 6, 2), (1, 2048, 128, 8)])
+def test_moe_route_one_launch_equals_router_and_select(R, E, NE, k):
+    """The one-launch routing (the row blocks' logits, each block routed by its last workgroup through its XCD's L2,
+    the grouping by the last block) against snk_moe_router + snk_moe_select: logits, ids, weights and the tile layout
+    bit for bit, with no row block's workgroups found on two XCDs."""
+    L = S.lib()
+    r = np.random.default_rng(R * 7 + NE)
+    hn = r.standard_normal((R, E)).astype(np.float32)
+    rw = (r.standard_normal((NE, E)) * 0.05).astype(np.float32)
+    if NE >= 8:
+        rw[3:7] = rw[3]  # ties among the logits
+    dh, dr = U.dev(hn), U.dev(rw)
+    lg = U.empty(R * NE * 4)
+    assert L.snk_moe_router(U.ptr(dh), R, E, U.ptr(dr), NE, U.ptr(lg), U.stream()) == 0
+    want = select_gpu(U.host(lg, np.float32)[:R * NE].reshape(R, NE), k)
+    P = L.snk_moe_tile_rows(R, NE, k)
+    for rep in range(3):  # (the counters return to zero: later launches alike)
+        lg2 = U.empty(R * NE * 4)
+        ids, w, prow = U.empty(R * k * 4), U.empty(R * k * 4), U.empty(R * k * 4)
+        rsrc, items, cnt = U.empty(P * 4), U.empty(P // 16 * 8), U.empty(4)
+        xerr = C.c_int(-1)
+        assert L.snk_moe_route(U.ptr(dh), R, E, U.ptr(dr), NE, k, U.ptr(lg2), U.ptr(ids), U.ptr(w), U.ptr(prow),
+                               U.ptr(rsrc), U.ptr(items), U.ptr(cnt), C.byref(xerr), U.stream()) == 0
+        assert xerr.value == 0
+        assert np.array_equal(U.host(lg2, np.uint32)[:R * NE], U.host(lg, np.uint32)[:R * NE])
+        n = int(U.host(cnt, np.int32)[0])
+        got = (U.host(ids, np.int32)[:R * k].reshape(R, k), U.host(w, np.float32)[:R * k].reshape(R, k),
+               U.host(prow, np.int32)[:R * k].reshape(R, k), U.host(rsrc, np.int32)[:P],
+               U.host(items, np.int32)[:2 * n].reshape(n, 2), n)
+        for a, b in zip(got, want[:6]):
+            a, b = np.asarray(a), np.asarray(b)
+            assert a.shape == b.shape and np.array_equal(a.view(np.uint8) if a.ndim else a, b.view(np.uint8) if b.ndim else b)
 
 
 def test_moe_select_rejects_bad_shapes():
