@@ -160,7 +160,7 @@ int snk_moe_select(const float* d_lg, int R, int NE, int k, int32_t* d_ids, floa
 // as snk_moe_router followed by snk_moe_select: each block of 4 rows is routed by the last of its workgroups to finish,
 // whose logits it reads through its XCD's L2, and the last block groups every pair. Allocates and frees its counters
 // and probes the XCD dealing (synchronous; for tests). *xerr (optional): 1 when a row block's workgroups ran on more
-// than one XCD. 0, or -1.
+// than one XCD. E <= 4096 (wider rows: snk_moe_router + snk_moe_select). 0, or -1.
 int snk_moe_route(const float* d_hn, int R, int E, const float* d_router, int NE, int k, float* d_lg, int32_t* d_ids,
                   float* d_w, int32_t* d_prow, int32_t* d_rsrc, int32_t* d_items, int32_t* d_count, int* xerr,
                   void* stream);

@@ -1061,7 +1061,7 @@ struct Dev {
             return resid_quant(x, e->gemm_ws, ks, R, E, l.ffn_norm, e->eps, e->xa, st, true, e->hn);
         });
         rc |= e->launch(SNX_K_OTHER, (double) NE * E * 4 + (double) R * E * 4, [&] {
-            if (e->fuse)  // (one launch: the same results)
+            if (e->fuse && E <= MOE_ROUTE_EMAX)  // (one launch: the same results)
                 return moe_route(e->hn, l.router, R, E, NE, NU, P, e->rlog, e->mid, e->mw, e->prow, e->rsrc, e->gitems,
                                  e->gcount, e->d_fcnt, e->fcnt_len, e->d_gcnt, e->d_xerr, e->nxcd, st);
             moe_router(e->hn, l.router, R, E, NE, e->rlog, st);

@@ -574,142 +574,213 @@ void cut_cells(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int CL, in
 
 // ---- mixture of experts (moe_ffn, sn_layers.inc.h:129-144) -----------------------------------------------------------
 
-// Router logits [R][NE] = hn [R][E] (the normed rows) x router [NE][E] (fp32). Workgroup (4 experts, RT_ROWS rows),
-// a wavefront per expert: lane l sums elements 4l + 256j .. 4l + 256j + 3 of each of the rows, j ascending (each load
-// of the wavefront is 1 KB contiguous), then the 64 lanes are added by a fixed xor tree: the order of a row's sum
-// depends on E alone, not on the other rows.
-#define RT_ROWS 4
-// expert x's logits of rows r0 .. r0 + RT_ROWS - 1 (one wavefront; lane 0 writes them)
-__device__ __forceinline__ void router_dot(const float* __restrict__ hn, const float* __restrict__ router, int R, int E,
-                                           int NE, float* __restrict__ out, int x, int r0, int lane) {
-    const float* wr = router + (size_t) x * E;
-    float s[RT_ROWS];
-    for (int i = 0; i < RT_ROWS; ++i) s[i] = 0.0f;
-    for (int e0 = 4 * lane; e0 < E; e0 += 256) {
-        const float4 wv = *(const float4*) (wr + e0);
-        float4 hv[RT_ROWS];
-        for (int i = 0; i < RT_ROWS; ++i) hv[i] = *(const float4*) (hn + (size_t) min(r0 + i, R - 1) * E + e0);
-        for (int i = 0; i < RT_ROWS; ++i) s[i] += hv[i].x * wv.x + hv[i].y * wv.y + hv[i].z * wv.z + hv[i].w * wv.w;
-    }
-    for (int i = 0; i < RT_ROWS; ++i)
-        for (int o = 32; o > 0; o >>= 1) s[i] += __shfl_xor(s[i], o);
-    if (lane == 0)
-        for (int i = 0; i < RT_ROWS; ++i)
-            if (r0 + i < R) out[(size_t) (r0 + i) * NE + x] = s[i];
+// Wavefront reductions by DPP, to lane 63 (then read from it): pairs, quads, half rows, rows, then row 0 into row 1 and
+// row 2 into row 3, then rows 0-1 into rows 2-3. A fixed order: the sum of 64 values depends on their lanes alone.
+// (a lane of a row that ROWMASK leaves out keeps `old`)
+template <int CTRL, int ROWMASK = 0xF>
+__device__ __forceinline__ float dppf(float old, float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                                 __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xF, false));
 }
-__global__ __launch_bounds__(256) void k_router(const float* __restrict__ hn, const float* __restrict__ router, int R,
-                                                int E, int NE, float* __restrict__ out) {
-    const int lane = threadIdx.x & 63, x = blockIdx.x * 4 + (threadIdx.x >> 6), r0 = blockIdx.y * RT_ROWS;
-    if (x >= NE) return;
-    router_dot(hn, router, R, E, NE, out, x, r0, lane);
+__device__ __forceinline__ float lane63(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dppf<0xB1>(0.0f, v);        // quad_perm [1,0,3,2]
+    v += dppf<0x4E>(0.0f, v);        // quad_perm [2,3,0,1]
+    v += dppf<0x141>(0.0f, v);       // row_half_mirror
+    v += dppf<0x140>(0.0f, v);       // row_mirror
+    v += dppf<0x142, 0xA>(0.0f, v);  // row_bcast15 into rows 1, 3
+    v += dppf<0x143, 0xC>(0.0f, v);  // row_bcast31 into rows 2, 3
+    return lane63(v);
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dppf<0xB1>(v, v));
+    v = fmaxf(v, dppf<0x4E>(v, v));
+    v = fmaxf(v, dppf<0x141>(v, v));
+    v = fmaxf(v, dppf<0x140>(v, v));
+    v = fmaxf(v, dppf<0x142, 0xA>(v, v));
+    v = fmaxf(v, dppf<0x143, 0xC>(v, v));
+    return lane63(v);
 }
 
-// Routing of a row (moe_topk1, kernels.metal:3419-3467): softmax of its NE <= 256 logits, the k <= 8 largest (ties: the
-// lower id), weights p / sum(p) renormalised by their own sum floored at 6.103515625e-5. Workgroup per row, thread per
-// expert: the max and the sum by workgroup reductions (an order fixed by NE), then each expert's rank (the experts
-// before it in probability-descending, id-ascending order) counted against the row's probabilities in LDS; ranks below
-// k are the picks. A NaN probability ranks below every number, so the ids are always k distinct experts of [0, NE).
-struct TopkShared {
-    __attribute__((aligned(16))) float sp[256];
-    float red[2][4];
-    int spick[8];
-    float sprob[8];
-};
-// row r's routing by the 256 threads t = 0..255 of a part of the workgroup (its own TopkShared); l: this thread's logit
-// (expert t; -inf past NE). Every part of the workgroup passes the same barriers.
-__device__ __forceinline__ void moe_topk_row(TopkShared& sh, float l, int r, int t, int NE, int k,
-                                             int32_t* __restrict__ ids, float* __restrict__ w) {
-    float* sp = sh.sp;
-    float (*red)[4] = sh.red;
-    int* spick = sh.spick;
-    float* sprob = sh.sprob;
-    const int lane = t & 63, wave = t >> 6;
-    float m = l;
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if (lane == 0) red[0][wave] = m;
+// Router logits [R][NE] = hn [R][E] (the normed rows) x router [NE][E] (fp32). Workgroup of 4 wavefronts: 4 experts x
+// RT_ROWS rows, wavefront q a quarter of E for all 16 (expert, row) pairs. Lane l's part of a pair is, for its quarter,
+// the elements 4l + 256j .. 4l + 256j + 3 (j of the quarter ascending, each 256-element step a 1 KB load of the
+// wavefront); the four quarters' parts are added in order through LDS, then the 64 lanes by wave_sum. The order of a
+// row's sum depends on E alone, not on the other rows. Every load of a wavefront (JM / 4 float4 of each of 4 rows and 4
+// experts a lane, E <= 256 JM) is issued before any is used.
+#define RT_ROWS 4
+// the quarters' parts (s_part [quarter][pair][lane], written by every wavefront) added, then the lanes: wavefront q
+// finishes expert x0 + q's rows
+__device__ __forceinline__ void router_finish(int R, int NE, float* __restrict__ out, int x0, int r0,
+                                              float (*s_part)[4 * RT_ROWS][64]) {
+    const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
     __syncthreads();
-    m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-    const float e = t < NE ? expf(l - m) : 0.0f;
-    const float p = e == e ? e : -1.0f;
-    float s = e;
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-    if (lane == 0) red[1][wave] = s;
-    sp[t] = p;
-    __syncthreads();
-    const float tot = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
-    if (t < NE) {
-        int rank = 0, j = 0;
-        for (; j + 4 <= NE; j += 4) {
-            const float4 v = *(const float4*) &sp[j];
-            rank += (v.x > p || (v.x == p && j < t)) + (v.y > p || (v.y == p && j + 1 < t)) +
-                    (v.z > p || (v.z == p && j + 2 < t)) + (v.w > p || (v.w == p && j + 3 < t));
+    float v[RT_ROWS];
+    for (int i = 0; i < RT_ROWS; ++i) {
+        const int p = q * RT_ROWS + i;
+        v[i] = ((s_part[0][p][lane] + s_part[1][p][lane]) + s_part[2][p][lane]) + s_part[3][p][lane];
+    }
+    for (int i = 0; i < RT_ROWS; ++i) v[i] = wave_sum(v[i]);
+    if (lane == 0 && x0 + q < NE)
+        for (int i = 0; i < RT_ROWS; ++i)
+            if (r0 + i < R) out[(size_t) (r0 + i) * NE + x0 + q] = v[i];
+}
+template <int JM>
+__device__ __forceinline__ void router_dot(const float* __restrict__ hn, const float* __restrict__ router, int R, int E,
+                                           int NE, float* __restrict__ out, int x0, int r0,
+                                           float (*s_part)[4 * RT_ROWS][64]) {
+    constexpr int JQ = JM / 4;
+    const int t = threadIdx.x, lane = t & 63, q = t >> 6;
+    float4 wv[4][JQ], hv[RT_ROWS][JQ];
+    for (int jj = 0; jj < JQ; ++jj) {
+        const int e0 = min(4 * lane + 256 * (q * JQ + jj), E - 4);
+        for (int u = 0; u < 4; ++u) wv[u][jj] = *(const float4*) (router + (size_t) min(x0 + u, NE - 1) * E + e0);
+        for (int i = 0; i < RT_ROWS; ++i) hv[i][jj] = *(const float4*) (hn + (size_t) min(r0 + i, R - 1) * E + e0);
+    }
+    for (int u = 0; u < 4; ++u)
+        for (int i = 0; i < RT_ROWS; ++i) {
+            float s = 0.0f;
+            for (int jj = 0; jj < JQ; ++jj)
+                if (4 * lane + 256 * (q * JQ + jj) < E) {
+                    const float4 h = hv[i][jj], w = wv[u][jj];
+                    s += h.x * w.x + h.y * w.y + h.z * w.z + h.w * w.w;
+                }
+            s_part[q][u * RT_ROWS + i][lane] = s;
         }
-        for (; j < NE; ++j) rank += sp[j] > p || (sp[j] == p && j < t);
-        if (rank < k) {
-            spick[rank] = t;
-            sprob[rank] = p;
+    router_finish(R, NE, out, x0, r0, s_part);
+}
+// the rows' logits for experts 4 blockIdx.x .. + 3, rows RT_ROWS blockIdx.y ..
+template <int JM>
+__global__ __launch_bounds__(256) void k_router(const float* __restrict__ hn, const float* __restrict__ router, int R,
+                                                int E, int NE, float* __restrict__ out) {
+    __shared__ float s_part[4][4 * RT_ROWS][64];
+    router_dot<JM>(hn, router, R, E, NE, out, blockIdx.x * 4, blockIdx.y * RT_ROWS, s_part);
+}
+// E > MOE_ROUTE_EMAX: quarters of ceil(E / 1024) steps, each step's loads in turn
+__global__ __launch_bounds__(256) void k_router_any(const float* __restrict__ hn, const float* __restrict__ router,
+                                                    int R, int E, int NE, float* __restrict__ out) {
+    __shared__ float s_part[4][4 * RT_ROWS][64];
+    const int lane = threadIdx.x & 63, q = threadIdx.x >> 6, x0 = blockIdx.x * 4, r0 = blockIdx.y * RT_ROWS;
+    const int JQ = (E + 1023) / 1024;
+    float s[4][RT_ROWS];
+    for (int u = 0; u < 4; ++u)
+        for (int i = 0; i < RT_ROWS; ++i) s[u][i] = 0.0f;
+    for (int jj = 0; jj < JQ; ++jj) {
+        const int e0 = 4 * lane + 256 * (q * JQ + jj);
+        if (e0 >= E) break;
+        for (int u = 0; u < 4; ++u) {
+            const float4 w = *(const float4*) (router + (size_t) min(x0 + u, NE - 1) * E + e0);
+            for (int i = 0; i < RT_ROWS; ++i) {
+                const float4 h = *(const float4*) (hn + (size_t) min(r0 + i, R - 1) * E + e0);
+                s[u][i] += h.x * w.x + h.y * w.y + h.z * w.z + h.w * w.w;
+            }
         }
     }
-    __syncthreads();
-    if (t == 0) {
-        float pk[8], sel = 0.0f;
-        for (int j = 0; j < k; ++j) {
-            pk[j] = sprob[j] / tot;
-            sel += pk[j];
+    for (int u = 0; u < 4; ++u)
+        for (int i = 0; i < RT_ROWS; ++i) s_part[q][u * RT_ROWS + i][lane] = s[u][i];
+    router_finish(R, NE, out, x0, r0, s_part);
+}
+// the register width of the routing kernels' instances for E (0: E > MOE_ROUTE_EMAX)
+static inline int router_jm(int E) { return E <= 1024 ? 4 : E <= 2048 ? 8 : E <= MOE_ROUTE_EMAX ? 16 : 0; }
+
+// Routing of a row (moe_topk1, kernels.metal:3419-3467): softmax of its NE <= 256 logits, the k <= 8 largest (ties: the
+// lower id), weights p / sum(p) renormalised by their own sum floored at 6.103515625e-5. One wavefront a row, lane l
+// holding experts l + 64 s (s = 0..3): the max and the sum by wave_max / wave_sum (lane l's four added first, in slot
+// order), then k rounds of: the largest remaining probability (wave_max), the lowest id holding it (ballots over the
+// slots, in id order), that slot marked taken. A NaN probability counts as -1, below every number, so the ids are
+// always k distinct experts of [0, NE). l4: this lane's logits (-inf past NE); ids, w: the row's k outputs.
+template <bool SYS = false>  // SYS: the ids stored system-coherently (read on another XCD in the same launch)
+__device__ __forceinline__ void moe_topk_wave(const float l4[4], int NE, int k, int32_t* __restrict__ ids,
+                                              float* __restrict__ w) {
+    const int lane = threadIdx.x & 63;
+    const float m = wave_max(fmaxf(fmaxf(l4[0], l4[1]), fmaxf(l4[2], l4[3])));
+    float p[4], e[4];
+    for (int s = 0; s < 4; ++s) {
+        e[s] = lane + 64 * s < NE ? expf(l4[s] - m) : 0.0f;
+        p[s] = lane + 64 * s < NE ? (e[s] == e[s] ? e[s] : -1.0f) : -4.0f;  // (-4: no expert; -3: taken)
+    }
+    const float tot = wave_sum((e[0] + e[1]) + (e[2] + e[3]));
+    int my_id = 0;
+    float my_p = 0.0f, sel = 0.0f;
+    for (int j = 0; j < MOE_MAX_K; ++j) {
+        if (j >= k) break;
+        const float M = wave_max(fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3])));
+        int id = -1;
+        for (int s = 0; s < 4; ++s) {
+            const uint64_t b = __ballot(p[s] == M);
+            if (id < 0 && b) id = 64 * s + __ffsll((unsigned long long) b) - 1;
         }
-        sel = fmaxf(sel, 6.103515625e-5f);
-        for (int j = 0; j < k; ++j) {
-            ids[r * k + j] = spick[j];
-            w[r * k + j] = pk[j] / sel;
+        for (int s = 0; s < 4; ++s)
+            if (id == lane + 64 * s) p[s] = -3.0f;
+        if (lane == j) {
+            my_id = id;
+            my_p = M;
         }
+        sel += M / tot;
+    }
+    sel = fmaxf(sel, 6.103515625e-5f);
+    if (lane < k) {
+        if (SYS)
+            __hip_atomic_store(ids + lane, my_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        else
+            ids[lane] = my_id;
+        w[lane] = (my_p / tot) / sel;
     }
 }
-__global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ lg, int NE, int k, int32_t* __restrict__ ids,
-                                                  float* __restrict__ w) {
-    __shared__ TopkShared sh;
-    const int r = blockIdx.x, t = threadIdx.x;
-    moe_topk_row(sh, t < NE ? lg[(size_t) r * NE + t] : -INFINITY, r, t, NE, k, ids, w);
+// rows 4 blockIdx.x + wave
+__global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ lg, int R, int NE, int k,
+                                                  int32_t* __restrict__ ids, float* __restrict__ w) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= R) return;
+    float l4[4];
+    for (int s = 0; s < 4; ++s) l4[s] = lane + 64 * s < NE ? lg[(size_t) r * NE + lane + 64 * s] : -INFINITY;
+    moe_topk_wave(l4, NE, k, ids + (size_t) r * k, w + (size_t) r * k);
 }
 
 // The (row, slot) pairs in expert-major tiles of 16 rows (moe_lists, kernels.metal:3468-3497), deterministically: expert
 // x's pairs take tiles toff[x] .. in (row, slot) order. prow[r][j] = the pair's row in that layout; rsrc[p] = the row
 // whose operand tile row p carries (-1: padding); items = (expert, tile) of every tile, count = their number. One
-// workgroup of 1024 threads: wavefront w owns the w-th sixteenth of the pairs (a chunk) and counts its experts (LDS
-// atomics: counts, not order); an expert's chunk counts become its chunks' starting places (a prefix over chunks) and
-// its total gives the tile offsets (a wavefront prefix over experts); then each wavefront walks its chunk 64 pairs at
-// a time, a pair's place = its chunk's place for the expert + the earlier pairs of the 64 with that expert.
+// workgroup of NW wavefronts: wavefront w owns the w-th of NW chunks of the pairs and counts its experts (LDS atomics:
+// counts, not order); an expert's chunk counts become its chunks' starting places (a prefix over chunks) and its total
+// gives the tile offsets (a wavefront prefix over experts); then each wavefront walks its chunk 64 pairs at a time, a
+// pair's place = its chunk's place for the expert + the earlier pairs of the 64 with that expert (the lanes holding
+// the same expert found by ballots over the id's bits). The result does not depend on NW.
 #define MOE_MAX_PAIRS 4096
+template <int NW>
 struct GroupShared {
     int sid[MOE_MAX_PAIRS];
-    int hist[16][256];  // [chunk][expert]: counts, then the chunk's next place for the expert
+    int hist[NW][256];  // [chunk][expert]: counts, then the chunk's next place for the expert
     int cnt[256], toff[257];
 };
-// by a workgroup of 1024 threads; SYS: the ids were written on other XCDs in this launch (system-coherent loads)
-template <bool SYS>
-__device__ __forceinline__ void moe_group(GroupShared& sh, const int32_t* __restrict__ ids, int RK, int NE, int P,
+// SYS: the ids were written on other XCDs in this launch (system-coherent loads)
+template <bool SYS, int NW>
+__device__ __forceinline__ void moe_group(GroupShared<NW>& sh, const int32_t* __restrict__ ids, int RK, int NE, int P,
                                           int k, int32_t* __restrict__ prow, int32_t* __restrict__ rsrc,
                                           int32_t* __restrict__ items, int32_t* __restrict__ count) {
+    constexpr int NT = 64 * NW;
     int* sid = sh.sid;
     int (*hist)[256] = sh.hist;
     int* cnt = sh.cnt;
     int* toff = sh.toff;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    for (int i = t; i < 16 * 256; i += 1024) (&hist[0][0])[i] = 0;
-    for (int p = t; p < P; p += 1024) rsrc[p] = -1;
-    for (int q = t; q < RK; q += 1024)
+    for (int i = t; i < NW * 256; i += NT) (&hist[0][0])[i] = 0;
+    for (int p = t; p < P; p += NT) rsrc[p] = -1;
+    for (int q = t; q < RK; q += NT)
         sid[q] = SYS ? __hip_atomic_load(ids + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) : ids[q];
     __syncthreads();
-    const int C = (RK + 15) / 16, q0 = wave * C, q1 = min(RK, q0 + C);
+    const int C = (RK + NW - 1) / NW, q0 = wave * C, q1 = min(RK, q0 + C);
     for (int q = q0 + lane; q < q1; q += 64) atomicAdd(&hist[wave][sid[q]], 1);
     __syncthreads();
-    if (t < NE) {
+    for (int x = t; x < NE; x += NT) {
         int s = 0;
-        for (int c = 0; c < 16; ++c) {
-            const int h = hist[c][t];
-            hist[c][t] = s;
+        for (int c = 0; c < NW; ++c) {
+            const int h = hist[c][x];
+            hist[c][x] = s;
             s += h;
         }
-        cnt[t] = s;
+        cnt[x] = s;
     }
     __syncthreads();
     if (wave == 0) {  // toff[x] = tiles of the experts before x (lane l: experts 4l .. 4l + 3)
@@ -737,15 +808,16 @@ __device__ __forceinline__ void moe_group(GroupShared& sh, const int32_t* __rest
     }
     __syncthreads();
     for (int g0 = q0; g0 < q1; g0 += 64) {  // (wavefront-uniform trips; LDS ops of a wavefront complete in order)
-        const int q = g0 + lane, n = min(64, q1 - g0);
+        const int q = g0 + lane;
         const bool in = q < q1;
-        const int x = in ? sid[q] : -1;
-        int before = 0, after = 0;
-        for (int j = 0; j < n; ++j) {
-            const int y = sid[g0 + j];
-            before += y == x && j < lane;
-            after += y == x && j > lane;
+        const int x = in ? sid[q] : 0x1FF;  // (no expert id: bit 8 set)
+        uint64_t same = __ballot(in);
+        for (int b = 0; b < 9; ++b) {
+            const bool bit = (x >> b) & 1;
+            const uint64_t m = __ballot(bit);
+            same &= bit ? m : ~m;
         }
+        const int before = __popcll(same & ((1ull << lane) - 1)), after = __popcll(same & ~((2ull << lane) - 1));
         if (in) {
             const int p = toff[x] * 16 + hist[wave][x] + before;
             prow[q] = p;
@@ -753,7 +825,7 @@ __device__ __forceinline__ void moe_group(GroupShared& sh, const int32_t* __rest
             if (after == 0) hist[wave][x] += before + 1;  // the group's last pair of x moves the place on
         }
     }
-    for (int x = t; x < NE; x += 1024)
+    for (int x = t; x < NE; x += NT)
         for (int i = toff[x]; i < toff[x + 1]; ++i) {
             items[2 * i] = x;
             items[2 * i + 1] = i;
@@ -762,91 +834,110 @@ __device__ __forceinline__ void moe_group(GroupShared& sh, const int32_t* __rest
 __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ ids, int RK, int NE, int P, int k,
                                                     int32_t* __restrict__ prow, int32_t* __restrict__ rsrc,
                                                     int32_t* __restrict__ items, int32_t* __restrict__ count) {
-    __shared__ GroupShared sh;
-    moe_group<false>(sh, ids, RK, NE, P, k, prow, rsrc, items, count);
+    __shared__ GroupShared<16> sh;
+    moe_group<false, 16>(sh, ids, RK, NE, P, k, prow, rsrc, items, count);
 }
 
 // The whole routing in one launch (router, top-k and grouping; the same arithmetic as k_router, k_moe_topk and
-// k_moe_group): workgroup (row block b of RT_ROWS rows, expert block x of 16 experts), 16 wavefronts, each an expert's
-// logits of the block's rows (router_dot). The row block's workgroups are dealt to one XCD (grid x: the row blocks,
-// padded to a multiple of nxcd), so the last of them to count itself (an L2 atomic; 5-bit per-XCD fields flag a block
-// spread over XCDs in *xerr) reads their logits from that L2 and routes the block's rows, 256 threads a row
-// (moe_topk_row). It stores the rows' expert ids system-coherently and counts itself in a system-scope counter; the
-// last row block to do so reads every id the same way and groups the pairs (moe_group). Counters return to zero.
-__global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ hn, const float* __restrict__ router, int R,
-                                                    int E, int NE, int k, int P, float* __restrict__ lg,
-                                                    int32_t* __restrict__ ids, float* __restrict__ w,
-                                                    int32_t* __restrict__ prow, int32_t* __restrict__ rsrc,
-                                                    int32_t* __restrict__ items, int32_t* __restrict__ count,
-                                                    uint64_t* __restrict__ cnt, int32_t* __restrict__ gcnt,
-                                                    int32_t* __restrict__ xerr) {
-    __shared__ TopkShared tsh[RT_ROWS];
-    __shared__ GroupShared gsh;
+// k_moe_group): workgroup (row block b of RT_ROWS rows, expert block of 4 experts), 4 wavefronts (router_dot). The row
+// block's workgroups are dealt to one XCD (grid x: the row blocks, padded to a multiple of the XCD count), so the last
+// of them to count itself in the block's counter (XCD-local, in the L2 that holds the block's logits) routes the
+// block's rows, a wavefront each (moe_topk_wave). It stores the rows' expert ids system-coherently and counts itself
+// in a system-scope counter; the last row block to do so reads every id the same way and groups the pairs
+// (moe_group). Counters return to zero. Counter layout: bits 0-7 the arrivals, 7 bits an XCD from bit 8 (the check
+// that a block's workgroups shared one XCD).
+template <int JM>
+__global__ __launch_bounds__(256) void k_moe_route(const float* __restrict__ hn, const float* __restrict__ router, int R,
+                                                   int E, int NE, int k, int P, float* __restrict__ lg,
+                                                   int32_t* __restrict__ ids, float* __restrict__ w,
+                                                   int32_t* __restrict__ prow, int32_t* __restrict__ rsrc,
+                                                   int32_t* __restrict__ items, int32_t* __restrict__ count,
+                                                   uint64_t* __restrict__ cnt, int32_t* __restrict__ gcnt,
+                                                   int32_t* __restrict__ xerr) {
+    __shared__ union {
+        float part[4][4 * RT_ROWS][64];  // the router's quarter sums
+        GroupShared<4> g;                // the grouping (the last row block, after its own rows are done)
+    } u;
     __shared__ int s_last;
     const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int nrb = (R + RT_ROWS - 1) / RT_ROWS, nxb = (int) gridDim.y;
     if (b >= nrb) return;  // a padding row block
-    const int x = blockIdx.y * 16 + wave, r0 = b * RT_ROWS;
-    if (x < NE) router_dot(hn, router, R, E, NE, lg, x, r0, lane);
+    const int r0 = b * RT_ROWS;
+    router_dot<JM>(hn, router, R, E, NE, lg, blockIdx.y * 4, r0, u.part);
     __builtin_amdgcn_s_waitcnt(0);  // the logits have reached the L2
     __syncthreads();
+    uint64_t done = 0;  // (the completer's thread 0: the count, taken back with the ids' stores)
     if (t == 0) {
         unsigned xcc;
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-        const int f = 8 + 5 * (int) (xcc & 7);
+        const int f = 8 + 7 * (int) (xcc & 7);
         const uint64_t add = 1ull + (1ull << f);
-        const uint64_t n = __hip_atomic_fetch_add(cnt + b, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+        const uint64_t n = __hip_atomic_fetch_add(cnt + b * CNT_STRIDE, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
         s_last = (int) (n & 255) == nxb;
         if (s_last) {
-            if ((int) ((n >> f) & 31) != nxb) __hip_atomic_fetch_or(xerr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            __hip_atomic_fetch_add(cnt + b, (uint64_t) 0 - n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((int) ((n >> f) & 127) != nxb) __hip_atomic_fetch_or(xerr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            done = n;
         }
     }
     __syncthreads();
     if (!s_last) return;
-    // the row block's rows, a quarter of the workgroup each (a row past R: the last row again, not written), into LDS
-    __shared__ int32_t s_ids[RT_ROWS][8];
-    __shared__ float s_w[RT_ROWS][8];
-    {
-        const int q = t >> 8, tq = t & 255, r = min(r0 + q, R - 1);
-        const float l = tq < NE ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                      buf_rsrc(lg, (uint32_t) ((size_t) R * NE * 4)), (r * NE + tq) * 4, 0, 1))
-                                : -INFINITY;  // (sc0: past the CU's L1, from the L2 the logits are in)
-        moe_topk_row(tsh[q], l, 0, tq, NE, k, &s_ids[q][0], &s_w[q][0]);
+    // row r0 + wave, its logits through the L2 (sc0: past the L1), its ids stored system-coherently (the last row
+    // block reads them from another XCD)
+    if (r0 + wave < R) {
+        const int r = r0 + wave;
+        const __amdgpu_buffer_rsrc_t rl = buf_rsrc(lg, (uint32_t) ((size_t) R * NE * 4));
+        float l4[4];
+        for (int s = 0; s < 4; ++s)
+            l4[s] = lane + 64 * s < NE ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                    rl, (r * NE + lane + 64 * s) * 4, 0, 1))
+                                       : -INFINITY;
+        moe_topk_wave<true>(l4, NE, k, ids + (size_t) r * k, w + (size_t) r * k);
     }
-    __syncthreads();
-    // the rows' ids stored system-coherently (the last row block reads them from another XCD), their weights plainly
-    if (t < RT_ROWS * k && r0 + t / k < R) {
-        __hip_atomic_store(ids + r0 * k + t, s_ids[t / k][t % k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        w[r0 * k + t] = s_w[t / k][t % k];
-    }
+    // the block's counter back to zero by an atomic of the same kind, where the counts were (every count of the
+    // block has been made); it lands with the ids' stores
+    if (t == 0) __hip_atomic_fetch_add(cnt + b * CNT_STRIDE, (uint64_t) 0 - done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (t == 0) {
         const int n = __hip_atomic_fetch_add(gcnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         s_last = n == nrb - 1;
-        if (s_last) __hip_atomic_store(gcnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     __syncthreads();
     if (!s_last) return;
-    moe_group<true>(gsh, ids, R * k, NE, P, k, prow, rsrc, items, count);
+    moe_group<true, 4>(u.g, ids, R * k, NE, P, k, prow, rsrc, items, count);
+    if (t == 0) __hip_atomic_store(gcnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);  // (no barrier waits for it)
 }
 
 void moe_router(const float* hn, const float* router, int R, int E, int NE, float* lg, hipStream_t st) {
-    if (R > 0)
-        hipLaunchKernelGGL(k_router, dim3((NE + 3) / 4, (R + RT_ROWS - 1) / RT_ROWS), dim3(256), 0, st, hn, router, R,
-                           E, NE, lg);
+    if (R <= 0) return;
+    const dim3 g((NE + 3) / 4, (R + RT_ROWS - 1) / RT_ROWS);
+    switch (router_jm(E)) {
+        case 4: hipLaunchKernelGGL(k_router<4>, g, dim3(256), 0, st, hn, router, R, E, NE, lg); break;
+        case 8: hipLaunchKernelGGL(k_router<8>, g, dim3(256), 0, st, hn, router, R, E, NE, lg); break;
+        case 16: hipLaunchKernelGGL(k_router<16>, g, dim3(256), 0, st, hn, router, R, E, NE, lg); break;
+        default: hipLaunchKernelGGL(k_router_any, g, dim3(256), 0, st, hn, router, R, E, NE, lg);
+    }
 }
 int moe_route(const float* hn, const float* router, int R, int E, int NE, int k, int P, float* lg, int32_t* ids,
               float* w, int32_t* prow, int32_t* rsrc, int32_t* items, int32_t* count, uint64_t* cnt, int cnt_len,
               int32_t* gcnt, int32_t* xerr, int nxcd, hipStream_t st) {
     if (R <= 0) return 0;
-    if (NE < 1 || NE > 256 || k < 1 || k > MOE_MAX_K || k > NE || R * k > MOE_MAX_PAIRS || E % 4 || nxcd < 1) return -1;
+    if (NE < 1 || NE > 256 || k < 1 || k > MOE_MAX_K || k > NE || R * k > MOE_MAX_PAIRS || E % 4 || nxcd < 1 ||
+        !router_jm(E))
+        return -1;
     if (P < 16 * (std::min(NE, R * k) + (R * k + 15) / 16)) return -1;
     const int nrb = (R + RT_ROWS - 1) / RT_ROWS, gx = (nrb + nxcd - 1) / nxcd * nxcd;
-    if (gx > cnt_len || (NE + 15) / 16 > 255) return -1;
-    hipLaunchKernelGGL(k_moe_route, dim3(gx, (NE + 15) / 16), dim3(1024), 0, st, hn, router, R, E, NE, k, P, lg, ids, w,
-                       prow, rsrc, items, count, cnt, gcnt, xerr);
+    if ((long) gx * CNT_STRIDE > cnt_len || (NE + 3) / 4 > 127) return -1;
+    const dim3 g(gx, (NE + 3) / 4);
+#define ROUTE(JM)                                                                                                     \
+    hipLaunchKernelGGL(k_moe_route<JM>, g, dim3(256), 0, st, hn, router, R, E, NE, k, P, lg, ids, w, prow, rsrc,    \
+                       items, count, cnt, gcnt, xerr)
+    switch (router_jm(E)) {
+        case 4: ROUTE(4); break;
+        case 8: ROUTE(8); break;
+        default: ROUTE(16); break;
+    }
+#undef ROUTE
     return 0;
 }
 
@@ -855,7 +946,7 @@ int moe_select(const float* lg, int R, int NE, int k, int P, int32_t* ids, float
     if (R <= 0) return 0;
     if (NE < 1 || NE > 256 || k < 1 || k > MOE_MAX_K || k > NE || R * k > MOE_MAX_PAIRS) return -1;
     if (P < 16 * (std::min(NE, R * k) + (R * k + 15) / 16)) return -1;  // the tiles of any grouping
-    hipLaunchKernelGGL(k_moe_topk, dim3(R), dim3(256), 0, st, lg, NE, k, ids, w);
+    hipLaunchKernelGGL(k_moe_topk, dim3((R + 3) / 4), dim3(256), 0, st, lg, R, NE, k, ids, w);
     hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(1024), 0, st, ids, R * k, NE, P, k, prow, rsrc, items, count);
     return 0;
 }

@@ -815,25 +815,28 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         __shared__ int s_last;
+        uint64_t* c = a.cnt + (size_t) (set + (int) gridDim.x * (int) blockIdx.z) * CNT_STRIDE;
+        uint64_t done = 0;  // (the completer's thread 0: the count, taken back once the epilogue is issued)
         if (threadIdx.x == 0) {
             unsigned xcc;
             asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
             const int f = 8 + 5 * (int) (xcc & 7);  // this XCD's field of the count
-            uint64_t* c = a.cnt + set + (int) gridDim.x * (int) blockIdx.z;
             const uint64_t add = 1ull + (1ull << f);
             const uint64_t n = __hip_atomic_fetch_add(c, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
             s_last = (int) (n & 255) == (int) gridDim.y;
             if (s_last) {
                 if ((int) ((n >> f) & 31) != (int) gridDim.y)  // some workgroup of the set ran on another XCD
                     __hip_atomic_fetch_or(a.xerr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                // back to zero by an atomic of the same kind, performed where the counts were (a plain store of an
-                // atomic compiles to a write-through store, which need not meet the L2's copy)
-                __hip_atomic_fetch_add(c, (uint64_t) 0 - n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                done = n;
             }
         }
         __syncthreads();
         if (!s_last) return;
         q4_epilogue<FE, MT, S>(a, set, mt0);
+        // back to zero by an atomic of the same kind, performed where the counts were (a plain store of an atomic
+        // compiles to a write-through store, which need not meet the L2's copy); after the epilogue, so that no
+        // barrier waits for it (every count of the set has been made: the next launch is the next to count)
+        if (threadIdx.x == 0) __hip_atomic_fetch_add(c, (uint64_t) 0 - done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -1162,7 +1165,7 @@ static bool fused_shape(int M, int N, int K, int wt, int fe, int nxcd, int cnt_l
     mt = std::min(p.smt, mtiles);
     const int sets = (p.nstripes + 4 * spw - 1) / (4 * spw);
     grid = dim3((sets + nxcd - 1) / nxcd * nxcd, p.ks, (mtiles + mt - 1) / mt);
-    return (long) grid.x * grid.z <= cnt_len;
+    return (long) grid.x * grid.z * CNT_STRIDE <= cnt_len;
 }
 
 bool q4_gemm_fused_fits(int M, int N, int K, int wt, int fe, int nxcd, int cnt_len) {

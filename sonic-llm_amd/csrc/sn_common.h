@@ -136,6 +136,11 @@ static inline size_t wt_bytes(int wt, int N, int K) {
 // any is used (the slice index is clamped, so no load sits behind a branch); the slices past ks are not added.
 #define KS_MAX 16
 #define MOE_MAX_K 8  // experts used per row
+#define MOE_ROUTE_EMAX 4096  // the widest rows (E) of the one-launch routing
+// The 64-bit counters by which one launch's workgroups hand work on sit CNT_STRIDE apart (256 bytes): counters that
+// share a line serialise each other's atomics (the routing's 8 row blocks of 32 arrivals: 2.6 us for the last
+// arrival's atomic with adjacent counters).
+#define CNT_STRIDE 32
 template <int KM>
 __device__ __forceinline__ float4 slices_sum4(const float* p, size_t stride, int ks) {
     float4 v[KM];

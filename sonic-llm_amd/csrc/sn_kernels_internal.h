@@ -87,7 +87,7 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
 // The raw matmul of decode-sized rows with a fused epilogue fe (FE_SWIGLU: a.h, a.xo; FE_ROPE: the rope fields of a)
 // through the streaming kernel: the same sums in the same order as q4_gemm_raw followed by swiglu_quant (xo must not be
 // xa) or qk_norm_rope_kv, so the same bits. `a` carries the epilogue's fields and the counters (a.cnt, cnt_len of
-// them), a.xerr and a.nxcd. Returns 1 when launched, 0 when the shape or weight type has no fused launch
+// them, a set's every CNT_STRIDE), a.xerr and a.nxcd. Returns 1 when launched, 0 when the shape or weight type has no fused launch
 // (nothing launched: use the split path), -1 on bad arguments.
 int q4_gemm_fused(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes,
                   hipStream_t st, int wt, int fe, const GemmArgs& a, int cnt_len);
@@ -279,8 +279,10 @@ int moe_select(const float* lg, int R, int NE, int k, int P, int32_t* ids, float
                int32_t* items, int32_t* count, hipStream_t st);
 // moe_router + moe_select in one launch, the same results: the row blocks' logits, then each block's routing by the
 // block's last workgroup (an XCD-local handoff: the launch's workgroups are dealt to nxcd XCDs in turn), then the
-// grouping by the last block (a system-coherent handoff). cnt: cnt_len 64-bit counters, gcnt one, both zero between
-// launches; *xerr set when a row block's workgroups ran on more than one XCD. -1 otherwise (nothing launched).
+// grouping by the last block (a system-coherent handoff). cnt: cnt_len 64-bit counters (a row block's every
+// CNT_STRIDE), gcnt one, both zero between
+// launches; *xerr set when a row block's workgroups ran on more than one XCD. E <= MOE_ROUTE_EMAX; -1 otherwise
+// (nothing launched).
 int moe_route(const float* hn, const float* router, int R, int E, int NE, int k, int P, float* lg, int32_t* ids,
               float* w, int32_t* prow, int32_t* rsrc, int32_t* items, int32_t* count, uint64_t* cnt, int cnt_len,
               int32_t* gcnt, int32_t* xerr, int nxcd, hipStream_t st);

@@ -52,7 +52,7 @@ extern "C" int snk_moe_route(const float* d_hn, int R, int E, const float* d_rou
     hipStream_t st = (hipStream_t) stream;
     int nxcd = 1;
     if (!xcd_round_robin(st, &nxcd)) return -1;
-    const int cnt_len = 1024;
+    const int cnt_len = 1 << 14;
     uint64_t* cnt = nullptr;
     int32_t* gx = nullptr;  // [0] the global counter, [1] the XCD check
     if (hipMalloc(&cnt, cnt_len * 8) != hipSuccess) return -1;
