@@ -577,6 +577,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
                                          e->head_t == GGML_Q6_K ? xk_bytes(MO, E) : 0}),
                                err, err_len);
     if (e->NE == 0 && F > 0) e->xa2 = e->dalloc<uint8_t>(xa_bytes(R, F), err, err_len);
+    if (e->NE > 0) e->xa2 = e->dalloc<uint8_t>(xa_bytes(P, e->FE), err, err_len);  // (grouped gate|up + SwiGLU)
     // the fused epilogues' arrival counters (sets x row-tile groups of any decode-sized launch; zero between launches:
     // each set's last workgroup resets its own) and the XCD check word
     e->fcnt_len = 1 << 16;
@@ -1082,15 +1083,30 @@ struct Dev {
             }
         }
         // (the expert tiles' rows gathered from hn's Q8_0 operand, which the resid above wrote in row order)
-        rc |= e->launch(SNX_K_GEMM, used * e->egu_stride + (double) R * NU * E * 4 + (double) R * NU * 2 * FE * 4, [&] {
-            return q4_gemm_grouped(l.egu, e->egu_stride, e->gitems, e->gcount, T, e->xa, P, 2 * FE, E, e->gemm_ws,
-                                   e->gemm_ws_bytes, st, e->wt, e->rsrc, e->rsrc, R) < 0 ? -1 : 0;
-        });
-        rc |= e->launch(SNX_K_QUANT, (double) R * NU * FE * 14, [&] {
-            return swiglu_quant(e->gemm_ws, 1, P, FE, nullptr, e->xa, st, e->rsrc);
-        });
+        // gate|up with its SwiGLU + Q8_0 in one launch (into xa2) where the shape takes it; else the sums, then the
+        // row kernel (into xa)
+        const bool gsw = e->fuse && q4_gemm_grouped_swiglu_fits(2 * FE, E, e->wt);
+        const uint8_t* xd = gsw ? e->xa2 : e->xa;  // the down projection's operand
+        if (gsw) {
+            rc |= e->launch(SNX_K_GEMM, used * e->egu_stride + (double) R * NU * E * 4 + (double) R * NU * FE * 1.0625,
+                            [&] {
+                                return q4_gemm_grouped_swiglu(l.egu, e->egu_stride, e->gitems, e->gcount, T, e->xa, P,
+                                                              2 * FE, E, e->xa2, st, e->wt, e->rsrc, e->rsrc, R) == 1
+                                           ? 0 : -1;
+                            });
+        } else {
+            rc |= e->launch(SNX_K_GEMM, used * e->egu_stride + (double) R * NU * E * 4 + (double) R * NU * 2 * FE * 4,
+                            [&] {
+                                return q4_gemm_grouped(l.egu, e->egu_stride, e->gitems, e->gcount, T, e->xa, P, 2 * FE,
+                                                       E, e->gemm_ws, e->gemm_ws_bytes, st, e->wt, e->rsrc, e->rsrc,
+                                                       R) < 0 ? -1 : 0;
+                            });
+            rc |= e->launch(SNX_K_QUANT, (double) R * NU * FE * 14, [&] {
+                return swiglu_quant(e->gemm_ws, 1, P, FE, nullptr, e->xa, st, e->rsrc);
+            });
+        }
         rc |= e->launch(SNX_K_GEMM, used * e->ed_stride + (double) R * NU * FE * 4 + (double) R * NU * E * 4, [&] {
-            return q4_gemm_grouped(l.ed, e->ed_stride, e->gitems, e->gcount, T, e->xa, P, E, FE, e->gemm_ws,
+            return q4_gemm_grouped(l.ed, e->ed_stride, e->gitems, e->gcount, T, xd, P, E, FE, e->gemm_ws,
                                    e->gemm_ws_bytes, st, e->wt, e->rsrc) < 0 ? -1 : 0;
         });
         moe_pending = true;  // x += the weighted expert rows: the next resid, fused with its norm and operand

@@ -632,7 +632,7 @@ __device__ __forceinline__ void q4_epilogue(const GemmArgs& a, int set, int mt0)
             }
             q8_store(v, g, a.xo, F, row, b);
         }
-    } else if constexpr (FE >= FE_ROPE) {  // (2 rows a wavefront at once)
+    } else if constexpr (FE >= FE_ROPE && FE < FE_GSWIGLU) {  // (2 rows a wavefront at once)
         constexpr int RC = 2;
         static_assert(S == 2, "a head is the 8 stripes of a set");
         const int h = set, H = a.H, KVH = a.KVH;
@@ -696,26 +696,46 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     if constexpr (FE != FE_NONE) {
         if (set * 4 * S >= a.nstripes) return;  // a padding set (the grid's sets: a multiple of nxcd)
     }
-    const int mt0 = __builtin_amdgcn_readfirstlane((int) blockIdx.z * MT);
+    int mt0 = (int) blockIdx.z * MT;
+    const uint8_t* wbase = a.w;
+    if (a.items) {  // grouped (MT = 1, no epilogue): this workgroup's (expert, row tile)
+        if ((int) blockIdx.z >= *a.count) return;
+        wbase = a.w + (size_t) a.items[2 * blockIdx.z] * a.wstride;
+        mt0 = a.items[2 * blockIdx.z + 1];
+    }
+    mt0 = __builtin_amdgcn_readfirstlane(mt0);
     const int c0 = slice * a.gps, ng = __builtin_amdgcn_readfirstlane(min(a.gps, a.ngroups - c0));
     const int s0 = set * (4 * S) + wave * S;
     const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(S, a.nstripes - s0)));
     const int sbytes = a.ngroups * TB;
-    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(a.w + (size_t) min(s0, a.nstripes - 1) * sbytes, (uint32_t) (nvalid * sbytes));
-    const size_t x0 = (size_t) mt0 * a.ngroups * XA_REC;
-    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xa + x0, (uint32_t) (xa_bytes(a.M, a.K) - x0));
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(wbase + (size_t) min(s0, a.nstripes - 1) * sbytes, (uint32_t) (nvalid * sbytes));
     const int rstride = a.ngroups * XA_REC;
+    // the activation: the operand's records from row tile mt0 on; or, gathering (a.gsrc, one row tile), lane l's row
+    // m = l % 16 of the tile taken from row gsrc[16 mt0 + m] of a row-ordered operand of a.gM rows (a padding row,
+    // gsrc < 0, reads as zeros: its offset is past the buffer). Per-lane offsets of a row's piece of a record:
+    // fragments 16 (row % 16 + 16 g), scales and corrections 4 (16 b + row % 16), b = l / 16.
+    size_t x0 = (size_t) mt0 * a.ngroups * XA_REC;
+    uint32_t xbytes = (uint32_t) (xa_bytes(a.M, a.K) - x0);
+    int vf_off = 16 * lane, vk_off = 4 * lane;
+    if (a.gsrc) {
+        const int sr = a.gsrc[16 * mt0 + (lane & 15)];
+        x0 = 0;
+        xbytes = (uint32_t) xa_bytes(a.gM, a.K);
+        vf_off = sr < 0 ? (int) XA_GATHER_OOB : (sr >> 4) * rstride + 16 * ((sr & 15) + 16 * g);
+        vk_off = sr < 0 ? (int) XA_GATHER_OOB : (sr >> 4) * rstride + 4 * (16 * g + (sr & 15));
+    }
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xa + x0, xbytes);
 
     // the slice's activation straight into LDS (buffer loads to LDS: lane l's 16 bytes land at 16 l of the fragment,
     // no registers; fragments past the slice repeat its last group: loads stay in bounds, never summed)
     for (int f = wave; f < NF; f += 4) {
         const int c = c0 + min(f / (4 * MT), ng - 1);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr) &s_act[f][0], 16, 16 * lane,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr) &s_act[f][0], 16, vf_off,
                                                  ((f / 4) % MT) * rstride + c * XA_REC + (f % 4) * 1024, 0, 0);
     }
     for (int k = wave; k < NK; k += 4) {
         const int c = c0 + min(k / (2 * MT), ng - 1);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr) &s_k[k / (2 * MT)][(k / 2) % MT][k % 2][0], 4, 4 * lane,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr) &s_k[k / (2 * MT)][(k / 2) % MT][k % 2][0], 4, vk_off,
                                                  ((k / 2) % MT) * rstride + c * XA_REC + (k % 2 ? CORR : XA_DX_OFF), 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -787,6 +807,32 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     // the sums out through LDS (the activation's space, once every wavefront is done with it): each wavefront's
     // [16 MT rows][16 S columns] tile is written back as 16-byte pieces of rows, part[slice][row][col]
     __syncthreads();
+    if constexpr (FE == FE_GSWIGLU) {
+        // grouped gate|up with its SwiGLU + Q8_0 (one slice: the workgroup's sums are whole). Wavefront w's 4 stripes
+        // are gate, up, gate, up of Q8_0 block b = 4 set + w of the F = N / 2 SwiGLU columns (the columns
+        // k_swiglu_quant reads: gate at 64 b + 4 g (+32), up 16 further), so silu(gate) * up of its 16 rows goes
+        // through its own LDS rows to lanes (row, part) for q8_store, into a.xo (the down matmul's operand)
+        static_assert(S == 4 && MT == 1, "a wavefront holds one block of SwiGLU columns");
+        constexpr int HW = 36;  // (a row's 32 values, padded)
+        float* hw = (float*) &s_act[0][0] + wave * 16 * HW;
+        for (int v = 0; v < 4; ++v) {
+            const int r = 4 * g + v;
+            hw[r * HW + n_in] = silu(acc[0][0][v]) * acc[1][0][v];
+            hw[r * HW + 16 + n_in] = silu(acc[2][0][v]) * acc[3][0][v];
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are written (this wavefront's own)
+        __builtin_amdgcn_wave_barrier();
+        const int m = lane >> 2, gq = lane & 3, row = mt0 * 16 + m, b = 4 * set + wave, F = a.N / 2;
+        float v8[8];
+        for (int j = 0; j < 4; ++j) {
+            v8[j] = hw[m * HW + 4 * gq + j];
+            v8[4 + j] = hw[m * HW + 16 + 4 * gq + j];
+        }
+        // (a row's 4 lane parts leave together: q8_store's shuffles stay within them)
+        if (row >= a.M || 32 * b >= F || (a.rmask && a.rmask[row] < 0)) return;
+        q8_store(v8, gq, a.xo, F, row, b);
+        return;
+    }
     constexpr int TW = 16 * S + 4;  // (a tile row's floats, padded)
     static_assert(4 * 16 * MT * TW * 4 <= NF * 1024, "the tiles fit the activation's LDS");
     float* tile = (float*) &s_act[0][0] + wave * 16 * MT * TW;
@@ -799,6 +845,7 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
         const int r = e / (4 * S), c4 = (e % (4 * S)) * 4;
         const int row = mt0 * 16 + r, col = s0 * 16 + c4;
         if (row >= a.M || col >= a.N) continue;  // (a stripe past the matrix is not stored)
+        if (a.rmask && a.rmask[row] < 0) continue;
         const float4 v = *(const float4*) &tile[r * TW + c4];
         float* dst = &a.part[((size_t) slice * a.M + row) * a.N + col];
         if (a.N % 4 == 0) {
@@ -809,7 +856,7 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
                 if (col + q < a.N) dst[q] = vv[q];
         }
     }
-    if constexpr (FE != FE_NONE) {
+    if constexpr (FE != FE_NONE && FE != FE_GSWIGLU) {
         // this workgroup's sums have reached the L2 (vmcnt counts stores); then it counts itself, and the count's
         // completer (it resets the counter for the next launch) finishes the set
         __builtin_amdgcn_s_waitcnt(0);
@@ -1275,6 +1322,24 @@ int q4_gemm_raw_plan(const uint8_t* w, const uint8_t* xa, int M, int N, int K, f
     return ok ? a.ks : -1;
 }
 
+// The grouped matmul through the streaming kernel: one slice (every group of K staged at once, ng <= 16), one row
+// tile a workgroup, S stripes a wavefront; false when the combination is not instantiated.
+template <int WT>
+static bool launch_grouped_s(int S, int ng, dim3 grid, const GemmArgs& a, hipStream_t st) {
+#define GSG(S_, GM_)                                                                                         \
+    if (S == S_ && ng <= GM_) {                                                                              \
+        hipLaunchKernelGGL((k_q4_gemm_s<WT, 1, S_, 2, GM_>), grid, dim3(256), 0, st, a);                     \
+        return true;                                                                                         \
+    }
+    if constexpr (WT == WT_Q4_0) {
+        GSG(2, 8) GSG(2, 16) GSG(4, 8) GSG(4, 16)
+    } else {
+        GSG(1, 8) GSG(1, 16)
+    }
+#undef GSG
+    return false;
+}
+
 int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
                     const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st, int wt,
                     const int32_t* rmask, const int32_t* gsrc, int gM) {
@@ -1289,13 +1354,46 @@ int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, cons
     a.M = M; a.N = N; a.K = K; a.epi = EPI_STORE;
     a.nstripes = (N + 15) / 16; a.ngroups = (K / 32 + 3) / 4; a.ks = 1; a.gps = a.ngroups;
     a.mtiles = (M + 15) / 16;
-    // Q4_0: 2 stripes a wavefront (Qwen3-30B-A3B at 32 rows: gate|up's workgroups then fit the chip at once; 4,080
-    // against 3,957 tok/s with one, 3,991 with four); Q8_0 tiles take one (twice the weight registers)
+    // the streaming kernel, one slice (K of at most 16 groups). Q4_0: 4 stripes a wavefront past 8 groups, else 2
+    // (Qwen3-30B-A3B at 32 rows, µs a launch against the ring kernel's 46.4 / 26.4: gate|up 2048 -> 1536 columns
+    // 43.0 with 4 stripes, 45.8 with 2; down 768 -> 2048 24.6 with 2, 25.9 with 4; deeper rings slower)
+    if (a.ngroups <= 16) {
+        const int gs = wt == WT_Q8_0 ? 1 : a.ngroups > 8 ? 4 : 2;
+        const dim3 grid((a.nstripes + 4 * gs - 1) / (4 * gs), 1, max_items);
+        if (wt == WT_Q8_0 ? launch_grouped_s<WT_Q8_0>(gs, a.ngroups, grid, a, st)
+                          : launch_grouped_s<WT_Q4_0>(gs, a.ngroups, grid, a, st))
+            return 1;
+    }
+    // (K past 16 groups) the ring kernel. Q4_0: 2 stripes a wavefront; Q8_0 tiles take one (twice the weight
+    // registers)
     if (wt == WT_Q8_0) {
         hipLaunchKernelGGL((k_q4_gemm<WT_Q8_0, 1, 1>), dim3((a.nstripes + 3) / 4, 1, max_items), dim3(256), 0, st, a);
     } else {
         hipLaunchKernelGGL((k_q4_gemm<WT_Q4_0, 1, 2>), dim3((a.nstripes + 7) / 8, 1, max_items), dim3(256), 0, st, a);
     }
+    return 1;
+}
+
+bool q4_gemm_grouped_swiglu_fits(int N, int K, int wt) {
+    return wt == WT_Q4_0 && N > 0 && N % 256 == 0 && K > 0 && (K / 32 + 3) / 4 <= 16;
+}
+int q4_gemm_grouped_swiglu(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
+                           const uint8_t* xa, int M, int N, int K, uint8_t* xo, hipStream_t st, int wt,
+                           const int32_t* rmask, const int32_t* gsrc, int gM) {
+    if (!q4_gemm_grouped_swiglu_fits(N, K, wt)) return 0;
+    if (M <= 0 || max_items <= 0) return 1;  // (nothing to do)
+    if (xo == nullptr || xo == xa || (gsrc && gM <= 0)) return -1;
+    const int ngroups = (K / 32 + 3) / 4;
+    GemmArgs a{};
+    a.w = w; a.xa = xa; a.xo = xo;
+    a.items = items; a.count = count; a.wstride = wstride; a.rmask = rmask;
+    a.gsrc = gsrc; a.gM = gM;
+    a.M = M; a.N = N; a.K = K; a.epi = EPI_STORE;
+    a.nstripes = N / 16; a.ngroups = ngroups; a.ks = 1; a.gps = ngroups;
+    a.mtiles = (M + 15) / 16;
+    const dim3 grid(a.nstripes / 16, 1, max_items);
+    if (ngroups <= 8) hipLaunchKernelGGL((k_q4_gemm_s<WT_Q4_0, 1, 4, 2, 8, FE_GSWIGLU>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_q4_gemm_s<WT_Q4_0, 1, 4, 2, 16, FE_GSWIGLU>), grid, dim3(256), 0, st, a);
     return 1;
 }
 

@@ -51,7 +51,7 @@ struct GemmArgs {
 // stripe-interleaved gate|up matrix (k_swiglu_quant's arithmetic), the q|k|v heads' QK-norm + RoPE + cache write
 // (k_qk_rope's arithmetic)
 // (the kernel's instances: FE + log2 KM, KM the slice bound of the epilogue's loads)
-enum { FE_NONE = 0, FE_SWIGLU = 8, FE_ROPE = 16 };
+enum { FE_NONE = 0, FE_SWIGLU = 8, FE_ROPE = 16, FE_GSWIGLU = 32 };  // (FE_GSWIGLU: grouped, one slice; no counters)
 
 // Launch shape of one matrix: a workgroup owns 4 spw stripes (a "set": spw per wavefront) and gps consecutive 4-block
 // groups (a slice). Layer-sized matrices at decode row counts run the streaming kernel (sspw stripes a wavefront,
@@ -101,6 +101,14 @@ bool xcd_round_robin(hipStream_t st, int* nxcd);
 // items, the device count in `count`; part[M][N] rows of each item's tile (one slice).
 // gsrc (optional): the operand's tile row p is row gsrc[p] of the row-ordered operand xa of gM rows (gathered while
 // loading; gsrc[p] < 0 reads zeros), as if the rows had been quantized into expert-tile order.
+// The grouped gate|up matmul (q4_gemm_grouped's arguments, N = 2F interleaved as swiglu_quant reads it) with SwiGLU +
+// Q8_0 of its rows into the operand xo [M][F] (rows with rmask < 0 not written), in one launch: the same bits as
+// q4_gemm_grouped followed by swiglu_quant(ks 1). 1 when launched, 0 when the shape has no such launch (Q4_0, K of at
+// most 16 groups, F a multiple of 128; nothing launched), -1 on bad arguments.
+bool q4_gemm_grouped_swiglu_fits(int N, int K, int wt);
+int q4_gemm_grouped_swiglu(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
+                           const uint8_t* xa, int M, int N, int K, uint8_t* xo, hipStream_t st, int wt,
+                           const int32_t* rmask, const int32_t* gsrc, int gM);
 int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, const int32_t* count, int max_items,
                     const uint8_t* xa, int M, int N, int K, float* part, size_t part_bytes, hipStream_t st,
                     int wt = WT_Q4_0, const int32_t* rmask = nullptr, const int32_t* gsrc = nullptr, int gM = 0);
