@@ -943,6 +943,7 @@ def bench_attn(args):
                              ptc.ctypes.data, err, 256)
     assert plan, err.value
     whole = bool(L.snk_attn_whole(plan))
+    fold = bool(L.snk_attn_fold(plan, 0))  # (the two launches: the fold measured slower, and this list shares chunks)
     scale = C.c_float(1.0 / np.sqrt(D))
 
     def run(i, st):
@@ -980,7 +981,7 @@ def bench_attn(args):
                "sample": f"the same 32-row attention through oracle/oracle.c (fp32 softmax over fp16 cells): median "
                          f"of {reps} warm calls, {dt * 1e3:.1f} ms each"}
     gbs = alg / (us * 1e-6) / 1e9
-    kern = "k_attn_whole" if whole else "k_attn_part + k_attn_merge"
+    kern = "k_attn_whole" if whole else "k_attn_fold" if fold else "k_attn_part + k_attn_merge"
     log(f"[bench] C2 attention: {us:.2f} us per launch ({kern}), {alg / 1e6:.1f} MB unique, "
         f"{alg_per_seq / 1e6:.1f} MB counting shared pages per sequence")
     line = {

@@ -264,11 +264,9 @@ __device__ __forceinline__ int attn_member(const AttnItem& it, int m) {
 // One work item = (query group, chunk), or a shared chunk of up to ATT_SHARE_MAX one-row groups; grid.y = KV head.
 // Writes the chunk's partial (acc[128], m, l) of every query of the item's rows; k_attn_merge folds them. A query's
 // partial depends on its own column only, so it is the same whichever item computes it.
-__global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
-    __shared__ AttnShared sh;
-    const AttnItem it = a.items[blockIdx.x];
+// (every thread of the workgroup reaches the end)
+__device__ __forceinline__ void attn_part_item(const AttnArgs& a, const AttnItem it, const int kvh, AttnShared& sh) {
     const AttnGroup gr = a.groups[it.group];
-    const int kvh = blockIdx.y;
     const int G = a.H / a.KVH;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
@@ -313,14 +311,19 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
     float M, L, acc[8];
     attn_combine(sh, wave, n, g, (shared ? nshare : gr.nrows) * G, m, l, o, qq, d0, M, L, acc);
     const int row = qq / G, head = kvh * G + qq % G;
-    if (row >= (shared ? nshare : gr.nrows)) return;
-    const int orow = shared ? a.groups[attn_member(it, row)].row0 : gr.row0 + row;
-    float* dst = a.part + (((size_t) orow * a.H + head) * a.max_chunks + it.chunk) * (ATT_D + 2);
-    *(float2*) (dst + d0) = (float2){acc[0], acc[1]};  // (a partial is 130 floats: 8-byte aligned)
-    *(float2*) (dst + d0 + 2) = (float2){acc[2], acc[3]};
-    *(float2*) (dst + d0 + 4) = (float2){acc[4], acc[5]};
-    *(float2*) (dst + d0 + 6) = (float2){acc[6], acc[7]};
-    if ((threadIdx.x & 15) == 0) *(float2*) (dst + ATT_D) = (float2){M, L};
+    if (row < (shared ? nshare : gr.nrows)) {
+        const int orow = shared ? a.groups[attn_member(it, row)].row0 : gr.row0 + row;
+        float* dst = a.part + (((size_t) orow * a.H + head) * a.max_chunks + it.chunk) * (ATT_D + 2);
+        *(float2*) (dst + d0) = (float2){acc[0], acc[1]};  // (a partial is 130 floats: 8-byte aligned)
+        *(float2*) (dst + d0 + 2) = (float2){acc[2], acc[3]};
+        *(float2*) (dst + d0 + 4) = (float2){acc[4], acc[5]};
+        *(float2*) (dst + d0 + 6) = (float2){acc[6], acc[7]};
+        if ((threadIdx.x & 15) == 0) *(float2*) (dst + ATT_D) = (float2){M, L};
+    }
+}
+__global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
+    __shared__ AttnShared sh;
+    attn_part_item(a, a.items[blockIdx.x], blockIdx.y, sh);
 }
 
 // The Q8_0 operand of the o-projection from a row's normalised outputs (ggml x86 quantize_row_q8_0, exactly as the
@@ -603,17 +606,26 @@ __global__ __launch_bounds__(512) void k_attn_run(AttnArgs a) {
 // row) are also quantized there, exactly as the activation quantizer does (ggml x86 quantize_row_q8_0), into the xa
 // operand of K = H * 128.
 #define MERGE_BATCH 16  // chunk partials a lane loads before folding them
-__global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
-    const int r = a.mrows[blockIdx.x], h = blockIdx.y, lane = threadIdx.x;
+// row r, head h by one wavefront (lane: dims 2 lane, 2 lane + 1). L2: the partials were stored in this launch by other
+// workgroups of this XCD (the caller has dropped its L1 lines: the loads read the XCD's L2)
+template <bool L2>
+__device__ __forceinline__ void attn_merge_one(const AttnArgs& a, const int r, const int h, const int lane) {
     const int nc = a.row_pos[r] / ATT_CHUNK + 1;
     const float* p0 = a.part + ((size_t) r * a.H + h) * a.max_chunks * (ATT_D + 2);
+    // (L2: a resource over the row's partials; offsets below 2^31 bytes)
+    const __amdgpu_buffer_rsrc_t pr = buf_rsrc(p0, (uint32_t) (a.max_chunks * (ATT_D + 2) * 4));
     float M = -INFINITY, L = 0.0f, o[2] = {0.0f, 0.0f};
     for (int c0 = 0; c0 < nc; c0 += MERGE_BATCH) {  // (contexts up to 4096 cells: one round of loads)
         float2 ov[MERGE_BATCH], ml[MERGE_BATCH];
         for (int j = 0; j < MERGE_BATCH; ++j) {
-            const float* pc = p0 + (size_t) (c0 + j < nc ? c0 + j : nc - 1) * (ATT_D + 2);
-            ov[j] = *(const float2*) (pc + 2 * lane);
-            ml[j] = *(const float2*) (pc + ATT_D);
+            const int pc = (c0 + j < nc ? c0 + j : nc - 1) * (ATT_D + 2);
+            if constexpr (L2) {
+                ov[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, (pc + 2 * lane) * 4, 0, 1));
+                ml[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, (pc + ATT_D) * 4, 0, 1));
+            } else {
+                ov[j] = *(const float2*) (p0 + pc + 2 * lane);
+                ml[j] = *(const float2*) (p0 + pc + ATT_D);
+            }
         }
 #pragma unroll
         for (int j = 0; j < MERGE_BATCH; ++j) {  // (a fixed trip count keeps ov and ml in registers)
@@ -656,6 +668,54 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
         }
     }
 }
+__global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
+    attn_merge_one<false>(a, a.mrows[blockIdx.x], blockIdx.y, threadIdx.x);
+}
+
+// The chunk items and their merge in one launch (plain chunk items: no shared chunks, runs or whole groups). Unit
+// (group g, KV head h) owns the group's nc chunk workgroups. The 1-D grid keeps the two-launch order (KV head, then
+// group, then chunk: measured 62.4 against 58.8 us for chunk-major) with 8 groups interleaved, so that a unit's linear
+// ids are equal modulo the XCD count nx: chunk c of (h, g) at nx ((h S + g / nx) NC + c) + g % nx (S = group slots a
+// head, NC = the most chunks of a group), and the hardware's in-turn dealing puts a unit's workgroups on one XCD. Each
+// stores its chunk's partials as k_attn_part does, then counts itself in the unit's 64-bit counter (bits 0-7 the
+// count, 7 bits an XCD from bit 8: a unit found on two XCDs sets *xerr); the count's completer folds the unit's (row,
+// head) pairs, a wavefront each, as k_attn_merge does, its loads through the XCD's L2, and takes the count back.
+__global__ __launch_bounds__(256) void k_attn_fold(AttnArgs a) {
+    __shared__ AttnShared sh;
+    __shared__ int s_last;
+    const int nx = a.nxcd, S = (a.n_groups + nx - 1) / nx, NC = a.fold_chunks;
+    const int L = (int) blockIdx.x, q = L / nx, c = q % NC, t = q / NC;
+    const int gi = (t % S) * nx + L % nx, kvh = t / S;
+    if (gi >= a.n_groups) return;  // (a padding slot)
+    const int u = gi * a.KVH + kvh;
+    const AttnGroup gr = a.groups[gi];
+    const int nc = (gr.pos0 + gr.nrows - 1) / ATT_CHUNK + 1;
+    if (c >= nc) return;  // (past the group's chunks)
+    const AttnItem it = {gi, c, 1, {-1, -1, -1}, 1};
+    attn_part_item(a, it, kvh, sh);
+    __builtin_amdgcn_s_waitcnt(0);  // the partials have reached the L2
+    __syncthreads();
+    uint64_t* cnt = a.cnt + (size_t) u * CNT_STRIDE;
+    uint64_t done = 0;
+    if (threadIdx.x == 0) {
+        unsigned xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        const int f = 8 + 7 * (int) (xcc & 7);
+        const uint64_t add = 1ull + (1ull << f);
+        const uint64_t n = __hip_atomic_fetch_add(cnt, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+        s_last = (int) (n & 255) == nc;
+        if (s_last) {
+            if ((int) ((n >> f) & 127) != nc) __hip_atomic_fetch_or(a.xerr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            done = n;
+        }
+    }
+    __syncthreads();
+    if (!s_last) return;
+    l1_drop();
+    const int G = a.H / a.KVH, wave = threadIdx.x >> 6;
+    for (int p = wave; p < gr.nrows * G; p += 4) attn_merge_one<true>(a, gr.row0 + p / G, kvh * G + p % G, threadIdx.x & 63);
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, (uint64_t) 0 - done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 int attention_runs(const AttnArgs& a, hipStream_t st) {
     if (a.n_runs <= 0) return 0;
@@ -666,12 +726,20 @@ int attention_runs(const AttnArgs& a, hipStream_t st) {
 int attention_items(const AttnArgs& a, hipStream_t st) {
     if (a.n_items <= 0) return 0;
     if (a.H % a.KVH != 0 || 16 % (a.H / a.KVH) != 0) return -1;
+    if (a.fold) {  // (the plan's chunk items in the fold's order, and their merge)
+        if (a.whole || a.n_runs > 0 || !a.cnt || !a.xerr || a.nxcd < 1 || a.n_groups < 1 || a.fold_chunks < 1 ||
+            a.fold_chunks > 127)
+            return -1;
+        const int S = (a.n_groups + a.nxcd - 1) / a.nxcd;
+        hipLaunchKernelGGL(k_attn_fold, dim3(a.nxcd * S * a.KVH * a.fold_chunks), dim3(256), 0, st, a);
+        return 0;
+    }
     if (a.whole) hipLaunchKernelGGL(k_attn_whole, dim3(a.n_items, a.KVH), dim3(512), 0, st, a);
     else hipLaunchKernelGGL(k_attn_part, dim3(a.n_items, a.KVH), dim3(256), 0, st, a);
     return 0;
 }
 int attention_merge(const AttnArgs& a, hipStream_t st) {
-    if (a.n_items <= 0 || a.whole || a.n_mrows <= 0) return 0;
+    if (a.n_items <= 0 || a.whole || a.n_mrows <= 0 || a.fold) return 0;
     hipLaunchKernelGGL(k_attn_merge, dim3(a.n_mrows, a.H), dim3(64), 0, st, a);
     return 0;
 }

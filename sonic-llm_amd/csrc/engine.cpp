@@ -101,6 +101,9 @@ struct sn_engine {
     float2* rope_cs = nullptr;  // a step's rotation table (rope_table) [max_rows][64]
     int32_t* d_xerr = nullptr;
     int fcnt_len = 0;
+    // the attention's chunk items and merge in one launch (k_attn_fold; off unless SN_ATTN_FOLD=1: measured slower, 60.2
+    // against 53.0 + 5.8 us a layer at configs[2], each chunk workgroup waiting on its count before it leaves)
+    bool attn_fold = false;
     float* apart = nullptr;
     int max_chunks = 0;
     uint8_t *d_stage = nullptr, *h_stage = nullptr;
@@ -591,6 +594,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     if (!e->rope_cs) return fail("");
     e->fuse_ok = xcd_round_robin(e->st, &e->nxcd);
     e->fuse = e->fuse_ok && !getenv("SN_NO_FUSE");
+    e->attn_fold = getenv("SN_ATTN_FOLD") && atoi(getenv("SN_ATTN_FOLD")) == 1;
     size_t ws = 0;
     ws = std::max(ws, q4_workspace_bytes(R, e->NQKV, E, e->wt));
     ws = std::max(ws, q4_workspace_bytes(R, E, QD, e->wt));
@@ -779,12 +783,17 @@ struct AttnList {
     size_t o_grp = 0, o_itm = 0, o_mrow = 0, o_run = 0;
     int n_items = 0, n_mrows = 0, n_runs = 0;
     bool whole = false;
+    // plain chunk items (no shared chunks, runs or whole groups: every group's chunks 0 .. nc - 1, one item each), the
+    // group count and the most chunks of a group: the form the fold launch takes
+    bool plain = false;
+    int n_groups = 0, max_nc = 0;
     double bytes = 0.0, merge_bytes = 0.0;
     // every value of the list the attention launches take, for a graph key: the form (whole groups launch another
     // kernel and no merge), the item, merge-row and run-item counts (grid sizes) and the staging offsets of the arrays
     void key(std::vector<int64_t>& k) const {
         k.insert(k.end(), {(int64_t) whole, (int64_t) n_items, (int64_t) n_mrows, (int64_t) o_grp, (int64_t) o_itm,
-                           (int64_t) o_mrow, (int64_t) n_runs, (int64_t) o_run});
+                           (int64_t) o_mrow, (int64_t) n_runs, (int64_t) o_run, (int64_t) plain, (int64_t) n_groups,
+                           (int64_t) max_nc});
     }
 };
 
@@ -801,6 +810,16 @@ AttnList attn_list(sn_engine* e, Stage& S, int R, const int32_t* seq, const int3
     al.n_mrows = (int) p.mrows.size();
     al.n_runs = (int) p.runs.size();
     al.whole = p.whole;
+    al.n_groups = (int) p.groups.size();
+    al.plain = !p.whole && p.runs.empty() && !p.items.empty();
+    int nct = 0;
+    for (const AttnGroup& g : p.groups) {
+        const int nc = (g.pos0 + g.nrows - 1) / ATT_CHUNK + 1;
+        al.max_nc = std::max(al.max_nc, nc);
+        nct += nc;
+    }
+    for (const AttnItem& it : p.items) al.plain = al.plain && it.share[0] < 0;
+    al.plain = al.plain && nct == al.n_items;
     // chunk partials: (acc[128], m, l) per (row, head, chunk of the row), for the rows the merge folds
     double part = 0.0;
     for (const AttnGroup& g : p.groups)
@@ -1015,11 +1034,18 @@ struct Dev {
         aa.whole = al.whole ? 1 : 0;
         aa.mrows = S.dev<const int32_t>(al.o_mrow);
         aa.n_mrows = al.n_mrows;
+        // the merge folded into the chunk launch where the list is plain chunk items (one launch, the same bits)
+        if (e->fuse && e->attn_fold && al.plain && al.max_nc <= 127 &&
+            (long) al.n_groups * e->KVH * CNT_STRIDE <= e->fcnt_len) {
+            aa.fold = 1, aa.n_groups = al.n_groups, aa.fold_chunks = al.max_nc, aa.nxcd = e->nxcd;
+            aa.cnt = e->d_fcnt, aa.xerr = e->d_xerr;
+        }
         if (al.n_runs > 0)  // (the class's bytes go with its first launch of the step)
             rc |= e->launch(SNX_K_ATTN, al.bytes, [&] { return attention_runs(aa, st); });
         if (al.n_items > 0)
-            rc |= e->launch(SNX_K_ATTN, al.n_runs > 0 ? 0.0 : al.bytes, [&] { return attention_items(aa, st); });
-        if (!al.whole && al.n_mrows > 0)
+            rc |= e->launch(SNX_K_ATTN, (al.n_runs > 0 ? 0.0 : al.bytes) + (aa.fold ? al.merge_bytes : 0.0),
+                            [&] { return attention_items(aa, st); });
+        if (!al.whole && al.n_mrows > 0 && !aa.fold)
             rc |= e->launch(SNX_K_MERGE, al.merge_bytes, [&] { return attention_merge(aa, st); });
     }
     uint16_t* kp(int layer) { return e->kbase + (size_t) layer * e->layer_halves; }

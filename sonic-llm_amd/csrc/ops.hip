@@ -881,8 +881,9 @@ __global__ __launch_bounds__(256) void k_moe_route(const float* __restrict__ hn,
     }
     __syncthreads();
     if (!s_last) return;
-    // row r0 + wave, its logits through the L2 (sc0: past the L1), its ids stored system-coherently (the last row
-    // block reads them from another XCD)
+    l1_drop();
+    // row r0 + wave, its logits through the XCD's L2 (L1 lines dropped), its ids stored system-coherently (the last
+    // row block reads them from another XCD)
     if (r0 + wave < R) {
         const int r = r0 + wave;
         const __amdgpu_buffer_rsrc_t rl = buf_rsrc(lg, (uint32_t) ((size_t) R * NE * 4));

@@ -580,8 +580,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     q4_gemm_ring<WT, MT, S, true, SW>(a);
 }
 
-// A k-slice sum of the workspace, read by the set's last workgroup (sc0: past the CU's L1, from the XCD's L2, where
-// the set's other workgroups' stores are)
+// A k-slice sum of the workspace, read by the set's last workgroup from the XCD's L2, where the set's other
+// workgroups' stores are (the workgroup has dropped its L1 lines first: l1_drop)
 __device__ __forceinline__ float4 part_load4(__amdgpu_buffer_rsrc_t r, int off) {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 1));
 }
@@ -879,6 +879,7 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
         }
         __syncthreads();
         if (!s_last) return;
+        l1_drop();
         q4_epilogue<FE, MT, S>(a, set, mt0);
         // back to zero by an atomic of the same kind, performed where the counts were (a plain store of an atomic
         // compiles to a write-through store, which need not meet the L2's copy); after the epilogue, so that no

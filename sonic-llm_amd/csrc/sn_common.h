@@ -22,6 +22,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short) 0, (int) bytes, RSRC_WORD3);
 }
 typedef __attribute__((address_space(3))) void* lds_ptr;  // an LDS address (buffer loads straight into LDS)
+// Drops this CU's vector L1 lines (buffer_inv sc0). A launch's last-arriving workgroup calls it before reading what
+// other workgroups of its XCD stored in the launch: their stores are in the XCD's L2, but a line this CU read earlier
+// in the launch (a neighbour's record sharing the line) may still sit in its L1, and a load's sc0 bit does not keep the
+// load off it.
+__device__ __forceinline__ void l1_drop() { asm volatile("buffer_inv sc0" ::: "memory"); }
 __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int vo, int so) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
 }

@@ -197,6 +197,13 @@ struct AttnArgs {
     int whole;               // items are whole groups: one kernel writes the outputs, no partials, no merge
     const int32_t* mrows;    // rows the merge folds (chunk items), n_mrows of them
     int n_mrows;
+    // (optional) fold: the chunk items and their merge in one launch (k_attn_fold: plain chunk items only, every group's
+    // chunks 0 .. nc - 1; the items array is not read). n_groups groups, fold_chunks = the most chunks of a group
+    // (<= 127); cnt: n_groups * KVH counters CNT_STRIDE apart, zero between launches; *xerr set when a (group, KV
+    // head)'s workgroups ran on two XCDs; nxcd: the XCDs the launch is dealt to in turn (xcd_round_robin).
+    int fold, n_groups, fold_chunks, nxcd;
+    uint64_t* cnt;
+    int32_t* xerr;
 };
 int paged_attention(const AttnArgs& a, hipStream_t st);  // attention_runs, attention_items, then attention_merge
 int attention_runs(const AttnArgs& a, hipStream_t st);   // the run items (nothing without)

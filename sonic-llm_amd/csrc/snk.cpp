@@ -249,6 +249,11 @@ extern "C" int snk_q4_gemm_plan_sums(const void* d_stripes, const void* d_xa, in
 struct snk_attn {
     int n_rows, H, KVH, max_pages, page_cells, max_chunks, n_items, n_mrows, n_runs;
     bool whole;
+    // the fold (chunk items and merge in one launch, k_attn_fold): plain chunk lists only; its counters and XCD check
+    bool plain = false, fold = false;
+    int n_groups = 0, max_nc = 0, nxcd = 0;
+    uint64_t* d_cnt = nullptr;
+    int32_t* d_xerr = nullptr;
     AttnGroup* d_groups = nullptr;
     AttnItem* d_items = nullptr;
     AttnItem* d_runs = nullptr;
@@ -307,7 +312,41 @@ extern "C" snk_attn* snk_attn_new_pt(int n_rows, const int32_t* seq, const int32
         snk_attn_free(p);
         return nullptr;
     }
+    // plain chunk items (every group's chunks, one item each, none shared): the fold's form, available where the device
+    // deals launches to its XCDs in turn (off until snk_attn_fold turns it on: measured slower than the two launches)
+    p->n_groups = (int) pl.groups.size();
+    int nct = 0;
+    for (const AttnGroup& g : pl.groups) {
+        const int nc = (g.pos0 + g.nrows - 1) / ATT_CHUNK + 1;
+        p->max_nc = std::max(p->max_nc, nc);
+        nct += nc;
+    }
+    p->plain = !pl.whole && pl.runs.empty() && nct == p->n_items && p->max_nc <= 127;
+    for (const AttnItem& it : pl.items) p->plain = p->plain && it.share[0] < 0;
+    if (p->plain && xcd_round_robin(nullptr, &p->nxcd)) {
+        const size_t nc8 = (size_t) p->n_groups * KVH * CNT_STRIDE * 8;
+        if (!(hipMalloc(&p->d_cnt, nc8) == hipSuccess && hipMalloc(&p->d_xerr, 4) == hipSuccess &&
+              hipMemset(p->d_cnt, 0, nc8) == hipSuccess && hipMemset(p->d_xerr, 0, 4) == hipSuccess &&
+              hipDeviceSynchronize() == hipSuccess)) {
+            hipFree(p->d_cnt);
+            hipFree(p->d_xerr);
+            p->d_cnt = nullptr, p->d_xerr = nullptr;  // (no fold for this list)
+        }
+    }
     return p;
+}
+
+extern "C" int snk_attn_fold(snk_attn* p, int on) {
+    if (!p) return 0;
+    if (!on) p->fold = false;
+    else p->fold = p->plain && p->d_cnt && p->d_xerr;
+    return p->fold ? 1 : 0;
+}
+
+extern "C" int snk_attn_xcd_faults(const snk_attn* p) {
+    int32_t v = 0;
+    if (!p || !p->d_xerr || hipMemcpy(&v, p->d_xerr, 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    return v;
 }
 
 extern "C" snk_attn* snk_attn_new(int n_rows, const int32_t* seq, const int32_t* pos, int H, int KVH, int max_pages,
@@ -342,6 +381,10 @@ static AttnArgs attn_args(snk_attn* p, const float* d_q, int ldq, const void* d_
     a.whole = p->whole ? 1 : 0;
     a.mrows = p->d_mrows;
     a.n_mrows = p->n_mrows;
+    if (p->fold) {
+        a.fold = 1, a.n_groups = p->n_groups, a.fold_chunks = p->max_nc, a.nxcd = p->nxcd;
+        a.cnt = p->d_cnt, a.xerr = p->d_xerr;
+    }
     return a;
 }
 
@@ -383,6 +426,8 @@ extern "C" void snk_attn_free(snk_attn* p) {
     hipFree(p->d_mrows);
     hipFree(p->d_pos);
     hipFree(p->d_part);
+    hipFree(p->d_cnt);
+    hipFree(p->d_xerr);
     delete p;
 }
 

@@ -125,6 +125,8 @@ SNK_API = [
     ("snk_attn_time", C.c_double, [P, P, I, P, P, P, C.c_float, P, I, I, P]),
     ("snk_attn_whole", I, [P]),
     ("snk_attn_runs", I, [P]),
+    ("snk_attn_fold", I, [P, I]),
+    ("snk_attn_xcd_faults", I, [P]),
     ("snk_attn_free", None, [P]),
     ("snk_qk_rope", I, [P, I, I, I, I, P, P, C.c_float, C.c_float, P, P, P, I, I, P, P, P]),
     ("snk_moe_router", I, [P, I, I, P, I, P, P]),

@@ -49,11 +49,13 @@ def config2_case(seed=2, S_=32, page=32, lo=256, hi=4096, n_share=8, share_cells
     return q, np.arange(S_, dtype=np.int32), (ctx - 1).astype(np.int32), kpool, vpool, pt, page
 
 
-def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None, whole=None, mode=-1, share=False, runs=None):
+def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None, whole=None, mode=-1, share=False, runs=None,
+             fold=None):
     """whole: when given, the work list's form the planner chose (whole groups, or per-chunk items and the merge) is
     checked too; mode: the form forced (snk_attn_new_mode), -1 the planner's; share: the planner sees the page table
     (snk_attn_new_pt) and reads shared chunks once for their rows; runs: when given, the number of run items the list
-    holds. The KV head count is the pools'."""
+    holds; fold: when given, the chunk items and their merge in one launch (True: the list must take it, and no unit
+    may have run on two XCDs) or in two (False). The KV head count is the pools'."""
     L = S.lib()
     kvh = kpool.shape[1]
     err = __import__("ctypes").create_string_buffer(256)
@@ -75,12 +77,16 @@ def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None, whole=None, 
         assert L.snk_attn_runs(plan) == runs, (L.snk_attn_runs(plan), runs)
     if bufs is None:
         bufs = (U.dev(kpool), U.dev(vpool), U.dev(pt))
+    if fold is not None:
+        assert L.snk_attn_fold(plan, int(fold)) == int(fold)
     dq = U.dev(q)
     out = U.empty(q.size * 4)
     rc = L.snk_attn_run(plan, U.ptr(dq), H * D, U.ptr(bufs[0]), U.ptr(bufs[1]), U.ptr(bufs[2]), scale, U.ptr(out),
                         H * D, U.stream())
+    faults = L.snk_attn_xcd_faults(plan) if fold else 0
     L.snk_attn_free(plan)
     assert rc == 0
+    assert faults == 0
     return U.host(out, np.float32)[:q.size].reshape(q.shape)
 
 
@@ -280,3 +286,25 @@ def test_prompt_runs_chosen_for_prompt_steps():
     sel = np.r_[0:8, 250:262, 504:512]  # rows at the first, middle and last chunk edges (the oracle is slow)
     ref = O.paged_attn(qr[sel], rseq[sel], rpos[sel], KVH, kp, vp, pg, pt, scale)
     assert np.all(np.abs(auto[sel] - ref) <= ATOL + RTOL * np.abs(ref))
+
+
+@pytest.mark.parametrize("kvh,page,lo,hi,verify", [(8, 32, 256, 4096, False), (8, 64, 2040, 2100, False),
+                                                   (4, 64, 1500, 2600, True), (8, 32, 1, 300, True),
+                                                   (16, 64, 300, 1200, False), (2, 64, 500, 900, True)])
+def test_fold_equals_two_launches_bitwise(kvh, page, lo, hi, verify):
+    """The chunk items and their merge in one launch (k_attn_fold: a (group, KV head)'s chunk workgroups dealt to one
+    XCD, the last of them folding the group's rows through its L2) against the partial kernel and the merge kernel:
+    the same bits on decode rows and on 4-row verify groups, at G = 2 .. 16 and both page sizes, against the oracle,
+    and no unit found on two XCDs."""
+    q, seq, pos, kp, vp, pt, pg = config2_case(seed=50 + kvh + lo, S_=32, page=page, lo=lo, hi=hi, n_share=0, kvh=kvh)
+    if verify:  # 4 consecutive positions of each of 8 sequences
+        seq = np.repeat(seq[:8], 4).astype(np.int32)
+        pos = (np.repeat(np.maximum(pos[:8], 3) - 3, 4) + np.tile(np.arange(4), 8)).astype(np.int32)
+        q = np.random.default_rng(kvh + 1).standard_normal((32, H, D), dtype=np.float32)
+    scale = 1 / math.sqrt(D)
+    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    one = attn_gpu(q, seq, pos, kp, vp, pt, pg, scale, bufs, mode=0, fold=True)
+    two = attn_gpu(q, seq, pos, kp, vp, pt, pg, scale, bufs, mode=0, fold=False)
+    assert np.array_equal(one.view(np.uint32), two.view(np.uint32))
+    ref = O.paged_attn(q, seq, pos, kvh, kp, vp, pg, pt, scale)
+    assert np.all(np.abs(one - ref) <= ATOL + RTOL * np.abs(ref))

@@ -8,8 +8,8 @@ import pytest
 import sllm_next as S
 
 # The attention plan's fields in the key: form, items, merge rows, the offsets of groups, items and merge rows, run
-# items and their offset
-ATTN_FIELDS = 8
+# items and their offset, then the fold's: plain chunk items, groups, the most chunks of a group
+ATTN_FIELDS = 11
 
 
 def rows(n, pos):
