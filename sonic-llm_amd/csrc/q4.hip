@@ -383,7 +383,7 @@ __device__ __forceinline__ half8 q8_unpack(uint32_t w_lo, uint32_t w_hi) {
 // as its own launch would (the same groups, an odd slice's extra group added with scale 0 as its own ring pads it),
 // and adds the slices in slice order as the consumers do ((p0 + p1) + p2 ...), so part[0] holds, bit for bit, what
 // the consumers would have made of the split launch's slices: they read it as one slice.
-template <int WT, int MT, int S, bool FK, bool SW = false>
+template <int WT, int MT, int S, bool FK, bool SW = false, bool GRP = false>
 __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
     constexpr int D = 2, FPW = MT;  // ring slots, fragments each wavefront stages
     // the loop below stages group i + 1 from register slot j (which holds group i's weights and group i + 1's records)
@@ -400,7 +400,7 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
     const int set = blockIdx.x, slice = blockIdx.y;
     int mt0 = blockIdx.z * MT;
     const uint8_t* wbase = a.w;
-    if (a.items) {  // grouped: this workgroup's (expert, row tile)
+    if constexpr (GRP) {  // grouped: this workgroup's (expert, row tile)
         if ((int) blockIdx.z >= *a.count) return;
         wbase = a.w + (size_t) a.items[2 * blockIdx.z] * a.wstride;
         mt0 = a.items[2 * blockIdx.z + 1];
@@ -410,9 +410,10 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
     // the groups in order, the last slice padded to an even count as its own launch pads it)
     const int c0 = FK ? 0 : slice * a.gps, ng = FK ? a.ngroups : min(a.gps, a.ngroups - c0);
     const int s0 = set * (4 * S) + wave * S;
-    const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(S, a.nstripes - s0)));
     const int sbytes = a.ngroups * TB;  // one stripe
-    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(wbase + (size_t) min(s0, a.nstripes - 1) * sbytes, (uint32_t) (nvalid * sbytes));
+    // one resource for the whole matrix, the wavefront's stripes by scalar offsets (stripes past the matrix read as
+    // zeros: the range check covers the scalar offset too)
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(wbase, (uint32_t) (a.nstripes * sbytes));
     const int rstride = a.ngroups * XA_REC;  // between row tiles' records
     // the activation: the operand's records from row tile mt0 on; or, gathering (a.gsrc, one row tile), each lane's row
     // m = lane % 16 of the tile taken from row gsrc[16 mt0 + m] of a row-ordered operand of a.gM rows (a padding row,
@@ -421,7 +422,7 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
     size_t x0 = (size_t) mt0 * a.ngroups * XA_REC;
     uint32_t xbytes = (uint32_t) (xa_bytes(a.M, a.K) - x0);
     int vf_off = 16 * lane, vk_off = 4 * lane;
-    if (a.gsrc) {
+    if (GRP && a.gsrc) {
         const int sr = a.gsrc[16 * mt0 + (lane & 15)];
         x0 = 0;
         xbytes = (uint32_t) xa_bytes(a.gM, a.K);
@@ -456,7 +457,7 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
         load_act(ra[slot], rk[slot], i + 1);
         const int c = c0 + min(i, ng - 1);
         for (int s = 0; s < S; ++s) {
-            const int so = s * sbytes + c * TB;
+            const int so = (s0 + s) * sbytes + c * TB;
             for (int h = 0; h < NW; ++h) wq[slot][s][h] = bload16(wr, 16 * NW * lane + 16 * h, so);
             ws[slot][s] = bload8(wr, SO + 8 * n_in, so);
         }
@@ -563,15 +564,16 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
         for (int mt = 0; mt < MT; ++mt)
             for (int v = 0; v < 4; ++v) {
                 const int row = (mt0 + mt) * 16 + 4 * g + v;
-                if (row < a.M && (!a.rmask || a.rmask[row] >= 0))
+                if (row < a.M && (!GRP || !a.rmask || a.rmask[row] >= 0))
                     a.part[((size_t) slice * a.M + row) * a.N + col] = acc[s][mt][v];
             }
     }
 }
 
-template <int WT, int MT, int S, bool FK = false>
+// GRP: grouped (expert items, gathered rows, row masks); compiled out of the other launches
+template <int WT, int MT, int S, bool FK = false, bool GRP = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_q4_gemm(GemmArgs a) {
-    q4_gemm_ring<WT, MT, S, FK>(a);
+    q4_gemm_ring<WT, MT, S, FK, false, GRP>(a);
 }
 // the FK walk with two stripes a wavefront (prompt rows of the wide matrices): its accumulators and slice sums need
 // more than the 168 registers of 3 wavefronts a SIMD. SW: the gate|up matrix's SwiGLU + Q8_0 as its epilogue
@@ -681,14 +683,14 @@ __device__ __forceinline__ void q4_epilogue(const GemmArgs& a, int set, int mt0)
 // stripes' weights through a ring of D register slots (group i + D's loads issued as soon as group i is summed), with
 // no further synchronisation. The activation fragment, scales and corrections read from LDS for a block serve S x MT
 // MFMAs. Same arithmetic and order as k_q4_gemm. FE: the fused epilogue run by each set's last workgroup (GemmArgs).
-template <int WT, int MT, int S, int D, int GMAX, int FE = FE_NONE>
+template <int WT, int MT, int S, int D, int GMAX, int FE = FE_NONE, bool GRP = FE == FE_GSWIGLU>
 __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     constexpr bool Q8 = WT == WT_Q8_0;
     constexpr int TB = Q8 ? Q8T_BYTES : Q4T_BYTES, SO = Q8 ? Q8T_SCALE_OFF : Q4T_SCALE_OFF;
     constexpr int NW = Q8 ? 2 : 1;
     constexpr int CORR = Q8 ? XA_CORR8_OFF : XA_CORR_OFF;
-    constexpr int NF = GMAX * MT * 4, FPW = NF / 4;
-    constexpr int NK = GMAX * MT * 2, KPW = (NK + 3) / 4;
+    constexpr int NF = GMAX * MT * 4;
+    constexpr int NK = GMAX * MT * 2;
     __shared__ __attribute__((aligned(16))) uint8_t s_act[NF][1024];
     __shared__ __attribute__((aligned(16))) float s_k[GMAX][MT][2][64];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -699,7 +701,7 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     }
     int mt0 = (int) blockIdx.z * MT;
     const uint8_t* wbase = a.w;
-    if (a.items) {  // grouped (MT = 1, no epilogue): this workgroup's (expert, row tile)
+    if constexpr (GRP) {  // grouped (MT = 1): this workgroup's (expert, row tile)
         if ((int) blockIdx.z >= *a.count) return;
         wbase = a.w + (size_t) a.items[2 * blockIdx.z] * a.wstride;
         mt0 = a.items[2 * blockIdx.z + 1];
@@ -707,9 +709,9 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     mt0 = __builtin_amdgcn_readfirstlane(mt0);
     const int c0 = slice * a.gps, ng = __builtin_amdgcn_readfirstlane(min(a.gps, a.ngroups - c0));
     const int s0 = set * (4 * S) + wave * S;
-    const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(S, a.nstripes - s0)));
     const int sbytes = a.ngroups * TB;
-    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(wbase + (size_t) min(s0, a.nstripes - 1) * sbytes, (uint32_t) (nvalid * sbytes));
+    // one resource for the whole matrix (see q4_gemm_ring)
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(wbase, (uint32_t) (a.nstripes * sbytes));
     const int rstride = a.ngroups * XA_REC;
     // the activation: the operand's records from row tile mt0 on; or, gathering (a.gsrc, one row tile), lane l's row
     // m = l % 16 of the tile taken from row gsrc[16 mt0 + m] of a row-ordered operand of a.gM rows (a padding row,
@@ -718,7 +720,7 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     size_t x0 = (size_t) mt0 * a.ngroups * XA_REC;
     uint32_t xbytes = (uint32_t) (xa_bytes(a.M, a.K) - x0);
     int vf_off = 16 * lane, vk_off = 4 * lane;
-    if (a.gsrc) {
+    if (GRP && a.gsrc) {
         const int sr = a.gsrc[16 * mt0 + (lane & 15)];
         x0 = 0;
         xbytes = (uint32_t) xa_bytes(a.gM, a.K);
@@ -745,7 +747,7 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     auto wload = [&](int slot, int i) {  // group i's weights (i past the slice: its last group again)
         const int c = c0 + min(i, ng - 1);
         for (int t = 0; t < S; ++t) {
-            const int so = t * sbytes + c * TB;
+            const int so = (s0 + t) * sbytes + c * TB;
             for (int h = 0; h < NW; ++h) wq[slot][t][h] = bload16(wr, 16 * NW * lane + 16 * h, so);
             ws[slot][t] = bload8(wr, SO + 8 * n_in, so);
         }
@@ -846,7 +848,7 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
         const int r = e / (4 * S), c4 = (e % (4 * S)) * 4;
         const int row = mt0 * 16 + r, col = s0 * 16 + c4;
         if (row >= a.M || col >= a.N) continue;  // (a stripe past the matrix is not stored)
-        if (a.rmask && a.rmask[row] < 0) continue;
+        if (GRP && a.rmask && a.rmask[row] < 0) continue;
         const float4 v = *(const float4*) &tile[r * TW + c4];
         float* dst = &a.part[((size_t) slice * a.M + row) * a.N + col];
         if (a.N % 4 == 0) {
@@ -917,8 +919,8 @@ __global__ __launch_bounds__(256) void k_q4_gemv(GemmArgs a) {
     const int s0 = set * 16 + wave * 4;
     const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(4, a.nstripes - s0)));
     const int sbytes = a.ngroups * TB;
-    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(a.w + (size_t) min(s0, a.nstripes - 1) * sbytes, (uint32_t) (nvalid * sbytes));
-    const int vst = sl * sbytes;  // this lane's stripe
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(a.w, (uint32_t) (a.nstripes * sbytes));  // (the whole matrix)
+    const int vst = sl * sbytes;  // this lane's stripe, from the wavefront's first
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xa, (uint32_t) xa_bytes(a.M, a.K));
     // the staging loads first (item (m, block, part g): the 8 fp16 of row m's fragment piece g), then the weights
     u32x4 rq[NIT];
@@ -935,7 +937,7 @@ __global__ __launch_bounds__(256) void k_q4_gemv(GemmArgs a) {
     u32x4 wq[D][4];
     u32x2 ws[D];
     auto load = [&](int slot, int i) {  // group i of the slice (past it: its last group again)
-        const int so = (c0 + min(i, ng - 1)) * TB;
+        const int so = s0 * sbytes + (c0 + min(i, ng - 1)) * TB;
         for (int g = 0; g < 4; ++g) wq[slot][g] = bload16(wr, vst + 16 * (n + 16 * g), so);
         ws[slot] = bload8(wr, vst + SO + 8 * n, so);
     };
@@ -1330,7 +1332,7 @@ template <int WT>
 static bool launch_grouped_s(int S, int ng, dim3 grid, const GemmArgs& a, hipStream_t st) {
 #define GSG(S_, GM_)                                                                                         \
     if (S == S_ && ng <= GM_) {                                                                              \
-        hipLaunchKernelGGL((k_q4_gemm_s<WT, 1, S_, 2, GM_>), grid, dim3(256), 0, st, a);                     \
+        hipLaunchKernelGGL((k_q4_gemm_s<WT, 1, S_, 2, GM_, FE_NONE, true>), grid, dim3(256), 0, st, a);      \
         return true;                                                                                         \
     }
     if constexpr (WT == WT_Q4_0) {
@@ -1369,9 +1371,11 @@ int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, cons
     // (K past 16 groups) the ring kernel. Q4_0: 2 stripes a wavefront; Q8_0 tiles take one (twice the weight
     // registers)
     if (wt == WT_Q8_0) {
-        hipLaunchKernelGGL((k_q4_gemm<WT_Q8_0, 1, 1>), dim3((a.nstripes + 3) / 4, 1, max_items), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((k_q4_gemm<WT_Q8_0, 1, 1, false, true>), dim3((a.nstripes + 3) / 4, 1, max_items), dim3(256), 0,
+                           st, a);
     } else {
-        hipLaunchKernelGGL((k_q4_gemm<WT_Q4_0, 1, 2>), dim3((a.nstripes + 7) / 8, 1, max_items), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((k_q4_gemm<WT_Q4_0, 1, 2, false, true>), dim3((a.nstripes + 7) / 8, 1, max_items), dim3(256), 0,
+                           st, a);
     }
     return 1;
 }

@@ -186,9 +186,9 @@ __global__ __launch_bounds__(256, MT == 1 ? 4 : 2) void k_q6k_gemm(const uint8_t
     const int nb = K / 256, nstripes = (N + Q6T_ROWS - 1) / Q6T_ROWS;
     const int stripe = blockIdx.x * 4 + wave;
     const int mt0 = mt_first + blockIdx.y * MT;
-    const int nvalid = __builtin_amdgcn_readfirstlane(stripe < nstripes ? 1 : 0);
-    const __amdgpu_buffer_rsrc_t wr =
-        buf_rsrc(tiles + (size_t) min(stripe, nstripes - 1) * nb * Q6T_BYTES, (uint32_t) (nvalid * nb * Q6T_BYTES));
+    // one resource for the whole matrix (a stripe past it reads zeros: the range check covers the scalar offset)
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(tiles, (uint32_t) ((size_t) nstripes * nb * Q6T_BYTES));
+    const int sofs = stripe * nb * Q6T_BYTES;
     // this workgroup's records: MT row tiles x nb blocks, row tile mt's block b at (mt * nb + b) * XK_REC
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(xk + (size_t) mt0 * nb * XK_REC, (uint32_t) ((size_t) MT * nb * XK_REC));
 
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256, MT == 1 ? 4 : 2) void k_q6k_gemm(const uint8_t
     u32x4 rq[QPT];
     uint32_t rd;
     auto load_w = [&](int slot, int b) {
-        const int so = min(b, nb - 1) * Q6T_BYTES;
+        const int so = sofs + min(b, nb - 1) * Q6T_BYTES;
         for (int k = 0; k < 6; ++k) wq[slot][k] = bload16(wr, 1024 * k + 16 * lane, so);
         sc4[slot] = bload16(wr, Q6T_SCALE_OFF + 16 * n, so);
         dw[slot] = __builtin_bit_cast(uint32_t, bload4f(wr, Q6T_D_OFF + 4 * (n >> 1), so));

@@ -84,6 +84,22 @@ def test_quantize_q4_0_first_of_equal_magnitudes():
     assert nib[3] == 0 and nib[9] == 15  # +0.25 / (0.25/8) + 8.5 = 16.5 -> clamped to 15
 
 
+def test_quantize_q4_0_half_steps_round_up():
+    """ggml's quantize_row_q4_0_ref truncates x * id + 8.5 toward zero, so a value exactly half-way between two levels
+    takes the upper one (7.5 -> 8 would be 8 under round-half-even: these cases tell the rules apart), clamped at 15."""
+    x = np.zeros((1, 32), np.float32)
+    x[0, 0] = -8.0  # the extreme element: d = -8 / -8 = 1, id = 1 (exact)
+    vals = [0.5, 2.5, -1.5, 4.5, -3.5, 6.5, -5.5, 1.5, -0.5, 7.5, -7.5, 3.0, -6.0]
+    x[0, 1:1 + len(vals)] = vals
+    q = O.quantize_q4_0(x).reshape(18)
+    assert float(q[:2].copy().view(np.float16)[0]) == 1.0
+    nib = np.concatenate([q[2:] & 15, q[2:] >> 4]).astype(np.int64)
+    want = [min(15, int(np.floor(v + 8.5))) for v in vals]
+    assert want[:3] == [9, 11, 7]  # (half-even would give 8, 10, 6)
+    assert list(nib[1:1 + len(vals)]) == want, (list(nib[1:1 + len(vals)]), want)
+    assert nib[0] == 0 and np.all(nib[1 + len(vals):] == 8)
+
+
 # ---- Q8_0 and the integer dot -------------------------------------------------------------------------------------------
 def test_quantize_q8_0_invariants():
     r = rng(3)
