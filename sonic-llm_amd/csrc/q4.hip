@@ -604,9 +604,9 @@ template <int FE, int MT, int S>
 __device__ __forceinline__ void q4_epilogue(const GemmArgs& a, int set, int mt0) {
     const int ks = (int) gridDim.y;
     const __amdgpu_buffer_rsrc_t pr = buf_rsrc(a.part, (uint32_t) ((size_t) ks * a.M * a.N * sizeof(float)));
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    constexpr int KM = 1 << (FE & 7);  // the slices' bound: every slice's values loaded at once (the index clamped,
-                                       // so no load sits behind a branch; the slices past ks are not added)
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int KM = fe_slice_bound(FE & 7);  // the slices' bound: every slice's values loaded at once (the index
+                                                // clamped, so no load sits behind a branch; slices past ks not added)
     if constexpr (FE >= FE_SWIGLU && FE < FE_ROPE) {
         const int F = a.N / 2;
         for (int it = threadIdx.x; it < 16 * MT * S * 4; it += 256) {
@@ -1241,25 +1241,29 @@ int q4_gemm_fused(const uint8_t* w, const uint8_t* xa, int M, int N, int K, floa
     a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
     a.mtiles = (M + 15) / 16;
     a.items = nullptr; a.count = nullptr; a.rmask = nullptr; a.gsrc = nullptr;
-    // the epilogue's slice bound (as the row kernels' KM): instance FE + log2 KM
-    const int lk = p.ks <= 1 ? 0 : p.ks <= 2 ? 1 : p.ks <= 4 ? 2 : p.ks <= 8 ? 3 : 4;
+    // the epilogue's slice bound: instance FE + fe_slice_index(ks) (KM = fe_slice_bound of it, the least one >= ks)
+    const int lk = fe_slice_index(p.ks);
     bool ok = false;
     auto go = [&](auto fe_c) {
         constexpr int F0 = decltype(fe_c)::value;
-        if (wt == WT_Q8_0) {
-            if constexpr (F0 == FE_SWIGLU) {  // (SwiGLU: at most 8 slices, fused_shape)
-                if (lk == 0) ok = launch_gemm_fe<WT_Q8_0, F0>(mt, spw, p.gps, grid, a, st);
-                else if (lk == 1) ok = launch_gemm_fe<WT_Q8_0, F0 + 1>(mt, spw, p.gps, grid, a, st);
-                else if (lk == 2) ok = launch_gemm_fe<WT_Q8_0, F0 + 2>(mt, spw, p.gps, grid, a, st);
-                else if (lk == 3) ok = launch_gemm_fe<WT_Q8_0, F0 + 3>(mt, spw, p.gps, grid, a, st);
+        auto pick = [&](auto wt_c) {
+            constexpr int W = decltype(wt_c)::value;
+            switch (lk) {
+                case 0: ok = launch_gemm_fe<W, F0 + 0>(mt, spw, p.gps, grid, a, st); break;
+                case 1: ok = launch_gemm_fe<W, F0 + 1>(mt, spw, p.gps, grid, a, st); break;
+                case 2: ok = launch_gemm_fe<W, F0 + 2>(mt, spw, p.gps, grid, a, st); break;
+                case 3: ok = launch_gemm_fe<W, F0 + 3>(mt, spw, p.gps, grid, a, st); break;
+                case 4: ok = launch_gemm_fe<W, F0 + 4>(mt, spw, p.gps, grid, a, st); break;
+                case 5: ok = launch_gemm_fe<W, F0 + 5>(mt, spw, p.gps, grid, a, st); break;
+                case 6: if constexpr (F0 == FE_ROPE) ok = launch_gemm_fe<W, F0 + 6>(mt, spw, p.gps, grid, a, st); break;
+                case 7: if constexpr (F0 == FE_ROPE) ok = launch_gemm_fe<W, F0 + 7>(mt, spw, p.gps, grid, a, st); break;
             }
+        };
+        if (wt == WT_Q8_0) {
+            if constexpr (F0 == FE_SWIGLU) pick(std::integral_constant<int, WT_Q8_0>{});  // (SwiGLU: at most 8 slices)
             return;
         }
-        if (lk == 0) ok = launch_gemm_fe<WT_Q4_0, F0>(mt, spw, p.gps, grid, a, st);
-        else if (lk == 1) ok = launch_gemm_fe<WT_Q4_0, F0 + 1>(mt, spw, p.gps, grid, a, st);
-        else if (lk == 2) ok = launch_gemm_fe<WT_Q4_0, F0 + 2>(mt, spw, p.gps, grid, a, st);
-        else if (lk == 3) ok = launch_gemm_fe<WT_Q4_0, F0 + 3>(mt, spw, p.gps, grid, a, st);
-        else if constexpr (F0 == FE_ROPE) ok = launch_gemm_fe<WT_Q4_0, F0 + 4>(mt, spw, p.gps, grid, a, st);
+        pick(std::integral_constant<int, WT_Q4_0>{});
     };
     if (fe == FE_SWIGLU) go(std::integral_constant<int, FE_SWIGLU>{});
     else go(std::integral_constant<int, FE_ROPE>{});

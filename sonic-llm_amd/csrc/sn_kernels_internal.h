@@ -50,8 +50,18 @@ struct GemmArgs {
 // the streaming kernel's fused epilogues: none (the k-slice sums for the row kernels), the SwiGLU + Q8_0 of a
 // stripe-interleaved gate|up matrix (k_swiglu_quant's arithmetic), the q|k|v heads' QK-norm + RoPE + cache write
 // (k_qk_rope's arithmetic)
-// (the kernel's instances: FE + log2 KM, KM the slice bound of the epilogue's loads)
+// (the kernel's instances: FE + i, i = 0..7, whose KM = fe_slice_bound(i) bounds the slices the epilogue loads)
 enum { FE_NONE = 0, FE_SWIGLU = 8, FE_ROPE = 16, FE_GSWIGLU = 32 };  // (FE_GSWIGLU: grouped, one slice; no counters)
+// the epilogue instances' slice bounds (the exact counts of the common plans: 3 gate|up, 5 q|k|v at K = 2560, 10 ...)
+__host__ __device__ constexpr int fe_slice_bound(int i) {
+    return i == 0 ? 1 : i == 1 ? 2 : i == 2 ? 3 : i == 3 ? 4 : i == 4 ? 5 : i == 5 ? 8 : i == 6 ? 10 : 16;
+}
+// the index of the least bound that holds ks slices (1 <= ks <= 16)
+static inline int fe_slice_index(int ks) {
+    int i = 0;
+    while (i < 7 && fe_slice_bound(i) < ks) ++i;
+    return i;
+}
 
 // Launch shape of one matrix: a workgroup owns 4 spw stripes (a "set": spw per wavefront) and gps consecutive 4-block
 // groups (a slice). Layer-sized matrices at decode row counts run the streaming kernel (sspw stripes a wavefront,
