@@ -1528,6 +1528,7 @@ static void launch_resid(int km, int nt, float* x, const float* part, int ks, in
     else if (km == 2) RQ(2);
     else if (km == 4) RQ(4);
     else if (km == 8) RQ(8);
+    else if (km == 10) RQ(10);
     else RQ(16);
 #undef RQ
 }
@@ -1537,7 +1538,8 @@ int resid_quant(float* x, const float* part, int ks, int M, int K, const float* 
     if (M <= 0) return 0;
     // 4 lanes per block of the padded row, in whole wavefronts, at most 1024 lanes (then IT passes)
     const int lanes = 4 * xa_nbp(K), nt = std::min(1024, (lanes + 63) / 64 * 64), it = (lanes + nt - 1) / nt;
-    const int km = ks_bound(ks);
+    // (10: the exact count of the deep down projections' plans, no clamped copies of the last slice loaded)
+    const int km = ks == 9 || ks == 10 ? 10 : ks_bound(ks);
     if (K % 32 || it > 4 || (xn && !xa) || km == 0) return -1;
     const int ad = add ? 1 : 0;
     if (it == 1) launch_resid<1>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
