@@ -1061,14 +1061,19 @@ GemmPlan q4_plan(int N, int K, int wt) {
     // stripes, both row tiles in one workgroup), down 8.4 (10 slices); the ring kernel with its earlier slices took
     // 7.5, 6.4, 15.0 and 10.8.
     p.stream = true;
-    p.gps = std::min(p.nstripes >= 1024 || p.ngroups >= 64 ? 8 : 4, (p.ngroups + 1) / 2 * 2);
+    // (8 groups also for the narrow and deep o projection, 4 slices at K = 4096: decode 7,820 -> 7,860 tok/s in the
+    // engine, measured against the other plans of the four matrices in one call)
+    const bool narrow_deep = p.nstripes < 384 && p.ngroups >= 32;
+    p.gps = std::min(p.nstripes >= 1024 || p.ngroups >= 64 || narrow_deep ? 8 : 4, (p.ngroups + 1) / 2 * 2);
     // the slices' consumers (the row kernels) add at most KS_MAX of them: deeper matrices take longer slices (Qwen3-14B's
     // down projection, K = 17408: 10 groups, 14 slices; Qwen3-32B's, K = 25600: 14 groups, 15 slices). The streaming
     // kernel stages at most 8 groups of a slice in LDS; longer slices go to the ring kernel, whose LDS holds two groups.
     while (slices(p.gps) > KS_MAX) p.gps += 2;
     if (p.gps > 8) p.stream = false;
     p.ks = slices(p.gps);
-    p.sspw = wt != WT_Q8_0 && p.nstripes >= 384 ? 2 : 1;
+    // two stripes a wavefront for the wide matrices and the deep down projection (whose 8-stripe sets then make 400
+    // workgroups at 32 rows: with the o projection's plan above, decode 7,820 -> 7,900 tok/s)
+    p.sspw = wt != WT_Q8_0 && (p.nstripes >= 384 || p.ngroups >= 64) ? 2 : 1;
     p.smt = p.nstripes >= 1024 ? 2 : 1;
     // the ring kernel (prompt rows) with the same slices: one stripe a wavefront
     p.spw = 1;
