@@ -606,19 +606,19 @@ __global__ __launch_bounds__(512) void k_attn_run(AttnArgs a) {
 // behind a branch), then folded in order. With a.xa the head's 128 outputs (4 Q8_0 blocks of the o-projection's input
 // row) are also quantized there, exactly as the activation quantizer does (ggml x86 quantize_row_q8_0), into the xa
 // operand of K = H * 128.
-#define MERGE_BATCH 16  // chunk partials a lane loads before folding them
+#define MERGE_BATCH 16  // chunk partials a lane loads before folding them (the fold's completers)
 // row r, head h by one wavefront (lane: dims 2 lane, 2 lane + 1). L2: the partials were stored in this launch by other
 // workgroups of this XCD (the caller has dropped its L1 lines: the loads read the XCD's L2)
-template <bool L2>
+template <bool L2, int MB = MERGE_BATCH>
 __device__ __forceinline__ void attn_merge_one(const AttnArgs& a, const int r, const int h, const int lane) {
     const int nc = a.row_pos[r] / ATT_CHUNK + 1;
     const float* p0 = a.part + ((size_t) r * a.H + h) * a.max_chunks * (ATT_D + 2);
     // (L2: a resource over the row's partials; offsets below 2^31 bytes)
     const __amdgpu_buffer_rsrc_t pr = buf_rsrc(p0, (uint32_t) (a.max_chunks * (ATT_D + 2) * 4));
     float M = -INFINITY, L = 0.0f, o[2] = {0.0f, 0.0f};
-    for (int c0 = 0; c0 < nc; c0 += MERGE_BATCH) {  // (contexts up to 4096 cells: one round of loads)
-        float2 ov[MERGE_BATCH], ml[MERGE_BATCH];
-        for (int j = 0; j < MERGE_BATCH; ++j) {
+    for (int c0 = 0; c0 < nc; c0 += MB) {  // (contexts up to 4096 cells: one round of loads)
+        float2 ov[MB], ml[MB];
+        for (int j = 0; j < MB; ++j) {
             const int pc = (c0 + j < nc ? c0 + j : nc - 1) * (ATT_D + 2);
             if constexpr (L2) {
                 ov[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, (pc + 2 * lane) * 4, 0, 1));
@@ -629,7 +629,7 @@ __device__ __forceinline__ void attn_merge_one(const AttnArgs& a, const int r, c
             }
         }
 #pragma unroll
-        for (int j = 0; j < MERGE_BATCH; ++j) {  // (a fixed trip count keeps ov and ml in registers)
+        for (int j = 0; j < MB; ++j) {  // (a fixed trip count keeps ov and ml in registers)
             if (c0 + j >= nc) continue;  // past the row's chunks
             const float v2[2] = {ov[j].x, ov[j].y};
             attn_fold<2>(M, L, o, ml[j].x, ml[j].y, v2);
@@ -669,8 +669,9 @@ __device__ __forceinline__ void attn_merge_one(const AttnArgs& a, const int r, c
         }
     }
 }
+template <int MB>
 __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
-    attn_merge_one<false>(a, a.mrows[blockIdx.x], blockIdx.y, threadIdx.x);
+    attn_merge_one<false, MB>(a, a.mrows[blockIdx.x], blockIdx.y, threadIdx.x);
 }
 
 // The chunk items and their merge in one launch (plain chunk items: no shared chunks, runs or whole groups). Unit
@@ -745,7 +746,15 @@ int attention_items(const AttnArgs& a, hipStream_t st) {
 }
 int attention_merge(const AttnArgs& a, hipStream_t st) {
     if (a.n_items <= 0 || a.whole || a.n_mrows <= 0 || a.fold) return 0;
-    hipLaunchKernelGGL(k_attn_merge, dim3(a.n_mrows, a.H), dim3(64), 0, st, a);
+    // a row's chunk partials in one round of loads, as few clamped copies as the instances allow (configs[2]'s 9
+    // chunks: 10 a round, decode 7,885 -> 7,918 tok/s against 16; configs[1]'s up to 16 chunks: 16)
+    const int mc = a.max_chunks;
+    const dim3 grid(a.n_mrows, a.H);
+    if (mc <= 8) hipLaunchKernelGGL(k_attn_merge<8>, grid, dim3(64), 0, st, a);
+    else if (mc <= 10) hipLaunchKernelGGL(k_attn_merge<10>, grid, dim3(64), 0, st, a);
+    else if (mc <= 12) hipLaunchKernelGGL(k_attn_merge<12>, grid, dim3(64), 0, st, a);
+    else if (mc <= 16) hipLaunchKernelGGL(k_attn_merge<16>, grid, dim3(64), 0, st, a);
+    else hipLaunchKernelGGL(k_attn_merge<20>, grid, dim3(64), 0, st, a);
     return 0;
 }
 int paged_attention(const AttnArgs& a, hipStream_t st) {
