@@ -965,7 +965,9 @@ def bench_attn(args):
         from oracle import oracle as O
         O.build() if not os.path.exists(O.LIB_PATH) else None
         kp, vp = pools[0]
-        kh = kp.cpu().numpy().view(np.uint16).reshape(need, KVH, page, D)
+        # (K regions are stored chunk-major, [16][cells][8]: back to cell-major for the oracle)
+        kh = np.ascontiguousarray(kp.cpu().numpy().view(np.uint16).reshape(need, KVH, D // 8, page, 8)
+                                  .transpose(0, 1, 3, 2, 4)).reshape(need, KVH, page, D)
         vh = vp.cpu().numpy().view(np.uint16).reshape(need, KVH, page, D)
         run(0, st0)
         got = U.host(out, np.float32)[:n_seq * H * D].reshape(n_seq, H, D)

@@ -101,7 +101,8 @@ int snk_q4_gemm_plan_sums(const void* d_stripes, const void* d_xa, int M, int N,
 
 // ---- paged GQA attention (decode and verify rows) -------------------------------------------------------------------
 // Replaces attn_part + attn_merge (kernels.metal:1122-1192) and fa2 (kernels.metal:2674-2770). q: [rows][H][128] fp32
-// (ldq floats apart); K/V pool fp16, page p of KV head h at pool + ((p * KVH + h) * page_cells) * 128; d_pt:
+// (ldq floats apart); K/V pool fp16, page p of KV head h at pool + ((p * KVH + h) * page_cells) * 128 (a V cell: 128
+// contiguous values; a K region: chunk-major, dim d of cell c at 8 * (page_cells * (d / 8) + c) + d % 8); d_pt:
 // [sequences][max_pages] int32; out: [rows][ldo] fp32. Row r of sequence seq[r] attends cells 0 .. pos[r].
 typedef struct snk_attn snk_attn;
 // the work list of a set of rows (host arrays), built once and reused by snk_attn_run; NULL on failure (err)
@@ -145,8 +146,9 @@ void snk_attn_free(snk_attn* p);
 
 // ---- per-head QK-norm + NEOX RoPE + K/V cache write (qk_rope, kernels.metal:149-197) -------------------------------
 // d_qkv: R rows of [q: H*128 | k: KVH*128 | v: KVH*128] fp32, ldqkv floats apart; q is normed and rotated in place, k
-// (normed, rotated) and v go to cell pos[r] of sequence seq[r] as fp16. theta_scale = base^(-2/128) (computed by the
-// caller in fp32, as ggml does); theta_i = pos * theta_scale^i by i successive fp32 multiplies.
+// (normed, rotated) and v go to cell pos[r] of sequence seq[r] as fp16, in the pools' layout (snk_attn_run's).
+// theta_scale = base^(-2/128) (computed by the caller in fp32, as ggml does); theta_i = pos * theta_scale^i by i
+// successive fp32 multiplies.
 int snk_qk_rope(float* d_qkv, int ldqkv, int R, int H, int KVH, const float* d_qw, const float* d_kw, float eps,
                 float theta_scale, const int32_t* d_seq, const int32_t* d_pos, const int32_t* d_pt, int max_pages,
                 int page_cells, void* d_kpool, void* d_vpool, void* stream);

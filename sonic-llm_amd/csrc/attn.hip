@@ -86,11 +86,13 @@ __device__ __forceinline__ AttnRsrc attn_rsrc(const AttnArgs& a, int kvh, int p_
 template <int CPOL = 2>  // the loads' cache policy: nt (cells read once a step), 0 for run items (cells read again)
 __device__ __forceinline__ void attn_issue_k(const AttnArgs& a, const AttnRsrc& r, int cbase, int pos_last, int n,
                                              int g, u32x4 (&kf)[4][4]) {
+    // (dims 32 t + 8 g .. +7 are chunk 4 t + g of the cell: 16 g pc bytes into the region for the lane, 64 t pc for
+    // the instruction)
     const int pc = a.page_cells;  // 32 or 64
     for (int jg = 0; jg < 4; ++jg) {
         const int c = cbase + 16 * jg + n;
-        const int off = c <= pos_last ? (c & (pc - 1)) * (ATT_D * 2) + 16 * g : ATT_OOB;
-        for (int t = 0; t < 4; ++t) kf[jg][t] = bload16nt<CPOL>(jg < 2 ? r.k0 : r.k1, off, 64 * t);
+        const int off = c <= pos_last ? (c & (pc - 1)) * 16 + 16 * pc * g : ATT_OOB;
+        for (int t = 0; t < 4; ++t) kf[jg][t] = bload16nt<CPOL>(jg < 2 ? r.k0 : r.k1, off, 64 * pc * t);
     }
 }
 template <int CPOL = 2>

@@ -550,7 +550,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     hipFree(tmp);
     if (!ok) return fail(why.empty() ? std::string() : why);
 
-    // ---- the KV pool: per layer, K then V, pages of [KVH][page_cells][128] fp16, zeroed
+    // ---- the KV pool: per layer, K then V, pages of [KVH][page_cells][128] fp16 (K regions chunk-major: kcell_at), zeroed
     e->layer_halves = (size_t) e->n_pages * e->KVH * e->page_cells * e->D;
     e->kbase = e->dalloc<uint16_t>(e->layer_halves * 2 * e->CL * sizeof(uint16_t), err, err_len);
     if (!e->kbase) return fail("");

@@ -100,9 +100,9 @@ __global__ __launch_bounds__(256) void k_qk_rope(float* __restrict__ qkv, int ld
         x[lane] = y0;
         x[lane + 64] = y1;
     } else {
-        uint16_t* kc = kpool + (((size_t) page * KVH + (h - H)) * page_cells + off) * 128;
-        kc[lane] = __builtin_bit_cast(uint16_t, (_Float16) y0);
-        kc[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16) y1);
+        uint16_t* kc = kpool + ((size_t) page * KVH + (h - H)) * page_cells * 128;
+        kc[kcell_at(page_cells, off, lane)] = __builtin_bit_cast(uint16_t, (_Float16) y0);
+        kc[kcell_at(page_cells, off, lane + 64)] = __builtin_bit_cast(uint16_t, (_Float16) y1);
     }
 }
 
@@ -345,12 +345,15 @@ int argmax_rows(const float* logits, int V, int n, const int32_t* ban, int nban,
 // ---- page operations of the cache (sn_copy / sn_clear / freed pages; sn_seq.inc.h:5-145) ----------------------------
 __global__ void k_kv_page_op(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int KVH, int page_cells, int src,
                              int dst, int a, int b) {
-    const int l = blockIdx.x, t = blockIdx.y, h = blockIdx.z;
+    const int l = blockIdx.x, t = blockIdx.y, h = blockIdx.z;  // (cells a .. b - 1 of the page)
     uint16_t* pool = (t == 0 ? kbase : vbase) + (size_t) l * layer_halves;
-    uint16_t* d = pool + (((size_t) dst * KVH + h) * page_cells + a) * 128;
-    const uint16_t* s = src >= 0 ? pool + (((size_t) src * KVH + h) * page_cells + a) * 128 : nullptr;
+    uint16_t* d = pool + ((size_t) dst * KVH + h) * page_cells * 128;
+    const uint16_t* s = src >= 0 ? pool + ((size_t) src * KVH + h) * page_cells * 128 : nullptr;
     const int n = (b - a) * 128;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) d[i] = s ? s[i] : (uint16_t) 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const size_t at = t == 0 ? kcell_at(page_cells, a + i / 128, i % 128) : (size_t) a * 128 + i;
+        d[at] = s ? s[at] : (uint16_t) 0;
+    }
 }
 
 void kv_page_op(uint16_t* kbase, uint16_t* vbase, size_t layer_halves, int L, int KVH, int page_cells, int src, int dst,
@@ -370,7 +373,8 @@ __global__ void k_kv_stage(uint16_t* kbase, uint16_t* vbase, size_t layer_halves
     uint16_t* stg = staging + (((size_t) l * 2 + t) * n + c) * (size_t) KVH * 128;
     for (int i = threadIdx.x; i < KVH * 128; i += blockDim.x) {
         const int h = i / 128, d = i % 128;
-        uint16_t* cell = pool + (((size_t) p * KVH + h) * page_cells + c % page_cells) * 128 + d;
+        const size_t in = t == 0 ? kcell_at(page_cells, c % page_cells, d) : (size_t) (c % page_cells) * 128 + d;
+        uint16_t* cell = pool + ((size_t) p * KVH + h) * page_cells * 128 + in;
         if (save) stg[i] = *cell;
         else *cell = stg[i];
     }
@@ -402,7 +406,8 @@ __global__ void k_kv_fill(uint16_t* kbase, uint16_t* vbase, size_t layer_halves,
         const uint64_t a = mix64(key), b = mix64(key ^ 0x9E3779B97F4A7C15ull);
         const float u1 = ((a >> 40) + 1) * 0x1.0p-24f, u2 = (b >> 40) * 0x1.0p-24f;
         const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.2831853f * u2);
-        pool[(((size_t) p * KVH + h) * page_cells + c % page_cells) * 128 + d] = __builtin_bit_cast(uint16_t, (_Float16) z);
+        const size_t in = t == 0 ? kcell_at(page_cells, c % page_cells, d) : (size_t) (c % page_cells) * 128 + d;
+        pool[((size_t) p * KVH + h) * page_cells * 128 + in] = __builtin_bit_cast(uint16_t, (_Float16) z);
     }
 }
 
@@ -547,9 +552,9 @@ __global__ void k_cut_cells(uint16_t* __restrict__ kbase, uint16_t* __restrict__
     const size_t base = (size_t) layer * layer_halves;
     for (int t = threadIdx.x; t < KVH * 128; t += 256) {
         const int h = t / 128, d = t % 128;
-        const size_t at = base + (((size_t) page * KVH + h) * page_cells + c % page_cells) * 128 + d;
-        kbase[at] = 0;
-        vbase[at] = 0;
+        const size_t reg = base + ((size_t) page * KVH + h) * page_cells * 128;
+        kbase[reg + kcell_at(page_cells, c % page_cells, d)] = 0;
+        vbase[reg + (size_t) (c % page_cells) * 128 + d] = 0;
     }
 }
 

@@ -14,6 +14,15 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 #define SN_WAVE 64
 
+// ---- the KV cache: per layer, K and V pools of pages; page p of KV head h is the region of page_cells cells at
+// pool + (p * KVH + h) * page_cells * 128 halves. A V cell is 128 contiguous fp16 (cell * 128 + d). A K region holds its
+// cells' dims in 16-byte chunks of 8, chunk-major: chunk j of every cell, then chunk j + 1, so chunk j of 16
+// consecutive cells is 256 contiguous bytes, the span a quarter-wavefront of an attention score load reads (a K cell
+// stored whole, that quarter-wavefront touched 16 cells 16 bytes each: the decode step's attention 8% slower).
+__host__ __device__ __forceinline__ size_t kcell_at(int page_cells, int cell, int d) {
+    return ((size_t) (d >> 3) * page_cells + cell) * 8 + (d & 7);
+}
+
 // ---- raw buffer loads: a per-lane byte offset and a wavefront-uniform one against a resource of `bytes`; a load
 // reaching past `bytes` returns zeros and touches no memory
 #define RSRC_WORD3 0x00020000  // raw buffer resource, gfx9 data format

@@ -185,7 +185,7 @@ struct AttnItem {
 struct AttnArgs {
     const float* q;          // [rows][H][D] fp32 (normed, roped; the softmax scale is applied inside)
     int ldq;                 // floats between rows of q
-    const uint16_t* kpool;   // fp16 cells: page p, kv head h: kpool + ((p * KVH + h) * page_cells) * D
+    const uint16_t* kpool;   // fp16 cells: page p, kv head h: kpool + ((p * KVH + h) * page_cells) * D (kcell_at)
     const uint16_t* vpool;
     const int32_t* pt;       // [n_seq][max_pages] page table
     int max_pages;

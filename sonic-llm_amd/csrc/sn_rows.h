@@ -39,9 +39,9 @@ __device__ __forceinline__ void qk_head(float* __restrict__ x, int lane, int h, 
         x[lane] = y0;
         x[lane + 64] = y1;
     } else {
-        uint16_t* kc = kpool + (((size_t) page * KVH + (h - H)) * page_cells + off) * 128;
-        kc[lane] = __builtin_bit_cast(uint16_t, (_Float16) y0);
-        kc[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16) y1);
+        uint16_t* kc = kpool + ((size_t) page * KVH + (h - H)) * page_cells * 128;
+        kc[kcell_at(page_cells, off, lane)] = __builtin_bit_cast(uint16_t, (_Float16) y0);
+        kc[kcell_at(page_cells, off, lane + 64)] = __builtin_bit_cast(uint16_t, (_Float16) y1);
     }
 }
 

@@ -17,6 +17,20 @@ def dev(a: np.ndarray):
     return t
 
 
+def k_pages(kpool: np.ndarray) -> np.ndarray:
+    """A K pool given cell-major, [pages][KVH][cells][128] fp16 (the reference's layout, the oracle's input), in the
+    library's layout: each (page, KV head) region holds its cells' dims in 16-byte chunks of 8, chunk-major
+    ([16][cells][8]), so that chunk j of consecutive cells is contiguous."""
+    P, KVH, pc, D = kpool.shape
+    return np.ascontiguousarray(kpool.reshape(P, KVH, pc, D // 8, 8).transpose(0, 1, 3, 2, 4)).reshape(P, KVH, pc, D)
+
+
+def k_cells(kdev: np.ndarray) -> np.ndarray:
+    """The inverse of k_pages: a K pool read back from the library, cell-major."""
+    P, KVH, pc, D = kdev.shape
+    return np.ascontiguousarray(kdev.reshape(P, KVH, D // 8, pc, 8).transpose(0, 1, 3, 2, 4)).reshape(P, KVH, pc, D)
+
+
 def empty(nbytes: int):
     T = torch()
     return T.zeros(max(int(nbytes), 256), dtype=T.uint8, device="cuda")

@@ -76,7 +76,7 @@ def attn_gpu(q, seq, pos, kpool, vpool, pt, page, scale, bufs=None, whole=None, 
     if runs is not None:
         assert L.snk_attn_runs(plan) == runs, (L.snk_attn_runs(plan), runs)
     if bufs is None:
-        bufs = (U.dev(kpool), U.dev(vpool), U.dev(pt))
+        bufs = (U.dev(U.k_pages(kpool)), U.dev(vpool), U.dev(pt))
     if fold is not None:
         assert L.snk_attn_fold(plan, int(fold)) == int(fold)
     dq = U.dev(q)
@@ -111,7 +111,7 @@ def test_shared_prefix_read_once(kvh, n_share):
     item; and it matches the oracle."""
     q, seq, pos, kp, vp, pt, page = config2_case(n_share=n_share, kvh=kvh)
     scale = 1 / math.sqrt(D)
-    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    bufs = (U.dev(U.k_pages(kp)), U.dev(vp), U.dev(pt))
     a = attn_gpu(q, seq, pos, kp, vp, pt, page, scale, bufs=bufs, mode=0)
     b = attn_gpu(q, seq, pos, kp, vp, pt, page, scale, bufs=bufs, mode=0, share=True)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
@@ -154,7 +154,7 @@ def test_verify_rows_equal_single_rows_bitwise():
     rows_pos = (np.repeat(p0, 4) + np.tile(np.arange(4), len(seq))).astype(np.int32)
     r = np.random.default_rng(8)
     qv = r.standard_normal((len(rows_seq), H, D), dtype=np.float32)
-    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    bufs = (U.dev(U.k_pages(kp)), U.dev(vp), U.dev(pt))
     grouped = attn_gpu(qv, rows_seq, rows_pos, kp, vp, pt, page, scale, bufs)
     for i in range(len(rows_seq)):
         one = attn_gpu(qv[i:i + 1].copy(), rows_seq[i:i + 1].copy(), rows_pos[i:i + 1].copy(), kp, vp, pt, page,
@@ -188,7 +188,7 @@ def test_whole_group_list_equals_chunk_list_bitwise(page, lo, hi, auto):
     for these 32 x 8 workgroups exactly when the contexts are long and alike (auto)."""
     q, seq, pos, kp, vp, pt, pg = config2_case(seed=11 + lo, S_=32, page=page, lo=lo, hi=hi, n_share=0)
     scale = 1 / math.sqrt(D)
-    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    bufs = (U.dev(U.k_pages(kp)), U.dev(vp), U.dev(pt))
     whole = attn_gpu(q, seq, pos, kp, vp, pt, pg, scale, bufs, mode=1)
     split = attn_gpu(q, seq, pos, kp, vp, pt, pg, scale, bufs, mode=0)
     assert np.array_equal(whole.view(np.uint32), split.view(np.uint32))
@@ -210,7 +210,7 @@ def test_gqa_group_sizes(kvh):
     q, seq, pos, kp, vp, pt, page = config2_case(seed=31 + kvh, S_=32, page=64, lo=1500, hi=2600, n_share=4,
                                                  kvh=kvh)
     scale = 1 / math.sqrt(D)
-    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    bufs = (U.dev(U.k_pages(kp)), U.dev(vp), U.dev(pt))
     got = attn_gpu(q, seq, pos, kp, vp, pt, page, scale, bufs)
     ref = O.paged_attn(q, seq, pos, kvh, kp, vp, page, pt, scale)
     err = np.abs(got - ref)
@@ -251,7 +251,7 @@ def test_prompt_runs_equal_chunk_items_bitwise(kvh, page):
     r = np.random.default_rng(kvh * page)
     qr = r.standard_normal((len(rseq), H, D), dtype=np.float32)
     scale = 1 / math.sqrt(D)
-    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    bufs = (U.dev(U.k_pages(kp)), U.dev(vp), U.dev(pt))
     # run items of up to 4 groups: 64 rows in groups of 16 / G rows; 41 rows in 10 (G = 4) or 20 (G = 8) full groups
     # and a short last one, which joins the run; the 6 rows from position 0 in 2 (G = 4) or 3 groups; the decode row
     # stays a group of its own
@@ -279,7 +279,7 @@ def test_prompt_runs_chosen_for_prompt_steps():
     rpos = np.arange(1536, 2048, dtype=np.int32)
     qr = np.random.default_rng(51).standard_normal((512, H, D), dtype=np.float32)
     scale = 1 / math.sqrt(D)
-    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    bufs = (U.dev(U.k_pages(kp)), U.dev(vp), U.dev(pt))
     auto = attn_gpu(qr, rseq, rpos, kp, vp, pt, pg, scale, bufs, runs=32)
     chunks = attn_gpu(qr, rseq, rpos, kp, vp, pt, pg, scale, bufs, mode=0, runs=0)
     assert np.array_equal(auto.view(np.uint32), chunks.view(np.uint32))
@@ -302,7 +302,7 @@ def test_fold_equals_two_launches_bitwise(kvh, page, lo, hi, verify):
         pos = (np.repeat(np.maximum(pos[:8], 3) - 3, 4) + np.tile(np.arange(4), 8)).astype(np.int32)
         q = np.random.default_rng(kvh + 1).standard_normal((32, H, D), dtype=np.float32)
     scale = 1 / math.sqrt(D)
-    bufs = (U.dev(kp), U.dev(vp), U.dev(pt))
+    bufs = (U.dev(U.k_pages(kp)), U.dev(vp), U.dev(pt))
     one = attn_gpu(q, seq, pos, kp, vp, pt, pg, scale, bufs, mode=0, fold=True)
     two = attn_gpu(q, seq, pos, kp, vp, pt, pg, scale, bufs, mode=0, fold=False)
     assert np.array_equal(one.view(np.uint32), two.view(np.uint32))

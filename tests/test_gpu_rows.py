@@ -46,7 +46,7 @@ def _qk_rope_run(qkv, seq, pos, pt, page, qw, kw, eps, ts, H, KVH, D=128):
                          U.ptr(U.dev(seq)), U.ptr(U.dev(pos)), U.ptr(U.dev(pt)), pt.shape[1], page, U.ptr(kp),
                          U.ptr(vp), U.stream()) == 0
     q_out = U.host(d_qkv, np.float32)[:qkv.size].reshape(qkv.shape)
-    kpool = U.host(kp, np.uint16)[:npg * KVH * page * D].reshape(npg, KVH, page, D)
+    kpool = U.k_cells(U.host(kp, np.uint16)[:npg * KVH * page * D].reshape(npg, KVH, page, D))
     vpool = U.host(vp, np.uint16)[:npg * KVH * page * D].reshape(npg, KVH, page, D)
     return q_out, kpool, vpool
 
