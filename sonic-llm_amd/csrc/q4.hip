@@ -9,7 +9,8 @@
 // v_mfma_f32_16x16x32_f16 multiplies exactly and accumulates in fp32 with a per-row integer correction as its C input;
 // every partial sum is an integer below 2^23, so the MFMA gives ggml's integer block sum isum = sum q (w - 8) exactly.
 // One fma per output then adds isum * (dw * dx) (the product of two fp16 values is exact in fp32) to the fp32
-// accumulator. The order of the sums of an output is fixed by (N, K) alone, never by the number of rows, so a row's
+// accumulator; the products dw * dx come from a 4 x 4 x 4 fp16 MFMA as well (scale_products), exactly as the VALU
+// would form them. The order of the sums of an output is fixed by (N, K) alone, never by the number of rows, so a row's
 // result is the same in any step (sn.h:1-3).
 #include <stdarg.h>
 
@@ -363,6 +364,24 @@ __device__ __forceinline__ half8 q8_unpack(uint32_t w_lo, uint32_t w_hi) {
     return __builtin_bit_cast(half8, (u32x4){p0, p1, p2, p3});
 }
 
+// The scale products dw * dx of a block on the matrix core, by v_mfma_f32_4x4x4_16b_f16: 16 independent 4 x 4 x 4
+// products, lane l holding row l % 4 of block l / 4's A (4 k values), column l % 4 of its B (4 k values) and column
+// l % 4 of its D (4 rows). For lane (n, g) that block is (g, n / 4): A = the one-hot dx of row 4 g + n % 4 of the row
+// tile (dx_b in k slot b, zeros in the other 3; dx an fp16 value, exact in fp32), B = the 4 blocks' fp16 scales dw of
+// stripe row n (the tile's scale word as loaded), so D = dx_b[4 g + v] * dw_b[n] for v = 0..3: the rows and column
+// of the block's sums in the 16 x 16 MFMA's layout. Each result is one product of two fp16 values (exact in fp32)
+// plus 3 terms 0 * dw (zero for finite scales), so it is the value the VALU would form, for 4 VALU multiplies less a
+// (block, stripe, row tile).
+__device__ __forceinline__ half4v scale_a(float dx, int b) {
+    const uint32_t h = __builtin_bit_cast(uint32_t, b & 1 ? __builtin_amdgcn_cvt_pkrtz(0.0f, dx)
+                                                          : __builtin_amdgcn_cvt_pkrtz(dx, 0.0f));
+    return __builtin_bit_cast(half4v, b < 2 ? (u32x2){h, 0u} : (u32x2){0u, h});
+}
+__device__ __forceinline__ floatx4 scale_products(half4v a, u32x2 ws) {
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(a, __builtin_bit_cast(half4v, ws), (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0,
+                                              0);
+}
+
 // One workgroup (4 wavefronts) owns a set of 4 S consecutive 16-row stripes (wavefront w: stripes S w .. S w + S - 1 of
 // the set; S = 2, or 1 for narrow matrices), MT row tiles and a k-slice of consecutive 4-block groups, which the 4 wavefronts walk together. Per group:
 //   - the activation records of the MT row tiles (MT x 4 KB of fragments, MT x 512 B of scales and corrections) are
@@ -414,6 +433,8 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
     // one resource for the whole matrix, the wavefront's stripes by scalar offsets (stripes past the matrix read as
     // zeros: the range check covers the scalar offset too)
     const __amdgpu_buffer_rsrc_t wr = buf_rsrc(wbase, (uint32_t) (a.nstripes * sbytes));
+    // the scales (B of scale_products): a group past the slice (the ring's padding) reads zeros, so it adds nothing
+    const int ws_off = SO + 8 * n_in;
     const int rstride = a.ngroups * XA_REC;  // between row tiles' records
     // the activation: the operand's records from row tile mt0 on; or, gathering (a.gsrc, one row tile), each lane's row
     // m = lane % 16 of the tile taken from row gsrc[16 mt0 + m] of a row-ordered operand of a.gM rows (a padding row,
@@ -459,29 +480,30 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
         for (int s = 0; s < S; ++s) {
             const int so = (s0 + s) * sbytes + c * TB;
             for (int h = 0; h < NW; ++h) wq[slot][s][h] = bload16(wr, 16 * NW * lane + 16 * h, so);
-            ws[slot][s] = bload8(wr, SO + 8 * n_in, so);
+            ws[slot][s] = bload8(wr, ws_off, i < ng ? so : (int) XA_GATHER_OOB);
         }
     };
     auto stage = [&](int buf, const u32x4 (&r)[FPW], float k) {
         for (int j = 0; j < FPW; ++j) *(u32x4*) &s_act[buf][wave * FPW + j][16 * lane] = r[j];
         if (wave < 2 * MT) s_k[buf][kb / 2][kb % 2][lane] = k;
     };
-    auto compute = [&](int slot, int buf, float m) {
+    auto compute = [&](int slot, int buf) {
         for (int b = 0; b < 4; ++b) {
             half8 A[MT];
-            floatx4 dx[MT], cr[MT];
+            half4v da[MT];
+            floatx4 cr[MT];
             for (int mt = 0; mt < MT; ++mt) {
                 A[mt] = *(const half8*) &s_act[buf][mt * 4 + b][16 * lane];
-                dx[mt] = *(const floatx4*) &s_k[buf][mt][0][b * 16 + 4 * g];
+                da[mt] = scale_a(s_k[buf][mt][0][b * 16 + 4 * g + (n_in & 3)], b);
                 cr[mt] = *(const floatx4*) &s_k[buf][mt][1][b * 16 + 4 * g];
             }
             for (int s = 0; s < S; ++s) {
                 const half8 bw = Q8 ? q8_unpack(wq[slot][s][b / 2][2 * (b % 2)], wq[slot][s][b / 2][2 * (b % 2) + 1])
                                     : q4_unpack(wq[slot][s][0][b]);
-                const float dw = (float) __builtin_bit_cast(half4v, ws[slot][s])[b] * m;
                 for (int mt = 0; mt < MT; ++mt) {
                     const floatx4 isum = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], bw, cr[mt], 0, 0, 0);
-                    for (int v = 0; v < 4; ++v) acc[s][mt][v] = __builtin_fmaf(isum[v], dw * dx[mt][v], acc[s][mt][v]);
+                    const floatx4 sc = scale_products(da[mt], ws[slot][s]);
+                    for (int v = 0; v < 4; ++v) acc[s][mt][v] = __builtin_fmaf(isum[v], sc[v], acc[s][mt][v]);
                 }
             }
         }
@@ -508,7 +530,7 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
             __syncthreads();  // group i is staged in buffer j; everyone is done reading buffer j ^ 1
             stage(j ^ 1, ra[j], rk[j]);  // group i + 1's records (loaded with group i's weights, slot i % D)
             __builtin_amdgcn_sched_barrier(0);
-            compute(j, j, i < ng ? 1.0f : 0.0f);
+            compute(j, j);
             // the group's sums are complete here: left to the compiler, they sank below the next loads, which then
             // could not reuse the slot's scale registers, and the copy back at the loop's end waited on those loads
             for (int s = 0; s < S; ++s)
@@ -712,6 +734,7 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     const int sbytes = a.ngroups * TB;
     // one resource for the whole matrix (see q4_gemm_ring)
     const __amdgpu_buffer_rsrc_t wr = buf_rsrc(wbase, (uint32_t) (a.nstripes * sbytes));
+    const int ws_off = SO + 8 * n_in;  // (as in q4_gemm_ring)
     const int rstride = a.ngroups * XA_REC;
     // the activation: the operand's records from row tile mt0 on; or, gathering (a.gsrc, one row tile), lane l's row
     // m = l % 16 of the tile taken from row gsrc[16 mt0 + m] of a row-ordered operand of a.gM rows (a padding row,
@@ -749,7 +772,7 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
         for (int t = 0; t < S; ++t) {
             const int so = (s0 + t) * sbytes + c * TB;
             for (int h = 0; h < NW; ++h) wq[slot][t][h] = bload16(wr, 16 * NW * lane + 16 * h, so);
-            ws[slot][t] = bload8(wr, SO + 8 * n_in, so);
+            ws[slot][t] = bload8(wr, ws_off, i < ng ? so : (int) XA_GATHER_OOB);
         }
     };
     for (int j = 0; j < D; ++j) {
@@ -769,28 +792,28 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     for (int tr = 0; tr < trips; ++tr)
         for (int j = 0; j < D; ++j) {
             const int i = tr * D + j;
-            const float m = i < ng ? 1.0f : 0.0f;
-            const int li = min(i, ng - 1);  // (its LDS group)
+            const int li = min(i, ng - 1);  // (its LDS group; a group past the slice has zero scales)
             __builtin_amdgcn_sched_barrier(0);
             // block b's MFMAs are issued before block b - 1's scale FMAs (the same FMAs in the same order per output,
             // so the same sums), so a block's matrix-core latency is spent on the previous block's VALU work
-            floatx4 is[2][S][MT], dxs[2][MT];
-            float dws[2][S];
+            floatx4 is[2][S][MT], sc[2][S][MT];
             for (int b = 0; b < 5; ++b) {
                 if (b < 4) {
                     half8 A[MT];
+                    half4v da[MT];
                     floatx4 cr[MT];
                     for (int mt = 0; mt < MT; ++mt) {
                         A[mt] = *(const half8*) &s_act[(li * MT + mt) * 4 + b][16 * lane];
-                        dxs[b & 1][mt] = *(const floatx4*) &s_k[li][mt][0][b * 16 + 4 * g];
+                        da[mt] = scale_a(s_k[li][mt][0][b * 16 + 4 * g + (n_in & 3)], b);
                         cr[mt] = *(const floatx4*) &s_k[li][mt][1][b * 16 + 4 * g];
                     }
                     for (int t = 0; t < S; ++t) {
                         const half8 bw = Q8 ? q8_unpack(wq[j][t][b / 2][2 * (b % 2)], wq[j][t][b / 2][2 * (b % 2) + 1])
                                             : q4_unpack(wq[j][t][0][b]);
-                        dws[b & 1][t] = (float) __builtin_bit_cast(half4v, ws[j][t])[b] * m;
-                        for (int mt = 0; mt < MT; ++mt)
+                        for (int mt = 0; mt < MT; ++mt) {
                             is[b & 1][t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], bw, cr[mt], 0, 0, 0);
+                            sc[b & 1][t][mt] = scale_products(da[mt], ws[j][t]);
+                        }
                     }
                 }
                 if (b > 0) {
@@ -798,7 +821,7 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
                     for (int t = 0; t < S; ++t)
                         for (int mt = 0; mt < MT; ++mt)
                             for (int v = 0; v < 4; ++v)
-                                acc[t][mt][v] = __builtin_fmaf(is[pb][t][mt][v], dws[pb][t] * dxs[pb][mt][v], acc[t][mt][v]);
+                                acc[t][mt][v] = __builtin_fmaf(is[pb][t][mt][v], sc[pb][t][mt][v], acc[t][mt][v]);
                 }
             }
             // the group's sums are complete here (left to the compiler, they sank below the next loads)

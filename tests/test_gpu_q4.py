@@ -278,3 +278,43 @@ def test_gemv_equals_mfma_bitwise(M, N, K):
         out.append(U.host(y, np.float32)[:M * N].reshape(M, N))
     assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
     assert np.count_nonzero(out[1]) > M * N // 2
+
+
+@pytest.mark.parametrize("N,K", [(19456, 2560), (2560, 9728), (98304, 2560)])
+def test_subnormal_scales_gemv_equals_mfma(N, K):
+    """Blocks whose fp16 scales are subnormal: weight rows scaled by 1e-4 (d about 1e-6) and activation rows scaled by
+    1e-5 (dx about 2e-7), so every kind of product dw * dx (normal x subnormal, subnormal x subnormal) occurs. The MFMA
+    kernels form those products on the matrix core (an fp16 MFMA of the two scales, exact only if it keeps subnormal
+    inputs); the GEMV forms them on the VALU in fp32. Both must give the same slice sums, bit for bit, and the tiny
+    rows must not be flushed to zero. Shapes: gate|up and down (streaming kernel) and the LM head's plan (ring)."""
+    L = S.lib()
+    st = U.stream()
+    M = 4
+    r = np.random.default_rng(500 + N)
+    nb = min(N, 4096)
+    W = r.normal(0, 0.02, (nb, K)).astype(np.float32)
+    W[::3] *= np.float32(1e-4)
+    Wq = O.quantize_q4_0(W)
+    d = Wq.reshape(nb, K // 32, 18)[:, :, :2].copy().view(np.float16)
+    assert np.any((d != 0) & (np.abs(d.astype(np.float32)) < 6.1e-5))  # subnormal weight scales are present
+    Wq = np.ascontiguousarray(np.tile(Wq, ((N + nb - 1) // nb, 1))[:N])
+    wbuf = U.empty(L.snk_q4_stripes_bytes(N, K))
+    assert L.snk_q4_repack(U.ptr(U.dev(Wq)), N, K, U.ptr(wbuf), st) == 0
+    X = r.normal(0, 1, (M, K)).astype(np.float32)
+    X[1::2] *= np.float32(1e-5)
+    xd = O.quantize_q8_0(X).reshape(M, K // 32, 34)[:, :, :2].copy().view(np.float16)
+    assert np.all(np.abs(xd[1::2].astype(np.float32)) < 6.1e-5)  # the tiny rows' scales are subnormal
+    xa = U.empty(L.snk_xa_bytes(M, K))
+    assert L.snk_quant_act(U.ptr(U.dev(X)), M, K, K, None, 0.0, U.ptr(xa), st) == 0
+    wsb = L.snk_q4_workspace_bytes(M, N, K)
+    out = []
+    for mt in (1, 0):
+        y, ws = U.empty(M * N * 4), U.empty(wsb)
+        assert L.snk_q4_gemm_plan_sums(U.ptr(wbuf), U.ptr(xa), M, N, K, U.ptr(y), U.ptr(ws), wsb, mt, mt, 0, st) == 0
+        out.append(U.host(y, np.float32)[:M * N].reshape(M, N))
+    assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
+    assert np.count_nonzero(out[0][1]) > N // 2 and np.count_nonzero(out[0][3]) > N // 2
+    ref = O.mul_mat_q4_0(Wq[:nb], K, X)
+    tiny = np.abs(ref[1]).max()
+    assert 0 < tiny < 1e-3 * np.abs(ref[0]).max()
+    assert np.all(np.abs(out[0][1, :nb] - ref[1]) <= 1e-3 * np.abs(ref[1]) + 1e-6 * tiny)
