@@ -39,7 +39,7 @@ __global__ void k_q4_repack(const uint8_t* __restrict__ src, int N, int K, uint8
         const int blk = grp * 4 + b;
         const bool ok = row < N && blk < nb;
         const uint8_t* s = src + ((size_t) row * nb + blk) * 18;
-        for (int j = 0; j < 4; ++j) q[4 * b + j] = ok ? s[2 + 4 * g + j] : 0;
+        for (int j = 0; j < 4; ++j) q[4 * b + j] = ok ? s[2 + 4 * g + (j == 1 ? 2 : j == 2 ? 1 : j)] : 0;
         d[b] = ok ? (uint16_t) (s[0] | (s[1] << 8)) : 0;
     }
     for (int j = 0; j < 16; ++j) t[16 * l + j] = q[j];
@@ -340,16 +340,24 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ 
 // ---------------------------------------------------------------------------------------------------------------------
 // the matmul
 
-// A weight lane's 4 bytes (one block: byte j holds element j in its low nibble, j + 16 in its high nibble) as the MFMA
-// operand in the lane order of the activation fragments: fp16 (1024 + w) for elements 4g..4g+3 and (1024 + 16 w) for
-// 16+4g..16+4g+3, built by two masks and four byte permutes (0x64 is the high byte of fp16 1024).
+// A weight lane's 4 bytes of one block (elements e = 4g + i, i = 0..3: byte 0 holds i = 0, byte 1 i = 2, byte 2 i = 1,
+// byte 3 i = 3, each with element e in its low nibble and e + 16 in its high nibble) as the MFMA operand in the lane
+// order of the activation fragments: fp16 (1024 + w) for elements 4g..4g+3 and (1024 + 16 w) for 16+4g..16+4g+3
+// (0x64 is the high byte of fp16 1024). Bytes 0 and 2 give elements i = 0, 1 by a mask and an OR each (v_and_or_b32),
+// bytes 1 and 3 give i = 2, 3 by a byte permute that places them under 0x64 and a mask each: 5 instructions.
+// (written as v_and_or_b32 with the mask in a scalar register and 0x64006400 in a vector one: left to the compiler, the
+// two literals became a v_and_b32 and a v_or_b32, since a VOP3 instruction here takes no literal)
+__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask, uint32_t k) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(mask), "v"(k));
+    return r;
+}
 __device__ __forceinline__ half8 q4_unpack(uint32_t w) {
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;
-    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u);
-    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u);
-    const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u);
-    const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u);
-    return __builtin_bit_cast(half8, (u32x4){p0, p1, p2, p3});
+    const uint32_t p01 = and_or(w, 0x000F000Fu, 0x64006400u);  // elements 0, 1
+    const uint32_t p45 = and_or(w, 0x00F000F0u, 0x64006400u);  // elements 16, 17 (x 16)
+    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u);  // bytes 1, 3 under 0x64
+    const uint32_t p23 = h & 0xFF0FFF0Fu, p67 = h & 0xFFF0FFF0u;
+    return __builtin_bit_cast(half8, (u32x4){p01, p23, p45, p67});
 }
 
 // A Q8_0 weight lane's 8 bytes of one block (int8 q of elements 4g..4g+3 in w_lo, of 16+4g..16+4g+3 in w_hi) as the
@@ -1004,9 +1012,10 @@ __global__ __launch_bounds__(256) void k_q4_gemv(GemmArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             for (int b = 0; b < 4; ++b) {
                 uint32_t wl[4], wh[4];
-                for (int g = 0; g < 4; ++g) {
-                    wl[g] = wq[j][g][b] & 0x0F0F0F0Fu;
-                    wh[g] = (wq[j][g][b] >> 4) & 0x0F0F0F0Fu;
+                for (int g = 0; g < 4; ++g) {  // (the tile's bytes 1 and 2 back in element order)
+                    const uint32_t w = __builtin_amdgcn_perm(wq[j][g][b], wq[j][g][b], 0x03010200u);
+                    wl[g] = w & 0x0F0F0F0Fu;
+                    wh[g] = (w >> 4) & 0x0F0F0F0Fu;
                 }
                 const float dw = (float) __builtin_bit_cast(half4v, ws[j])[b] * msc;
                 for (int m = 0; m < MR; ++m) {

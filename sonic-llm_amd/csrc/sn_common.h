@@ -71,8 +71,9 @@ void sn_set_err(char* err, int err_len, const char* fmt, ...);
 // A GGUF Q4_0 matrix (N rows of K/32 18-byte blocks: fp16 d, 16 nibble bytes) is re-laid at upload into tiles of 16
 // rows x 4 blocks, 1152 bytes each, so that one wavefront reads a tile with one 16-byte load per lane:
 //   bytes [0, 1024): lane l = n + 16 g (n = row in tile, g = 0..3) holds, for blocks b = 0..3 of the tile, the 4 bytes
-//                    qs[4g .. 4g+3] of row n (offset 16 l + 4 b). Byte j's low nibble is element j, its high nibble
-//                    element j + 16, so lane (n, g) holds elements {4g..4g+3} and {16+4g..16+4g+3} of each block.
+//                    qs[4g], qs[4g+2], qs[4g+1], qs[4g+3] of row n (offset 16 l + 4 b: the middle two swapped, so
+//                    that the unpack takes 5 instructions, q4_unpack). GGUF byte qs[j]'s low nibble is element j, its
+//                    high nibble element j + 16, so lane (n, g) holds elements {4g..4g+3} and {16+4g..16+4g+3}.
 //   bytes [1024, 1152): the 16 rows' fp16 scales d, 4 per row (offset 1024 + 8 n + 2 b).
 // Tiles of one 16-row stripe follow each other along K, so a stripe is one contiguous stream of K/128 tiles.
 // Bytes per weight are those of GGUF (18 per 32); only their order changes. Rows are padded to 16 and blocks to 4
