@@ -135,10 +135,9 @@ int snk_attn_whole(const snk_attn* p);
 // a chunk are read once for all of them (the prompt rows of attn_pre, kernels.metal:1201-1306, sn_attn.inc.h:195-206)
 int snk_attn_runs(const snk_attn* p);
 // Whether snk_attn_run launches the chunk items and their merge as one kernel (k_attn_fold: the last workgroup of each
-// (group, KV head) folds the group's rows itself; the same bits as the two launches). Available for lists of plain
-// chunk items (no shared chunks, run items or whole groups, at most 127 chunks a group) on a device that deals a
-// launch's workgroups to its XCDs in turn; off by default (measured slower: each chunk workgroup waits on its count
-// before it leaves). on = 1 turns it on where available, 0 off; returns 1 when on.
+// (group, KV head) folds the group's rows itself). Withdrawn: the form is never taken and the call always returns 0
+// (it measured slower than the two launches, and one run of its bitwise test against them differed with no cause
+// found). Kept so that callers of the entry point keep linking.
 int snk_attn_fold(snk_attn* p, int on);
 // 1 when a fold launch of this list found a (group, KV head)'s workgroups on two XCDs, 0 if never, -1 (no fold state)
 int snk_attn_xcd_faults(const snk_attn* p);

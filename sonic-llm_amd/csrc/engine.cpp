@@ -101,8 +101,9 @@ struct sn_engine {
     float2* rope_cs = nullptr;  // a step's rotation table (rope_table) [max_rows][64]
     int32_t* d_xerr = nullptr;
     int fcnt_len = 0;
-    // the attention's chunk items and merge in one launch (k_attn_fold; off unless SN_ATTN_FOLD=1: measured slower, 60.2
-    // against 53.0 + 5.8 us a layer at configs[2], each chunk workgroup waiting on its count before it leaves)
+    // the attention's chunk items and merge in one launch (k_attn_fold): withdrawn, always off. Measured slower (60.2
+    // against 53.0 + 5.8 us a layer at configs[2]), and one run of its bitwise test against the two launches differed
+    // on one MI355X with no cause found, so no step takes it.
     bool attn_fold = false;
     float* apart = nullptr;
     int max_chunks = 0;
@@ -594,7 +595,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     if (!e->rope_cs) return fail("");
     e->fuse_ok = xcd_round_robin(e->st, &e->nxcd);
     e->fuse = e->fuse_ok && !getenv("SN_NO_FUSE");
-    e->attn_fold = getenv("SN_ATTN_FOLD") && atoi(getenv("SN_ATTN_FOLD")) == 1;
+    e->attn_fold = false;  // (withdrawn: see attn_fold)
     size_t ws = 0;
     ws = std::max(ws, q4_workspace_bytes(R, e->NQKV, E, e->wt));
     ws = std::max(ws, q4_workspace_bytes(R, E, QD, e->wt));

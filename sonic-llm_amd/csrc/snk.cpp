@@ -337,10 +337,11 @@ extern "C" snk_attn* snk_attn_new_pt(int n_rows, const int32_t* seq, const int32
 }
 
 extern "C" int snk_attn_fold(snk_attn* p, int on) {
-    if (!p) return 0;
-    if (!on) p->fold = false;
-    else p->fold = p->plain && p->d_cnt && p->d_xerr;
-    return p->fold ? 1 : 0;
+    // withdrawn: one run of the fold's bitwise test against the two launches differed on one MI355X (no cause found
+    // by reading the handoff, 45 repeats on another box equal), so the form is never taken and `on` is refused
+    (void) on;
+    if (p) p->fold = false;
+    return 0;
 }
 
 extern "C" int snk_attn_xcd_faults(const snk_attn* p) {

@@ -288,6 +288,9 @@ def test_prompt_runs_chosen_for_prompt_steps():
     assert np.all(np.abs(auto[sel] - ref) <= ATOL + RTOL * np.abs(ref))
 
 
+@pytest.mark.skip(reason="k_attn_fold withdrawn: one run of this test differed (kvh 16, 64-cell pages, contexts "
+                         "300..1200) on one MI355X, 45 repeats on another box were equal and no cause was found by "
+                         "reading the handoff; snk_attn_fold now refuses the form")
 @pytest.mark.parametrize("kvh,page,lo,hi,verify", [(8, 32, 256, 4096, False), (8, 64, 2040, 2100, False),
                                                    (4, 64, 1500, 2600, True), (8, 32, 1, 300, True),
                                                    (16, 64, 300, 1200, False), (2, 64, 500, 900, True)])
