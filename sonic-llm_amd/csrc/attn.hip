@@ -671,9 +671,18 @@ __device__ __forceinline__ void attn_merge_one(const AttnArgs& a, const int r, c
         }
     }
 }
-template <int MB>
+// XA (KV head count a multiple of 8): a 1-D grid whose workgroup L, dealt to XCD L mod 8, takes a (row, head) of a KV
+// head k with k = L (mod 8): k_attn_part's grid (KV head fastest) dealt every item of KV head k to XCD k mod 8, so the
+// merge reads its partials where they were written. Otherwise (row, head) = (blockIdx.x, blockIdx.y).
+template <int MB, bool XA>
 __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
-    attn_merge_one<false, MB>(a, a.mrows[blockIdx.x], blockIdx.y, threadIdx.x);
+    int row = blockIdx.x, h = blockIdx.y;
+    if constexpr (XA) {
+        const int L = blockIdx.x, kx = L & 7, q = L >> 3, hx = a.H >> 3, G = a.H / a.KVH, t = q % hx;
+        row = q / hx;
+        h = ((t / G) * 8 + kx) * G + t % G;
+    }
+    attn_merge_one<false, MB>(a, a.mrows[row], h, threadIdx.x);
 }
 
 // The chunk items and their merge in one launch (plain chunk items: no shared chunks, runs or whole groups). Unit
@@ -751,12 +760,19 @@ int attention_merge(const AttnArgs& a, hipStream_t st) {
     // a row's chunk partials in one round of loads, as few clamped copies as the instances allow (configs[2]'s 9
     // chunks: 10 a round, decode 7,885 -> 7,918 tok/s against 16; configs[1]'s up to 16 chunks: 16)
     const int mc = a.max_chunks;
-    const dim3 grid(a.n_mrows, a.H);
-    if (mc <= 8) hipLaunchKernelGGL(k_attn_merge<8>, grid, dim3(64), 0, st, a);
-    else if (mc <= 10) hipLaunchKernelGGL(k_attn_merge<10>, grid, dim3(64), 0, st, a);
-    else if (mc <= 12) hipLaunchKernelGGL(k_attn_merge<12>, grid, dim3(64), 0, st, a);
-    else if (mc <= 16) hipLaunchKernelGGL(k_attn_merge<16>, grid, dim3(64), 0, st, a);
-    else hipLaunchKernelGGL(k_attn_merge<20>, grid, dim3(64), 0, st, a);
+    const bool xa = a.KVH % 8 == 0;
+    const dim3 grid = xa ? dim3(a.n_mrows * a.H) : dim3(a.n_mrows, a.H);
+#define MERGE(MB_)                                                                               \
+    do {                                                                                         \
+        if (xa) hipLaunchKernelGGL((k_attn_merge<MB_, true>), grid, dim3(64), 0, st, a);         \
+        else hipLaunchKernelGGL((k_attn_merge<MB_, false>), grid, dim3(64), 0, st, a);           \
+    } while (0)
+    if (mc <= 8) MERGE(8);
+    else if (mc <= 10) MERGE(10);
+    else if (mc <= 12) MERGE(12);
+    else if (mc <= 16) MERGE(16);
+    else MERGE(20);
+#undef MERGE
     return 0;
 }
 int paged_attention(const AttnArgs& a, hipStream_t st) {
