@@ -71,6 +71,7 @@ struct GemmPlan {
     int nstripes, ngroups, spw, sets, ks, gps;
     bool stream;    // the streaming kernel serves this matrix below Q4_PAIR_ROWS rows
     int sspw, smt;  // its stripes a wavefront and row tiles a workgroup
+    int sd;         // its ring depth (groups of weights in flight a wavefront)
 };
 
 // Depends on (N, K) only, never on the rows.
