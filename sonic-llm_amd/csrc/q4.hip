@@ -630,8 +630,37 @@ __device__ __forceinline__ float part_load1(__amdgpu_buffer_rsrc_t r, int off) {
 //   FE_ROPE:   the set's 8 stripes are head `set` (128 columns): wavefront w takes rows w, w + 4, ..., lane i the dims
 //              (i, i + 64), and qk_head norms, rotates and writes q to a.qkv, k and v to the row's cell (and k, v as
 //              summed to a.qkv), as k_qk_rope does.
-template <int FE, int MT, int S>
-__device__ __forceinline__ void q4_epilogue(const GemmArgs& a, int set, int mt0) {
+// (FE_ROPE) the epilogue's row data, loaded by every workgroup while its slice streams (the set's last workgroup is
+// known only at the end). Wavefront w of the row tiles mt0 .. mt0 + MT - 1 owns rows mt0 16 + 4 MT w + j, j < 4 MT;
+// lane j holds row j's position and page (lanes past the rows, and rows past M, hold row M - 1's), and cs[j] row j's
+// rotation of this lane. pos and seq are loaded before the activation is staged, the page entry and the rotation
+// after it, so none of them is waited for before the epilogue.
+template <int MT>
+struct RopeRows {
+    int pos, page;
+    float2 cs[4 * MT];
+};
+template <int MT>
+__device__ __forceinline__ void rope_rows_begin(const GemmArgs& a, int mt0, int wave, int lane, RopeRows<MT>& rr) {
+    const int row = min(mt0 * 16 + 4 * MT * wave + min(lane, 4 * MT - 1), a.M - 1);
+    rr.pos = __builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(a.pos, (uint32_t) a.M * 4), row * 4, 0, 0);
+    rr.page = __builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(a.seq, (uint32_t) a.M * 4), row * 4, 0, 0);  // (the slot)
+}
+template <int MT>
+__device__ __forceinline__ void rope_rows_end(const GemmArgs& a, int set, int mt0, int wave, int lane, RopeRows<MT>& rr) {
+    rr.page = __builtin_amdgcn_raw_buffer_load_b32(
+        buf_rsrc(a.pt, 0xfffffff0u), (int) (((size_t) rr.page * a.max_pages + rr.pos / a.page_cells) * 4), 0, 0);
+    if (a.rope_cs && set < a.H + a.KVH) {  // (v heads are not rotated)
+#pragma unroll
+        for (int j = 0; j < 4 * MT; ++j) {
+            const int row = min(mt0 * 16 + 4 * MT * wave + j, a.M - 1);
+            rr.cs[j] = a.rope_cs[(size_t) row * 64 + lane];
+        }
+    }
+}
+
+template <int FE, int MT, int S, class RR>
+__device__ __forceinline__ void q4_epilogue(const GemmArgs& a, int set, int mt0, const RR& rr) {
     const int ks = (int) gridDim.y;
     const __amdgpu_buffer_rsrc_t pr = buf_rsrc(a.part, (uint32_t) ((size_t) ks * a.M * a.N * sizeof(float)));
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -665,45 +694,46 @@ __device__ __forceinline__ void q4_epilogue(const GemmArgs& a, int set, int mt0)
             q8_store(v, g, a.xo, F, row, b);
         }
     } else if constexpr (FE >= FE_ROPE && FE < FE_GSWIGLU) {
-        // RC rows a wavefront at once (4 rows, a 16-row tile in one pass: no faster, 109 against 88 VGPRs)
-        constexpr int RC = 2;
+        // every row of the wavefront (4 MT) in one round of loads: the k-slice sums (the rows' positions, pages and
+        // rotations are already in registers, RopeRows)
+        constexpr int RN = 4 * MT;
         static_assert(S == 2, "a head is the 8 stripes of a set");
         const int h = set, H = a.H, KVH = a.KVH;
         const bool isq = h < H, isv = h >= H + KVH;
         const float* w = isq ? a.qw : a.kw;
         const float w0 = isv ? 0.0f : w[lane], w1 = isv ? 0.0f : w[lane + 64];
-        for (int r0 = wave * RC; r0 < 16 * MT; r0 += 4 * RC) {
-            if (mt0 * 16 + r0 >= a.M) break;
-            float x0[RC][KM], x1[RC][KM];
-            for (int j = 0; j < RC; ++j) {
-                const int row = min(mt0 * 16 + r0 + j, a.M - 1);  // (past M: the last row again, not written)
-                const int off = (row * a.N + h * 128 + lane) * 4;
-                for (int k = 0; k < KM; ++k) {
-                    const int o = off + min(k, ks - 1) * a.M * a.N * 4;
-                    x0[j][k] = part_load1(pr, o);
-                    x1[j][k] = part_load1(pr, o + 256);
+        const int r0 = mt0 * 16 + RN * wave;
+        float x0[RN][KM], x1[RN][KM];
+#pragma unroll
+        for (int j = 0; j < RN; ++j) {
+            const int row = min(r0 + j, a.M - 1);  // (past M: the last row again, not written)
+            const int off = (row * a.N + h * 128 + lane) * 4;
+#pragma unroll
+            for (int k = 0; k < KM; ++k) {
+                const int o = off + min(k, ks - 1) * a.M * a.N * 4;
+                x0[j][k] = part_load1(pr, o);
+                x1[j][k] = part_load1(pr, o + 256);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < RN; ++j) {
+            const int row = r0 + j;
+            float v0 = x0[j][0], v1 = x1[j][0];
+#pragma unroll
+            for (int k = 1; k < KM; ++k)
+                if (k < ks) v0 += x0[j][k], v1 += x1[j][k];
+            const int p = __builtin_amdgcn_readlane(rr.pos, j), page = __builtin_amdgcn_readlane(rr.page, j);
+            float c = 0.0f, sn = 0.0f;
+            if (!isv) {
+                if (a.rope_cs) {
+                    c = rr.cs[j].x, sn = rr.cs[j].y;
+                } else {
+                    rope_cs(p, lane, a.theta_scale, c, sn);
                 }
             }
-            for (int j = 0; j < RC; ++j) {
-                const int row = mt0 * 16 + r0 + j;
-                if (row >= a.M) break;
-                float v0 = x0[j][0], v1 = x1[j][0];
-                for (int k = 1; k < KM; ++k)
-                    if (k < ks) v0 += x0[j][k], v1 += x1[j][k];
-                const int p = a.pos[row];
-                const int page = a.pt[(size_t) a.seq[row] * a.max_pages + p / a.page_cells];
-                float c = 0.0f, sn = 0.0f;
-                if (!isv) {
-                    if (a.rope_cs) {
-                        const float2 t = a.rope_cs[(size_t) row * 64 + lane];
-                        c = t.x, sn = t.y;
-                    } else {
-                        rope_cs(p, lane, a.theta_scale, c, sn);
-                    }
-                }
+            if (row < a.M)
                 qk_head(a.qkv + (size_t) row * a.ldqkv + (size_t) h * 128, lane, h, H, KVH, true, v0, v1, c, sn, w0,
                         w1, a.eps, a.kpool, a.vpool, page, a.page_cells, p % a.page_cells);
-            }
         }
     }
 }
@@ -759,6 +789,9 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
         vk_off = sr < 0 ? (int) XA_GATHER_OOB : (sr >> 4) * rstride + 4 * (16 * g + (sr & 15));
     }
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xa + x0, xbytes);
+    constexpr bool ROPE = FE >= FE_ROPE && FE < FE_GSWIGLU;
+    [[maybe_unused]] RopeRows<MT> rr;
+    if constexpr (ROPE) rope_rows_begin<MT>(a, mt0, wave, lane, rr);
 
     // the slice's activation straight into LDS (buffer loads to LDS: lane l's 16 bytes land at 16 l of the fragment,
     // no registers; fragments past the slice repeat its last group: loads stay in bounds, never summed)
@@ -792,6 +825,10 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
     static_assert(NWL < 64, "vmcnt holds 6 bits");
     __builtin_amdgcn_s_waitcnt((NWL & 15) | ((NWL >> 4) << 14) | (7 << 4) | (15 << 8));
     __syncthreads();
+    if constexpr (ROPE) {
+        rope_rows_end<MT>(a, set, mt0, wave, lane, rr);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     floatx4 acc[S][MT];
     for (int t = 0; t < S; ++t)
@@ -914,7 +951,7 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
         __syncthreads();
         if (!s_last) return;
         l1_drop();
-        q4_epilogue<FE, MT, S>(a, set, mt0);
+        q4_epilogue<FE, MT, S>(a, set, mt0, rr);
         // back to zero by an atomic of the same kind, performed where the counts were (a plain store of an atomic
         // compiles to a write-through store, which need not meet the L2's copy); after the epilogue, so that no
         // barrier waits for it (every count of the set has been made: the next launch is the next to count)
