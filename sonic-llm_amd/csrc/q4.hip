@@ -743,8 +743,16 @@ __device__ __forceinline__ void q4_epilogue(const GemmArgs& a, int set, int mt0,
 // stripes' weights through a ring of D register slots (group i + D's loads issued as soon as group i is summed), with
 // no further synchronisation. The activation fragment, scales and corrections read from LDS for a block serve S x MT
 // MFMAs. Same arithmetic and order as k_q4_gemm. FE: the fused epilogue run by each set's last workgroup (GemmArgs).
+// The launch's hot arguments come first as scalars (GS_ARGS), which the hardware preloads into SGPRs at wavefront
+// start (-amdgpu-kernarg-preload-count), so a workgroup issues its first loads without waiting for the argument block;
+// the rest of GemmArgs is read from it as before.
+#define GS_ARGS(a) (a).w, (a).xa, (a).part, (a).M, (a).N, (a).K, (a).nstripes, (a).ngroups, (a).gps, (a).pos, (a).seq, (a)
 template <int WT, int MT, int S, int D, int GMAX, int FE = FE_NONE, bool GRP = FE == FE_GSWIGLU>
-__global__ __launch_bounds__(256) void k_q4_gemm_s(GemmArgs a) {
+__global__ __launch_bounds__(256) void k_q4_gemm_s(const uint8_t* w_, const uint8_t* xa_, float* part_, int M_, int N_,
+                                                   int K_, int nstripes_, int ngroups_, int gps_, const int32_t* pos_,
+                                                   const int32_t* seq_, GemmArgs a) {
+    a.w = w_, a.xa = xa_, a.part = part_, a.M = M_, a.N = N_, a.K = K_;
+    a.nstripes = nstripes_, a.ngroups = ngroups_, a.gps = gps_, a.pos = pos_, a.seq = seq_;
     constexpr bool Q8 = WT == WT_Q8_0;
     constexpr int TB = Q8 ? Q8T_BYTES : Q4T_BYTES, SO = Q8 ? Q8T_SCALE_OFF : Q4T_SCALE_OFF;
     constexpr int NW = Q8 ? 2 : 1;
@@ -1181,7 +1189,7 @@ template <int WT>
 static bool launch_gemm_s(int mt, int spw, int D, int gps, dim3 grid, const GemmArgs& a, hipStream_t st) {
 #define GSX(MT_, S_, D_, GM_)                                                                                \
     if (mt == MT_ && spw == S_ && D == D_ && gps <= GM_) {                                                   \
-        hipLaunchKernelGGL((k_q4_gemm_s<WT, MT_, S_, D_, GM_>), grid, dim3(256), 0, st, a);                  \
+        hipLaunchKernelGGL((k_q4_gemm_s<WT, MT_, S_, D_, GM_>), grid, dim3(256), 0, st, GS_ARGS(a));                  \
         return true;                                                                                         \
     }
     GSX(1, 1, 2, 4) GSX(1, 1, 2, 8) GSX(2, 1, 2, 4) GSX(2, 1, 2, 8)
@@ -1261,7 +1269,7 @@ template <int WT, int FE>
 static bool launch_gemm_fe(int mt, int spw, int gps, dim3 grid, const GemmArgs& a, hipStream_t st) {
 #define GSF(MT_, S_, GM_)                                                                                    \
     if (mt == MT_ && spw == S_ && gps <= GM_) {                                                              \
-        hipLaunchKernelGGL((k_q4_gemm_s<WT, MT_, S_, 2, GM_, FE>), grid, dim3(256), 0, st, a);               \
+        hipLaunchKernelGGL((k_q4_gemm_s<WT, MT_, S_, 2, GM_, FE>), grid, dim3(256), 0, st, GS_ARGS(a));               \
         return true;                                                                                         \
     }
     if constexpr (WT == WT_Q4_0) {
@@ -1415,7 +1423,7 @@ template <int WT>
 static bool launch_grouped_s(int S, int ng, dim3 grid, const GemmArgs& a, hipStream_t st) {
 #define GSG(S_, GM_)                                                                                         \
     if (S == S_ && ng <= GM_) {                                                                              \
-        hipLaunchKernelGGL((k_q4_gemm_s<WT, 1, S_, 2, GM_, FE_NONE, true>), grid, dim3(256), 0, st, a);      \
+        hipLaunchKernelGGL((k_q4_gemm_s<WT, 1, S_, 2, GM_, FE_NONE, true>), grid, dim3(256), 0, st, GS_ARGS(a));      \
         return true;                                                                                         \
     }
     if constexpr (WT == WT_Q4_0) {
@@ -1481,8 +1489,8 @@ int q4_gemm_grouped_swiglu(const uint8_t* w, size_t wstride, const int32_t* item
     a.nstripes = N / 16; a.ngroups = ngroups; a.ks = 1; a.gps = ngroups;
     a.mtiles = (M + 15) / 16;
     const dim3 grid(a.nstripes / 16, 1, max_items);
-    if (ngroups <= 8) hipLaunchKernelGGL((k_q4_gemm_s<WT_Q4_0, 1, 4, 2, 8, FE_GSWIGLU>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_q4_gemm_s<WT_Q4_0, 1, 4, 2, 16, FE_GSWIGLU>), grid, dim3(256), 0, st, a);
+    if (ngroups <= 8) hipLaunchKernelGGL((k_q4_gemm_s<WT_Q4_0, 1, 4, 2, 8, FE_GSWIGLU>), grid, dim3(256), 0, st, GS_ARGS(a));
+    else hipLaunchKernelGGL((k_q4_gemm_s<WT_Q4_0, 1, 4, 2, 16, FE_GSWIGLU>), grid, dim3(256), 0, st, GS_ARGS(a));
     return 1;
 }
 
