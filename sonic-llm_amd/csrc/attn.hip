@@ -324,7 +324,16 @@ __device__ __forceinline__ void attn_part_item(const AttnArgs& a, const AttnItem
     }
 }
 // grid (KV head, item): see attention_items
-__global__ __launch_bounds__(256) void k_attn_part(AttnArgs a) {
+// The launches' hot arguments come first as scalars, which the hardware preloads into SGPRs at wavefront start
+// (-amdgpu-kernarg-preload-count): the item, group, page-table and cell loads are issued without waiting for the
+// argument block; the rest of AttnArgs is read from it as before.
+#define AP_ARGS(a) (a).items, (a).groups, (a).pt, (a).kpool, (a).vpool, (a).q, (a).H, (a).KVH, (a).page_cells, (a).max_pages, (a)
+#define AM_ARGS(a) (a).mrows, (a).row_pos, (a).part, (a).out, (a).xa, (a).H, (a).KVH, (a).max_chunks, (a).ldo, (a)
+__global__ __launch_bounds__(256) void k_attn_part(const AttnItem* items_, const AttnGroup* groups_, const int32_t* pt_,
+                                                   const uint16_t* kpool_, const uint16_t* vpool_, const float* q_,
+                                                   int H_, int KVH_, int page_cells_, int max_pages_, AttnArgs a) {
+    a.items = items_, a.groups = groups_, a.pt = pt_, a.kpool = kpool_, a.vpool = vpool_, a.q = q_;
+    a.H = H_, a.KVH = KVH_, a.page_cells = page_cells_, a.max_pages = max_pages_;
     __shared__ AttnShared sh;
     attn_part_item(a, a.items[blockIdx.y], blockIdx.x, sh);
 }
@@ -675,7 +684,11 @@ __device__ __forceinline__ void attn_merge_one(const AttnArgs& a, const int r, c
 // head k with k = L (mod 8): k_attn_part's grid (KV head fastest) dealt every item of KV head k to XCD k mod 8, so the
 // merge reads its partials where they were written. Otherwise (row, head) = (blockIdx.x, blockIdx.y).
 template <int MB, bool XA>
-__global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
+__global__ __launch_bounds__(64) void k_attn_merge(const int32_t* mrows_, const int32_t* row_pos_, float* part_,
+                                                   float* out_, uint8_t* xa_, int H_, int KVH_, int max_chunks_,
+                                                   int ldo_, AttnArgs a) {
+    a.mrows = mrows_, a.row_pos = row_pos_, a.part = part_, a.out = out_, a.xa = xa_;
+    a.H = H_, a.KVH = KVH_, a.max_chunks = max_chunks_, a.ldo = ldo_;
     int row = blockIdx.x, h = blockIdx.y;
     if constexpr (XA) {
         const int L = blockIdx.x, kx = L & 7, q = L >> 3, hx = a.H >> 3, G = a.H / a.KVH, t = q % hx;
@@ -752,7 +765,7 @@ int attention_items(const AttnArgs& a, hipStream_t st) {
     // grids: configs[2]'s chunk items 55.2 -> 51.3 us a layer (with the item order of attn_plan), configs[1] 60.2 ->
     // 56.8 us; the run items (prompt rows) unchanged.
     if (a.whole) hipLaunchKernelGGL(k_attn_whole, dim3(a.KVH, a.n_items), dim3(512), 0, st, a);
-    else hipLaunchKernelGGL(k_attn_part, dim3(a.KVH, a.n_items), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(k_attn_part, dim3(a.KVH, a.n_items), dim3(256), 0, st, AP_ARGS(a));
     return 0;
 }
 int attention_merge(const AttnArgs& a, hipStream_t st) {
@@ -764,8 +777,8 @@ int attention_merge(const AttnArgs& a, hipStream_t st) {
     const dim3 grid = xa ? dim3(a.n_mrows * a.H) : dim3(a.n_mrows, a.H);
 #define MERGE(MB_)                                                                               \
     do {                                                                                         \
-        if (xa) hipLaunchKernelGGL((k_attn_merge<MB_, true>), grid, dim3(64), 0, st, a);         \
-        else hipLaunchKernelGGL((k_attn_merge<MB_, false>), grid, dim3(64), 0, st, a);           \
+        if (xa) hipLaunchKernelGGL((k_attn_merge<MB_, true>), grid, dim3(64), 0, st, AM_ARGS(a));         \
+        else hipLaunchKernelGGL((k_attn_merge<MB_, false>), grid, dim3(64), 0, st, AM_ARGS(a));           \
     } while (0)
     if (mc <= 8) MERGE(8);
     else if (mc <= 10) MERGE(10);

@@ -601,14 +601,26 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
 }
 
 // GRP: grouped (expert items, gathered rows, row masks); compiled out of the other launches
+// The kernels' hot arguments come first as scalars, which the hardware preloads into SGPRs at wavefront start
+// (-amdgpu-kernarg-preload-count): a workgroup issues its first loads without waiting for the argument block; the rest
+// of GemmArgs is read from it as before. A launch passes GS_ARGS(a).
+#define GS_PARAMS                                                                                                   \
+    const uint8_t *w_, const uint8_t *xa_, float *part_, int M_, int N_, int K_, int nstripes_, int ngroups_,        \
+        int gps_, const int32_t *pos_, const int32_t *seq_, GemmArgs a
+#define GS_TAKE()                                                                                                   \
+    a.w = w_, a.xa = xa_, a.part = part_, a.M = M_, a.N = N_, a.K = K_, a.nstripes = nstripes_,                     \
+    a.ngroups = ngroups_, a.gps = gps_, a.pos = pos_, a.seq = seq_
+#define GS_ARGS(a) (a).w, (a).xa, (a).part, (a).M, (a).N, (a).K, (a).nstripes, (a).ngroups, (a).gps, (a).pos, (a).seq, (a)
 template <int WT, int MT, int S, bool FK = false, bool GRP = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_q4_gemm(GemmArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_q4_gemm(GS_PARAMS) {
+    GS_TAKE();
     q4_gemm_ring<WT, MT, S, FK, false, GRP>(a);
 }
 // the FK walk with two stripes a wavefront (prompt rows of the wide matrices): its accumulators and slice sums need
 // more than the 168 registers of 3 wavefronts a SIMD. SW: the gate|up matrix's SwiGLU + Q8_0 as its epilogue
 template <int WT, int MT, int S, bool SW = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_q4_gemm_fk2(GemmArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_q4_gemm_fk2(GS_PARAMS) {
+    GS_TAKE();
     q4_gemm_ring<WT, MT, S, true, SW>(a);
 }
 
@@ -743,16 +755,10 @@ __device__ __forceinline__ void q4_epilogue(const GemmArgs& a, int set, int mt0,
 // stripes' weights through a ring of D register slots (group i + D's loads issued as soon as group i is summed), with
 // no further synchronisation. The activation fragment, scales and corrections read from LDS for a block serve S x MT
 // MFMAs. Same arithmetic and order as k_q4_gemm. FE: the fused epilogue run by each set's last workgroup (GemmArgs).
-// The launch's hot arguments come first as scalars (GS_ARGS), which the hardware preloads into SGPRs at wavefront
-// start (-amdgpu-kernarg-preload-count), so a workgroup issues its first loads without waiting for the argument block;
-// the rest of GemmArgs is read from it as before.
-#define GS_ARGS(a) (a).w, (a).xa, (a).part, (a).M, (a).N, (a).K, (a).nstripes, (a).ngroups, (a).gps, (a).pos, (a).seq, (a)
+// (the hot arguments as preloaded scalars, GS_PARAMS)
 template <int WT, int MT, int S, int D, int GMAX, int FE = FE_NONE, bool GRP = FE == FE_GSWIGLU>
-__global__ __launch_bounds__(256) void k_q4_gemm_s(const uint8_t* w_, const uint8_t* xa_, float* part_, int M_, int N_,
-                                                   int K_, int nstripes_, int ngroups_, int gps_, const int32_t* pos_,
-                                                   const int32_t* seq_, GemmArgs a) {
-    a.w = w_, a.xa = xa_, a.part = part_, a.M = M_, a.N = N_, a.K = K_;
-    a.nstripes = nstripes_, a.ngroups = ngroups_, a.gps = gps_, a.pos = pos_, a.seq = seq_;
+__global__ __launch_bounds__(256) void k_q4_gemm_s(GS_PARAMS) {
+    GS_TAKE();
     constexpr bool Q8 = WT == WT_Q8_0;
     constexpr int TB = Q8 ? Q8T_BYTES : Q4T_BYTES, SO = Q8 ? Q8T_SCALE_OFF : Q4T_SCALE_OFF;
     constexpr int NW = Q8 ? 2 : 1;
@@ -1170,16 +1176,16 @@ template <int WT, bool FK = false>
 static void launch_gemm(int mt, int spw, dim3 grid, const GemmArgs& a, hipStream_t st) {
     if constexpr (WT == WT_Q4_0 && !FK) {
         if (mt == 1) {
-            if (spw == 2) hipLaunchKernelGGL((k_q4_gemm<WT, 1, 2, FK>), grid, dim3(256), 0, st, a);
-            else hipLaunchKernelGGL((k_q4_gemm<WT, 1, 1, FK>), grid, dim3(256), 0, st, a);
+            if (spw == 2) hipLaunchKernelGGL((k_q4_gemm<WT, 1, 2, FK>), grid, dim3(256), 0, st, GS_ARGS(a));
+            else hipLaunchKernelGGL((k_q4_gemm<WT, 1, 1, FK>), grid, dim3(256), 0, st, GS_ARGS(a));
         } else {
-            if (spw == 2) hipLaunchKernelGGL((k_q4_gemm<WT, 2, 2, FK>), grid, dim3(256), 0, st, a);
-            else hipLaunchKernelGGL((k_q4_gemm<WT, 2, 1, FK>), grid, dim3(256), 0, st, a);
+            if (spw == 2) hipLaunchKernelGGL((k_q4_gemm<WT, 2, 2, FK>), grid, dim3(256), 0, st, GS_ARGS(a));
+            else hipLaunchKernelGGL((k_q4_gemm<WT, 2, 1, FK>), grid, dim3(256), 0, st, GS_ARGS(a));
         }
     } else {  // Q8_0: one stripe per wavefront (q4_plan); FK likewise
         (void) spw;
-        if (mt == 1) hipLaunchKernelGGL((k_q4_gemm<WT, 1, 1, FK>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_q4_gemm<WT, 2, 1, FK>), grid, dim3(256), 0, st, a);
+        if (mt == 1) hipLaunchKernelGGL((k_q4_gemm<WT, 1, 1, FK>), grid, dim3(256), 0, st, GS_ARGS(a));
+        else hipLaunchKernelGGL((k_q4_gemm<WT, 2, 1, FK>), grid, dim3(256), 0, st, GS_ARGS(a));
     }
 }
 
@@ -1250,7 +1256,7 @@ int q4_gemm_raw(const uint8_t* w, const uint8_t* xa, int M, int N, int K, float*
         const int fmt = p.nstripes < 384 ? 1 : 2;
         if (wt == WT_Q4_0 && p.nstripes >= 384) {
             const dim3 grid((p.nstripes + 7) / 8, 1, (a.mtiles + 1) / 2);
-            hipLaunchKernelGGL((k_q4_gemm_fk2<WT_Q4_0, 2, 2>), grid, dim3(256), 0, st, a);
+            hipLaunchKernelGGL((k_q4_gemm_fk2<WT_Q4_0, 2, 2>), grid, dim3(256), 0, st, GS_ARGS(a));
         } else {
             const dim3 grid(p.sets, 1, (a.mtiles + fmt - 1) / fmt);
             if (wt == WT_Q8_0) launch_gemm<WT_Q8_0, true>(fmt, 1, grid, a, st);
@@ -1463,10 +1469,10 @@ int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, cons
     // registers)
     if (wt == WT_Q8_0) {
         hipLaunchKernelGGL((k_q4_gemm<WT_Q8_0, 1, 1, false, true>), dim3((a.nstripes + 3) / 4, 1, max_items), dim3(256), 0,
-                           st, a);
+                           st, GS_ARGS(a));
     } else {
         hipLaunchKernelGGL((k_q4_gemm<WT_Q4_0, 1, 2, false, true>), dim3((a.nstripes + 7) / 8, 1, max_items), dim3(256), 0,
-                           st, a);
+                           st, GS_ARGS(a));
     }
     return 1;
 }
@@ -1510,7 +1516,7 @@ int q4_gemm_swiglu(const uint8_t* w, const uint8_t* xa, int M, int N, int K, flo
     a.nstripes = p.nstripes; a.ngroups = p.ngroups; a.ks = p.ks; a.gps = p.gps;
     a.mtiles = (M + 15) / 16;
     const dim3 grid((p.nstripes + 7) / 8, 1, (a.mtiles + 1) / 2);
-    hipLaunchKernelGGL((k_q4_gemm_fk2<WT_Q4_0, 2, 2, true>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((k_q4_gemm_fk2<WT_Q4_0, 2, 2, true>), grid, dim3(256), 0, st, GS_ARGS(a));
     return 1;
 }
 
