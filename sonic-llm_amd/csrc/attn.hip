@@ -622,29 +622,39 @@ __global__ __launch_bounds__(512) void k_attn_run(AttnArgs a) {
 // workgroups of this XCD (the caller has dropped its L1 lines: the loads read the XCD's L2)
 template <bool L2, int MB = MERGE_BATCH>
 __device__ __forceinline__ void attn_merge_one(const AttnArgs& a, const int r, const int h, const int lane) {
-    const int nc = a.row_pos[r] / ATT_CHUNK + 1;
+    // the chunk count (the row's position) is loaded beside the first round's partials: their addresses are clamped
+    // to the (row, head)'s max_chunks slots, not to its chunks, so no load waits for it (slots past the row's chunks
+    // are loaded and not folded); the loads are buffer loads, all issued before any is folded (as plain loads, the
+    // uniform (m, l) pairs became scalar loads, each waited for in the fold)
+    const int rp = (int) __builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(a.row_pos + r, 4), 0, 0, 0);
     const float* p0 = a.part + ((size_t) r * a.H + h) * a.max_chunks * (ATT_D + 2);
     // (L2: a resource over the row's partials; offsets below 2^31 bytes)
     const __amdgpu_buffer_rsrc_t pr = buf_rsrc(p0, (uint32_t) (a.max_chunks * (ATT_D + 2) * 4));
     float M = -INFINITY, L = 0.0f, o[2] = {0.0f, 0.0f};
-    for (int c0 = 0; c0 < nc; c0 += MB) {  // (contexts up to 4096 cells: one round of loads)
-        float2 ov[MB], ml[MB];
+    float2 ov[MB], ml[MB];
+    auto load = [&](int c0) {
         for (int j = 0; j < MB; ++j) {
-            const int pc = (c0 + j < nc ? c0 + j : nc - 1) * (ATT_D + 2);
-            if constexpr (L2) {
-                ov[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, (pc + 2 * lane) * 4, 0, 1));
-                ml[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, (pc + ATT_D) * 4, 0, 1));
-            } else {
-                ov[j] = *(const float2*) (p0 + pc + 2 * lane);
-                ml[j] = *(const float2*) (p0 + pc + ATT_D);
-            }
+            const int pc = min(c0 + j, a.max_chunks - 1) * (ATT_D + 2);
+            ov[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, (pc + 2 * lane) * 4, 0, L2 ? 1 : 0));
+            ml[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, (pc + ATT_D) * 4, 0, L2 ? 1 : 0));
         }
+    };
+    auto fold = [&](int c0, int nc) {
 #pragma unroll
         for (int j = 0; j < MB; ++j) {  // (a fixed trip count keeps ov and ml in registers)
             if (c0 + j >= nc) continue;  // past the row's chunks
             const float v2[2] = {ov[j].x, ov[j].y};
             attn_fold<2>(M, L, o, ml[j].x, ml[j].y, v2);
         }
+    };
+    int rpv = rp;
+    load(0);
+    asm volatile("" : "+v"(rpv));  // (rpv stays where the load put it until the first round's loads are issued)
+    const int nc = rpv / ATT_CHUNK + 1;
+    fold(0, nc);
+    for (int c0 = MB; c0 < nc; c0 += MB) {  // (contexts up to 4096 cells: one round of loads)
+        load(c0);
+        fold(c0, nc);
     }
     attn_finish<2>(L, o);
     const float o0 = o[0], o1 = o[1];
