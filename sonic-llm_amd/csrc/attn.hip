@@ -268,7 +268,7 @@ __device__ __forceinline__ int attn_member(const AttnItem& it, int m) {
 // partial depends on its own column only, so it is the same whichever item computes it.
 // (every thread of the workgroup reaches the end)
 __device__ __forceinline__ void attn_part_item(const AttnArgs& a, const AttnItem it, const int kvh, AttnShared& sh) {
-    const AttnGroup gr = a.groups[it.group];
+    const AttnGroup gr = it.g;
     const int G = a.H / a.KVH;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
@@ -386,7 +386,7 @@ struct AttnPairShared {
 __global__ __launch_bounds__(512) void k_attn_whole(AttnArgs a) {
     __shared__ AttnPairShared sh;
     const AttnItem it = a.items[blockIdx.y];  // (grid: KV head, item)
-    const AttnGroup gr = a.groups[it.group];
+    const AttnGroup gr = it.g;
     const int kvh = blockIdx.x;
     const int G = a.H / a.KVH;
     const int lane = threadIdx.x & 63, w8 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -727,7 +727,7 @@ __global__ __launch_bounds__(256) void k_attn_fold(AttnArgs a) {
     const AttnGroup gr = a.groups[gi];
     const int nc = (gr.pos0 + gr.nrows - 1) / ATT_CHUNK + 1;
     if (c >= nc) return;  // (past the group's chunks)
-    const AttnItem it = {gi, c, 1, {-1, -1, -1}, 1};
+    const AttnItem it = {gi, c, 1, {-1, -1, -1}, 1, a.groups[gi]};
     attn_part_item(a, it, kvh, sh);
     __builtin_amdgcn_s_waitcnt(0);  // the partials have reached the L2
     __syncthreads();
@@ -922,6 +922,8 @@ void attn_plan(int R, const int32_t* seq, const int32_t* pos, int H, int KVH, in
             for (int i = 0; i < gr.nrows; ++i) p.mrows.push_back(gr.row0 + i);
         }
     }
+    for (auto& it : p.items) it.g = p.groups[it.group];
+    for (auto& it : p.runs) it.g = p.groups[it.group];
     // chunk items with more cells first (a context's short last chunk at the end of the launch): configs[2] 51.9 ->
     // 51.3 us a layer, configs[3]'s verify groups 33.3 -> 32.4 us; the results do not depend on the order
     if (!p.whole) {

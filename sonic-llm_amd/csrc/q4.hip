@@ -528,6 +528,7 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
         }
         stage(0, r0, k0);
     }
+    asm volatile("" ::"s"(a.part), "s"(a.N));  // (the tail's arguments read behind the first loads, as k_q4_gemm_s)
     const int trips = (ng + D - 1) / D;
     int in_slice = 0;  // FK: groups of the current slice summed so far
     bool first = true;
@@ -604,13 +605,14 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
 // The kernels' hot arguments come first as scalars, which the hardware preloads into SGPRs at wavefront start
 // (-amdgpu-kernarg-preload-count): a workgroup issues its first loads without waiting for the argument block; the rest
 // of GemmArgs is read from it as before. A launch passes GS_ARGS(a).
+// (14 dwords are preloaded: those a workgroup needs before its first loads come first; part, read at the end, last)
 #define GS_PARAMS                                                                                                   \
-    const uint8_t *w_, const uint8_t *xa_, float *part_, int M_, int N_, int K_, int nstripes_, int ngroups_,        \
-        int gps_, const int32_t *pos_, const int32_t *seq_, GemmArgs a
+    const uint8_t *w_, const uint8_t *xa_, int M_, int K_, int nstripes_, int ngroups_, int gps_,                   \
+        const int32_t *pos_, const int32_t *seq_, int N_, float *part_, GemmArgs a
 #define GS_TAKE()                                                                                                   \
     a.w = w_, a.xa = xa_, a.part = part_, a.M = M_, a.N = N_, a.K = K_, a.nstripes = nstripes_,                     \
     a.ngroups = ngroups_, a.gps = gps_, a.pos = pos_, a.seq = seq_
-#define GS_ARGS(a) (a).w, (a).xa, (a).part, (a).M, (a).N, (a).K, (a).nstripes, (a).ngroups, (a).gps, (a).pos, (a).seq, (a)
+#define GS_ARGS(a) (a).w, (a).xa, (a).M, (a).K, (a).nstripes, (a).ngroups, (a).gps, (a).pos, (a).seq, (a).N, (a).part, (a)
 template <int WT, int MT, int S, bool FK = false, bool GRP = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_q4_gemm(GS_PARAMS) {
     GS_TAKE();
@@ -834,6 +836,9 @@ __global__ __launch_bounds__(256) void k_q4_gemm_s(GS_PARAMS) {
         wload(j, j);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // the arguments past the preloaded ones that the tail uses, read now (behind the first loads) rather than where
+    // the compiler would sink them, at the tail, a round trip after the loop
+    asm volatile("" ::"s"(a.part), "s"(a.N));
     // the LDS loads were issued first: waiting until no more than the weights' loads are outstanding waits for them
     constexpr int NWL = D * S * (NW + 1);
     static_assert(NWL < 64, "vmcnt holds 6 bits");

@@ -180,6 +180,9 @@ struct AttnItem {
     // a run item (k_attn_run): groups group .. group + nmem - 1, consecutive groups of one sequence at consecutive
     // positions (prompt rows), walked together over the last one's nchunk chunks; 1 for every other item
     int32_t nmem;
+    // a copy of groups[group] (attn_plan fills it), so that a chunk or whole-group workgroup's first loads need no
+    // load of its group
+    AttnGroup g;
 };
 #define ATT_RUN_MAX 4       // groups a run item holds (their queries staged in LDS, K/V cells read once for all)
 #define ATT_RUN_MIN_WG 128  // run items are used when they make at least this many workgroups (items x KV heads)
