@@ -609,10 +609,14 @@ __device__ __forceinline__ void q4_gemm_ring(const GemmArgs& a) {
 #define GS_PARAMS                                                                                                   \
     const uint8_t *w_, const uint8_t *xa_, int M_, int K_, int nstripes_, int ngroups_, int gps_,                   \
         const int32_t *pos_, const int32_t *seq_, int N_, float *part_, GemmArgs a
+// (grouped launches, GRP: the item list and its count in the slots of pos and seq, GSG_ARGS)
 #define GS_TAKE()                                                                                                   \
     a.w = w_, a.xa = xa_, a.part = part_, a.M = M_, a.N = N_, a.K = K_, a.nstripes = nstripes_,                     \
-    a.ngroups = ngroups_, a.gps = gps_, a.pos = pos_, a.seq = seq_
+    a.ngroups = ngroups_, a.gps = gps_;                                                                              \
+    if constexpr (GRP) a.items = pos_, a.count = seq_;                                                               \
+    else a.pos = pos_, a.seq = seq_
 #define GS_ARGS(a) (a).w, (a).xa, (a).M, (a).K, (a).nstripes, (a).ngroups, (a).gps, (a).pos, (a).seq, (a).N, (a).part, (a)
+#define GSG_ARGS(a) (a).w, (a).xa, (a).M, (a).K, (a).nstripes, (a).ngroups, (a).gps, (a).items, (a).count, (a).N, (a).part, (a)
 template <int WT, int MT, int S, bool FK = false, bool GRP = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_q4_gemm(GS_PARAMS) {
     GS_TAKE();
@@ -622,6 +626,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
 // more than the 168 registers of 3 wavefronts a SIMD. SW: the gate|up matrix's SwiGLU + Q8_0 as its epilogue
 template <int WT, int MT, int S, bool SW = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_q4_gemm_fk2(GS_PARAMS) {
+    constexpr bool GRP = false;
     GS_TAKE();
     q4_gemm_ring<WT, MT, S, true, SW>(a);
 }
@@ -1434,7 +1439,7 @@ template <int WT>
 static bool launch_grouped_s(int S, int ng, dim3 grid, const GemmArgs& a, hipStream_t st) {
 #define GSG(S_, GM_)                                                                                         \
     if (S == S_ && ng <= GM_) {                                                                              \
-        hipLaunchKernelGGL((k_q4_gemm_s<WT, 1, S_, 2, GM_, FE_NONE, true>), grid, dim3(256), 0, st, GS_ARGS(a));      \
+        hipLaunchKernelGGL((k_q4_gemm_s<WT, 1, S_, 2, GM_, FE_NONE, true>), grid, dim3(256), 0, st, GSG_ARGS(a));      \
         return true;                                                                                         \
     }
     if constexpr (WT == WT_Q4_0) {
@@ -1474,10 +1479,10 @@ int q4_gemm_grouped(const uint8_t* w, size_t wstride, const int32_t* items, cons
     // registers)
     if (wt == WT_Q8_0) {
         hipLaunchKernelGGL((k_q4_gemm<WT_Q8_0, 1, 1, false, true>), dim3((a.nstripes + 3) / 4, 1, max_items), dim3(256), 0,
-                           st, GS_ARGS(a));
+                           st, GSG_ARGS(a));
     } else {
         hipLaunchKernelGGL((k_q4_gemm<WT_Q4_0, 1, 2, false, true>), dim3((a.nstripes + 7) / 8, 1, max_items), dim3(256), 0,
-                           st, GS_ARGS(a));
+                           st, GSG_ARGS(a));
     }
     return 1;
 }
@@ -1500,8 +1505,8 @@ int q4_gemm_grouped_swiglu(const uint8_t* w, size_t wstride, const int32_t* item
     a.nstripes = N / 16; a.ngroups = ngroups; a.ks = 1; a.gps = ngroups;
     a.mtiles = (M + 15) / 16;
     const dim3 grid(a.nstripes / 16, 1, max_items);
-    if (ngroups <= 8) hipLaunchKernelGGL((k_q4_gemm_s<WT_Q4_0, 1, 4, 2, 8, FE_GSWIGLU>), grid, dim3(256), 0, st, GS_ARGS(a));
-    else hipLaunchKernelGGL((k_q4_gemm_s<WT_Q4_0, 1, 4, 2, 16, FE_GSWIGLU>), grid, dim3(256), 0, st, GS_ARGS(a));
+    if (ngroups <= 8) hipLaunchKernelGGL((k_q4_gemm_s<WT_Q4_0, 1, 4, 2, 8, FE_GSWIGLU>), grid, dim3(256), 0, st, GSG_ARGS(a));
+    else hipLaunchKernelGGL((k_q4_gemm_s<WT_Q4_0, 1, 4, 2, 16, FE_GSWIGLU>), grid, dim3(256), 0, st, GSG_ARGS(a));
     return 1;
 }
 
