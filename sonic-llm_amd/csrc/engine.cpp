@@ -98,6 +98,9 @@ struct sn_engine {
     int nxcd = 1;
     uint64_t* d_fcnt = nullptr;
     int32_t* d_gcnt = nullptr;  // the one-launch MoE routing's system-scope counter
+    // the row kernels read the next matmul's first weight groups into the Infinity Cache (resid_quant's next_w); off
+    // with SN_NO_PREFETCH
+    bool prefetch = true;
     float2* rope_cs = nullptr;  // a step's rotation table (rope_table) [max_rows][64]
     int32_t* d_xerr = nullptr;
     int fcnt_len = 0;
@@ -595,6 +598,7 @@ extern "C" sn_engine* sn_open(const char* path, const char* kernels, int slots, 
     if (!e->rope_cs) return fail("");
     e->fuse_ok = xcd_round_robin(e->st, &e->nxcd);
     e->fuse = e->fuse_ok && !getenv("SN_NO_FUSE");
+    e->prefetch = !getenv("SN_NO_PREFETCH");
     e->attn_fold = false;  // (withdrawn: see attn_fold)
     size_t ws = 0;
     ws = std::max(ws, q4_workspace_bytes(R, e->NQKV, E, e->wt));
@@ -979,7 +983,9 @@ struct Dev {
         });
     }
     // x (R rows of E) += the last matmul's sums (add false: x = the sums); then the Q8_0 operand of norm(x) when asked
-    void resid(float* x, int R, const float* nw, bool quantize, bool add = true) {
+    // (next_w: the next matmul's N x E matrix, whose first weight groups the launch reads into the Infinity Cache)
+    void resid(float* x, int R, const float* nw, bool quantize, bool add = true, const uint8_t* next_w = nullptr,
+               int next_N = 0) {
         const int E = e->E;
         if (moe_pending) {  // x += the MoE output (the grouped down matmul's rows, weighted), then the operand
             moe_pending = false;
@@ -991,7 +997,8 @@ struct Dev {
             return;
         }
         rc |= e->launch(SNX_K_QUANT, (double) R * E * (8 + 4 * ks) + (quantize ? (double) R * E * 2 : 0.0), [&] {
-            return resid_quant(x, e->gemm_ws, ks, R, E, nw, e->eps, quantize ? e->xa : nullptr, st, add);
+            return resid_quant(x, e->gemm_ws, ks, R, E, nw, e->eps, quantize ? e->xa : nullptr, st, add, nullptr,
+                               e->prefetch ? next_w : nullptr, next_N, E, e->wt);
         });
     }
     void swiglu(int R) {
@@ -1068,7 +1075,7 @@ struct Dev {
             moe(l, x, R);
             return true;
         }
-        resid(x, R, l.ffn_norm, true);
+        resid(x, R, l.ffn_norm, true, true, l.wgu, 2 * F);
         if (gemm_swiglu(l.wgu, R) || gemm_swiglu_dec(l.wgu, R)) {
             gemm(l.wd, R, E, F, e->xa2);
             return true;
@@ -1146,7 +1153,7 @@ struct Dev {
         rc |= e->launch(SNX_K_OTHER, (double) R * E * 8, [&] { embed_rows(e->tok_embd, e->V, E, d_tok, R, e->x, st); return 0; });
         bool pending = false;  // x awaits the previous layer's down projection sums
         for (int i = 0; i < e->L && rc == 0; ++i) {
-            if (pending) resid(e->x, R, e->ly[i].attn_norm, true);  // x += them, then the attn_norm operand
+            if (pending) resid(e->x, R, e->ly[i].attn_norm, true, true, e->ly[i].wqkv, e->NQKV);  // x += them, then the attn_norm operand
             else quant(e->x, nullptr, R, E, e->ly[i].attn_norm);
             pending = block(e->ly[i], i, e->x, R, S, al, d_seq, d_pos);
         }

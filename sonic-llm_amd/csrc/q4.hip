@@ -216,6 +216,30 @@ __device__ __forceinline__ float4 pairs_sum4(const float* y, const int32_t* prow
     return acc;
 }
 
+// The next matmul's first weight groups read by extra workgroups of a row kernel, whose own work leaves HBM idle, so
+// that the matmul finds them in the Infinity Cache: for every stripe s and k-slice y of the next matrix, the bytes
+// [s sbytes + y gstep, + len) (the groups its workgroups load first), in 128-byte lines, WP_LINES a thread with every
+// load in flight (a line past the ranges is an out-of-range buffer load: no access).
+#define WP_LINES 4
+struct WeightPrefetch {
+    const uint8_t* w;
+    int nranges, ks, sbytes, gstep, lines;  // ranges = stripes x ks, lines of 128 bytes a range
+    uint32_t total;                         // the matrix's bytes
+};
+__device__ __forceinline__ void weight_prefetch(const WeightPrefetch& pf, int wg, int nwg) {
+    const __amdgpu_buffer_rsrc_t r = buf_rsrc(pf.w, pf.total);
+    const int nl = pf.nranges * pf.lines;
+    uint32_t v[WP_LINES];
+    for (int k = 0; k < WP_LINES; ++k) {
+        const int L = (k * nwg + wg) * (int) blockDim.x + (int) threadIdx.x;
+        const int i = L / pf.lines, ln = L % pf.lines;
+        const uint32_t off = L < nl ? (uint32_t) (i / pf.ks) * pf.sbytes + (uint32_t) (i % pf.ks) * pf.gstep + 128u * ln
+                                    : pf.total;
+        v[k] = __builtin_amdgcn_raw_buffer_load_b32(r, (int) off, 0, 0);
+    }
+    for (int k = 0; k < WP_LINES; ++k) asm volatile("" ::"v"(v[k]));
+}
+
 // Residual rows: x[m] += the k-slice sums of a matmul (part[ks][M][K], slices added in order; add 0: x[m] = the
 // sums), or with PAIRS the MoE output (pairs_sum4 over part = the grouped down matmul's rows), written back; then,
 // when xa is given, the RMSNorm (weight nw) and Q8_0 operand of the new row. One workgroup per row (the norm needs the
@@ -226,7 +250,11 @@ __global__ __launch_bounds__(1024) void k_resid_quant(float* __restrict__ X, con
                                                       int M, int K, const float* __restrict__ nw, float eps,
                                                       uint8_t* __restrict__ xa, int add, float* __restrict__ xn,
                                                       const int32_t* __restrict__ prow = nullptr,
-                                                      const float* __restrict__ pw = nullptr) {
+                                                      const float* __restrict__ pw = nullptr, WeightPrefetch pf = {}) {
+    if ((int) blockIdx.x >= M) {  // a prefetch workgroup (WeightPrefetch)
+        weight_prefetch(pf, (int) blockIdx.x - M, (int) gridDim.x - M);
+        return;
+    }
     __shared__ float red[16];
     const int m = blockIdx.x, t = threadIdx.x, g = t & 3, bstep = blockDim.x >> 2;
     const int nb = K / 32, nbp = xa_nbp(K);
@@ -1625,8 +1653,10 @@ void q4_repack(const uint8_t* src, int N, int K, uint8_t* dst, int sstride, int 
 
 template <int IT>
 static void launch_resid(int km, int nt, float* x, const float* part, int ks, int M, int K, const float* nw, float eps,
-                         uint8_t* xa, int ad, float* xn, hipStream_t st) {
-#define RQ(KM_) hipLaunchKernelGGL((k_resid_quant<IT, KM_>), dim3(M), dim3(nt), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn)
+                         uint8_t* xa, int ad, float* xn, hipStream_t st, const WeightPrefetch& pf, int npf) {
+#define RQ(KM_)                                                                                                     \
+    hipLaunchKernelGGL((k_resid_quant<IT, KM_>), dim3(M + npf), dim3(nt), 0, st, x, part, ks, M, K, nw, eps, xa, ad, xn, \
+                       (const int32_t*) nullptr, (const float*) nullptr, pf)
     if (km == 1) RQ(1);
     else if (km == 2) RQ(2);
     else if (km == 4) RQ(4);
@@ -1637,17 +1667,33 @@ static void launch_resid(int km, int nt, float* x, const float* part, int ks, in
 }
 
 int resid_quant(float* x, const float* part, int ks, int M, int K, const float* nw, float eps, uint8_t* xa,
-                hipStream_t st, bool add, float* xn) {
+                hipStream_t st, bool add, float* xn, const uint8_t* next_w, int next_N, int next_K, int wt) {
     if (M <= 0) return 0;
+    // (next_w: the next matmul's first groups into the Infinity Cache by extra workgroups; decode-sized rows only,
+    // where that matmul streams its slices)
+    WeightPrefetch pf{};
+    int npf = 0;
+    if (next_w && M < Q4_PAIR_ROWS) {
+        const GemmPlan p = q4_plan(next_N, next_K, wt);
+        const int tb = wt_tile_bytes(wt);
+        if (p.stream) {
+            pf.w = next_w, pf.nranges = p.nstripes * p.ks, pf.ks = p.ks, pf.sbytes = p.ngroups * tb;
+            // (the groups of each slice a wavefront's ring loads first; each slice's first group alone: the matmuls
+            // gained 30 against 61 us a step, the row kernels lost 36 against 45)
+            pf.gstep = p.gps * tb, pf.lines = (std::min(p.sd, p.gps) * tb + 127) / 128;
+            pf.total = (uint32_t) ((size_t) p.nstripes * pf.sbytes);
+            npf = (int) (((long) pf.nranges * pf.lines + 256L * WP_LINES - 1) / (256L * WP_LINES));
+        }
+    }
     // 4 lanes per block of the padded row, in whole wavefronts, at most 1024 lanes (then IT passes)
     const int lanes = 4 * xa_nbp(K), nt = std::min(1024, (lanes + 63) / 64 * 64), it = (lanes + nt - 1) / nt;
     // (10: the exact count of the deep down projections' plans, no clamped copies of the last slice loaded)
     const int km = ks == 9 || ks == 10 ? 10 : ks_bound(ks);
     if (K % 32 || it > 4 || (xn && !xa) || km == 0) return -1;
     const int ad = add ? 1 : 0;
-    if (it == 1) launch_resid<1>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
-    else if (it == 2) launch_resid<2>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
-    else launch_resid<4>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st);
+    if (it == 1) launch_resid<1>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st, pf, npf);
+    else if (it == 2) launch_resid<2>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st, pf, npf);
+    else launch_resid<4>(km, nt, x, part, ks, M, K, nw, eps, xa, ad, xn, st, pf, npf);
     return 0;
 }
 

@@ -139,8 +139,11 @@ void quant_act(const float* x, const int32_t* rows, int M, int K, int ldx, const
 // SwiGLU of the stripe-interleaved gate/up pair (output column 16p + n = silu(column 32p + n) * column 32p + 16 + n).
 // x[m] += the k-slice sums part[ks][M][K] (added in slice order; add false: x[m] = the sums); then, with xa, the Q8_0
 // operand of the new rows (RMS-normed by nw when given). K <= 8192. 0, or -1 (shape).
+// next_w (optional): the next matmul's N x K matrix (weight type wt), whose first weight groups extra workgroups read
+// into the Infinity Cache meanwhile (decode-sized rows).
 int resid_quant(float* x, const float* part, int ks, int M, int K, const float* nw, float eps, uint8_t* xa,
-                hipStream_t st, bool add = true, float* xn = nullptr);
+                hipStream_t st, bool add = true, float* xn = nullptr, const uint8_t* next_w = nullptr, int next_N = 0,
+                int next_K = 0, int wt = 2);
 // h (optional) and the Q8_0 operand of silu(gate) * up from a stripe-interleaved gate/up matmul's k-slice sums
 // part[ks][M][2F]. 0, or -1 (more than KS_MAX slices, F not a multiple of 32: nothing launched).
 int swiglu_quant(const float* part, int ks, int M, int F, float* h, uint8_t* xa, hipStream_t st,
